@@ -1,0 +1,134 @@
+/*
+ * kda_mi355x.h — C ABI of the MI355X (gfx950) Kimi Delta Attention backend.
+ *
+ * Plain C: device pointers, sizes, a dtype enum and an opaque HIP stream
+ * (`void*`, a `hipStream_t`).  No torch types cross this boundary.  All calls
+ * are asynchronous on `stream`; they allocate nothing (the chunked prefill
+ * takes a caller-provided workspace) and return a status code.
+ *
+ * Tensor layouts are the reference's canonical contiguous layouts
+ * (pablo-reyes8/kimi-k3-pytorch, src/kda):
+ *   q, k, g : [tokens, H, K]   (dense batches are [B, T, H, K] = tokens B*T)
+ *   v, out  : [tokens, H, V]
+ *   beta    : [tokens, H]
+ *   states  : [N, H, K, V]     (the `recurrent_state` of src/kda/state.py:16)
+ *
+ * Sequences.  `cu_seqlens == NULL` means N dense sequences of `dense_span`
+ * tokens each (sequence s owns rows [s*T, (s+1)*T)).  Otherwise
+ * `cu_seqlens` is an int32 device array of N+1 monotone offsets (packed
+ * documents; the state starts from zero or `initial_state[s]` at each
+ * document start).  `valid_lens` (int32 device array [N], or NULL) marks a
+ * monotone right-padding: tokens at positions >= valid_lens[s] of sequence s
+ * neither decay, write nor read the state and their output rows are zero
+ * (src/kda/utils.py:82-94).
+ *
+ * Arithmetic: bf16/f16/f32 inputs compute in f32 with an f32 state; f64
+ * inputs compute in f64 with an f64 state (src/kda/utils.py:74-79).
+ */
+#ifndef KDA_MI355X_H
+#define KDA_MI355X_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define KDA_ABI_VERSION 1
+
+/* status codes */
+#define KDA_OK 0
+#define KDA_ERR_INVALID_ARGUMENT 1
+#define KDA_ERR_UNSUPPORTED 2
+#define KDA_ERR_WORKSPACE 3
+#define KDA_ERR_LAUNCH 4
+
+/* element types */
+#define KDA_DTYPE_F32 0
+#define KDA_DTYPE_F16 1
+#define KDA_DTYPE_BF16 2
+#define KDA_DTYPE_F64 3
+
+/* Version of this ABI (KDA_ABI_VERSION). No reference counterpart. */
+int kda_abi_version(void);
+
+/* Human-readable text for a status code, including the last error detail
+ * recorded on the calling thread. No reference counterpart. */
+const char* kda_status_string(int status);
+
+/*
+ * Exact token-by-token KDA recurrence: per token
+ *   S <- diag(exp g_t) S;  e = v_t - S^T k_t;  S <- S + beta_t k_t e^T;  o_t = S^T q_t.
+ * Replaces `recurrent_kda` (src/kda/recurrent.py:25-80) for T >= 1.
+ *   in_dtype        : dtype of q, k, v, g, beta and `out`.
+ *   state_dtype     : KDA_DTYPE_F32 for bf16/f16/f32 inputs, KDA_DTYPE_F64 for f64.
+ *   initial_state   : [N,H,K,V] or NULL (zero state). May alias final_state.
+ *   final_state     : [N,H,K,V] or NULL.
+ *   states_per_token: NULL, or [T,N,H,K,V] written after every token
+ *                     (`return_states_per_token`, recurrent.py:61,73-74,79);
+ *                     dense sequences only (cu_seqlens == NULL).
+ */
+int kda_recurrent_fwd(const void* q, const void* k, const void* v, const void* g,
+                      const void* beta, int in_dtype, const void* initial_state,
+                      void* final_state, int state_dtype, void* out, void* states_per_token,
+                      const int32_t* cu_seqlens, int64_t dense_span, const int32_t* valid_lens,
+                      int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
+                      int64_t value_dim, void* stream);
+
+/*
+ * One decode step (T = 1) for `batch` sequences: the memory-bound
+ * diagonal-decay, rank-1 delta update of the cached state, read once and
+ * written once.  This is what `KimiDeltaAttention.forward(mode="decode")`
+ * runs through `recurrent_kda` with T = 1 (src/kda/kda.py:144-145,
+ * src/kda/recurrent.py:62-74).  `state_out` may equal `state_in` (in-place
+ * update); `state_in == NULL` means a zero state.
+ */
+int kda_decode_step(const void* q, const void* k, const void* v, const void* g,
+                    const void* beta, int in_dtype, const void* state_in, void* state_out,
+                    int state_dtype, void* out, int64_t batch, int64_t heads, int64_t key_dim,
+                    int64_t value_dim, void* stream);
+
+/*
+ * Workspace bytes `kda_chunk_fwd` needs for these sizes (0 if none).
+ * No reference counterpart (the reference allocates per call).
+ */
+size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads,
+                                     int64_t key_dim, int64_t value_dim, int in_dtype);
+
+/*
+ * Chunkwise-parallel KDA prefill (chunk 64): intra-chunk UT transform with a
+ * forward-substitution solve, bf16 MFMA chunk products with f32 accumulation
+ * and an f32 inter-chunk state scan.  Replaces `chunkwise_kda`
+ * (src/kda/chunkwise.py:17-107); its result does not depend on the
+ * reference's chunk_size / secondary_tile_size (the reference's own
+ * invariance, tests/kda/test_kda_chunkwise_equivalence.py:42-57,
+ * tests/kda/test_kda_ut_transform.py:94-103).  Packed documents via
+ * `cu_seqlens` have no reference counterpart: each document equals an
+ * independent `chunkwise_kda` call.
+ * Shapes the MFMA path does not cover (K != 128, V not a multiple of 16,
+ * f32/f64 inputs) run the exact recurrence kernel instead.
+ */
+int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                  int in_dtype, const void* initial_state, void* final_state, int state_dtype,
+                  void* out, const int32_t* cu_seqlens, int64_t dense_span,
+                  const int32_t* valid_lens, int64_t num_seqs, int64_t total_tokens,
+                  int64_t heads, int64_t key_dim, int64_t value_dim, void* workspace,
+                  size_t workspace_bytes, void* stream);
+
+/*
+ * UT transform of independent chunks, canonical [B,C,H,*] inputs.
+ * Replaces `ut_transform` (src/kda/ut_transform.py:61-92).  Outputs, in
+ * `out_dtype` (f32 for bf16/f16/f32 inputs, f64 for f64):
+ *   M [B,H,C,C]; U [B,C,H,V]; W, log_gamma, k_gamma [B,C,H,K].
+ */
+int kda_ut_transform(const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                     void* M, void* U, void* W, void* log_gamma, void* k_gamma, int out_dtype,
+                     int64_t batch, int64_t count, int64_t heads, int64_t key_dim,
+                     int64_t value_dim, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* KDA_MI355X_H */

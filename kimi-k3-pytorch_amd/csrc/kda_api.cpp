@@ -1,0 +1,187 @@
+// extern "C" entry points of libkda_mi355x.so (declared in include/kda_mi355x.h).
+// Argument checks happen here, before any launch, so a bad call returns
+// KDA_ERR_INVALID_ARGUMENT instead of launching a kernel whose grid or
+// indexing would not match the buffers.
+#include <hip/hip_runtime.h>
+
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "kda_common.h"
+#include "kda_launch.h"
+
+namespace kda_host {
+
+static thread_local char g_detail[512];
+static thread_local char g_status[640];
+
+void set_detail(const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_detail, sizeof(g_detail), fmt, ap);
+  va_end(ap);
+}
+
+const char* detail() { return g_detail; }
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) {
+    set_detail("%s launch failed: %s", what, hipGetErrorString(e));
+    return KDA_ERR_LAUNCH;
+  }
+  return KDA_OK;
+}
+
+static bool is_input_dtype(int d) {
+  return d == KDA_DTYPE_F32 || d == KDA_DTYPE_F16 || d == KDA_DTYPE_BF16 || d == KDA_DTYPE_F64;
+}
+
+static int expected_state_dtype(int in_dtype) { return in_dtype == KDA_DTYPE_F64 ? KDA_DTYPE_F64 : KDA_DTYPE_F32; }
+
+static int check_common(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                        int state_dtype, const void* out, int64_t num_seqs, int64_t total_tokens, int64_t heads,
+                        int64_t key_dim, int64_t value_dim) {
+  g_detail[0] = '\0';
+  if (!is_input_dtype(in_dtype)) {
+    set_detail("unknown input dtype %d", in_dtype);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (state_dtype != expected_state_dtype(in_dtype)) {
+    set_detail("state dtype %d does not match input dtype %d", state_dtype, in_dtype);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (num_seqs <= 0 || total_tokens <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) {
+    set_detail("sizes must be positive (N=%lld tokens=%lld H=%lld K=%lld V=%lld)", (long long)num_seqs,
+               (long long)total_tokens, (long long)heads, (long long)key_dim, (long long)value_dim);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!q || !k || !v || !g || !beta || !out) {
+    set_detail("q, k, v, g, beta and out must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return KDA_OK;
+}
+
+static int check_seq(const int32_t* cu_seqlens, int64_t dense_span, int64_t num_seqs, int64_t total_tokens) {
+  if (cu_seqlens == nullptr) {
+    if (dense_span <= 0 || dense_span * num_seqs != total_tokens) {
+      set_detail("dense layout needs dense_span * num_seqs == total_tokens (%lld * %lld != %lld)",
+                 (long long)dense_span, (long long)num_seqs, (long long)total_tokens);
+      return KDA_ERR_INVALID_ARGUMENT;
+    }
+  }
+  if (total_tokens > 0x7fffffffLL) {
+    set_detail("total_tokens %lld exceeds int32 offsets", (long long)total_tokens);
+    return KDA_ERR_UNSUPPORTED;
+  }
+  return KDA_OK;
+}
+
+}  // namespace kda_host
+
+using namespace kda_host;
+
+extern "C" {
+
+int kda_abi_version(void) { return KDA_ABI_VERSION; }
+
+const char* kda_status_string(int status) {
+  const char* base = "unknown status";
+  switch (status) {
+    case KDA_OK: base = "ok"; break;
+    case KDA_ERR_INVALID_ARGUMENT: base = "invalid argument"; break;
+    case KDA_ERR_UNSUPPORTED: base = "unsupported configuration"; break;
+    case KDA_ERR_WORKSPACE: base = "workspace too small"; break;
+    case KDA_ERR_LAUNCH: base = "kernel launch failed"; break;
+    default: break;
+  }
+  if (g_detail[0] != '\0')
+    snprintf(g_status, sizeof(g_status), "%s: %s", base, g_detail);
+  else
+    snprintf(g_status, sizeof(g_status), "%s", base);
+  return g_status;
+}
+
+int kda_recurrent_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                      const void* initial_state, void* final_state, int state_dtype, void* out,
+                      void* states_per_token, const int32_t* cu_seqlens, int64_t dense_span,
+                      const int32_t* valid_lens, int64_t num_seqs, int64_t total_tokens, int64_t heads,
+                      int64_t key_dim, int64_t value_dim, void* stream) {
+  int st = check_common(q, k, v, g, beta, in_dtype, state_dtype, out, num_seqs, total_tokens, heads, key_dim,
+                        value_dim);
+  if (st != KDA_OK) return st;
+  st = check_seq(cu_seqlens, dense_span, num_seqs, total_tokens);
+  if (st != KDA_OK) return st;
+  if (states_per_token != nullptr && cu_seqlens != nullptr) {
+    set_detail("states_per_token needs dense sequences (cu_seqlens == NULL)");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
+  return launch_recurrent(q, k, v, g, beta, in_dtype, initial_state, final_state, state_dtype, out,
+                          states_per_token, seq, num_seqs, heads, key_dim, value_dim,
+                          static_cast<hipStream_t>(stream), false);
+}
+
+int kda_decode_step(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                    const void* state_in, void* state_out, int state_dtype, void* out, int64_t batch,
+                    int64_t heads, int64_t key_dim, int64_t value_dim, void* stream) {
+  int st = check_common(q, k, v, g, beta, in_dtype, state_dtype, out, batch, batch, heads, key_dim, value_dim);
+  if (st != KDA_OK) return st;
+  if (state_out == nullptr) {
+    set_detail("decode step needs state_out");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  kda::SeqDesc seq{nullptr, 1, nullptr};
+  return launch_recurrent(q, k, v, g, beta, in_dtype, state_in, state_out, state_dtype, out, nullptr, seq, batch,
+                          heads, key_dim, value_dim, static_cast<hipStream_t>(stream), true);
+}
+
+size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
+                                     int64_t value_dim, int in_dtype) {
+  return chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype);
+}
+
+int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                  const void* initial_state, void* final_state, int state_dtype, void* out,
+                  const int32_t* cu_seqlens, int64_t dense_span, const int32_t* valid_lens, int64_t num_seqs,
+                  int64_t total_tokens, int64_t heads, int64_t key_dim, int64_t value_dim, void* workspace,
+                  size_t workspace_bytes, void* stream) {
+  int st = check_common(q, k, v, g, beta, in_dtype, state_dtype, out, num_seqs, total_tokens, heads, key_dim,
+                        value_dim);
+  if (st != KDA_OK) return st;
+  st = check_seq(cu_seqlens, dense_span, num_seqs, total_tokens);
+  if (st != KDA_OK) return st;
+  const size_t need = chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    set_detail("chunk_fwd needs %zu workspace bytes, got %zu", need, workspace_bytes);
+    return KDA_ERR_WORKSPACE;
+  }
+  kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
+  return launch_chunk(q, k, v, g, beta, in_dtype, initial_state, final_state, state_dtype, out, seq, num_seqs,
+                      total_tokens, heads, key_dim, value_dim, workspace, workspace_bytes,
+                      static_cast<hipStream_t>(stream));
+}
+
+int kda_ut_transform(const void* k, const void* v, const void* g, const void* beta, int in_dtype, void* M, void* U,
+                     void* W, void* log_gamma, void* k_gamma, int out_dtype, int64_t batch, int64_t count,
+                     int64_t heads, int64_t key_dim, int64_t value_dim, void* stream) {
+  g_detail[0] = '\0';
+  if (!is_input_dtype(in_dtype) || out_dtype != expected_state_dtype(in_dtype)) {
+    set_detail("ut_transform: bad dtypes (in %d, out %d)", in_dtype, out_dtype);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (batch <= 0 || count <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) {
+    set_detail("ut_transform: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!k || !v || !g || !beta || !M || !U || !W || !log_gamma || !k_gamma) {
+    set_detail("ut_transform: all pointers must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return launch_ut_transform(k, v, g, beta, in_dtype, M, U, W, log_gamma, k_gamma, out_dtype, batch, count, heads,
+                             key_dim, value_dim, static_cast<hipStream_t>(stream));
+}
+
+}  // extern "C"

@@ -1,0 +1,30 @@
+// Host-side launchers shared between the kernels' translation units and the
+// C-ABI glue in kda_api.cpp.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+#include "kda_common.h"
+
+namespace kda_host {
+
+int launch_recurrent(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                     const void* s_in, void* s_out, int state_dtype, void* out, void* s_hist,
+                     const kda::SeqDesc& seq, int64_t N, int64_t H, int64_t K, int64_t V, hipStream_t stream,
+                     bool streaming_state);
+
+size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
+                             int64_t value_dim, int in_dtype);
+
+int launch_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                 const void* s_in, void* s_out, int state_dtype, void* out, const kda::SeqDesc& seq, int64_t N,
+                 int64_t total_tokens, int64_t H, int64_t K, int64_t V, void* workspace, size_t workspace_bytes,
+                 hipStream_t stream);
+
+int launch_ut_transform(const void* k, const void* v, const void* g, const void* beta, int in_dtype, void* M,
+                        void* U, void* W, void* log_gamma, void* k_gamma, int out_dtype, int64_t batch,
+                        int64_t count, int64_t heads, int64_t key_dim, int64_t value_dim, hipStream_t stream);
+
+}  // namespace kda_host

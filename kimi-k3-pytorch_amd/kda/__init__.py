@@ -1,0 +1,23 @@
+"""MI355X (gfx950) backend for the Kimi Delta Attention operators.
+
+Mirrors the operator surface of pablo-reyes8/kimi-k3-pytorch ``src/kda``
+(src/kda/__init__.py:1-25): ``chunkwise_kda``, ``recurrent_kda``,
+``ut_transform``, ``KDAOperatorOutput``, ``UTTransformOutput`` and
+``KDAState``.  All arithmetic runs in hand-written HIP kernels in
+``libkda_mi355x.so``; see include/kda_mi355x.h for the C ABI.
+"""
+
+from .chunkwise import chunkwise_kda
+from .recurrent import KDAOperatorOutput, recurrent_kda
+from .state import KDAState, ShortConvState
+from .ut_transform import UTTransformOutput, ut_transform
+
+__all__ = [
+    "KDAOperatorOutput",
+    "KDAState",
+    "ShortConvState",
+    "UTTransformOutput",
+    "chunkwise_kda",
+    "recurrent_kda",
+    "ut_transform",
+]

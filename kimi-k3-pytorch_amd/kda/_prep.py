@@ -1,0 +1,65 @@
+"""Shared argument preparation for the operator wrappers (host side only)."""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def reject_autograd(*tensors: torch.Tensor | None) -> None:
+    """The GPU path is forward-only; refuse to silently drop gradients."""
+    if not torch.is_grad_enabled():
+        return
+    if any(t is not None and t.requires_grad for t in tensors):
+        raise RuntimeError(
+            "the MI355X KDA backend implements the forward pass only; "
+            "call it under torch.no_grad()/inference_mode() or detach the inputs"
+        )
+
+
+def kernel_inputs(q, k, v, g, beta, work_dtype: torch.dtype):
+    """Pick the element type the kernels read and make the inputs contiguous.
+
+    The reference upcasts every input to the work dtype before any arithmetic
+    (src/kda/chunkwise.py:41-45, src/kda/recurrent.py:42-46).  The kernels do
+    that upcast on load, so inputs that already share one dtype are passed
+    as they are (bf16 stays bf16 in HBM).  Mixed dtypes are cast to the
+    arithmetic type first, which loses nothing.
+    """
+    tensors = (q, k, v, g, beta)
+    dtypes = {t.dtype for t in tensors}
+    arith = torch.float64 if work_dtype == torch.float64 else torch.float32
+    if len(dtypes) == 1:
+        (common,) = dtypes
+        if arith == torch.float64:
+            kernel_dtype = torch.float64
+        elif common in (torch.bfloat16, torch.float16, torch.float32):
+            kernel_dtype = common
+        else:
+            kernel_dtype = arith
+    else:
+        kernel_dtype = arith
+    out = tuple(t.to(kernel_dtype).contiguous() for t in tensors)
+    return out, kernel_dtype, arith
+
+
+def valid_lengths(attention_mask: torch.Tensor | None, device: torch.device) -> torch.Tensor | None:
+    """Monotone right-padding mask -> int32 valid length per row."""
+    if attention_mask is None:
+        return None
+    return attention_mask.to(device=device).sum(dim=1, dtype=torch.int32).contiguous()
+
+
+def state_arg(initial_state: torch.Tensor | None, arith: torch.dtype) -> torch.Tensor | None:
+    if initial_state is None:
+        return None
+    return initial_state.to(arith).contiguous()
+
+
+def cu_tensor(offsets: list[int], device: torch.device) -> torch.Tensor:
+    return torch.tensor(offsets, dtype=torch.int32, device=device)
+
+
+def stream(device: torch.device) -> int:
+    return _lib.stream_of(device)

@@ -1,0 +1,119 @@
+"""Exact token recurrence (decode and ``mode="recurrent"``) on the gfx950 backend.
+
+Drop-in for ``recurrent_kda`` (src/kda/recurrent.py:25-80): same signature,
+defaults, validation errors and dtype rules; the arithmetic runs in the HIP
+kernel behind ``kda_recurrent_fwd`` / ``kda_decode_step``.
+
+Additive keyword-only extensions (every existing call is unchanged):
+* ``cu_seqlens``: packed documents ``[1, sum T, H, *]``; each document is an
+  independent recurrence, ``initial_state``/``final_state`` are ``[N,H,K,V]``.
+* ``update_state_in_place``: write the new state into ``initial_state``
+  (which must already be contiguous and in the work dtype) and return it as
+  ``final_state``; the default keeps the reference's functional update
+  (src/kda/recurrent.py:50-59).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib, _prep
+from .utils import accumulation_dtype, validate_core_inputs, validate_cu_seqlens
+
+
+@dataclass
+class KDAOperatorOutput:
+    """Output and updated recurrent matrix from a KDA operator backend
+    (src/kda/recurrent.py:16-22)."""
+
+    hidden_states: torch.Tensor
+    final_state: torch.Tensor | None = None
+    states_per_token: tuple[torch.Tensor, ...] | None = None
+
+
+def recurrent_kda(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    g: torch.Tensor,
+    beta: torch.Tensor,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    attention_mask: torch.Tensor | None = None,
+    *,
+    accumulate_state_in_fp32: bool = True,
+    return_states_per_token: bool = False,
+    cu_seqlens: torch.Tensor | list[int] | None = None,
+    update_state_in_place: bool = False,
+) -> KDAOperatorOutput:
+    """Exact KDA recurrence with decay, delta update, then read-after-write."""
+    offsets = None
+    if cu_seqlens is not None:
+        offsets = validate_cu_seqlens(cu_seqlens, q.shape[0] if q.ndim == 4 else -1,
+                                      q.shape[1] if q.ndim == 4 else -1, attention_mask)
+    num_states = None if offsets is None else len(offsets) - 1
+    batch, tokens, heads, key_dim, value_dim = validate_core_inputs(
+        q, k, v, g, beta, initial_state, attention_mask, num_states=num_states
+    )
+    if return_states_per_token and offsets is not None:
+        raise ValueError("return_states_per_token is not supported with cu_seqlens")
+    _lib.require_gpu(q)
+    _prep.reject_autograd(q, k, v, g, beta, initial_state)
+    lib = _lib.load()
+
+    work_dtype = accumulation_dtype(v.dtype, accumulate_state_in_fp32)
+    (qc, kc, vc, gc, bc), kernel_dtype, arith = _prep.kernel_inputs(q, k, v, g, beta, work_dtype)
+    device = q.device
+    n_seq = batch if offsets is None else len(offsets) - 1
+    total = batch * tokens
+
+    if update_state_in_place:
+        if initial_state is None:
+            raise ValueError("update_state_in_place needs an initial_state")
+        if initial_state.dtype != arith or not initial_state.is_contiguous():
+            raise ValueError(
+                f"update_state_in_place needs a contiguous {arith} initial_state, "
+                f"got {initial_state.dtype} (contiguous={initial_state.is_contiguous()})"
+            )
+        s_in = initial_state
+        s_out = initial_state
+    else:
+        s_in = _prep.state_arg(initial_state, arith)
+        need_state = output_final_state or return_states_per_token
+        s_out = torch.empty(n_seq, heads, key_dim, value_dim, dtype=arith, device=device) if need_state else None
+
+    out = torch.empty(batch, tokens, heads, value_dim, dtype=kernel_dtype, device=device)
+    hist = None
+    if return_states_per_token:
+        hist = torch.empty(tokens, n_seq, heads, key_dim, value_dim, dtype=arith, device=device)
+
+    stream = _prep.stream(device)
+    code = _lib.dtype_code(kernel_dtype)
+    scode = _lib.dtype_code(arith)
+    if offsets is None and tokens == 1 and hist is None and s_out is not None:
+        # one decode step: the state streams through once (mask rows are all valid at T=1)
+        status = lib.kda_decode_step(
+            qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr(), bc.data_ptr(), code,
+            _lib.ptr(s_in), s_out.data_ptr(), scode, out.data_ptr(),
+            batch, heads, key_dim, value_dim, stream,
+        )
+    else:
+        cu = None if offsets is None else _prep.cu_tensor(offsets, device)
+        valid = _prep.valid_lengths(attention_mask, device)
+        status = lib.kda_recurrent_fwd(
+            qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr(), bc.data_ptr(), code,
+            _lib.ptr(s_in), _lib.ptr(s_out), scode, out.data_ptr(), _lib.ptr(hist),
+            _lib.ptr(cu), tokens, _lib.ptr(valid), n_seq, total, heads, key_dim, value_dim, stream,
+        )
+    _lib.check(status)
+
+    hidden = out if out.dtype == v.dtype else out.to(v.dtype)
+    final = None
+    if output_final_state:
+        final = s_out if s_out.dtype == work_dtype else s_out.to(work_dtype)
+    states = None
+    if hist is not None:
+        states = tuple(x if x.dtype == work_dtype else x.to(work_dtype) for x in hist.unbind(0))
+    return KDAOperatorOutput(hidden_states=hidden, final_state=final, states_per_token=states)

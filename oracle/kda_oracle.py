@@ -1,0 +1,222 @@
+"""CPU oracle for the Kimi Delta Attention (KDA) operator path.
+
+TEST INFRASTRUCTURE ONLY.  Nothing in the product package imports this module;
+only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
+``bench.py`` may use it, and only as the checker / the timed CPU baseline.
+
+This is a PyTorch-on-CPU restatement of the reference operator
+(pablo-reyes8/kimi-k3-pytorch, ``src/kda``).  It keeps the reference's
+algorithmic steps so that it doubles as "the reference's own CPU path" for the
+CPU baseline, but the code is written independently:
+
+* ``recurrent``            follows ``src/kda/recurrent.py:38-80``
+* ``tiled_causal_decay_dot`` follows ``src/kda/utils.py:97-143``
+* ``ut_transform_internal`` follows ``src/kda/ut_transform.py:23-58``
+* ``chunkwise``            follows ``src/kda/chunkwise.py:34-107``
+* ``work_dtype``           follows ``src/kda/utils.py:74-79``
+* ``mask_inputs``          follows ``src/kda/utils.py:82-94``
+* ``varlen_chunkwise`` / ``varlen_recurrent`` have no reference counterpart
+  (the reference has no ``cu_seqlens``); they are defined as independent runs
+  of the functions above on each document, which is the semantics the GPU
+  path implements.
+
+How each function is pinned (tests/test_oracle_*.py):
+
+* ``recurrent``: the reference's literal known-answer tests
+  (tests/kda/test_kda_recurrent.py:70-139), the matrix/error-correction
+  identity (:48-67), an independent scalar C implementation
+  (``oracle/kda_recurrent_ref.c``) and the beta=0 closed form.
+* ``tiled_causal_decay_dot``: brute-force pairwise sums on tiny inputs and
+  tile-size invariance.
+* ``ut_transform_internal``: an explicit inverse (``torch.linalg.inv``) and a
+  row-by-row forward substitution.
+* ``chunkwise``: equality with ``recurrent`` in float64 at 2e-11 over the
+  reference's shape/chunk grid, prefix causality and mask==truncation.
+* varlen: per-document equality (by construction) plus state reset checks.
+
+Rounding: the reference's bit-level float32/bfloat16 rounding order (einsum /
+BLAS / LAPACK) is not reproduced; parity is judged with tolerances.
+"""
+
+from __future__ import annotations
+
+import torch
+
+__all__ = [
+    "work_dtype",
+    "mask_inputs",
+    "recurrent",
+    "tiled_causal_decay_dot",
+    "ut_transform_internal",
+    "chunkwise",
+    "varlen_recurrent",
+    "varlen_chunkwise",
+]
+
+
+def work_dtype(activation_dtype: torch.dtype, accumulate_state_in_fp32: bool = True) -> torch.dtype:
+    """Arithmetic dtype of the operator (src/kda/utils.py:74-79)."""
+    if accumulate_state_in_fp32 and activation_dtype in (torch.float16, torch.bfloat16):
+        return torch.float32
+    return activation_dtype
+
+
+def mask_inputs(q, g, beta, attention_mask):
+    """Zero q, g and beta at padded positions (src/kda/utils.py:82-94).
+
+    A padded token then neither decays, writes nor reads the state."""
+    if attention_mask is None:
+        return q, g, beta
+    keep = attention_mask.to(torch.bool)
+    q = torch.where(keep[:, :, None, None], q, torch.zeros((), dtype=q.dtype))
+    g = torch.where(keep[:, :, None, None], g, torch.zeros((), dtype=g.dtype))
+    beta = torch.where(keep[:, :, None], beta, torch.zeros((), dtype=beta.dtype))
+    return q, g, beta
+
+
+def _prepare(q, k, v, g, beta, initial_state, attention_mask, accumulate_state_in_fp32):
+    dtype = work_dtype(v.dtype, accumulate_state_in_fp32)
+    qw, kw, vw, gw, bw = (t.to(dtype) for t in (q, k, v, g, beta))
+    qw, gw, bw = mask_inputs(qw, gw, bw, attention_mask)
+    batch, _, heads, key_dim = q.shape
+    value_dim = v.shape[-1]
+    state = torch.zeros(batch, heads, key_dim, value_dim, dtype=dtype)
+    if initial_state is not None:
+        state = state + initial_state.to(dtype)
+    return dtype, qw, kw, vw, gw, bw, state
+
+
+def recurrent(
+    q, k, v, g, beta, initial_state=None, attention_mask=None, *,
+    accumulate_state_in_fp32: bool = True, return_states: bool = False,
+):
+    """Token-by-token KDA (src/kda/recurrent.py:38-80).
+
+    Per token t (recurrent.py:66-72):
+      S <- diag(exp g_t) S ;  e = v_t - S^T k_t ;  S <- S + beta_t k_t e^T ;  o_t = S^T q_t
+    Returns (output in v.dtype, final state in the work dtype, [states]).
+    """
+    dtype, qw, kw, vw, gw, bw, state = _prepare(
+        q, k, v, g, beta, initial_state, attention_mask, accumulate_state_in_fp32)
+    tokens = q.shape[1]
+    outputs = []
+    history = []
+    for t in range(tokens):
+        state = state * gw[:, t].exp().unsqueeze(-1)
+        recalled = (state * kw[:, t].unsqueeze(-1)).sum(dim=-2)
+        error = vw[:, t] - recalled
+        write = (bw[:, t].unsqueeze(-1) * kw[:, t]).unsqueeze(-1) * error.unsqueeze(-2)
+        state = state + write
+        outputs.append((state * qw[:, t].unsqueeze(-1)).sum(dim=-2))
+        if return_states:
+            history.append(state)
+    out = torch.stack(outputs, dim=1).to(v.dtype)
+    return out, state, (tuple(history) if return_states else None)
+
+
+def tiled_causal_decay_dot(left, right, log_left, log_right, tile: int, *, include_diagonal: bool):
+    """out[b,h,i,j] = sum_c left[i,c] exp(log_left[i,c] - log_right[j,c]) right[j,c]
+    for j <= i (or j < i), computed tile by tile with an explicit pairwise
+    exponent (src/kda/utils.py:97-143).  Inputs are ``[B,H,C,K]``."""
+    if tile <= 0:
+        raise ValueError("tile_size must be > 0")
+    batch, heads, count, _ = left.shape
+    out = torch.zeros(batch, heads, count, count, dtype=left.dtype)
+    rows = torch.arange(count)
+    for r0 in range(0, count, tile):
+        r1 = min(r0 + tile, count)
+        for c0 in range(0, r1, tile):
+            c1 = min(c0 + tile, count)
+            pair_log = log_left[:, :, r0:r1, None, :] - log_right[:, :, None, c0:c1, :]
+            weighted = left[:, :, r0:r1, None, :] * pair_log.exp()
+            block = (weighted * right[:, :, None, c0:c1, :]).sum(dim=-1)
+            ri = rows[r0:r1, None]
+            ci = rows[None, c0:c1]
+            keep = (ri >= ci) if include_diagonal else (ri > ci)
+            out[:, :, r0:r1, c0:c1] = block * keep.to(block.dtype)
+    return out
+
+
+def ut_transform_internal(k, v, g, beta, tile: int):
+    """UT/WY transform of one chunk, internal ``[B,H,C,*]`` layout
+    (src/kda/ut_transform.py:23-58).
+
+    log_gamma = cumsum(g);  A = strict-lower decayed k k^T;  L = I + diag(beta) A;
+    M = L^{-1} diag(beta);  W = M (exp(log_gamma) * k);  U = M v.
+    """
+    count = k.shape[2]
+    log_gamma = g.cumsum(dim=2)
+    strict = tiled_causal_decay_dot(k, k, log_gamma, log_gamma, tile, include_diagonal=False)
+    lower = torch.eye(count, dtype=k.dtype) + beta.unsqueeze(-1) * strict
+    rhs = torch.diag_embed(beta)
+    M = torch.linalg.solve_triangular(lower, rhs, upper=False, unitriangular=True)
+    k_gamma = log_gamma.exp() * k
+    return {
+        "M": M,
+        "W": M @ k_gamma,
+        "U": M @ v,
+        "log_gamma": log_gamma,
+        "k_gamma": k_gamma,
+    }
+
+
+def chunkwise(
+    q, k, v, g, beta, initial_state=None, attention_mask=None, *,
+    chunk_size: int = 64, secondary_tile_size: int = 16, accumulate_state_in_fp32: bool = True,
+):
+    """Chunkwise KDA with the UT transform inside each chunk
+    (src/kda/chunkwise.py:34-107).  Returns (output, final state)."""
+    dtype, qw, kw, vw, gw, bw, state = _prepare(
+        q, k, v, g, beta, initial_state, attention_mask, accumulate_state_in_fp32)
+    tokens = q.shape[1]
+    pieces = []
+    for start in range(0, tokens, chunk_size):
+        stop = min(start + chunk_size, tokens)
+        qc, kc, vc, gc = (x[:, start:stop].transpose(1, 2) for x in (qw, kw, vw, gw))
+        bc = bw[:, start:stop].transpose(1, 2)
+        ut = ut_transform_internal(kc, vc, gc, bc, secondary_tile_size)
+        lg = ut["log_gamma"]
+        pseudo = ut["U"] - ut["W"] @ state                                   # chunkwise.py:76
+        causal_qk = tiled_causal_decay_dot(qc, kc, lg, lg, secondary_tile_size,
+                                           include_diagonal=True)         # chunkwise.py:77-84
+        out_c = (lg.exp() * qc) @ state + causal_qk @ pseudo                # chunkwise.py:85-88
+        pieces.append(out_c.transpose(1, 2))
+        last = lg[:, :, -1]                                                  # chunkwise.py:91
+        to_end = (last.unsqueeze(2) - lg).exp() * kc                         # chunkwise.py:93-99
+        state = state * last.exp().unsqueeze(-1) + to_end.transpose(-2, -1) @ pseudo  # :92,100-102
+    out = torch.cat(pieces, dim=1).to(v.dtype)
+    return out, state
+
+
+def _split_docs(cu_seqlens):
+    bounds = [int(x) for x in torch.as_tensor(cu_seqlens).tolist()]
+    return list(zip(bounds[:-1], bounds[1:]))
+
+
+def varlen_recurrent(q, k, v, g, beta, cu_seqlens, initial_states=None, *,
+                     accumulate_state_in_fp32: bool = True):
+    """Packed documents ``[1, sum T, H, *]``: each document is an independent
+    ``recurrent`` run starting from its own initial state (or zero)."""
+    outs, finals = [], []
+    for index, (s0, s1) in enumerate(_split_docs(cu_seqlens)):
+        init = None if initial_states is None else initial_states[index:index + 1]
+        o, s, _ = recurrent(q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], g[:, s0:s1], beta[:, s0:s1],
+                            init, accumulate_state_in_fp32=accumulate_state_in_fp32)
+        outs.append(o)
+        finals.append(s)
+    return torch.cat(outs, dim=1), torch.cat(finals, dim=0)
+
+
+def varlen_chunkwise(q, k, v, g, beta, cu_seqlens, initial_states=None, *,
+                     chunk_size: int = 64, secondary_tile_size: int = 16,
+                     accumulate_state_in_fp32: bool = True):
+    """Packed documents: each document is an independent ``chunkwise`` run."""
+    outs, finals = [], []
+    for index, (s0, s1) in enumerate(_split_docs(cu_seqlens)):
+        init = None if initial_states is None else initial_states[index:index + 1]
+        o, s = chunkwise(q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], g[:, s0:s1], beta[:, s0:s1],
+                         init, chunk_size=chunk_size, secondary_tile_size=secondary_tile_size,
+                         accumulate_state_in_fp32=accumulate_state_in_fp32)
+        outs.append(o)
+        finals.append(s)
+    return torch.cat(outs, dim=1), torch.cat(finals, dim=0)

@@ -1,0 +1,77 @@
+"""The C-ABI library loads and exports every entry point include/kda_mi355x.h
+declares (no compute calls: this suite runs without a GPU)."""
+
+from __future__ import annotations
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from kda import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "kda_mi355x.h"
+
+
+def declared_functions() -> list[str]:
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(kda_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    names = declared_functions()
+    for required in ("kda_recurrent_fwd", "kda_decode_step", "kda_chunk_fwd", "kda_chunk_fwd_workspace_bytes",
+                     "kda_ut_transform", "kda_abi_version", "kda_status_string"):
+        assert required in names
+
+
+def test_library_exports_every_declared_symbol():
+    if not _lib.LIB_PATH.exists():
+        pytest.fail(f"{_lib.LIB_PATH} is not built (run kimi-k3-pytorch_amd/build_lib.py)")
+    raw = ctypes.CDLL(str(_lib.LIB_PATH))
+    missing = [name for name in declared_functions() if not hasattr(raw, name)]
+    assert missing == []
+
+
+def test_python_binding_types_every_declared_symbol():
+    assert sorted(_lib.SIGNATURES) == declared_functions()
+
+
+def test_abi_version_and_status_strings():
+    lib = _lib.load()
+    assert lib.kda_abi_version() == _lib.ABI_VERSION
+    assert lib.kda_status_string(0).decode() == "ok"
+    assert "invalid argument" in lib.kda_status_string(1).decode()
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    lib = _lib.load()
+    # null input pointers: rejected by the argument checks, nothing is launched
+    status = lib.kda_recurrent_fwd(None, None, None, None, None, 2, None, None, 0, None, None, None, 4, None,
+                                   1, 4, 1, 128, 128, None)
+    assert status == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert "non-null" in lib.kda_status_string(status).decode()
+    # mismatched state dtype for bf16 inputs
+    status = lib.kda_decode_step(1, 1, 1, 1, 1, 2, None, 1, 3, 1, 1, 1, 128, 128, None)
+    assert status == _lib.KDA_ERR_INVALID_ARGUMENT
+    # dense layout whose sizes do not add up
+    status = lib.kda_chunk_fwd(1, 1, 1, 1, 1, 2, None, None, 0, 1, None, 3, None, 2, 7, 1, 128, 128, None, 0, None)
+    assert status == _lib.KDA_ERR_INVALID_ARGUMENT
+
+
+def declared_arities() -> dict[str, int]:
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    out = {}
+    for name, params in re.findall(r"\b(kda_[a-z0-9_]+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+        params = params.strip()
+        out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
+def test_binding_arity_matches_header():
+    arities = declared_arities()
+    assert sorted(arities) == declared_functions()
+    for name, (_, argtypes) in _lib.SIGNATURES.items():
+        assert len(argtypes) == arities[name], name
