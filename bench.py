@@ -1,0 +1,289 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X KDA backend on one GPU.
+
+Metric: "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s".
+
+* value      : chunkwise prefill throughput (tokens/s) on the long-context
+               workload B=1, T=8192, H=16, K=V=128, bf16 inputs, f32 state
+               N(0, 0.02), chunk 64 — output and final state are produced.
+               One step = one prefill over the whole batch, inputs resident
+               in HBM; timed with HIP events over exactly `--steps` steps.
+* decode     : the memory-bound decode step at B=256, H=32, K=V=128 with the
+               512 MiB f32 state updated in place for 64 consecutive steps,
+               reported as algorithmic HBM GB/s.
+* roofline   : the dominant kernel of the prefill (per-kernel HIP-event
+               timing) and the decode kernel, against MI355X peaks
+               (HBM 8 TB/s, dense bf16 MFMA 2.5 PFLOP/s).
+* cpu_baseline: the oracle's PyTorch-CPU restatement of the reference path
+               (oracle/kda_oracle.py) on a bounded sample of the same
+               workload, on the host cores (thread count reported).
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3]
+"""
+
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+REPO = Path(__file__).resolve().parent
+for p in (REPO / "kimi-k3-pytorch_amd", REPO):
+    if str(p) not in sys.path:
+        sys.path.insert(0, str(p))
+
+METRIC = "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s"
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+# long-context prefill workload
+P_B, P_T, P_H, P_K, P_V = 1, 8192, 16, 128, 128
+# decode workload
+D_B, D_H, D_K, D_V, D_STEPS = 256, 32, 128, 128, 64
+
+
+def prefill_bytes(B, T, H, K, V, n_state_io=2):
+    """Compulsory HBM bytes: q,k,g,v (bf16) + beta + output (bf16) + f32 states in/out."""
+    return 2 * B * T * H * (3 * K + V) + 2 * B * T * H + 2 * B * T * H * V + 4 * B * H * K * V * n_state_io
+
+
+def prefill_flops(B, T, H, K, V, C=64):
+    """Causal-counted chunk GEMM flops: 6KV + (3C+1)K + 2(C+1)V per token per head."""
+    return B * T * H * (6 * K * V + (3 * C + 1) * K + 2 * (C + 1) * V)
+
+
+def decode_bytes(B, H, K, V):
+    """State read + write (f32) plus the token's q,k,g,v,beta (bf16) and output (bf16)."""
+    return 2 * 4 * B * H * K * V + 2 * B * H * (3 * K + V) + 2 * B * H + 2 * B * H * V
+
+
+def _inputs(B, T, H, K, V, state_std, seed, device):
+    import torch
+
+    from tests._inputs import workload
+
+    q, k, v, g, beta, state = workload(B, T, H, K, V, state_std=state_std, seed=seed)
+    dev = lambda t: None if t is None else t.to(device).contiguous()  # noqa: E731
+    return dev(q), dev(k), dev(v), dev(g), dev(beta), dev(state)
+
+
+def bench_prefill(steps, warmup):
+    import torch
+
+    from kda import _lib
+
+    lib = _lib.load()
+    device = torch.device("cuda", 0)
+    q, k, v, g, beta, s0 = _inputs(P_B, P_T, P_H, P_K, P_V, 0.02, 0, device)
+    total = P_B * P_T
+    out = torch.empty(P_B, P_T, P_H, P_V, dtype=torch.bfloat16, device=device)
+    s_out = torch.empty(P_B, P_H, P_K, P_V, dtype=torch.float32, device=device)
+    code = _lib.dtype_code(torch.bfloat16)
+    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(P_B, total, P_H, P_K, P_V, code)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code,
+            s0.data_ptr(), s_out.data_ptr(), 0, out.data_ptr(), None, P_T, None,
+            P_B, total, P_H, P_K, P_V, ws.data_ptr(), ws_bytes, stream)
+
+    def step():
+        _lib.check(lib.kda_chunk_fwd(*args))
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(steps):
+        step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+
+    # per-kernel HIP-event timing on the launch stream
+    kms = (ctypes.c_float * 3)()
+    nk = ctypes.c_int(0)
+    sums = [0.0, 0.0, 0.0]
+    reps = max(5, min(steps, 20))
+    for _ in range(reps):
+        _lib.check(lib.kda_chunk_fwd_profiled(*args, kms, ctypes.byref(nk)))
+        for i in range(3):
+            sums[i] += kms[i]
+    per_kernel = {name: sums[i] / reps for i, name in enumerate(("chunk_map_kernel", "chunk_prepare_kernel",
+                                                                   "chunk_scan_kernel"))}
+    return ms, per_kernel, ws_bytes
+
+
+def bench_decode(warmup):
+    import torch
+
+    from kda import _lib
+
+    lib = _lib.load()
+    device = torch.device("cuda", 0)
+    gen = torch.Generator().manual_seed(1)
+    state = (torch.randn(D_B, D_H, D_K, D_V, generator=gen) * 0.02).to(device)
+    q, k, v, g, beta, _ = _inputs(D_B, D_STEPS, D_H, D_K, D_V, None, 2, device)
+    out = torch.empty(D_B, 1, D_H, D_V, dtype=torch.bfloat16, device=device)
+    code = _lib.dtype_code(torch.bfloat16)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    # one token per sequence per step: slice step t out of the [B, 64, H, *] inputs
+    steps_in = [tuple(x[:, t:t + 1].contiguous() for x in (q, k, v, g, beta)) for t in range(D_STEPS)]
+
+    def step(t):
+        qq, kk, vv, gg, bb = steps_in[t]
+        _lib.check(lib.kda_decode_step(qq.data_ptr(), kk.data_ptr(), vv.data_ptr(), gg.data_ptr(), bb.data_ptr(),
+                                       code, state.data_ptr(), state.data_ptr(), 0, out.data_ptr(),
+                                       D_B, D_H, D_K, D_V, stream))
+
+    for t in range(warmup):
+        step(t % D_STEPS)
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for t in range(D_STEPS):
+        step(t)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / D_STEPS
+
+
+def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
+    """The oracle's CPU restatement, timed like benchmarks/benchmark_kda.py:30-40
+    (one warm-up, then min over repeats of time.perf_counter, inference_mode)."""
+    import torch
+
+    from oracle import kda_oracle as ora
+    from tests._inputs import workload
+
+    threads = max(1, min(16, os.cpu_count() or 1))
+    torch.set_num_threads(threads)
+
+    def timed(fn):
+        with torch.inference_mode():
+            fn()
+            best = float("inf")
+            for _ in range(repeats):
+                t0 = time.perf_counter()
+                fn()
+                best = min(best, time.perf_counter() - t0)
+        return best
+
+    q, k, v, g, beta, s0 = workload(1, prefill_sample_t, P_H, P_K, P_V, state_std=0.02, seed=0)
+    t_pre = timed(lambda: ora.chunkwise(q, k, v, g, beta, s0, chunk_size=64, secondary_tile_size=16))
+    qd, kd, vd, gd, bd, _ = workload(decode_sample_b, 1, D_H, D_K, D_V, seed=2)
+    sd = torch.randn(decode_sample_b, D_H, D_K, D_V) * 0.02
+    t_dec = timed(lambda: ora.recurrent(qd, kd, vd, gd, bd, sd))
+    return {
+        "prefill": {
+            "value": prefill_sample_t / t_pre, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle chunkwise (torch CPU, f32 work) B=1 T={prefill_sample_t} H={P_H} K=V=128 bf16, "
+                      f"min of {repeats} after 1 warm-up",
+        },
+        "decode": {
+            "value": decode_bytes(decode_sample_b, D_H, D_K, D_V) / t_dec / 1e9, "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"oracle recurrent one step (torch CPU) B={decode_sample_b} H={D_H} K=V=128, "
+                      f"min of {repeats} after 1 warm-up",
+        },
+    }
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the KDA operator has no collective; --gpus {args.gpus} "
+              "is not supported: run with --gpus 1)", file=sys.stderr)
+        return 2
+
+    import torch
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 1
+
+    ms, per_kernel, ws_bytes = bench_prefill(args.steps, args.warmup)
+    dec_ms = bench_decode(args.warmup)
+
+    tokens_per_s = P_B * P_T / (ms * 1e-3)
+    pbytes = prefill_bytes(P_B, P_T, P_H, P_K, P_V)
+    pflops = prefill_flops(P_B, P_T, P_H, P_K, P_V)
+    dom = max(("chunk_prepare_kernel", "chunk_scan_kernel"), key=lambda n: per_kernel[n])
+    dom_ms = per_kernel[dom]
+    op_ms = sum(per_kernel.values())
+    dbytes = decode_bytes(D_B, D_H, D_K, D_V)
+    dec_gbs = dbytes / (dec_ms * 1e-3) / 1e9
+
+    result = {
+        "metric": METRIC,
+        "value": round(tokens_per_s, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded q,k L2-normalised, g=-softplus(N(0,1)+2), beta=sigmoid(N(0,1)))",
+        "config": {
+            "workload": "kda chunkwise prefill, long context",
+            "batch": P_B, "tokens": P_T, "heads": P_H, "key_dim": P_K, "value_dim": P_V, "chunk": 64,
+            "inputs": "bf16", "state": "f32 N(0,0.02) initial, final state returned",
+            "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dom,
+            "achieved": round(pbytes / (dom_ms * 1e-3) / 1e9, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(pbytes / (dom_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": None,
+            "algorithmic_bytes": pbytes,
+            "kernel_ms": round(dom_ms, 5),
+        },
+        "roofline_operator": {
+            "bound": "hbm",
+            "kernels_ms": {k: round(v, 5) for k, v in per_kernel.items()},
+            "achieved_gbs": round(pbytes / (op_ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(pbytes / (op_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "achieved_tflops": round(pflops / (op_ms * 1e-3) / 1e12, 2),
+            "frac_bf16_mfma": round(pflops / (op_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "algorithmic_flops": pflops,
+            "workspace_bytes": ws_bytes,
+        },
+        "decode": {
+            "workload": f"decode step B={D_B} H={D_H} K=V=128, f32 state updated in place, {D_STEPS} steps",
+            "value": round(dec_gbs, 1),
+            "unit": "GB/s",
+            "ms_per_step": round(dec_ms, 5),
+            "roofline": {
+                "bound": "hbm", "kernel": "recurrent_kernel", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
+                "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "algorithmic_bytes": dbytes,
+            },
+        },
+    }
+    if not args.no_cpu_baseline:
+        cpu = cpu_baseline()
+        result["cpu_baseline"] = cpu["prefill"]
+        result["decode"]["cpu_baseline"] = cpu["decode"]
+    print(json.dumps(result), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

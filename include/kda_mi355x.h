@@ -117,6 +117,20 @@ int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, co
                   size_t workspace_bytes, void* stream);
 
 /*
+ * `kda_chunk_fwd` with a HIP event recorded between its kernels; returns,
+ * after synchronising `stream`, the duration of each kernel in
+ * kernel_ms[0..2] (chunk map, prepare, scan; zeros for kernels the call did
+ * not launch) and how many kernels ran in *num_kernels.  No reference
+ * counterpart: it exists so that a benchmark can attribute time per kernel.
+ */
+int kda_chunk_fwd_profiled(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                           int in_dtype, const void* initial_state, void* final_state, int state_dtype,
+                           void* out, const int32_t* cu_seqlens, int64_t dense_span,
+                           const int32_t* valid_lens, int64_t num_seqs, int64_t total_tokens,
+                           int64_t heads, int64_t key_dim, int64_t value_dim, void* workspace,
+                           size_t workspace_bytes, void* stream, float* kernel_ms, int* num_kernels);
+
+/*
  * UT transform of independent chunks, canonical [B,C,H,*] inputs.
  * Replaces `ut_transform` (src/kda/ut_transform.py:61-92).  Outputs, in
  * `out_dtype` (f32 for bf16/f16/f32 inputs, f64 for f64):

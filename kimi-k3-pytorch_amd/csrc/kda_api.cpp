@@ -164,6 +164,48 @@ int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, co
                       static_cast<hipStream_t>(stream));
 }
 
+int kda_chunk_fwd_profiled(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                           const void* initial_state, void* final_state, int state_dtype, void* out,
+                           const int32_t* cu_seqlens, int64_t dense_span, const int32_t* valid_lens, int64_t num_seqs,
+                           int64_t total_tokens, int64_t heads, int64_t key_dim, int64_t value_dim, void* workspace,
+                           size_t workspace_bytes, void* stream, float* kernel_ms, int* num_kernels) {
+  if (kernel_ms == nullptr || num_kernels == nullptr) {
+    g_detail[0] = '\0';
+    set_detail("kernel_ms and num_kernels must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  int st = check_common(q, k, v, g, beta, in_dtype, state_dtype, out, num_seqs, total_tokens, heads, key_dim,
+                        value_dim);
+  if (st != KDA_OK) return st;
+  st = check_seq(cu_seqlens, dense_span, num_seqs, total_tokens);
+  if (st != KDA_OK) return st;
+  const size_t need = chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    set_detail("chunk_fwd needs %zu workspace bytes, got %zu", need, workspace_bytes);
+    return KDA_ERR_WORKSPACE;
+  }
+  KernelEvents ev;
+  ev.n_launched = 0;
+  for (auto& e : ev.ev) {
+    if (hipEventCreate(&e) != hipSuccess) {
+      set_detail("hipEventCreate failed");
+      return KDA_ERR_LAUNCH;
+    }
+  }
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
+  st = launch_chunk(q, k, v, g, beta, in_dtype, initial_state, final_state, state_dtype, out, seq, num_seqs,
+                    total_tokens, heads, key_dim, value_dim, workspace, workspace_bytes, s, &ev);
+  for (int i = 0; i < 3; ++i) kernel_ms[i] = 0.f;
+  *num_kernels = 0;
+  if (st == KDA_OK && hipStreamSynchronize(s) == hipSuccess) {
+    *num_kernels = ev.n_launched;
+    for (int i = 0; i < ev.n_launched && i < 3; ++i) (void)hipEventElapsedTime(&kernel_ms[i], ev.ev[i], ev.ev[i + 1]);
+  }
+  for (auto& e : ev.ev) (void)hipEventDestroy(e);
+  return st;
+}
+
 int kda_ut_transform(const void* k, const void* v, const void* g, const void* beta, int in_dtype, void* M, void* U,
                      void* W, void* log_gamma, void* k_gamma, int out_dtype, int64_t batch, int64_t count,
                      int64_t heads, int64_t key_dim, int64_t value_dim, void* stream) {

@@ -578,15 +578,24 @@ static bool mfma_path(int in_dtype, int state_dtype, int64_t K, int64_t V) {
 
 static size_t map_bytes(int64_t N) { return static_cast<size_t>(((N + 1) * 4 + 255) / 256 * 256); }
 
+static void mark(kda_host::KernelEvents* ev, int i, hipStream_t stream) {
+  if (ev != nullptr) {
+    (void)hipEventRecord(ev->ev[i], stream);
+    ev->n_launched = i;
+  }
+}
+
 template <class IT>
 static int run_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, const void* s_in,
                      void* s_out, void* out, const SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
-                     int64_t V, void* workspace, hipStream_t stream) {
+                     int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev) {
   int32_t* chunk_start = static_cast<int32_t*>(workspace);
   unsigned char* records = static_cast<unsigned char*>(workspace) + map_bytes(N);
+  mark(ev, 0, stream);
   hipLaunchKernelGGL(chunk_map_kernel, dim3(1), dim3(1024), 0, stream, seq, N, chunk_start);
   int st = kda_host::check_launch("chunk_map_kernel");
   if (st != KDA_OK) return st;
+  mark(ev, 1, stream);
 
   static bool attr_done = false;
   const size_t smem = sizeof(PrepSmem);
@@ -615,6 +624,7 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
                      dim3(kPrepThreads), smem, stream, pa);
   st = kda_host::check_launch("chunk_prepare_kernel");
   if (st != KDA_OK) return st;
+  mark(ev, 2, stream);
 
   ScanArgs<IT> sa;
   sa.out = static_cast<IT*>(out);
@@ -628,7 +638,9 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
   sa.V = V;
   const int64_t blocks = N * H * (V / 16);
   hipLaunchKernelGGL(chunk_scan_kernel<IT>, dim3(static_cast<unsigned>(blocks)), dim3(64), 0, stream, sa);
-  return kda_host::check_launch("chunk_scan_kernel");
+  st = kda_host::check_launch("chunk_scan_kernel");
+  mark(ev, 3, stream);
+  return st;
 }
 
 }  // namespace kda
@@ -646,11 +658,15 @@ size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t hea
 int launch_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
                  const void* s_in, void* s_out, int state_dtype, void* out, const kda::SeqDesc& seq, int64_t N,
                  int64_t total_tokens, int64_t H, int64_t K, int64_t V, void* workspace, size_t workspace_bytes,
-                 hipStream_t stream) {
+                 hipStream_t stream, KernelEvents* ev) {
   using namespace kda;
-  if (!mfma_path(in_dtype, state_dtype, K, V))
-    return launch_recurrent(q, k, v, g, beta, in_dtype, s_in, s_out, state_dtype, out, nullptr, seq, N, H, K, V,
-                            stream, false);
+  if (!mfma_path(in_dtype, state_dtype, K, V)) {
+    mark(ev, 0, stream);
+    const int st = launch_recurrent(q, k, v, g, beta, in_dtype, s_in, s_out, state_dtype, out, nullptr, seq, N, H,
+                                    K, V, stream, false);
+    mark(ev, 1, stream);
+    return st;
+  }
   if (workspace_bytes < chunk_workspace_bytes(N, total_tokens, H, K, V, in_dtype)) {
     set_detail("chunk_fwd: workspace too small");
     return KDA_ERR_WORKSPACE;
@@ -660,8 +676,8 @@ int launch_chunk(const void* q, const void* k, const void* v, const void* g, con
     return KDA_ERR_UNSUPPORTED;
   }
   if (in_dtype == KDA_DTYPE_BF16)
-    return run_chunk<bf16>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream);
-  return run_chunk<f16>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream);
+    return run_chunk<bf16>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream, ev);
+  return run_chunk<f16>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream, ev);
 }
 
 }  // namespace kda_host

@@ -18,10 +18,17 @@ int launch_recurrent(const void* q, const void* k, const void* v, const void* g,
 size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
                              int64_t value_dim, int in_dtype);
 
+// Optional per-kernel timing: events[i] is recorded before kernel i and
+// events[n] after the last one; *n_launched receives n.
+struct KernelEvents {
+  hipEvent_t ev[4];
+  int n_launched;
+};
+
 int launch_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
                  const void* s_in, void* s_out, int state_dtype, void* out, const kda::SeqDesc& seq, int64_t N,
                  int64_t total_tokens, int64_t H, int64_t K, int64_t V, void* workspace, size_t workspace_bytes,
-                 hipStream_t stream);
+                 hipStream_t stream, KernelEvents* events = nullptr);
 
 int launch_ut_transform(const void* k, const void* v, const void* g, const void* beta, int in_dtype, void* M,
                         void* U, void* W, void* log_gamma, void* k_gamma, int out_dtype, int64_t batch,

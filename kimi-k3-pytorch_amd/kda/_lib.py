@@ -47,6 +47,10 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P, _S, _P],
     ),
+    "kda_chunk_fwd_profiled": (
+        _I,
+        [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P, _S, _P, _P, _P],
+    ),
     "kda_ut_transform": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _P]),
 }
 
