@@ -82,8 +82,10 @@ __device__ __forceinline__ V negate_bf16(V x) {
 
 template <class IT>
 __device__ __forceinline__ void load_pair(const IT* p, float& lo, float& hi) {
-  lo = to_float(p[0]);
-  hi = to_float(p[1]);
+  typedef IT pair_t __attribute__((ext_vector_type(2)));
+  const pair_t x = *reinterpret_cast<const pair_t*>(p);
+  lo = to_float(x[0]);
+  hi = to_float(x[1]);
 }
 
 // ---- chunk map ------------------------------------------------------------
@@ -132,24 +134,35 @@ struct PrepSmem {
   bf16 L[kChunk][72];    // beta_i * A_ij, strict lower (bf16, MFMA A operand)
   float Ld[4][16][16];   // diagonal blocks of L in f32 (for the block inverses)
   bf16 Tinv[4][16][16];  // inverses of the unit-lower diagonal blocks of L
-  float G[4][kKey];      // exp(lg_{16J+15} - lg_{16J-1})  (block decay incl. its first row)
-  float A0[4][kKey];     // alpha at the first row of block J
-  float P[4][kKey];      // exp(lg_{16J+15} - lg_{16J})
-  float Gs[4][kKey];     // exp(lg_{16J})  (chunk start to block start, inclusive)
-  float Ge[4][kKey];     // exp(lg_63 - lg_{16J+15})
+  // Per-channel block factors.  G, A0 and P are only read while building Gs,
+  // Ge and the pair scales; the pair scales then overlay them (each thread
+  // owns one channel column of all of them, so the overlay needs no barrier).
+  union {
+    struct {
+      float G[4][kKey];   // exp(lg_{16J+15} - lg_{16J-1})  (block decay incl. its first row)
+      float A0[4][kKey];  // alpha at the first row of block J
+      float P[4][kKey];   // exp(lg_{16J+15} - lg_{16J})
+    };
+    float Sc[10][kKey];   // per block pair (I, J <= I): D_IJ (J < I) or 1 / P_I (J = I)
+  };
+  float Gs[4][kKey];      // exp(lg_{16J})  (chunk start to block start, inclusive)
+  float Ge[4][kKey];      // exp(lg_63 - lg_{16J+15})
   float beta[kChunk];
 };
 
+// two prepare workgroups must fit in the 160 KB of LDS of one CU
+static_assert(2 * sizeof(PrepSmem) <= 160 * 1024, "prepare kernel LDS no longer allows two workgroups per CU");
+
 template <class IT>
 struct PrepArgs {
-  const IT* q;
-  const IT* k;
-  const IT* v;
-  const IT* g;
-  const IT* beta;
+  const IT* __restrict__ q;
+  const IT* __restrict__ k;
+  const IT* __restrict__ v;
+  const IT* __restrict__ g;
+  const IT* __restrict__ beta;
   SeqDesc seq;
-  const int32_t* chunk_start;
-  unsigned char* records;
+  const int32_t* __restrict__ chunk_start;
+  unsigned char* __restrict__ records;
   int64_t N, H, V;
 };
 
@@ -182,18 +195,28 @@ __global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const Pr
     const int J = wave;
     const int cp = lane;
     float gv[2][16], kv[2][16], qv[2][16];
+    {
+      // all 48 paired loads are issued before any use (tokens past the valid
+      // range read row tok0 instead and are zeroed afterwards)
+      typedef IT pair_t __attribute__((ext_vector_type(2)));
+      pair_t gp[16], kp[16], qp[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int tl = 16 * J + r;
-      if (tl < n_valid) {
-        const int64_t off = (tok0 + tl) * krow + h * kKey + 2 * cp;
-        load_pair(a.g + off, gv[0][r], gv[1][r]);
-        load_pair(a.k + off, kv[0][r], kv[1][r]);
-        load_pair(a.q + off, qv[0][r], qv[1][r]);
-      } else {
-        gv[0][r] = gv[1][r] = 0.f;
-        kv[0][r] = kv[1][r] = 0.f;
-        qv[0][r] = qv[1][r] = 0.f;
+      for (int r = 0; r < 16; ++r) {
+        const int tl = 16 * J + r;
+        const int64_t off = (tok0 + (tl < n_valid ? tl : 0)) * krow + h * kKey + 2 * cp;
+        gp[r] = *reinterpret_cast<const pair_t*>(a.g + off);
+        kp[r] = *reinterpret_cast<const pair_t*>(a.k + off);
+        qp[r] = *reinterpret_cast<const pair_t*>(a.q + off);
+      }
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const bool ok = 16 * J + r < n_valid;
+#pragma unroll
+        for (int ch = 0; ch < 2; ++ch) {
+          gv[ch][r] = ok ? to_float(gp[r][ch]) : 0.f;
+          kv[ch][r] = ok ? to_float(kp[r][ch]) : 0.f;
+          qv[ch][r] = ok ? to_float(qp[r][ch]) : 0.f;
+        }
       }
     }
     float ka[2][16], qa[2][16], ke[2][16];
@@ -236,19 +259,44 @@ __global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const Pr
   // ---- P1b: block-level decay tables and gamma_C ---------------------------
   if (tid < kKey) {
     const int cc = tid;
+    float G[4], A0[4], P[4];
+#pragma unroll
+    for (int J = 0; J < 4; ++J) {
+      G[J] = sm.G[J][cc];
+      A0[J] = sm.A0[J][cc];
+      P[J] = sm.P[J][cc];
+    }
     float pre = 1.f;
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
-      sm.Gs[J][cc] = pre * sm.A0[J][cc];
-      pre *= sm.G[J][cc];
+      sm.Gs[J][cc] = pre * A0[J];
+      pre *= G[J];
     }
     float post = 1.f;
 #pragma unroll
     for (int J = 3; J >= 0; --J) {
       sm.Ge[J][cc] = post;
-      post *= sm.G[J][cc];
+      post *= G[J];
     }
     reinterpret_cast<float*>(rec + rec_gam(a.V))[cc] = pre;  // exp(lg_63)
+    // scale of the k_j E_j operand for block pair (I, J): D_IJ = alpha_{16I} prod_{J<J'<I} G_J'
+    // for J < I, 1 / P_I on the diagonal (written over G/A0/P of this same channel)
+    int pidx = 0;
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+#pragma unroll
+      for (int J = 0; J <= I; ++J, ++pidx) {
+        float sc;
+        if (J < I) {
+          sc = A0[I];
+#pragma unroll
+          for (int jj = J + 1; jj < I; ++jj) sc *= G[jj];
+        } else {
+          sc = P[I] > 0.f ? 1.f / P[I] : 0.f;
+        }
+        sm.Sc[pidx][cc] = sc;
+      }
+    }
   }
   __syncthreads();
 
@@ -280,29 +328,23 @@ __global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const Pr
 
   // ---- P2: A (strict) and Aqk (causal) 16x16 blocks on MFMA ---------------
   {
-    constexpr int PI[10] = {0, 1, 1, 2, 2, 2, 3, 3, 3, 3};
-    constexpr int PJ[10] = {0, 0, 1, 0, 1, 2, 0, 1, 2, 3};
     for (int p = wave; p < 10; p += 4) {
-      const int I = PI[p], J = PJ[p];
+      // block pair p = I (I + 1) / 2 + J, J <= I
+      const int I = p >= 6 ? 3 : (p >= 3 ? 2 : (p >= 1 ? 1 : 0));
+      const int J = p - I * (I + 1) / 2;
       f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
       f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
         const int c0 = 32 * st + 8 * g4;
         const bf16x8_t ke = *reinterpret_cast<const bf16x8_t*>(&sm.KE[16 * J + n16][c0]);
+        const f32x4_t sc0 = *reinterpret_cast<const f32x4_t*>(&sm.Sc[p][c0]);
+        const f32x4_t sc1 = *reinterpret_cast<const f32x4_t*>(&sm.Sc[p][c0 + 4]);
         bf16x8_t af;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const int cc = c0 + e;
-          float sc;
-          if (J < I) {
-            sc = sm.A0[I][cc];
-            for (int jj = J + 1; jj < I; ++jj) sc *= sm.G[jj][cc];
-          } else {
-            const float pb = sm.P[I][cc];
-            sc = pb > 0.f ? 1.f / pb : 0.f;
-          }
-          af[e] = (bf16)((float)ke[e] * sc);
+        for (int e = 0; e < 4; ++e) {
+          af[e] = (bf16)((float)ke[e] * sc0[e]);
+          af[4 + e] = (bf16)((float)ke[4 + e] * sc1[e]);
         }
         const bf16x8_t kb = *reinterpret_cast<const bf16x8_t*>(&sm.KA[16 * I + n16][c0]);
         const bf16x8_t qb = *reinterpret_cast<const bf16x8_t*>(&sm.QA[16 * I + n16][c0]);
@@ -400,6 +442,19 @@ __global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const Pr
     for (int nt = wave; nt < n_tiles; nt += 4) {
       const bool is_w = nt < 8;
       const int col = 16 * (is_w ? nt : nt - 8) + n16;
+      // right-hand side diag(beta) [Kgamma | v] of this column tile, loaded up front
+      float rhs[4][4];
+#pragma unroll
+      for (int I = 0; I < 4; ++I) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int tl = 16 * I + 4 * g4 + r;
+          if (is_w)
+            rhs[I][r] = (float)sm.KA[tl][col] * sm.Gs[I][col];
+          else
+            rhs[I][r] = to_float(a.v[(tok0 + (tl < n_valid ? tl : 0)) * vrow + h * a.V + col]);
+        }
+      }
       f32x4_t X[4];
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
@@ -407,13 +462,7 @@ __global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const Pr
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tl = 16 * I + 4 * g4 + r;
-          const float b = sm.beta[tl];
-          float val;
-          if (is_w)
-            val = (float)sm.KA[tl][col] * sm.Gs[I][col];
-          else
-            val = tl < n_valid ? to_float(a.v[(tok0 + tl) * vrow + h * a.V + col]) : 0.f;
-          acc[r] = val * b;
+          acc[r] = (tl < n_valid ? rhs[I][r] : 0.f) * sm.beta[tl];
         }
 #pragma unroll
         for (int J = 0; J < I; ++J) {
@@ -453,6 +502,20 @@ __global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const Pr
 }
 
 // ---- scan kernel ----------------------------------------------------------
+// One workgroup of two waves per (sequence, head, 32 value columns); wave w
+// owns the 16-column state slice S[:, 16 (2 wp + w) .. +16] in accumulator
+// registers.  The shared part of each chunk record (W, Q, KT, A fragments),
+// the workgroup's two U tiles and gamma (60.5 KB) are copied into LDS with
+// direct global->LDS loads one chunk ahead (two LDS buffers, two distinct
+// __shared__ arrays so the compiler can tell the in-flight copy from the
+// buffer being read), and records three chunks ahead are touched once so
+// that the copy hits L2.
+constexpr int kScanWaves = 2;
+constexpr int kScanThreads = 64 * kScanWaves;
+constexpr int kScanShared = 57344;                          // W | Q | KT | A
+constexpr int kScanBuf = kScanShared + 2 * 2048 + 512;      // + two U tiles + gamma = 61952 B
+constexpr int kScanPrefetch = 3;
+
 template <class IT>
 struct ScanArgs {
   IT* out;
@@ -464,22 +527,180 @@ struct ScanArgs {
   int64_t N, H, V;
 };
 
+// copy one chunk's record pieces into an LDS buffer (all threads of the workgroup)
+__device__ __forceinline__ void scan_copy(const unsigned char* rec, unsigned char* buf, int64_t vt0, int ntiles,
+                                          int64_t gam_off, int tid) {
+  const int wave = tid >> 6, lane = tid & 63;
+  // W | Q | KT | A : 3584 16-byte units, 28 per thread
+#pragma unroll 4
+  for (int i = 0; i < kScanShared / (16 * kScanThreads); ++i) {
+    const int u = i * kScanThreads + wave * 64;
+    __builtin_amdgcn_global_load_lds(rec + (u + lane) * 16, buf + u * 16, 16, 0, 0);
+  }
+  // U tiles of this workgroup's (up to) two value slices: 128 units per tile
+  for (int t = 0; t < ntiles; ++t) {
+    const int u = t * 128 + wave * 64;
+    __builtin_amdgcn_global_load_lds(rec + kRecU + vt0 * 2048 + (u + lane) * 16, buf + kScanShared + u * 16, 16, 0,
+                                     0);
+  }
+  // gamma: 32 units
+  if (wave == 0 && lane < 32)
+    __builtin_amdgcn_global_load_lds(rec + gam_off + lane * 16, buf + kScanShared + 4096, 16, 0, 0);
+}
+
+// touch one dword of every 128-byte line of a future record so that its copy
+// hits L2; the loaded words land in a scratch LDS area and are never read
+constexpr int kWarmLoads = 4;  // per thread: 4 x 128 threads x 128 B lines cover the 56 KB shared part
+__device__ __forceinline__ void scan_warm_l2(const unsigned char* rec, unsigned char* scratch, int tid) {
+  const int wave = tid >> 6;
+#pragma unroll
+  for (int k = 0; k < kWarmLoads; ++k) {
+    int off = tid * 128 + k * kScanThreads * 128;
+    off = off < kScanShared - 4 ? off : kScanShared - 4;
+    __builtin_amdgcn_global_load_lds(rec + off, scratch + wave * 256, 4, 0, 0);
+  }
+}
+
+// Wait until only the kWarmLoads L2-warming loads of this step may still be
+// in flight (vector memory operations of a wave retire in issue order, and a
+// step issues its output stores, then the record copy, then the warming
+// loads, so the stores and the copy are complete), drain LDS traffic, then
+// barrier.  The asm statements keep the
+// compiler from moving memory accesses across the barrier.
+__device__ __forceinline__ void scan_step_barrier() {
+  asm volatile("" ::: "memory");
+  // s_waitcnt vmcnt(4) expcnt(7) lgkmcnt(0)
+  __builtin_amdgcn_s_waitcnt((kWarmLoads & 15) | (7 << 4) | (0 << 8) | ((kWarmLoads >> 4) << 14));
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
+// store a chunk's 64 x 16 output tile from its accumulator layout
+// (lane (n, g) holds rows 16 I + 4 g + r of column n)
 template <class IT>
-__global__ __launch_bounds__(64) void chunk_scan_kernel(const ScanArgs<IT> a) {
+__device__ __forceinline__ void scan_store_out(const f32x4_t (&O)[4], IT* out, int64_t tokbase, int64_t n_span,
+                                               int64_t H, int64_t h, int64_t V, int64_t col, int lane) {
+  const int g4 = lane >> 4;
+#pragma unroll
+  for (int I = 0; I < 4; ++I) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t tl = 16 * I + 4 * g4 + r;
+      if (tl < n_span) out[((tokbase + tl) * H + h) * V + col] = from_compute<IT>(O[I][r]);
+    }
+  }
+}
+
+template <class IT>
+__device__ __forceinline__ void scan_chunk(const unsigned char* buf, f32x4_t (&S)[8], int w, int lane,
+                                           f32x4_t (&O)[4]) {
+  // Fragment loads are batched per phase ahead of the MFMAs that use them so
+  // that LDS latency overlaps instead of being paid per product.
+  bf16x8_t wf[4][4], qf[4][4], af[6];
+  bf16x4_t uf[4];
+#pragma unroll
+  for (int I = 0; I < 4; ++I) {
+    uf[I] = *reinterpret_cast<const bf16x4_t*>(buf + kScanShared + w * 2048 + (I * 64 + lane) * 8);
+#pragma unroll
+    for (int st = 0; st < 4; ++st) {
+      wf[I][st] = *reinterpret_cast<const bf16x8_t*>(buf + kRecW + ((I * 4 + st) * 64 + lane) * 16);
+      qf[I][st] = *reinterpret_cast<const bf16x8_t*>(buf + kRecQ + ((I * 4 + st) * 64 + lane) * 16);
+    }
+  }
+  // Aqk fragments actually used: (I, s') for s' <= I / 2 -> slots 0, 2, 4, 5, 6, 7
+#pragma unroll
+  for (int j = 0; j < 6; ++j) {
+    const int slot = j < 2 ? 2 * j : j + 2;
+    af[j] = *reinterpret_cast<const bf16x8_t*>(buf + kRecA + (slot * 64 + lane) * 16);
+  }
+  bf16x8_t Sb[4];
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      Sb[st][r] = (bf16)S[2 * st][r];
+      Sb[st][4 + r] = (bf16)S[2 * st + 1][r];
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);  // keep the fragment loads ahead of the products
+  f32x4_t Vt[4];
+#pragma unroll
+  for (int I = 0; I < 4; ++I) {
+    Vt[I] = f32x4_t{(float)uf[I][0], (float)uf[I][1], (float)uf[I][2], (float)uf[I][3]};
+    O[I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  }
+#pragma unroll
+  for (int st = 0; st < 4; ++st) {
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      Vt[I] = mfma32(negate_bf16(wf[I][st]), Sb[st], Vt[I]);
+      O[I] = mfma32(qf[I][st], Sb[st], O[I]);
+    }
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  // K~^T fragments and gamma for the state update
+  bf16x8_t kf[8][2];
+  f32x4_t gm[8];
+  const int g4 = lane >> 4;
+  const float* gam = reinterpret_cast<const float*>(buf + kScanShared + 4096);
+#pragma unroll
+  for (int ct = 0; ct < 8; ++ct) {
+    gm[ct] = *reinterpret_cast<const f32x4_t*>(gam + 16 * ct + 4 * g4);
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+      kf[ct][st] = *reinterpret_cast<const bf16x8_t*>(buf + kRecKT + ((ct * 2 + st) * 64 + lane) * 16);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+  bf16x8_t Vb[2];
+#pragma unroll
+  for (int st = 0; st < 2; ++st) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      Vb[st][r] = (bf16)Vt[2 * st][r];
+      Vb[st][4 + r] = (bf16)Vt[2 * st + 1][r];
+    }
+  }
+  O[0] = mfma32(af[0], Vb[0], O[0]);
+  O[1] = mfma32(af[1], Vb[0], O[1]);
+  O[2] = mfma32(af[2], Vb[0], O[2]);
+  O[2] = mfma32(af[3], Vb[1], O[2]);
+  O[3] = mfma32(af[4], Vb[0], O[3]);
+  O[3] = mfma32(af[5], Vb[1], O[3]);
+#pragma unroll
+  for (int ct = 0; ct < 8; ++ct) {
+    S[ct] *= gm[ct];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) S[ct] = mfma32(kf[ct][st], Vb[st], S[ct]);
+  }
+}
+
+template <class IT>
+__global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const ScanArgs<IT> a) {
+  __shared__ __align__(16) unsigned char buf0[kScanBuf];
+  __shared__ __align__(16) unsigned char buf1[kScanBuf];
+  __shared__ __align__(16) unsigned char warm[kScanWaves * 256];
   const int64_t nvt = a.V / 16;
+  const int64_t nwp = (nvt + kScanWaves - 1) / kScanWaves;  // workgroups per (sequence, head)
   const int64_t bid = blockIdx.x;
-  const int64_t vt = bid % nvt;
-  const int64_t h = (bid / nvt) % a.H;
-  const int64_t s = bid / (nvt * a.H);
-  const int lane = threadIdx.x;
+  const int64_t wp = bid % nwp;
+  const int64_t h = (bid / nwp) % a.H;
+  const int64_t s = bid / (nwp * a.H);
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int w = tid >> 6;
   const int n16 = lane & 15;
   const int g4 = lane >> 4;
+  const int64_t vt0 = wp * kScanWaves;
+  const int ntiles = static_cast<int>(nvt - vt0 < kScanWaves ? nvt - vt0 : kScanWaves);
+  const bool active = w < ntiles;
   const SeqRange sr = seq_range(a.seq, s);
   const int64_t c0 = a.chunk_start[s];
   const int64_t c1 = a.chunk_start[s + 1];
   const int64_t rb = rec_bytes(a.V);
-  const int64_t col = 16 * vt + n16;
+  const int64_t gam_off = rec_gam(a.V);
+  const int64_t col = 16 * (vt0 + w) + n16;
   const int64_t sbase = (s * a.H + h) * kKey * a.V;
+  auto rec_of = [&](int64_t c) { return a.records + (c * a.H + h) * rb; };
 
   f32x4_t S[8];
 #pragma unroll
@@ -487,76 +708,43 @@ __global__ __launch_bounds__(64) void chunk_scan_kernel(const ScanArgs<IT> a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int64_t row = 16 * ct + 4 * g4 + r;
-      S[ct][r] = a.s_in ? a.s_in[sbase + row * a.V + col] : 0.f;
+      S[ct][r] = (a.s_in && active) ? a.s_in[sbase + row * a.V + col] : 0.f;
     }
   }
 
+  // warm L2 for the first chunks, then fill buffer 0
+  for (int64_t p = c0 + 1; p < c1 && p <= c0 + kScanPrefetch; ++p) scan_warm_l2(rec_of(p), warm, tid);
+  if (c0 < c1) scan_copy(rec_of(c0), buf0, vt0, ntiles, gam_off, tid);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+
+  f32x4_t O[4];
+  int64_t prev_tok = -1, prev_span = 0;  // the output tile of the previous chunk, still in O
+  // one step: store the previous chunk's output, start copying chunk c + 1
+  // into the other buffer, warm L2 for a later chunk, compute chunk c.  The
+  // loop is unrolled by two so that each half names its LDS buffers
+  // statically (the copy target never aliases the buffer being read).
+#define KDA_SCAN_STEP(CUR, NXT)                                                                              \
+  {                                                                                                          \
+    if (active && prev_tok >= 0)                                                                             \
+      scan_store_out<IT>(O, a.out, prev_tok, prev_span, a.H, h, a.V, col, lane);                             \
+    if (c + 1 < c1) scan_copy(rec_of(c + 1), NXT, vt0, ntiles, gam_off, tid);                                \
+    scan_warm_l2(rec_of(c + 1 + kScanPrefetch < c1 ? c + 1 + kScanPrefetch : c1 - 1), warm, tid);            \
+    const int64_t lc = c - c0;                                                                               \
+    if (active) scan_chunk<IT>(CUR, S, w, lane, O);                                                          \
+    prev_tok = sr.start + kChunk * lc;                                                                       \
+    prev_span = sr.span - kChunk * lc < kChunk ? sr.span - kChunk * lc : kChunk;                             \
+    scan_step_barrier();                                                                                     \
+  }
   for (int64_t c = c0; c < c1; ++c) {
-    const int64_t lc = c - c0;
-    const int64_t tokbase = sr.start + kChunk * lc;
-    const int64_t n_span = sr.span - kChunk * lc < kChunk ? sr.span - kChunk * lc : kChunk;
-    const unsigned char* rec = a.records + (c * a.H + h) * rb;
-
-    bf16x8_t Sb[4];
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        Sb[st][r] = (bf16)S[2 * st][r];
-        Sb[st][4 + r] = (bf16)S[2 * st + 1][r];
-      }
-    }
-    f32x4_t Vt[4], O[4];
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-      const bf16x4_t u = *reinterpret_cast<const bf16x4_t*>(rec + kRecU + ((vt * 4 + I) * 64 + lane) * 8);
-      Vt[I] = f32x4_t{(float)u[0], (float)u[1], (float)u[2], (float)u[3]};
-      O[I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const bf16x8_t w =
-            negate_bf16(*reinterpret_cast<const bf16x8_t*>(rec + kRecW + ((I * 4 + st) * 64 + lane) * 16));
-        const bf16x8_t qf = *reinterpret_cast<const bf16x8_t*>(rec + kRecQ + ((I * 4 + st) * 64 + lane) * 16);
-        Vt[I] = mfma32(w, Sb[st], Vt[I]);
-        O[I] = mfma32(qf, Sb[st], O[I]);
-      }
-    }
-    bf16x8_t Vb[2];
-#pragma unroll
-    for (int st = 0; st < 2; ++st) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        Vb[st][r] = (bf16)Vt[2 * st][r];
-        Vb[st][4 + r] = (bf16)Vt[2 * st + 1][r];
-      }
-    }
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-#pragma unroll
-      for (int st = 0; st <= I / 2; ++st) {
-        const bf16x8_t af = *reinterpret_cast<const bf16x8_t*>(rec + kRecA + ((I * 2 + st) * 64 + lane) * 16);
-        O[I] = mfma32(af, Vb[st], O[I]);
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t tl = 16 * I + 4 * g4 + r;
-        if (tl < n_span) a.out[((tokbase + tl) * a.H + h) * a.V + col] = from_compute<IT>(O[I][r]);
-      }
-    }
-    const float* gam = reinterpret_cast<const float*>(rec + rec_gam(a.V));
-#pragma unroll
-    for (int ct = 0; ct < 8; ++ct) {
-      const f32x4_t gm = *reinterpret_cast<const f32x4_t*>(gam + 16 * ct + 4 * g4);
-      S[ct] *= gm;
-#pragma unroll
-      for (int st = 0; st < 2; ++st) {
-        const bf16x8_t kf = *reinterpret_cast<const bf16x8_t*>(rec + kRecKT + ((ct * 2 + st) * 64 + lane) * 16);
-        S[ct] = mfma32(kf, Vb[st], S[ct]);
-      }
-    }
+    KDA_SCAN_STEP(buf0, buf1)
+    if (++c >= c1) break;
+    KDA_SCAN_STEP(buf1, buf0)
   }
+#undef KDA_SCAN_STEP
+  if (active && prev_tok >= 0) scan_store_out<IT>(O, a.out, prev_tok, prev_span, a.H, h, a.V, col, lane);
 
-  if (a.s_out) {
+  if (a.s_out && active) {
 #pragma unroll
     for (int ct = 0; ct < 8; ++ct) {
 #pragma unroll
@@ -636,8 +824,8 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
   sa.N = N;
   sa.H = H;
   sa.V = V;
-  const int64_t blocks = N * H * (V / 16);
-  hipLaunchKernelGGL(chunk_scan_kernel<IT>, dim3(static_cast<unsigned>(blocks)), dim3(64), 0, stream, sa);
+  const int64_t blocks = N * H * ((V / 16 + kScanWaves - 1) / kScanWaves);
+  hipLaunchKernelGGL(chunk_scan_kernel<IT>, dim3(static_cast<unsigned>(blocks)), dim3(kScanThreads), 0, stream, sa);
   st = kda_host::check_launch("chunk_scan_kernel");
   mark(ev, 3, stream);
   return st;
