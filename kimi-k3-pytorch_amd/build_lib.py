@@ -34,6 +34,9 @@ COMMON_FLAGS = [
     # Packed FP32 VALU ops are not generated (device pass only; the host pass
     # warns that it does not know the feature).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # keep MFMA accumulators in ordinary VGPRs instead of round-tripping them
+    # through AGPRs (the state-scan loop converts and rescales them every chunk)
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
 ]
 
 

@@ -436,57 +436,91 @@ __global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const Pr
   __syncthreads();
 
   // ---- P4: blocked forward substitution  [W | U] = L^{-1} diag(beta) [Kgamma | v]
+  // Wave w owns column tiles nt = w, w+4, ... of the 8 + V/16 tiles (8 key
+  // tiles of W, V/16 value tiles of U) and walks the four row blocks once for
+  // all of them, so the L and inverse fragments are read once per block and
+  // the column tiles form independent MFMA chains.
   {
+    constexpr int kMaxT = 6;  // up to (8 + 256/16) / 4 column tiles per wave
     const int n_tiles = 8 + static_cast<int>(a.V / 16);
     const int64_t vrow = a.H * a.V;
-    for (int nt = wave; nt < n_tiles; nt += 4) {
+    int nts[kMaxT];
+    int nown = 0;
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t) {
+      nts[t] = wave + 4 * t;
+      if (nts[t] < n_tiles) ++nown;
+    }
+    // right-hand sides diag(beta) [Kgamma | v], loaded up front
+    float rhs[kMaxT][4][4];
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t) {
+      if (t >= nown) {
+#pragma unroll
+        for (int I = 0; I < 4; ++I)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) rhs[t][I][r] = 0.f;
+        continue;
+      }
+      const int nt = nts[t];
       const bool is_w = nt < 8;
       const int col = 16 * (is_w ? nt : nt - 8) + n16;
-      // right-hand side diag(beta) [Kgamma | v] of this column tile, loaded up front
-      float rhs[4][4];
 #pragma unroll
       for (int I = 0; I < 4; ++I) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int tl = 16 * I + 4 * g4 + r;
+          float val;
           if (is_w)
-            rhs[I][r] = (float)sm.KA[tl][col] * sm.Gs[I][col];
+            val = (float)sm.KA[tl][col] * sm.Gs[I][col];
           else
-            rhs[I][r] = to_float(a.v[(tok0 + (tl < n_valid ? tl : 0)) * vrow + h * a.V + col]);
+            val = to_float(a.v[(tok0 + (tl < n_valid ? tl : 0)) * vrow + h * a.V + col]);
+          rhs[t][I][r] = (tl < n_valid ? val : 0.f) * sm.beta[tl];
         }
       }
-      f32x4_t X[4];
+    }
+    f32x4_t X[kMaxT][4];
 #pragma unroll
-      for (int I = 0; I < 4; ++I) {
-        f32x4_t acc;
+    for (int I = 0; I < 4; ++I) {
+      f32x4_t acc[kMaxT];
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tl = 16 * I + 4 * g4 + r;
-          acc[r] = (tl < n_valid ? rhs[I][r] : 0.f) * sm.beta[tl];
+      for (int t = 0; t < kMaxT; ++t) acc[t] = f32x4_t{rhs[t][I][0], rhs[t][I][1], rhs[t][I][2], rhs[t][I][3]};
+#pragma unroll
+      for (int J = 0; J < I; ++J) {
+        const bf16x4_t la = negate_bf16(*reinterpret_cast<const bf16x4_t*>(&sm.L[16 * I + n16][16 * J + 4 * g4]));
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) {
+          if (t >= nown) continue;
+          const bf16x4_t xb = {(bf16)X[t][J][0], (bf16)X[t][J][1], (bf16)X[t][J][2], (bf16)X[t][J][3]};
+          acc[t] = mfma16(la, xb, acc[t]);
         }
-#pragma unroll
-        for (int J = 0; J < I; ++J) {
-          const bf16x4_t la = negate_bf16(*reinterpret_cast<const bf16x4_t*>(&sm.L[16 * I + n16][16 * J + 4 * g4]));
-          const bf16x4_t xb = {(bf16)X[J][0], (bf16)X[J][1], (bf16)X[J][2], (bf16)X[J][3]};
-          acc = mfma16(la, xb, acc);
-        }
-        const bf16x4_t ta = *reinterpret_cast<const bf16x4_t*>(&sm.Tinv[I][n16][4 * g4]);
-        const bf16x4_t ab = {(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
-        X[I] = mfma16(ta, ab, f32x4_t{0.f, 0.f, 0.f, 0.f});
       }
-      if (is_w) {
-        // scatter into W fragments: channel col -> (s, q) -> (g', e)
+      const bf16x4_t ta = *reinterpret_cast<const bf16x4_t*>(&sm.Tinv[I][n16][4 * g4]);
+#pragma unroll
+      for (int t = 0; t < kMaxT; ++t) {
+        if (t >= nown) continue;
+        const bf16x4_t ab = {(bf16)acc[t][0], (bf16)acc[t][1], (bf16)acc[t][2], (bf16)acc[t][3]};
+        X[t][I] = mfma16(ta, ab, f32x4_t{0.f, 0.f, 0.f, 0.f});
+      }
+    }
+    // exports
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t) {
+      if (t >= nown) continue;
+      const int nt = nts[t];
+      if (nt < 8) {
+        // scatter into W fragments: channel 16 nt + n16 -> step st, lane group gq, element eq
         const int st = nt >> 1;
-        const int q = 16 * (nt & 1) + n16;
-        const int gq = (q & 15) >> 2;
-        const int eq = 4 * (nt & 1) + (q & 3);
+        const int gq = n16 >> 2;
+        const int eq = 4 * (nt & 1) + (n16 & 3);
 #pragma unroll
         for (int I = 0; I < 4; ++I) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int il = 4 * g4 + r;
-            bf16* dst = reinterpret_cast<bf16*>(rec + kRecW + (static_cast<int64_t>(I * 4 + st) * 64 + il + 16 * gq) * 16);
-            dst[eq] = (bf16)X[I][r];
+            bf16* dst =
+                reinterpret_cast<bf16*>(rec + kRecW + (static_cast<int64_t>(I * 4 + st) * 64 + il + 16 * gq) * 16);
+            dst[eq] = (bf16)X[t][I][r];
           }
         }
       } else {
@@ -494,7 +528,7 @@ __global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const Pr
 #pragma unroll
         for (int I = 0; I < 4; ++I) {
           *reinterpret_cast<bf16x4_t*>(rec + kRecU + (static_cast<int64_t>(vt * 4 + I) * 64 + lane) * 8) =
-              bf16x4_t{(bf16)X[I][0], (bf16)X[I][1], (bf16)X[I][2], (bf16)X[I][3]};
+              bf16x4_t{(bf16)X[t][I][0], (bf16)X[t][I][1], (bf16)X[t][I][2], (bf16)X[t][I][3]};
         }
       }
     }
@@ -502,19 +536,21 @@ __global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const Pr
 }
 
 // ---- scan kernel ----------------------------------------------------------
-// One workgroup of two waves per (sequence, head, 32 value columns); wave w
-// owns the 16-column state slice S[:, 16 (2 wp + w) .. +16] in accumulator
-// registers.  The shared part of each chunk record (W, Q, KT, A fragments),
-// the workgroup's two U tiles and gamma (60.5 KB) are copied into LDS with
-// direct global->LDS loads one chunk ahead (two LDS buffers, two distinct
-// __shared__ arrays so the compiler can tell the in-flight copy from the
-// buffer being read), and records three chunks ahead are touched once so
-// that the copy hits L2.
-constexpr int kScanWaves = 2;
-constexpr int kScanThreads = 64 * kScanWaves;
-constexpr int kScanShared = 57344;                          // W | Q | KT | A
-constexpr int kScanBuf = kScanShared + 2 * 2048 + 512;      // + two U tiles + gamma = 61952 B
-constexpr int kScanPrefetch = 3;
+// One workgroup of three waves per (sequence, head, 32 value columns).
+// Waves 0 and 1 ("compute") own the 16-column state slices
+// S[:, 16 (2 wp + w) .. +16] in accumulator registers; they only read LDS,
+// run MFMAs and issue output stores, and never wait on vector memory.
+// Wave 2 ("copier") moves the next chunk's record (W, Q, KT, A fragments,
+// the two U tiles and gamma: 60.5 KB) into the other of two LDS buffers with
+// direct global->LDS loads and touches the record a few chunks ahead so that
+// the copy hits L2.  The roles run separate loops with one barrier per chunk.
+constexpr int kScanComputeWaves = 2;
+constexpr int kScanThreads = 64 * (kScanComputeWaves + 1);
+constexpr int kScanShared = 57344;                                       // W | Q | KT | A
+constexpr int kScanBuf = kScanShared + kScanComputeWaves * 2048 + 512;   // + U tiles + gamma = 61952 B
+constexpr int kScanUnits = kScanShared / 16;                             // 16-byte units of the shared part
+constexpr int kScanPrefetch = 4;
+constexpr int kWarmLoads = 8;                                            // 8 x 64 lanes x 128 B = 64 KB
 
 template <class IT>
 struct ScanArgs {
@@ -527,92 +563,58 @@ struct ScanArgs {
   int64_t N, H, V;
 };
 
-// copy one chunk's record pieces into an LDS buffer (all threads of the workgroup)
+// copier wave: one chunk's record pieces into an LDS buffer
 __device__ __forceinline__ void scan_copy(const unsigned char* rec, unsigned char* buf, int64_t vt0, int ntiles,
-                                          int64_t gam_off, int tid) {
-  const int wave = tid >> 6, lane = tid & 63;
-  // W | Q | KT | A : 3584 16-byte units, 28 per thread
-#pragma unroll 4
-  for (int i = 0; i < kScanShared / (16 * kScanThreads); ++i) {
-    const int u = i * kScanThreads + wave * 64;
-    __builtin_amdgcn_global_load_lds(rec + (u + lane) * 16, buf + u * 16, 16, 0, 0);
-  }
-  // U tiles of this workgroup's (up to) two value slices: 128 units per tile
-  for (int t = 0; t < ntiles; ++t) {
-    const int u = t * 128 + wave * 64;
-    __builtin_amdgcn_global_load_lds(rec + kRecU + vt0 * 2048 + (u + lane) * 16, buf + kScanShared + u * 16, 16, 0,
+                                          int64_t gam_off, int lane) {
+#pragma unroll 8
+  for (int i = 0; i < kScanUnits / 64; ++i)  // 56 instructions of 64 x 16 B
+    __builtin_amdgcn_global_load_lds(rec + (i * 64 + lane) * 16, buf + i * 1024, 16, 0, 0);
+  for (int t = 0; t < 2 * ntiles; ++t)       // U tiles: 2 instructions each
+    __builtin_amdgcn_global_load_lds(rec + kRecU + vt0 * 2048 + (t * 64 + lane) * 16, buf + kScanShared + t * 1024,
+                                     16, 0, 0);
+  if (lane < 32)  // gamma
+    __builtin_amdgcn_global_load_lds(rec + gam_off + lane * 16, buf + kScanShared + kScanComputeWaves * 2048, 16, 0,
                                      0);
-  }
-  // gamma: 32 units
-  if (wave == 0 && lane < 32)
-    __builtin_amdgcn_global_load_lds(rec + gam_off + lane * 16, buf + kScanShared + 4096, 16, 0, 0);
 }
 
-// touch one dword of every 128-byte line of a future record so that its copy
-// hits L2; the loaded words land in a scratch LDS area and are never read
-constexpr int kWarmLoads = 4;  // per thread: 4 x 128 threads x 128 B lines cover the 56 KB shared part
-__device__ __forceinline__ void scan_warm_l2(const unsigned char* rec, unsigned char* scratch, int tid) {
-  const int wave = tid >> 6;
+// copier wave: touch one dword of each 128-byte line of a future record's
+// shared part (the words land in a scratch LDS area that is never read)
+__device__ __forceinline__ void scan_warm_l2(const unsigned char* rec, unsigned char* scratch, int lane) {
 #pragma unroll
   for (int k = 0; k < kWarmLoads; ++k) {
-    int off = tid * 128 + k * kScanThreads * 128;
+    int off = (k * 64 + lane) * 128;
     off = off < kScanShared - 4 ? off : kScanShared - 4;
-    __builtin_amdgcn_global_load_lds(rec + off, scratch + wave * 256, 4, 0, 0);
+    __builtin_amdgcn_global_load_lds(rec + off, scratch, 4, 0, 0);
   }
 }
 
-// Wait until only the kWarmLoads L2-warming loads of this step may still be
-// in flight (vector memory operations of a wave retire in issue order, and a
-// step issues its output stores, then the record copy, then the warming
-// loads, so the stores and the copy are complete), drain LDS traffic, then
-// barrier.  The asm statements keep the
-// compiler from moving memory accesses across the barrier.
-__device__ __forceinline__ void scan_step_barrier() {
+// barrier without a memory fence: the asm statements only stop the compiler
+// from moving memory accesses across it; LDS ordering comes from the waits
+// each role performs before arriving
+__device__ __forceinline__ void scan_barrier() {
   asm volatile("" ::: "memory");
-  // s_waitcnt vmcnt(4) expcnt(7) lgkmcnt(0)
-  __builtin_amdgcn_s_waitcnt((kWarmLoads & 15) | (7 << 4) | (0 << 8) | ((kWarmLoads >> 4) << 14));
   __builtin_amdgcn_s_barrier();
   asm volatile("" ::: "memory");
-}
-
-// store a chunk's 64 x 16 output tile from its accumulator layout
-// (lane (n, g) holds rows 16 I + 4 g + r of column n)
-template <class IT>
-__device__ __forceinline__ void scan_store_out(const f32x4_t (&O)[4], IT* out, int64_t tokbase, int64_t n_span,
-                                               int64_t H, int64_t h, int64_t V, int64_t col, int lane) {
-  const int g4 = lane >> 4;
-#pragma unroll
-  for (int I = 0; I < 4; ++I) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t tl = 16 * I + 4 * g4 + r;
-      if (tl < n_span) out[((tokbase + tl) * H + h) * V + col] = from_compute<IT>(O[I][r]);
-    }
-  }
 }
 
 template <class IT>
 __device__ __forceinline__ void scan_chunk(const unsigned char* buf, f32x4_t (&S)[8], int w, int lane,
                                            f32x4_t (&O)[4]) {
-  // Fragment loads are batched per phase ahead of the MFMAs that use them so
-  // that LDS latency overlaps instead of being paid per product.
-  bf16x8_t wf[4][4], qf[4][4], af[6];
+  // Two-stage software pipeline over the reduction steps: the fragments of
+  // step st + 1 are read from LDS while the 8 products of step st run.
+  auto load_wq = [&](int st, bf16x8_t (&wf)[4], bf16x8_t (&qf)[4]) {
+#pragma unroll
+    for (int I = 0; I < 4; ++I) {
+      wf[I] = *reinterpret_cast<const bf16x8_t*>(buf + kRecW + ((I * 4 + st) * 64 + lane) * 16);
+      qf[I] = *reinterpret_cast<const bf16x8_t*>(buf + kRecQ + ((I * 4 + st) * 64 + lane) * 16);
+    }
+  };
+  bf16x8_t wa[4], qa[4], wb[4], qb[4];
   bf16x4_t uf[4];
 #pragma unroll
-  for (int I = 0; I < 4; ++I) {
+  for (int I = 0; I < 4; ++I)
     uf[I] = *reinterpret_cast<const bf16x4_t*>(buf + kScanShared + w * 2048 + (I * 64 + lane) * 8);
-#pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      wf[I][st] = *reinterpret_cast<const bf16x8_t*>(buf + kRecW + ((I * 4 + st) * 64 + lane) * 16);
-      qf[I][st] = *reinterpret_cast<const bf16x8_t*>(buf + kRecQ + ((I * 4 + st) * 64 + lane) * 16);
-    }
-  }
-  // Aqk fragments actually used: (I, s') for s' <= I / 2 -> slots 0, 2, 4, 5, 6, 7
-#pragma unroll
-  for (int j = 0; j < 6; ++j) {
-    const int slot = j < 2 ? 2 * j : j + 2;
-    af[j] = *reinterpret_cast<const bf16x8_t*>(buf + kRecA + (slot * 64 + lane) * 16);
-  }
+  load_wq(0, wa, qa);
   bf16x8_t Sb[4];
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
@@ -622,7 +624,6 @@ __device__ __forceinline__ void scan_chunk(const unsigned char* buf, f32x4_t (&S
       Sb[st][4 + r] = (bf16)S[2 * st + 1][r];
     }
   }
-  __builtin_amdgcn_sched_barrier(0);  // keep the fragment loads ahead of the products
   f32x4_t Vt[4];
 #pragma unroll
   for (int I = 0; I < 4; ++I) {
@@ -631,26 +632,41 @@ __device__ __forceinline__ void scan_chunk(const unsigned char* buf, f32x4_t (&S
   }
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
+    bf16x8_t(&wc)[4] = (st & 1) ? wb : wa;
+    bf16x8_t(&qc)[4] = (st & 1) ? qb : qa;
+    if (st + 1 < 4) {
+      if (st & 1)
+        load_wq(st + 1, wa, qa);
+      else
+        load_wq(st + 1, wb, qb);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      Vt[I] = mfma32(negate_bf16(wf[I][st]), Sb[st], Vt[I]);
-      O[I] = mfma32(qf[I][st], Sb[st], O[I]);
+      Vt[I] = mfma32(negate_bf16(wc[I]), Sb[st], Vt[I]);
+      O[I] = mfma32(qc[I], Sb[st], O[I]);
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  __builtin_amdgcn_sched_barrier(0);
-  // K~^T fragments and gamma for the state update
-  bf16x8_t kf[8][2];
-  f32x4_t gm[8];
-  const int g4 = lane >> 4;
-  const float* gam = reinterpret_cast<const float*>(buf + kScanShared + 4096);
+  // Aqk fragments used: (I, s') for s' <= I / 2 -> slots 0, 2, 4, 5, 6, 7;
+  // gamma and the first half of the K~^T fragments
+  bf16x8_t af[6];
 #pragma unroll
-  for (int ct = 0; ct < 8; ++ct) {
+  for (int j = 0; j < 6; ++j) {
+    const int slot = j < 2 ? 2 * j : j + 2;
+    af[j] = *reinterpret_cast<const bf16x8_t*>(buf + kRecA + (slot * 64 + lane) * 16);
+  }
+  const int g4 = lane >> 4;
+  const float* gam = reinterpret_cast<const float*>(buf + kScanShared + kScanComputeWaves * 2048);
+  f32x4_t gm[8];
+  bf16x8_t kf[8][2];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
     gm[ct] = *reinterpret_cast<const f32x4_t*>(gam + 16 * ct + 4 * g4);
 #pragma unroll
     for (int st = 0; st < 2; ++st)
       kf[ct][st] = *reinterpret_cast<const bf16x8_t*>(buf + kRecKT + ((ct * 2 + st) * 64 + lane) * 16);
   }
-  __builtin_amdgcn_sched_barrier(0);
   bf16x8_t Vb[2];
 #pragma unroll
   for (int st = 0; st < 2; ++st) {
@@ -660,6 +676,7 @@ __device__ __forceinline__ void scan_chunk(const unsigned char* buf, f32x4_t (&S
       Vb[st][4 + r] = (bf16)Vt[2 * st + 1][r];
     }
   }
+  __builtin_amdgcn_sched_barrier(0);
   O[0] = mfma32(af[0], Vb[0], O[0]);
   O[1] = mfma32(af[1], Vb[0], O[1]);
   O[2] = mfma32(af[2], Vb[0], O[2]);
@@ -667,10 +684,49 @@ __device__ __forceinline__ void scan_chunk(const unsigned char* buf, f32x4_t (&S
   O[3] = mfma32(af[4], Vb[0], O[3]);
   O[3] = mfma32(af[5], Vb[1], O[3]);
 #pragma unroll
-  for (int ct = 0; ct < 8; ++ct) {
+  for (int ct = 4; ct < 8; ++ct) {
+    gm[ct] = *reinterpret_cast<const f32x4_t*>(gam + 16 * ct + 4 * g4);
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+      kf[ct][st] = *reinterpret_cast<const bf16x8_t*>(buf + kRecKT + ((ct * 2 + st) * 64 + lane) * 16);
+  }
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
     S[ct] *= gm[ct];
 #pragma unroll
     for (int st = 0; st < 2; ++st) S[ct] = mfma32(kf[ct][st], Vb[st], S[ct]);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int ct = 4; ct < 8; ++ct) {
+    S[ct] *= gm[ct];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) S[ct] = mfma32(kf[ct][st], Vb[st], S[ct]);
+  }
+}
+
+// Store a chunk's 64 x 16 output tile.  The accumulator layout (lane (n, g)
+// holds rows 16 I + 4 g + r of column n) is transposed through a per-wave
+// 2 KB LDS stage so that each lane writes 16 contiguous bytes of a row.
+template <class IT>
+__device__ __forceinline__ void scan_store_out(const f32x4_t (&O)[4], IT* out, int64_t tokbase, int64_t n_span,
+                                               int64_t H, int64_t h, int64_t V, int64_t col0, int lane,
+                                               IT* stage) {
+  const int g4 = lane >> 4, n16 = lane & 15;
+#pragma unroll
+  for (int I = 0; I < 4; ++I) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) stage[(16 * I + 4 * g4 + r) * 16 + n16] = from_compute<IT>(O[I][r]);
+  }
+  // lanes now read what other lanes of the wave wrote: complete the writes and
+  // keep the compiler from moving the reads above them
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#pragma unroll
+  for (int j = 0; j < 2; ++j) {
+    const int row = j * 32 + (lane >> 1);
+    const int half = lane & 1;
+    const uint4 val = *reinterpret_cast<const uint4*>(stage + row * 16 + 8 * half);
+    if (row < n_span) *reinterpret_cast<uint4*>(out + ((tokbase + row) * H + h) * V + col0 + 8 * half) = val;
   }
 }
 
@@ -678,9 +734,10 @@ template <class IT>
 __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const ScanArgs<IT> a) {
   __shared__ __align__(16) unsigned char buf0[kScanBuf];
   __shared__ __align__(16) unsigned char buf1[kScanBuf];
-  __shared__ __align__(16) unsigned char warm[kScanWaves * 256];
+  __shared__ __align__(16) unsigned char warm[256];
+  __shared__ __align__(16) IT stage_all[kScanComputeWaves][64 * 16];  // output transpose, one tile per wave
   const int64_t nvt = a.V / 16;
-  const int64_t nwp = (nvt + kScanWaves - 1) / kScanWaves;  // workgroups per (sequence, head)
+  const int64_t nwp = (nvt + kScanComputeWaves - 1) / kScanComputeWaves;  // workgroups per (sequence, head)
   const int64_t bid = blockIdx.x;
   const int64_t wp = bid % nwp;
   const int64_t h = (bid / nwp) % a.H;
@@ -688,20 +745,50 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const ScanArgs
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = tid >> 6;
-  const int n16 = lane & 15;
-  const int g4 = lane >> 4;
-  const int64_t vt0 = wp * kScanWaves;
-  const int ntiles = static_cast<int>(nvt - vt0 < kScanWaves ? nvt - vt0 : kScanWaves);
-  const bool active = w < ntiles;
+  const int64_t vt0 = wp * kScanComputeWaves;
+  const int ntiles = static_cast<int>(nvt - vt0 < kScanComputeWaves ? nvt - vt0 : kScanComputeWaves);
   const SeqRange sr = seq_range(a.seq, s);
   const int64_t c0 = a.chunk_start[s];
   const int64_t c1 = a.chunk_start[s + 1];
   const int64_t rb = rec_bytes(a.V);
-  const int64_t gam_off = rec_gam(a.V);
-  const int64_t col = 16 * (vt0 + w) + n16;
-  const int64_t sbase = (s * a.H + h) * kKey * a.V;
   auto rec_of = [&](int64_t c) { return a.records + (c * a.H + h) * rb; };
 
+  if (w == kScanComputeWaves) {
+    // ---------------- copier wave ----------------
+    const int64_t gam_off = rec_gam(a.V);
+    for (int64_t p = c0 + 1; p < c1 && p <= c0 + kScanPrefetch; ++p) scan_warm_l2(rec_of(p), warm, lane);
+    scan_copy(rec_of(c0), buf0, vt0, ntiles, gam_off, lane);
+    __builtin_amdgcn_s_waitcnt(0);
+    scan_barrier();
+    // step c: the compute waves read buffer (c - c0) % 2; the copier fills the other
+    // with chunk c + 1, waits for it (the warming loads issued after it may stay in
+    // flight: a wave's vector memory loads retire in issue order), then arrives
+    for (int64_t c = c0; c < c1; ++c) {
+      const bool odd = ((c - c0) & 1) != 0;
+      if (c + 1 < c1) {
+        if (odd)
+          scan_copy(rec_of(c + 1), buf0, vt0, ntiles, gam_off, lane);
+        else
+          scan_copy(rec_of(c + 1), buf1, vt0, ntiles, gam_off, lane);
+      }
+      // always exactly kWarmLoads warming loads (clamped to a valid record) so
+      // that vmcnt(kWarmLoads) below means "the copy has landed"
+      scan_warm_l2(rec_of(c + 1 + kScanPrefetch < c1 ? c + 1 + kScanPrefetch : c1 - 1), warm, lane);
+      asm volatile("" ::: "memory");
+      // s_waitcnt vmcnt(kWarmLoads) expcnt(7) lgkmcnt(15)
+      __builtin_amdgcn_s_waitcnt((kWarmLoads & 15) | (7 << 4) | (15 << 8) | ((kWarmLoads >> 4) << 14));
+      scan_barrier();
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // no copy may land in LDS after the workgroup ends
+    return;
+  }
+
+  // ---------------- compute waves ----------------
+  const bool active = w < ntiles;
+  const int n16 = lane & 15;
+  const int g4 = lane >> 4;
+  const int64_t col = 16 * (vt0 + w) + n16;
+  const int64_t sbase = (s * a.H + h) * kKey * a.V;
   f32x4_t S[8];
 #pragma unroll
   for (int ct = 0; ct < 8; ++ct) {
@@ -711,39 +798,22 @@ __global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const ScanArgs
       S[ct][r] = (a.s_in && active) ? a.s_in[sbase + row * a.V + col] : 0.f;
     }
   }
-
-  // warm L2 for the first chunks, then fill buffer 0
-  for (int64_t p = c0 + 1; p < c1 && p <= c0 + kScanPrefetch; ++p) scan_warm_l2(rec_of(p), warm, tid);
-  if (c0 < c1) scan_copy(rec_of(c0), buf0, vt0, ntiles, gam_off, tid);
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-
+  scan_barrier();
   f32x4_t O[4];
-  int64_t prev_tok = -1, prev_span = 0;  // the output tile of the previous chunk, still in O
-  // one step: store the previous chunk's output, start copying chunk c + 1
-  // into the other buffer, warm L2 for a later chunk, compute chunk c.  The
-  // loop is unrolled by two so that each half names its LDS buffers
-  // statically (the copy target never aliases the buffer being read).
-#define KDA_SCAN_STEP(CUR, NXT)                                                                              \
-  {                                                                                                          \
-    if (active && prev_tok >= 0)                                                                             \
-      scan_store_out<IT>(O, a.out, prev_tok, prev_span, a.H, h, a.V, col, lane);                             \
-    if (c + 1 < c1) scan_copy(rec_of(c + 1), NXT, vt0, ntiles, gam_off, tid);                                \
-    scan_warm_l2(rec_of(c + 1 + kScanPrefetch < c1 ? c + 1 + kScanPrefetch : c1 - 1), warm, tid);            \
-    const int64_t lc = c - c0;                                                                               \
-    if (active) scan_chunk<IT>(CUR, S, w, lane, O);                                                          \
-    prev_tok = sr.start + kChunk * lc;                                                                       \
-    prev_span = sr.span - kChunk * lc < kChunk ? sr.span - kChunk * lc : kChunk;                             \
-    scan_step_barrier();                                                                                     \
-  }
   for (int64_t c = c0; c < c1; ++c) {
-    KDA_SCAN_STEP(buf0, buf1)
-    if (++c >= c1) break;
-    KDA_SCAN_STEP(buf1, buf0)
+    const int64_t lc = c - c0;
+    if (active) {
+      if ((lc & 1) == 0)
+        scan_chunk<IT>(buf0, S, w, lane, O);
+      else
+        scan_chunk<IT>(buf1, S, w, lane, O);
+      const int64_t n_span = sr.span - kChunk * lc < kChunk ? sr.span - kChunk * lc : kChunk;
+      scan_store_out<IT>(O, a.out, sr.start + kChunk * lc, n_span, a.H, h, a.V, col - n16, lane, stage_all[w]);
+    }
+    asm volatile("" ::: "memory");
+    __builtin_amdgcn_s_waitcnt((63 & 15) | (7 << 4) | (0 << 8) | ((63 >> 4) << 14));  // lgkmcnt(0): LDS reads done
+    scan_barrier();
   }
-#undef KDA_SCAN_STEP
-  if (active && prev_tok >= 0) scan_store_out<IT>(O, a.out, prev_tok, prev_span, a.H, h, a.V, col, lane);
-
   if (a.s_out && active) {
 #pragma unroll
     for (int ct = 0; ct < 8; ++ct) {
@@ -824,7 +894,7 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
   sa.N = N;
   sa.H = H;
   sa.V = V;
-  const int64_t blocks = N * H * ((V / 16 + kScanWaves - 1) / kScanWaves);
+  const int64_t blocks = N * H * ((V / 16 + kScanComputeWaves - 1) / kScanComputeWaves);
   hipLaunchKernelGGL(chunk_scan_kernel<IT>, dim3(static_cast<unsigned>(blocks)), dim3(kScanThreads), 0, stream, sa);
   st = kda_host::check_launch("chunk_scan_kernel");
   mark(ev, 3, stream);
