@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 1
+#define KDA_ABI_VERSION 2
 
 /* status codes */
 #define KDA_OK 0
@@ -99,7 +99,8 @@ size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int
 /*
  * Chunkwise-parallel KDA prefill (chunk 64): intra-chunk UT transform with a
  * forward-substitution solve, bf16 MFMA chunk products with f32 accumulation
- * and an f32 inter-chunk state scan.  Replaces `chunkwise_kda`
+ * and an f32 inter-chunk state scan, cut into segments whose affine state
+ * maps are composed when batch * heads alone would not fill the GPU.  Replaces `chunkwise_kda`
  * (src/kda/chunkwise.py:17-107); its result does not depend on the
  * reference's chunk_size / secondary_tile_size (the reference's own
  * invariance, tests/kda/test_kda_chunkwise_equivalence.py:42-57,
@@ -118,10 +119,11 @@ int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, co
 
 /*
  * `kda_chunk_fwd` with a HIP event recorded between its kernels; returns,
- * after synchronising `stream`, the duration of each kernel in
- * kernel_ms[0..2] (chunk map, prepare, scan; zeros for kernels the call did
- * not launch) and how many kernels ran in *num_kernels.  No reference
- * counterpart: it exists so that a benchmark can attribute time per kernel.
+ * after synchronising `stream`, the duration of each stage in kernel_ms[0..3]
+ * (chunk map, segment summaries, segment combine, chunk outputs; zero for a
+ * stage the call did not run) and the number of stages in *num_kernels.  No
+ * reference counterpart: it exists so that a benchmark can attribute time
+ * per kernel.
  */
 int kda_chunk_fwd_profiled(const void* q, const void* k, const void* v, const void* g, const void* beta,
                            int in_dtype, const void* initial_state, void* final_state, int state_dtype,

@@ -196,11 +196,11 @@ int kda_chunk_fwd_profiled(const void* q, const void* k, const void* v, const vo
   kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
   st = launch_chunk(q, k, v, g, beta, in_dtype, initial_state, final_state, state_dtype, out, seq, num_seqs,
                     total_tokens, heads, key_dim, value_dim, workspace, workspace_bytes, s, &ev);
-  for (int i = 0; i < 3; ++i) kernel_ms[i] = 0.f;
+  for (int i = 0; i < 4; ++i) kernel_ms[i] = 0.f;
   *num_kernels = 0;
   if (st == KDA_OK && hipStreamSynchronize(s) == hipSuccess) {
     *num_kernels = ev.n_launched;
-    for (int i = 0; i < ev.n_launched && i < 3; ++i) (void)hipEventElapsedTime(&kernel_ms[i], ev.ev[i], ev.ev[i + 1]);
+    for (int i = 0; i < ev.n_launched && i < 4; ++i) (void)hipEventElapsedTime(&kernel_ms[i], ev.ev[i], ev.ev[i + 1]);
   }
   for (auto& e : ev.ev) (void)hipEventDestroy(e);
   return st;

@@ -1,25 +1,45 @@
-// Chunkwise KDA prefill on gfx950 bf16 MFMA (chunk C = 64, K = 128).
+// Chunkwise KDA prefill on gfx950 bf16 MFMA (chunk C = 64, K = 128, V <= 256).
 //
 // Reference algorithm: src/kda/chunkwise.py:61-102 with the UT transform of
 // src/kda/ut_transform.py:23-58.  For one chunk (rows i, j = 0..63, key
 // channels c, lg = inclusive cumsum of g inside the chunk):
 //   A_ij   = sum_c k_i k_j exp(lg_i - lg_j)            j <  i   (strict)
 //   Aqk_ij = sum_c q_i k_j exp(lg_i - lg_j)            j <= i
-//   L = I + diag(beta) A ;  [W | U] = L^{-1} diag(beta) [exp(lg) k | v]
-//   V~ = U - W S ;  O = (exp(lg) q) S + Aqk V~ ;  S <- diag(exp lg_63) S + (exp(lg_63 - lg) k)^T V~
+//   M = (I + diag(beta) A)^{-1} diag(beta)             (64 x 64, lower)
+//   V~ = M (v - exp(lg) k S) ;  O = (exp(lg) q) S + Aqk V~ ;  S <- diag(exp lg_63) S + (exp(lg_63 - lg) k)^T V~
+// The reference forms W = M exp(lg) k and U = M v (its UT transform,
+// ut_transform.py:53-55) and then V~ = U - W S; multiplying M into
+// (v - exp(lg) k S) instead is the same quantity and needs only the 64 x 64
+// matrix M per chunk rather than the forward substitution of 8 + V/16
+// column tiles.
 //
-// Two kernels:
-//  * kda_chunk_prepare: one workgroup per (chunk, head), fully parallel.
-//    Computes the decay factors, A and Aqk on MFMA, the blocked
-//    forward-substitution solve, and writes a per-chunk record whose
-//    operands are already in MFMA fragment order (see "record layout").
-//  * kda_chunk_scan: one wave per (sequence, head, 16-column V tile) walks
-//    the chunks in order with its state slice S[:, 16 cols] in MFMA
-//    accumulator registers (f32).  The accumulator layout of S converts to
-//    the B-operand layout of the next product without any data movement: a
-//    C tile lane holds rows 4g..4g+3 of one column, so two consecutive row
-//    tiles give the 8 values a 16x16x32 B operand needs, with the reduction
-//    index permuted; the A operands are stored pre-permuted to match.
+// Every chunk is an affine map of the state, S_out = P_c S_in + R_c.  A
+// sequence of chunks is cut into segments of L chunks so that the serial
+// chain does not limit parallelism when batch * heads is small:
+//  * phase A, chunk_segment_kernel<.., kSummary>: one workgroup per
+//    (segment, head, 128-column group) folds its segment into
+//    (P_g, Q_g) by running the chunk recurrence on X = [Q | P] from
+//    X = [0 | I]: the V value columns give Q_g, 128 more columns give P_g.
+//    The first segment of a sequence starts from the real initial state and
+//    directly yields the start state of the second segment.
+//  * phase B, segment_combine_kernel: S_{g+1} = P_g S_g + Q_g along each
+//    sequence, one workgroup per (sequence, head, 16-column tile).
+//  * phase C, chunk_segment_kernel<.., kOutput>: one workgroup per
+//    (segment, head, column group) re-runs its segment from the true start
+//    state and writes the outputs (and the final state).
+// When batch * heads alone fills the GPU, each sequence is one segment and
+// only phase C runs.
+//
+// Inside phases A and C a workgroup of 8 waves walks its chunks; per chunk
+// it builds every chunk operand in LDS (decay factors, A and Aqk on MFMA,
+// the diagonal-block inverses and M) and then the 4 scanner waves advance
+// their 16-column state tiles, held in f32 MFMA accumulators.  The
+// accumulator layout of a state tile converts to the B-operand layout of the
+// next product without data movement: a C tile lane holds rows 4g..4g+3 of
+// one column, so two consecutive row tiles give the 8 values a 16x16x32 B
+// operand needs, with the reduction index permuted; the A operands are
+// written pre-permuted to match.  The raw inputs of the next chunk are loaded
+// into registers while the current chunk is scanned.
 //
 // Numerical scheme for the decays (per-channel, any g <= 0):
 //   alpha_j = exp(g_j); within each 16-row block J the running products
@@ -31,6 +51,8 @@
 //   chunks take an exact pairwise-exponent path for the diagonal blocks (the
 //   reference evaluates every tile with an explicit pairwise exponent,
 //   src/kda/utils.py:128-136).
+#include <cstdlib>
+
 #include "kda_launch.h"
 
 namespace kda {
@@ -43,26 +65,47 @@ typedef float f32x4_t __attribute__((ext_vector_type(4)));
 
 constexpr int kChunk = 64;
 constexpr int kKey = 128;
-constexpr int kPrepThreads = 256;
+constexpr int kColGroup = 128;  // value columns per workgroup
+constexpr int kThreads = 512;   // 8 waves
 constexpr float kExtremeDecay = 7.888609052210118e-31f;  // 2^-100
+constexpr int32_t kOneSegment = 0x3fffffff;              // L: every sequence is one segment
 
-// ---- record layout (bytes, per chunk and head) ----------------------------
-//  W   [I=4][s=4][lane=64][8] bf16 : A fragments of W (token tile I, channel step s)
-//  Q   [I=4][s=4][lane=64][8] bf16 : A fragments of exp(lg) q
-//  KT  [ct=8][s'=2][lane=64][8] bf16 : A fragments of (exp(lg_63 - lg) k)^T
-//  A   [I=4][s'=2][lane=64][8] bf16 : A fragments of Aqk (token tile I, token step s')
-//  U   [vt=V/16][I=4][lane=64][4] bf16 : C tiles of U (accumulator init of V~)
-//  GAM [128] f32 : exp(lg_63) per key channel
+constexpr int kSummary = 0;  // phase A
+constexpr int kOutput = 1;   // phase C
+
+// ---- LDS map of chunk_segment_kernel (bytes) ------------------------------
+// Natural bf16 tiles use a padded row of 136 elements.
+constexpr int kRow = 136;
+constexpr int kNat = kChunk * kRow * 2;     // 17408
+constexpr int kOffKA = 0;                   // bf16 [64][136] k_j a_j
+constexpr int kOffQA = kOffKA + kNat;       // bf16 [64][136] q_j a_j    -> Kgamma fragments after P2
+constexpr int kOffKE = kOffQA + kNat;       // bf16 [64][136] k_j E_j    -> M fragments after P2
+constexpr int kOffL = kOffKE + kNat;        // bf16 [64][72] beta_i A_ij, strict lower
+constexpr int kOffLd = kOffL + kChunk * 72 * 2;  // f32 [4][16][16] diagonal blocks of L
+constexpr int kOffTinv = kOffLd + 4 * 256 * 4;   // bf16 [4][16][16] T_I = inverses of those blocks
+constexpr int kOffTinvT = kOffTinv + 4 * 256 * 2;  // bf16 [4][16][16] T_I transposed
+constexpr int kOffTab = kOffTinvT + 4 * 256 * 2;   // f32 G/A0/P [3][4][128], then pair scales [10][128]
+constexpr int kOffGs = kOffTab + 3 * 4 * kKey * 4;  // f32 [4][128] exp(lg_{16J})
+constexpr int kOffGe = kOffGs + 4 * kKey * 4;       // f32 [4][128] exp(lg_63 - lg_{16J+15})
+constexpr int kOffBeta = kOffGe + 4 * kKey * 4;     // f32 [64]
+constexpr int kOffVn = kOffBeta + 256;              // bf16 [64][136] v of the column group
+constexpr int kOffQf = kOffVn + kNat;               // Q~ A fragments  [I=4][s=4][lane][8] bf16
+constexpr int kOffKTf = kOffQf + 16384;             // K~^T A fragments [ct=8][s=2][lane][8]
+constexpr int kOffAf = kOffKTf + 16384;             // Aqk A fragments [I=4][s=2][lane][8]
+constexpr int kOffGam = kOffAf + 8192;              // f32 [128] exp(lg_63)
+constexpr int kOffFlag = kOffGam + 512;             // int [4] extreme-decay flags of P1b's waves
+constexpr int kSmemBytes = kOffFlag + 16;
+constexpr int kOffKgf = kOffQA;    // -Kgamma = -exp(lg) k A fragments [I=4][s=4][lane][8] bf16
+constexpr int kOffMf = kOffKE;     // M = (I + diag(beta) A)^-1 diag(beta) A fragments [I=4][s=2][lane][8]
+constexpr int kOffStage = kOffKA;  // output transpose [4 waves][64][32]
+constexpr int kOffPnat = kOffKA;   // phase A: P_g natural bf16 [128][136]
+static_assert(kSmemBytes <= 160 * 1024, "chunk_segment_kernel LDS exceeds one CU");
+static_assert(4 * 64 * 32 * 2 <= kNat, "output stage must fit in the k a tile");
+static_assert(kKey * kRow * 2 <= 2 * kNat, "P transpose must fit in the k a and q a tiles");
+static_assert(16384 <= kNat && 8192 <= kNat, "Kgamma and M fragments must fit in the q a and k E tiles");
 // Fragment element e of lane (i, g) covers reduction index
 //   32 s + (e < 4 ? 4 g + e : 16 + 4 g + e - 4),
 // the order in which two stacked C tiles provide a B operand.
-constexpr int64_t kRecW = 0;
-constexpr int64_t kRecQ = 16384;
-constexpr int64_t kRecKT = 32768;
-constexpr int64_t kRecA = 49152;
-constexpr int64_t kRecU = 57344;
-__host__ __device__ constexpr int64_t rec_gam(int64_t V) { return kRecU + (V / 16) * 2048; }
-__host__ __device__ constexpr int64_t rec_bytes(int64_t V) { return ((rec_gam(V) + 512 + 255) / 256) * 256; }
 
 __device__ __forceinline__ f32x4_t mfma32(bf16x8_t a, bf16x8_t b, f32x4_t c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
@@ -73,52 +116,85 @@ __device__ __forceinline__ f32x4_t mfma16(bf16x4_t a, bf16x4_t b, f32x4_t c) {
 }
 template <class V>
 __device__ __forceinline__ V negate_bf16(V x) {
-  // flip the sign bit of every bf16 lane
-  typedef unsigned short u16v __attribute__((ext_vector_type(sizeof(V) / 2)));
-  u16v b = __builtin_bit_cast(u16v, x);
-  b ^= (unsigned short)0x8000;
+  // flip the sign bit of every bf16 lane, two lanes per 32-bit word
+  typedef unsigned int u32v __attribute__((ext_vector_type(sizeof(V) / 4)));
+  u32v b = __builtin_bit_cast(u32v, x);
+  b ^= 0x80008000u;
   return __builtin_bit_cast(V, b);
 }
+__device__ __forceinline__ int perm_index(int e, int g) { return e < 4 ? 4 * g + e : 16 + 4 * g + e - 4; }
 
-template <class IT>
-__device__ __forceinline__ void load_pair(const IT* p, float& lo, float& hi) {
-  typedef IT pair_t __attribute__((ext_vector_type(2)));
-  const pair_t x = *reinterpret_cast<const pair_t*>(p);
-  lo = to_float(x[0]);
-  hi = to_float(x[1]);
+// The value of x, hidden from the optimiser (it cannot be hoisted or
+// assumed loop-invariant).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
 }
 
-// ---- chunk map ------------------------------------------------------------
-// chunk_start[s] = sum_{s' < s} ceil(span_{s'} / 64);  chunk_start[N] = total chunks.
-__global__ __launch_bounds__(1024) void chunk_map_kernel(SeqDesc seq, int64_t N, int32_t* chunk_start) {
-  __shared__ int32_t part[1024];
+// Wave index of a thread, as a wave-uniform (scalar) value: conditions on it
+// become scalar branches instead of exec-masked divergent regions.
+__device__ __forceinline__ int wave_of(int tid) { return __builtin_amdgcn_readfirstlane(tid >> 6); }
+
+template <class T>
+__device__ __forceinline__ T* lds(unsigned char* base, int off) {
+  return reinterpret_cast<T*>(base + off);
+}
+
+// ---- chunk and segment maps -------------------------------------------------
+// chunk_start[s] = sum_{s' < s} ceil(span_{s'} / 64), chunk_start[N] = total chunks;
+// seg_start[s]   = sum_{s' < s} max(1, ceil(chunks_{s'} / L)).
+__device__ __forceinline__ int32_t seq_chunks(const SeqDesc& seq, int64_t s) {
+  return static_cast<int32_t>((seq_range(seq, s).span + kChunk - 1) / kChunk);
+}
+__device__ __forceinline__ int32_t seq_segments(int32_t chunks, int32_t L) {
+  const int32_t n = (chunks + L - 1) / L;
+  return n > 1 ? n : 1;
+}
+
+__global__ __launch_bounds__(1024) void chunk_map_kernel(SeqDesc seq, int64_t N, int32_t L, int32_t* chunk_start,
+                                                         int32_t* seg_start) {
+  __shared__ int32_t pc[1024];
+  __shared__ int32_t ps[1024];
   const int tid = threadIdx.x;
   const int64_t per = (N + 1023) / 1024;
   const int64_t b0 = tid * per;
   const int64_t b1 = (b0 + per < N) ? b0 + per : N;
-  int32_t local = 0;
-  for (int64_t s = b0; s < b1; ++s) local += static_cast<int32_t>((seq_range(seq, s).span + kChunk - 1) / kChunk);
-  part[tid] = local;
+  int32_t lc = 0, ls = 0;
+  for (int64_t s = b0; s < b1; ++s) {
+    const int32_t c = seq_chunks(seq, s);
+    lc += c;
+    ls += seq_segments(c, L);
+  }
+  pc[tid] = lc;
+  ps[tid] = ls;
   __syncthreads();
   for (int off = 1; off < 1024; off <<= 1) {
-    const int32_t add = tid >= off ? part[tid - off] : 0;
+    const int32_t ac = tid >= off ? pc[tid - off] : 0;
+    const int32_t as = tid >= off ? ps[tid - off] : 0;
     __syncthreads();
-    part[tid] += add;
+    pc[tid] += ac;
+    ps[tid] += as;
     __syncthreads();
   }
-  int32_t run = part[tid] - local;
+  int32_t rc = pc[tid] - lc, rs = ps[tid] - ls;
   for (int64_t s = b0; s < b1; ++s) {
-    chunk_start[s] = run;
-    run += static_cast<int32_t>((seq_range(seq, s).span + kChunk - 1) / kChunk);
+    chunk_start[s] = rc;
+    seg_start[s] = rs;
+    const int32_t c = seq_chunks(seq, s);
+    rc += c;
+    rs += seq_segments(c, L);
   }
-  if (tid == 1023) chunk_start[N] = part[1023];
+  if (tid == 1023) {
+    chunk_start[N] = pc[1023];
+    seg_start[N] = ps[1023];
+  }
 }
 
-__device__ __forceinline__ int64_t find_seq(const int32_t* chunk_start, int64_t N, int64_t c) {
-  int64_t lo = 0, hi = N - 1;  // largest s with chunk_start[s] <= c
+__device__ __forceinline__ int64_t find_seq(const int32_t* start, int64_t N, int64_t x) {
+  int64_t lo = 0, hi = N - 1;  // largest s with start[s] <= x
   while (lo < hi) {
     const int64_t mid = (lo + hi + 1) >> 1;
-    if (chunk_start[mid] <= c)
+    if (start[mid] <= x)
       lo = mid;
     else
       hi = mid - 1;
@@ -126,159 +202,353 @@ __device__ __forceinline__ int64_t find_seq(const int32_t* chunk_start, int64_t 
   return lo;
 }
 
-// ---- prepare kernel -------------------------------------------------------
-struct PrepSmem {
-  bf16 KA[kChunk][136];  // k_j * a_j          (natural: token rows, key channels)
-  bf16 QA[kChunk][136];  // q_j * a_j
-  bf16 KE[kChunk][136];  // k_j * E_j
-  bf16 L[kChunk][72];    // beta_i * A_ij, strict lower (bf16, MFMA A operand)
-  float Ld[4][16][16];   // diagonal blocks of L in f32 (for the block inverses)
-  bf16 Tinv[4][16][16];  // inverses of the unit-lower diagonal blocks of L
-  // Per-channel block factors.  G, A0 and P are only read while building Gs,
-  // Ge and the pair scales; the pair scales then overlay them (each thread
-  // owns one channel column of all of them, so the overlay needs no barrier).
-  union {
-    struct {
-      float G[4][kKey];   // exp(lg_{16J+15} - lg_{16J-1})  (block decay incl. its first row)
-      float A0[4][kKey];  // alpha at the first row of block J
-      float P[4][kKey];   // exp(lg_{16J+15} - lg_{16J})
-    };
-    float Sc[10][kKey];   // per block pair (I, J <= I): D_IJ (J < I) or 1 / P_I (J = I)
-  };
-  float Gs[4][kKey];      // exp(lg_{16J})  (chunk start to block start, inclusive)
-  float Ge[4][kKey];      // exp(lg_63 - lg_{16J+15})
-  float beta[kChunk];
-};
-
-// two prepare workgroups must fit in the 160 KB of LDS of one CU
-static_assert(2 * sizeof(PrepSmem) <= 160 * 1024, "prepare kernel LDS no longer allows two workgroups per CU");
+// ---- workspace layouts of the segment buffers --------------------------------
+// seg_state / seg_q: f32 in accumulator order [seg][h][V/16 tiles][ct=8][lane][4]
+//   (element r of lane (n, g) in row tile ct is row 16 ct + 4 g + r, column 16 t + n);
+// seg_p: bf16 A fragments [seg][h][I=8][s=4][lane][8] of the 128x128 transition.
+__host__ __device__ constexpr int64_t seg_state_floats(int64_t V) { return kKey * V; }
+__host__ __device__ constexpr int64_t seg_p_elems() { return kKey * kKey; }
 
 template <class IT>
-struct PrepArgs {
+struct SegArgs {
   const IT* __restrict__ q;
   const IT* __restrict__ k;
   const IT* __restrict__ v;
   const IT* __restrict__ g;
   const IT* __restrict__ beta;
+  IT* __restrict__ out;
+  const float* s_in;
+  float* s_out;
   SeqDesc seq;
   const int32_t* __restrict__ chunk_start;
-  unsigned char* __restrict__ records;
+  const int32_t* __restrict__ seg_start;
+  float* seg_state;
+  float* seg_q;
+  bf16* seg_p;
   int64_t N, H, V;
+  int32_t L;
 };
 
-template <class IT>
-__global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const PrepArgs<IT> a) {
-  extern __shared__ __align__(16) unsigned char smem_raw[];
-  PrepSmem& sm = *reinterpret_cast<PrepSmem*>(smem_raw);
-  const int64_t c = blockIdx.x;
-  const int64_t h = blockIdx.y;
-  if (c >= a.chunk_start[a.N]) return;  // uniform: grid is an upper bound
-  const int64_t s = find_seq(a.chunk_start, a.N, c);
-  const SeqRange sr = seq_range(a.seq, s);
-  const int64_t lc = c - a.chunk_start[s];
-  const int64_t tok0 = sr.start + kChunk * lc;
-  const int n_span = static_cast<int>(sr.span - kChunk * lc < kChunk ? sr.span - kChunk * lc : kChunk);
-  int64_t nv = sr.valid - kChunk * lc;
-  const int n_valid = static_cast<int>(nv < 0 ? 0 : (nv > n_span ? n_span : nv));
-  unsigned char* rec = a.records + (c * a.H + h) * rec_bytes(a.V);
+struct ChunkGeo {
+  int64_t tok0;
+  int n_span;
+  int n_valid;
+};
 
-  const int tid = threadIdx.x;
+__device__ __forceinline__ ChunkGeo chunk_geo(const SeqRange& sr, int64_t lc) {
+  ChunkGeo c;
+  c.tok0 = sr.start + kChunk * lc;
+  const int64_t rest = sr.span - kChunk * lc;
+  c.n_span = static_cast<int>(rest < kChunk ? rest : kChunk);
+  const int64_t nv = sr.valid - kChunk * lc;
+  c.n_valid = static_cast<int>(nv < 0 ? 0 : (nv > c.n_span ? c.n_span : nv));
+  return c;
+}
+
+// Raw inputs of one chunk, held in the registers of the four loader waves
+// (4-7) between chunks: loader thread (block J = wave - 4, channel pair
+// cp = lane) holds g, k (and q) of its 16 rows, and the 256 loader threads
+// together hold the chunk's v slice of this column group and beta.
+template <class IT>
+struct Raw {
+  typedef IT pair_t __attribute__((ext_vector_type(2)));
+  pair_t gp[16], kp[16], qp[16];
+  uint4 vv[4];
+  IT bt;
+};
+
+// Part PART (0..7) of the loads of one chunk's raw inputs: rows 2 PART and
+// 2 PART + 1 of g, k (and q) of this thread's block, one 16-byte v unit on
+// even parts and beta on the last.  Spreading the eight parts over a chunk's
+// phases keeps any single moment's burst of requests small: issued at once,
+// every CU's 64 KB would saturate HBM and stall the issuing waves.
+template <class IT, int MODE, int PART>
+__device__ __forceinline__ void load_raw_part(Raw<IT>& raw, const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h,
+                                              int64_t col0, int vcg, int tid) {
+  typedef typename Raw<IT>::pair_t pair_t;
+  const int t2 = tid - 256;  // loader thread index
+  const int J = wave_of(tid) - 4;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int64_t krow = a.H * kKey;
+  // rows past the valid range read row tok0 instead and are zeroed when used
+#pragma unroll
+  for (int r = 2 * PART; r < 2 * PART + 2; ++r) {
+    const int tl = 16 * J + r;
+    const int64_t off = (cg.tok0 + (tl < cg.n_valid ? tl : 0)) * krow + h * kKey + 2 * lane;
+    raw.gp[r] = *reinterpret_cast<const pair_t*>(a.g + off);
+    raw.kp[r] = *reinterpret_cast<const pair_t*>(a.k + off);
+    if constexpr (MODE == kOutput) raw.qp[r] = *reinterpret_cast<const pair_t*>(a.q + off);
+  }
+  if constexpr ((PART & 1) == 0) {
+    const int i = PART / 2;
+    const int upr = vcg / 8;  // 16-byte units per row
+    const int u = t2 + 256 * i;
+    const int row = u / upr;
+    if (row < kChunk) {
+      const int64_t off = (cg.tok0 + (row < cg.n_valid ? row : 0)) * (a.H * a.V) + h * a.V + col0 + 8 * (u % upr);
+      raw.vv[i] = *reinterpret_cast<const uint4*>(a.v + off);
+    }
+  }
+  if constexpr (PART == 7) {
+    if (t2 < kChunk) raw.bt = a.beta[(cg.tok0 + (t2 < cg.n_valid ? t2 : 0)) * a.H + h];
+  }
+}
+
+template <class IT, int MODE>
+__device__ __forceinline__ void load_raw(Raw<IT>& raw, const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h,
+                                         int64_t col0, int vcg, int tid) {
+  load_raw_part<IT, MODE, 0>(raw, a, cg, h, col0, vcg, tid);
+  load_raw_part<IT, MODE, 1>(raw, a, cg, h, col0, vcg, tid);
+  load_raw_part<IT, MODE, 2>(raw, a, cg, h, col0, vcg, tid);
+  load_raw_part<IT, MODE, 3>(raw, a, cg, h, col0, vcg, tid);
+  load_raw_part<IT, MODE, 4>(raw, a, cg, h, col0, vcg, tid);
+  load_raw_part<IT, MODE, 5>(raw, a, cg, h, col0, vcg, tid);
+  load_raw_part<IT, MODE, 6>(raw, a, cg, h, col0, vcg, tid);
+  load_raw_part<IT, MODE, 7>(raw, a, cg, h, col0, vcg, tid);
+}
+
+// Where the loader waves are in a chunk's phases, for the spread loads of
+// the chunk after next: `load_part<P>()` issues part P if there is one.
+template <class IT, int MODE>
+struct NextLoads {
+  Raw<IT>* raw;
+  const SegArgs<IT>* a;
+  ChunkGeo cg;
+  int64_t h, col0;
+  int vcg, tid;
+  bool active;
+  template <int P>
+  __device__ __forceinline__ void load_part() const {
+    if (active) load_raw_part<IT, MODE, P>(*raw, *a, cg, h, col0, vcg, tid);
+  }
+};
+
+// Block row I of M = (I + B)^{-1} diag(beta) (B = diag(beta) A, strictly
+// lower) as A fragments.  With N = (I + B)^{-1}, block row I of Z = N^T obeys
+//   Z_II = T_I^T ;  Z_IJ = -T_J^T sum_{K=J+1..I} B_KJ^T Z_IK   (J < I),
+// a chain in which Z_IK is the B operand of the next product.  In the
+// accumulator layout lane (i, g) holds Z_IJ[4 g + r][i] = N[16 I + i][16 J + 4 g + r],
+// which is half of an A fragment of M (rows i, reduction over j).
+template <int I>
+__device__ __forceinline__ void m_block_row(unsigned char* sm, int lane) {
   const int n16 = lane & 15;
   const int g4 = lane >> 4;
-  const int64_t krow = a.H * kKey;
-
-  // ---- P1: per-channel decay factors (thread = channel pair cp, block J) ---
-  int extreme_local = 0;
+  bf16(*Lm)[72] = lds<bf16[72]>(sm, kOffL);
+  bf16(*Tinv)[16][16] = lds<bf16[16][16]>(sm, kOffTinv);
+  bf16(*TinvT)[16][16] = lds<bf16[16][16]>(sm, kOffTinvT);
+  const float* betas = lds<float>(sm, kOffBeta);
+  unsigned char* mf = sm + kOffMf;
+  auto put = [&](int J, const f32x4_t& z) {  // M_IJ = N_IJ diag(beta_J)
+    const f32x4_t b4 = *reinterpret_cast<const f32x4_t*>(&betas[16 * J + 4 * g4]);
+    *reinterpret_cast<bf16x4_t*>(mf + ((I * 2 + J / 2) * 64 + lane) * 16 + (J & 1) * 8) =
+        bf16x4_t{(bf16)(z[0] * b4[0]), (bf16)(z[1] * b4[1]), (bf16)(z[2] * b4[2]), (bf16)(z[3] * b4[3])};
+  };
+  f32x4_t Z[I + 1];
   {
-    const int J = wave;
-    const int cp = lane;
-    float gv[2][16], kv[2][16], qv[2][16];
-    {
-      // all 48 paired loads are issued before any use (tokens past the valid
-      // range read row tok0 instead and are zeroed afterwards)
-      typedef IT pair_t __attribute__((ext_vector_type(2)));
-      pair_t gp[16], kp[16], qp[16];
+    const bf16x4_t t = *reinterpret_cast<const bf16x4_t*>(&Tinv[I][n16][4 * g4]);  // T_I[i][4g + r]
+    Z[I] = f32x4_t{(float)t[0], (float)t[1], (float)t[2], (float)t[3]};
+    put(I, Z[I]);
+    if constexpr ((I & 1) == 0)  // block (I, I + 1) is above the diagonal
+      *reinterpret_cast<bf16x4_t*>(mf + ((I * 2 + I / 2) * 64 + lane) * 16 + 8) = bf16x4_t{};
+  }
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int tl = 16 * J + r;
-        const int64_t off = (tok0 + (tl < n_valid ? tl : 0)) * krow + h * kKey + 2 * cp;
-        gp[r] = *reinterpret_cast<const pair_t*>(a.g + off);
-        kp[r] = *reinterpret_cast<const pair_t*>(a.k + off);
-        qp[r] = *reinterpret_cast<const pair_t*>(a.q + off);
-      }
+  for (int J = I - 1; J >= 0; --J) {
+    f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const bool ok = 16 * J + r < n_valid;
+    for (int K = J + 1; K <= I; ++K) {
+      // A = B_KJ^T: lane (j, g) holds B[16K + 4g + r][16J + j]
+      bf16x4_t bt;
 #pragma unroll
-        for (int ch = 0; ch < 2; ++ch) {
-          gv[ch][r] = ok ? to_float(gp[r][ch]) : 0.f;
-          kv[ch][r] = ok ? to_float(kp[r][ch]) : 0.f;
-          qv[ch][r] = ok ? to_float(qp[r][ch]) : 0.f;
-        }
-      }
+      for (int r = 0; r < 4; ++r) bt[r] = Lm[16 * K + 4 * g4 + r][16 * J + n16];
+      const bf16x4_t zb = {(bf16)Z[K][0], (bf16)Z[K][1], (bf16)Z[K][2], (bf16)Z[K][3]};
+      acc = mfma16(bt, zb, acc);
     }
-    float ka[2][16], qa[2][16], ke[2][16];
+    // A = -T_J^T: lane (j, g) holds T_J[4g + r][j] = T_J^T[j][4g + r]
+    const bf16x4_t ta = negate_bf16(*reinterpret_cast<const bf16x4_t*>(&TinvT[J][n16][4 * g4]));
+    const bf16x4_t ab = {(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+    Z[J] = mfma16(ta, ab, f32x4_t{0.f, 0.f, 0.f, 0.f});
+    put(J, Z[J]);
+  }
+}
+
+// ---- per-chunk preparation: every chunk operand, in LDS ---------------------
+// P1 of one chunk, computed by a loader thread (block J = wave - 4, channel
+// pair cp = lane) from the raw inputs into registers: the decayed rows
+// k a, q a, k E as bf16 pairs, the per-channel block factors, the v slice
+// (bf16) and beta.  The loaders compute it for chunk c + 1 while the
+// scanners advance the state through chunk c, and write it to LDS at the top
+// of the next chunk (p1_write).
+struct P1Out {
+  uint32_t ka[16], qa[16], ke[16];  // bf16 pairs (channels 2cp, 2cp + 1) of rows 16 J + r
+  float pblk[2], a0[2];             // exp(lg_{16J+15} - lg_{16J}) and alpha at row 16 J
+  uint4 vv[4];                      // bf16 v units of this thread (zero past the valid rows)
+  float bt;                         // beta of row t2 (< 64), zero past the valid rows
+};
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, bf16x2_t{(bf16)lo, (bf16)hi});
+}
+
+template <class IT, int MODE>
+__device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const ChunkGeo& cg, int vcg, int tid) {
+  const int J = wave_of(tid) - 4;
+  const int n_valid = cg.n_valid;
+  float al[2][16];
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const bool ok = 16 * J + r < n_valid;
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) al[ch][r] = ok ? fast_exp(to_float(raw.gp[r][ch])) : 1.f;
+  }
+  float run[2] = {1.f, 1.f};
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const bool ok = 16 * J + r < n_valid;
+    float kv[2], qv[2];
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
-      float al[16];
-#pragma unroll
-      for (int r = 0; r < 16; ++r) al[r] = fast_exp(gv[ch][r]);
-      float run = 1.f;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        if (r > 0) run *= al[r];
-        ka[ch][r] = kv[ch][r] * run;
-        qa[ch][r] = qv[ch][r] * run;
-      }
-      const float p_blk = run;  // a at the last row = exp(lg_{16J+15} - lg_{16J})
-      float suf = 1.f;
-#pragma unroll
-      for (int r = 15; r >= 0; --r) {
-        ke[ch][r] = kv[ch][r] * suf;
-        suf *= al[r];
-      }
-      const int cc = 2 * cp + ch;
-      sm.P[J][cc] = p_blk;
-      sm.A0[J][cc] = al[0];
-      sm.G[J][cc] = al[0] * p_blk;
-      if (!(p_blk >= kExtremeDecay)) extreme_local = 1;
+      if (r > 0) run[ch] *= al[ch][r];
+      kv[ch] = ok ? to_float(raw.kp[r][ch]) : 0.f;
+      qv[ch] = (MODE == kOutput && ok) ? to_float(raw.qp[r][ch]) : 0.f;
     }
+    po.ka[r] = pack_bf16x2(kv[0] * run[0], kv[1] * run[1]);
+    if constexpr (MODE == kOutput) po.qa[r] = pack_bf16x2(qv[0] * run[0], qv[1] * run[1]);
+  }
+  float suf[2] = {1.f, 1.f};
+#pragma unroll
+  for (int r = 15; r >= 0; --r) {
+    const bool ok = 16 * J + r < n_valid;
+    float kv[2];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) kv[ch] = ok ? to_float(raw.kp[r][ch]) * suf[ch] : 0.f;
+    po.ke[r] = pack_bf16x2(kv[0], kv[1]);
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) suf[ch] *= al[ch][r];
+  }
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch) {
+    po.pblk[ch] = run[ch];  // a at the last row = exp(lg_{16J+15} - lg_{16J})
+    po.a0[ch] = al[ch][0];
+  }
+  const int t2 = tid - 256;
+  const int upr = vcg / 8;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = (t2 + 256 * i) / upr;
+    uint4 val = raw.vv[i];
+    if (row >= n_valid) val = uint4{0u, 0u, 0u, 0u};
+    if constexpr (sizeof(IT) == 2 && !__is_same(IT, bf16)) {
+      // f16 inputs: convert the 8 values to bf16 operands
+      typedef IT h8_t __attribute__((ext_vector_type(8)));
+      const h8_t x = __builtin_bit_cast(h8_t, val);
+      bf16x8_t y;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = (bf16)to_float(x[e]);
+      val = __builtin_bit_cast(uint4, y);
+    }
+    po.vv[i] = val;
+  }
+  po.bt = (t2 < kChunk && t2 < n_valid) ? to_float(raw.bt) : 0.f;
+}
+
+// Writes P1 (loader waves) and joins every wave at the first barrier of the
+// chunk.
+template <int MODE, bool LOADER>
+__device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, int vcg, int tid) {
+  if constexpr (LOADER) {
+    const int J = wave_of(tid) - 4;
+    const int cp = tid & 63;
+    bf16(*KA)[kRow] = lds<bf16[kRow]>(sm, kOffKA);
+    bf16(*QA)[kRow] = lds<bf16[kRow]>(sm, kOffQA);
+    bf16(*KE)[kRow] = lds<bf16[kRow]>(sm, kOffKE);
+    float(*Gt)[kKey] = lds<float[kKey]>(sm, kOffTab);                      // G  [4][128]
+    float(*A0t)[kKey] = lds<float[kKey]>(sm, kOffTab + 4 * kKey * 4);      // A0 [4][128]
+    float(*Pt)[kKey] = lds<float[kKey]>(sm, kOffTab + 8 * kKey * 4);       // P  [4][128]
+    float* betas = lds<float>(sm, kOffBeta);
+    bf16(*Vn)[kRow] = lds<bf16[kRow]>(sm, kOffVn);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int tl = 16 * J + r;
-      *reinterpret_cast<bf16x2_t*>(&sm.KA[tl][2 * cp]) = bf16x2_t{(bf16)ka[0][r], (bf16)ka[1][r]};
-      *reinterpret_cast<bf16x2_t*>(&sm.QA[tl][2 * cp]) = bf16x2_t{(bf16)qa[0][r], (bf16)qa[1][r]};
-      *reinterpret_cast<bf16x2_t*>(&sm.KE[tl][2 * cp]) = bf16x2_t{(bf16)ke[0][r], (bf16)ke[1][r]};
+      *reinterpret_cast<uint32_t*>(&KA[tl][2 * cp]) = po.ka[r];
+      if constexpr (MODE == kOutput) *reinterpret_cast<uint32_t*>(&QA[tl][2 * cp]) = po.qa[r];
+      *reinterpret_cast<uint32_t*>(&KE[tl][2 * cp]) = po.ke[r];
     }
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      const int cc = 2 * cp + ch;
+      Pt[J][cc] = po.pblk[ch];
+      A0t[J][cc] = po.a0[ch];
+      Gt[J][cc] = po.a0[ch] * po.pblk[ch];
+    }
+    const int t2 = tid - 256;
+    const int upr = vcg / 8;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int u = t2 + 256 * i;
+      const int row = u / upr;
+      if (row < kChunk) *reinterpret_cast<uint4*>(&Vn[row][8 * (u % upr)]) = po.vv[i];
+    }
+    if (t2 < kChunk) betas[t2] = po.bt;
   }
-  if (tid < kChunk) sm.beta[tid] = tid < n_valid ? to_float(a.beta[(tok0 + tid) * a.H + h]) : 0.f;
-  const int extreme = __syncthreads_or(extreme_local);
+  __syncthreads();
+}
 
+// Everything after P1 (reads only LDS, plus global q/k/g on the rare
+// extreme-decay path).
+template <class IT, int MODE, bool LOADER>
+__device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h,
+                                            int vcg, int tid, const NextLoads<IT, MODE>& nl) {
+  const int lane = tid & 63;
+  const int wave = wave_of(tid);
+  const int n16 = lane & 15;
+  const int g4 = lane >> 4;
+  const int n_valid = cg.n_valid;
+  bf16(*KA)[kRow] = lds<bf16[kRow]>(sm, kOffKA);
+  bf16(*QA)[kRow] = lds<bf16[kRow]>(sm, kOffQA);
+  bf16(*KE)[kRow] = lds<bf16[kRow]>(sm, kOffKE);
+  bf16(*Lm)[72] = lds<bf16[72]>(sm, kOffL);
+  float(*Ld)[16][16] = lds<float[16][16]>(sm, kOffLd);
+  bf16(*Tinv)[16][16] = lds<bf16[16][16]>(sm, kOffTinv);
+  bf16(*TinvT)[16][16] = lds<bf16[16][16]>(sm, kOffTinvT);
+  float(*Gt)[kKey] = lds<float[kKey]>(sm, kOffTab);                      // G  [4][128]
+  float(*A0t)[kKey] = lds<float[kKey]>(sm, kOffTab + 4 * kKey * 4);      // A0 [4][128]
+  float(*Pt)[kKey] = lds<float[kKey]>(sm, kOffTab + 8 * kKey * 4);       // P  [4][128]
+  float(*Sc)[kKey] = lds<float[kKey]>(sm, kOffTab);                      // pair scales [10][128]
+  float(*Gs)[kKey] = lds<float[kKey]>(sm, kOffGs);
+  float(*Ge)[kKey] = lds<float[kKey]>(sm, kOffGe);
+  float* betas = lds<float>(sm, kOffBeta);
+  float* gam = lds<float>(sm, kOffGam);
+
+  if constexpr (LOADER) nl.template load_part<0>();
   // ---- P1b: block-level decay tables and gamma_C ---------------------------
+  int* flags = lds<int>(sm, kOffFlag);
   if (tid < kKey) {
     const int cc = tid;
     float G[4], A0[4], P[4];
+    bool ext = false;
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
-      G[J] = sm.G[J][cc];
-      A0[J] = sm.A0[J][cc];
-      P[J] = sm.P[J][cc];
+      G[J] = Gt[J][cc];
+      A0[J] = A0t[J][cc];
+      P[J] = Pt[J][cc];
+      ext = ext || !(P[J] >= kExtremeDecay);
     }
+    // a 16-row block decaying by more than 2^-100 takes the exact path below
+    const int any_ext = __any(ext) ? 1 : 0;
+    if (lane == 0) flags[wave] = any_ext;
     float pre = 1.f;
 #pragma unroll
     for (int J = 0; J < 4; ++J) {
-      sm.Gs[J][cc] = pre * A0[J];
+      Gs[J][cc] = pre * A0[J];
       pre *= G[J];
     }
     float post = 1.f;
 #pragma unroll
     for (int J = 3; J >= 0; --J) {
-      sm.Ge[J][cc] = post;
+      Ge[J][cc] = post;
       post *= G[J];
     }
-    reinterpret_cast<float*>(rec + rec_gam(a.V))[cc] = pre;  // exp(lg_63)
+    gam[cc] = pre;  // exp(lg_63)
     // scale of the k_j E_j operand for block pair (I, J): D_IJ = alpha_{16I} prod_{J<J'<I} G_J'
     // for J < I, 1 / P_I on the diagonal (written over G/A0/P of this same channel)
     int pidx = 0;
@@ -294,547 +564,717 @@ __global__ __launch_bounds__(kPrepThreads, 2) void chunk_prepare_kernel(const Pr
         } else {
           sc = P[I] > 0.f ? 1.f / P[I] : 0.f;
         }
-        sm.Sc[pidx][cc] = sc;
+        Sc[pidx][cc] = sc;
       }
     }
   }
   __syncthreads();
 
-  // ---- export: Q~ and K~^T fragments (read-only on the tables) -------------
-  for (int task = tid; task < 2048; task += kPrepThreads) {
+  if constexpr (LOADER) nl.template load_part<1>();
+  // ---- export: Q~ (phase C) and K~^T fragments ------------------------------
+  for (int task = (MODE == kOutput ? 0 : 1024) + tid; task < 2048; task += kThreads) {
     const int frag = (task >> 6) & 15;
     const int fl = task & 63;
     const int fi = fl & 15, fg = fl >> 4;
-    bf16x8_t out;
+    bf16x8_t o;
     if (task < 1024) {  // Q~ = exp(lg) q : fragment (I, s), lane (i, g)
       const int I = frag >> 2, st = frag & 3;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int ch = 32 * st + (e < 4 ? 4 * fg + e : 16 + 4 * fg + e - 4);
-        out[e] = (bf16)((float)sm.QA[16 * I + fi][ch] * sm.Gs[I][ch]);
+        const int ch = 32 * st + perm_index(e, fg);
+        o[e] = (bf16)((float)QA[16 * I + fi][ch] * Gs[I][ch]);
       }
-      *reinterpret_cast<bf16x8_t*>(rec + kRecQ + (static_cast<int64_t>(frag) * 64 + fl) * 16) = out;
+      *lds<bf16x8_t>(sm, kOffQf + (frag * 64 + fl) * 16) = o;
     } else {  // K~^T : fragment (ct, s'), lane (c, g)
       const int ct = frag >> 1, st = frag & 1;
       const int ch = 16 * ct + fi;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int tk = 32 * st + (e < 4 ? 4 * fg + e : 16 + 4 * fg + e - 4);
-        out[e] = (bf16)((float)sm.KE[tk][ch] * sm.Ge[tk >> 4][ch]);
+        const int tk = 32 * st + perm_index(e, fg);
+        o[e] = (bf16)((float)KE[tk][ch] * Ge[tk >> 4][ch]);
       }
-      *reinterpret_cast<bf16x8_t*>(rec + kRecKT + (static_cast<int64_t>(frag) * 64 + fl) * 16) = out;
+      *lds<bf16x8_t>(sm, kOffKTf + (frag * 64 + fl) * 16) = o;
     }
   }
 
+  if constexpr (LOADER) nl.template load_part<2>();
   // ---- P2: A (strict) and Aqk (causal) 16x16 blocks on MFMA ---------------
-  {
-    for (int p = wave; p < 10; p += 4) {
-      // block pair p = I (I + 1) / 2 + J, J <= I
-      const int I = p >= 6 ? 3 : (p >= 3 ? 2 : (p >= 1 ? 1 : 0));
-      const int J = p - I * (I + 1) / 2;
-      f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
-      f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
+  for (int p = wave; p < 10; p += 8) {
+    // block pair p = I (I + 1) / 2 + J, J <= I
+    const int I = p >= 6 ? 3 : (p >= 3 ? 2 : (p >= 1 ? 1 : 0));
+    const int J = p - I * (I + 1) / 2;
+    f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
+    f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int st = 0; st < 4; ++st) {
-        const int c0 = 32 * st + 8 * g4;
-        const bf16x8_t ke = *reinterpret_cast<const bf16x8_t*>(&sm.KE[16 * J + n16][c0]);
-        const f32x4_t sc0 = *reinterpret_cast<const f32x4_t*>(&sm.Sc[p][c0]);
-        const f32x4_t sc1 = *reinterpret_cast<const f32x4_t*>(&sm.Sc[p][c0 + 4]);
-        bf16x8_t af;
+    for (int st = 0; st < 4; ++st) {
+      const int c0 = 32 * st + 8 * g4;
+      const bf16x8_t ke = *reinterpret_cast<const bf16x8_t*>(&KE[16 * J + n16][c0]);
+      const f32x4_t sc0 = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0]);
+      const f32x4_t sc1 = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0 + 4]);
+      bf16x8_t af;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          af[e] = (bf16)((float)ke[e] * sc0[e]);
-          af[4 + e] = (bf16)((float)ke[4 + e] * sc1[e]);
-        }
-        const bf16x8_t kb = *reinterpret_cast<const bf16x8_t*>(&sm.KA[16 * I + n16][c0]);
-        const bf16x8_t qb = *reinterpret_cast<const bf16x8_t*>(&sm.QA[16 * I + n16][c0]);
-        akk = mfma32(af, kb, akk);
+      for (int e = 0; e < 4; ++e) {
+        af[e] = (bf16)((float)ke[e] * sc0[e]);
+        af[4 + e] = (bf16)((float)ke[4 + e] * sc1[e]);
+      }
+      const bf16x8_t kb = *reinterpret_cast<const bf16x8_t*>(&KA[16 * I + n16][c0]);
+      akk = mfma32(af, kb, akk);
+      if constexpr (MODE == kOutput) {
+        const bf16x8_t qb = *reinterpret_cast<const bf16x8_t*>(&QA[16 * I + n16][c0]);
         aqk = mfma32(af, qb, aqk);
       }
-      // lane (n16, g4) holds Akk[16I + n16][16J + 4 g4 + r] (and likewise Aqk)
-      const int i = 16 * I + n16;
-      const float bi = sm.beta[i];
-      bf16x4_t lrow;
-      bf16x4_t qrow;
+    }
+    // lane (n16, g4) holds A[16I + n16][16J + 4 g4 + r] (and likewise Aqk)
+    const int i = 16 * I + n16;
+    const float bi = betas[i];
+    bf16x4_t lrow;
+    bf16x4_t qrow;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int j = 16 * J + 4 * g4 + r;
-        const float vk = (j < i) ? akk[r] * bi : 0.f;
-        lrow[r] = (bf16)vk;
-        qrow[r] = (bf16)((j <= i) ? aqk[r] : 0.f);
-        if (I == J) sm.Ld[I][n16][4 * g4 + r] = vk;
-      }
-      *reinterpret_cast<bf16x4_t*>(&sm.L[i][16 * J + 4 * g4]) = lrow;
-      unsigned char* afrag = rec + kRecA + (static_cast<int64_t>(I * 2 + J / 2) * 64 + lane) * 16;
+    for (int r = 0; r < 4; ++r) {
+      const int j = 16 * J + 4 * g4 + r;
+      const float vk = (j < i) ? akk[r] * bi : 0.f;
+      lrow[r] = (bf16)vk;
+      qrow[r] = (bf16)((j <= i) ? aqk[r] : 0.f);
+      if (I == J) Ld[I][n16][4 * g4 + r] = vk;
+    }
+    *reinterpret_cast<bf16x4_t*>(&Lm[i][16 * J + 4 * g4]) = lrow;
+    if constexpr (MODE == kOutput) {
+      unsigned char* afrag = sm + kOffAf + ((I * 2 + J / 2) * 64 + lane) * 16;
       *reinterpret_cast<bf16x4_t*>(afrag + (J & 1) * 8) = qrow;
       if (I == J && (I & 1) == 0) *reinterpret_cast<bf16x4_t*>(afrag + 8) = bf16x4_t{};  // tile J = I+1 is above
     }
   }
+  if constexpr (LOADER) nl.template load_part<3>();
   __syncthreads();
 
+  if constexpr (LOADER) nl.template load_part<4>();
   // ---- exact diagonal blocks for chunks with extreme decay ----------------
-  if (extreme) {
-    float* Lr = reinterpret_cast<float*>(&sm.QA[0][0]);  // [64][128] f32, overlays QA and KE (dead now)
-    {
+  if (flags[0] | flags[1]) {
+    float* Lr = lds<float>(sm, kOffQA);  // [64][128] f32 over the dead q a and k E tiles
+    const int64_t krow = a.H * kKey;
+    if (wave < 4) {
       const int J = wave, cp = lane;
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch) {
         float run = 0.f;
         for (int r = 0; r < 16; ++r) {
           const int tl = 16 * J + r;
-          const float gvv = tl < n_valid ? to_float(a.g[(tok0 + tl) * krow + h * kKey + 2 * cp + ch]) : 0.f;
+          const float gvv = tl < n_valid ? to_float(a.g[(cg.tok0 + tl) * krow + h * kKey + 2 * cp + ch]) : 0.f;
           if (r > 0) run += gvv;
           Lr[tl * kKey + 2 * cp + ch] = run;
         }
       }
     }
     __syncthreads();
-    for (int task = tid; task < 4 * 136; task += kPrepThreads) {
+    for (int task = tid; task < 4 * 136; task += kThreads) {
       const int I = task / 136;
-      int p = task % 136;
+      const int p = task % 136;
       int il = 0;
       while ((il + 1) * (il + 2) / 2 <= p) ++il;
       const int jl = p - il * (il + 1) / 2;
       const int i = 16 * I + il, j = 16 * I + jl;
       float acc_k = 0.f, acc_q = 0.f;
       if (i < n_valid && j < n_valid) {
-        const int64_t oi = (tok0 + i) * krow + h * kKey;
-        const int64_t oj = (tok0 + j) * krow + h * kKey;
+        const int64_t oi = (cg.tok0 + i) * krow + h * kKey;
+        const int64_t oj = (cg.tok0 + j) * krow + h * kKey;
         for (int cc = 0; cc < kKey; ++cc) {
           const float e = fast_exp(Lr[i * kKey + cc] - Lr[j * kKey + cc]);
           const float kj = to_float(a.k[oj + cc]);
           acc_k += to_float(a.k[oi + cc]) * kj * e;
-          acc_q += to_float(a.q[oi + cc]) * kj * e;
+          if constexpr (MODE == kOutput) acc_q += to_float(a.q[oi + cc]) * kj * e;
         }
       }
       if (jl < il) {
-        const float vk = sm.beta[i] * acc_k;
-        sm.L[i][j] = (bf16)vk;
-        sm.Ld[I][il][jl] = vk;
+        const float vk = betas[i] * acc_k;
+        Lm[i][j] = (bf16)vk;
+        Ld[I][il][jl] = vk;
       }
-      const int fl = il + 16 * (jl >> 2);
-      bf16* afrag = reinterpret_cast<bf16*>(rec + kRecA + (static_cast<int64_t>(I * 2 + I / 2) * 64 + fl) * 16);
-      afrag[(I & 1) * 4 + (jl & 3)] = (bf16)acc_q;
+      if constexpr (MODE == kOutput) {
+        const int fl = il + 16 * (jl >> 2);
+        bf16* afrag = reinterpret_cast<bf16*>(sm + kOffAf + ((I * 2 + I / 2) * 64 + fl) * 16);
+        afrag[(I & 1) * 4 + (jl & 3)] = (bf16)acc_q;
+      }
     }
     __syncthreads();
   }
 
-  // ---- P3: inverses of the four unit-lower diagonal blocks (f32) ----------
-  if (lane < 16) {
-    const int I = wave;
-    float x[16];
+  if constexpr (LOADER) nl.template load_part<5>();
+  // ---- P3: inverses T_I of the four unit-lower diagonal blocks (f32), waves
+  // 0-3; meanwhile waves 4-7 export Kgamma = exp(lg) k over the dead q a tile
+  if (wave < 4) {
+    if (lane < 16) {
+      // column `lane` of T_I, row by row; one row of L is loaded at a time
+      const int I = wave;
+      float x[16];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      float acc = (r == lane) ? 1.f : 0.f;
+      for (int r = 0; r < 16; ++r) {
+        float row[16];
 #pragma unroll
-      for (int j = 0; j < r; ++j) acc -= sm.Ld[I][r][j] * x[j];
-      x[r] = acc;
+        for (int q4 = 0; q4 < 4; ++q4) {
+          const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(&Ld[I][r][4 * q4]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) row[4 * q4 + e] = v4[e];
+        }
+        float acc = (r == lane) ? 1.f : 0.f;
+#pragma unroll
+        for (int j = 0; j < r; ++j) acc -= row[j] * x[j];
+        x[r] = acc;
+        Tinv[I][r][lane] = (bf16)acc;
+        __builtin_amdgcn_sched_barrier(0);
+      }
+      bf16x8_t t0, t1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        t0[e] = (bf16)x[e];
+        t1[e] = (bf16)x[8 + e];
+      }
+      *reinterpret_cast<bf16x8_t*>(&TinvT[I][lane][0]) = t0;
+      *reinterpret_cast<bf16x8_t*>(&TinvT[I][lane][8]) = t1;
     }
+  } else {
+    for (int task = tid - 256; task < 1024; task += 256) {  // -Kgamma : fragment (I, s), lane (i, g)
+      const int frag = task >> 6;
+      const int fl = task & 63;
+      const int fi = fl & 15, fg = fl >> 4;
+      const int I = frag >> 2, st = frag & 3;
+      bf16x8_t o;
 #pragma unroll
-    for (int r = 0; r < 16; ++r) sm.Tinv[I][r][lane] = (bf16)x[r];
+      for (int e = 0; e < 8; ++e) {
+        const int ch = 32 * st + perm_index(e, fg);
+        o[e] = (bf16)(-(float)KA[16 * I + fi][ch] * Gs[I][ch]);
+      }
+      *lds<bf16x8_t>(sm, kOffKgf + (frag * 64 + fl) * 16) = o;
+    }
+    if constexpr (LOADER) nl.template load_part<6>();
   }
   __syncthreads();
 
-  // ---- P4: blocked forward substitution  [W | U] = L^{-1} diag(beta) [Kgamma | v]
-  // Wave w owns column tiles nt = w, w+4, ... of the 8 + V/16 tiles (8 key
-  // tiles of W, V/16 value tiles of U) and walks the four row blocks once for
-  // all of them, so the L and inverse fragments are read once per block and
-  // the column tiles form independent MFMA chains.
-  {
-    constexpr int kMaxT = 6;  // up to (8 + 256/16) / 4 column tiles per wave
-    const int n_tiles = 8 + static_cast<int>(a.V / 16);
-    const int64_t vrow = a.H * a.V;
-    int nts[kMaxT];
-    int nown = 0;
+  // ---- P4: M = (I + B)^{-1} diag(beta), B = diag(beta) A strictly lower.
+  // With N = (I + B)^{-1}, block row I of Z = N^T satisfies
+  //   Z_II = T_I^T ;  Z_IJ = -T_J^T sum_{K=J+1..I} B_KJ^T Z_IK   (J < I),
+  // a chain in which Z_IK is the B operand of the next product.  In the
+  // accumulator layout lane (i, g) holds Z_IJ[4 g + r][i] = N[16 I + i][16 J + 4 g + r],
+  // which is half of an A fragment of M (rows i, reduction over j); the
+  // fragments go over the dead k E tile.  Wave I < 4 owns block row I.
+}
+
+// ---- P4: M, block row I by wave I < 4 (the loader waves are free here) ------
+template <class IT, int MODE, bool LOADER>
+__device__ __forceinline__ void prepare_m(unsigned char* sm, int tid, const NextLoads<IT, MODE>& nl) {
+  const int lane = tid & 63;
+  const int wave = wave_of(tid);
+  if constexpr (LOADER) nl.template load_part<7>();
+  switch (wave) {
+    case 0: m_block_row<0>(sm, lane); break;
+    case 1: m_block_row<1>(sm, lane); break;
+    case 2: m_block_row<2>(sm, lane); break;
+    case 3: m_block_row<3>(sm, lane); break;
+    default: break;
+  }
+  __syncthreads();
+}
+
+// ---- per-chunk state advance of one wave's pair of 16-column tiles ----------
+// ut[t] >= 0: U tile index of tile t (value columns); -1: a transition column
+// (U = 0).  MODE == kOutput also forms O = Q~ S + Aqk V~ for both tiles.
+template <int MODE>
+__device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[2][8], const int (&ut)[2], int lane,
+                                          f32x4_t (&O)[2][4]) {
+  const int g4 = lane >> 4;
+  const int n16 = lane & 15;
+  const bf16(*Vn)[kRow] = reinterpret_cast<const bf16(*)[kRow]>(sm + kOffVn);
+  // Y = v - Kgamma S (value columns) or -Kgamma S (transition columns)
+  f32x4_t Y[2][4];
 #pragma unroll
-    for (int t = 0; t < kMaxT; ++t) {
-      nts[t] = wave + 4 * t;
-      if (nts[t] < n_tiles) ++nown;
-    }
-    // right-hand sides diag(beta) [Kgamma | v], loaded up front
-    float rhs[kMaxT][4][4];
-#pragma unroll
-    for (int t = 0; t < kMaxT; ++t) {
-      if (t >= nown) {
-#pragma unroll
-        for (int I = 0; I < 4; ++I)
-#pragma unroll
-          for (int r = 0; r < 4; ++r) rhs[t][I][r] = 0.f;
-        continue;
-      }
-      const int nt = nts[t];
-      const bool is_w = nt < 8;
-      const int col = 16 * (is_w ? nt : nt - 8) + n16;
-#pragma unroll
-      for (int I = 0; I < 4; ++I) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int tl = 16 * I + 4 * g4 + r;
-          float val;
-          if (is_w)
-            val = (float)sm.KA[tl][col] * sm.Gs[I][col];
-          else
-            val = to_float(a.v[(tok0 + (tl < n_valid ? tl : 0)) * vrow + h * a.V + col]);
-          rhs[t][I][r] = (tl < n_valid ? val : 0.f) * sm.beta[tl];
-        }
-      }
-    }
-    f32x4_t X[kMaxT][4];
+  for (int t = 0; t < 2; ++t) {
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      f32x4_t acc[kMaxT];
+      if (ut[t] >= 0) {
 #pragma unroll
-      for (int t = 0; t < kMaxT; ++t) acc[t] = f32x4_t{rhs[t][I][0], rhs[t][I][1], rhs[t][I][2], rhs[t][I][3]};
-#pragma unroll
-      for (int J = 0; J < I; ++J) {
-        const bf16x4_t la = negate_bf16(*reinterpret_cast<const bf16x4_t*>(&sm.L[16 * I + n16][16 * J + 4 * g4]));
-#pragma unroll
-        for (int t = 0; t < kMaxT; ++t) {
-          if (t >= nown) continue;
-          const bf16x4_t xb = {(bf16)X[t][J][0], (bf16)X[t][J][1], (bf16)X[t][J][2], (bf16)X[t][J][3]};
-          acc[t] = mfma16(la, xb, acc[t]);
-        }
-      }
-      const bf16x4_t ta = *reinterpret_cast<const bf16x4_t*>(&sm.Tinv[I][n16][4 * g4]);
-#pragma unroll
-      for (int t = 0; t < kMaxT; ++t) {
-        if (t >= nown) continue;
-        const bf16x4_t ab = {(bf16)acc[t][0], (bf16)acc[t][1], (bf16)acc[t][2], (bf16)acc[t][3]};
-        X[t][I] = mfma16(ta, ab, f32x4_t{0.f, 0.f, 0.f, 0.f});
-      }
-    }
-    // exports
-#pragma unroll
-    for (int t = 0; t < kMaxT; ++t) {
-      if (t >= nown) continue;
-      const int nt = nts[t];
-      if (nt < 8) {
-        // scatter into W fragments: channel 16 nt + n16 -> step st, lane group gq, element eq
-        const int st = nt >> 1;
-        const int gq = n16 >> 2;
-        const int eq = 4 * (nt & 1) + (n16 & 3);
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int il = 4 * g4 + r;
-            bf16* dst =
-                reinterpret_cast<bf16*>(rec + kRecW + (static_cast<int64_t>(I * 4 + st) * 64 + il + 16 * gq) * 16);
-            dst[eq] = (bf16)X[t][I][r];
-          }
-        }
+        for (int r = 0; r < 4; ++r) Y[t][I][r] = (float)Vn[16 * I + 4 * g4 + r][16 * ut[t] + n16];
       } else {
-        const int vt = nt - 8;
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          *reinterpret_cast<bf16x4_t*>(rec + kRecU + (static_cast<int64_t>(vt * 4 + I) * 64 + lane) * 8) =
-              bf16x4_t{(bf16)X[t][I][0], (bf16)X[t][I][1], (bf16)X[t][I][2], (bf16)X[t][I][3]};
-        }
+        Y[t][I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
+      if constexpr (MODE == kOutput) O[t][I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
   }
-}
-
-// ---- scan kernel ----------------------------------------------------------
-// One workgroup of three waves per (sequence, head, 32 value columns).
-// Waves 0 and 1 ("compute") own the 16-column state slices
-// S[:, 16 (2 wp + w) .. +16] in accumulator registers; they only read LDS,
-// run MFMAs and issue output stores, and never wait on vector memory.
-// Wave 2 ("copier") moves the next chunk's record (W, Q, KT, A fragments,
-// the two U tiles and gamma: 60.5 KB) into the other of two LDS buffers with
-// direct global->LDS loads and touches the record a few chunks ahead so that
-// the copy hits L2.  The roles run separate loops with one barrier per chunk.
-constexpr int kScanComputeWaves = 2;
-constexpr int kScanThreads = 64 * (kScanComputeWaves + 1);
-constexpr int kScanShared = 57344;                                       // W | Q | KT | A
-constexpr int kScanBuf = kScanShared + kScanComputeWaves * 2048 + 512;   // + U tiles + gamma = 61952 B
-constexpr int kScanUnits = kScanShared / 16;                             // 16-byte units of the shared part
-constexpr int kScanPrefetch = 4;
-constexpr int kWarmLoads = 8;                                            // 8 x 64 lanes x 128 B = 64 KB
-
-template <class IT>
-struct ScanArgs {
-  IT* out;
-  const float* s_in;
-  float* s_out;
-  SeqDesc seq;
-  const int32_t* chunk_start;
-  const unsigned char* records;
-  int64_t N, H, V;
-};
-
-// copier wave: one chunk's record pieces into an LDS buffer
-__device__ __forceinline__ void scan_copy(const unsigned char* rec, unsigned char* buf, int64_t vt0, int ntiles,
-                                          int64_t gam_off, int lane) {
-#pragma unroll 8
-  for (int i = 0; i < kScanUnits / 64; ++i)  // 56 instructions of 64 x 16 B
-    __builtin_amdgcn_global_load_lds(rec + (i * 64 + lane) * 16, buf + i * 1024, 16, 0, 0);
-  for (int t = 0; t < 2 * ntiles; ++t)       // U tiles: 2 instructions each
-    __builtin_amdgcn_global_load_lds(rec + kRecU + vt0 * 2048 + (t * 64 + lane) * 16, buf + kScanShared + t * 1024,
-                                     16, 0, 0);
-  if (lane < 32)  // gamma
-    __builtin_amdgcn_global_load_lds(rec + gam_off + lane * 16, buf + kScanShared + kScanComputeWaves * 2048, 16, 0,
-                                     0);
-}
-
-// copier wave: touch one dword of each 128-byte line of a future record's
-// shared part (the words land in a scratch LDS area that is never read)
-__device__ __forceinline__ void scan_warm_l2(const unsigned char* rec, unsigned char* scratch, int lane) {
-#pragma unroll
-  for (int k = 0; k < kWarmLoads; ++k) {
-    int off = (k * 64 + lane) * 128;
-    off = off < kScanShared - 4 ? off : kScanShared - 4;
-    __builtin_amdgcn_global_load_lds(rec + off, scratch, 4, 0, 0);
-  }
-}
-
-// barrier without a memory fence: the asm statements only stop the compiler
-// from moving memory accesses across it; LDS ordering comes from the waits
-// each role performs before arriving
-__device__ __forceinline__ void scan_barrier() {
-  asm volatile("" ::: "memory");
-  __builtin_amdgcn_s_barrier();
-  asm volatile("" ::: "memory");
-}
-
-template <class IT>
-__device__ __forceinline__ void scan_chunk(const unsigned char* buf, f32x4_t (&S)[8], int w, int lane,
-                                           f32x4_t (&O)[4]) {
-  // Two-stage software pipeline over the reduction steps: the fragments of
-  // step st + 1 are read from LDS while the 8 products of step st run.
-  auto load_wq = [&](int st, bf16x8_t (&wf)[4], bf16x8_t (&qf)[4]) {
+  // one reduction step at a time: the B operands of the step come from row
+  // tiles 2 st and 2 st + 1 of the state, and the -Kgamma and Q~ fragments of
+  // the step serve both tiles (Q~ S is the first part of the output); the
+  // fragments of step st + 1 are read while the products of step st run
+  auto load_step = [&](int st, bf16x8_t (&kf)[4], bf16x8_t (&qf)[4]) {
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      wf[I] = *reinterpret_cast<const bf16x8_t*>(buf + kRecW + ((I * 4 + st) * 64 + lane) * 16);
-      qf[I] = *reinterpret_cast<const bf16x8_t*>(buf + kRecQ + ((I * 4 + st) * 64 + lane) * 16);
+      kf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kOffKgf + ((I * 4 + st) * 64 + lane) * 16);
+      if constexpr (MODE == kOutput)
+        qf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kOffQf + ((I * 4 + st) * 64 + lane) * 16);
     }
   };
-  bf16x8_t wa[4], qa[4], wb[4], qb[4];
-  bf16x4_t uf[4];
-#pragma unroll
-  for (int I = 0; I < 4; ++I)
-    uf[I] = *reinterpret_cast<const bf16x4_t*>(buf + kScanShared + w * 2048 + (I * 64 + lane) * 8);
-  load_wq(0, wa, qa);
-  bf16x8_t Sb[4];
+  bf16x8_t kfa[4], qfa[4], kfb[4], qfb[4];
+  load_step(0, kfa, qfa);
 #pragma unroll
   for (int st = 0; st < 4; ++st) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      Sb[st][r] = (bf16)S[2 * st][r];
-      Sb[st][4 + r] = (bf16)S[2 * st + 1][r];
-    }
-  }
-  f32x4_t Vt[4];
-#pragma unroll
-  for (int I = 0; I < 4; ++I) {
-    Vt[I] = f32x4_t{(float)uf[I][0], (float)uf[I][1], (float)uf[I][2], (float)uf[I][3]};
-    O[I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  }
-#pragma unroll
-  for (int st = 0; st < 4; ++st) {
-    bf16x8_t(&wc)[4] = (st & 1) ? wb : wa;
-    bf16x8_t(&qc)[4] = (st & 1) ? qb : qa;
+    bf16x8_t(&kf)[4] = (st & 1) ? kfb : kfa;
+    bf16x8_t(&qf)[4] = (st & 1) ? qfb : qfa;
     if (st + 1 < 4) {
       if (st & 1)
-        load_wq(st + 1, wa, qa);
+        load_step(st + 1, kfa, qfa);
       else
-        load_wq(st + 1, wb, qb);
+        load_step(st + 1, kfb, qfb);
     }
-    __builtin_amdgcn_sched_barrier(0);
+    bf16x8_t sb[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        sb[t][r] = (bf16)S[t][2 * st][r];
+        sb[t][4 + r] = (bf16)S[t][2 * st + 1][r];
+      }
+    }
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      Vt[I] = mfma32(negate_bf16(wc[I]), Sb[st], Vt[I]);
-      O[I] = mfma32(qc[I], Sb[st], O[I]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-  }
-  // Aqk fragments used: (I, s') for s' <= I / 2 -> slots 0, 2, 4, 5, 6, 7;
-  // gamma and the first half of the K~^T fragments
-  bf16x8_t af[6];
 #pragma unroll
-  for (int j = 0; j < 6; ++j) {
-    const int slot = j < 2 ? 2 * j : j + 2;
-    af[j] = *reinterpret_cast<const bf16x8_t*>(buf + kRecA + (slot * 64 + lane) * 16);
-  }
-  const int g4 = lane >> 4;
-  const float* gam = reinterpret_cast<const float*>(buf + kScanShared + kScanComputeWaves * 2048);
-  f32x4_t gm[8];
-  bf16x8_t kf[8][2];
+      for (int t = 0; t < 2; ++t) Y[t][I] = mfma32(kf[I], sb[t], Y[t][I]);
+      if constexpr (MODE == kOutput) {
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    gm[ct] = *reinterpret_cast<const f32x4_t*>(gam + 16 * ct + 4 * g4);
-#pragma unroll
-    for (int st = 0; st < 2; ++st)
-      kf[ct][st] = *reinterpret_cast<const bf16x8_t*>(buf + kRecKT + ((ct * 2 + st) * 64 + lane) * 16);
-  }
-  bf16x8_t Vb[2];
-#pragma unroll
-  for (int st = 0; st < 2; ++st) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      Vb[st][r] = (bf16)Vt[2 * st][r];
-      Vb[st][4 + r] = (bf16)Vt[2 * st + 1][r];
+        for (int t = 0; t < 2; ++t) O[t][I] = mfma32(qf[I], sb[t], O[t][I]);
+      }
     }
   }
-  __builtin_amdgcn_sched_barrier(0);
-  O[0] = mfma32(af[0], Vb[0], O[0]);
-  O[1] = mfma32(af[1], Vb[0], O[1]);
-  O[2] = mfma32(af[2], Vb[0], O[2]);
-  O[2] = mfma32(af[3], Vb[1], O[2]);
-  O[3] = mfma32(af[4], Vb[0], O[3]);
-  O[3] = mfma32(af[5], Vb[1], O[3]);
+  // lower-triangular 64 x 64 fragments (I, s') with s' <= I / 2 sit in slots 0, 2, 4, 5, 6, 7
+  auto lower_product = [&](int off, const bf16x8_t (&xb)[2][2], f32x4_t (&acc)[2][4]) {
+    bf16x8_t af[6];
 #pragma unroll
-  for (int ct = 4; ct < 8; ++ct) {
-    gm[ct] = *reinterpret_cast<const f32x4_t*>(gam + 16 * ct + 4 * g4);
+    for (int j = 0; j < 6; ++j) {
+      const int slot = j < 2 ? 2 * j : j + 2;
+      af[j] = *reinterpret_cast<const bf16x8_t*>(sm + off + (slot * 64 + lane) * 16);
+    }
 #pragma unroll
-    for (int st = 0; st < 2; ++st)
-      kf[ct][st] = *reinterpret_cast<const bf16x8_t*>(buf + kRecKT + ((ct * 2 + st) * 64 + lane) * 16);
-  }
+    for (int j = 0; j < 6; ++j) {
+      const int I = j < 2 ? j : (j < 4 ? 2 : 3);
+      const int sp = (j == 3 || j == 5) ? 1 : 0;
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    S[ct] *= gm[ct];
+      for (int t = 0; t < 2; ++t) acc[t][I] = mfma32(af[j], xb[t][sp], acc[t][I]);
+    }
+  };
+  auto pack = [&](const f32x4_t (&x)[2][4], bf16x8_t (&xb)[2][2]) {
 #pragma unroll
-    for (int st = 0; st < 2; ++st) S[ct] = mfma32(kf[ct][st], Vb[st], S[ct]);
-  }
-  __builtin_amdgcn_sched_barrier(0);
+    for (int t = 0; t < 2; ++t) {
 #pragma unroll
-  for (int ct = 4; ct < 8; ++ct) {
-    S[ct] *= gm[ct];
+      for (int st = 0; st < 2; ++st) {
 #pragma unroll
-    for (int st = 0; st < 2; ++st) S[ct] = mfma32(kf[ct][st], Vb[st], S[ct]);
+        for (int r = 0; r < 4; ++r) {
+          xb[t][st][r] = (bf16)x[t][2 * st][r];
+          xb[t][st][4 + r] = (bf16)x[t][2 * st + 1][r];
+        }
+      }
+    }
+  };
+  // V~ = M Y
+  bf16x8_t Yb[2][2];
+  pack(Y, Yb);
+  f32x4_t Vt[2][4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t)
+#pragma unroll
+    for (int I = 0; I < 4; ++I) Vt[t][I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+  lower_product(kOffMf, Yb, Vt);
+  bf16x8_t Vb[2][2];
+  pack(Vt, Vb);
+  // O += Aqk V~
+  if constexpr (MODE == kOutput) lower_product(kOffAf, Vb, O);
+  // S <- diag(gamma) S + K~^T V~
+  const float* gam = reinterpret_cast<const float*>(sm + kOffGam);
+#pragma unroll
+  for (int h4 = 0; h4 < 2; ++h4) {
+    bf16x8_t kt[4][2];
+    f32x4_t gm[4];
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      const int ct = 4 * h4 + c4;
+      gm[c4] = *reinterpret_cast<const f32x4_t*>(gam + 16 * ct + 4 * g4);
+#pragma unroll
+      for (int sp = 0; sp < 2; ++sp)
+        kt[c4][sp] = *reinterpret_cast<const bf16x8_t*>(sm + kOffKTf + ((ct * 2 + sp) * 64 + lane) * 16);
+    }
+#pragma unroll
+    for (int c4 = 0; c4 < 4; ++c4) {
+      const int ct = 4 * h4 + c4;
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        S[t][ct] *= gm[c4];
+        S[t][ct] = mfma32(kt[c4][0], Vb[t][0], S[t][ct]);
+        S[t][ct] = mfma32(kt[c4][1], Vb[t][1], S[t][ct]);
+      }
+    }
   }
 }
 
-// Store a chunk's 64 x 16 output tile.  The accumulator layout (lane (n, g)
-// holds rows 16 I + 4 g + r of column n) is transposed through a per-wave
-// 2 KB LDS stage so that each lane writes 16 contiguous bytes of a row.
+// Store a chunk's 64 x (16 ntile) output slice of one wave.  The accumulator
+// layout (lane (n, g) holds rows 16 I + 4 g + r of column n) is transposed
+// through a per-wave 4 KB LDS stage so that each lane writes 16 contiguous
+// bytes of a row.
 template <class IT>
-__device__ __forceinline__ void scan_store_out(const f32x4_t (&O)[4], IT* out, int64_t tokbase, int64_t n_span,
-                                               int64_t H, int64_t h, int64_t V, int64_t col0, int lane,
-                                               IT* stage) {
+__device__ __forceinline__ void store_out(const f32x4_t (&O)[2][4], int ntile, IT* out, const ChunkGeo& cg,
+                                          int64_t H, int64_t h, int64_t V, int64_t col, int lane, IT* stage) {
   const int g4 = lane >> 4, n16 = lane & 15;
 #pragma unroll
-  for (int I = 0; I < 4; ++I) {
+  for (int t = 0; t < 2; ++t) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) stage[(16 * I + 4 * g4 + r) * 16 + n16] = from_compute<IT>(O[I][r]);
+    for (int I = 0; I < 4; ++I) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) stage[(16 * I + 4 * g4 + r) * 32 + 16 * t + n16] = from_compute<IT>(O[t][I][r]);
+    }
   }
   // lanes now read what other lanes of the wave wrote: complete the writes and
   // keep the compiler from moving the reads above them
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
 #pragma unroll
-  for (int j = 0; j < 2; ++j) {
-    const int row = j * 32 + (lane >> 1);
-    const int half = lane & 1;
-    const uint4 val = *reinterpret_cast<const uint4*>(stage + row * 16 + 8 * half);
-    if (row < n_span) *reinterpret_cast<uint4*>(out + ((tokbase + row) * H + h) * V + col0 + 8 * half) = val;
+  for (int u = 0; u < 4; ++u) {
+    const int unit = lane + 64 * u;
+    const int row = unit >> 2;
+    const int c8 = unit & 3;
+    const uint4 val = *reinterpret_cast<const uint4*>(stage + row * 32 + 8 * c8);
+    if (row < cg.n_span && c8 < 2 * ntile)
+      *reinterpret_cast<uint4*>(out + ((cg.tok0 + row) * H + h) * V + col + 8 * c8) = val;
   }
 }
 
-template <class IT>
-__global__ __launch_bounds__(kScanThreads) void chunk_scan_kernel(const ScanArgs<IT> a) {
-  __shared__ __align__(16) unsigned char buf0[kScanBuf];
-  __shared__ __align__(16) unsigned char buf1[kScanBuf];
-  __shared__ __align__(16) unsigned char warm[256];
-  __shared__ __align__(16) IT stage_all[kScanComputeWaves][64 * 16];  // output transpose, one tile per wave
-  const int64_t nvt = a.V / 16;
-  const int64_t nwp = (nvt + kScanComputeWaves - 1) / kScanComputeWaves;  // workgroups per (sequence, head)
-  const int64_t bid = blockIdx.x;
-  const int64_t wp = bid % nwp;
-  const int64_t h = (bid / nwp) % a.H;
-  const int64_t s = bid / (nwp * a.H);
+// ---- phases A and C -----------------------------------------------------------
+// Waves 0-3 (scanners) hold the state tiles: in phase C wave w owns tiles
+// 2w, 2w+1 of the column group; in phase A with the transition tracked it
+// also owns tiles 2w+8, 2w+9 (the 16 tiles are [value tiles | transition
+// tiles]).  Waves 4-7 (loaders) hold the raw inputs of the next chunk.  The
+// two roles run separate loops with the same barriers, so neither role's
+// registers are live in the other's code.
+template <class IT, int MODE>
+__global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<IT> a) {
+  extern __shared__ __align__(16) unsigned char sm[];
+  // one-dimensional grid, segment slowest: the workgroups past the real
+  // segment count (the grid is an upper bound) are all at the end, so the
+  // active ones spread evenly over the XCDs
+  const int64_t ncg = (a.V + kColGroup - 1) / kColGroup;
+  const int64_t gsg = blockIdx.x / (a.H * ncg);
+  const int64_t h = (blockIdx.x / ncg) % a.H;
+  const int64_t cgi = blockIdx.x % ncg;
+  if (gsg >= a.seg_start[a.N]) return;  // uniform
+  const int64_t s = find_seq(a.seg_start, a.N, gsg);
+  const int64_t lg = gsg - a.seg_start[s];
+  const int64_t nseg = a.seg_start[s + 1] - a.seg_start[s];
+  if (MODE == kSummary && lg == nseg - 1) return;  // the last segment needs no summary
+  const SeqRange sr = seq_range(a.seq, s);
+  const int64_t cs = a.chunk_start[s];
+  const int64_t c_begin = cs + lg * a.L;
+  const int64_t c_end_seq = a.chunk_start[s + 1];
+  const int64_t c_end = (c_begin + a.L < c_end_seq) ? c_begin + a.L : c_end_seq;
+
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int w = tid >> 6;
-  const int64_t vt0 = wp * kScanComputeWaves;
-  const int ntiles = static_cast<int>(nvt - vt0 < kScanComputeWaves ? nvt - vt0 : kScanComputeWaves);
-  const SeqRange sr = seq_range(a.seq, s);
-  const int64_t c0 = a.chunk_start[s];
-  const int64_t c1 = a.chunk_start[s + 1];
-  const int64_t rb = rec_bytes(a.V);
-  auto rec_of = [&](int64_t c) { return a.records + (c * a.H + h) * rb; };
-
-  if (w == kScanComputeWaves) {
-    // ---------------- copier wave ----------------
-    const int64_t gam_off = rec_gam(a.V);
-    for (int64_t p = c0 + 1; p < c1 && p <= c0 + kScanPrefetch; ++p) scan_warm_l2(rec_of(p), warm, lane);
-    scan_copy(rec_of(c0), buf0, vt0, ntiles, gam_off, lane);
-    __builtin_amdgcn_s_waitcnt(0);
-    scan_barrier();
-    // step c: the compute waves read buffer (c - c0) % 2; the copier fills the other
-    // with chunk c + 1, waits for it (the warming loads issued after it may stay in
-    // flight: a wave's vector memory loads retire in issue order), then arrives
-    for (int64_t c = c0; c < c1; ++c) {
-      const bool odd = ((c - c0) & 1) != 0;
-      if (c + 1 < c1) {
-        if (odd)
-          scan_copy(rec_of(c + 1), buf0, vt0, ntiles, gam_off, lane);
-        else
-          scan_copy(rec_of(c + 1), buf1, vt0, ntiles, gam_off, lane);
-      }
-      // always exactly kWarmLoads warming loads (clamped to a valid record) so
-      // that vmcnt(kWarmLoads) below means "the copy has landed"
-      scan_warm_l2(rec_of(c + 1 + kScanPrefetch < c1 ? c + 1 + kScanPrefetch : c1 - 1), warm, lane);
-      asm volatile("" ::: "memory");
-      // s_waitcnt vmcnt(kWarmLoads) expcnt(7) lgkmcnt(15)
-      __builtin_amdgcn_s_waitcnt((kWarmLoads & 15) | (7 << 4) | (15 << 8) | ((kWarmLoads >> 4) << 14));
-      scan_barrier();
-    }
-    __builtin_amdgcn_s_waitcnt(0);  // no copy may land in LDS after the workgroup ends
-    return;
-  }
-
-  // ---------------- compute waves ----------------
-  const bool active = w < ntiles;
+  const int w = wave_of(tid);
   const int n16 = lane & 15;
   const int g4 = lane >> 4;
-  const int64_t col = 16 * (vt0 + w) + n16;
+  const int64_t col0 = cgi * kColGroup;
+  const int vcg = static_cast<int>(a.V - col0 < kColGroup ? a.V - col0 : kColGroup);
+  const int nvt = vcg / 16;
+  const bool track_p = MODE == kSummary && lg > 0 && cgi == 0;
+  const int ntiles = nvt + (track_p ? 8 : 0);
   const int64_t sbase = (s * a.H + h) * kKey * a.V;
-  f32x4_t S[8];
+  constexpr int kPairs = MODE == kSummary ? 2 : 1;  // tile pairs per scanner wave
+
+  f32x4_t S[kPairs][2][8];
+  if (w < 4) {
+    // ---------------- scanners ----------------
 #pragma unroll
-  for (int ct = 0; ct < 8; ++ct) {
+    for (int pp = 0; pp < kPairs; ++pp) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int64_t row = 16 * ct + 4 * g4 + r;
-      S[ct][r] = (a.s_in && active) ? a.s_in[sbase + row * a.V + col] : 0.f;
-    }
-  }
-  scan_barrier();
-  f32x4_t O[4];
-  for (int64_t c = c0; c < c1; ++c) {
-    const int64_t lc = c - c0;
-    if (active) {
-      if ((lc & 1) == 0)
-        scan_chunk<IT>(buf0, S, w, lane, O);
-      else
-        scan_chunk<IT>(buf1, S, w, lane, O);
-      const int64_t n_span = sr.span - kChunk * lc < kChunk ? sr.span - kChunk * lc : kChunk;
-      scan_store_out<IT>(O, a.out, sr.start + kChunk * lc, n_span, a.H, h, a.V, col - n16, lane, stage_all[w]);
-    }
-    asm volatile("" ::: "memory");
-    __builtin_amdgcn_s_waitcnt((63 & 15) | (7 << 4) | (0 << 8) | ((63 >> 4) << 14));  // lgkmcnt(0): LDS reads done
-    scan_barrier();
-  }
-  if (a.s_out && active) {
+      for (int t = 0; t < 2; ++t) {
+        const int tile = 2 * w + 8 * pp + t;
 #pragma unroll
-    for (int ct = 0; ct < 8; ++ct) {
+        for (int ct = 0; ct < 8; ++ct) {
+          if (tile < nvt) {
+            if (lg == 0) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int64_t row = 16 * ct + 4 * g4 + r;
-        a.s_out[sbase + row * a.V + col] = S[ct][r];
+              for (int r = 0; r < 4; ++r) {
+                const int64_t row = 16 * ct + 4 * g4 + r;
+                S[pp][t][ct][r] = a.s_in ? a.s_in[sbase + row * a.V + col0 + 16 * tile + n16] : 0.f;
+              }
+            } else if (MODE == kOutput) {
+              const float* p = a.seg_state + (gsg * a.H + h) * seg_state_floats(a.V) +
+                               ((col0 / 16 + tile) * 8 + ct) * 256 + lane * 4;
+              S[pp][t][ct] = *reinterpret_cast<const f32x4_t*>(p);
+            } else {
+              S[pp][t][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+            }
+          } else if (tile < ntiles) {  // transition columns start at the identity
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              S[pp][t][ct][r] = (16 * ct + 4 * g4 + r == 16 * (tile - nvt) + n16) ? 1.f : 0.f;
+          } else {
+            S[pp][t][ct] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+          }
+        }
       }
+    }
+    P1Out none;
+    const NextLoads<IT, MODE> nl{};
+    for (int64_t c = c_begin; c < c_end; ++c) {
+      const ChunkGeo geo = chunk_geo(sr, c - cs);
+      // an opaque copy of the thread index keeps the compiler from hoisting
+      // the many lane-dependent LDS addresses of a chunk out of the loop,
+      // where they would stay live (and spill) next to the state tiles
+      const int tid_c = opaque(tid);
+      p1_write<MODE, false>(sm, none, vcg, tid_c);
+      prepare_mid<IT, MODE, false>(sm, a, geo, h, vcg, tid_c, nl);
+      prepare_m<IT, MODE, false>(sm, tid_c, nl);
+#pragma unroll
+      for (int pp = 0; pp < kPairs; ++pp) {
+        const int tile0 = 2 * w + 8 * pp;
+        if (tile0 < ntiles) {
+          const int ut[2] = {tile0 < nvt ? tile0 : -1, tile0 + 1 < nvt ? tile0 + 1 : -1};
+          f32x4_t O[2][4];
+          scan_pair<MODE>(sm, S[pp], ut, tid_c & 63, O);
+          if constexpr (MODE == kOutput) {
+            const int nt = ntiles - tile0 < 2 ? ntiles - tile0 : 2;
+            store_out<IT>(O, nt, a.out, geo, a.H, h, a.V, col0 + 16 * tile0, tid_c & 63,
+                          lds<IT>(sm, kOffStage + w * 4096));
+          }
+        }
+      }
+      __syncthreads();
+    }
+  } else {
+    // ---------------- loaders ----------------
+    // The raw inputs of chunk c + 1 are loaded in eight parts spread over
+    // the phases of chunk c (one burst of every CU's 64 KB would saturate the
+    // memory system and stall the issuing waves); while the scanners advance
+    // the state through chunk c the loaders turn them into P1 registers.
+    Raw<IT> raw;
+    P1Out po;
+    if (c_begin < c_end) {
+      const ChunkGeo g0 = chunk_geo(sr, c_begin - cs);
+      load_raw<IT, MODE>(raw, a, g0, h, col0, vcg, tid);
+      p1_math<IT, MODE>(po, raw, g0, vcg, tid);
+    }
+    for (int64_t c = c_begin; c < c_end; ++c) {
+      const ChunkGeo geo = chunk_geo(sr, c - cs);
+      const int tid_c = opaque(tid);
+      p1_write<MODE, true>(sm, po, vcg, tid_c);
+      const NextLoads<IT, MODE> nl{&raw, &a, chunk_geo(sr, c + 1 - cs), h, col0, vcg, tid_c, c + 1 < c_end};
+      prepare_mid<IT, MODE, true>(sm, a, geo, h, vcg, tid_c, nl);
+      prepare_m<IT, MODE, true>(sm, tid_c, nl);
+      if (c + 1 < c_end) p1_math<IT, MODE>(po, raw, chunk_geo(sr, c + 1 - cs), vcg, tid_c);
+      __syncthreads();
+    }
+  }
+
+  // ---- end of the segment ----------------------------------------------------
+  if constexpr (MODE == kOutput) {
+    if (w < 4 && lg == nseg - 1 && a.s_out != nullptr) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        const int tile = 2 * w + t;
+        if (tile >= nvt) continue;
+#pragma unroll
+        for (int ct = 0; ct < 8; ++ct) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t row = 16 * ct + 4 * g4 + r;
+            a.s_out[sbase + row * a.V + col0 + 16 * tile + n16] = S[0][t][ct][r];
+          }
+        }
+      }
+    }
+  } else {
+    // value tiles: the start state of the next segment (first segment) or Q_g
+    float* dst = (lg == 0) ? a.seg_state + ((gsg + 1) * a.H + h) * seg_state_floats(a.V)
+                           : a.seg_q + (gsg * a.H + h) * seg_state_floats(a.V);
+    bf16(*Pn)[kRow] = lds<bf16[kRow]>(sm, kOffPnat);
+    if (w < 4) {
+#pragma unroll
+      for (int pp = 0; pp < kPairs; ++pp) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int tile = 2 * w + 8 * pp + t;
+          if (tile < nvt) {
+#pragma unroll
+            for (int ct = 0; ct < 8; ++ct)
+              *reinterpret_cast<f32x4_t*>(dst + ((col0 / 16 + tile) * 8 + ct) * 256 + lane * 4) = S[pp][t][ct];
+          } else if (tile < ntiles) {
+            // transition tile -> natural bf16 [i][j] in LDS
+            const int j = 16 * (tile - nvt) + n16;
+#pragma unroll
+            for (int ct = 0; ct < 8; ++ct)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) Pn[16 * ct + 4 * g4 + r][j] = (bf16)S[pp][t][ct][r];
+          }
+        }
+      }
+    }
+    if (track_p) {
+      // natural P_g in LDS -> A fragments in the workspace
+      __syncthreads();
+      bf16* pdst = a.seg_p + (gsg * a.H + h) * seg_p_elems();
+      for (int f = tid; f < 8 * 4 * 64; f += kThreads) {
+        const int I = f >> 8, st = (f >> 6) & 3, fl = f & 63;
+        const int i = 16 * I + (fl & 15), gq = fl >> 4;
+        const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&Pn[i][32 * st + 4 * gq]);
+        const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&Pn[i][32 * st + 16 + 4 * gq]);
+        *reinterpret_cast<bf16x8_t*>(pdst + static_cast<int64_t>(f) * 8) =
+            bf16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    }
+  }
+}
+
+// ---- phase B: S_{g+1} = P_g S_g + Q_g along each sequence ---------------------
+// One workgroup of 8 waves per (sequence, head, 16-column tile); wave ct owns
+// output row tile ct.  The state moves between waves as bf16 B-operand
+// halves through LDS (double-buffered, one barrier per segment); P_g and
+// Q_g of the next kCombineDepth segments are in flight in registers.
+constexpr int kCombineDepth = 4;
+
+struct CombineArgs {
+  const int32_t* seg_start;
+  float* seg_state;
+  const float* seg_q;
+  const bf16* seg_p;
+  int64_t N, H, V;
+};
+
+__global__ __launch_bounds__(512) void segment_combine_kernel(const CombineArgs a) {
+  __shared__ __align__(16) bf16x4_t Sh[2][8][64];
+  const int64_t s = blockIdx.x;
+  const int64_t h = blockIdx.y;
+  const int64_t tile = blockIdx.z;
+  const int64_t g0 = a.seg_start[s];
+  const int64_t nseg = a.seg_start[s + 1] - g0;
+  if (nseg <= 2) return;  // phase A already produced every start state
+  const int64_t last = nseg - 2;  // steps lg = 1..last produce the start state of segment lg + 1
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int ct = wave_of(tid);
+  const int64_t tstride = seg_state_floats(a.V);
+  auto state_ptr = [&](float* base, int64_t seg) { return base + (seg * a.H + h) * tstride + (tile * 8 + ct) * 256 + lane * 4; };
+  auto p_ptr = [&](int64_t seg, int st) {
+    return a.seg_p + (seg * a.H + h) * seg_p_elems() + ((ct * 4 + st) * 64 + lane) * 8;
+  };
+
+  bf16x8_t Pf[kCombineDepth][4];
+  f32x4_t Qv[kCombineDepth];
+#pragma unroll
+  for (int d = 0; d < kCombineDepth; ++d) {
+    const int64_t lg = 1 + d;
+    if (lg <= last) {
+#pragma unroll
+      for (int st = 0; st < 4; ++st) Pf[d][st] = *reinterpret_cast<const bf16x8_t*>(p_ptr(g0 + lg, st));
+      Qv[d] = *reinterpret_cast<const f32x4_t*>(state_ptr(const_cast<float*>(a.seg_q), g0 + lg));
+    }
+  }
+  {
+    const f32x4_t x = *reinterpret_cast<const f32x4_t*>(state_ptr(a.seg_state, g0 + 1));
+    Sh[0][ct][lane] = bf16x4_t{(bf16)x[0], (bf16)x[1], (bf16)x[2], (bf16)x[3]};
+  }
+  __syncthreads();
+  for (int64_t lg0 = 1; lg0 <= last; lg0 += kCombineDepth) {
+#pragma unroll
+    for (int d = 0; d < kCombineDepth; ++d) {
+      const int64_t lg = lg0 + d;
+      if (lg > last) break;
+      const int buf = static_cast<int>((lg - 1) & 1);
+      f32x4_t acc = Qv[d];
+#pragma unroll
+      for (int st = 0; st < 4; ++st) {
+        const bf16x4_t lo = Sh[buf][2 * st][lane];
+        const bf16x4_t hi = Sh[buf][2 * st + 1][lane];
+        const bf16x8_t sb = bf16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        acc = mfma32(Pf[d][st], sb, acc);
+      }
+      const int64_t nx = lg + kCombineDepth;
+      if (nx <= last) {
+#pragma unroll
+        for (int st = 0; st < 4; ++st) Pf[d][st] = *reinterpret_cast<const bf16x8_t*>(p_ptr(g0 + nx, st));
+        Qv[d] = *reinterpret_cast<const f32x4_t*>(state_ptr(const_cast<float*>(a.seg_q), g0 + nx));
+      }
+      *reinterpret_cast<f32x4_t*>(state_ptr(a.seg_state, g0 + lg + 1)) = acc;
+      Sh[buf ^ 1][ct][lane] = bf16x4_t{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
+      __syncthreads();
     }
   }
 }
 
 // ---- host side ------------------------------------------------------------
-static int64_t chunk_bound(int64_t N, int64_t total_tokens) { return total_tokens / kChunk + N + 1; }
-
 static bool mfma_path(int in_dtype, int state_dtype, int64_t K, int64_t V) {
   return (in_dtype == KDA_DTYPE_BF16 || in_dtype == KDA_DTYPE_F16) && state_dtype == KDA_DTYPE_F32 && K == kKey &&
          V % 16 == 0 && V >= 16 && V <= 256;
 }
 
-static size_t map_bytes(int64_t N) { return static_cast<size_t>(((N + 1) * 4 + 255) / 256 * 256); }
+static int device_cus() {
+  static int cus = 0;
+  if (cus == 0) {
+    int dev = 0, n = 0;
+    if (hipGetDevice(&dev) == hipSuccess &&
+        hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) == hipSuccess && n > 0)
+      cus = n;
+    else
+      cus = 256;
+  }
+  return cus;
+}
+
+// How a prefill is cut into segments: L chunks per segment, or one segment
+// per sequence when (sequences x heads x column groups) alone fill the GPU.
+struct Plan {
+  int32_t L;
+  bool segmented;
+  int64_t ncg;
+  int64_t segs_bound;  // upper bound on the total number of segments
+};
+
+// KDA_MI355X_SEGMENT_CHUNKS=<L> (L >= 1) forces L chunks per segment; 0 forces
+// one segment per sequence.  The result does not depend on it (tests use it
+// to cover both schedules at small sizes).
+static int64_t segment_override() {
+  const char* env = getenv("KDA_MI355X_SEGMENT_CHUNKS");
+  if (env == nullptr || *env == '\0') return -1;
+  const long v = strtol(env, nullptr, 10);
+  return v < 0 ? -1 : v;
+}
+
+static Plan make_plan(int64_t N, int64_t total_tokens, int64_t H, int64_t V) {
+  Plan p;
+  p.ncg = (V + kColGroup - 1) / kColGroup;
+  const int64_t cus = device_cus();
+  const int64_t chunks_bound = total_tokens / kChunk + N;
+  const int64_t work = (total_tokens / kChunk) * H * p.ncg;  // chunk-workgroups of one pass
+  const int64_t forced = segment_override();
+  if (forced > 0) {
+    p.L = static_cast<int32_t>(forced < kOneSegment ? forced : kOneSegment - 1);
+    p.segmented = true;
+    p.segs_bound = chunks_bound / p.L + N + 1;
+    return p;
+  }
+  if (forced == 0 || N * H * p.ncg * 4 >= cus * 3 || work < 2 * cus) {
+    p.L = kOneSegment;
+    p.segmented = false;
+    p.segs_bound = N;
+  } else {
+    int64_t L = (work + cus - 1) / cus;
+    if (L < 2) L = 2;
+    p.L = static_cast<int32_t>(L);
+    p.segmented = true;
+    p.segs_bound = chunks_bound / L + N + 1;
+  }
+  return p;
+}
+
+static size_t map_bytes(int64_t N) { return static_cast<size_t>(((2 * (N + 1)) * 4 + 255) / 256 * 256); }
+
+static size_t segment_bytes(const Plan& p, int64_t H, int64_t V) {
+  if (!p.segmented) return 0;
+  const size_t st = static_cast<size_t>(p.segs_bound * H * seg_state_floats(V)) * 4;
+  const size_t pp = static_cast<size_t>(p.segs_bound * H * seg_p_elems()) * 2;
+  return 2 * st + pp;
+}
 
 static void mark(kda_host::KernelEvents* ev, int i, hipStream_t stream) {
   if (ev != nullptr) {
@@ -843,61 +1283,74 @@ static void mark(kda_host::KernelEvents* ev, int i, hipStream_t stream) {
   }
 }
 
-template <class IT>
-static int run_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, const void* s_in,
-                     void* s_out, void* out, const SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
-                     int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev) {
-  int32_t* chunk_start = static_cast<int32_t*>(workspace);
-  unsigned char* records = static_cast<unsigned char*>(workspace) + map_bytes(N);
-  mark(ev, 0, stream);
-  hipLaunchKernelGGL(chunk_map_kernel, dim3(1), dim3(1024), 0, stream, seq, N, chunk_start);
-  int st = kda_host::check_launch("chunk_map_kernel");
-  if (st != KDA_OK) return st;
-  mark(ev, 1, stream);
-
+template <class IT, int MODE>
+static int launch_segments(const SegArgs<IT>& sa, const Plan& p, int64_t H, hipStream_t stream) {
   static bool attr_done = false;
-  const size_t smem = sizeof(PrepSmem);
   if (!attr_done) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_prepare_kernel<IT>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, static_cast<int>(smem)) != hipSuccess) {
-      kda_host::set_detail("cannot reserve %zu bytes of LDS for chunk_prepare_kernel", smem);
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_segment_kernel<IT, MODE>),
+                            hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes) != hipSuccess) {
+      kda_host::set_detail("cannot reserve %d bytes of LDS for chunk_segment_kernel", kSmemBytes);
       return KDA_ERR_LAUNCH;
     }
     attr_done = true;
   }
-  PrepArgs<IT> pa;
-  pa.q = static_cast<const IT*>(q);
-  pa.k = static_cast<const IT*>(k);
-  pa.v = static_cast<const IT*>(v);
-  pa.g = static_cast<const IT*>(g);
-  pa.beta = static_cast<const IT*>(beta);
-  pa.seq = seq;
-  pa.chunk_start = chunk_start;
-  pa.records = records;
-  pa.N = N;
-  pa.H = H;
-  pa.V = V;
-  const int64_t nchunks = chunk_bound(N, total_tokens);
-  hipLaunchKernelGGL(chunk_prepare_kernel<IT>, dim3(static_cast<unsigned>(nchunks), static_cast<unsigned>(H)),
-                     dim3(kPrepThreads), smem, stream, pa);
-  st = kda_host::check_launch("chunk_prepare_kernel");
-  if (st != KDA_OK) return st;
-  mark(ev, 2, stream);
+  hipLaunchKernelGGL((chunk_segment_kernel<IT, MODE>), dim3(static_cast<unsigned>(p.segs_bound * H * p.ncg)),
+                     dim3(kThreads), kSmemBytes, stream, sa);
+  return kda_host::check_launch(MODE == kSummary ? "chunk_segment_kernel<summary>" : "chunk_segment_kernel<output>");
+}
 
-  ScanArgs<IT> sa;
+template <class IT>
+static int run_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, const void* s_in,
+                     void* s_out, void* out, const SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
+                     int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev) {
+  const Plan p = make_plan(N, total_tokens, H, V);
+  int32_t* chunk_start = static_cast<int32_t*>(workspace);
+  int32_t* seg_start = chunk_start + (N + 1);
+  unsigned char* segbuf = static_cast<unsigned char*>(workspace) + map_bytes(N);
+  const size_t st_bytes = p.segmented ? static_cast<size_t>(p.segs_bound * H * seg_state_floats(V)) * 4 : 0;
+
+  SegArgs<IT> sa;
+  sa.q = static_cast<const IT*>(q);
+  sa.k = static_cast<const IT*>(k);
+  sa.v = static_cast<const IT*>(v);
+  sa.g = static_cast<const IT*>(g);
+  sa.beta = static_cast<const IT*>(beta);
   sa.out = static_cast<IT*>(out);
   sa.s_in = static_cast<const float*>(s_in);
   sa.s_out = static_cast<float*>(s_out);
   sa.seq = seq;
   sa.chunk_start = chunk_start;
-  sa.records = records;
+  sa.seg_start = seg_start;
+  sa.seg_state = p.segmented ? reinterpret_cast<float*>(segbuf) : nullptr;
+  sa.seg_q = p.segmented ? reinterpret_cast<float*>(segbuf + st_bytes) : nullptr;
+  sa.seg_p = p.segmented ? reinterpret_cast<bf16*>(segbuf + 2 * st_bytes) : nullptr;
   sa.N = N;
   sa.H = H;
   sa.V = V;
-  const int64_t blocks = N * H * ((V / 16 + kScanComputeWaves - 1) / kScanComputeWaves);
-  hipLaunchKernelGGL(chunk_scan_kernel<IT>, dim3(static_cast<unsigned>(blocks)), dim3(kScanThreads), 0, stream, sa);
-  st = kda_host::check_launch("chunk_scan_kernel");
-  mark(ev, 3, stream);
+  sa.L = p.L;
+
+  mark(ev, 0, stream);
+  hipLaunchKernelGGL(chunk_map_kernel, dim3(1), dim3(1024), 0, stream, seq, N, p.L, chunk_start, seg_start);
+  int st = kda_host::check_launch("chunk_map_kernel");
+  if (st != KDA_OK) return st;
+  mark(ev, 1, stream);
+  if (p.segmented) {
+    st = launch_segments<IT, kSummary>(sa, p, H, stream);
+    if (st != KDA_OK) return st;
+    mark(ev, 2, stream);
+    CombineArgs ca{seg_start, sa.seg_state, sa.seg_q, sa.seg_p, N, H, V};
+    hipLaunchKernelGGL(segment_combine_kernel, dim3(static_cast<unsigned>(N), static_cast<unsigned>(H),
+                                                    static_cast<unsigned>(V / 16)),
+                       dim3(512), 0, stream, ca);
+    st = kda_host::check_launch("segment_combine_kernel");
+    if (st != KDA_OK) return st;
+    mark(ev, 3, stream);
+  } else {
+    mark(ev, 2, stream);
+    mark(ev, 3, stream);
+  }
+  st = launch_segments<IT, kOutput>(sa, p, H, stream);
+  mark(ev, 4, stream);
   return st;
 }
 
@@ -909,8 +1362,8 @@ size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t hea
                              int64_t value_dim, int in_dtype) {
   if (!kda::mfma_path(in_dtype, in_dtype == KDA_DTYPE_F64 ? KDA_DTYPE_F64 : KDA_DTYPE_F32, key_dim, value_dim))
     return 0;
-  return kda::map_bytes(num_seqs) +
-         static_cast<size_t>(kda::chunk_bound(num_seqs, total_tokens) * heads * kda::rec_bytes(value_dim));
+  const kda::Plan p = kda::make_plan(num_seqs, total_tokens, heads, value_dim);
+  return kda::map_bytes(num_seqs) + kda::segment_bytes(p, heads, value_dim);
 }
 
 int launch_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
@@ -929,8 +1382,9 @@ int launch_chunk(const void* q, const void* k, const void* v, const void* g, con
     set_detail("chunk_fwd: workspace too small");
     return KDA_ERR_WORKSPACE;
   }
-  if (H > 65535 || chunk_bound(N, total_tokens) > 0x7fffffffLL || N * H * (V / 16) > 0x7fffffffLL) {
-    set_detail("chunk_fwd: grid too large (H=%lld)", (long long)H);
+  const Plan p = make_plan(N, total_tokens, H, V);
+  if (H > 65535 || p.segs_bound * H * p.ncg > 0x7fffffffLL || N > 0x7fffffffLL) {
+    set_detail("chunk_fwd: grid too large (N=%lld, H=%lld)", (long long)N, (long long)H);
     return KDA_ERR_UNSUPPORTED;
   }
   if (in_dtype == KDA_DTYPE_BF16)

@@ -21,7 +21,7 @@ size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t hea
 // Optional per-kernel timing: events[i] is recorded before kernel i and
 // events[n] after the last one; *n_launched receives n.
 struct KernelEvents {
-  hipEvent_t ev[4];
+  hipEvent_t ev[5];
   int n_launched;
 };
 

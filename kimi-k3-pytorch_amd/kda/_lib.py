@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libkda_mi355x.so")
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 KDA_OK = 0
 KDA_ERR_INVALID_ARGUMENT = 1

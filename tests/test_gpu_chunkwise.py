@@ -187,3 +187,63 @@ def test_long_context_full_length_single_head():
         es = rel_err(got.final_state[:, sl], rs)
         print(f"T=8192 head {h}: output rel err {eo:.2e} state rel err {es:.2e}")
         assert eo < TOL16 and es < TOL16
+
+
+# ---------------------------------------------------------------------------
+# Segmented schedule: the chunk chain is cut into segments whose affine state
+# maps are composed (KDA_MI355X_SEGMENT_CHUNKS forces the segment length; the
+# default plan only segments when batch * heads is small).  The result must
+# match the oracle whatever the segment length.
+
+@pytest.mark.parametrize("chunks_per_segment", ["1", "2", "3"])
+def test_chunkwise_segmented_matches_oracle(monkeypatch, chunks_per_segment):
+    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", chunks_per_segment)
+    q, k, v, g, beta, state = workload(2, 64 * 10 + 17, 2, 128, 128, state_std=0.02, seed=31)
+    ro, rs = _oracle_f32(q, k, v, g, beta, state)
+    got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True)
+    _check(got, ro, rs, label=f"segments of {chunks_per_segment} chunks")
+
+
+@pytest.mark.parametrize("value_dim", [64, 256])
+def test_chunkwise_segmented_value_widths(monkeypatch, value_dim):
+    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "2")
+    q, k, v, g, beta, state = workload(1, 64 * 7 + 5, 2, 128, value_dim, state_std=0.02, seed=32)
+    ro, rs = _oracle_f32(q, k, v, g, beta, state)
+    got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True)
+    _check(got, ro, rs, label=f"segmented V={value_dim}")
+
+
+def test_chunkwise_segmented_varlen_and_slow_decay(monkeypatch):
+    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "2")
+    q, k, v, g, beta, _ = workload(1, 600, 2, 128, 128, g_shift=-2.0, seed=33)
+    cu = [0, 100, 164, 165, 600]
+    init = torch.randn(4, 2, 128, 128, generator=torch.Generator().manual_seed(34)) * 0.02
+    ro, rs = ora.varlen_chunkwise(*(t.float() for t in (q, k, v, g, beta)), cu, init,
+                                  chunk_size=64, secondary_tile_size=16)
+    got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, init), True,
+                            cu_seqlens=torch.tensor(cu, dtype=torch.int32, device=DEV))
+    _check(got, ro, rs, label="segmented varlen, slow decay")
+
+
+def test_chunkwise_segmented_mask_and_zero_decay(monkeypatch):
+    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "1")
+    q, k, v, _, beta, state = workload(2, 300, 2, 128, 128, state_std=0.02, seed=35)
+    g = torch.zeros_like(q)
+    mask = torch.arange(300)[None, :] < torch.tensor([300, 130])[:, None]
+    ro, rs = _oracle_f32(q, k, v, g, beta, state, mask)
+    got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True, mask.to(DEV))
+    _check(got, ro, rs, label="segmented mask, g=0")
+    assert torch.count_nonzero(got.hidden_states[1, 130:]) == 0
+
+
+def test_chunkwise_segmented_equals_single_segment(monkeypatch):
+    q, k, v, g, beta, state = workload(1, 64 * 12, 3, 128, 128, state_std=0.02, seed=36)
+    d = _dev(q, k, v, g, beta, state)
+    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "0")
+    one = kda.chunkwise_kda(*d, True)
+    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "4")
+    seg = kda.chunkwise_kda(*d, True)
+    assert rel_err(seg.hidden_states, one.hidden_states.float()) < 1e-2
+    assert rel_err(seg.final_state, one.final_state) < 1e-2
+    # the first segment of a sequence runs the same arithmetic as the unsegmented kernel
+    assert torch.equal(seg.hidden_states[:, :256], one.hidden_states[:, :256])
