@@ -212,12 +212,52 @@ def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
     }
 
 
+TRAFFIC_FILE = REPO / "profiles" / "hbm_traffic.json"
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
+    runs of `--profile-pass` (calibrated against a device copy of known size), if
+    they have been recorded; None otherwise."""
+    try:
+        data = json.loads(TRAFFIC_FILE.read_text())
+        entry = data["kernels"][kernel]
+        return int(entry["read_bytes"] + entry["write_bytes"])
+    except (OSError, KeyError, ValueError, TypeError):
+        return None
+
+
+def profile_pass():
+    """The workload of the counter runs: after one warm-up round, one prefill at
+    the benchmark shape, one in-place decode step at the benchmark shape, and a
+    256 MiB device-to-device copy whose byte counts calibrate the counters."""
+    import torch
+
+    import kda
+
+    device = torch.device("cuda", 0)
+    q, k, v, g, beta, s0 = _inputs(P_B, P_T, P_H, P_K, P_V, 0.02, 0, device)
+    qd, kd, vd, gd, bd, _ = _inputs(D_B, 1, D_H, D_K, D_V, None, 2, device)
+    state = torch.randn(D_B, D_H, D_K, D_V, generator=torch.Generator().manual_seed(1)).mul_(0.02).to(device)
+    src = torch.rand(256 * 2**20 // 4, generator=torch.Generator().manual_seed(3)).to(device)
+    dst = torch.empty_like(src)
+    with torch.no_grad():
+        for _ in range(2):
+            kda.chunkwise_kda(q, k, v, g, beta, s0, True)
+            kda.recurrent_kda(qd, kd, vd, gd, bd, state, True, update_state_in_place=True)
+            dst.copy_(src)
+    torch.cuda.synchronize()
+    print("profile pass done", flush=True)
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-pass", action="store_true",
+                    help="run the counter-collection workload only (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the KDA operator has no collective; --gpus {args.gpus} "
@@ -229,6 +269,9 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
+    if args.profile_pass:
+        profile_pass()
+        return 0
 
     ms, per_kernel, ws_bytes = bench_prefill(args.steps, args.warmup)
     dec_ms = bench_decode(args.warmup)
@@ -269,7 +312,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(dom_bytes / (dom_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": None,
+            "traffic": measured_traffic(dom),
             "algorithmic_bytes": dom_bytes,
             "kernel_ms": round(dom_ms, 5),
         },
@@ -290,7 +333,7 @@ def main() -> int:
             "ms_per_step": round(dec_ms, 5),
             "roofline": {
                 "bound": "hbm", "kernel": "recurrent_kernel", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("recurrent_kernel"),
                 "algorithmic_bytes": dbytes,
             },
         },

@@ -220,14 +220,32 @@ struct SegArgs {
   const float* s_in;
   float* s_out;
   SeqDesc seq;
-  const int32_t* __restrict__ chunk_start;
-  const int32_t* __restrict__ seg_start;
+  const int32_t* __restrict__ chunk_start;  // [N+1], or nullptr for dense sequences (closed form)
+  const int32_t* __restrict__ seg_start;    // [N+1], or nullptr for dense sequences (closed form)
+  int64_t dense_chunks;                     // dense: chunks per sequence
+  int64_t dense_segs;                       // dense: segments per sequence
   float* seg_state;
   float* seg_q;
   bf16* seg_p;
   int64_t N, H, V;
   int32_t L;
 };
+
+// Chunk and segment maps: the arrays of chunk_map_kernel for packed
+// documents, a closed form for dense sequences (every sequence has the same
+// number of chunks and segments).
+template <class A>
+__device__ __forceinline__ int64_t chunk_start_of(const A& a, int64_t s) {
+  return a.chunk_start ? a.chunk_start[s] : s * a.dense_chunks;
+}
+template <class A>
+__device__ __forceinline__ int64_t seg_start_of(const A& a, int64_t s) {
+  return a.seg_start ? a.seg_start[s] : s * a.dense_segs;
+}
+template <class A>
+__device__ __forceinline__ int64_t seq_of_segment(const A& a, int64_t gsg) {
+  return a.seg_start ? find_seq(a.seg_start, a.N, gsg) : gsg / a.dense_segs;
+}
 
 struct ChunkGeo {
   int64_t tok0;
@@ -957,15 +975,15 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
   const int64_t gsg = blockIdx.x / (a.H * ncg);
   const int64_t h = (blockIdx.x / ncg) % a.H;
   const int64_t cgi = blockIdx.x % ncg;
-  if (gsg >= a.seg_start[a.N]) return;  // uniform
-  const int64_t s = find_seq(a.seg_start, a.N, gsg);
-  const int64_t lg = gsg - a.seg_start[s];
-  const int64_t nseg = a.seg_start[s + 1] - a.seg_start[s];
+  if (gsg >= seg_start_of(a, a.N)) return;  // uniform
+  const int64_t s = seq_of_segment(a, gsg);
+  const int64_t lg = gsg - seg_start_of(a, s);
+  const int64_t nseg = seg_start_of(a, s + 1) - seg_start_of(a, s);
   if (MODE == kSummary && lg == nseg - 1) return;  // the last segment needs no summary
   const SeqRange sr = seq_range(a.seq, s);
-  const int64_t cs = a.chunk_start[s];
+  const int64_t cs = chunk_start_of(a, s);
   const int64_t c_begin = cs + lg * a.L;
-  const int64_t c_end_seq = a.chunk_start[s + 1];
+  const int64_t c_end_seq = chunk_start_of(a, s + 1);
   const int64_t c_end = (c_begin + a.L < c_end_seq) ? c_begin + a.L : c_end_seq;
 
   const int tid = threadIdx.x;
@@ -1134,7 +1152,8 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
 constexpr int kCombineDepth = 4;
 
 struct CombineArgs {
-  const int32_t* seg_start;
+  const int32_t* seg_start;  // [N+1], or nullptr for dense sequences
+  int64_t dense_segs;
   float* seg_state;
   const float* seg_q;
   const bf16* seg_p;
@@ -1146,8 +1165,8 @@ __global__ __launch_bounds__(512) void segment_combine_kernel(const CombineArgs 
   const int64_t s = blockIdx.x;
   const int64_t h = blockIdx.y;
   const int64_t tile = blockIdx.z;
-  const int64_t g0 = a.seg_start[s];
-  const int64_t nseg = a.seg_start[s + 1] - g0;
+  const int64_t g0 = seg_start_of(a, s);
+  const int64_t nseg = seg_start_of(a, s + 1) - g0;
   if (nseg <= 2) return;  // phase A already produced every start state
   const int64_t last = nseg - 2;  // steps lg = 1..last produce the start state of segment lg + 1
   const int tid = threadIdx.x;
@@ -1319,8 +1338,14 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
   sa.s_in = static_cast<const float*>(s_in);
   sa.s_out = static_cast<float*>(s_out);
   sa.seq = seq;
-  sa.chunk_start = chunk_start;
-  sa.seg_start = seg_start;
+  const bool dense = seq.cu_seqlens == nullptr;
+  sa.chunk_start = dense ? nullptr : chunk_start;
+  sa.seg_start = dense ? nullptr : seg_start;
+  sa.dense_chunks = dense ? (seq.dense_span + kChunk - 1) / kChunk : 0;
+  {
+    const int64_t nseg = dense ? (sa.dense_chunks + p.L - 1) / p.L : 0;
+    sa.dense_segs = nseg > 1 ? nseg : 1;
+  }
   sa.seg_state = p.segmented ? reinterpret_cast<float*>(segbuf) : nullptr;
   sa.seg_q = p.segmented ? reinterpret_cast<float*>(segbuf + st_bytes) : nullptr;
   sa.seg_p = p.segmented ? reinterpret_cast<bf16*>(segbuf + 2 * st_bytes) : nullptr;
@@ -1330,15 +1355,18 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
   sa.L = p.L;
 
   mark(ev, 0, stream);
-  hipLaunchKernelGGL(chunk_map_kernel, dim3(1), dim3(1024), 0, stream, seq, N, p.L, chunk_start, seg_start);
-  int st = kda_host::check_launch("chunk_map_kernel");
-  if (st != KDA_OK) return st;
+  int st = KDA_OK;
+  if (!dense) {
+    hipLaunchKernelGGL(chunk_map_kernel, dim3(1), dim3(1024), 0, stream, seq, N, p.L, chunk_start, seg_start);
+    st = kda_host::check_launch("chunk_map_kernel");
+    if (st != KDA_OK) return st;
+  }
   mark(ev, 1, stream);
   if (p.segmented) {
     st = launch_segments<IT, kSummary>(sa, p, H, stream);
     if (st != KDA_OK) return st;
     mark(ev, 2, stream);
-    CombineArgs ca{seg_start, sa.seg_state, sa.seg_q, sa.seg_p, N, H, V};
+    CombineArgs ca{sa.seg_start, sa.dense_segs, sa.seg_state, sa.seg_q, sa.seg_p, N, H, V};
     hipLaunchKernelGGL(segment_combine_kernel, dim3(static_cast<unsigned>(N), static_cast<unsigned>(H),
                                                     static_cast<unsigned>(V / 16)),
                        dim3(512), 0, stream, ca);
