@@ -74,9 +74,11 @@ constexpr int kSummary = 0;  // phase A
 constexpr int kOutput = 1;   // phase C
 
 // ---- LDS map of chunk_segment_kernel (bytes) ------------------------------
-// Natural bf16 tiles use a padded row of 136 elements.
+// Natural bf16 tiles use a padded row of 136 elements; the k a, q a and k E
+// tiles also shift each 16-row block by 64 bytes, so that the four rows a
+// loader wave writes at once (one per block) fall in different LDS banks.
 constexpr int kRow = 136;
-constexpr int kNat = kChunk * kRow * 2;     // 17408
+constexpr int kNat = kChunk * kRow * 2 + 3 * 64;  // 17600
 constexpr int kOffKA = 0;                   // bf16 [64][136] k_j a_j
 constexpr int kOffQA = kOffKA + kNat;       // bf16 [64][136] q_j a_j    -> Kgamma fragments after P2
 constexpr int kOffKE = kOffQA + kNat;       // bf16 [64][136] k_j E_j    -> M fragments after P2
@@ -84,8 +86,8 @@ constexpr int kOffL = kOffKE + kNat;        // bf16 [64][72] beta_i A_ij, strict
 constexpr int kOffLd = kOffL + kChunk * 72 * 2;  // f32 [4][16][16] diagonal blocks of L
 constexpr int kOffTinv = kOffLd + 4 * 256 * 4;   // bf16 [4][16][16] T_I = inverses of those blocks
 constexpr int kOffTinvT = kOffTinv + 4 * 256 * 2;  // bf16 [4][16][16] T_I transposed
-constexpr int kOffTab = kOffTinvT + 4 * 256 * 2;   // f32 G/A0/P [3][4][128], then pair scales [10][128]
-constexpr int kOffGs = kOffTab + 3 * 4 * kKey * 4;  // f32 [4][128] exp(lg_{16J})
+constexpr int kOffTab = kOffTinvT + 4 * 256 * 2;   // f32 pair scales [10][128]
+constexpr int kOffGs = kOffTab + 10 * kKey * 4;     // f32 [4][128] exp(lg_{16J})
 constexpr int kOffGe = kOffGs + 4 * kKey * 4;       // f32 [4][128] exp(lg_63 - lg_{16J+15})
 constexpr int kOffBeta = kOffGe + 4 * kKey * 4;     // f32 [64]
 constexpr int kOffVn = kOffBeta + 256;              // bf16 [64][136] v of the column group
@@ -93,13 +95,16 @@ constexpr int kOffQf = kOffVn + kNat;               // Q~ A fragments  [I=4][s=4
 constexpr int kOffKTf = kOffQf + 16384;             // K~^T A fragments [ct=8][s=2][lane][8]
 constexpr int kOffAf = kOffKTf + 16384;             // Aqk A fragments [I=4][s=2][lane][8]
 constexpr int kOffGam = kOffAf + 8192;              // f32 [128] exp(lg_63)
-constexpr int kOffFlag = kOffGam + 512;             // int [4] extreme-decay flags of P1b's waves
-constexpr int kSmemBytes = kOffFlag + 16;
+constexpr int kOffFlag = kOffGam + 512;             // int [4] extreme-decay flags of the loader waves
+constexpr int kRowT = 72;                           // padded row of the channel-major tile
+constexpr int kOffKEt = kOffFlag + 16;              // bf16 [128][72] k_j E_j, channel-major
+constexpr int kSmemBytes = kOffKEt + kKey * kRowT * 2;
 constexpr int kOffKgf = kOffQA;    // -Kgamma = -exp(lg) k A fragments [I=4][s=4][lane][8] bf16
 constexpr int kOffMf = kOffKE;     // M = (I + diag(beta) A)^-1 diag(beta) A fragments [I=4][s=2][lane][8]
 constexpr int kOffStage = kOffKA;  // output transpose [4 waves][64][32]
 constexpr int kOffPnat = kOffKA;   // phase A: P_g natural bf16 [128][136]
 static_assert(kSmemBytes <= 160 * 1024, "chunk_segment_kernel LDS exceeds one CU");
+static_assert(kOffKEt % 16 == 0 && kOffGs % 16 == 0 && kOffGe % 16 == 0, "16-byte LDS accesses need aligned tiles");
 static_assert(4 * 64 * 32 * 2 <= kNat, "output stage must fit in the k a tile");
 static_assert(kKey * kRow * 2 <= 2 * kNat, "P transpose must fit in the k a and q a tiles");
 static_assert(16384 <= kNat && 8192 <= kNat, "Kgamma and M fragments must fit in the q a and k E tiles");
@@ -138,6 +143,10 @@ __device__ __forceinline__ int wave_of(int tid) { return __builtin_amdgcn_readfi
 template <class T>
 __device__ __forceinline__ T* lds(unsigned char* base, int off) {
   return reinterpret_cast<T*>(base + off);
+}
+// Row `row` of a block-shifted natural tile at byte offset `off`.
+__device__ __forceinline__ bf16* nat_row(unsigned char* sm, int off, int row) {
+  return reinterpret_cast<bf16*>(sm + off + row * (kRow * 2) + (row >> 4) * 64);
 }
 
 // ---- chunk and segment maps -------------------------------------------------
@@ -264,9 +273,14 @@ __device__ __forceinline__ ChunkGeo chunk_geo(const SeqRange& sr, int64_t lc) {
 }
 
 // Raw inputs of one chunk, held in the registers of the four loader waves
-// (4-7) between chunks: loader thread (block J = wave - 4, channel pair
-// cp = lane) holds g, k (and q) of its 16 rows, and the 256 loader threads
-// together hold the chunk's v slice of this column group and beta.
+// (4-7) between chunks: loader thread (block J = lane / 16, channel pair
+// cp = 16 (wave - 4) + lane % 16) holds g, k (and q) of the 16 rows of block
+// J, so the four blocks of a channel pair sit in lanes l, l + 16, l + 32,
+// l + 48 of one wave; the 256 loader threads together hold the chunk's v
+// slice of this column group and beta.
+__device__ __forceinline__ int loader_block(int tid) { return (tid & 63) >> 4; }
+__device__ __forceinline__ int loader_pair(int tid) { return 16 * (wave_of(tid) - 4) + (tid & 15); }
+
 template <class IT>
 struct Raw {
   typedef IT pair_t __attribute__((ext_vector_type(2)));
@@ -275,69 +289,114 @@ struct Raw {
   IT bt;
 };
 
+// Raw buffer resource over `bytes` bytes from `base` (dword 3 is the gfx9
+// family's untyped 32-bit data format).  The hardware checks each lane's
+// offset against `bytes`: a load past it returns zero.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, int64_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes), 0x00020000);
+}
+
+// One chunk's raw inputs as buffer resources over this head's rows of the
+// chunk's valid tokens (rows past them read as zero), built once per chunk in
+// scalar registers; every load then needs only a lane offset.
+struct ChunkLoads {
+  __amdgpu_buffer_rsrc_t g, k, q, v, beta;
+  int krow;  // bytes per token of q, k, g
+};
+
+template <class IT>
+__device__ __forceinline__ ChunkLoads chunk_loads(const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h, int64_t col0) {
+  constexpr int64_t kEl = sizeof(IT);
+  ChunkLoads cl;
+  cl.krow = static_cast<int>(a.H * kKey * kEl);
+  const int64_t kb = (cg.tok0 * a.H + h) * kKey * kEl;
+  const int64_t kbytes = static_cast<int64_t>(cg.n_valid) * cl.krow;
+  cl.g = buffer_rsrc(reinterpret_cast<const char*>(a.g) + kb, kbytes);
+  cl.k = buffer_rsrc(reinterpret_cast<const char*>(a.k) + kb, kbytes);
+  cl.q = buffer_rsrc(reinterpret_cast<const char*>(a.q) + kb, kbytes);
+  cl.v = buffer_rsrc(reinterpret_cast<const char*>(a.v) + ((cg.tok0 * a.H + h) * a.V + col0) * kEl,
+                     static_cast<int64_t>(cg.n_valid) * a.H * a.V * kEl);
+  cl.beta = buffer_rsrc(reinterpret_cast<const char*>(a.beta) + (cg.tok0 * a.H + h) * kEl,
+                        static_cast<int64_t>(cg.n_valid) * a.H * kEl);
+  return cl;
+}
+
+// Lane offsets of a loader thread's v units in the chunk (-1: no unit) and
+// in the LDS tile, and of beta, fixed for the whole segment.
+struct LoaderLanes {
+  int v[4];
+  int vlds[4];
+  int beta;
+};
+
+template <class IT>
+__device__ __forceinline__ LoaderLanes loader_lanes(const SegArgs<IT>& a, int vcg, int tid) {
+  constexpr int kEl = sizeof(IT);
+  const int t2 = tid - 256;
+  const int upr = vcg / 8;  // 16-byte units per row
+  LoaderLanes ll;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int u = t2 + 256 * i;
+    const int row = u / upr;
+    ll.v[i] = row < kChunk ? row * static_cast<int>(a.H * a.V * kEl) + 16 * (u % upr) : -1;
+    ll.vlds[i] = row < kChunk ? (row * kRow + 8 * (u % upr)) * 2 : -1;
+  }
+  ll.beta = t2 < kChunk ? t2 * static_cast<int>(a.H * kEl) : -1;
+  return ll;
+}
+
 // Part PART (0..7) of the loads of one chunk's raw inputs: rows 2 PART and
 // 2 PART + 1 of g, k (and q) of this thread's block, one 16-byte v unit on
 // even parts and beta on the last.  Spreading the eight parts over a chunk's
 // phases keeps any single moment's burst of requests small: issued at once,
 // every CU's 64 KB would saturate HBM and stall the issuing waves.
 template <class IT, int MODE, int PART>
-__device__ __forceinline__ void load_raw_part(Raw<IT>& raw, const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h,
-                                              int64_t col0, int vcg, int tid) {
+__device__ __forceinline__ void load_raw_part(Raw<IT>& raw, const ChunkLoads& cl, const LoaderLanes& ll, int tid) {
   typedef typename Raw<IT>::pair_t pair_t;
-  const int t2 = tid - 256;  // loader thread index
-  const int J = wave_of(tid) - 4;
-  const int lane = tid & 63;
-  const int64_t krow = a.H * kKey;
-  // rows past the valid range read row tok0 instead and are zeroed when used
+  const int J = loader_block(tid);
+  const int cp = loader_pair(tid);
 #pragma unroll
   for (int r = 2 * PART; r < 2 * PART + 2; ++r) {
-    const int tl = 16 * J + r;
-    const int64_t off = (cg.tok0 + (tl < cg.n_valid ? tl : 0)) * krow + h * kKey + 2 * lane;
-    raw.gp[r] = *reinterpret_cast<const pair_t*>(a.g + off);
-    raw.kp[r] = *reinterpret_cast<const pair_t*>(a.k + off);
-    if constexpr (MODE == kOutput) raw.qp[r] = *reinterpret_cast<const pair_t*>(a.q + off);
+    const int off = (16 * J + r) * cl.krow + 4 * cp;
+    raw.gp[r] = __builtin_bit_cast(pair_t, __builtin_amdgcn_raw_buffer_load_b32(cl.g, off, 0, 0));
+    raw.kp[r] = __builtin_bit_cast(pair_t, __builtin_amdgcn_raw_buffer_load_b32(cl.k, off, 0, 0));
+    if constexpr (MODE == kOutput)
+      raw.qp[r] = __builtin_bit_cast(pair_t, __builtin_amdgcn_raw_buffer_load_b32(cl.q, off, 0, 0));
   }
   if constexpr ((PART & 1) == 0) {
     const int i = PART / 2;
-    const int upr = vcg / 8;  // 16-byte units per row
-    const int u = t2 + 256 * i;
-    const int row = u / upr;
-    if (row < kChunk) {
-      const int64_t off = (cg.tok0 + (row < cg.n_valid ? row : 0)) * (a.H * a.V) + h * a.V + col0 + 8 * (u % upr);
-      raw.vv[i] = *reinterpret_cast<const uint4*>(a.v + off);
-    }
+    if (ll.v[i] >= 0) raw.vv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(cl.v, ll.v[i], 0, 0));
   }
   if constexpr (PART == 7) {
-    if (t2 < kChunk) raw.bt = a.beta[(cg.tok0 + (t2 < cg.n_valid ? t2 : 0)) * a.H + h];
+    if (ll.beta >= 0) raw.bt = __builtin_bit_cast(IT, __builtin_amdgcn_raw_buffer_load_b16(cl.beta, ll.beta, 0, 0));
   }
 }
 
 template <class IT, int MODE>
-__device__ __forceinline__ void load_raw(Raw<IT>& raw, const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h,
-                                         int64_t col0, int vcg, int tid) {
-  load_raw_part<IT, MODE, 0>(raw, a, cg, h, col0, vcg, tid);
-  load_raw_part<IT, MODE, 1>(raw, a, cg, h, col0, vcg, tid);
-  load_raw_part<IT, MODE, 2>(raw, a, cg, h, col0, vcg, tid);
-  load_raw_part<IT, MODE, 3>(raw, a, cg, h, col0, vcg, tid);
-  load_raw_part<IT, MODE, 4>(raw, a, cg, h, col0, vcg, tid);
-  load_raw_part<IT, MODE, 5>(raw, a, cg, h, col0, vcg, tid);
-  load_raw_part<IT, MODE, 6>(raw, a, cg, h, col0, vcg, tid);
-  load_raw_part<IT, MODE, 7>(raw, a, cg, h, col0, vcg, tid);
+__device__ __forceinline__ void load_raw(Raw<IT>& raw, const ChunkLoads& cl, const LoaderLanes& ll, int tid) {
+  load_raw_part<IT, MODE, 0>(raw, cl, ll, tid);
+  load_raw_part<IT, MODE, 1>(raw, cl, ll, tid);
+  load_raw_part<IT, MODE, 2>(raw, cl, ll, tid);
+  load_raw_part<IT, MODE, 3>(raw, cl, ll, tid);
+  load_raw_part<IT, MODE, 4>(raw, cl, ll, tid);
+  load_raw_part<IT, MODE, 5>(raw, cl, ll, tid);
+  load_raw_part<IT, MODE, 6>(raw, cl, ll, tid);
+  load_raw_part<IT, MODE, 7>(raw, cl, ll, tid);
 }
 
 // Where the loader waves are in a chunk's phases, for the spread loads of
-// the chunk after next: `load_part<P>()` issues part P if there is one.
+// the next chunk: `load_part<P>()` issues part P if there is one.
 template <class IT, int MODE>
 struct NextLoads {
   Raw<IT>* raw;
-  const SegArgs<IT>* a;
-  ChunkGeo cg;
-  int64_t h, col0;
-  int vcg, tid;
+  ChunkLoads cl;
+  const LoaderLanes* ll;
+  int tid;
   bool active;
   template <int P>
   __device__ __forceinline__ void load_part() const {
-    if (active) load_raw_part<IT, MODE, P>(*raw, *a, cg, h, col0, vcg, tid);
+    if (active) load_raw_part<IT, MODE, P>(*raw, cl, *ll, tid);
   }
 };
 
@@ -356,49 +415,62 @@ __device__ __forceinline__ void m_block_row(unsigned char* sm, int lane) {
   bf16(*TinvT)[16][16] = lds<bf16[16][16]>(sm, kOffTinvT);
   const float* betas = lds<float>(sm, kOffBeta);
   unsigned char* mf = sm + kOffMf;
+  // every operand of the chain first (one LDS round trip):
+  //   bt[J][K - J - 1] = B_KJ^T (lane (j, g) holds B[16K + 4g + r][16J + j]),
+  //   ta[J] = -T_J^T (lane (j, g) holds T_J[4g + r][j]), b4[J] = beta of block J
+  bf16x4_t tI = *reinterpret_cast<const bf16x4_t*>(&Tinv[I][n16][4 * g4]);  // T_I[i][4g + r]
+  bf16x4_t bt[I > 0 ? I : 1][I > 0 ? I : 1];
+  bf16x4_t ta[I > 0 ? I : 1];
+  f32x4_t b4[I + 1];
+#pragma unroll
+  for (int J = 0; J <= I; ++J) b4[J] = *reinterpret_cast<const f32x4_t*>(&betas[16 * J + 4 * g4]);
+#pragma unroll
+  for (int J = 0; J < I; ++J) {
+    ta[J] = negate_bf16(*reinterpret_cast<const bf16x4_t*>(&TinvT[J][n16][4 * g4]));
+#pragma unroll
+    for (int K = J + 1; K <= I; ++K)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bt[J][K - J - 1][r] = Lm[16 * K + 4 * g4 + r][16 * J + n16];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   auto put = [&](int J, const f32x4_t& z) {  // M_IJ = N_IJ diag(beta_J)
-    const f32x4_t b4 = *reinterpret_cast<const f32x4_t*>(&betas[16 * J + 4 * g4]);
     *reinterpret_cast<bf16x4_t*>(mf + ((I * 2 + J / 2) * 64 + lane) * 16 + (J & 1) * 8) =
-        bf16x4_t{(bf16)(z[0] * b4[0]), (bf16)(z[1] * b4[1]), (bf16)(z[2] * b4[2]), (bf16)(z[3] * b4[3])};
+        bf16x4_t{(bf16)(z[0] * b4[J][0]), (bf16)(z[1] * b4[J][1]), (bf16)(z[2] * b4[J][2]), (bf16)(z[3] * b4[J][3])};
   };
   f32x4_t Z[I + 1];
-  {
-    const bf16x4_t t = *reinterpret_cast<const bf16x4_t*>(&Tinv[I][n16][4 * g4]);  // T_I[i][4g + r]
-    Z[I] = f32x4_t{(float)t[0], (float)t[1], (float)t[2], (float)t[3]};
-    put(I, Z[I]);
-    if constexpr ((I & 1) == 0)  // block (I, I + 1) is above the diagonal
-      *reinterpret_cast<bf16x4_t*>(mf + ((I * 2 + I / 2) * 64 + lane) * 16 + 8) = bf16x4_t{};
-  }
+  Z[I] = f32x4_t{(float)tI[0], (float)tI[1], (float)tI[2], (float)tI[3]};
+  put(I, Z[I]);
+  if constexpr ((I & 1) == 0)  // block (I, I + 1) is above the diagonal
+    *reinterpret_cast<bf16x4_t*>(mf + ((I * 2 + I / 2) * 64 + lane) * 16 + 8) = bf16x4_t{};
 #pragma unroll
   for (int J = I - 1; J >= 0; --J) {
     f32x4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int K = J + 1; K <= I; ++K) {
-      // A = B_KJ^T: lane (j, g) holds B[16K + 4g + r][16J + j]
-      bf16x4_t bt;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) bt[r] = Lm[16 * K + 4 * g4 + r][16 * J + n16];
       const bf16x4_t zb = {(bf16)Z[K][0], (bf16)Z[K][1], (bf16)Z[K][2], (bf16)Z[K][3]};
-      acc = mfma16(bt, zb, acc);
+      acc = mfma16(bt[J][K - J - 1], zb, acc);
     }
-    // A = -T_J^T: lane (j, g) holds T_J[4g + r][j] = T_J^T[j][4g + r]
-    const bf16x4_t ta = negate_bf16(*reinterpret_cast<const bf16x4_t*>(&TinvT[J][n16][4 * g4]));
     const bf16x4_t ab = {(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
-    Z[J] = mfma16(ta, ab, f32x4_t{0.f, 0.f, 0.f, 0.f});
+    Z[J] = mfma16(ta[J], ab, f32x4_t{0.f, 0.f, 0.f, 0.f});
     put(J, Z[J]);
   }
 }
 
 // ---- per-chunk preparation: every chunk operand, in LDS ---------------------
-// P1 of one chunk, computed by a loader thread (block J = wave - 4, channel
-// pair cp = lane) from the raw inputs into registers: the decayed rows
-// k a, q a, k E as bf16 pairs, the per-channel block factors, the v slice
-// (bf16) and beta.  The loaders compute it for chunk c + 1 while the
-// scanners advance the state through chunk c, and write it to LDS at the top
-// of the next chunk (p1_write).
+// P1 of one chunk, computed by a loader thread (block J, channel pair cp)
+// from the raw inputs into registers: the decayed rows k a, q a, k E as bf16
+// pairs, the per-channel decay tables of block J (from the four blocks'
+// products, exchanged between the lanes that hold them), the v slice (bf16)
+// and beta.  The loaders compute it for chunk c + 1 while the scanners
+// advance the state through chunk c, and write it to LDS at the top of the
+// next chunk (p1_write).
 struct P1Out {
   uint32_t ka[16], qa[16], ke[16];  // bf16 pairs (channels 2cp, 2cp + 1) of rows 16 J + r
-  float pblk[2], a0[2];             // exp(lg_{16J+15} - lg_{16J}) and alpha at row 16 J
+  float gs[2];                      // exp(lg_{16J})
+  float ge[2];                      // exp(lg_63 - lg_{16J+15})
+  float gam[2];                     // exp(lg_63)
+  float sc[4][2];                   // scales of block pairs (J, J'), J' <= J
+  int ext;                          // some block of the wave's channels decays past 2^-100
   uint4 vv[4];                      // bf16 v units of this thread (zero past the valid rows)
   float bt;                         // beta of row t2 (< 64), zero past the valid rows
 };
@@ -409,7 +481,7 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 template <class IT, int MODE>
 __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const ChunkGeo& cg, int vcg, int tid) {
-  const int J = wave_of(tid) - 4;
+  const int J = loader_block(tid);
   const int n_valid = cg.n_valid;
   float al[2][16];
 #pragma unroll
@@ -443,18 +515,43 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) suf[ch] *= al[ch][r];
   }
+  // Block J's products P_J = exp(lg_{16J+15} - lg_{16J}) (a at its last row)
+  // and alpha at its first row A0_J give G_J = A0_J P_J, the decay across the
+  // block; the other blocks' G come from lanes l ^ 16, l ^ 32, l ^ 48.
+  //   Gs_J = A0_J prod_{J' < J} G_J',  Ge_J = prod_{J' > J} G_J',  gamma = prod G_J',
+  //   pair (J, J') scale: A0_J prod_{J' < j < J} G_j (J' < J), 1 / P_J (J' = J).
+  const int lane = tid & 63;
+  bool ext = false;
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch) {
-    po.pblk[ch] = run[ch];  // a at the last row = exp(lg_{16J+15} - lg_{16J})
-    po.a0[ch] = al[ch][0];
+    const float a0 = al[ch][0];
+    const float pj = run[ch];
+    ext = ext || !(pj >= kExtremeDecay);
+    float G[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) G[jb] = __shfl(a0 * pj, (lane & 15) + 16 * jb);
+    float pre = 1.f, post = 1.f;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      pre *= jb < J ? G[jb] : 1.f;
+      post *= jb > J ? G[jb] : 1.f;
+    }
+    po.gs[ch] = pre * a0;
+    po.ge[ch] = post;
+    po.gam[ch] = G[0] * G[1] * G[2] * G[3];
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp) {
+      float sc = a0;
+#pragma unroll
+      for (int jj = 1; jj < 3; ++jj) sc *= (jj > jp && jj < J) ? G[jj] : 1.f;
+      po.sc[jp][ch] = jp < J ? sc : (pj > 0.f ? 1.f / pj : 0.f);
+    }
   }
+  po.ext = __any(ext) ? 1 : 0;
   const int t2 = tid - 256;
-  const int upr = vcg / 8;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
-    const int row = (t2 + 256 * i) / upr;
-    uint4 val = raw.vv[i];
-    if (row >= n_valid) val = uint4{0u, 0u, 0u, 0u};
+    uint4 val = raw.vv[i];  // rows past the valid ones were read as zero
     if constexpr (sizeof(IT) == 2 && !__is_same(IT, bf16)) {
       // f16 inputs: convert the 8 values to bf16 operands
       typedef IT h8_t __attribute__((ext_vector_type(8)));
@@ -472,40 +569,49 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
 // Writes P1 (loader waves) and joins every wave at the first barrier of the
 // chunk.
 template <int MODE, bool LOADER>
-__device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, int vcg, int tid) {
+__device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, const LoaderLanes* ll, int tid) {
   if constexpr (LOADER) {
-    const int J = wave_of(tid) - 4;
-    const int cp = tid & 63;
-    bf16(*KA)[kRow] = lds<bf16[kRow]>(sm, kOffKA);
-    bf16(*QA)[kRow] = lds<bf16[kRow]>(sm, kOffQA);
-    bf16(*KE)[kRow] = lds<bf16[kRow]>(sm, kOffKE);
-    float(*Gt)[kKey] = lds<float[kKey]>(sm, kOffTab);                      // G  [4][128]
-    float(*A0t)[kKey] = lds<float[kKey]>(sm, kOffTab + 4 * kKey * 4);      // A0 [4][128]
-    float(*Pt)[kKey] = lds<float[kKey]>(sm, kOffTab + 8 * kKey * 4);       // P  [4][128]
+    const int J = loader_block(tid);
+    const int cp = loader_pair(tid);
+    bf16(*KEt)[kRowT] = lds<bf16[kRowT]>(sm, kOffKEt);
+    float(*Sc)[kKey] = lds<float[kKey]>(sm, kOffTab);
+    float(*Gs)[kKey] = lds<float[kKey]>(sm, kOffGs);
+    float(*Ge)[kKey] = lds<float[kKey]>(sm, kOffGe);
+    float* gam = lds<float>(sm, kOffGam);
     float* betas = lds<float>(sm, kOffBeta);
-    bf16(*Vn)[kRow] = lds<bf16[kRow]>(sm, kOffVn);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int tl = 16 * J + r;
-      *reinterpret_cast<uint32_t*>(&KA[tl][2 * cp]) = po.ka[r];
-      if constexpr (MODE == kOutput) *reinterpret_cast<uint32_t*>(&QA[tl][2 * cp]) = po.qa[r];
-      *reinterpret_cast<uint32_t*>(&KE[tl][2 * cp]) = po.ke[r];
+      *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKA, tl) + 2 * cp) = po.ka[r];
+      if constexpr (MODE == kOutput) *reinterpret_cast<uint32_t*>(nat_row(sm, kOffQA, tl) + 2 * cp) = po.qa[r];
+      *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKE, tl) + 2 * cp) = po.ke[r];
+    }
+    // channel-major k E: rows 16 J .. 16 J + 15 of channels 2 cp, 2 cp + 1
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      uint32_t w[8];
+#pragma unroll
+      for (int m = 0; m < 8; ++m)
+        w[m] = ch == 0 ? (po.ke[2 * m] & 0xffffu) | (po.ke[2 * m + 1] << 16)
+                       : (po.ke[2 * m] >> 16) | (po.ke[2 * m + 1] & 0xffff0000u);
+      *reinterpret_cast<uint4*>(&KEt[2 * cp + ch][16 * J]) = uint4{w[0], w[1], w[2], w[3]};
+      *reinterpret_cast<uint4*>(&KEt[2 * cp + ch][16 * J + 8]) = uint4{w[4], w[5], w[6], w[7]};
     }
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
       const int cc = 2 * cp + ch;
-      Pt[J][cc] = po.pblk[ch];
-      A0t[J][cc] = po.a0[ch];
-      Gt[J][cc] = po.a0[ch] * po.pblk[ch];
-    }
-    const int t2 = tid - 256;
-    const int upr = vcg / 8;
+      Gs[J][cc] = po.gs[ch];
+      Ge[J][cc] = po.ge[ch];
+      if (J == 0) gam[cc] = po.gam[ch];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int u = t2 + 256 * i;
-      const int row = u / upr;
-      if (row < kChunk) *reinterpret_cast<uint4*>(&Vn[row][8 * (u % upr)]) = po.vv[i];
+      for (int jp = 0; jp < 4; ++jp)
+        if (jp <= J) Sc[J * (J + 1) / 2 + jp][cc] = po.sc[jp][ch];
     }
+    if ((tid & 63) == 0) lds<int>(sm, kOffFlag)[wave_of(tid) - 4] = po.ext;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (ll->vlds[i] >= 0) *reinterpret_cast<uint4*>(sm + kOffVn + ll->vlds[i]) = po.vv[i];
+    const int t2 = tid - 256;
     if (t2 < kChunk) betas[t2] = po.bt;
   }
   __syncthreads();
@@ -521,97 +627,61 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
   const int n16 = lane & 15;
   const int g4 = lane >> 4;
   const int n_valid = cg.n_valid;
-  bf16(*KA)[kRow] = lds<bf16[kRow]>(sm, kOffKA);
-  bf16(*QA)[kRow] = lds<bf16[kRow]>(sm, kOffQA);
-  bf16(*KE)[kRow] = lds<bf16[kRow]>(sm, kOffKE);
   bf16(*Lm)[72] = lds<bf16[72]>(sm, kOffL);
   float(*Ld)[16][16] = lds<float[16][16]>(sm, kOffLd);
   bf16(*Tinv)[16][16] = lds<bf16[16][16]>(sm, kOffTinv);
   bf16(*TinvT)[16][16] = lds<bf16[16][16]>(sm, kOffTinvT);
-  float(*Gt)[kKey] = lds<float[kKey]>(sm, kOffTab);                      // G  [4][128]
-  float(*A0t)[kKey] = lds<float[kKey]>(sm, kOffTab + 4 * kKey * 4);      // A0 [4][128]
-  float(*Pt)[kKey] = lds<float[kKey]>(sm, kOffTab + 8 * kKey * 4);       // P  [4][128]
-  float(*Sc)[kKey] = lds<float[kKey]>(sm, kOffTab);                      // pair scales [10][128]
+  bf16(*KEt)[kRowT] = lds<bf16[kRowT]>(sm, kOffKEt);
+  float(*Sc)[kKey] = lds<float[kKey]>(sm, kOffTab);  // pair scales [10][128]
   float(*Gs)[kKey] = lds<float[kKey]>(sm, kOffGs);
   float(*Ge)[kKey] = lds<float[kKey]>(sm, kOffGe);
   float* betas = lds<float>(sm, kOffBeta);
-  float* gam = lds<float>(sm, kOffGam);
+  const int* flags = lds<int>(sm, kOffFlag);
 
-  if constexpr (LOADER) nl.template load_part<0>();
-  // ---- P1b: block-level decay tables and gamma_C ---------------------------
-  int* flags = lds<int>(sm, kOffFlag);
-  if (tid < kKey) {
-    const int cc = tid;
-    float G[4], A0[4], P[4];
-    bool ext = false;
-#pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      G[J] = Gt[J][cc];
-      A0[J] = A0t[J][cc];
-      P[J] = Pt[J][cc];
-      ext = ext || !(P[J] >= kExtremeDecay);
-    }
-    // a 16-row block decaying by more than 2^-100 takes the exact path below
-    const int any_ext = __any(ext) ? 1 : 0;
-    if (lane == 0) flags[wave] = any_ext;
-    float pre = 1.f;
-#pragma unroll
-    for (int J = 0; J < 4; ++J) {
-      Gs[J][cc] = pre * A0[J];
-      pre *= G[J];
-    }
-    float post = 1.f;
-#pragma unroll
-    for (int J = 3; J >= 0; --J) {
-      Ge[J][cc] = post;
-      post *= G[J];
-    }
-    gam[cc] = pre;  // exp(lg_63)
-    // scale of the k_j E_j operand for block pair (I, J): D_IJ = alpha_{16I} prod_{J<J'<I} G_J'
-    // for J < I, 1 / P_I on the diagonal (written over G/A0/P of this same channel)
-    int pidx = 0;
-#pragma unroll
-    for (int I = 0; I < 4; ++I) {
-#pragma unroll
-      for (int J = 0; J <= I; ++J, ++pidx) {
-        float sc;
-        if (J < I) {
-          sc = A0[I];
-#pragma unroll
-          for (int jj = J + 1; jj < I; ++jj) sc *= G[jj];
-        } else {
-          sc = P[I] > 0.f ? 1.f / P[I] : 0.f;
-        }
-        Sc[pidx][cc] = sc;
-      }
-    }
+  if constexpr (LOADER) {
+    nl.template load_part<0>();
+    nl.template load_part<1>();
   }
-  __syncthreads();
-
-  if constexpr (LOADER) nl.template load_part<1>();
   // ---- export: Q~ (phase C) and K~^T fragments ------------------------------
-  for (int task = (MODE == kOutput ? 0 : 1024) + tid; task < 2048; task += kThreads) {
-    const int frag = (task >> 6) & 15;
-    const int fl = task & 63;
-    const int fi = fl & 15, fg = fl >> 4;
-    bf16x8_t o;
-    if (task < 1024) {  // Q~ = exp(lg) q : fragment (I, s), lane (i, g)
-      const int I = frag >> 2, st = frag & 3;
+  // element e of lane (i, g) of fragment s covers index 32 s + 4 g + e (e < 4)
+  // and 32 s + 16 + 4 g + e - 4: two runs of four, one 8-byte read each.  Task
+  // tid + 512 k is a Q~ fragment lane for k < 2 (phase C) and a K~^T one
+  // otherwise; every task's reads go out before any is used.
+  {
+    constexpr int k0 = MODE == kOutput ? 0 : 2;
+    bf16x4_t lo[4], hi[4];
+    f32x4_t slo[4], shi[4];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int ch = 32 * st + perm_index(e, fg);
-        o[e] = (bf16)((float)QA[16 * I + fi][ch] * Gs[I][ch]);
+    for (int k = k0; k < 4; ++k) {
+      const int task = tid + kThreads * k;
+      const int frag = (task >> 6) & 15;
+      const int fi = task & 15, fg = (task >> 4) & 3;
+      if (k < 2) {  // Q~ = exp(lg) q : fragment (I, s), lane (i, g)
+        const int I = frag >> 2, c0 = 32 * (frag & 3) + 4 * fg;
+        const bf16* row = nat_row(sm, kOffQA, 16 * I + fi);
+        lo[k] = *reinterpret_cast<const bf16x4_t*>(row + c0);
+        hi[k] = *reinterpret_cast<const bf16x4_t*>(row + c0 + 16);
+        slo[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0]);
+        shi[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
+      } else {  // K~^T : fragment (ct, s'), lane (c, g); rows r0.. and r0 + 16.. each sit in one block
+        const int ch = 16 * (frag >> 1) + fi, r0 = 32 * (frag & 1) + 4 * fg;
+        lo[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0]);
+        hi[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0 + 16]);
+        slo[k][0] = Ge[r0 >> 4][ch];
+        shi[k][0] = Ge[(r0 + 16) >> 4][ch];
       }
-      *lds<bf16x8_t>(sm, kOffQf + (frag * 64 + fl) * 16) = o;
-    } else {  // K~^T : fragment (ct, s'), lane (c, g)
-      const int ct = frag >> 1, st = frag & 1;
-      const int ch = 16 * ct + fi;
+    }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int tk = 32 * st + perm_index(e, fg);
-        o[e] = (bf16)((float)KE[tk][ch] * Ge[tk >> 4][ch]);
+    for (int k = k0; k < 4; ++k) {
+      const int task = tid + kThreads * k;
+      bf16x8_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = (bf16)((float)lo[k][e] * (k < 2 ? slo[k][e] : slo[k][0]));
+        o[4 + e] = (bf16)((float)hi[k][e] * (k < 2 ? shi[k][e] : shi[k][0]));
       }
-      *lds<bf16x8_t>(sm, kOffKTf + (frag * 64 + fl) * 16) = o;
+      *lds<bf16x8_t>(sm, (k < 2 ? kOffQf : kOffKTf) + (task & 1023) * 16) = o;
     }
   }
 
@@ -621,30 +691,41 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
     // block pair p = I (I + 1) / 2 + J, J <= I
     const int I = p >= 6 ? 3 : (p >= 3 ? 2 : (p >= 1 ? 1 : 0));
     const int J = p - I * (I + 1) / 2;
+    // the operands of two reduction steps at a time (two LDS round trips per pair)
+    const bf16* ke_row = nat_row(sm, kOffKE, 16 * J + n16);
+    const bf16* ka_row = nat_row(sm, kOffKA, 16 * I + n16);
+    const bf16* qa_row = nat_row(sm, kOffQA, 16 * I + n16);
+    const int i = 16 * I + n16;
+    const float bi = betas[i];
     f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
     f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int st = 0; st < 4; ++st) {
-      const int c0 = 32 * st + 8 * g4;
-      const bf16x8_t ke = *reinterpret_cast<const bf16x8_t*>(&KE[16 * J + n16][c0]);
-      const f32x4_t sc0 = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0]);
-      const f32x4_t sc1 = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0 + 4]);
-      bf16x8_t af;
+    for (int half = 0; half < 2; ++half) {
+      bf16x8_t ke[2], kb[2], qb[2];
+      f32x4_t sc0[2], sc1[2];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        af[e] = (bf16)((float)ke[e] * sc0[e]);
-        af[4 + e] = (bf16)((float)ke[4 + e] * sc1[e]);
+      for (int u = 0; u < 2; ++u) {
+        const int c0 = 32 * (2 * half + u) + 8 * g4;
+        ke[u] = *reinterpret_cast<const bf16x8_t*>(ke_row + c0);
+        sc0[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0]);
+        sc1[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0 + 4]);
+        kb[u] = *reinterpret_cast<const bf16x8_t*>(ka_row + c0);
+        if constexpr (MODE == kOutput) qb[u] = *reinterpret_cast<const bf16x8_t*>(qa_row + c0);
       }
-      const bf16x8_t kb = *reinterpret_cast<const bf16x8_t*>(&KA[16 * I + n16][c0]);
-      akk = mfma32(af, kb, akk);
-      if constexpr (MODE == kOutput) {
-        const bf16x8_t qb = *reinterpret_cast<const bf16x8_t*>(&QA[16 * I + n16][c0]);
-        aqk = mfma32(af, qb, aqk);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        bf16x8_t af;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          af[e] = (bf16)((float)ke[u][e] * sc0[u][e]);
+          af[4 + e] = (bf16)((float)ke[u][4 + e] * sc1[u][e]);
+        }
+        akk = mfma32(af, kb[u], akk);
+        if constexpr (MODE == kOutput) aqk = mfma32(af, qb[u], aqk);
       }
     }
     // lane (n16, g4) holds A[16I + n16][16J + 4 g4 + r] (and likewise Aqk)
-    const int i = 16 * I + n16;
-    const float bi = betas[i];
     bf16x4_t lrow;
     bf16x4_t qrow;
 #pragma unroll
@@ -667,7 +748,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
 
   if constexpr (LOADER) nl.template load_part<4>();
   // ---- exact diagonal blocks for chunks with extreme decay ----------------
-  if (flags[0] | flags[1]) {
+  if (flags[0] | flags[1] | flags[2] | flags[3]) {
     float* Lr = lds<float>(sm, kOffQA);  // [64][128] f32 over the dead q a and k E tiles
     const int64_t krow = a.H * kKey;
     if (wave < 4) {
@@ -721,23 +802,36 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
   // 0-3; meanwhile waves 4-7 export Kgamma = exp(lg) k over the dead q a tile
   if (wave < 4) {
     if (lane < 16) {
-      // column `lane` of T_I, row by row; one row of L is loaded at a time
+      // column `lane` of T_I, row by row.  Row r + 1 of L is read while row r
+      // is formed (its entries j < r + 1 only), and each row's sum runs in two
+      // independent halves, so neither the LDS latency nor one long chain of
+      // dependent FMAs sets the pace.
       const int I = wave;
       float x[16];
+      f32x4_t cur[4] = {}, nxt[4] = {};
+      x[0] = lane == 0 ? 1.f : 0.f;
+      Tinv[I][0][lane] = (bf16)x[0];
+      cur[0] = *reinterpret_cast<const f32x4_t*>(&Ld[I][1][0]);
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float row[16];
+      for (int r = 1; r < 16; ++r) {
+        if (r + 1 < 16) {
 #pragma unroll
-        for (int q4 = 0; q4 < 4; ++q4) {
-          const f32x4_t v4 = *reinterpret_cast<const f32x4_t*>(&Ld[I][r][4 * q4]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) row[4 * q4 + e] = v4[e];
+          for (int q4 = 0; q4 < 4; ++q4)
+            if (4 * q4 < r + 1) nxt[q4] = *reinterpret_cast<const f32x4_t*>(&Ld[I][r + 1][4 * q4]);
         }
-        float acc = (r == lane) ? 1.f : 0.f;
+        float acc0 = (r == lane) ? 1.f : 0.f;
+        float acc1 = 0.f;
 #pragma unroll
-        for (int j = 0; j < r; ++j) acc -= row[j] * x[j];
-        x[r] = acc;
-        Tinv[I][r][lane] = (bf16)acc;
+        for (int j = 0; j < r; ++j) {
+          if (j & 1)
+            acc1 -= cur[j >> 2][j & 3] * x[j];
+          else
+            acc0 -= cur[j >> 2][j & 3] * x[j];
+        }
+        x[r] = acc0 + acc1;
+        Tinv[I][r][lane] = (bf16)x[r];
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) cur[q4] = nxt[q4];
         __builtin_amdgcn_sched_barrier(0);
       }
       bf16x8_t t0, t1;
@@ -750,18 +844,31 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
       *reinterpret_cast<bf16x8_t*>(&TinvT[I][lane][8]) = t1;
     }
   } else {
-    for (int task = tid - 256; task < 1024; task += 256) {  // -Kgamma : fragment (I, s), lane (i, g)
+    // -Kgamma : fragment (I, s), lane (i, g); tasks tid - 256 + 256 k, reads first
+    bf16x4_t lo[4], hi[4];
+    f32x4_t glo[4], ghi[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int task = tid - 256 + 256 * k;
       const int frag = task >> 6;
-      const int fl = task & 63;
-      const int fi = fl & 15, fg = fl >> 4;
-      const int I = frag >> 2, st = frag & 3;
+      const int fi = task & 15, fg = (task >> 4) & 3;
+      const int I = frag >> 2, c0 = 32 * (frag & 3) + 4 * fg;
+      const bf16* row = nat_row(sm, kOffKA, 16 * I + fi);
+      lo[k] = *reinterpret_cast<const bf16x4_t*>(row + c0);
+      hi[k] = *reinterpret_cast<const bf16x4_t*>(row + c0 + 16);
+      glo[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0]);
+      ghi[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
       bf16x8_t o;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int ch = 32 * st + perm_index(e, fg);
-        o[e] = (bf16)(-(float)KA[16 * I + fi][ch] * Gs[I][ch]);
+      for (int e = 0; e < 4; ++e) {
+        o[e] = (bf16)(-(float)lo[k][e] * glo[k][e]);
+        o[4 + e] = (bf16)(-(float)hi[k][e] * ghi[k][e]);
       }
-      *lds<bf16x8_t>(sm, kOffKgf + (frag * 64 + fl) * 16) = o;
+      *lds<bf16x8_t>(sm, kOffKgf + (tid - 256 + 256 * k) * 16) = o;
     }
     if constexpr (LOADER) nl.template load_part<6>();
   }
@@ -1041,7 +1148,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       // the many lane-dependent LDS addresses of a chunk out of the loop,
       // where they would stay live (and spill) next to the state tiles
       const int tid_c = opaque(tid);
-      p1_write<MODE, false>(sm, none, vcg, tid_c);
+      p1_write<MODE, false>(sm, none, nullptr, tid_c);
       prepare_mid<IT, MODE, false>(sm, a, geo, h, vcg, tid_c, nl);
       prepare_m<IT, MODE, false>(sm, tid_c, nl);
 #pragma unroll
@@ -1065,19 +1172,24 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
     // The raw inputs of chunk c + 1 are loaded in eight parts spread over
     // the phases of chunk c (one burst of every CU's 64 KB would saturate the
     // memory system and stall the issuing waves); while the scanners advance
-    // the state through chunk c the loaders turn them into P1 registers.
+    // the state through chunk c the loaders turn them into P1 registers.  All
+    // eight parts are loaded and consumed within one iteration: raw inputs
+    // carried across the loop edge end up copied between registers, which
+    // waits for the loads.
     Raw<IT> raw;
     P1Out po;
+    const LoaderLanes ll = loader_lanes<IT>(a, vcg, tid);
     if (c_begin < c_end) {
       const ChunkGeo g0 = chunk_geo(sr, c_begin - cs);
-      load_raw<IT, MODE>(raw, a, g0, h, col0, vcg, tid);
+      load_raw<IT, MODE>(raw, chunk_loads<IT>(a, g0, h, col0), ll, tid);
       p1_math<IT, MODE>(po, raw, g0, vcg, tid);
     }
     for (int64_t c = c_begin; c < c_end; ++c) {
       const ChunkGeo geo = chunk_geo(sr, c - cs);
       const int tid_c = opaque(tid);
-      p1_write<MODE, true>(sm, po, vcg, tid_c);
-      const NextLoads<IT, MODE> nl{&raw, &a, chunk_geo(sr, c + 1 - cs), h, col0, vcg, tid_c, c + 1 < c_end};
+      p1_write<MODE, true>(sm, po, &ll, tid_c);
+      const NextLoads<IT, MODE> nl{&raw, chunk_loads<IT>(a, chunk_geo(sr, c + 1 - cs), h, col0), &ll, tid_c,
+                                   c + 1 < c_end};
       prepare_mid<IT, MODE, true>(sm, a, geo, h, vcg, tid_c, nl);
       prepare_m<IT, MODE, true>(sm, tid_c, nl);
       if (c + 1 < c_end) p1_math<IT, MODE>(po, raw, chunk_geo(sr, c + 1 - cs), vcg, tid_c);
