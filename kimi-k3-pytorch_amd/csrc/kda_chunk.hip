@@ -99,7 +99,16 @@ constexpr int kOffFlag = kOffGam + 512;             // int [4] extreme-decay fla
 constexpr int kRowT = 72;                           // padded row of the channel-major tile
 constexpr int kOffKEt = kOffFlag + 16;              // bf16 [128][72] k_j E_j, channel-major
 constexpr int kSmemBytes = kOffKEt + kKey * kRowT * 2;
-constexpr int kOffKgf = kOffQA;    // -Kgamma = -exp(lg) k A fragments [I=4][s=4][lane][8] bf16
+// -Kgamma = -exp(lg) k A fragments, 1 KB each (64 lanes x 8 bf16), fragment
+// (I, s) at kgf_off<MODE>(I, s): in phase C [I][s] over the q a tile, which is
+// dead after P2; in phase A [s][I] with block s over the channel-major k E
+// rows of channels 32 s .. 32 s + 31, which the loader wave that owns those
+// channels has finished reading when it writes block s.
+constexpr int kKgfStride = 32 * kRowT * 2;  // 4608
+template <int MODE>
+__host__ __device__ constexpr int kgf_off(int I, int s) {
+  return MODE == kOutput ? kOffQA + (I * 4 + s) * 1024 : kOffKEt + s * kKgfStride + I * 1024;
+}
 constexpr int kOffMf = kOffKE;     // M = (I + diag(beta) A)^-1 diag(beta) A fragments [I=4][s=2][lane][8]
 constexpr int kOffStage = kOffKA;  // output transpose [4 waves][64][32]
 constexpr int kOffPnat = kOffKA;   // phase A: P_g natural bf16 [128][136]
@@ -108,6 +117,7 @@ static_assert(kOffKEt % 16 == 0 && kOffGs % 16 == 0 && kOffGe % 16 == 0, "16-byt
 static_assert(4 * 64 * 32 * 2 <= kNat, "output stage must fit in the k a tile");
 static_assert(kKey * kRow * 2 <= 2 * kNat, "P transpose must fit in the k a and q a tiles");
 static_assert(16384 <= kNat && 8192 <= kNat, "Kgamma and M fragments must fit in the q a and k E tiles");
+static_assert(4 * kKgfStride == kKey * kRowT * 2 && 4 * 1024 <= kKgfStride, "Kgamma blocks must fit their k E rows");
 // Fragment element e of lane (i, g) covers reduction index
 //   32 s + (e < 4 ? 4 g + e : 16 + 4 g + e - 4),
 // the order in which two stacked C tiles provide a B operand.
@@ -642,105 +652,229 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
     nl.template load_part<0>();
     nl.template load_part<1>();
   }
+  if constexpr (MODE == kOutput) {
+    // phase C: every wave exports Q~ and K~^T and takes block pairs of P2;
+    // the loaders export -Kgamma during P3
   // ---- export: Q~ (phase C) and K~^T fragments ------------------------------
-  // element e of lane (i, g) of fragment s covers index 32 s + 4 g + e (e < 4)
-  // and 32 s + 16 + 4 g + e - 4: two runs of four, one 8-byte read each.  Task
-  // tid + 512 k is a Q~ fragment lane for k < 2 (phase C) and a K~^T one
-  // otherwise; every task's reads go out before any is used.
-  {
-    constexpr int k0 = MODE == kOutput ? 0 : 2;
-    bf16x4_t lo[4], hi[4];
-    f32x4_t slo[4], shi[4];
-#pragma unroll
-    for (int k = k0; k < 4; ++k) {
-      const int task = tid + kThreads * k;
-      const int frag = (task >> 6) & 15;
-      const int fi = task & 15, fg = (task >> 4) & 3;
-      if (k < 2) {  // Q~ = exp(lg) q : fragment (I, s), lane (i, g)
-        const int I = frag >> 2, c0 = 32 * (frag & 3) + 4 * fg;
-        const bf16* row = nat_row(sm, kOffQA, 16 * I + fi);
-        lo[k] = *reinterpret_cast<const bf16x4_t*>(row + c0);
-        hi[k] = *reinterpret_cast<const bf16x4_t*>(row + c0 + 16);
-        slo[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0]);
-        shi[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
-      } else {  // K~^T : fragment (ct, s'), lane (c, g); rows r0.. and r0 + 16.. each sit in one block
-        const int ch = 16 * (frag >> 1) + fi, r0 = 32 * (frag & 1) + 4 * fg;
-        lo[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0]);
-        hi[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0 + 16]);
-        slo[k][0] = Ge[r0 >> 4][ch];
-        shi[k][0] = Ge[(r0 + 16) >> 4][ch];
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = k0; k < 4; ++k) {
-      const int task = tid + kThreads * k;
-      bf16x8_t o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[e] = (bf16)((float)lo[k][e] * (k < 2 ? slo[k][e] : slo[k][0]));
-        o[4 + e] = (bf16)((float)hi[k][e] * (k < 2 ? shi[k][e] : shi[k][0]));
-      }
-      *lds<bf16x8_t>(sm, (k < 2 ? kOffQf : kOffKTf) + (task & 1023) * 16) = o;
-    }
-  }
-
-  if constexpr (LOADER) nl.template load_part<2>();
-  // ---- P2: A (strict) and Aqk (causal) 16x16 blocks on MFMA ---------------
-  for (int p = wave; p < 10; p += 8) {
-    // block pair p = I (I + 1) / 2 + J, J <= I
-    const int I = p >= 6 ? 3 : (p >= 3 ? 2 : (p >= 1 ? 1 : 0));
-    const int J = p - I * (I + 1) / 2;
-    // the operands of two reduction steps at a time (two LDS round trips per pair)
-    const bf16* ke_row = nat_row(sm, kOffKE, 16 * J + n16);
-    const bf16* ka_row = nat_row(sm, kOffKA, 16 * I + n16);
-    const bf16* qa_row = nat_row(sm, kOffQA, 16 * I + n16);
-    const int i = 16 * I + n16;
-    const float bi = betas[i];
-    f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
-    f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      bf16x8_t ke[2], kb[2], qb[2];
-      f32x4_t sc0[2], sc1[2];
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int c0 = 32 * (2 * half + u) + 8 * g4;
-        ke[u] = *reinterpret_cast<const bf16x8_t*>(ke_row + c0);
-        sc0[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0]);
-        sc1[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0 + 4]);
-        kb[u] = *reinterpret_cast<const bf16x8_t*>(ka_row + c0);
-        if constexpr (MODE == kOutput) qb[u] = *reinterpret_cast<const bf16x8_t*>(qa_row + c0);
+    // element e of lane (i, g) of fragment s covers index 32 s + 4 g + e (e < 4)
+    // and 32 s + 16 + 4 g + e - 4: two runs of four, one 8-byte read each.  Task
+    // tid + 512 k is a Q~ fragment lane for k < 2 (phase C) and a K~^T one
+    // otherwise; every task's reads go out before any is used.
+    {
+      constexpr int k0 = MODE == kOutput ? 0 : 2;
+      bf16x4_t lo[4], hi[4];
+      f32x4_t slo[4], shi[4];
+  #pragma unroll
+      for (int k = k0; k < 4; ++k) {
+        const int task = tid + kThreads * k;
+        const int frag = (task >> 6) & 15;
+        const int fi = task & 15, fg = (task >> 4) & 3;
+        if (k < 2) {  // Q~ = exp(lg) q : fragment (I, s), lane (i, g)
+          const int I = frag >> 2, c0 = 32 * (frag & 3) + 4 * fg;
+          const bf16* row = nat_row(sm, kOffQA, 16 * I + fi);
+          lo[k] = *reinterpret_cast<const bf16x4_t*>(row + c0);
+          hi[k] = *reinterpret_cast<const bf16x4_t*>(row + c0 + 16);
+          slo[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0]);
+          shi[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
+        } else {  // K~^T : fragment (ct, s'), lane (c, g); rows r0.. and r0 + 16.. each sit in one block
+          const int ch = 16 * (frag >> 1) + fi, r0 = 32 * (frag & 1) + 4 * fg;
+          lo[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0]);
+          hi[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0 + 16]);
+          slo[k][0] = Ge[r0 >> 4][ch];
+          shi[k][0] = Ge[(r0 + 16) >> 4][ch];
+        }
       }
       __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        bf16x8_t af;
-#pragma unroll
+  #pragma unroll
+      for (int k = k0; k < 4; ++k) {
+        const int task = tid + kThreads * k;
+        bf16x8_t o;
+  #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          af[e] = (bf16)((float)ke[u][e] * sc0[u][e]);
-          af[4 + e] = (bf16)((float)ke[u][4 + e] * sc1[u][e]);
+          o[e] = (bf16)((float)lo[k][e] * (k < 2 ? slo[k][e] : slo[k][0]));
+          o[4 + e] = (bf16)((float)hi[k][e] * (k < 2 ? shi[k][e] : shi[k][0]));
         }
-        akk = mfma32(af, kb[u], akk);
-        if constexpr (MODE == kOutput) aqk = mfma32(af, qb[u], aqk);
+        *lds<bf16x8_t>(sm, (k < 2 ? kOffQf : kOffKTf) + (task & 1023) * 16) = o;
       }
     }
-    // lane (n16, g4) holds A[16I + n16][16J + 4 g4 + r] (and likewise Aqk)
-    bf16x4_t lrow;
-    bf16x4_t qrow;
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int j = 16 * J + 4 * g4 + r;
-      const float vk = (j < i) ? akk[r] * bi : 0.f;
-      lrow[r] = (bf16)vk;
-      qrow[r] = (bf16)((j <= i) ? aqk[r] : 0.f);
-      if (I == J) Ld[I][n16][4 * g4 + r] = vk;
+  
+    if constexpr (LOADER) nl.template load_part<2>();
+    // ---- P2: A (strict) and Aqk (causal) 16x16 blocks on MFMA ---------------
+    for (int p = wave; p < 10; p += 8) {
+      // block pair p = I (I + 1) / 2 + J, J <= I
+      const int I = p >= 6 ? 3 : (p >= 3 ? 2 : (p >= 1 ? 1 : 0));
+      const int J = p - I * (I + 1) / 2;
+      // the operands of two reduction steps at a time (two LDS round trips per pair)
+      const bf16* ke_row = nat_row(sm, kOffKE, 16 * J + n16);
+      const bf16* ka_row = nat_row(sm, kOffKA, 16 * I + n16);
+      const bf16* qa_row = nat_row(sm, kOffQA, 16 * I + n16);
+      const int i = 16 * I + n16;
+      const float bi = betas[i];
+      f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        bf16x8_t ke[2], kb[2], qb[2];
+        f32x4_t sc0[2], sc1[2];
+  #pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int c0 = 32 * (2 * half + u) + 8 * g4;
+          ke[u] = *reinterpret_cast<const bf16x8_t*>(ke_row + c0);
+          sc0[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0]);
+          sc1[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0 + 4]);
+          kb[u] = *reinterpret_cast<const bf16x8_t*>(ka_row + c0);
+          if constexpr (MODE == kOutput) qb[u] = *reinterpret_cast<const bf16x8_t*>(qa_row + c0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          bf16x8_t af;
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            af[e] = (bf16)((float)ke[u][e] * sc0[u][e]);
+            af[4 + e] = (bf16)((float)ke[u][4 + e] * sc1[u][e]);
+          }
+          akk = mfma32(af, kb[u], akk);
+          if constexpr (MODE == kOutput) aqk = mfma32(af, qb[u], aqk);
+        }
+      }
+      // lane (n16, g4) holds A[16I + n16][16J + 4 g4 + r] (and likewise Aqk)
+      bf16x4_t lrow;
+      bf16x4_t qrow;
+  #pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * J + 4 * g4 + r;
+        const float vk = (j < i) ? akk[r] * bi : 0.f;
+        lrow[r] = (bf16)vk;
+        qrow[r] = (bf16)((j <= i) ? aqk[r] : 0.f);
+        if (I == J) Ld[I][n16][4 * g4 + r] = vk;
+      }
+      *reinterpret_cast<bf16x4_t*>(&Lm[i][16 * J + 4 * g4]) = lrow;
+      if constexpr (MODE == kOutput) {
+        unsigned char* afrag = sm + kOffAf + ((I * 2 + J / 2) * 64 + lane) * 16;
+        *reinterpret_cast<bf16x4_t*>(afrag + (J & 1) * 8) = qrow;
+        if (I == J && (I & 1) == 0) *reinterpret_cast<bf16x4_t*>(afrag + 8) = bf16x4_t{};  // tile J = I+1 is above
+      }
     }
-    *reinterpret_cast<bf16x4_t*>(&Lm[i][16 * J + 4 * g4]) = lrow;
-    if constexpr (MODE == kOutput) {
-      unsigned char* afrag = sm + kOffAf + ((I * 2 + J / 2) * 64 + lane) * 16;
-      *reinterpret_cast<bf16x4_t*>(afrag + (J & 1) * 8) = qrow;
-      if (I == J && (I & 1) == 0) *reinterpret_cast<bf16x4_t*>(afrag + 8) = bf16x4_t{};  // tile J = I+1 is above
+  } else {
+    // phase A: the scanners take all ten block pairs of P2 (no Aqk), each
+    // loader wave exports K~^T and -Kgamma for its own 32 channels
+    // Element e of lane (i, g) of an A fragment s covers index 32 s + 4 g + e
+    // (e < 4) and 32 s + 16 + 4 g + e - 4: two runs of four, one 8-byte LDS read
+    // each.  Every task's reads go out before any is used.
+    if (wave < 4) {
+      // ---- scanners: A (strict) and Aqk (causal) 16x16 block pairs on MFMA -----
+      for (int p = wave; p < 10; p += 4) {
+        // block pair p = I (I + 1) / 2 + J, J <= I
+        const int I = p >= 6 ? 3 : (p >= 3 ? 2 : (p >= 1 ? 1 : 0));
+        const int J = p - I * (I + 1) / 2;
+        // the operands of two reduction steps at a time (two LDS round trips per pair)
+        const bf16* ke_row = nat_row(sm, kOffKE, 16 * J + n16);
+        const bf16* ka_row = nat_row(sm, kOffKA, 16 * I + n16);
+        const bf16* qa_row = nat_row(sm, kOffQA, 16 * I + n16);
+        const int i = 16 * I + n16;
+        const float bi = betas[i];
+        f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
+        f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
+  #pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          bf16x8_t ke[2], kb[2], qb[2];
+          f32x4_t sc0[2], sc1[2];
+  #pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            const int c0 = 32 * (2 * half + u) + 8 * g4;
+            ke[u] = *reinterpret_cast<const bf16x8_t*>(ke_row + c0);
+            sc0[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0]);
+            sc1[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0 + 4]);
+            kb[u] = *reinterpret_cast<const bf16x8_t*>(ka_row + c0);
+            if constexpr (MODE == kOutput) qb[u] = *reinterpret_cast<const bf16x8_t*>(qa_row + c0);
+          }
+          __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+          for (int u = 0; u < 2; ++u) {
+            bf16x8_t af;
+  #pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              af[e] = (bf16)((float)ke[u][e] * sc0[u][e]);
+              af[4 + e] = (bf16)((float)ke[u][4 + e] * sc1[u][e]);
+            }
+            akk = mfma32(af, kb[u], akk);
+            if constexpr (MODE == kOutput) aqk = mfma32(af, qb[u], aqk);
+          }
+        }
+        // lane (n16, g4) holds A[16I + n16][16J + 4 g4 + r] (and likewise Aqk)
+        bf16x4_t lrow;
+        bf16x4_t qrow;
+  #pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int j = 16 * J + 4 * g4 + r;
+          const float vk = (j < i) ? akk[r] * bi : 0.f;
+          lrow[r] = (bf16)vk;
+          qrow[r] = (bf16)((j <= i) ? aqk[r] : 0.f);
+          if (I == J) Ld[I][n16][4 * g4 + r] = vk;
+        }
+        *reinterpret_cast<bf16x4_t*>(&Lm[i][16 * J + 4 * g4]) = lrow;
+        if constexpr (MODE == kOutput) {
+          unsigned char* afrag = sm + kOffAf + ((I * 2 + J / 2) * 64 + lane) * 16;
+          *reinterpret_cast<bf16x4_t*>(afrag + (J & 1) * 8) = qrow;
+          if (I == J && (I & 1) == 0) *reinterpret_cast<bf16x4_t*>(afrag + 8) = bf16x4_t{};  // tile J = I+1 is above
+        }
+      }
+    } else {
+      // ---- loader wave w' = wave - 4 owns channels 32 w' .. 32 w' + 31: their
+      // K~^T fragments (ct = 2 w', 2 w' + 1) from the channel-major k E rows,
+      // then the -Kgamma fragments (I, s = w') written over those same rows
+      const int wl = wave - 4;
+      {
+        bf16x4_t lo[4], hi[4];
+        float elo[4], ehi[4];
+  #pragma unroll
+        for (int k = 0; k < 4; ++k) {  // fragment (ct, s') = (2 w' + k / 2, k % 2), lane (c, g)
+          const int ch = 32 * wl + 16 * (k >> 1) + n16, r0 = 32 * (k & 1) + 4 * g4;
+          lo[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0]);
+          hi[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0 + 16]);
+          elo[k] = Ge[r0 >> 4][ch];  // rows r0 .. r0 + 3 sit in one block, as do r0 + 16 ..
+          ehi[k] = Ge[(r0 + 16) >> 4][ch];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+        for (int k = 0; k < 4; ++k) {
+          bf16x8_t o;
+  #pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[e] = (bf16)((float)lo[k][e] * elo[k]);
+            o[4 + e] = (bf16)((float)hi[k][e] * ehi[k]);
+          }
+          *lds<bf16x8_t>(sm, kOffKTf + ((4 * wl + k) * 64 + lane) * 16) = o;  // fragment 2 ct + s'
+        }
+      }
+      if constexpr (LOADER) nl.template load_part<2>();
+      // -Kgamma = -exp(lg) k fragments (I, s = w'), lane (i, g), over this
+      // wave's own channel-major rows (read above, in order before these writes)
+      {
+        bf16x4_t lo[4], hi[4];
+        f32x4_t glo[4], ghi[4];
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          const int c0 = 32 * wl + 4 * g4;
+          const bf16* row = nat_row(sm, kOffKA, 16 * I + n16);
+          lo[I] = *reinterpret_cast<const bf16x4_t*>(row + c0);
+          hi[I] = *reinterpret_cast<const bf16x4_t*>(row + c0 + 16);
+          glo[I] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0]);
+          ghi[I] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int I = 0; I < 4; ++I) {
+          bf16x8_t o;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            o[e] = (bf16)(-(float)lo[I][e] * glo[I][e]);
+            o[4 + e] = (bf16)(-(float)hi[I][e] * ghi[I][e]);
+          }
+          *lds<bf16x8_t>(sm, kgf_off<MODE>(I, wl) + lane * 16) = o;
+        }
+      }
     }
   }
   if constexpr (LOADER) nl.template load_part<3>();
@@ -799,7 +933,8 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
 
   if constexpr (LOADER) nl.template load_part<5>();
   // ---- P3: inverses T_I of the four unit-lower diagonal blocks (f32), waves
-  // 0-3; meanwhile waves 4-7 export Kgamma = exp(lg) k over the dead q a tile
+  // 0-3; meanwhile (phase C) waves 4-7 export Kgamma = exp(lg) k over the dead
+  // q a tile
   if (wave < 4) {
     if (lane < 16) {
       // column `lane` of T_I, row by row.  Row r + 1 of L is read while row r
@@ -844,31 +979,33 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
       *reinterpret_cast<bf16x8_t*>(&TinvT[I][lane][8]) = t1;
     }
   } else {
-    // -Kgamma : fragment (I, s), lane (i, g); tasks tid - 256 + 256 k, reads first
+    // phase C: -Kgamma : fragment (I, s), lane (i, g); tasks tid - 256 + 256 k, reads first
+    if constexpr (MODE == kOutput) {
     bf16x4_t lo[4], hi[4];
-    f32x4_t glo[4], ghi[4];
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int task = tid - 256 + 256 * k;
-      const int frag = task >> 6;
-      const int fi = task & 15, fg = (task >> 4) & 3;
-      const int I = frag >> 2, c0 = 32 * (frag & 3) + 4 * fg;
-      const bf16* row = nat_row(sm, kOffKA, 16 * I + fi);
-      lo[k] = *reinterpret_cast<const bf16x4_t*>(row + c0);
-      hi[k] = *reinterpret_cast<const bf16x4_t*>(row + c0 + 16);
-      glo[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0]);
-      ghi[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
-    }
-    __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      bf16x8_t o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[e] = (bf16)(-(float)lo[k][e] * glo[k][e]);
-        o[4 + e] = (bf16)(-(float)hi[k][e] * ghi[k][e]);
+      f32x4_t glo[4], ghi[4];
+  #pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        const int task = tid - 256 + 256 * k;
+        const int frag = task >> 6;
+        const int fi = task & 15, fg = (task >> 4) & 3;
+        const int I = frag >> 2, c0 = 32 * (frag & 3) + 4 * fg;
+        const bf16* row = nat_row(sm, kOffKA, 16 * I + fi);
+        lo[k] = *reinterpret_cast<const bf16x4_t*>(row + c0);
+        hi[k] = *reinterpret_cast<const bf16x4_t*>(row + c0 + 16);
+        glo[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0]);
+        ghi[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
       }
-      *lds<bf16x8_t>(sm, kOffKgf + (tid - 256 + 256 * k) * 16) = o;
+      __builtin_amdgcn_sched_barrier(0);
+  #pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        bf16x8_t o;
+  #pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[e] = (bf16)(-(float)lo[k][e] * glo[k][e]);
+          o[4 + e] = (bf16)(-(float)hi[k][e] * ghi[k][e]);
+        }
+        *lds<bf16x8_t>(sm, kgf_off<MODE>(0, 0) + (tid - 256 + 256 * k) * 16) = o;
+      }
     }
     if constexpr (LOADER) nl.template load_part<6>();
   }
@@ -930,7 +1067,7 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
   auto load_step = [&](int st, bf16x8_t (&kf)[4], bf16x8_t (&qf)[4]) {
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      kf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kOffKgf + ((I * 4 + st) * 64 + lane) * 16);
+      kf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kgf_off<MODE>(I, st) + lane * 16);
       if constexpr (MODE == kOutput)
         qf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kOffQf + ((I * 4 + st) * 64 + lane) * 16);
     }
@@ -1260,7 +1397,11 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
 // One workgroup of 8 waves per (sequence, head, 16-column tile); wave ct owns
 // output row tile ct.  The state moves between waves as bf16 B-operand
 // halves through LDS (double-buffered, one barrier per segment); P_g and
-// Q_g of the next kCombineDepth segments are in flight in registers.
+// Q_g of the next kCombineDepth segments are in flight in registers.  The
+// step loop is unrolled by kCombineDepth with every load unconditional (the
+// segment index clamped) and the last group padded with steps whose results
+// are dropped, so each register set is reloaded at one fixed place and the
+// waits for a step's operands cover only that step's loads.
 constexpr int kCombineDepth = 4;
 
 struct CombineArgs {
@@ -1280,38 +1421,37 @@ __global__ __launch_bounds__(512) void segment_combine_kernel(const CombineArgs 
   const int64_t g0 = seg_start_of(a, s);
   const int64_t nseg = seg_start_of(a, s + 1) - g0;
   if (nseg <= 2) return;  // phase A already produced every start state
-  const int64_t last = nseg - 2;  // steps lg = 1..last produce the start state of segment lg + 1
+  const int last = static_cast<int>(nseg - 2);  // steps lg = 1..last produce the start state of segment lg + 1
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int ct = wave_of(tid);
-  const int64_t tstride = seg_state_floats(a.V);
-  auto state_ptr = [&](float* base, int64_t seg) { return base + (seg * a.H + h) * tstride + (tile * 8 + ct) * 256 + lane * 4; };
-  auto p_ptr = [&](int64_t seg, int st) {
-    return a.seg_p + (seg * a.H + h) * seg_p_elems() + ((ct * 4 + st) * 64 + lane) * 8;
-  };
+  // this lane's element of segment g0 + g: base + g * stride
+  const int64_t st_stride = a.H * seg_state_floats(a.V);
+  const int64_t p_stride = a.H * seg_p_elems();
+  const float* q_base = a.seg_q + (g0 * a.H + h) * seg_state_floats(a.V) + (tile * 8 + ct) * 256 + lane * 4;
+  float* s_base = a.seg_state + (g0 * a.H + h) * seg_state_floats(a.V) + (tile * 8 + ct) * 256 + lane * 4;
+  const bf16* p_base = a.seg_p + (g0 * a.H + h) * seg_p_elems() + (ct * 4 * 64 + lane) * 8;
 
   bf16x8_t Pf[kCombineDepth][4];
   f32x4_t Qv[kCombineDepth];
+  auto load_step = [&](int d, int lg) {
+    const int g = lg < last ? lg : last;
 #pragma unroll
-  for (int d = 0; d < kCombineDepth; ++d) {
-    const int64_t lg = 1 + d;
-    if (lg <= last) {
+    for (int st = 0; st < 4; ++st) Pf[d][st] = *reinterpret_cast<const bf16x8_t*>(p_base + g * p_stride + st * 64 * 8);
+    Qv[d] = *reinterpret_cast<const f32x4_t*>(q_base + g * st_stride);
+  };
 #pragma unroll
-      for (int st = 0; st < 4; ++st) Pf[d][st] = *reinterpret_cast<const bf16x8_t*>(p_ptr(g0 + lg, st));
-      Qv[d] = *reinterpret_cast<const f32x4_t*>(state_ptr(const_cast<float*>(a.seg_q), g0 + lg));
-    }
-  }
+  for (int d = 0; d < kCombineDepth; ++d) load_step(d, 1 + d);
   {
-    const f32x4_t x = *reinterpret_cast<const f32x4_t*>(state_ptr(a.seg_state, g0 + 1));
+    const f32x4_t x = *reinterpret_cast<const f32x4_t*>(s_base + st_stride);
     Sh[0][ct][lane] = bf16x4_t{(bf16)x[0], (bf16)x[1], (bf16)x[2], (bf16)x[3]};
   }
   __syncthreads();
-  for (int64_t lg0 = 1; lg0 <= last; lg0 += kCombineDepth) {
+  for (int lg0 = 1; lg0 <= last; lg0 += kCombineDepth) {
 #pragma unroll
     for (int d = 0; d < kCombineDepth; ++d) {
-      const int64_t lg = lg0 + d;
-      if (lg > last) break;
-      const int buf = static_cast<int>((lg - 1) & 1);
+      const int lg = lg0 + d;
+      const int buf = (lg - 1) & 1;
       f32x4_t acc = Qv[d];
 #pragma unroll
       for (int st = 0; st < 4; ++st) {
@@ -1320,13 +1460,8 @@ __global__ __launch_bounds__(512) void segment_combine_kernel(const CombineArgs 
         const bf16x8_t sb = bf16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         acc = mfma32(Pf[d][st], sb, acc);
       }
-      const int64_t nx = lg + kCombineDepth;
-      if (nx <= last) {
-#pragma unroll
-        for (int st = 0; st < 4; ++st) Pf[d][st] = *reinterpret_cast<const bf16x8_t*>(p_ptr(g0 + nx, st));
-        Qv[d] = *reinterpret_cast<const f32x4_t*>(state_ptr(const_cast<float*>(a.seg_q), g0 + nx));
-      }
-      *reinterpret_cast<f32x4_t*>(state_ptr(a.seg_state, g0 + lg + 1)) = acc;
+      load_step(d, lg + kCombineDepth);
+      if (lg <= last) *reinterpret_cast<f32x4_t*>(s_base + (lg + 1) * st_stride) = acc;
       Sh[buf ^ 1][ct][lane] = bf16x4_t{(bf16)acc[0], (bf16)acc[1], (bf16)acc[2], (bf16)acc[3]};
       __syncthreads();
     }
