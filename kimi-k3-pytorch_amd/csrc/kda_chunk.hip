@@ -70,8 +70,18 @@ constexpr int kThreads = 512;   // 8 waves
 constexpr float kExtremeDecay = 7.888609052210118e-31f;  // 2^-100
 constexpr int32_t kOneSegment = 0x3fffffff;              // L: every sequence is one segment
 
-constexpr int kSummary = 0;  // phase A
-constexpr int kOutput = 1;   // phase C
+constexpr int kSummary = 0;   // phase A: segment summaries, and each chunk's M and Aqk
+constexpr int kOutput = 1;    // phase C preparing every chunk itself (sequences of one segment)
+constexpr int kOutputMA = 2;  // phase C reading each chunk's M and Aqk written by phase A
+template <int MODE>
+inline constexpr bool kWritesOut = MODE != kSummary;  // outputs, Q~, start states from phase B
+template <int MODE>
+inline constexpr bool kPrepares = MODE != kOutputMA;  // P2, the diagonal-block inverses and M in the loop
+// M and Aqk of one (chunk, head) in the workspace: the six lower-triangular
+// 64 x 64 A fragments of each, [M | Aqk][j = 0..5][lane][8] bf16 (j -> slot
+// j < 2 ? 2 j : j + 2 of the [I][s'] fragment layout)
+constexpr int64_t kMaBytes = 12 * 1024;
+__host__ __device__ constexpr int lower_slot(int j) { return j < 2 ? 2 * j : j + 2; }
 
 // ---- LDS map of chunk_segment_kernel (bytes) ------------------------------
 // Natural bf16 tiles use a padded row of 136 elements; the k a, q a and k E
@@ -100,19 +110,30 @@ constexpr int kRowT = 72;                           // padded row of the channel
 constexpr int kOffKEt = kOffFlag + 16;              // bf16 [128][72] k_j E_j, channel-major
 constexpr int kSmemBytes = kOffKEt + kKey * kRowT * 2;
 // -Kgamma = -exp(lg) k A fragments, 1 KB each (64 lanes x 8 bf16), fragment
-// (I, s) at kgf_off<MODE>(I, s): in phase C [I][s] over the q a tile, which is
-// dead after P2; in phase A [s][I] with block s over the channel-major k E
-// rows of channels 32 s .. 32 s + 31, which the loader wave that owns those
-// channels has finished reading when it writes block s.
+// (I, s) at kgf_off<MODE>(I, s): in phase C with P2 [I][s] over the q a tile,
+// which is dead after P2; in phase C without P2 [I][s] over the k E tile; in
+// phase A [s][I] with block s over the channel-major k E rows of channels
+// 32 s .. 32 s + 31, which the loader wave that owns those channels has
+// finished reading when it writes block s.
 constexpr int kKgfStride = 32 * kRowT * 2;  // 4608
 template <int MODE>
 __host__ __device__ constexpr int kgf_off(int I, int s) {
-  return MODE == kOutput ? kOffQA + (I * 4 + s) * 1024 : kOffKEt + s * kKgfStride + I * 1024;
+  return MODE == kOutput     ? kOffQA + (I * 4 + s) * 1024
+         : MODE == kOutputMA ? kOffKE + (I * 4 + s) * 1024  // k E tile, unused without P2
+                             : kOffKEt + s * kKgfStride + I * 1024;
 }
-constexpr int kOffMf = kOffKE;     // M = (I + diag(beta) A)^-1 diag(beta) A fragments [I=4][s=2][lane][8]
+// M = (I + diag(beta) A)^-1 diag(beta) A fragments [I=4][s=2][lane][8]: over
+// the k E tile (dead after P2) when M is formed in the loop, over the L tile
+// (unused) when it comes from phase A
+template <int MODE>
+__host__ __device__ constexpr int mf_off() {
+  return MODE == kOutputMA ? kOffL : kOffKE;
+}
 constexpr int kOffStage = kOffKA;  // output transpose [4 waves][64][32]
 constexpr int kOffPnat = kOffKA;   // phase A: P_g natural bf16 [128][136]
 static_assert(kSmemBytes <= 160 * 1024, "chunk_segment_kernel LDS exceeds one CU");
+static_assert(kChunk * 72 * 2 >= 8192, "M fragments must fit in the L tile");
+static_assert(mf_off<kSummary>() == kOffKE && mf_off<kOutput>() == kOffKE, "m_block_row writes M over the k E tile");
 static_assert(kOffKEt % 16 == 0 && kOffGs % 16 == 0 && kOffGe % 16 == 0, "16-byte LDS accesses need aligned tiles");
 static_assert(4 * 64 * 32 * 2 <= kNat, "output stage must fit in the k a tile");
 static_assert(kKey * kRow * 2 <= 2 * kNat, "P transpose must fit in the k a and q a tiles");
@@ -246,6 +267,7 @@ struct SegArgs {
   float* seg_state;
   float* seg_q;
   bf16* seg_p;
+  bf16* chunk_ma;  // [chunk][h] M and Aqk fragments (kMaBytes), or nullptr
   int64_t N, H, V;
   int32_t L;
 };
@@ -297,6 +319,7 @@ struct Raw {
   pair_t gp[16], kp[16], qp[16];
   uint4 vv[4];
   IT bt;
+  uint4 ma[3];  // M and Aqk units t2, t2 + 256, t2 + 512 (phase C without P2)
 };
 
 // Raw buffer resource over `bytes` bytes from `base` (dword 3 is the gfx9
@@ -310,24 +333,29 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_rsrc(const void* base, 
 // chunk's valid tokens (rows past them read as zero), built once per chunk in
 // scalar registers; every load then needs only a lane offset.
 struct ChunkLoads {
-  __amdgpu_buffer_rsrc_t g, k, q, v, beta;
+  __amdgpu_buffer_rsrc_t g, k, q, v, beta, ma;
   int krow;  // bytes per token of q, k, g
 };
 
+// `active` false gives resources of zero size: every load returns zero and
+// reads no memory, so the loads need no branch around them.
 template <class IT>
-__device__ __forceinline__ ChunkLoads chunk_loads(const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h, int64_t col0) {
+__device__ __forceinline__ ChunkLoads chunk_loads(const SegArgs<IT>& a, const ChunkGeo& cg, int64_t c, int64_t h,
+                                                  int64_t col0, bool active = true) {
   constexpr int64_t kEl = sizeof(IT);
   ChunkLoads cl;
   cl.krow = static_cast<int>(a.H * kKey * kEl);
+  const int64_t nv = active ? cg.n_valid : 0;
   const int64_t kb = (cg.tok0 * a.H + h) * kKey * kEl;
-  const int64_t kbytes = static_cast<int64_t>(cg.n_valid) * cl.krow;
+  const int64_t kbytes = nv * cl.krow;
   cl.g = buffer_rsrc(reinterpret_cast<const char*>(a.g) + kb, kbytes);
   cl.k = buffer_rsrc(reinterpret_cast<const char*>(a.k) + kb, kbytes);
   cl.q = buffer_rsrc(reinterpret_cast<const char*>(a.q) + kb, kbytes);
   cl.v = buffer_rsrc(reinterpret_cast<const char*>(a.v) + ((cg.tok0 * a.H + h) * a.V + col0) * kEl,
-                     static_cast<int64_t>(cg.n_valid) * a.H * a.V * kEl);
-  cl.beta = buffer_rsrc(reinterpret_cast<const char*>(a.beta) + (cg.tok0 * a.H + h) * kEl,
-                        static_cast<int64_t>(cg.n_valid) * a.H * kEl);
+                     nv * a.H * a.V * kEl);
+  cl.beta = buffer_rsrc(reinterpret_cast<const char*>(a.beta) + (cg.tok0 * a.H + h) * kEl, nv * a.H * kEl);
+  cl.ma = buffer_rsrc(a.chunk_ma ? reinterpret_cast<const char*>(a.chunk_ma) + (c * a.H + h) * kMaBytes : nullptr,
+                      (a.chunk_ma && active) ? kMaBytes : 0);
   return cl;
 }
 
@@ -357,8 +385,9 @@ __device__ __forceinline__ LoaderLanes loader_lanes(const SegArgs<IT>& a, int vc
 }
 
 // Part PART (0..7) of the loads of one chunk's raw inputs: rows 2 PART and
-// 2 PART + 1 of g, k (and q) of this thread's block, one 16-byte v unit on
-// even parts and beta on the last.  Spreading the eight parts over a chunk's
+// 2 PART + 1 of g, k and q of this thread's block, one 16-byte v unit on
+// even parts, beta on the last and, in phase C without P2, one 16-byte unit
+// of the chunk's M and Aqk fragments on parts 5-7.  Spreading the eight parts over a chunk's
 // phases keeps any single moment's burst of requests small: issued at once,
 // every CU's 64 KB would saturate HBM and stall the issuing waves.
 template <class IT, int MODE, int PART>
@@ -371,9 +400,11 @@ __device__ __forceinline__ void load_raw_part(Raw<IT>& raw, const ChunkLoads& cl
     const int off = (16 * J + r) * cl.krow + 4 * cp;
     raw.gp[r] = __builtin_bit_cast(pair_t, __builtin_amdgcn_raw_buffer_load_b32(cl.g, off, 0, 0));
     raw.kp[r] = __builtin_bit_cast(pair_t, __builtin_amdgcn_raw_buffer_load_b32(cl.k, off, 0, 0));
-    if constexpr (MODE == kOutput)
-      raw.qp[r] = __builtin_bit_cast(pair_t, __builtin_amdgcn_raw_buffer_load_b32(cl.q, off, 0, 0));
+    raw.qp[r] = __builtin_bit_cast(pair_t, __builtin_amdgcn_raw_buffer_load_b32(cl.q, off, 0, 0));
   }
+  if constexpr (MODE == kOutputMA && PART >= 5)
+    raw.ma[PART - 5] = __builtin_bit_cast(
+        uint4, __builtin_amdgcn_raw_buffer_load_b128(cl.ma, ((tid - 256) + 256 * (PART - 5)) * 16, 0, 0));
   if constexpr ((PART & 1) == 0) {
     const int i = PART / 2;
     if (ll.v[i] >= 0) raw.vv[i] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(cl.v, ll.v[i], 0, 0));
@@ -396,17 +427,19 @@ __device__ __forceinline__ void load_raw(Raw<IT>& raw, const ChunkLoads& cl, con
 }
 
 // Where the loader waves are in a chunk's phases, for the spread loads of
-// the next chunk: `load_part<P>()` issues part P if there is one.
+// the next chunk: `load_part<P>()` issues part P (of zero-size resources past
+// the segment's last chunk).  The loads carry no branch: a conditional load
+// leaves its registers possibly pending on the other path, and the waits the
+// compiler then places before reusing registers stall every later part.
 template <class IT, int MODE>
 struct NextLoads {
   Raw<IT>* raw;
   ChunkLoads cl;
   const LoaderLanes* ll;
   int tid;
-  bool active;
   template <int P>
   __device__ __forceinline__ void load_part() const {
-    if (active) load_raw_part<IT, MODE, P>(*raw, cl, *ll, tid);
+    load_raw_part<IT, MODE, P>(*raw, cl, *ll, tid);
   }
 };
 
@@ -424,7 +457,7 @@ __device__ __forceinline__ void m_block_row(unsigned char* sm, int lane) {
   bf16(*Tinv)[16][16] = lds<bf16[16][16]>(sm, kOffTinv);
   bf16(*TinvT)[16][16] = lds<bf16[16][16]>(sm, kOffTinvT);
   const float* betas = lds<float>(sm, kOffBeta);
-  unsigned char* mf = sm + kOffMf;
+  unsigned char* mf = sm + kOffKE;  // where the modes that form M keep it
   // every operand of the chain first (one LDS round trip):
   //   bt[J][K - J - 1] = B_KJ^T (lane (j, g) holds B[16K + 4g + r][16J + j]),
   //   ta[J] = -T_J^T (lane (j, g) holds T_J[4g + r][j]), b4[J] = beta of block J
@@ -483,6 +516,7 @@ struct P1Out {
   int ext;                          // some block of the wave's channels decays past 2^-100
   uint4 vv[4];                      // bf16 v units of this thread (zero past the valid rows)
   float bt;                         // beta of row t2 (< 64), zero past the valid rows
+  uint4 ma[3];                      // M and Aqk units (phase C without P2)
 };
 
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
@@ -509,10 +543,10 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
     for (int ch = 0; ch < 2; ++ch) {
       if (r > 0) run[ch] *= al[ch][r];
       kv[ch] = ok ? to_float(raw.kp[r][ch]) : 0.f;
-      qv[ch] = (MODE == kOutput && ok) ? to_float(raw.qp[r][ch]) : 0.f;
+      qv[ch] = ok ? to_float(raw.qp[r][ch]) : 0.f;
     }
     po.ka[r] = pack_bf16x2(kv[0] * run[0], kv[1] * run[1]);
-    if constexpr (MODE == kOutput) po.qa[r] = pack_bf16x2(qv[0] * run[0], qv[1] * run[1]);
+    po.qa[r] = pack_bf16x2(qv[0] * run[0], qv[1] * run[1]);
   }
   float suf[2] = {1.f, 1.f};
 #pragma unroll
@@ -574,6 +608,10 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
     po.vv[i] = val;
   }
   po.bt = (t2 < kChunk && t2 < n_valid) ? to_float(raw.bt) : 0.f;
+  if constexpr (MODE == kOutputMA) {
+#pragma unroll
+    for (int k = 0; k < 3; ++k) po.ma[k] = raw.ma[k];
+  }
 }
 
 // Writes P1 (loader waves) and joins every wave at the first barrier of the
@@ -593,8 +631,8 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
     for (int r = 0; r < 16; ++r) {
       const int tl = 16 * J + r;
       *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKA, tl) + 2 * cp) = po.ka[r];
-      if constexpr (MODE == kOutput) *reinterpret_cast<uint32_t*>(nat_row(sm, kOffQA, tl) + 2 * cp) = po.qa[r];
-      *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKE, tl) + 2 * cp) = po.ke[r];
+      *reinterpret_cast<uint32_t*>(nat_row(sm, kOffQA, tl) + 2 * cp) = po.qa[r];
+      if constexpr (kPrepares<MODE>) *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKE, tl) + 2 * cp) = po.ke[r];
     }
     // channel-major k E: rows 16 J .. 16 J + 15 of channels 2 cp, 2 cp + 1
 #pragma unroll
@@ -623,6 +661,14 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
       if (ll->vlds[i] >= 0) *reinterpret_cast<uint4*>(sm + kOffVn + ll->vlds[i]) = po.vv[i];
     const int t2 = tid - 256;
     if (t2 < kChunk) betas[t2] = po.bt;
+    if constexpr (MODE == kOutputMA) {
+#pragma unroll
+      for (int k = 0; k < 3; ++k) {
+        const int u = t2 + 256 * k;  // [M | Aqk][j][lane]
+        const int slot = lower_slot((u >> 6) % 6);
+        *reinterpret_cast<uint4*>(sm + (u < 384 ? mf_off<MODE>() : kOffAf) + (slot * 64 + (u & 63)) * 16) = po.ma[k];
+      }
+    }
   }
   __syncthreads();
 }
@@ -647,6 +693,67 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
   float(*Ge)[kKey] = lds<float[kKey]>(sm, kOffGe);
   float* betas = lds<float>(sm, kOffBeta);
   const int* flags = lds<int>(sm, kOffFlag);
+
+  if constexpr (MODE == kOutputMA) {
+    // phase C with M and Aqk from phase A: only the three fragment exports,
+    // tasks tid + 512 k: Q~ (k = 0, 1), K~^T (k = 2, 3), -Kgamma (k = 4, 5).
+    // Element e of lane (i, g) of an A fragment s covers index 32 s + 4 g + e
+    // (e < 4) and 32 s + 16 + 4 g + e - 4: two runs of four, one 8-byte read
+    // each; every task's reads go out before any is used.
+    if constexpr (LOADER) {
+      nl.template load_part<0>();
+      nl.template load_part<1>();
+      nl.template load_part<2>();
+    }
+    bf16x4_t lo[6], hi[6];
+    f32x4_t slo[6], shi[6];
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const int task = tid + kThreads * k;
+      const int frag = (task >> 6) & 15;
+      const int fi = task & 15, fg = (task >> 4) & 3;
+      if (k < 2 || k >= 4) {  // exp(lg) q or exp(lg) k : fragment (I, s), lane (i, g)
+        const int I = frag >> 2, c0 = 32 * (frag & 3) + 4 * fg;
+        const bf16* row = nat_row(sm, k < 2 ? kOffQA : kOffKA, 16 * I + fi);
+        lo[k] = *reinterpret_cast<const bf16x4_t*>(row + c0);
+        hi[k] = *reinterpret_cast<const bf16x4_t*>(row + c0 + 16);
+        slo[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0]);
+        shi[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
+      } else {  // K~^T : fragment (ct, s'), lane (c, g); rows r0.. and r0 + 16.. each sit in one block
+        const int ch = 16 * (frag >> 1) + fi, r0 = 32 * (frag & 1) + 4 * fg;
+        lo[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0]);
+        hi[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0 + 16]);
+        slo[k][0] = Ge[r0 >> 4][ch];
+        shi[k][0] = Ge[(r0 + 16) >> 4][ch];
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    if constexpr (LOADER) {
+      nl.template load_part<3>();
+      nl.template load_part<4>();
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k) {
+      const int task = tid + kThreads * k;
+      const bool per_ch = k < 2 || k >= 4;
+      const float sgn = k >= 4 ? -1.f : 1.f;
+      bf16x8_t o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        o[e] = (bf16)(sgn * (float)lo[k][e] * (per_ch ? slo[k][e] : slo[k][0]));
+        o[4 + e] = (bf16)(sgn * (float)hi[k][e] * (per_ch ? shi[k][e] : shi[k][0]));
+      }
+      const int dst = k < 2 ? kOffQf : (k < 4 ? kOffKTf : kgf_off<MODE>(0, 0));
+      *lds<bf16x8_t>(sm, dst + (task & 1023) * 16) = o;
+    }
+    if constexpr (LOADER) {
+      nl.template load_part<5>();
+      nl.template load_part<6>();
+      nl.template load_part<7>();
+    }
+    __syncthreads();
+    return;
+  }
 
   if constexpr (LOADER) {
     nl.template load_part<0>();
@@ -723,7 +830,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
           sc0[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0]);
           sc1[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0 + 4]);
           kb[u] = *reinterpret_cast<const bf16x8_t*>(ka_row + c0);
-          if constexpr (MODE == kOutput) qb[u] = *reinterpret_cast<const bf16x8_t*>(qa_row + c0);
+          qb[u] = *reinterpret_cast<const bf16x8_t*>(qa_row + c0);
         }
         __builtin_amdgcn_sched_barrier(0);
   #pragma unroll
@@ -735,7 +842,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
             af[4 + e] = (bf16)((float)ke[u][4 + e] * sc1[u][e]);
           }
           akk = mfma32(af, kb[u], akk);
-          if constexpr (MODE == kOutput) aqk = mfma32(af, qb[u], aqk);
+          aqk = mfma32(af, qb[u], aqk);
         }
       }
       // lane (n16, g4) holds A[16I + n16][16J + 4 g4 + r] (and likewise Aqk)
@@ -750,7 +857,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
         if (I == J) Ld[I][n16][4 * g4 + r] = vk;
       }
       *reinterpret_cast<bf16x4_t*>(&Lm[i][16 * J + 4 * g4]) = lrow;
-      if constexpr (MODE == kOutput) {
+      {
         unsigned char* afrag = sm + kOffAf + ((I * 2 + J / 2) * 64 + lane) * 16;
         *reinterpret_cast<bf16x4_t*>(afrag + (J & 1) * 8) = qrow;
         if (I == J && (I & 1) == 0) *reinterpret_cast<bf16x4_t*>(afrag + 8) = bf16x4_t{};  // tile J = I+1 is above
@@ -787,7 +894,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
             sc0[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0]);
             sc1[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0 + 4]);
             kb[u] = *reinterpret_cast<const bf16x8_t*>(ka_row + c0);
-            if constexpr (MODE == kOutput) qb[u] = *reinterpret_cast<const bf16x8_t*>(qa_row + c0);
+            qb[u] = *reinterpret_cast<const bf16x8_t*>(qa_row + c0);
           }
           __builtin_amdgcn_sched_barrier(0);
   #pragma unroll
@@ -799,7 +906,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
               af[4 + e] = (bf16)((float)ke[u][4 + e] * sc1[u][e]);
             }
             akk = mfma32(af, kb[u], akk);
-            if constexpr (MODE == kOutput) aqk = mfma32(af, qb[u], aqk);
+            aqk = mfma32(af, qb[u], aqk);
           }
         }
         // lane (n16, g4) holds A[16I + n16][16J + 4 g4 + r] (and likewise Aqk)
@@ -814,7 +921,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
           if (I == J) Ld[I][n16][4 * g4 + r] = vk;
         }
         *reinterpret_cast<bf16x4_t*>(&Lm[i][16 * J + 4 * g4]) = lrow;
-        if constexpr (MODE == kOutput) {
+        {
           unsigned char* afrag = sm + kOffAf + ((I * 2 + J / 2) * 64 + lane) * 16;
           *reinterpret_cast<bf16x4_t*>(afrag + (J & 1) * 8) = qrow;
           if (I == J && (I & 1) == 0) *reinterpret_cast<bf16x4_t*>(afrag + 8) = bf16x4_t{};  // tile J = I+1 is above
@@ -914,7 +1021,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
           const float e = fast_exp(Lr[i * kKey + cc] - Lr[j * kKey + cc]);
           const float kj = to_float(a.k[oj + cc]);
           acc_k += to_float(a.k[oi + cc]) * kj * e;
-          if constexpr (MODE == kOutput) acc_q += to_float(a.q[oi + cc]) * kj * e;
+          acc_q += to_float(a.q[oi + cc]) * kj * e;
         }
       }
       if (jl < il) {
@@ -922,7 +1029,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
         Lm[i][j] = (bf16)vk;
         Ld[I][il][jl] = vk;
       }
-      if constexpr (MODE == kOutput) {
+      {
         const int fl = il + 16 * (jl >> 2);
         bf16* afrag = reinterpret_cast<bf16*>(sm + kOffAf + ((I * 2 + I / 2) * 64 + fl) * 16);
         afrag[(I & 1) * 4 + (jl & 3)] = (bf16)acc_q;
@@ -981,9 +1088,9 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
   } else {
     // phase C: -Kgamma : fragment (I, s), lane (i, g); tasks tid - 256 + 256 k, reads first
     if constexpr (MODE == kOutput) {
-    bf16x4_t lo[4], hi[4];
+      bf16x4_t lo[4], hi[4];
       f32x4_t glo[4], ghi[4];
-  #pragma unroll
+#pragma unroll
       for (int k = 0; k < 4; ++k) {
         const int task = tid - 256 + 256 * k;
         const int frag = task >> 6;
@@ -996,10 +1103,10 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
         ghi[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
       }
       __builtin_amdgcn_sched_barrier(0);
-  #pragma unroll
+#pragma unroll
       for (int k = 0; k < 4; ++k) {
         bf16x8_t o;
-  #pragma unroll
+#pragma unroll
         for (int e = 0; e < 4; ++e) {
           o[e] = (bf16)(-(float)lo[k][e] * glo[k][e]);
           o[4 + e] = (bf16)(-(float)hi[k][e] * ghi[k][e]);
@@ -1023,6 +1130,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
 // ---- P4: M, block row I by wave I < 4 (the loader waves are free here) ------
 template <class IT, int MODE, bool LOADER>
 __device__ __forceinline__ void prepare_m(unsigned char* sm, int tid, const NextLoads<IT, MODE>& nl) {
+  if constexpr (!kPrepares<MODE>) return;  // M comes with the chunk's loads
   const int lane = tid & 63;
   const int wave = wave_of(tid);
   if constexpr (LOADER) nl.template load_part<7>();
@@ -1038,7 +1146,7 @@ __device__ __forceinline__ void prepare_m(unsigned char* sm, int tid, const Next
 
 // ---- per-chunk state advance of one wave's pair of 16-column tiles ----------
 // ut[t] >= 0: U tile index of tile t (value columns); -1: a transition column
-// (U = 0).  MODE == kOutput also forms O = Q~ S + Aqk V~ for both tiles.
+// (U = 0).  Phase C also forms O = Q~ S + Aqk V~ for both tiles.
 template <int MODE>
 __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[2][8], const int (&ut)[2], int lane,
                                           f32x4_t (&O)[2][4]) {
@@ -1057,7 +1165,7 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
       } else {
         Y[t][I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       }
-      if constexpr (MODE == kOutput) O[t][I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+      if constexpr (kWritesOut<MODE>) O[t][I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
   }
   // one reduction step at a time: the B operands of the step come from row
@@ -1068,7 +1176,7 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
       kf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kgf_off<MODE>(I, st) + lane * 16);
-      if constexpr (MODE == kOutput)
+      if constexpr (kWritesOut<MODE>)
         qf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kOffQf + ((I * 4 + st) * 64 + lane) * 16);
     }
   };
@@ -1097,7 +1205,7 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
     for (int I = 0; I < 4; ++I) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) Y[t][I] = mfma32(kf[I], sb[t], Y[t][I]);
-      if constexpr (MODE == kOutput) {
+      if constexpr (kWritesOut<MODE>) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) O[t][I] = mfma32(qf[I], sb[t], O[t][I]);
       }
@@ -1140,11 +1248,11 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
   for (int t = 0; t < 2; ++t)
 #pragma unroll
     for (int I = 0; I < 4; ++I) Vt[t][I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
-  lower_product(kOffMf, Yb, Vt);
+  lower_product(mf_off<MODE>(), Yb, Vt);
   bf16x8_t Vb[2][2];
   pack(Vt, Vb);
   // O += Aqk V~
-  if constexpr (MODE == kOutput) lower_product(kOffAf, Vb, O);
+  if constexpr (kWritesOut<MODE>) lower_product(kOffAf, Vb, O);
   // S <- diag(gamma) S + K~^T V~
   const float* gam = reinterpret_cast<const float*>(sm + kOffGam);
 #pragma unroll
@@ -1223,7 +1331,8 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
   const int64_t s = seq_of_segment(a, gsg);
   const int64_t lg = gsg - seg_start_of(a, s);
   const int64_t nseg = seg_start_of(a, s + 1) - seg_start_of(a, s);
-  if (MODE == kSummary && lg == nseg - 1) return;  // the last segment needs no summary
+  // the last segment needs no summary; phase A still prepares its chunks' M and Aqk
+  const bool scan_state = !(MODE == kSummary && lg == nseg - 1);
   const SeqRange sr = seq_range(a.seq, s);
   const int64_t cs = chunk_start_of(a, s);
   const int64_t c_begin = cs + lg * a.L;
@@ -1260,7 +1369,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
                 const int64_t row = 16 * ct + 4 * g4 + r;
                 S[pp][t][ct][r] = a.s_in ? a.s_in[sbase + row * a.V + col0 + 16 * tile + n16] : 0.f;
               }
-            } else if (MODE == kOutput) {
+            } else if (kWritesOut<MODE>) {
               const float* p = a.seg_state + (gsg * a.H + h) * seg_state_floats(a.V) +
                                ((col0 / 16 + tile) * 8 + ct) * 256 + lane * 4;
               S[pp][t][ct] = *reinterpret_cast<const f32x4_t*>(p);
@@ -1291,11 +1400,11 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
 #pragma unroll
       for (int pp = 0; pp < kPairs; ++pp) {
         const int tile0 = 2 * w + 8 * pp;
-        if (tile0 < ntiles) {
+        if (tile0 < ntiles && scan_state) {
           const int ut[2] = {tile0 < nvt ? tile0 : -1, tile0 + 1 < nvt ? tile0 + 1 : -1};
           f32x4_t O[2][4];
           scan_pair<MODE>(sm, S[pp], ut, tid_c & 63, O);
-          if constexpr (MODE == kOutput) {
+          if constexpr (kWritesOut<MODE>) {
             const int nt = ntiles - tile0 < 2 ? ntiles - tile0 : 2;
             store_out<IT>(O, nt, a.out, geo, a.H, h, a.V, col0 + 16 * tile0, tid_c & 63,
                           lds<IT>(sm, kOffStage + w * 4096));
@@ -1318,24 +1427,38 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
     const LoaderLanes ll = loader_lanes<IT>(a, vcg, tid);
     if (c_begin < c_end) {
       const ChunkGeo g0 = chunk_geo(sr, c_begin - cs);
-      load_raw<IT, MODE>(raw, chunk_loads<IT>(a, g0, h, col0), ll, tid);
+      load_raw<IT, MODE>(raw, chunk_loads<IT>(a, g0, c_begin, h, col0), ll, tid);
       p1_math<IT, MODE>(po, raw, g0, vcg, tid);
     }
     for (int64_t c = c_begin; c < c_end; ++c) {
       const ChunkGeo geo = chunk_geo(sr, c - cs);
       const int tid_c = opaque(tid);
       p1_write<MODE, true>(sm, po, &ll, tid_c);
-      const NextLoads<IT, MODE> nl{&raw, chunk_loads<IT>(a, chunk_geo(sr, c + 1 - cs), h, col0), &ll, tid_c,
-                                   c + 1 < c_end};
+      const NextLoads<IT, MODE> nl{&raw, chunk_loads<IT>(a, chunk_geo(sr, c + 1 - cs), c + 1, h, col0, c + 1 < c_end),
+                                   &ll, tid_c};
       prepare_mid<IT, MODE, true>(sm, a, geo, h, vcg, tid_c, nl);
       prepare_m<IT, MODE, true>(sm, tid_c, nl);
+      if constexpr (MODE == kSummary) {
+        // hand the chunk's M and Aqk fragments to phase C (one column group
+        // writes them); the scanners only read these tiles meanwhile
+        if (a.chunk_ma != nullptr && cgi == 0) {
+          unsigned char* dst = reinterpret_cast<unsigned char*>(a.chunk_ma) + (c * a.H + h) * kMaBytes;
+#pragma unroll
+          for (int k = 0; k < 3; ++k) {
+            const int u = (tid_c - 256) + 256 * k;  // [M | Aqk][j][lane]
+            const int slot = lower_slot((u >> 6) % 6);
+            *reinterpret_cast<uint4*>(dst + u * 16) =
+                *reinterpret_cast<const uint4*>(sm + (u < 384 ? mf_off<MODE>() : kOffAf) + (slot * 64 + (u & 63)) * 16);
+          }
+        }
+      }
       if (c + 1 < c_end) p1_math<IT, MODE>(po, raw, chunk_geo(sr, c + 1 - cs), vcg, tid_c);
       __syncthreads();
     }
   }
 
   // ---- end of the segment ----------------------------------------------------
-  if constexpr (MODE == kOutput) {
+  if constexpr (kWritesOut<MODE>) {
     if (w < 4 && lg == nseg - 1 && a.s_out != nullptr) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -1352,6 +1475,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       }
     }
   } else {
+    if (!scan_state) return;  // uniform: the last segment has no summary
     // value tiles: the start state of the next segment (first segment) or Q_g
     float* dst = (lg == 0) ? a.seg_state + ((gsg + 1) * a.H + h) * seg_state_floats(a.V)
                            : a.seg_q + (gsg * a.H + h) * seg_state_floats(a.V);
@@ -1493,7 +1617,8 @@ struct Plan {
   int32_t L;
   bool segmented;
   int64_t ncg;
-  int64_t segs_bound;  // upper bound on the total number of segments
+  int64_t segs_bound;    // upper bound on the total number of segments
+  int64_t chunks_bound;  // upper bound on the total number of chunks
 };
 
 // KDA_MI355X_SEGMENT_CHUNKS=<L> (L >= 1) forces L chunks per segment; 0 forces
@@ -1511,6 +1636,7 @@ static Plan make_plan(int64_t N, int64_t total_tokens, int64_t H, int64_t V) {
   p.ncg = (V + kColGroup - 1) / kColGroup;
   const int64_t cus = device_cus();
   const int64_t chunks_bound = total_tokens / kChunk + N;
+  p.chunks_bound = chunks_bound;
   const int64_t work = (total_tokens / kChunk) * H * p.ncg;  // chunk-workgroups of one pass
   const int64_t forced = segment_override();
   if (forced > 0) {
@@ -1539,7 +1665,8 @@ static size_t segment_bytes(const Plan& p, int64_t H, int64_t V) {
   if (!p.segmented) return 0;
   const size_t st = static_cast<size_t>(p.segs_bound * H * seg_state_floats(V)) * 4;
   const size_t pp = static_cast<size_t>(p.segs_bound * H * seg_p_elems()) * 2;
-  return 2 * st + pp;
+  const size_t ma = static_cast<size_t>(p.chunks_bound * H * kMaBytes);
+  return 2 * st + pp + ma;
 }
 
 static void mark(kda_host::KernelEvents* ev, int i, hipStream_t stream) {
@@ -1596,6 +1723,9 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
   sa.seg_state = p.segmented ? reinterpret_cast<float*>(segbuf) : nullptr;
   sa.seg_q = p.segmented ? reinterpret_cast<float*>(segbuf + st_bytes) : nullptr;
   sa.seg_p = p.segmented ? reinterpret_cast<bf16*>(segbuf + 2 * st_bytes) : nullptr;
+  sa.chunk_ma = p.segmented ? reinterpret_cast<bf16*>(segbuf + 2 * st_bytes +
+                                                      static_cast<size_t>(p.segs_bound * H * seg_p_elems()) * 2)
+                            : nullptr;
   sa.N = N;
   sa.H = H;
   sa.V = V;
@@ -1624,7 +1754,7 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
     mark(ev, 2, stream);
     mark(ev, 3, stream);
   }
-  st = launch_segments<IT, kOutput>(sa, p, H, stream);
+  st = p.segmented ? launch_segments<IT, kOutputMA>(sa, p, H, stream) : launch_segments<IT, kOutput>(sa, p, H, stream);
   mark(ev, 4, stream);
   return st;
 }
