@@ -60,9 +60,20 @@ def prefill_flops(B, T, H, K, V, C=64):
     return B * T * H * (6 * K * V + (3 * C + 1) * K + 2 * (C + 1) * V)
 
 
-def summary_bytes(B, T, H, K, V):
-    """Compulsory reads of the segment-summary pass: k, g, v (bf16) and beta."""
-    return 2 * B * T * H * (2 * K + V) + 2 * B * T * H
+SEGMENT_CHUNKS = 8  # chunks per segment the library picks for the long-context workload on 256 CUs
+MA_BYTES = 12 * 1024  # each chunk's M and Aqk fragments handed from the summary pass to the output pass
+
+
+def summary_bytes(B, T, H, K, V, C=64, L=SEGMENT_CHUNKS):
+    """Bytes the segment-summary pass must move: it reads q, k, g, v (bf16) and
+    beta of every chunk, writes each chunk's M and Aqk fragments, and writes
+    per segment but the last the f32 zero-start end state (or the second
+    segment's start state) and, past the first, the bf16 128x128 transition."""
+    chunks = T // C
+    nseg = (chunks + L - 1) // L
+    reads = 2 * B * T * H * (3 * K + V) + 2 * B * T * H
+    writes = B * H * (chunks * MA_BYTES + (nseg - 1) * 4 * K * V + max(nseg - 2, 0) * 2 * K * K)
+    return reads + writes
 
 
 def kernel_bytes(name, B, T, H, K, V):
@@ -282,7 +293,7 @@ def main() -> int:
     dom = max(PREFILL_KERNELS[1:], key=lambda n: per_kernel[n] if kernel_bytes(n, P_B, P_T, P_H, P_K, P_V) else -1)
     dom_ms = per_kernel[dom]
     dom_bytes = kernel_bytes(dom, P_B, P_T, P_H, P_K, P_V)
-    op_ms = sum(per_kernel.values())
+    op_ms = ms  # the whole operator, end to end
     dbytes = decode_bytes(D_B, D_H, D_K, D_V)
     dec_gbs = dbytes / (dec_ms * 1e-3) / 1e9
 

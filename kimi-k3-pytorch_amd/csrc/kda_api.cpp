@@ -186,6 +186,7 @@ int kda_chunk_fwd_profiled(const void* q, const void* k, const void* v, const vo
   }
   KernelEvents ev;
   ev.n_launched = 0;
+  ev.empty = 0;
   for (auto& e : ev.ev) {
     if (hipEventCreate(&e) != hipSuccess) {
       set_detail("hipEventCreate failed");
@@ -200,7 +201,8 @@ int kda_chunk_fwd_profiled(const void* q, const void* k, const void* v, const vo
   *num_kernels = 0;
   if (st == KDA_OK && hipStreamSynchronize(s) == hipSuccess) {
     *num_kernels = ev.n_launched;
-    for (int i = 0; i < ev.n_launched && i < 4; ++i) (void)hipEventElapsedTime(&kernel_ms[i], ev.ev[i], ev.ev[i + 1]);
+    for (int i = 0; i < ev.n_launched && i < 4; ++i)
+      if (!((ev.empty >> i) & 1u)) (void)hipEventElapsedTime(&kernel_ms[i], ev.ev[i], ev.ev[i + 1]);
   }
   for (auto& e : ev.ev) (void)hipEventDestroy(e);
   return st;

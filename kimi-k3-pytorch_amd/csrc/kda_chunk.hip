@@ -1733,6 +1733,7 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
 
   mark(ev, 0, stream);
   int st = KDA_OK;
+  if (ev != nullptr && dense) ev->empty |= 1u;  // dense batches need no chunk map
   if (!dense) {
     hipLaunchKernelGGL(chunk_map_kernel, dim3(1), dim3(1024), 0, stream, seq, N, p.L, chunk_start, seg_start);
     st = kda_host::check_launch("chunk_map_kernel");
@@ -1753,6 +1754,7 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
   } else {
     mark(ev, 2, stream);
     mark(ev, 3, stream);
+    if (ev != nullptr) ev->empty |= 6u;  // one segment per sequence: no summaries, no combine
   }
   st = p.segmented ? launch_segments<IT, kOutputMA>(sa, p, H, stream) : launch_segments<IT, kOutput>(sa, p, H, stream);
   mark(ev, 4, stream);

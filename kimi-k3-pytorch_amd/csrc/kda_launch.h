@@ -19,10 +19,12 @@ size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t hea
                              int64_t value_dim, int in_dtype);
 
 // Optional per-kernel timing: events[i] is recorded before kernel i and
-// events[n] after the last one; *n_launched receives n.
+// events[n] after the last one; *n_launched receives n.  Bit i of `empty`
+// marks a slot whose kernel the call does not need (its time reads zero).
 struct KernelEvents {
   hipEvent_t ev[5];
   int n_launched;
+  unsigned empty;
 };
 
 int launch_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
