@@ -17,18 +17,21 @@
 // sequence of chunks is cut into segments of L chunks so that the serial
 // chain does not limit parallelism when batch * heads is small:
 //  * phase A, chunk_segment_kernel<.., kSummary>: one workgroup per
-//    (segment, head, 128-column group) folds its segment into
-//    (P_g, Q_g) by running the chunk recurrence on X = [Q | P] from
-//    X = [0 | I]: the V value columns give Q_g, 128 more columns give P_g.
-//    The first segment of a sequence starts from the real initial state and
-//    directly yields the start state of the second segment.
+//    (segment, head, 128-column group) prepares every chunk of its segment,
+//    hands each chunk's M and Aqk fragments to phase C through the
+//    workspace, and folds the segment into (P_g, Q_g) by running the chunk
+//    recurrence on X = [Q | P] from X = [0 | I]: the V value columns give
+//    Q_g, 128 more columns give P_g.  The first segment of a sequence starts
+//    from the real initial state and directly yields the start state of the
+//    second segment; the last segment only prepares its chunks.
 //  * phase B, segment_combine_kernel: S_{g+1} = P_g S_g + Q_g along each
 //    sequence, one workgroup per (sequence, head, 16-column tile).
-//  * phase C, chunk_segment_kernel<.., kOutput>: one workgroup per
+//  * phase C, chunk_segment_kernel<.., kOutputMA>: one workgroup per
 //    (segment, head, column group) re-runs its segment from the true start
-//    state and writes the outputs (and the final state).
+//    state with M and Aqk from phase A and writes the outputs (and the final
+//    state).
 // When batch * heads alone fills the GPU, each sequence is one segment and
-// only phase C runs.
+// only phase C runs, preparing every chunk itself (kOutput).
 //
 // Inside phases A and C a workgroup of 8 waves walks its chunks; per chunk
 // it builds every chunk operand in LDS (decay factors, A and Aqk on MFMA,
