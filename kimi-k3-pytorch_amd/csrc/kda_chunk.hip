@@ -113,17 +113,15 @@ constexpr int kRowT = 72;                           // padded row of the channel
 constexpr int kOffKEt = kOffFlag + 16;              // bf16 [128][72] k_j E_j, channel-major
 constexpr int kSmemBytes = kOffKEt + kKey * kRowT * 2;
 // -Kgamma = -exp(lg) k A fragments, 1 KB each (64 lanes x 8 bf16), fragment
-// (I, s) at kgf_off<MODE>(I, s): in phase C with P2 [I][s] over the q a tile,
-// which is dead after P2; in phase C without P2 [I][s] over the k E tile; in
-// phase A [s][I] with block s over the channel-major k E rows of channels
-// 32 s .. 32 s + 31, which the loader wave that owns those channels has
-// finished reading when it writes block s.
-constexpr int kKgfStride = 32 * kRowT * 2;  // 4608
+// (I, s) at kgf_off<MODE>(I, s), [I][s]: in phase C with P2 over the q a
+// tile, which is dead after P2; in phase C without P2 over the k E tile and
+// in phase A over the channel-major k E tile, neither of which those modes
+// use.
 template <int MODE>
 __host__ __device__ constexpr int kgf_off(int I, int s) {
   return MODE == kOutput     ? kOffQA + (I * 4 + s) * 1024
-         : MODE == kOutputMA ? kOffKE + (I * 4 + s) * 1024  // k E tile, unused without P2
-                             : kOffKEt + s * kKgfStride + I * 1024;
+         : MODE == kOutputMA ? kOffKE + (I * 4 + s) * 1024
+                             : kOffKEt + (I * 4 + s) * 1024;
 }
 // M = (I + diag(beta) A)^-1 diag(beta) A fragments [I=4][s=2][lane][8]: over
 // the k E tile (dead after P2) when M is formed in the loop, over the L tile
@@ -132,6 +130,21 @@ template <int MODE>
 __host__ __device__ constexpr int mf_off() {
   return MODE == kOutputMA ? kOffL : kOffKE;
 }
+// Lane slots of the Q~, -Kgamma and K~^T fragments.  Phase A and phase C
+// without P2 write them straight from the loader registers (a loader thread
+// holds 16 rows x 2 channels), and XOR-swizzle the slots so that a loader
+// wave's 4- and 8-byte writes spread over the LDS banks; every swizzle
+// permutes slots inside aligned groups of eight, which keeps the scanners'
+// 16-byte fragment reads conflict-free.  Phase C with P2 exports whole
+// 16-byte lanes from the natural tiles, unswizzled.
+template <int MODE>
+__device__ __forceinline__ int qk_slot(int I, int lane) {  // Q~ / -Kgamma fragment (I, s)
+  return MODE != kOutput ? lane ^ ((4 * I + (lane >> 4)) & 7) : lane;
+}
+template <int MODE>
+__device__ __forceinline__ int kt_slot(int ct, int lane) {  // K~^T fragment (ct, s')
+  return MODE != kOutput ? lane ^ (ct & 1) : lane;
+}
 constexpr int kOffStage = kOffKA;  // output transpose [4 waves][64][32]
 constexpr int kOffPnat = kOffKA;   // phase A: P_g natural bf16 [128][136]
 static_assert(kSmemBytes <= 160 * 1024, "chunk_segment_kernel LDS exceeds one CU");
@@ -139,9 +152,11 @@ static_assert(kChunk * 72 * 2 >= 8192, "M fragments must fit in the L tile");
 static_assert(mf_off<kSummary>() == kOffKE && mf_off<kOutput>() == kOffKE, "m_block_row writes M over the k E tile");
 static_assert(kOffKEt % 16 == 0 && kOffGs % 16 == 0 && kOffGe % 16 == 0, "16-byte LDS accesses need aligned tiles");
 static_assert(4 * 64 * 32 * 2 <= kNat, "output stage must fit in the k a tile");
+static_assert(kOffStage + 4 * 64 * 32 * 2 <= kgf_off<kOutputMA>(0, 0) && kOffStage + 4 * 64 * 32 * 2 <= kOffVn,
+              "phase C without P2 stores a chunk's outputs while the next chunk's operands are written");
 static_assert(kKey * kRow * 2 <= 2 * kNat, "P transpose must fit in the k a and q a tiles");
 static_assert(16384 <= kNat && 8192 <= kNat, "Kgamma and M fragments must fit in the q a and k E tiles");
-static_assert(4 * kKgfStride == kKey * kRowT * 2 && 4 * 1024 <= kKgfStride, "Kgamma blocks must fit their k E rows");
+static_assert(16384 <= kKey * kRowT * 2, "phase A Kgamma fragments must fit in the channel-major k E tile");
 // Fragment element e of lane (i, g) covers reduction index
 //   32 s + (e < 4 ? 4 g + e : 16 + 4 g + e - 4),
 // the order in which two stacked C tiles provide a B operand.
@@ -512,6 +527,7 @@ __device__ __forceinline__ void m_block_row(unsigned char* sm, int lane) {
 // next chunk (p1_write).
 struct P1Out {
   uint32_t ka[16], qa[16], ke[16];  // bf16 pairs (channels 2cp, 2cp + 1) of rows 16 J + r
+  uint32_t kg[16], kt[16];          // phase A: -Kgamma and K~ rows, written straight into fragments
   float gs[2];                      // exp(lg_{16J})
   float ge[2];                      // exp(lg_63 - lg_{16J+15})
   float gam[2];                     // exp(lg_63)
@@ -530,53 +546,31 @@ template <class IT, int MODE>
 __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const ChunkGeo& cg, int vcg, int tid) {
   const int J = loader_block(tid);
   const int n_valid = cg.n_valid;
+  const int lane = tid & 63;
   float al[2][16];
+  float pj[2] = {1.f, 1.f};  // P_J = exp(lg_{16J+15} - lg_{16J})
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
     const bool ok = 16 * J + r < n_valid;
-#pragma unroll
-    for (int ch = 0; ch < 2; ++ch) al[ch][r] = ok ? fast_exp(to_float(raw.gp[r][ch])) : 1.f;
-  }
-  float run[2] = {1.f, 1.f};
-#pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const bool ok = 16 * J + r < n_valid;
-    float kv[2], qv[2];
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
-      if (r > 0) run[ch] *= al[ch][r];
-      kv[ch] = ok ? to_float(raw.kp[r][ch]) : 0.f;
-      qv[ch] = ok ? to_float(raw.qp[r][ch]) : 0.f;
+      al[ch][r] = ok ? fast_exp(to_float(raw.gp[r][ch])) : 1.f;
+      if (r > 0) pj[ch] *= al[ch][r];
     }
-    po.ka[r] = pack_bf16x2(kv[0] * run[0], kv[1] * run[1]);
-    po.qa[r] = pack_bf16x2(qv[0] * run[0], qv[1] * run[1]);
   }
-  float suf[2] = {1.f, 1.f};
-#pragma unroll
-  for (int r = 15; r >= 0; --r) {
-    const bool ok = 16 * J + r < n_valid;
-    float kv[2];
-#pragma unroll
-    for (int ch = 0; ch < 2; ++ch) kv[ch] = ok ? to_float(raw.kp[r][ch]) * suf[ch] : 0.f;
-    po.ke[r] = pack_bf16x2(kv[0], kv[1]);
-#pragma unroll
-    for (int ch = 0; ch < 2; ++ch) suf[ch] *= al[ch][r];
-  }
-  // Block J's products P_J = exp(lg_{16J+15} - lg_{16J}) (a at its last row)
-  // and alpha at its first row A0_J give G_J = A0_J P_J, the decay across the
-  // block; the other blocks' G come from lanes l ^ 16, l ^ 32, l ^ 48.
+  // Block J's products P_J and alpha at its first row A0_J give G_J = A0_J P_J,
+  // the decay across the block; the other blocks' G come from lanes l ^ 16,
+  // l ^ 32, l ^ 48.
   //   Gs_J = A0_J prod_{J' < J} G_J',  Ge_J = prod_{J' > J} G_J',  gamma = prod G_J',
   //   pair (J, J') scale: A0_J prod_{J' < j < J} G_j (J' < J), 1 / P_J (J' = J).
-  const int lane = tid & 63;
   bool ext = false;
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch) {
     const float a0 = al[ch][0];
-    const float pj = run[ch];
-    ext = ext || !(pj >= kExtremeDecay);
+    ext = ext || !(pj[ch] >= kExtremeDecay);
     float G[4];
 #pragma unroll
-    for (int jb = 0; jb < 4; ++jb) G[jb] = __shfl(a0 * pj, (lane & 15) + 16 * jb);
+    for (int jb = 0; jb < 4; ++jb) G[jb] = __shfl(a0 * pj[ch], (lane & 15) + 16 * jb);
     float pre = 1.f, post = 1.f;
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) {
@@ -591,10 +585,38 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
       float sc = a0;
 #pragma unroll
       for (int jj = 1; jj < 3; ++jj) sc *= (jj > jp && jj < J) ? G[jj] : 1.f;
-      po.sc[jp][ch] = jp < J ? sc : (pj > 0.f ? 1.f / pj : 0.f);
+      po.sc[jp][ch] = jp < J ? sc : (pj[ch] > 0.f ? 1.f / pj[ch] : 0.f);
     }
   }
   po.ext = __any(ext) ? 1 : 0;
+  // k a, q a (and in phase A -Kgamma = -k a Gs) forward; k E (and K~ = k E Ge) backward
+  float run[2] = {1.f, 1.f};
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const bool ok = 16 * J + r < n_valid;
+    float kv[2], qv[2];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      if (r > 0) run[ch] *= al[ch][r];
+      kv[ch] = ok ? to_float(raw.kp[r][ch]) * run[ch] : 0.f;
+      qv[ch] = ok ? to_float(raw.qp[r][ch]) * run[ch] : 0.f;
+    }
+    po.ka[r] = pack_bf16x2(kv[0], kv[1]);
+    po.qa[r] = pack_bf16x2(qv[0], qv[1]);
+    if constexpr (MODE == kSummary) po.kg[r] = pack_bf16x2(-kv[0] * po.gs[0], -kv[1] * po.gs[1]);
+  }
+  float suf[2] = {1.f, 1.f};
+#pragma unroll
+  for (int r = 15; r >= 0; --r) {
+    const bool ok = 16 * J + r < n_valid;
+    float kv[2];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) kv[ch] = ok ? to_float(raw.kp[r][ch]) * suf[ch] : 0.f;
+    po.ke[r] = pack_bf16x2(kv[0], kv[1]);
+    if constexpr (MODE == kSummary) po.kt[r] = pack_bf16x2(kv[0] * po.ge[0], kv[1] * po.ge[1]);
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) suf[ch] *= al[ch][r];
+  }
   const int t2 = tid - 256;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -611,9 +633,41 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
     po.vv[i] = val;
   }
   po.bt = (t2 < kChunk && t2 < n_valid) ? to_float(raw.bt) : 0.f;
-  if constexpr (MODE == kOutputMA) {
+}
+
+// Operand rows of a loader thread (block J, channel pair cp) written straight
+// into A fragments.  A wave owns channels 32 s .. 32 s + 31 (s = wave - 4):
+// for an operand that reduces over channels (Q~, -Kgamma) they are reduction
+// step s, and channel pair (2 cp, 2 cp + 1) of row 16 J + r is one 4-byte
+// piece of lane (r, g) of fragment (J, s) at `frag`.
+template <int MODE>
+__device__ __forceinline__ void write_channel_frags(unsigned char* frag, const uint32_t (&x)[16], int J, int lane) {
+  const int m = lane & 15;
+  const int g = (m & 7) >> 1;                  // channel 32 s + 2 m: lane group g,
+  const int eb = 4 * (m & 1) + 8 * (m >> 3);  // byte 2 e of the lane's 16 bytes
 #pragma unroll
-    for (int k = 0; k < 3; ++k) po.ma[k] = raw.ma[k];
+  for (int r = 0; r < 16; ++r) *reinterpret_cast<uint32_t*>(frag + qk_slot<MODE>(J, r + 16 * g) * 16 + eb) = x[r];
+}
+// K~ rows into the K~^T fragments, which reduce over rows: channel ch is row
+// ch % 16 of row tile ct = ch / 16, and rows 16 J + 4 g .. 16 J + 4 g + 3 are
+// one 8-byte half of lane (ch % 16, g) of reduction step J / 2.
+template <int MODE>
+__device__ __forceinline__ void write_kt_frags(unsigned char* sm, const uint32_t (&kt)[16], int J, int cp) {
+#pragma unroll
+  for (int chp = 0; chp < 2; ++chp) {
+    const int ch = 2 * cp + chp;
+    const int ct = ch >> 4;
+    unsigned char* frag = sm + kOffKTf + (ct * 2 + (J >> 1)) * 1024 + (J & 1) * 8;
+#pragma unroll
+    for (int gg = 0; gg < 4; ++gg) {
+      uint32_t w[2];
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const uint32_t a = kt[4 * gg + 2 * h2], b = kt[4 * gg + 2 * h2 + 1];
+        w[h2] = chp == 0 ? (a & 0xffffu) | (b << 16) : (a >> 16) | (b & 0xffff0000u);
+      }
+      *reinterpret_cast<uint2*>(frag + kt_slot<MODE>(ct, (ch & 15) + 16 * gg) * 16) = uint2{w[0], w[1]};
+    }
   }
 }
 
@@ -637,22 +691,30 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
       *reinterpret_cast<uint32_t*>(nat_row(sm, kOffQA, tl) + 2 * cp) = po.qa[r];
       if constexpr (kPrepares<MODE>) *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKE, tl) + 2 * cp) = po.ke[r];
     }
-    // channel-major k E: rows 16 J .. 16 J + 15 of channels 2 cp, 2 cp + 1
+    if constexpr (MODE == kSummary) {
+      // phase A: -Kgamma and K~^T fragments straight from the registers
+      write_channel_frags<MODE>(sm + kgf_off<MODE>(J, wave_of(tid) - 4), po.kg, J, tid & 63);
+      write_kt_frags<MODE>(sm, po.kt, J, cp);
+    } else {
+      // channel-major k E: rows 16 J .. 16 J + 15 of channels 2 cp, 2 cp + 1
 #pragma unroll
-    for (int ch = 0; ch < 2; ++ch) {
-      uint32_t w[8];
+      for (int ch = 0; ch < 2; ++ch) {
+        uint32_t w[8];
 #pragma unroll
-      for (int m = 0; m < 8; ++m)
-        w[m] = ch == 0 ? (po.ke[2 * m] & 0xffffu) | (po.ke[2 * m + 1] << 16)
-                       : (po.ke[2 * m] >> 16) | (po.ke[2 * m + 1] & 0xffff0000u);
-      *reinterpret_cast<uint4*>(&KEt[2 * cp + ch][16 * J]) = uint4{w[0], w[1], w[2], w[3]};
-      *reinterpret_cast<uint4*>(&KEt[2 * cp + ch][16 * J + 8]) = uint4{w[4], w[5], w[6], w[7]};
+        for (int m = 0; m < 8; ++m)
+          w[m] = ch == 0 ? (po.ke[2 * m] & 0xffffu) | (po.ke[2 * m + 1] << 16)
+                         : (po.ke[2 * m] >> 16) | (po.ke[2 * m + 1] & 0xffff0000u);
+        *reinterpret_cast<uint4*>(&KEt[2 * cp + ch][16 * J]) = uint4{w[0], w[1], w[2], w[3]};
+        *reinterpret_cast<uint4*>(&KEt[2 * cp + ch][16 * J + 8]) = uint4{w[4], w[5], w[6], w[7]};
+      }
     }
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
       const int cc = 2 * cp + ch;
-      Gs[J][cc] = po.gs[ch];
-      Ge[J][cc] = po.ge[ch];
+      if constexpr (MODE == kOutput) {
+        Gs[J][cc] = po.gs[ch];
+        Ge[J][cc] = po.ge[ch];
+      }
       if (J == 0) gam[cc] = po.gam[ch];
 #pragma unroll
       for (int jp = 0; jp < 4; ++jp)
@@ -664,16 +726,121 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
       if (ll->vlds[i] >= 0) *reinterpret_cast<uint4*>(sm + kOffVn + ll->vlds[i]) = po.vv[i];
     const int t2 = tid - 256;
     if (t2 < kChunk) betas[t2] = po.bt;
-    if constexpr (MODE == kOutputMA) {
-#pragma unroll
-      for (int k = 0; k < 3; ++k) {
-        const int u = t2 + 256 * k;  // [M | Aqk][j][lane]
-        const int slot = lower_slot((u >> 6) % 6);
-        *reinterpret_cast<uint4*>(sm + (u < 384 ? mf_off<MODE>() : kOffAf) + (slot * 64 + (u & 63)) * 16) = po.ma[k];
-      }
-    }
   }
   __syncthreads();
+}
+
+// P1 of phase C without P2, which needs no natural tiles: the loader thread
+// turns its rows straight into operand values,
+//   Q~ = exp(lg) q,  -Kgamma = -exp(lg) k  (running products from exp(lg_{16J})),
+//   K~ = exp(lg_63 - lg) k                 (running products back from exp(lg_63 - lg_{16J+15})),
+// with the block products of the other three blocks of its channels taken
+// from the lanes that hold them.  Rows past the chunk's valid tokens were read
+// as zero (g = 0, k = q = 0), so they give zero operands and a unit decay.
+template <class IT>
+__device__ __forceinline__ void p1_math_ma(P1Out& po, const Raw<IT>& raw, int tid) {
+  const int J = loader_block(tid);
+  const int lane = tid & 63;
+  float al[2][16];
+  float pj[2] = {1.f, 1.f};
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      al[ch][r] = fast_exp(to_float(raw.gp[r][ch]));
+      if (r > 0) pj[ch] *= al[ch][r];
+    }
+  }
+  float x[2], y[2];
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch) {
+    const float a0 = al[ch][0];
+    float G[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) G[jb] = __shfl(a0 * pj[ch], (lane & 15) + 16 * jb);
+    float pre = 1.f, post = 1.f;
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+      pre *= jb < J ? G[jb] : 1.f;
+      post *= jb > J ? G[jb] : 1.f;
+    }
+    x[ch] = pre * a0;  // exp(lg_{16J})
+    y[ch] = post;      // exp(lg_63 - lg_{16J+15})
+    po.gam[ch] = G[0] * G[1] * G[2] * G[3];
+  }
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    float kv[2], qv[2];
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) {
+      if (r > 0) x[ch] *= al[ch][r];
+      kv[ch] = to_float(raw.kp[r][ch]) * x[ch];
+      qv[ch] = to_float(raw.qp[r][ch]) * x[ch];
+    }
+    po.qa[r] = pack_bf16x2(qv[0], qv[1]);
+    po.ka[r] = pack_bf16x2(-kv[0], -kv[1]);
+  }
+#pragma unroll
+  for (int r = 15; r >= 0; --r) {
+    po.ke[r] = pack_bf16x2(to_float(raw.kp[r][0]) * y[0], to_float(raw.kp[r][1]) * y[1]);
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) y[ch] *= al[ch][r];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint4 val = raw.vv[i];
+    if constexpr (sizeof(IT) == 2 && !__is_same(IT, bf16)) {
+      typedef IT h8_t __attribute__((ext_vector_type(8)));
+      const h8_t xv = __builtin_bit_cast(h8_t, val);
+      bf16x8_t yv;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) yv[e] = (bf16)to_float(xv[e]);
+      val = __builtin_bit_cast(uint4, yv);
+    }
+    po.vv[i] = val;
+  }
+#pragma unroll
+  for (int k = 0; k < 3; ++k) po.ma[k] = raw.ma[k];
+}
+
+// Writes P1 of phase C without P2 into the fragment tiles the scanners read,
+// issuing parts 0-5 of the next chunk's loads between the writes.  A loader
+// wave owns channels 32 s .. 32 s + 31 (s = wave - 4), which are reduction
+// step s of the Q~ and -Kgamma fragments: channel pair (2 cp, 2 cp + 1) of
+// row 16 J + r is one 4-byte piece of lane (r, g) of fragment (J, s).  Of
+// the K~^T fragments, channel ch is row ch % 16 of row tile ch / 16, and
+// rows 16 J + 4 g .. 16 J + 4 g + 3 are one 8-byte half of lane (ch % 16, g)
+// of reduction step J / 2.
+template <class IT, int MODE>
+__device__ __forceinline__ void p1_write_ma(unsigned char* sm, const P1Out& po, const LoaderLanes& ll, int tid,
+                                            const NextLoads<IT, MODE>& nl) {
+  const int lane = tid & 63;
+  const int J = loader_block(tid);
+  const int cp = loader_pair(tid);
+  const int s = wave_of(tid) - 4;
+  nl.template load_part<0>();
+  nl.template load_part<1>();
+  write_channel_frags<MODE>(sm + kOffQf + (J * 4 + s) * 1024, po.qa, J, lane);
+  write_channel_frags<MODE>(sm + kgf_off<MODE>(J, s), po.ka, J, lane);
+  nl.template load_part<2>();
+  nl.template load_part<3>();
+  write_kt_frags<MODE>(sm, po.ke, J, cp);
+  nl.template load_part<4>();
+  nl.template load_part<5>();
+  if (J == 0) {
+    float* gam = lds<float>(sm, kOffGam);
+    gam[2 * cp] = po.gam[0];
+    gam[2 * cp + 1] = po.gam[1];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (ll.vlds[i] >= 0) *reinterpret_cast<uint4*>(sm + kOffVn + ll.vlds[i]) = po.vv[i];
+#pragma unroll
+  for (int k = 0; k < 3; ++k) {
+    const int u = (tid - 256) + 256 * k;  // [M | Aqk][j][lane]
+    const int slot = lower_slot((u >> 6) % 6);
+    *reinterpret_cast<uint4*>(sm + (u < 384 ? mf_off<MODE>() : kOffAf) + (slot * 64 + (u & 63)) * 16) = po.ma[k];
+  }
 }
 
 // Everything after P1 (reads only LDS, plus global q/k/g on the rare
@@ -697,66 +864,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
   float* betas = lds<float>(sm, kOffBeta);
   const int* flags = lds<int>(sm, kOffFlag);
 
-  if constexpr (MODE == kOutputMA) {
-    // phase C with M and Aqk from phase A: only the three fragment exports,
-    // tasks tid + 512 k: Q~ (k = 0, 1), K~^T (k = 2, 3), -Kgamma (k = 4, 5).
-    // Element e of lane (i, g) of an A fragment s covers index 32 s + 4 g + e
-    // (e < 4) and 32 s + 16 + 4 g + e - 4: two runs of four, one 8-byte read
-    // each; every task's reads go out before any is used.
-    if constexpr (LOADER) {
-      nl.template load_part<0>();
-      nl.template load_part<1>();
-      nl.template load_part<2>();
-    }
-    bf16x4_t lo[6], hi[6];
-    f32x4_t slo[6], shi[6];
-#pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      const int task = tid + kThreads * k;
-      const int frag = (task >> 6) & 15;
-      const int fi = task & 15, fg = (task >> 4) & 3;
-      if (k < 2 || k >= 4) {  // exp(lg) q or exp(lg) k : fragment (I, s), lane (i, g)
-        const int I = frag >> 2, c0 = 32 * (frag & 3) + 4 * fg;
-        const bf16* row = nat_row(sm, k < 2 ? kOffQA : kOffKA, 16 * I + fi);
-        lo[k] = *reinterpret_cast<const bf16x4_t*>(row + c0);
-        hi[k] = *reinterpret_cast<const bf16x4_t*>(row + c0 + 16);
-        slo[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0]);
-        shi[k] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
-      } else {  // K~^T : fragment (ct, s'), lane (c, g); rows r0.. and r0 + 16.. each sit in one block
-        const int ch = 16 * (frag >> 1) + fi, r0 = 32 * (frag & 1) + 4 * fg;
-        lo[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0]);
-        hi[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0 + 16]);
-        slo[k][0] = Ge[r0 >> 4][ch];
-        shi[k][0] = Ge[(r0 + 16) >> 4][ch];
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);
-    if constexpr (LOADER) {
-      nl.template load_part<3>();
-      nl.template load_part<4>();
-    }
-#pragma unroll
-    for (int k = 0; k < 6; ++k) {
-      const int task = tid + kThreads * k;
-      const bool per_ch = k < 2 || k >= 4;
-      const float sgn = k >= 4 ? -1.f : 1.f;
-      bf16x8_t o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        o[e] = (bf16)(sgn * (float)lo[k][e] * (per_ch ? slo[k][e] : slo[k][0]));
-        o[4 + e] = (bf16)(sgn * (float)hi[k][e] * (per_ch ? shi[k][e] : shi[k][0]));
-      }
-      const int dst = k < 2 ? kOffQf : (k < 4 ? kOffKTf : kgf_off<MODE>(0, 0));
-      *lds<bf16x8_t>(sm, dst + (task & 1023) * 16) = o;
-    }
-    if constexpr (LOADER) {
-      nl.template load_part<5>();
-      nl.template load_part<6>();
-      nl.template load_part<7>();
-    }
-    __syncthreads();
-    return;
-  }
+  static_assert(MODE != kOutputMA, "phase C without P2 builds its operands in p1_write_ma");
 
   if constexpr (LOADER) {
     nl.template load_part<0>();
@@ -867,124 +975,71 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
       }
     }
   } else {
-    // phase A: the scanners take all ten block pairs of P2 (no Aqk), each
-    // loader wave exports K~^T and -Kgamma for its own 32 channels
-    // Element e of lane (i, g) of an A fragment s covers index 32 s + 4 g + e
-    // (e < 4) and 32 s + 16 + 4 g + e - 4: two runs of four, one 8-byte LDS read
-    // each.  Every task's reads go out before any is used.
+    // phase A: block pair p of P2 (A and Aqk) goes to wave p, and pairs 8
+    // and 9 to waves 0 and 1 (the K~^T and -Kgamma fragments came with P1)
+    // ---- A (strict) and Aqk (causal) 16x16 block pair p on MFMA -------------
+    auto p2_pair = [&](int p) {
+      // block pair p = I (I + 1) / 2 + J, J <= I
+      const int I = p >= 6 ? 3 : (p >= 3 ? 2 : (p >= 1 ? 1 : 0));
+      const int J = p - I * (I + 1) / 2;
+      // the operands of two reduction steps at a time (two LDS round trips per pair)
+      const bf16* ke_row = nat_row(sm, kOffKE, 16 * J + n16);
+      const bf16* ka_row = nat_row(sm, kOffKA, 16 * I + n16);
+      const bf16* qa_row = nat_row(sm, kOffQA, 16 * I + n16);
+      const int i = 16 * I + n16;
+      const float bi = betas[i];
+      f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
+      f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int half = 0; half < 2; ++half) {
+        bf16x8_t ke[2], kb[2], qb[2];
+        f32x4_t sc0[2], sc1[2];
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          const int c0 = 32 * (2 * half + u) + 8 * g4;
+          ke[u] = *reinterpret_cast<const bf16x8_t*>(ke_row + c0);
+          sc0[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0]);
+          sc1[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0 + 4]);
+          kb[u] = *reinterpret_cast<const bf16x8_t*>(ka_row + c0);
+          qb[u] = *reinterpret_cast<const bf16x8_t*>(qa_row + c0);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int u = 0; u < 2; ++u) {
+          bf16x8_t af;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            af[e] = (bf16)((float)ke[u][e] * sc0[u][e]);
+            af[4 + e] = (bf16)((float)ke[u][4 + e] * sc1[u][e]);
+          }
+          akk = mfma32(af, kb[u], akk);
+          aqk = mfma32(af, qb[u], aqk);
+        }
+      }
+      // lane (n16, g4) holds A[16I + n16][16J + 4 g4 + r] (and likewise Aqk)
+      bf16x4_t lrow;
+      bf16x4_t qrow;
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int j = 16 * J + 4 * g4 + r;
+        const float vk = (j < i) ? akk[r] * bi : 0.f;
+        lrow[r] = (bf16)vk;
+        qrow[r] = (bf16)((j <= i) ? aqk[r] : 0.f);
+        if (I == J) Ld[I][n16][4 * g4 + r] = vk;
+      }
+      *reinterpret_cast<bf16x4_t*>(&Lm[i][16 * J + 4 * g4]) = lrow;
+      {
+        unsigned char* afrag = sm + kOffAf + ((I * 2 + J / 2) * 64 + lane) * 16;
+        *reinterpret_cast<bf16x4_t*>(afrag + (J & 1) * 8) = qrow;
+        if (I == J && (I & 1) == 0) *reinterpret_cast<bf16x4_t*>(afrag + 8) = bf16x4_t{};  // tile J = I+1 is above
+      }
+    };
     if (wave < 4) {
-      // ---- scanners: A (strict) and Aqk (causal) 16x16 block pairs on MFMA -----
-      for (int p = wave; p < 10; p += 4) {
-        // block pair p = I (I + 1) / 2 + J, J <= I
-        const int I = p >= 6 ? 3 : (p >= 3 ? 2 : (p >= 1 ? 1 : 0));
-        const int J = p - I * (I + 1) / 2;
-        // the operands of two reduction steps at a time (two LDS round trips per pair)
-        const bf16* ke_row = nat_row(sm, kOffKE, 16 * J + n16);
-        const bf16* ka_row = nat_row(sm, kOffKA, 16 * I + n16);
-        const bf16* qa_row = nat_row(sm, kOffQA, 16 * I + n16);
-        const int i = 16 * I + n16;
-        const float bi = betas[i];
-        f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
-        f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
-  #pragma unroll
-        for (int half = 0; half < 2; ++half) {
-          bf16x8_t ke[2], kb[2], qb[2];
-          f32x4_t sc0[2], sc1[2];
-  #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            const int c0 = 32 * (2 * half + u) + 8 * g4;
-            ke[u] = *reinterpret_cast<const bf16x8_t*>(ke_row + c0);
-            sc0[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0]);
-            sc1[u] = *reinterpret_cast<const f32x4_t*>(&Sc[p][c0 + 4]);
-            kb[u] = *reinterpret_cast<const bf16x8_t*>(ka_row + c0);
-            qb[u] = *reinterpret_cast<const bf16x8_t*>(qa_row + c0);
-          }
-          __builtin_amdgcn_sched_barrier(0);
-  #pragma unroll
-          for (int u = 0; u < 2; ++u) {
-            bf16x8_t af;
-  #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              af[e] = (bf16)((float)ke[u][e] * sc0[u][e]);
-              af[4 + e] = (bf16)((float)ke[u][4 + e] * sc1[u][e]);
-            }
-            akk = mfma32(af, kb[u], akk);
-            aqk = mfma32(af, qb[u], aqk);
-          }
-        }
-        // lane (n16, g4) holds A[16I + n16][16J + 4 g4 + r] (and likewise Aqk)
-        bf16x4_t lrow;
-        bf16x4_t qrow;
-  #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int j = 16 * J + 4 * g4 + r;
-          const float vk = (j < i) ? akk[r] * bi : 0.f;
-          lrow[r] = (bf16)vk;
-          qrow[r] = (bf16)((j <= i) ? aqk[r] : 0.f);
-          if (I == J) Ld[I][n16][4 * g4 + r] = vk;
-        }
-        *reinterpret_cast<bf16x4_t*>(&Lm[i][16 * J + 4 * g4]) = lrow;
-        {
-          unsigned char* afrag = sm + kOffAf + ((I * 2 + J / 2) * 64 + lane) * 16;
-          *reinterpret_cast<bf16x4_t*>(afrag + (J & 1) * 8) = qrow;
-          if (I == J && (I & 1) == 0) *reinterpret_cast<bf16x4_t*>(afrag + 8) = bf16x4_t{};  // tile J = I+1 is above
-        }
-      }
+      p2_pair(wave);
+      if (wave < 2) p2_pair(wave + 8);
     } else {
-      // ---- loader wave w' = wave - 4 owns channels 32 w' .. 32 w' + 31: their
-      // K~^T fragments (ct = 2 w', 2 w' + 1) from the channel-major k E rows,
-      // then the -Kgamma fragments (I, s = w') written over those same rows
-      const int wl = wave - 4;
-      {
-        bf16x4_t lo[4], hi[4];
-        float elo[4], ehi[4];
-  #pragma unroll
-        for (int k = 0; k < 4; ++k) {  // fragment (ct, s') = (2 w' + k / 2, k % 2), lane (c, g)
-          const int ch = 32 * wl + 16 * (k >> 1) + n16, r0 = 32 * (k & 1) + 4 * g4;
-          lo[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0]);
-          hi[k] = *reinterpret_cast<const bf16x4_t*>(&KEt[ch][r0 + 16]);
-          elo[k] = Ge[r0 >> 4][ch];  // rows r0 .. r0 + 3 sit in one block, as do r0 + 16 ..
-          ehi[k] = Ge[(r0 + 16) >> 4][ch];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-  #pragma unroll
-        for (int k = 0; k < 4; ++k) {
-          bf16x8_t o;
-  #pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            o[e] = (bf16)((float)lo[k][e] * elo[k]);
-            o[4 + e] = (bf16)((float)hi[k][e] * ehi[k]);
-          }
-          *lds<bf16x8_t>(sm, kOffKTf + ((4 * wl + k) * 64 + lane) * 16) = o;  // fragment 2 ct + s'
-        }
-      }
       if constexpr (LOADER) nl.template load_part<2>();
-      // -Kgamma = -exp(lg) k fragments (I, s = w'), lane (i, g), over this
-      // wave's own channel-major rows (read above, in order before these writes)
-      {
-        bf16x4_t lo[4], hi[4];
-        f32x4_t glo[4], ghi[4];
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          const int c0 = 32 * wl + 4 * g4;
-          const bf16* row = nat_row(sm, kOffKA, 16 * I + n16);
-          lo[I] = *reinterpret_cast<const bf16x4_t*>(row + c0);
-          hi[I] = *reinterpret_cast<const bf16x4_t*>(row + c0 + 16);
-          glo[I] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0]);
-          ghi[I] = *reinterpret_cast<const f32x4_t*>(&Gs[I][c0 + 16]);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-        for (int I = 0; I < 4; ++I) {
-          bf16x8_t o;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            o[e] = (bf16)(-(float)lo[I][e] * glo[I][e]);
-            o[4 + e] = (bf16)(-(float)hi[I][e] * ghi[I][e]);
-          }
-          *lds<bf16x8_t>(sm, kgf_off<MODE>(I, wl) + lane * 16) = o;
-        }
-      }
+      p2_pair(wave);
     }
   }
   if constexpr (LOADER) nl.template load_part<3>();
@@ -1178,9 +1233,9 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
   auto load_step = [&](int st, bf16x8_t (&kf)[4], bf16x8_t (&qf)[4]) {
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
-      kf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kgf_off<MODE>(I, st) + lane * 16);
+      kf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kgf_off<MODE>(I, st) + qk_slot<MODE>(I, lane) * 16);
       if constexpr (kWritesOut<MODE>)
-        qf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kOffQf + ((I * 4 + st) * 64 + lane) * 16);
+        qf[I] = *reinterpret_cast<const bf16x8_t*>(sm + kOffQf + ((I * 4 + st) * 64 + qk_slot<MODE>(I, lane)) * 16);
     }
   };
   bf16x8_t kfa[4], qfa[4], kfb[4], qfb[4];
@@ -1268,7 +1323,7 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
       gm[c4] = *reinterpret_cast<const f32x4_t*>(gam + 16 * ct + 4 * g4);
 #pragma unroll
       for (int sp = 0; sp < 2; ++sp)
-        kt[c4][sp] = *reinterpret_cast<const bf16x8_t*>(sm + kOffKTf + ((ct * 2 + sp) * 64 + lane) * 16);
+        kt[c4][sp] = *reinterpret_cast<const bf16x8_t*>(sm + kOffKTf + ((ct * 2 + sp) * 64 + kt_slot<MODE>(ct, lane)) * 16);
     }
 #pragma unroll
     for (int c4 = 0; c4 < 4; ++c4) {
@@ -1389,6 +1444,27 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
         }
       }
     }
+    if constexpr (MODE == kOutputMA) {
+      // two barriers per chunk: the loaders' operand writes end at the first,
+      // the scanners' reads of them at the second; the outputs of a chunk are
+      // stored (through a stage that the operand writes do not touch) while
+      // the loaders write the next chunk's operands
+      for (int64_t c = c_begin; c < c_end; ++c) {
+        const ChunkGeo geo = chunk_geo(sr, c - cs);
+        const int tid_c = opaque(tid);
+        __syncthreads();
+        const int tile0 = 2 * w;
+        f32x4_t O[2][4];
+        const int ut[2] = {tile0 < nvt ? tile0 : -1, tile0 + 1 < nvt ? tile0 + 1 : -1};
+        if (tile0 < ntiles) scan_pair<MODE>(sm, S[0], ut, tid_c & 63, O);
+        __syncthreads();
+        if (tile0 < ntiles) {
+          const int nt = ntiles - tile0 < 2 ? ntiles - tile0 : 2;
+          store_out<IT>(O, nt, a.out, geo, a.H, h, a.V, col0 + 16 * tile0, tid_c & 63,
+                        lds<IT>(sm, kOffStage + w * 4096));
+        }
+      }
+    } else {
     P1Out none;
     const NextLoads<IT, MODE> nl{};
     for (int64_t c = c_begin; c < c_end; ++c) {
@@ -1414,6 +1490,27 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
           }
         }
       }
+      __syncthreads();
+    }
+    }
+  } else if constexpr (MODE == kOutputMA) {
+    // ---------------- loaders, phase C without P2 ----------------
+    Raw<IT> raw;
+    P1Out po;
+    const LoaderLanes ll = loader_lanes<IT>(a, vcg, tid);
+    if (c_begin < c_end) {
+      load_raw<IT, MODE>(raw, chunk_loads<IT>(a, chunk_geo(sr, c_begin - cs), c_begin, h, col0), ll, tid);
+      p1_math_ma<IT>(po, raw, tid);
+    }
+    for (int64_t c = c_begin; c < c_end; ++c) {
+      const int tid_c = opaque(tid);
+      const NextLoads<IT, MODE> nl{&raw, chunk_loads<IT>(a, chunk_geo(sr, c + 1 - cs), c + 1, h, col0, c + 1 < c_end),
+                                   &ll, tid_c};
+      p1_write_ma<IT, MODE>(sm, po, ll, tid_c, nl);
+      __syncthreads();
+      nl.template load_part<6>();
+      nl.template load_part<7>();
+      if (c + 1 < c_end) p1_math_ma<IT>(po, raw, tid_c);
       __syncthreads();
     }
   } else {

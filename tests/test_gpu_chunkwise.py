@@ -245,5 +245,9 @@ def test_chunkwise_segmented_equals_single_segment(monkeypatch):
     seg = kda.chunkwise_kda(*d, True)
     assert rel_err(seg.hidden_states, one.hidden_states.float()) < 1e-2
     assert rel_err(seg.final_state, one.final_state) < 1e-2
-    # the first segment of a sequence runs the same arithmetic as the unsegmented kernel
-    assert torch.equal(seg.hidden_states[:, :256], one.hidden_states[:, :256])
+    # the first segment of a sequence runs the unsegmented kernel's arithmetic
+    # except for the rounding of its Q~, Kgamma and K~ operands (the segmented
+    # output pass rounds them once from f32, the unsegmented kernel twice,
+    # through its decayed natural tiles): within two bf16 steps of the
+    # largest output
+    assert rel_err(seg.hidden_states[:, :256], one.hidden_states[:, :256].float()) < 8e-3
