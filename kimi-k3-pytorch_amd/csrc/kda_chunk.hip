@@ -544,17 +544,17 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 template <class IT, int MODE>
 __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const ChunkGeo& cg, int vcg, int tid) {
+  // rows past the chunk's valid tokens were read as zero (g = 0, k = q = 0),
+  // so they give a unit decay and zero operands without a test
   const int J = loader_block(tid);
-  const int n_valid = cg.n_valid;
   const int lane = tid & 63;
   float al[2][16];
   float pj[2] = {1.f, 1.f};  // P_J = exp(lg_{16J+15} - lg_{16J})
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const bool ok = 16 * J + r < n_valid;
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
-      al[ch][r] = ok ? fast_exp(to_float(raw.gp[r][ch])) : 1.f;
+      al[ch][r] = fast_exp(to_float(raw.gp[r][ch]));
       if (r > 0) pj[ch] *= al[ch][r];
     }
   }
@@ -593,13 +593,12 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
   float run[2] = {1.f, 1.f};
 #pragma unroll
   for (int r = 0; r < 16; ++r) {
-    const bool ok = 16 * J + r < n_valid;
     float kv[2], qv[2];
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
       if (r > 0) run[ch] *= al[ch][r];
-      kv[ch] = ok ? to_float(raw.kp[r][ch]) * run[ch] : 0.f;
-      qv[ch] = ok ? to_float(raw.qp[r][ch]) * run[ch] : 0.f;
+      kv[ch] = to_float(raw.kp[r][ch]) * run[ch];
+      qv[ch] = to_float(raw.qp[r][ch]) * run[ch];
     }
     po.ka[r] = pack_bf16x2(kv[0], kv[1]);
     po.qa[r] = pack_bf16x2(qv[0], qv[1]);
@@ -608,10 +607,9 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
   float suf[2] = {1.f, 1.f};
 #pragma unroll
   for (int r = 15; r >= 0; --r) {
-    const bool ok = 16 * J + r < n_valid;
     float kv[2];
 #pragma unroll
-    for (int ch = 0; ch < 2; ++ch) kv[ch] = ok ? to_float(raw.kp[r][ch]) * suf[ch] : 0.f;
+    for (int ch = 0; ch < 2; ++ch) kv[ch] = to_float(raw.kp[r][ch]) * suf[ch];
     po.ke[r] = pack_bf16x2(kv[0], kv[1]);
     if constexpr (MODE == kSummary) po.kt[r] = pack_bf16x2(kv[0] * po.ge[0], kv[1] * po.ge[1]);
 #pragma unroll
@@ -632,7 +630,7 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
     }
     po.vv[i] = val;
   }
-  po.bt = (t2 < kChunk && t2 < n_valid) ? to_float(raw.bt) : 0.f;
+  po.bt = (t2 < kChunk && t2 < cg.n_valid) ? to_float(raw.bt) : 0.f;
 }
 
 // Operand rows of a loader thread (block J, channel pair cp) written straight
