@@ -17,6 +17,8 @@ Metric: "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s".
 * cpu_baseline: the oracle's PyTorch-CPU restatement of the reference path
                (oracle/kda_oracle.py) on a bounded sample of the same
                workload, on the host cores (thread count reported).
+* fused_stages: the kernels around the operator (kda.fused) on the same
+               shape, as HBM GB/s (not part of `value`).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3]
 """
@@ -180,6 +182,63 @@ def bench_decode(warmup):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / D_STEPS
+
+
+def bench_fused(reps=50):
+    """The fused stages around the operator on the prefill shape (B=1, T=8192,
+    H=16, D=128, bf16): ShortConv + SiLU + L2 norm of one projection, the
+    decay and beta gates in one launch, and RMSNorm with the output gate.
+    Each is launched `reps` times back to back through the C ABI into
+    preallocated outputs, between two HIP events on the launch stream;
+    algorithmic bytes = every input read once and every output written once
+    (the conv weight and gate parameters, a few KiB, are not counted)."""
+    import torch
+
+    from kda import _lib, _prep
+
+    lib = _lib.load()
+    device = torch.device("cuda", 0)
+    gen = torch.Generator(device=device).manual_seed(7)
+    B, T, H, D = P_B, P_T, P_H, P_K
+    C = H * D
+    rnd = lambda *shape: torch.randn(*shape, generator=gen, device=device).to(torch.bfloat16)  # noqa: E731
+    x, w, y = rnd(B, T, C), rnd(C, 4), rnd(B, T, C)
+    z, zb, a_log, bl = rnd(B, T, H, D), rnd(H, D), torch.zeros(H, device=device), rnd(B, T, H)
+    g, alpha, beta = torch.empty_like(z), torch.empty_like(z), torch.empty_like(bl)
+    o, nw, gl, out = rnd(B, T, H, D), rnd(H, D), rnd(B, T, C), rnd(B, T, H, D)
+    bf, el = _lib.dtype_code(torch.bfloat16), 2
+    stream = _prep.stream(device)
+    cases = {
+        "conv_silu_l2norm": (
+            lambda: lib.kda_conv_silu_fwd(x.data_ptr(), w.data_ptr(), None, None, y.data_ptr(), None, None,
+                                          B, T, C, 4, D, 1, 1e-6, bf, stream),
+            2 * B * T * C * el),
+        "decay_and_beta_gates": (
+            lambda: lib.kda_gates_fwd(z.data_ptr(), zb.data_ptr(), a_log.data_ptr(), -5.0, g.data_ptr(),
+                                      alpha.data_ptr(), bl.data_ptr(), beta.data_ptr(), B * T, H, D, bf, stream),
+            3 * B * T * H * D * el + 2 * B * T * H * el),
+        "rmsnorm_output_gate": (
+            lambda: lib.kda_rmsnorm_gate_fwd(o.data_ptr(), nw.data_ptr(), 1, gl.data_ptr(), out.data_ptr(),
+                                             B * T, H, D, 1e-6, bf, stream),
+            3 * B * T * H * D * el),
+    }
+    res = {}
+    for name, (fn, nbytes) in cases.items():
+        for _ in range(3):
+            _lib.check(fn())
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"ms": round(ms, 5), "algorithmic_bytes": nbytes, "achieved_gbs": round(gbs, 1),
+                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    return res
 
 
 def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
@@ -348,6 +407,10 @@ def main() -> int:
                 "algorithmic_bytes": dbytes,
             },
         },
+    }
+    result["fused_stages"] = {
+        "workload": f"B={P_B} T={P_T} H={P_H} D={P_K} bf16, one call each (median of 20)",
+        "kernels": bench_fused(),
     }
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 2
+#define KDA_ABI_VERSION 3
 
 /* status codes */
 #define KDA_OK 0
@@ -142,6 +142,60 @@ int kda_ut_transform(const void* k, const void* v, const void* g, const void* be
                      void* M, void* U, void* W, void* log_gamma, void* k_gamma, int out_dtype,
                      int64_t batch, int64_t count, int64_t heads, int64_t key_dim,
                      int64_t value_dim, void* stream);
+
+/*
+ * Fused stages around the operator.  Tensors are contiguous, of one dtype
+ * (`dtype`: f32, f16, bf16 or f64); arithmetic is f32 (f64 for f64) with one
+ * rounding to the output type.
+ *
+ * ShortConv + SiLU, and for q/k the per-head L2 normalisation, of one
+ * projection: y = silu(causal_depthwise_conv(x)) [/ max(||y_head||_2, eps)].
+ * Replaces, for one of q/k/v, KDAProjections._run_conv + F.silu (+ F.normalize)
+ * (src/kda/projections.py:100-140,164-206) over CausalShortConv1D
+ * (src/kimi_primitives/short_conv.py:69-98).
+ *   x, y         : [batch, tokens, channels]
+ *   weight       : [channels, kernel_size] in lag order (weight[c, j] multiplies x[t - j]); kernel_size <= 8
+ *   bias         : [channels] or NULL
+ *   history_in   : [batch, kernel_size - 1, channels] (the last inputs, oldest first) or NULL (zeros)
+ *   history_out  : same shape or NULL; receives the last kernel_size - 1 rows of [history | valid prefix]
+ *   valid_lens   : int32 [batch] right-padding lengths or NULL; padded outputs are zero and padding
+ *                  never enters the history
+ *   normalize    : nonzero for q/k; head_dim must then be a power of two in 16..512
+ * channels must be a multiple of 16 bytes' worth of elements; x, y and the histories are
+ * 16-byte aligned.  Each HBM row is read once and written once (one wave per 8-token tile).
+ */
+int kda_conv_silu_fwd(const void* x, const void* weight, const void* bias, const void* history_in,
+                      void* y, void* history_out, const int32_t* valid_lens, int64_t batch,
+                      int64_t tokens, int64_t channels, int64_t kernel_size, int64_t head_dim,
+                      int normalize, double eps, int dtype, void* stream);
+
+/*
+ * The lower-bounded decay g = g_min * clamp(sigmoid(exp(a_log[h]) * (z + decay_bias)), eps, 1 - eps),
+ * alpha = exp(g), and the beta gate clamp(sigmoid(beta_logits), eps, 1 - eps), with eps the
+ * machine epsilon of `dtype`.  Replaces LowerBoundedDecay.forward (src/kda/decay.py:30-43) with
+ * the decay-logit bias and the beta gate of KDAProjections.forward (src/kda/projections.py:207-218).
+ *   decay_logits, g, alpha : [rows, heads, key_dim], 16-byte aligned (alpha may be NULL); or all NULL;
+ *                            key_dim a multiple of 16 bytes' worth of elements
+ *   decay_bias             : [heads, key_dim], 16-byte aligned, or NULL;  a_log : f32 [heads]
+ *   beta_logits, beta      : [rows, heads] or NULL
+ */
+int kda_gates_fwd(const void* decay_logits, const void* decay_bias, const float* a_log, double g_min,
+                  void* g, void* alpha, const void* beta_logits, void* beta, int64_t rows,
+                  int64_t heads, int64_t key_dim, int dtype, void* stream);
+
+/*
+ * Head-wise RMSNorm x * rsqrt(mean(x^2) + eps) * weight, times sigmoid(gate_logits) when given:
+ * the input of the output projection.  Replaces HeadwiseRMSNorm.forward
+ * (src/kimi_primitives/headwise_rmsnorm.py:39-64) followed by the gate product of
+ * FullRankOutputGate.forward (src/kimi_primitives/output_gate.py:62-75).
+ *   x, y        : [rows, heads, head_dim], head_dim a power of two in 16..512
+ *   weight      : [heads, head_dim] (weight_per_head != 0), [head_dim], or NULL
+ *   gate_logits : [rows, heads * head_dim] (pre-sigmoid) or NULL
+ * All pointers 16-byte aligned.
+ */
+int kda_rmsnorm_gate_fwd(const void* x, const void* weight, int weight_per_head,
+                         const void* gate_logits, void* y, int64_t rows, int64_t heads,
+                         int64_t head_dim, double eps, int dtype, void* stream);
 
 #ifdef __cplusplus
 }

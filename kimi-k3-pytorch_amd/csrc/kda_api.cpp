@@ -228,4 +228,79 @@ int kda_ut_transform(const void* k, const void* v, const void* g, const void* be
                              key_dim, value_dim, static_cast<hipStream_t>(stream));
 }
 
+int kda_conv_silu_fwd(const void* x, const void* weight, const void* bias, const void* history_in, void* y,
+                      void* history_out, const int32_t* valid_lens, int64_t batch, int64_t tokens, int64_t channels,
+                      int64_t kernel_size, int64_t head_dim, int normalize, double eps, int dtype, void* stream) {
+  g_detail[0] = '\0';
+  if (!is_input_dtype(dtype)) {
+    set_detail("conv_silu: bad dtype %d", dtype);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (batch <= 0 || tokens <= 0 || channels <= 0 || kernel_size <= 0 || (normalize && head_dim <= 0)) {
+    set_detail("conv_silu: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (normalize && channels % head_dim != 0) {
+    set_detail("conv_silu: channels %lld not a multiple of head_dim %lld", (long long)channels, (long long)head_dim);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!x || !weight || !y) {
+    set_detail("conv_silu: x, weight and y must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!(eps > 0.0)) {
+    set_detail("conv_silu: eps must be > 0");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return launch_conv_silu(x, weight, bias, history_in, y, history_out, valid_lens, batch, tokens, channels,
+                          kernel_size, head_dim, normalize, eps, dtype, static_cast<hipStream_t>(stream));
+}
+
+int kda_gates_fwd(const void* decay_logits, const void* decay_bias, const float* a_log, double g_min, void* g,
+                  void* alpha, const void* beta_logits, void* beta, int64_t rows, int64_t heads, int64_t key_dim,
+                  int dtype, void* stream) {
+  g_detail[0] = '\0';
+  if (!is_input_dtype(dtype)) {
+    set_detail("gates: bad dtype %d", dtype);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (rows <= 0 || heads <= 0 || key_dim <= 0) {
+    set_detail("gates: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!(g_min < 0.0)) {
+    set_detail("gates: g_min must be negative");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!decay_logits && !beta_logits) {
+    set_detail("gates: nothing to do (both logits null)");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return launch_gates(decay_logits, decay_bias, a_log, g_min, g, alpha, beta_logits, beta, rows, heads, key_dim,
+                      dtype, static_cast<hipStream_t>(stream));
+}
+
+int kda_rmsnorm_gate_fwd(const void* x, const void* weight, int weight_per_head, const void* gate_logits, void* y,
+                         int64_t rows, int64_t heads, int64_t head_dim, double eps, int dtype, void* stream) {
+  g_detail[0] = '\0';
+  if (!is_input_dtype(dtype)) {
+    set_detail("rmsnorm_gate: bad dtype %d", dtype);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (rows <= 0 || heads <= 0 || head_dim <= 0) {
+    set_detail("rmsnorm_gate: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!x || !y) {
+    set_detail("rmsnorm_gate: x and y must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!(eps > 0.0)) {
+    set_detail("rmsnorm_gate: eps must be > 0");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return launch_rmsnorm_gate(x, weight, weight_per_head, gate_logits, y, rows, heads, head_dim, eps, dtype,
+                             static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

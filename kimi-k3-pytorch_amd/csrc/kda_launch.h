@@ -36,4 +36,15 @@ int launch_ut_transform(const void* k, const void* v, const void* g, const void*
                         void* U, void* W, void* log_gamma, void* k_gamma, int out_dtype, int64_t batch,
                         int64_t count, int64_t heads, int64_t key_dim, int64_t value_dim, hipStream_t stream);
 
+// Fused stages around the operator (csrc/kda_fused.hip).
+int launch_conv_silu(const void* x, const void* w, const void* bias, const void* hist_in, void* y, void* hist_out,
+                     const int32_t* valid_lens, int64_t B, int64_t T, int64_t C, int64_t K, int64_t head_dim,
+                     int normalize, double eps, int dtype, hipStream_t stream);
+
+int launch_gates(const void* z, const void* zbias, const float* a_log, double g_min, void* g, void* alpha,
+                 const void* bl, void* beta, int64_t rows, int64_t H, int64_t K, int dtype, hipStream_t stream);
+
+int launch_rmsnorm_gate(const void* x, const void* w, int w_per_head, const void* gl, void* y, int64_t rows,
+                        int64_t H, int64_t D, double eps, int dtype, hipStream_t stream);
+
 }  // namespace kda_host

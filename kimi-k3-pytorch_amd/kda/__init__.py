@@ -3,10 +3,12 @@
 Mirrors the operator surface of pablo-reyes8/kimi-k3-pytorch ``src/kda``
 (src/kda/__init__.py:1-25): ``chunkwise_kda``, ``recurrent_kda``,
 ``ut_transform``, ``KDAOperatorOutput``, ``UTTransformOutput`` and
-``KDAState``.  All arithmetic runs in hand-written HIP kernels in
-``libkda_mi355x.so``; see include/kda_mi355x.h for the C ABI.
+``KDAState``, plus the fused stages around the operator in ``kda.fused``.
+All arithmetic runs in hand-written HIP kernels in ``libkda_mi355x.so``; see
+include/kda_mi355x.h for the C ABI.
 """
 
+from . import fused
 from .chunkwise import chunkwise_kda
 from .recurrent import KDAOperatorOutput, recurrent_kda
 from .state import KDAState, ShortConvState
@@ -18,6 +20,7 @@ __all__ = [
     "ShortConvState",
     "UTTransformOutput",
     "chunkwise_kda",
+    "fused",
     "recurrent_kda",
     "ut_transform",
 ]

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libkda_mi355x.so")
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 KDA_OK = 0
 KDA_ERR_INVALID_ARGUMENT = 1
@@ -52,6 +52,15 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P, _S, _P, _P, _P],
     ),
     "kda_ut_transform": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _P]),
+    "kda_conv_silu_fwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _I, ctypes.c_double, _I, _P],
+    ),
+    "kda_gates_fwd": (
+        _I,
+        [_P, _P, _P, ctypes.c_double, _P, _P, _P, _P, _L, _L, _L, _I, _P],
+    ),
+    "kda_rmsnorm_gate_fwd": (_I, [_P, _P, _I, _P, _P, _L, _L, _L, ctypes.c_double, _I, _P]),
 }
 
 _lock = threading.Lock()

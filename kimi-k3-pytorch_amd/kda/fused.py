@@ -1,0 +1,241 @@
+"""Fused stages around the KDA operator, one HIP kernel each.
+
+* ``conv_silu``: the ShortConv + SiLU (+ per-head L2 normalisation for q and
+  k) that KDAProjections applies to each projection
+  (src/kda/projections.py:100-140,164-206 over CausalShortConv1D,
+  src/kimi_primitives/short_conv.py:69-98), with its incremental history and
+  right-padding semantics; decode is the T=1 case.
+* ``lower_bounded_decay`` / ``beta_gate``: LowerBoundedDecay
+  (src/kda/decay.py:30-43, with the decay-logit bias of
+  projections.py:211-218) and the beta gate (projections.py:207-209).
+* ``rmsnorm_gate``: HeadwiseRMSNorm (src/kimi_primitives/headwise_rmsnorm.py:39-64)
+  times the sigmoid output gate (src/kimi_primitives/output_gate.py:62-75),
+  i.e. the input of the output projection.
+
+Every function runs on the tensors' GPU stream through libkda_mi355x.so and
+returns new tensors; there is no CPU fallback.  Arithmetic is f32 (f64 for
+f64 tensors) with one rounding to the tensors' dtype, where the reference
+rounds after each step in the model dtype.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib, _prep
+from .state import ShortConvState
+from .utils import validate_attention_mask
+
+_DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.float64)
+
+
+def _check_dtype(name: str, tensor: torch.Tensor, dtype: torch.dtype) -> None:
+    if tensor.dtype != dtype:
+        raise TypeError(f"{name} must have dtype {dtype}, got {tensor.dtype}")
+
+
+def _check_device(name: str, tensor: torch.Tensor, device: torch.device) -> None:
+    if tensor.device != device:
+        raise ValueError(f"{name} must be on {device}, got {tensor.device}")
+
+
+def _aligned(tensor: torch.Tensor) -> torch.Tensor:
+    """Contiguous and 16-byte aligned (the kernels move 16-byte vectors)."""
+    tensor = tensor.contiguous()
+    return tensor if tensor.data_ptr() % 16 == 0 else tensor.clone()
+
+
+def conv_silu(
+    x: torch.Tensor,
+    weight: torch.Tensor,
+    bias: torch.Tensor | None = None,
+    state: ShortConvState | None = None,
+    attention_mask: torch.Tensor | None = None,
+    *,
+    num_heads: int | None = None,
+    normalize: bool = False,
+    eps: float = 1e-6,
+    output_final_state: bool = False,
+) -> tuple[torch.Tensor, ShortConvState | None]:
+    """Depthwise causal ShortConv over ``x [B,T,C]``, SiLU, and optionally
+    L2 normalisation over each of ``num_heads`` heads.
+
+    ``weight [C,K]`` is in lag order (``weight[c, j]`` multiplies ``x[t-j]``,
+    short_conv.py:12-18); ``state`` carries the last ``K-1`` inputs.  Right
+    padding (``attention_mask``) gives zero outputs and never enters the
+    returned history (projections.py:119-140).  Returns ``y`` as ``[B,T,H,C/H]``
+    when ``num_heads`` is given (``[B,T,C]`` otherwise) and the next state when
+    ``output_final_state``.
+    """
+    if x.ndim != 3:
+        raise ValueError(f"x must have shape [B,T,C], got {tuple(x.shape)}")
+    batch, tokens, channels = x.shape
+    if tokens == 0:
+        raise ValueError("conv_silu does not support empty sequences")
+    if x.dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {x.dtype}")
+    if weight.ndim != 2 or weight.shape[0] != channels or weight.shape[1] < 1:
+        raise ValueError(f"weight must have shape [{channels},K], got {tuple(weight.shape)}")
+    kernel_size = weight.shape[1]
+    _check_dtype("weight", weight, x.dtype)
+    _check_device("weight", weight, x.device)
+    if bias is not None:
+        if bias.shape != (channels,):
+            raise ValueError(f"bias must have shape [{channels}], got {tuple(bias.shape)}")
+        _check_dtype("bias", bias, x.dtype)
+        _check_device("bias", bias, x.device)
+    if state is not None:
+        expected = (batch, kernel_size - 1, channels)
+        if state.buffer.shape != expected:
+            raise ValueError(f"state buffer must have shape {expected}, got {tuple(state.buffer.shape)}")
+        _check_dtype("state buffer", state.buffer, x.dtype)
+        _check_device("state buffer", state.buffer, x.device)
+    if num_heads is not None and (num_heads <= 0 or channels % num_heads != 0):
+        raise ValueError(f"channels {channels} must split into num_heads={num_heads} heads")
+    if normalize and num_heads is None:
+        raise ValueError("normalize needs num_heads")
+    if eps <= 0:
+        raise ValueError("eps must be > 0")
+    validate_attention_mask(attention_mask, batch, tokens)
+    _lib.require_gpu(x)
+    _prep.reject_autograd(x, weight, bias, None if state is None else state.buffer)
+    lib = _lib.load()
+
+    head_dim = channels // num_heads if num_heads is not None else channels
+    xc = _aligned(x)
+    wc = weight.contiguous()
+    bc = None if bias is None else bias.contiguous()
+    hist = None if state is None or kernel_size == 1 else _aligned(state.buffer)
+    y = torch.empty_like(xc)
+    hist_out = None
+    if output_final_state:
+        hist_out = torch.empty(batch, kernel_size - 1, channels, dtype=x.dtype, device=x.device)
+    valid = _prep.valid_lengths(attention_mask, x.device)
+    status = lib.kda_conv_silu_fwd(
+        xc.data_ptr(), wc.data_ptr(), _lib.ptr(bc), _lib.ptr(hist), y.data_ptr(),
+        _lib.ptr(hist_out) if hist_out is not None and kernel_size > 1 else None, _lib.ptr(valid),
+        batch, tokens, channels, kernel_size, head_dim, 1 if normalize else 0, float(eps),
+        _lib.dtype_code(x.dtype), _prep.stream(x.device),
+    )
+    _lib.check(status)
+    if num_heads is not None:
+        y = y.view(batch, tokens, num_heads, head_dim)
+    return y, (ShortConvState(hist_out) if hist_out is not None else None)
+
+
+def _gates(decay_logits, a_log, g_min, bias, beta_logits, want_alpha):
+    ref = decay_logits if decay_logits is not None else beta_logits
+    if ref.dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {ref.dtype}")
+    g = alpha = beta = None
+    rows = heads = key_dim = 0
+    z = zb = al = None
+    if decay_logits is not None:
+        if decay_logits.ndim != 4:
+            raise ValueError(f"logits must have shape [B,T,H,K], got {tuple(decay_logits.shape)}")
+        batch, tokens, heads, key_dim = decay_logits.shape
+        rows = batch * tokens
+        _lib.require_gpu(decay_logits)
+        if a_log.shape != (heads,):
+            raise ValueError(f"A_log must have shape [{heads}], got {tuple(a_log.shape)}")
+        _check_device("A_log", a_log, decay_logits.device)
+        if g_min >= 0:
+            raise ValueError("g_min must be negative")
+        if bias is not None:
+            if bias.shape != (heads, key_dim):
+                raise ValueError(f"bias must have shape [{heads},{key_dim}], got {tuple(bias.shape)}")
+            _check_device("bias", bias, decay_logits.device)
+            zb = _aligned(bias.to(decay_logits.dtype))
+        z = _aligned(decay_logits)
+        al = a_log.to(torch.float32).contiguous()
+        g = torch.empty_like(z)
+        alpha = torch.empty_like(z) if want_alpha else None
+    if beta_logits is not None:
+        if beta_logits.ndim < 1:
+            raise ValueError("beta logits must have at least one dimension")
+        _lib.require_gpu(beta_logits)
+        bl = beta_logits.contiguous()
+        beta = torch.empty_like(bl)
+        if decay_logits is None:
+            rows, heads, key_dim = 1, bl.numel(), 1
+        elif bl.numel() != rows * heads:
+            raise ValueError("beta logits must have shape [B,T,H] matching the decay logits")
+    else:
+        bl = None
+    _prep.reject_autograd(decay_logits, a_log, bias, beta_logits)
+    lib = _lib.load()
+    status = lib.kda_gates_fwd(
+        _lib.ptr(z), _lib.ptr(zb), _lib.ptr(al), float(g_min), _lib.ptr(g), _lib.ptr(alpha),
+        _lib.ptr(bl), _lib.ptr(beta), rows, heads, key_dim, _lib.dtype_code(ref.dtype), _prep.stream(ref.device),
+    )
+    _lib.check(status)
+    return g, alpha, beta
+
+
+def lower_bounded_decay(
+    logits: torch.Tensor,
+    a_log: torch.Tensor,
+    g_min: float = -5.0,
+    *,
+    bias: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(g, exp(g))`` with ``g = g_min * clamp(sigmoid(exp(A_log) * (logits + bias)), eps, 1-eps)``
+    for ``logits [B,T,H,K]``, ``A_log [H]`` and an optional bias ``[H,K]``
+    (decay.py:30-43; eps is the dtype's machine epsilon)."""
+    g, alpha, _ = _gates(logits, a_log, g_min, bias, None, True)
+    return g, alpha
+
+
+def beta_gate(logits: torch.Tensor) -> torch.Tensor:
+    """``clamp(sigmoid(logits), eps, 1-eps)`` elementwise (projections.py:207-209)."""
+    _, _, beta = _gates(None, None, -1.0, None, logits, False)
+    return beta
+
+
+def rmsnorm_gate(
+    x: torch.Tensor,
+    weight: torch.Tensor | None = None,
+    eps: float = 1e-6,
+    *,
+    gate_logits: torch.Tensor | None = None,
+) -> torch.Tensor:
+    """Head-wise RMSNorm of ``x [B,T,H,D]`` (weight ``[H,D]`` per head, ``[D]``
+    shared, or None), times ``sigmoid(gate_logits)`` (``[B,T,H*D]``) when given.
+    headwise_rmsnorm.py:39-64 and output_gate.py:62-75."""
+    if x.ndim != 4:
+        raise ValueError(f"x must have shape [B,T,H,Dh], got {tuple(x.shape)}")
+    if x.dtype not in _DTYPES:
+        raise TypeError(f"unsupported dtype {x.dtype}")
+    batch, tokens, heads, head_dim = x.shape
+    per_head = 0
+    if weight is not None:
+        if weight.shape == (heads, head_dim):
+            per_head = 1
+        elif weight.shape != (head_dim,):
+            raise ValueError(f"weight must have shape [{heads},{head_dim}] or [{head_dim}], got {tuple(weight.shape)}")
+        _check_device("weight", weight, x.device)
+    if gate_logits is not None:
+        if gate_logits.shape != (batch, tokens, heads * head_dim):
+            raise ValueError(
+                f"gate_logits must have shape {(batch, tokens, heads * head_dim)}, got {tuple(gate_logits.shape)}"
+            )
+        _check_dtype("gate_logits", gate_logits, x.dtype)
+        _check_device("gate_logits", gate_logits, x.device)
+    if eps <= 0:
+        raise ValueError("eps must be > 0")
+    _lib.require_gpu(x)
+    _prep.reject_autograd(x, weight, gate_logits)
+    lib = _lib.load()
+    xc = _aligned(x)
+    wc = None if weight is None else _aligned(weight.to(x.dtype))
+    gc = None if gate_logits is None else _aligned(gate_logits)
+    y = torch.empty_like(xc)
+    status = lib.kda_rmsnorm_gate_fwd(
+        xc.data_ptr(), _lib.ptr(wc), per_head, _lib.ptr(gc), y.data_ptr(), batch * tokens, heads, head_dim,
+        float(eps), _lib.dtype_code(x.dtype), _prep.stream(x.device),
+    )
+    _lib.check(status)
+    return y
+
+
+__all__ = ["beta_gate", "conv_silu", "lower_bounded_decay", "rmsnorm_gate"]

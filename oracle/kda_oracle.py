@@ -19,6 +19,12 @@ CPU baseline, but the code is written independently:
   (the reference has no ``cu_seqlens``); they are defined as independent runs
   of the functions above on each document, which is the semantics the GPU
   path implements.
+* ``short_conv``           follows ``src/kimi_primitives/short_conv.py:69-98``
+* ``conv_silu``            follows ``src/kda/projections.py:100-140,164-206``
+* ``lower_bounded_decay``  follows ``src/kda/decay.py:30-43`` (+ projections.py:211-218)
+* ``beta_gate``            follows ``src/kda/projections.py:207-209``
+* ``rmsnorm_gate``         follows ``src/kimi_primitives/headwise_rmsnorm.py:39-64``
+  and the gate product of ``src/kimi_primitives/output_gate.py:62-75``
 
 How each function is pinned (tests/test_oracle_*.py):
 
@@ -33,6 +39,12 @@ How each function is pinned (tests/test_oracle_*.py):
 * ``chunkwise``: equality with ``recurrent`` in float64 at 2e-11 over the
   reference's shape/chunk grid, prefix causality and mask==truncation.
 * varlen: per-document equality (by construction) plus state reset checks.
+* ``short_conv``: ``torch.nn.functional.conv1d`` on the history-padded input,
+  streaming (two calls chained through the history equal one call).
+* ``conv_silu``: masked rows equal the truncated run, unit head norms.
+* ``lower_bounded_decay`` / ``beta_gate``: the sigmoid midpoint, the clamp
+  bounds, monotonicity.
+* ``rmsnorm_gate``: unit mean square, scale invariance, the gate midpoint.
 
 Rounding: the reference's bit-level float32/bfloat16 rounding order (einsum /
 BLAS / LAPACK) is not reproduced; parity is judged with tolerances.
@@ -51,6 +63,11 @@ __all__ = [
     "chunkwise",
     "varlen_recurrent",
     "varlen_chunkwise",
+    "short_conv",
+    "conv_silu",
+    "lower_bounded_decay",
+    "beta_gate",
+    "rmsnorm_gate",
 ]
 
 
@@ -220,3 +237,95 @@ def varlen_chunkwise(q, k, v, g, beta, cu_seqlens, initial_states=None, *,
         outs.append(o)
         finals.append(s)
     return torch.cat(outs, dim=1), torch.cat(finals, dim=0)
+
+
+
+# ---- the fused stages around the operator ------------------------------------
+
+def _compute_dtype(dtype: torch.dtype) -> torch.dtype:
+    return torch.float64 if dtype == torch.float64 else torch.float32
+
+
+def short_conv(x, weight, bias=None, history=None):
+    """Depthwise causal convolution over ``x [B,T,C]`` with lag-ordered
+    ``weight [C,K]`` (``weight[c, j]`` multiplies ``x[t - j]``) and the last
+    ``K-1`` inputs ``history [B,K-1,C]`` (zeros when None), as
+    CausalShortConv1D.forward (src/kimi_primitives/short_conv.py:69-98).
+    Computes in f32 (f64 for f64); returns (y, next history)."""
+    cd = _compute_dtype(x.dtype)
+    batch, tokens, channels = x.shape
+    taps = weight.shape[1]
+    hist = (torch.zeros(batch, taps - 1, channels, dtype=x.dtype) if history is None else history)
+    combined = torch.cat((hist, x), dim=1).to(cd)
+    w = weight.to(cd)
+    y = torch.zeros(batch, tokens, channels, dtype=cd)
+    for j in range(taps):
+        # input at t - j sits at combined row (taps - 1) + t - j
+        y = y + w[:, j] * combined[:, taps - 1 - j:taps - 1 - j + tokens]
+    if bias is not None:
+        y = y + bias.to(cd)
+    nxt = combined[:, combined.shape[1] - (taps - 1):].to(x.dtype)
+    return y, nxt
+
+
+def conv_silu(x, weight, bias=None, history=None, attention_mask=None, *, num_heads=None,
+              normalize=False, eps=1e-6):
+    """ShortConv, SiLU and (``normalize``) L2 normalisation per head, with a
+    right-padded row run on its valid prefix only (padded outputs zero,
+    padding never in the history), as KDAProjections._run_conv and forward
+    (src/kda/projections.py:100-140,185-204).  Returns (y [B,T,C] in the
+    compute dtype, next history)."""
+    batch, tokens, channels = x.shape
+    outs, hists = [], []
+    for b in range(batch):
+        length = tokens if attention_mask is None else int(attention_mask[b].sum())
+        hb = None if history is None else history[b:b + 1]
+        y, nxt = short_conv(x[b:b + 1, :length], weight, bias, hb)
+        y = y * torch.sigmoid(y)
+        if normalize:
+            heads = y.reshape(1, length, num_heads, channels // num_heads)
+            norm = heads.square().sum(dim=-1, keepdim=True).sqrt()
+            y = (heads / torch.clamp(norm, min=eps)).reshape(1, length, channels)
+        outs.append(torch.cat((y, torch.zeros(1, tokens - length, channels, dtype=y.dtype)), dim=1))
+        hists.append(nxt)
+    return torch.cat(outs, dim=0), torch.cat(hists, dim=0)
+
+
+def _clamp_eps(p, dtype):
+    eps = torch.finfo(dtype).eps
+    return p.clamp(eps, 1.0 - eps)
+
+
+def lower_bounded_decay(logits, a_log, g_min=-5.0, bias=None):
+    """``g = g_min * clamp(sigmoid(exp(A_log[h]) * z), eps, 1-eps)``, ``alpha = exp(g)``
+    with ``z = logits (+ bias [H,K])`` and eps the logits dtype's machine
+    epsilon (src/kda/decay.py:30-43, projections.py:211-218).  Compute dtype
+    f32 (f64 for f64)."""
+    cd = _compute_dtype(logits.dtype)
+    z = logits.to(cd)
+    if bias is not None:
+        z = z + bias.to(cd)
+    scale = a_log.to(cd).exp()[None, None, :, None]
+    p = _clamp_eps(torch.sigmoid(scale * z), logits.dtype)
+    g = g_min * p
+    return g, g.exp()
+
+
+def beta_gate(logits):
+    """``clamp(sigmoid(logits), eps, 1-eps)`` (src/kda/projections.py:207-209)."""
+    return _clamp_eps(torch.sigmoid(logits.to(_compute_dtype(logits.dtype))), logits.dtype)
+
+
+def rmsnorm_gate(x, weight=None, eps=1e-6, gate_logits=None):
+    """``x * rsqrt(mean(x^2) + eps) * weight`` over each head of ``x [B,T,H,D]``
+    (src/kimi_primitives/headwise_rmsnorm.py:39-64), times
+    ``sigmoid(gate_logits)`` (``[B,T,H*D]``) when given
+    (src/kimi_primitives/output_gate.py:62-75)."""
+    cd = _compute_dtype(x.dtype)
+    xf = x.to(cd)
+    y = xf * torch.rsqrt(xf.square().mean(dim=-1, keepdim=True) + eps)
+    if weight is not None:
+        y = y * (weight.to(cd) if weight.ndim == 2 else weight.to(cd)[None, :])
+    if gate_logits is not None:
+        y = y * torch.sigmoid(gate_logits.to(cd)).reshape(x.shape)
+    return y

@@ -75,3 +75,25 @@ def test_binding_arity_matches_header():
     assert sorted(arities) == declared_functions()
     for name, (_, argtypes) in _lib.SIGNATURES.items():
         assert len(argtypes) == arities[name], name
+
+
+def test_fused_entry_points_reject_unsupported_layouts():
+    # every case fails a host-side check before anything is launched
+    lib = _lib.load()
+    bf16 = _lib.dtype_code(__import__("torch").bfloat16)
+    a, b = 4096, 8192  # 16-byte aligned stand-in addresses (never dereferenced)
+    conv = lambda **kw: lib.kda_conv_silu_fwd(  # noqa: E731
+        kw.get("x", a), a, None, None, b, None, None, 1, 8, kw.get("c", 256), kw.get("k", 4), kw.get("d", 128),
+        kw.get("norm", 1), 1e-6, bf16, None)
+    assert conv(k=9) == _lib.KDA_ERR_UNSUPPORTED
+    assert conv(c=288, d=96) == _lib.KDA_ERR_UNSUPPORTED  # normalised heads are powers of two
+    assert conv(c=260, norm=0) == _lib.KDA_ERR_UNSUPPORTED  # rows are whole 16-byte vectors
+    assert conv(x=a + 2) == _lib.KDA_ERR_INVALID_ARGUMENT  # misaligned
+    assert conv(c=250) == _lib.KDA_ERR_INVALID_ARGUMENT  # channels not a multiple of head_dim
+    gates = lambda z, k: lib.kda_gates_fwd(z, None, a, -5.0, b, None, None, None, 4, 2, k, bf16, None)  # noqa: E731
+    assert gates(a, 12) == _lib.KDA_ERR_UNSUPPORTED  # key_dim not a multiple of 8 bf16 elements
+    assert gates(a + 8, 16) == _lib.KDA_ERR_INVALID_ARGUMENT
+    norm = lambda x, d: lib.kda_rmsnorm_gate_fwd(x, None, 0, None, b, 4, 2, d, 1e-6, bf16, None)  # noqa: E731
+    assert norm(a, 96) == _lib.KDA_ERR_UNSUPPORTED
+    assert norm(a, 1024) == _lib.KDA_ERR_UNSUPPORTED
+    assert norm(a + 4, 128) == _lib.KDA_ERR_INVALID_ARGUMENT
