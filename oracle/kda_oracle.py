@@ -15,6 +15,8 @@ CPU baseline, but the code is written independently:
 * ``chunkwise``            follows ``src/kda/chunkwise.py:34-107``
 * ``work_dtype``           follows ``src/kda/utils.py:74-79``
 * ``mask_inputs``          follows ``src/kda/utils.py:82-94``
+* ``chunkwise_backward``   differentiates ``chunkwise`` (the reference gets
+  these gradients from autograd through src/kda/chunkwise.py:34-107)
 * ``varlen_chunkwise`` / ``varlen_recurrent`` have no reference counterpart
   (the reference has no ``cu_seqlens``); they are defined as independent runs
   of the functions above on each document, which is the semantics the GPU
@@ -39,6 +41,10 @@ How each function is pinned (tests/test_oracle_*.py):
 * ``chunkwise``: equality with ``recurrent`` in float64 at 2e-11 over the
   reference's shape/chunk grid, prefix causality and mask==truncation.
 * varlen: per-document equality (by construction) plus state reset checks.
+* ``chunkwise_backward``: torch.autograd through ``chunkwise`` and through
+  ``recurrent`` in f64 (the reference's own gradient tests,
+  tests/kda/test_kda_chunkwise_equivalence.py:92-134), gradcheck of
+  ``chunkwise``, chunk-size invariance, and extreme decays.
 * ``short_conv``: ``torch.nn.functional.conv1d`` on the history-padded input,
   streaming (two calls chained through the history equal one call).
 * ``conv_silu``: masked rows equal the truncated run, unit head norms.
@@ -63,6 +69,7 @@ __all__ = [
     "chunkwise",
     "varlen_recurrent",
     "varlen_chunkwise",
+    "chunkwise_backward",
     "short_conv",
     "conv_silu",
     "lower_bounded_decay",
@@ -238,6 +245,130 @@ def varlen_chunkwise(q, k, v, g, beta, cu_seqlens, initial_states=None, *,
         finals.append(s)
     return torch.cat(outs, dim=1), torch.cat(finals, dim=0)
 
+
+
+# ---- backward of the chunkwise operator ---------------------------------------
+
+def _pair_exp(lg):
+    """exp(lg_i - lg_j) for the position pairs j <= i of a chunk, zero above
+    the diagonal (where the exponent is positive and may overflow): [B,H,C,C,K]."""
+    n = lg.shape[2]
+    upper = torch.ones(n, n, dtype=torch.bool).triu(1)
+    diff = (lg.unsqueeze(3) - lg.unsqueeze(2)).masked_fill(upper[:, :, None], float("-inf"))
+    return diff.exp()
+
+
+def chunkwise_backward(q, k, v, g, beta, initial_state, d_out, d_final_state=None, *, chunk_size: int = 64):
+    """Gradients of ``chunkwise`` (src/kda/chunkwise.py:34-107, with the UT
+    transform of src/kda/ut_transform.py:23-58) written out chunk by chunk.
+
+    Inputs are the (already masked) operator inputs; ``d_out [B,T,H,V]`` and
+    ``d_final_state [B,H,K,V]`` (None: zero) are the upstream gradients.
+    Computes in f64 for f64 inputs and f32 otherwise and returns
+    ``(dq, dk, dv, dg, dbeta, d_initial_state)`` in that dtype.
+
+    Per chunk, with lg = cumsum(g), E_ij = exp(lg_i - lg_j), A = strict-lower
+    sum_k k_i k_j E_ij, Aqk = lower sum_k q_i k_j E_ij, N = (I + diag(b) A)^-1,
+    M = N diag(b), Kg = e^lg k, Qg = e^lg q, D = e^lg_last,
+    Kt = e^(lg_last - lg) k, W = M Kg, U = M v, Vt = U - W S:
+      forward   O = Qg S + Aqk Vt,   S' = D S + Kt^T Vt
+      backward  dVt = Kt dS' + Aqk^T dO
+                dS  = D dS' + Qg^T dO - W^T dVt
+                dQg = dO S^T, dAqk = tril(dO Vt^T), dKt = Vt dS'^T,
+                dD = rowsum(dS' * S), dW = -dVt S^T, dv = M^T dVt,
+                dM = dVt v^T + dW Kg^T, dKg = M^T dW,
+                db_j = sum_i N_ij dM_ij,  dL = -strict(N^T (dM diag b) N^T),
+                dA = diag(b) dL,  db_i += sum_j dL_ij A_ij,
+      then the pair sums of dA and dAqk, the exp factors, and
+      dg = reverse cumulative sum of d lg within the chunk.
+    """
+    cd = torch.float64 if q.dtype == torch.float64 else torch.float32
+    qw, kw, vw, gw, dO = (t.to(cd).transpose(1, 2) for t in (q, k, v, g, d_out))  # [B,H,T,*]
+    bw = beta.to(cd).transpose(1, 2)  # [B,H,T]
+    batch, heads, tokens, key_dim = qw.shape
+    value_dim = vw.shape[-1]
+    state = torch.zeros(batch, heads, key_dim, value_dim, dtype=cd)
+    if initial_state is not None:
+        state = state + initial_state.to(cd)
+    spans = [(s0, min(s0 + chunk_size, tokens)) for s0 in range(0, tokens, chunk_size)]
+
+    def chunk_terms(s0, s1):
+        qc, kc, vc, gc, bc = qw[:, :, s0:s1], kw[:, :, s0:s1], vw[:, :, s0:s1], gw[:, :, s0:s1], bw[:, :, s0:s1]
+        n = s1 - s0
+        lg = gc.cumsum(dim=2)
+        E = _pair_exp(lg)
+        strict = torch.ones(n, n, dtype=torch.bool).tril(-1)
+        lower = torch.ones(n, n, dtype=torch.bool).tril()
+        A = ((kc.unsqueeze(3) * kc.unsqueeze(2)) * E).sum(-1) * strict
+        Aqk = ((qc.unsqueeze(3) * kc.unsqueeze(2)) * E).sum(-1) * lower
+        L = torch.eye(n, dtype=cd) + bc.unsqueeze(-1) * A
+        N = torch.linalg.solve_triangular(L, torch.eye(n, dtype=cd).expand_as(L), upper=False, unitriangular=True)
+        M = N * bc.unsqueeze(-2)
+        last = lg[:, :, -1]
+        t = dict(q=qc, k=kc, v=vc, b=bc, lg=lg, E=E, A=A, Aqk=Aqk, N=N, M=M, strict=strict, lower=lower,
+                 Kg=lg.exp() * kc, Qg=lg.exp() * qc, D=last.exp(), Kt=(last.unsqueeze(2) - lg).exp() * kc)
+        t["W"] = M @ t["Kg"]
+        t["U"] = M @ vc
+        return t
+
+    starts = []
+    for s0, s1 in spans:  # forward: the state at each chunk start
+        c = chunk_terms(s0, s1)
+        starts.append(state)
+        vt = c["U"] - c["W"] @ state
+        state = c["D"].unsqueeze(-1) * state + c["Kt"].transpose(-2, -1) @ vt
+
+    dq, dk, dv, dg = (torch.zeros_like(x) for x in (qw, kw, vw, gw))
+    dbeta = torch.zeros_like(bw)
+    dS = torch.zeros(batch, heads, key_dim, value_dim, dtype=cd)
+    if d_final_state is not None:
+        dS = dS + d_final_state.to(cd)
+    for (s0, s1), S in zip(reversed(spans), reversed(starts)):
+        c = chunk_terms(s0, s1)
+        dOc = dO[:, :, s0:s1]
+        vt = c["U"] - c["W"] @ S
+        dvt = c["Kt"] @ dS + c["Aqk"].transpose(-2, -1) @ dOc
+        dQg = dOc @ S.transpose(-2, -1)
+        dAqk = (dOc @ vt.transpose(-2, -1)) * c["lower"]
+        dKt = vt @ dS.transpose(-2, -1)
+        dD = (dS * S).sum(-1)
+        dW = -dvt @ S.transpose(-2, -1)
+        dv[:, :, s0:s1] = c["M"].transpose(-2, -1) @ dvt
+        dM = dvt @ c["v"].transpose(-2, -1) + dW @ c["Kg"].transpose(-2, -1)
+        dKg = c["M"].transpose(-2, -1) @ dW
+        N, b = c["N"], c["b"]
+        db = (N * dM).sum(-2)
+        Nt = N.transpose(-2, -1)
+        dL = -(Nt @ (dM * b.unsqueeze(-2)) @ Nt) * c["strict"]
+        dA = b.unsqueeze(-1) * dL
+        db = db + (dL * c["A"]).sum(-1)
+        # pair sums: A_ij = sum_k k_i k_j E_ij (strict), Aqk_ij = sum_k q_i k_j E_ij (lower)
+        E, qc, kc = c["E"], c["q"], c["k"]
+        PA = dA.unsqueeze(-1) * E            # [B,H,i,j,K]
+        PQ = dAqk.unsqueeze(-1) * E
+        dk_c = (PA * kc.unsqueeze(2)).sum(3) + (PA * kc.unsqueeze(3)).sum(2) + (PQ * qc.unsqueeze(3)).sum(2)
+        dq_c = (PQ * kc.unsqueeze(2)).sum(3)
+        pa = PA * kc.unsqueeze(3) * kc.unsqueeze(2)
+        pq = PQ * qc.unsqueeze(3) * kc.unsqueeze(2)
+        dlg = pa.sum(3) - pa.sum(2) + pq.sum(3) - pq.sum(2)
+        # exp factors
+        elg = c["lg"].exp()
+        dk_c = dk_c + elg * dKg
+        dlg = dlg + c["Kg"] * dKg
+        dq_c = dq_c + elg * dQg
+        dlg = dlg + c["Qg"] * dQg
+        to_end = (c["lg"][:, :, -1:] - c["lg"]).exp()
+        dk_c = dk_c + to_end * dKt
+        dlg = dlg - c["Kt"] * dKt
+        dlast = (c["Kt"] * dKt).sum(2) + c["D"] * dD
+        dlg[:, :, -1] = dlg[:, :, -1] + dlast
+        dq[:, :, s0:s1] = dq_c
+        dk[:, :, s0:s1] = dk_c
+        dg[:, :, s0:s1] = dlg.flip(2).cumsum(2).flip(2)
+        dbeta[:, :, s0:s1] = db
+        dS = c["D"].unsqueeze(-1) * dS + c["Qg"].transpose(-2, -1) @ dOc - c["W"].transpose(-2, -1) @ dvt
+    back = lambda x: x.transpose(1, 2).contiguous()  # noqa: E731
+    return back(dq), back(dk), back(dv), back(dg), back(dbeta), dS
 
 
 # ---- the fused stages around the operator ------------------------------------
