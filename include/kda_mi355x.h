@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 3
+#define KDA_ABI_VERSION 4
 
 /* status codes */
 #define KDA_OK 0
@@ -142,6 +142,30 @@ int kda_ut_transform(const void* k, const void* v, const void* g, const void* be
                      void* M, void* U, void* W, void* log_gamma, void* k_gamma, int out_dtype,
                      int64_t batch, int64_t count, int64_t heads, int64_t key_dim,
                      int64_t value_dim, void* stream);
+
+/*
+ * Backward of the chunkwise operator: the gradients of a loss through
+ * (out, final_state) = chunkwise(q, k, v, g, beta, initial_state) with respect
+ * to every input.  Replaces the autograd backward of chunkwise_kda
+ * (src/kda/chunkwise.py:17-107; its gradients are pinned by
+ * tests/kda/test_kda_chunkwise_equivalence.py:92-134).
+ *   q, k, g [batch, tokens, heads, key_dim]; v, d_out [batch, tokens, heads, value_dim];
+ *   beta [batch, tokens, heads]: dtype bf16, f16 or f32 (inputs already masked);
+ *   initial_state, d_final_state : f32 [batch, heads, key_dim, value_dim] or NULL (zero)
+ *   dq, dk, dv, dg, dbeta        : outputs, shaped and typed like the inputs
+ *   d_initial_state              : f32 [batch, heads, key_dim, value_dim] or NULL
+ *   key_dim, value_dim <= 128; dense layout (no packed documents).
+ * Arithmetic is f32 throughout.  The workspace (kda_chunk_bwd_workspace_bytes,
+ * 16-byte aligned) holds per-chunk intermediates and is fully rewritten.
+ */
+size_t kda_chunk_bwd_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim,
+                                     int64_t value_dim);
+
+int kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                  const void* d_out, int dtype, const float* initial_state, const float* d_final_state,
+                  void* dq, void* dk, void* dv, void* dg, void* dbeta, float* d_initial_state,
+                  int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
+                  void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Fused stages around the operator.  Tensors are contiguous, of one dtype

@@ -228,6 +228,34 @@ int kda_ut_transform(const void* k, const void* v, const void* g, const void* be
                              key_dim, value_dim, static_cast<hipStream_t>(stream));
 }
 
+size_t kda_chunk_bwd_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim,
+                                     int64_t value_dim) {
+  if (batch <= 0 || tokens <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) return 0;
+  return chunk_bwd_workspace_bytes(batch, tokens, heads, key_dim, value_dim);
+}
+
+int kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta, const void* d_out,
+                  int in_dtype, const float* initial_state, const float* d_final_state, void* dq, void* dk, void* dv,
+                  void* dg, void* dbeta, float* d_initial_state, int64_t batch, int64_t tokens, int64_t heads,
+                  int64_t key_dim, int64_t value_dim, void* workspace, size_t workspace_bytes, void* stream) {
+  g_detail[0] = '\0';
+  if (in_dtype != KDA_DTYPE_BF16 && in_dtype != KDA_DTYPE_F16 && in_dtype != KDA_DTYPE_F32) {
+    set_detail("chunk_bwd: inputs must be bf16, f16 or f32 (dtype %d)", in_dtype);
+    return in_dtype == KDA_DTYPE_F64 ? KDA_ERR_UNSUPPORTED : KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (batch <= 0 || tokens <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) {
+    set_detail("chunk_bwd: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!q || !k || !v || !g || !beta || !d_out || !dq || !dk || !dv || !dg || !dbeta) {
+    set_detail("chunk_bwd: inputs, d_out and the input gradients must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return launch_chunk_bwd(q, k, v, g, beta, d_out, in_dtype, initial_state, d_final_state, dq, dk, dv, dg, dbeta,
+                          d_initial_state, batch, tokens, heads, key_dim, value_dim, workspace, workspace_bytes,
+                          static_cast<hipStream_t>(stream));
+}
+
 int kda_conv_silu_fwd(const void* x, const void* weight, const void* bias, const void* history_in, void* y,
                       void* history_out, const int32_t* valid_lens, int64_t batch, int64_t tokens, int64_t channels,
                       int64_t kernel_size, int64_t head_dim, int normalize, double eps, int dtype, void* stream) {

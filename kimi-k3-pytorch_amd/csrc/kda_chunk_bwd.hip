@@ -1,0 +1,839 @@
+// Backward of the chunkwise KDA operator on gfx950: the gradients of the
+// output and final state with respect to q, k, v, g, beta and the initial
+// state, for the differentiation of chunkwise_kda (src/kda/chunkwise.py:34-107,
+// whose gradients the reference takes from autograd).
+//
+// Per chunk of 64 tokens (rows i, j; channels along K; columns along V), with
+//   lg = cumsum(g), E_ij = exp(lg_i - lg_j), A = strict-lower sum_k k_i k_j E_ij,
+//   Aqk = lower sum_k q_i k_j E_ij, N = (I + diag(b) A)^-1, M = N diag(b),
+//   Kg = e^lg k, Qg = e^lg q, D = e^lg_last, Kt = e^(lg_last - lg) k,
+//   W = M Kg, U = M v, Vt = U - W S,
+//   O = Qg S + Aqk Vt,  S' = D S + Kt^T Vt,
+// the backward is
+//   dVt = Kt dS' + Aqk^T dO,   dS = D dS' + Qg^T dO - W^T dVt,
+//   dQg = dO S^T, dAqk = tril(dO Vt^T), dKt = Vt dS'^T, dD = rowsum(dS' * S),
+//   dW = -dVt S^T, dv = M^T dVt, dM = dVt v^T + dW Kg^T, dKg = M^T dW,
+//   db_j = sum_i N_ij dM_ij + sum_k dL_jk A_jk,  dL = -strict(N^T dM diag(b) N^T),
+//   dA = diag(b) dL, then the pair sums of dA and dAqk with exact exponents,
+//   the exp factors, and dg = reverse cumulative sum of d lg over the chunk.
+//
+// Five kernels, all arithmetic in f32 on the f32 MFMA (v_mfma_f32_16x16x4f32):
+//   prep_kernel   one block per (sequence, head, chunk): A, Aqk (exact pair
+//                 exponents), N by forward substitution, W, U, Kt, Qg, Kg, D;
+//   fscan_kernel  one block per (sequence, head, 16 state columns): the chunk
+//                 start states S and the pseudo-values Vt, chunk by chunk;
+//   bscan_kernel  the same blocks backwards: dS' and dVt per chunk, dS0;
+//   grad_kernel   one block per chunk: dv, dbeta, and dQg, dKt, dKg, dA, dAqk;
+//   pair_kernel   one block per chunk: the pair sums and the final dq, dk, dg.
+// Intermediates live in a caller-owned f32 workspace, one record per
+// (sequence, head, chunk).
+#include <math.h>
+
+#include "kda_launch.h"
+
+namespace kda {
+namespace bwd {
+
+constexpr int kC = 64;     // chunk rows
+constexpr int kRS = 132;   // LDS row stride of [64][<=128] channel matrices
+constexpr int kRC = 68;    // LDS row stride of [64][64] chunk matrices
+constexpr int kSW = 32;    // state columns per slab in grad_kernel
+constexpr int kSS = 36;    // LDS row stride of slab matrices
+constexpr int kTS = 20;    // LDS row stride of 16-column scan tiles
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+// Offsets (floats) of one (sequence, head, chunk) record of the workspace.
+struct Layout {
+  int Kp, Vp;  // K and V rounded up to a power of two >= 16
+  int64_t N, A, Aqk, W, Kt, Qg, Kg, U, D, S, Vt, dS, dVt, dQg, dKt, dKg, dA, dAqk, dD, per;
+};
+
+__host__ __device__ inline int pow2_at_least16(int64_t x) {
+  int p = 16;
+  while (p < x) p *= 2;
+  return p;
+}
+
+__host__ __device__ inline Layout make_layout(int64_t K, int64_t V) {
+  Layout L;
+  L.Kp = pow2_at_least16(K);
+  L.Vp = pow2_at_least16(V);
+  const int64_t cc = kC * kC, ck = kC * L.Kp, cv = kC * L.Vp, kv = static_cast<int64_t>(L.Kp) * L.Vp;
+  int64_t o = 0;
+  L.N = o; o += cc;
+  L.A = o; o += cc;
+  L.Aqk = o; o += cc;
+  L.W = o; o += ck;
+  L.Kt = o; o += ck;
+  L.Qg = o; o += ck;
+  L.Kg = o; o += ck;
+  L.U = o; o += cv;
+  L.D = o; o += L.Kp;
+  L.S = o; o += kv;
+  L.Vt = o; o += cv;
+  L.dS = o; o += kv;
+  L.dVt = o; o += cv;
+  L.dQg = o; o += ck;
+  L.dKt = o; o += ck;
+  L.dKg = o; o += ck;
+  L.dA = o; o += cc;
+  L.dAqk = o; o += cc;
+  L.dD = o; o += L.Kp;
+  L.per = (o + 63) / 64 * 64;  // 256-byte records
+  return L;
+}
+
+template <class IT>
+struct Args {
+  const IT *q, *k, *v, *g, *beta, *dout;  // [B,T,H,*], beta [B,T,H]
+  const float* s0;                        // [B,H,K,V] or null
+  const float* dsT;                       // [B,H,K,V] or null
+  IT *dq, *dk, *dv, *dg, *dbeta;
+  float* ds0;                             // [B,H,K,V] or null
+  float* ws;
+  int64_t B, T, H, K, V, NC;
+  Layout L;
+};
+
+// An LDS matrix: element (r, c) at p[r * rs + c * cs] (a transpose swaps rs, cs).
+struct Mat {
+  const float* p;
+  int rs, cs;
+};
+
+// acc += A[r0:r0+16, 0:kd] * B[0:kd, c0:c0+16] on the f32 MFMA.  Lane
+// (i = lane % 16, g = lane / 16) supplies A[r0+i][kk+g] and B[kk+g][c0+i];
+// the accumulator lane holds D[r0 + 4g + r][c0 + i], r = 0..3.
+__device__ __forceinline__ f32x4 mma(f32x4 acc, Mat A, int r0, Mat B, int c0, int kd) {
+  const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  const float* a = A.p + (r0 + i) * A.rs + g * A.cs;
+  const float* b = B.p + g * B.rs + (c0 + i) * B.cs;
+  for (int kk = 0; kk < kd; kk += 4)
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[kk * A.cs], b[kk * B.rs], acc, 0, 0, 0);
+  return acc;
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+__device__ __forceinline__ int64_t tok(const int64_t b, const int64_t t, const int64_t T, const int64_t H,
+                                       const int64_t h) {
+  return (b * T + t) * H + h;
+}
+
+// Blocks b and b + 8 run on the same XCD; renumber so that each XCD owns one
+// contiguous range of logical blocks (the column blocks of one head then
+// share their XCD's L2 for the chunk operands they all read).
+__device__ __forceinline__ int64_t xcd_block(unsigned b, unsigned nb) {
+  const unsigned per = nb / 8, rem = nb % 8, x = b % 8;
+  return static_cast<int64_t>(x) * per + (x < rem ? x : rem) + b / 8;
+}
+
+// ---- prep_kernel: per-chunk intermediates ----------------------------------
+template <class IT>
+__global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
+  __shared__ float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS];
+  __shared__ float AS[kC * kRC], AqkS[kC * kRC], NS[kC * kRC];
+  __shared__ float bS[kC];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
+  const int64_t ch = blockIdx.x;
+  const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
+  const int64_t t0 = c * kC;
+  const int Kp = a.L.Kp, Vp = a.L.Vp;
+  float* ws = a.ws + ch * a.L.per;
+
+  for (int idx = tid; idx < kC * Kp; idx += 256) {
+    const int r = idx / Kp, col = idx % Kp;
+    const int64_t t = t0 + r;
+    float kv = 0.f, qv = 0.f, gv = 0.f;
+    if (t < a.T && col < a.K) {
+      const int64_t off = tok(b, t, a.T, a.H, h) * a.K + col;
+      kv = to_float(a.k[off]);
+      qv = to_float(a.q[off]);
+      gv = to_float(a.g[off]);
+    }
+    kS[r * kRS + col] = kv;
+    qS[r * kRS + col] = qv;
+    lgS[r * kRS + col] = gv;
+  }
+  if (tid < kC) {
+    const int64_t t = t0 + tid;
+    bS[tid] = t < a.T ? to_float(a.beta[tok(b, t, a.T, a.H, h)]) : 0.f;
+  }
+  for (int idx = tid; idx < kC * kRC; idx += 256) {
+    AS[idx] = 0.f;
+    AqkS[idx] = 0.f;
+  }
+  __syncthreads();
+  if (tid < Kp) {  // lg = cumsum(g) down the chunk
+    float s = 0.f;
+    for (int r = 0; r < kC; ++r) {
+      s += lgS[r * kRS + tid];
+      lgS[r * kRS + tid] = s;
+    }
+  }
+  __syncthreads();
+  // A and Aqk with exact pair exponents, 2x2 blocks of (i, j <= i)
+  for (int blk = tid; blk < 528; blk += 256) {
+    int I2 = static_cast<int>((sqrtf(8.f * blk + 1.f) - 1.f) * 0.5f);
+    while (I2 * (I2 + 1) / 2 > blk) --I2;
+    while ((I2 + 1) * (I2 + 2) / 2 <= blk) ++I2;
+    const int J2 = blk - I2 * (I2 + 1) / 2;
+    const int i0 = 2 * I2, j0 = 2 * J2;
+    const bool off_diag = I2 != J2;  // pair (i0, j0 + 1) lies above the diagonal on the diagonal block
+    float aa[2][2] = {{0.f, 0.f}, {0.f, 0.f}}, aq[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+    for (int kc = 0; kc < Kp; kc += 4) {
+      float4 ki[2], qi[2], li[2], kj[2], lj[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        ki[x] = *reinterpret_cast<const float4*>(&kS[(i0 + x) * kRS + kc]);
+        qi[x] = *reinterpret_cast<const float4*>(&qS[(i0 + x) * kRS + kc]);
+        li[x] = *reinterpret_cast<const float4*>(&lgS[(i0 + x) * kRS + kc]);
+        kj[x] = *reinterpret_cast<const float4*>(&kS[(j0 + x) * kRS + kc]);
+        lj[x] = *reinterpret_cast<const float4*>(&lgS[(j0 + x) * kRS + kc]);
+      }
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) {
+          const bool ok = !(x == 0 && y == 1) || off_diag;
+          const float e0 = ok ? fast_exp(li[x].x - lj[y].x) : 0.f;
+          const float e1 = ok ? fast_exp(li[x].y - lj[y].y) : 0.f;
+          const float e2 = ok ? fast_exp(li[x].z - lj[y].z) : 0.f;
+          const float e3 = ok ? fast_exp(li[x].w - lj[y].w) : 0.f;
+          aa[x][y] += ki[x].x * kj[y].x * e0 + ki[x].y * kj[y].y * e1 + ki[x].z * kj[y].z * e2 + ki[x].w * kj[y].w * e3;
+          aq[x][y] += qi[x].x * kj[y].x * e0 + qi[x].y * kj[y].y * e1 + qi[x].z * kj[y].z * e2 + qi[x].w * kj[y].w * e3;
+        }
+    }
+#pragma unroll
+    for (int x = 0; x < 2; ++x)
+#pragma unroll
+      for (int y = 0; y < 2; ++y) {
+        const int i = i0 + x, j = j0 + y;
+        if (j < i) AS[i * kRC + j] = aa[x][y];
+        if (j <= i) AqkS[i * kRC + j] = aq[x][y];
+      }
+  }
+  __syncthreads();
+  if (w == 0) {
+    // N = (I + diag(b) A)^-1 by forward substitution; lane c holds column c
+    float nc[kC];
+#pragma unroll
+    for (int i = 0; i < kC; ++i) {
+      float s = 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) s += AS[i * kRC + j] * nc[j];
+      nc[i] = (i == lane) ? 1.f : (i > lane ? -bS[i] * s : 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < kC; ++i) NS[i * kRC + lane] = nc[i];
+  } else {
+    for (int idx = tid - 64; idx < kC * kC; idx += 192) {
+      const int r = idx >> 6, cc = idx & 63;
+      ws[a.L.A + idx] = AS[r * kRC + cc];
+      ws[a.L.Aqk + idx] = AqkS[r * kRC + cc];
+    }
+    for (int idx = tid - 64; idx < kC * Kp; idx += 192) {
+      const int r = idx / Kp, col = idx % Kp;
+      const float lg = lgS[r * kRS + col], last = lgS[(kC - 1) * kRS + col];
+      const float e = fast_exp(lg), kv = kS[r * kRS + col];
+      ws[a.L.Qg + idx] = e * qS[r * kRS + col];
+      ws[a.L.Kt + idx] = fast_exp(last - lg) * kv;
+      ws[a.L.Kg + idx] = e * kv;
+      kS[r * kRS + col] = e * kv;  // Kg, the B operand of W = M Kg
+    }
+    if (tid - 64 < Kp) ws[a.L.D + (tid - 64)] = fast_exp(lgS[(kC - 1) * kRS + (tid - 64)]);
+  }
+  __syncthreads();
+  for (int idx = tid; idx < kC * kC; idx += 256) {  // M = N diag(b) over A
+    const int r = idx >> 6, cc = idx & 63;
+    const float n = NS[r * kRC + cc];
+    ws[a.L.N + idx] = n;
+    AS[r * kRC + cc] = n * bS[cc];
+  }
+  __syncthreads();
+  const int nkt = Kp / 16, nvt = Vp / 16;
+  for (int tt = w; tt < 4 * nkt; tt += 4) {  // W = M Kg
+    const int rt = tt & 3, ct = tt >> 2;
+    const f32x4 acc = mma(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{kS, kRS, 1}, 16 * ct, kC);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ws[a.L.W + (16 * rt + 4 * lg4 + r) * Kp + 16 * ct + li] = acc[r];
+  }
+  for (int idx = tid; idx < kC * Vp; idx += 256) {  // v over lg (no longer read)
+    const int r = idx / Vp, col = idx % Vp;
+    const int64_t t = t0 + r;
+    lgS[r * kRS + col] = (t < a.T && col < a.V) ? to_float(a.v[tok(b, t, a.T, a.H, h) * a.V + col]) : 0.f;
+  }
+  __syncthreads();
+  for (int tt = w; tt < 4 * nvt; tt += 4) {  // U = M v
+    const int rt = tt & 3, ct = tt >> 2;
+    const f32x4 acc = mma(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{lgS, kRS, 1}, 16 * ct, kC);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) ws[a.L.U + (16 * rt + 4 * lg4 + r) * Vp + 16 * ct + li] = acc[r];
+  }
+}
+
+// ---- fscan_kernel: chunk start states and pseudo-values ----------------------
+// Block (sequence, head, 16 columns) carries S[:, cols] through the chunks:
+//   Vt = U[:, cols] - W S,  S <- D S + Kt^T Vt.
+// The next chunk's W, Kt, U and D are loaded into registers while the current
+// chunk is computed.
+constexpr int kPF = 8;  // float4 per thread of one [64][128] f32 matrix
+
+template <class IT>
+__global__ __launch_bounds__(256) void fscan_kernel(const Args<IT> a) {
+  __shared__ float WS[kC * kRS], KtS[kC * kRS], SS[128 * kTS], US[kC * kTS], DS[128];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
+  const int Kp = a.L.Kp, Vp = a.L.Vp, ncb = Vp / 16;
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
+  const int col0 = 16 * static_cast<int>(lb % ncb);
+  const int nq = kC * Kp / 4;  // float4 per [64][Kp] matrix
+  for (int idx = tid; idx < Kp * 16; idx += 256) {
+    const int r = idx >> 4, cc = idx & 15;
+    SS[r * kTS + cc] = (a.s0 != nullptr && r < a.K && col0 + cc < a.V)
+                           ? a.s0[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
+                           : 0.f;
+  }
+  float4 pw[kPF], pk[kPF];
+  float pu[4], pd = 0.f;
+  auto fetch = [&](int64_t c) {
+    const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
+#pragma unroll
+    for (int m = 0; m < kPF; ++m) {
+      const int q4 = tid + 256 * m;
+      if (q4 < nq) {
+        pw[m] = *reinterpret_cast<const float4*>(ws + a.L.W + 4 * q4);
+        pk[m] = *reinterpret_cast<const float4*>(ws + a.L.Kt + 4 * q4);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int idx = tid + 256 * m;  // [64][16]
+      pu[m] = ws[a.L.U + (idx >> 4) * Vp + col0 + (idx & 15)];
+    }
+    if (tid < Kp) pd = ws[a.L.D + tid];
+  };
+  fetch(0);
+  for (int64_t c = 0; c < a.NC; ++c) {
+    float* ws = a.ws + (bh * a.NC + c) * a.L.per;
+#pragma unroll
+    for (int m = 0; m < kPF; ++m) {
+      const int q4 = tid + 256 * m;
+      if (q4 < nq) {
+        const int e = 4 * q4, r = e / Kp, col = e % Kp;
+        *reinterpret_cast<float4*>(&WS[r * kRS + col]) = pw[m];
+        *reinterpret_cast<float4*>(&KtS[r * kRS + col]) = pk[m];
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int idx = tid + 256 * m;
+      US[(idx >> 4) * kTS + (idx & 15)] = pu[m];
+    }
+    if (tid < Kp) DS[tid] = pd;
+    for (int idx = tid; idx < Kp * 16; idx += 256) {  // the chunk's start state
+      const int r = idx >> 4, cc = idx & 15;
+      ws[a.L.S + r * Vp + col0 + cc] = SS[r * kTS + cc];
+    }
+    __syncthreads();
+    if (c + 1 < a.NC) fetch(c + 1);
+    // Vt = U - W S, rows 16w..16w+15
+    const f32x4 acc = mma(zero4(), Mat{WS, kRS, 1}, 16 * w, Mat{SS, kTS, 1}, 0, Kp);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * w + 4 * lg4 + r;
+      const float vt = US[row * kTS + li] - acc[r];
+      US[row * kTS + li] = vt;
+      ws[a.L.Vt + row * Vp + col0 + li] = vt;
+    }
+    __syncthreads();
+    for (int rt = w; rt < Kp / 16; rt += 4) {  // S <- D S + Kt^T Vt
+      const f32x4 upd = mma(zero4(), Mat{KtS, 1, kRS}, 16 * rt, Mat{US, kTS, 1}, 0, kC);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * rt + 4 * lg4 + r;
+        SS[row * kTS + li] = DS[row] * SS[row * kTS + li] + upd[r];
+      }
+    }
+    __syncthreads();
+  }
+}
+
+// ---- bscan_kernel: state gradients backwards through the chunks -------------
+//   dVt = Kt dS + Aqk^T dO[:, cols],  dS <- D dS + Qg^T dO[:, cols] - W^T dVt.
+template <class IT>
+__global__ __launch_bounds__(256) void bscan_kernel(const Args<IT> a) {
+  __shared__ float KtS[kC * kRS], QgS[kC * kRS], WS[kC * kRS], AqkS[kC * kRC];
+  __shared__ float dSS[128 * kTS], dOS[kC * kTS], XS[kC * kTS], DS[128];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
+  const int Kp = a.L.Kp, Vp = a.L.Vp, ncb = Vp / 16;
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
+  const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
+  const int col0 = 16 * static_cast<int>(lb % ncb);
+  const int nq = kC * Kp / 4;
+  for (int idx = tid; idx < Kp * 16; idx += 256) {
+    const int r = idx >> 4, cc = idx & 15;
+    dSS[r * kTS + cc] = (a.dsT != nullptr && r < a.K && col0 + cc < a.V)
+                            ? a.dsT[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
+                            : 0.f;
+  }
+  float4 pk[kPF], pq[kPF], pw[kPF], pa[4];
+  float po[4], pd = 0.f;
+  auto fetch = [&](int64_t c) {
+    const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
+#pragma unroll
+    for (int m = 0; m < kPF; ++m) {
+      const int q4 = tid + 256 * m;
+      if (q4 < nq) {
+        pk[m] = *reinterpret_cast<const float4*>(ws + a.L.Kt + 4 * q4);
+        pq[m] = *reinterpret_cast<const float4*>(ws + a.L.Qg + 4 * q4);
+        pw[m] = *reinterpret_cast<const float4*>(ws + a.L.W + 4 * q4);
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) pa[m] = *reinterpret_cast<const float4*>(ws + a.L.Aqk + 4 * (tid + 256 * m));
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int idx = tid + 256 * m, r = idx >> 4, cc = idx & 15;
+      const int64_t t = c * kC + r;
+      po[m] = (t < a.T && col0 + cc < a.V) ? to_float(a.dout[tok(b, t, a.T, a.H, h) * a.V + col0 + cc]) : 0.f;
+    }
+    if (tid < Kp) pd = ws[a.L.D + tid];
+  };
+  fetch(a.NC - 1);
+  for (int64_t c = a.NC - 1; c >= 0; --c) {
+    float* ws = a.ws + (bh * a.NC + c) * a.L.per;
+#pragma unroll
+    for (int m = 0; m < kPF; ++m) {
+      const int q4 = tid + 256 * m;
+      if (q4 < nq) {
+        const int e = 4 * q4, r = e / Kp, col = e % Kp;
+        *reinterpret_cast<float4*>(&KtS[r * kRS + col]) = pk[m];
+        *reinterpret_cast<float4*>(&QgS[r * kRS + col]) = pq[m];
+        *reinterpret_cast<float4*>(&WS[r * kRS + col]) = pw[m];
+      }
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int e = 4 * (tid + 256 * m), r = e >> 6, cc = e & 63;
+      *reinterpret_cast<float4*>(&AqkS[r * kRC + cc]) = pa[m];
+    }
+#pragma unroll
+    for (int m = 0; m < 4; ++m) {
+      const int idx = tid + 256 * m;
+      dOS[(idx >> 4) * kTS + (idx & 15)] = po[m];
+    }
+    if (tid < Kp) DS[tid] = pd;
+    for (int idx = tid; idx < Kp * 16; idx += 256) {  // gradient of the chunk's end state
+      const int r = idx >> 4, cc = idx & 15;
+      ws[a.L.dS + r * Vp + col0 + cc] = dSS[r * kTS + cc];
+    }
+    __syncthreads();
+    if (c > 0) fetch(c - 1);
+    // dVt = Kt dS + Aqk^T dO, rows 16w..16w+15
+    f32x4 acc = mma(zero4(), Mat{KtS, kRS, 1}, 16 * w, Mat{dSS, kTS, 1}, 0, Kp);
+    acc = mma(acc, Mat{AqkS, 1, kRC}, 16 * w, Mat{dOS, kTS, 1}, 0, kC);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * w + 4 * lg4 + r;
+      XS[row * kTS + li] = acc[r];
+      ws[a.L.dVt + row * Vp + col0 + li] = acc[r];
+    }
+    __syncthreads();
+    for (int rt = w; rt < Kp / 16; rt += 4) {  // dS <- D dS + Qg^T dO - W^T dVt
+      const f32x4 p = mma(zero4(), Mat{QgS, 1, kRS}, 16 * rt, Mat{dOS, kTS, 1}, 0, kC);
+      const f32x4 n = mma(zero4(), Mat{WS, 1, kRS}, 16 * rt, Mat{XS, kTS, 1}, 0, kC);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * rt + 4 * lg4 + r;
+        dSS[row * kTS + li] = DS[row] * dSS[row * kTS + li] + p[r] - n[r];
+      }
+    }
+    __syncthreads();
+  }
+  if (a.ds0 != nullptr) {
+    for (int idx = tid; idx < Kp * 16; idx += 256) {
+      const int r = idx >> 4, cc = idx & 15;
+      if (r < a.K && col0 + cc < a.V) a.ds0[((b * a.H + h) * a.K + r) * a.V + col0 + cc] = dSS[r * kTS + cc];
+    }
+  }
+}
+
+// ---- grad_kernel: products that reduce over the state columns -----------------
+// Slabs of 32 state columns accumulate dQg, dKt, dW (wave w: rows 16w..),
+// dAqk and dM in MFMA accumulators and write dv; then dKg = M^T dW,
+// dM += dW Kg^T, dbeta and dA follow from N.
+constexpr int kOffM = 0;                        // [64][68] M = N diag(b)
+constexpr int kOffSs = kOffM + kC * kRC;        // [128][36] S slab
+constexpr int kOffdSn = kOffSs + 128 * kSS;     // [128][36] dS' slab
+constexpr int kOffdOs = kOffdSn + 128 * kSS;    // [64][36] dO slab
+constexpr int kOffVts = kOffdOs + kC * kSS;     // [64][36] Vt slab
+constexpr int kOffdVts = kOffVts + kC * kSS;    // [64][36] dVt slab
+constexpr int kOffvs = kOffdVts + kC * kSS;     // [64][36] v slab
+constexpr int kGradFloats = kOffvs + kC * kSS;
+// second stage, over the slabs
+constexpr int kOffX = kOffSs;                   // [64][132] -dW... stored as dW
+constexpr int kOffY = kOffdOs;                  // [64][132] Kg
+constexpr int kOffN = kOffSs;                   // [64][68]
+constexpr int kOffDM = kOffN + kC * kRC;        // [64][68] dM, then T1 = N^T dN
+constexpr int kOffDN = kOffdOs;                 // [64][68] dN, then dL
+constexpr int kOffA = kOffDN + kC * kRC;        // [64][68]
+static_assert(kOffX + kC * kRS <= kOffY, "dW must not overlap Kg");
+static_assert(kOffY + kC * kRS <= kGradFloats, "Kg must fit");
+static_assert(kOffDM + kC * kRC <= kOffDN && kOffA + kC * kRC <= kGradFloats, "second-stage tiles must fit");
+
+template <class IT>
+__global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
+  __shared__ float sm[kGradFloats];
+  __shared__ float bS[kC];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
+  const int64_t ch = blockIdx.x;
+  const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
+  const int64_t t0 = c * kC;
+  const int Kp = a.L.Kp, Vp = a.L.Vp, nkt = Kp / 16;
+  float* ws = a.ws + ch * a.L.per;
+  float* MS = sm + kOffM;
+  if (tid < kC) {
+    const int64_t t = t0 + tid;
+    bS[tid] = t < a.T ? to_float(a.beta[tok(b, t, a.T, a.H, h)]) : 0.f;
+  }
+  __syncthreads();
+  for (int idx = tid; idx < kC * kC; idx += 256) MS[(idx >> 6) * kRC + (idx & 63)] = ws[a.L.N + idx] * bS[idx & 63];
+
+  f32x4 aQ[8], aT[8], aW[8], aA[4], aM[4];
+#pragma unroll
+  for (int m = 0; m < 8; ++m) aQ[m] = aT[m] = aW[m] = zero4();
+#pragma unroll
+  for (int m = 0; m < 4; ++m) aA[m] = aM[m] = zero4();
+  float dd = 0.f;
+  float *Ss = sm + kOffSs, *dSn = sm + kOffdSn, *dOs = sm + kOffdOs, *Vts = sm + kOffVts, *dVts = sm + kOffdVts,
+        *vs = sm + kOffvs;
+  for (int s0 = 0; s0 < Vp; s0 += kSW) {
+    const int sw = Vp - s0 < kSW ? Vp - s0 : kSW;
+    for (int idx = tid; idx < Kp * kSW; idx += 256) {
+      const int r = idx / kSW, cc = idx % kSW;
+      const bool in = cc < sw;
+      Ss[r * kSS + cc] = in ? ws[a.L.S + r * Vp + s0 + cc] : 0.f;
+      dSn[r * kSS + cc] = in ? ws[a.L.dS + r * Vp + s0 + cc] : 0.f;
+    }
+    for (int idx = tid; idx < kC * kSW; idx += 256) {
+      const int r = idx / kSW, cc = idx % kSW;
+      const int64_t t = t0 + r;
+      const bool in = cc < sw, real = in && t < a.T && s0 + cc < a.V;
+      const int64_t off = tok(b, t, a.T, a.H, h) * a.V + s0 + cc;
+      dOs[r * kSS + cc] = real ? to_float(a.dout[off]) : 0.f;
+      vs[r * kSS + cc] = real ? to_float(a.v[off]) : 0.f;
+      Vts[r * kSS + cc] = in ? ws[a.L.Vt + r * Vp + s0 + cc] : 0.f;
+      dVts[r * kSS + cc] = in ? ws[a.L.dVt + r * Vp + s0 + cc] : 0.f;
+    }
+    __syncthreads();
+    for (int tt = w; tt < 4 * (sw / 16); tt += 4) {  // dv = M^T dVt
+      const int rt = tt & 3, ct = tt >> 2;
+      const f32x4 acc = mma(zero4(), Mat{MS, 1, kRC}, 16 * rt, Mat{dVts, kSS, 1}, 16 * ct, kC);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * rt + 4 * lg4 + r, col = s0 + 16 * ct + li;
+        const int64_t t = t0 + row;
+        if (t < a.T && col < a.V) a.dv[tok(b, t, a.T, a.H, h) * a.V + col] = from_compute<IT>(acc[r]);
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < 8; ++ct) {
+      if (ct < nkt) {
+        aQ[ct] = mma(aQ[ct], Mat{dOs, kSS, 1}, 16 * w, Mat{Ss, 1, kSS}, 16 * ct, sw);
+        aT[ct] = mma(aT[ct], Mat{Vts, kSS, 1}, 16 * w, Mat{dSn, 1, kSS}, 16 * ct, sw);
+        aW[ct] = mma(aW[ct], Mat{dVts, kSS, 1}, 16 * w, Mat{Ss, 1, kSS}, 16 * ct, sw);
+      }
+    }
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      aA[ct] = mma(aA[ct], Mat{dOs, kSS, 1}, 16 * w, Mat{Vts, 1, kSS}, 16 * ct, sw);
+      aM[ct] = mma(aM[ct], Mat{dVts, kSS, 1}, 16 * w, Mat{vs, 1, kSS}, 16 * ct, sw);
+    }
+    if (tid < Kp)
+      for (int cc = 0; cc < sw; ++cc) dd += dSn[tid * kSS + cc] * Ss[tid * kSS + cc];
+    __syncthreads();
+  }
+
+  // dW = -(dVt S^T) over the slabs, Kg, and the finished dQg, dKt, dAqk, dD
+  float *X = sm + kOffX, *Y = sm + kOffY;
+#pragma unroll
+  for (int ct = 0; ct < 8; ++ct) {
+    if (ct < nkt) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * w + 4 * lg4 + r, col = 16 * ct + li;
+        X[row * kRS + col] = -aW[ct][r];
+        ws[a.L.dQg + row * Kp + col] = aQ[ct][r];
+        ws[a.L.dKt + row * Kp + col] = aT[ct][r];
+      }
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * w + 4 * lg4 + r, col = 16 * ct + li;
+      ws[a.L.dAqk + row * kC + col] = col <= row ? aA[ct][r] : 0.f;
+    }
+  for (int idx = tid; idx < kC * Kp; idx += 256) Y[(idx / Kp) * kRS + idx % Kp] = ws[a.L.Kg + idx];
+  if (tid < Kp) ws[a.L.dD + tid] = dd;
+  __syncthreads();
+#pragma unroll
+  for (int ct = 0; ct < 8; ++ct) {  // dKg = M^T dW
+    if (ct < nkt) {
+      const f32x4 acc = mma(zero4(), Mat{MS, 1, kRC}, 16 * w, Mat{X, kRS, 1}, 16 * ct, kC);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) ws[a.L.dKg + (16 * w + 4 * lg4 + r) * Kp + 16 * ct + li] = acc[r];
+    }
+  }
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) aM[ct] = mma(aM[ct], Mat{X, kRS, 1}, 16 * w, Mat{Y, 1, kRS}, 16 * ct, Kp);  // dM += dW Kg^T
+  __syncthreads();
+
+  // dbeta and dA from N: dN = dM diag(b), T1 = N^T dN, dL = -strict(T1 N^T)
+  float *NS = sm + kOffN, *DM = sm + kOffDM, *DN = sm + kOffDN, *AS = sm + kOffA;
+  for (int idx = tid; idx < kC * kC; idx += 256) {
+    const int r = idx >> 6, cc = idx & 63;
+    NS[r * kRC + cc] = ws[a.L.N + idx];
+    AS[r * kRC + cc] = ws[a.L.A + idx];
+  }
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * w + 4 * lg4 + r, col = 16 * ct + li;
+      DM[row * kRC + col] = aM[ct][r];
+      DN[row * kRC + col] = aM[ct][r] * bS[col];
+    }
+  __syncthreads();
+  float db = 0.f;
+  if (tid < kC)
+    for (int r = 0; r < kC; ++r) db += NS[r * kRC + tid] * DM[r * kRC + tid];
+  f32x4 t1[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) t1[ct] = mma(zero4(), Mat{NS, 1, kRC}, 16 * w, Mat{DN, kRC, 1}, 16 * ct, kC);
+  __syncthreads();
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) DM[(16 * w + 4 * lg4 + r) * kRC + 16 * ct + li] = t1[ct][r];
+  __syncthreads();
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    const f32x4 acc = mma(zero4(), Mat{DM, kRC, 1}, 16 * w, Mat{NS, 1, kRC}, 16 * ct, kC);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * w + 4 * lg4 + r, col = 16 * ct + li;
+      const float dl = col < row ? -acc[r] : 0.f;
+      DN[row * kRC + col] = dl;
+      ws[a.L.dA + row * kC + col] = bS[row] * dl;
+    }
+  }
+  __syncthreads();
+  if (tid < kC) {
+    for (int j = 0; j < kC; ++j) db += DN[tid * kRC + j] * AS[tid * kRC + j];
+    const int64_t t = t0 + tid;
+    if (t < a.T) a.dbeta[tok(b, t, a.T, a.H, h)] = from_compute<IT>(db);
+  }
+}
+
+// ---- pair_kernel: pair sums with exact exponents and the final dq, dk, dg ----
+// Thread (column col, part p) owns rows i = p + P m of its column (P = 256 / Kp)
+// and forms
+//   R1_i = sum_j dA_ij k_j E_ij,  R2_i = sum_j dAqk_ij k_j E_ij   (j <= i)
+//   R3_j = sum_i dA_ij k_i E_ij,  R4_j = sum_i dAqk_ij q_i E_ij   (i >= j)
+// then dk = R1 + R3 + R4 + e^lg dKg + e^(lg_last - lg) dKt, dq = R2 + e^lg dQg,
+// d lg = k R1 - k R3 + q R2 - k R4 + Kg dKg + Qg dQg - Kt dKt (+ the last row's
+// sum(Kt dKt) + D dD), and dg as its reverse cumulative sum.
+template <class IT, int RP>
+__global__ __launch_bounds__(256) void pair_kernel(const Args<IT> a) {
+  __shared__ float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS], dAS[kC * kRC], dQS[kC * kRC];
+  __shared__ float red[16 * 128];
+  const int tid = threadIdx.x;
+  const int64_t ch = blockIdx.x;
+  const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
+  const int64_t t0 = c * kC;
+  const int Kp = a.L.Kp;
+  constexpr int P = kC / RP;  // parts per column (Kp = 256 / P)
+  const float* ws = a.ws + ch * a.L.per;
+  for (int idx = tid; idx < kC * Kp; idx += 256) {
+    const int r = idx / Kp, col = idx % Kp;
+    const int64_t t = t0 + r;
+    float kv = 0.f, qv = 0.f, gv = 0.f;
+    if (t < a.T && col < a.K) {
+      const int64_t off = tok(b, t, a.T, a.H, h) * a.K + col;
+      kv = to_float(a.k[off]);
+      qv = to_float(a.q[off]);
+      gv = to_float(a.g[off]);
+    }
+    kS[r * kRS + col] = kv;
+    qS[r * kRS + col] = qv;
+    lgS[r * kRS + col] = gv;
+  }
+  for (int idx = tid; idx < kC * kC; idx += 256) {
+    dAS[(idx >> 6) * kRC + (idx & 63)] = ws[a.L.dA + idx];
+    dQS[(idx >> 6) * kRC + (idx & 63)] = ws[a.L.dAqk + idx];
+  }
+  __syncthreads();
+  if (tid < Kp) {
+    float s = 0.f;
+    for (int r = 0; r < kC; ++r) {
+      s += lgS[r * kRS + tid];
+      lgS[r * kRS + tid] = s;
+    }
+  }
+  __syncthreads();
+  const int col = tid % Kp, part = tid / Kp;
+  float li[RP], ki[RP], qi[RP], R1[RP], R2[RP], R3[RP], R4[RP];
+#pragma unroll
+  for (int m = 0; m < RP; ++m) {
+    const int i = part + P * m;
+    li[m] = lgS[i * kRS + col];
+    ki[m] = kS[i * kRS + col];
+    qi[m] = qS[i * kRS + col];
+    R1[m] = R2[m] = R3[m] = R4[m] = 0.f;
+  }
+  for (int j = 0; j < kC; ++j) {  // j-sums: rows i >= j of this thread
+    const float kj = kS[j * kRS + col], lj = lgS[j * kRS + col];
+#pragma unroll
+    for (int m = 0; m < RP; ++m) {
+      const int i = part + P * m;
+      if (i >= j) {
+        const float ke = kj * fast_exp(li[m] - lj);
+        R1[m] += dAS[i * kRC + j] * ke;
+        R2[m] += dQS[i * kRC + j] * ke;
+      }
+    }
+  }
+  for (int i = 0; i < kC; ++i) {  // i-sums: rows j <= i of this thread
+    const float kv = kS[i * kRS + col], qv = qS[i * kRS + col], lv = lgS[i * kRS + col];
+#pragma unroll
+    for (int m = 0; m < RP; ++m) {
+      const int j = part + P * m;
+      if (i >= j) {
+        const float e = fast_exp(lv - li[m]);
+        R3[m] += dAS[i * kRC + j] * kv * e;
+        R4[m] += dQS[i * kRC + j] * qv * e;
+      }
+    }
+  }
+  const float last = lgS[(kC - 1) * kRS + col];
+  __syncthreads();  // every read of q ends before d lg overwrites it
+  float lastsum = 0.f;
+#pragma unroll
+  for (int m = 0; m < RP; ++m) {
+    const int i = part + P * m;
+    const int64_t rec = static_cast<int64_t>(i) * Kp + col;
+    const float e = fast_exp(li[m]), te = fast_exp(last - li[m]);
+    const float dKg = ws[a.L.dKg + rec], dKt = ws[a.L.dKt + rec], dQg = ws[a.L.dQg + rec];
+    const float dk = R1[m] + R3[m] + R4[m] + e * dKg + te * dKt;
+    const float dq = R2[m] + e * dQg;
+    const float ktd = te * ki[m] * dKt;
+    qS[i * kRS + col] = ki[m] * (R1[m] - R3[m] - R4[m]) + qi[m] * R2[m] + e * ki[m] * dKg + e * qi[m] * dQg - ktd;
+    lastsum += ktd;
+    const int64_t t = t0 + i;
+    if (t < a.T && col < a.K) {
+      const int64_t off = tok(b, t, a.T, a.H, h) * a.K + col;
+      a.dq[off] = from_compute<IT>(dq);
+      a.dk[off] = from_compute<IT>(dk);
+    }
+  }
+  red[part * 128 + col] = lastsum;
+  __syncthreads();
+  if (tid < Kp) {
+    float run = fast_exp(last) * ws[a.L.dD + tid];
+    for (int p = 0; p < P; ++p) run += red[p * 128 + tid];
+    for (int i = kC - 1; i >= 0; --i) {
+      run += qS[i * kRS + tid];
+      const int64_t t = t0 + i;
+      if (t < a.T && tid < a.K) a.dg[tok(b, t, a.T, a.H, h) * a.K + tid] = from_compute<IT>(run);
+    }
+  }
+}
+
+}  // namespace bwd
+}  // namespace kda
+
+namespace kda_host {
+
+using namespace kda;
+
+size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
+  const bwd::Layout L = bwd::make_layout(K, V);
+  const int64_t nc = (T + bwd::kC - 1) / bwd::kC;
+  return static_cast<size_t>(B * H * nc * L.per) * sizeof(float);
+}
+
+template <class IT>
+static int run_bwd(const bwd::Args<IT>& a, hipStream_t s) {
+  const int64_t chunks = a.B * a.H * a.NC;
+  const int64_t scans = a.B * a.H * (a.L.Vp / 16);
+  if (chunks > 0x7fffffffLL || scans > 0x7fffffffLL) {
+    set_detail("chunk backward: grid too large");
+    return KDA_ERR_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL((bwd::prep_kernel<IT>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bwd::fscan_kernel<IT>), dim3(static_cast<unsigned>(scans)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bwd::bscan_kernel<IT>), dim3(static_cast<unsigned>(scans)), dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bwd::grad_kernel<IT>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a);
+  switch (a.L.Kp) {
+    case 16: hipLaunchKernelGGL((bwd::pair_kernel<IT, 4>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a); break;
+    case 32: hipLaunchKernelGGL((bwd::pair_kernel<IT, 8>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a); break;
+    case 64: hipLaunchKernelGGL((bwd::pair_kernel<IT, 16>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a); break;
+    default: hipLaunchKernelGGL((bwd::pair_kernel<IT, 32>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a); break;
+  }
+  return check_launch("chunk backward");
+}
+
+int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                     const void* dout, int in_dtype, const float* s0, const float* dsT, void* dq, void* dk, void* dv,
+                     void* dg, void* dbeta, float* ds0, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (K > 128 || V > 128) {
+    set_detail("chunk backward: key_dim and value_dim must be <= 128 (got %lld, %lld)", (long long)K, (long long)V);
+    return KDA_ERR_UNSUPPORTED;
+  }
+  const size_t need = chunk_bwd_workspace_bytes(B, T, H, K, V);
+  if (workspace == nullptr || workspace_bytes < need) {
+    set_detail("chunk backward: workspace of %zu bytes needed", need);
+    return KDA_ERR_WORKSPACE;
+  }
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) {
+    set_detail("chunk backward: workspace must be 16-byte aligned");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  const bwd::Layout L = bwd::make_layout(K, V);
+  const int64_t NC = (T + bwd::kC - 1) / bwd::kC;
+  float* ws = static_cast<float*>(workspace);
+  switch (in_dtype) {
+    case KDA_DTYPE_BF16:
+      return run_bwd(bwd::Args<bf16>{static_cast<const bf16*>(q), static_cast<const bf16*>(k),
+                                     static_cast<const bf16*>(v), static_cast<const bf16*>(g),
+                                     static_cast<const bf16*>(beta), static_cast<const bf16*>(dout), s0, dsT,
+                                     static_cast<bf16*>(dq), static_cast<bf16*>(dk), static_cast<bf16*>(dv),
+                                     static_cast<bf16*>(dg), static_cast<bf16*>(dbeta), ds0, ws, B, T, H, K, V, NC, L},
+                     stream);
+    case KDA_DTYPE_F16:
+      return run_bwd(bwd::Args<f16>{static_cast<const f16*>(q), static_cast<const f16*>(k),
+                                    static_cast<const f16*>(v), static_cast<const f16*>(g),
+                                    static_cast<const f16*>(beta), static_cast<const f16*>(dout), s0, dsT,
+                                    static_cast<f16*>(dq), static_cast<f16*>(dk), static_cast<f16*>(dv),
+                                    static_cast<f16*>(dg), static_cast<f16*>(dbeta), ds0, ws, B, T, H, K, V, NC, L},
+                     stream);
+    case KDA_DTYPE_F32:
+      return run_bwd(bwd::Args<float>{static_cast<const float*>(q), static_cast<const float*>(k),
+                                      static_cast<const float*>(v), static_cast<const float*>(g),
+                                      static_cast<const float*>(beta), static_cast<const float*>(dout), s0, dsT,
+                                      static_cast<float*>(dq), static_cast<float*>(dk), static_cast<float*>(dv),
+                                      static_cast<float*>(dg), static_cast<float*>(dbeta), ds0, ws, B, T, H, K, V,
+                                      NC, L},
+                     stream);
+    default:
+      set_detail("chunk backward: inputs must be bf16, f16 or f32 (dtype %d)", in_dtype);
+      return KDA_ERR_UNSUPPORTED;
+  }
+}
+
+}  // namespace kda_host

@@ -36,6 +36,14 @@ int launch_ut_transform(const void* k, const void* v, const void* g, const void*
                         void* U, void* W, void* log_gamma, void* k_gamma, int out_dtype, int64_t batch,
                         int64_t count, int64_t heads, int64_t key_dim, int64_t value_dim, hipStream_t stream);
 
+// Backward of the chunkwise operator (csrc/kda_chunk_bwd.hip).
+size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
+
+int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                     const void* dout, int in_dtype, const float* s0, const float* dsT, void* dq, void* dk, void* dv,
+                     void* dg, void* dbeta, float* ds0, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                     void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 // Fused stages around the operator (csrc/kda_fused.hip).
 int launch_conv_silu(const void* x, const void* w, const void* bias, const void* hist_in, void* y, void* hist_out,
                      const int32_t* valid_lens, int64_t B, int64_t T, int64_t C, int64_t K, int64_t head_dim,

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libkda_mi355x.so")
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 KDA_OK = 0
 KDA_ERR_INVALID_ARGUMENT = 1
@@ -61,6 +61,11 @@ SIGNATURES = {
         [_P, _P, _P, ctypes.c_double, _P, _P, _P, _P, _L, _L, _L, _I, _P],
     ),
     "kda_rmsnorm_gate_fwd": (_I, [_P, _P, _I, _P, _P, _L, _L, _L, ctypes.c_double, _I, _P]),
+    "kda_chunk_bwd_workspace_bytes": (_S, [_L, _L, _L, _L, _L]),
+    "kda_chunk_bwd": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _P, _S, _P],
+    ),
 }
 
 _lock = threading.Lock()

@@ -12,6 +12,13 @@ the reference does and otherwise only select nothing.
 Additive keyword-only extension: ``cu_seqlens`` (packed documents
 ``[1, sum T, H, *]``, state reset at every document start, per-document
 ``initial_state``/``final_state`` of shape ``[N,H,K,V]``).
+
+Gradients: with autograd enabled and an input that requires grad, the call
+goes through ``_ChunkwiseFunction``, whose backward is the HIP chunk backward
+(``kda_chunk_bwd``) for bf16/f16/f32 inputs, key_dim and value_dim <= 128 and
+the dense layout; the attention mask is applied with differentiable tensor
+ops first (src/kda/utils.py:82-94), so padded positions get zero gradients.
+Other cases raise instead of dropping gradients.
 """
 
 from __future__ import annotations
@@ -52,10 +59,24 @@ def chunkwise_kda(
         q, k, v, g, beta, initial_state, attention_mask, num_states=num_states
     )
     _lib.require_gpu(q)
-    _prep.reject_autograd(q, k, v, g, beta, initial_state)
-    lib = _lib.load()
-
     work_dtype = accumulation_dtype(v.dtype, accumulate_state_in_fp32)
+    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, g, beta, initial_state)):
+        if offsets is not None:
+            raise RuntimeError("the MI355X KDA backward does not support cu_seqlens; run the documents separately")
+        if work_dtype == torch.float64:
+            raise RuntimeError("the MI355X KDA backward supports bf16, f16 and f32 inputs (f32 arithmetic)")
+        if key_dim > 128 or value_dim > 128:
+            raise RuntimeError("the MI355X KDA backward supports key_dim and value_dim up to 128")
+        qm, gm, bm = _mask_differentiable(q, g, beta, attention_mask)
+        hidden, final = _ChunkwiseFunction.apply(qm, k, v, gm, bm, initial_state, output_final_state, work_dtype)
+        return KDAOperatorOutput(hidden_states=hidden, final_state=final)
+    return _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype, offsets,
+                    batch, tokens, heads, key_dim, value_dim)
+
+
+def _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype, offsets,
+             batch, tokens, heads, key_dim, value_dim) -> KDAOperatorOutput:
+    lib = _lib.load()
     (qc, kc, vc, gc, bc), kernel_dtype, arith = _prep.kernel_inputs(q, k, v, g, beta, work_dtype)
     device = q.device
     n_seq = batch if offsets is None else len(offsets) - 1
@@ -84,3 +105,61 @@ def chunkwise_kda(
     if s_out is not None:
         final = s_out if s_out.dtype == work_dtype else s_out.to(work_dtype)
     return KDAOperatorOutput(hidden_states=hidden, final_state=final)
+
+
+def _mask_differentiable(q, g, beta, attention_mask):
+    """Zero q, g and beta at padded positions with tensor ops that autograd
+    differentiates (src/kda/utils.py:82-94)."""
+    if attention_mask is None:
+        return q, g, beta
+    keep = attention_mask.to(device=q.device, dtype=torch.bool)
+    return (torch.where(keep[:, :, None, None], q, torch.zeros((), dtype=q.dtype, device=q.device)),
+            torch.where(keep[:, :, None, None], g, torch.zeros((), dtype=g.dtype, device=g.device)),
+            torch.where(keep[:, :, None], beta, torch.zeros((), dtype=beta.dtype, device=beta.device)))
+
+
+class _ChunkwiseFunction(torch.autograd.Function):
+    """chunkwise_kda on masked, dense inputs with the HIP backward."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, initial_state, output_final_state, work_dtype):
+        batch, tokens, heads, key_dim = q.shape
+        value_dim = v.shape[-1]
+        out = _forward(q, k, v, g, beta, initial_state, output_final_state, None, work_dtype, None,
+                       batch, tokens, heads, key_dim, value_dim)
+        ctx.save_for_backward(q, k, v, g, beta, initial_state)
+        ctx.work_dtype = work_dtype
+        if out.final_state is None:
+            return out.hidden_states, None
+        return out.hidden_states, out.final_state
+
+    @staticmethod
+    def backward(ctx, d_hidden, d_final):
+        q, k, v, g, beta, initial_state = ctx.saved_tensors
+        lib = _lib.load()
+        (qc, kc, vc, gc, bc), kernel_dtype, _ = _prep.kernel_inputs(q, k, v, g, beta, ctx.work_dtype)
+        batch, tokens, heads, key_dim = q.shape
+        value_dim = v.shape[-1]
+        device = q.device
+        if d_hidden is None:
+            d_hidden = torch.zeros(batch, tokens, heads, value_dim, dtype=kernel_dtype, device=device)
+        d_out = d_hidden.to(kernel_dtype).contiguous()
+        s0 = None if initial_state is None else initial_state.detach().to(torch.float32).contiguous()
+        ds_t = None if d_final is None else d_final.to(torch.float32).contiguous()
+        dq, dk, dv, dg = (torch.empty_like(t) for t in (qc, kc, vc, gc))
+        dbeta = torch.empty_like(bc)
+        ds0 = None
+        if initial_state is not None and ctx.needs_input_grad[5]:
+            ds0 = torch.empty(batch, heads, key_dim, value_dim, dtype=torch.float32, device=device)
+        ws_bytes = lib.kda_chunk_bwd_workspace_bytes(batch, tokens, heads, key_dim, value_dim)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        status = lib.kda_chunk_bwd(
+            qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr(), bc.data_ptr(), d_out.data_ptr(),
+            _lib.dtype_code(kernel_dtype), _lib.ptr(s0), _lib.ptr(ds_t), dq.data_ptr(), dk.data_ptr(),
+            dv.data_ptr(), dg.data_ptr(), dbeta.data_ptr(), _lib.ptr(ds0), batch, tokens, heads, key_dim,
+            value_dim, workspace.data_ptr(), ws_bytes, _prep.stream(device),
+        )
+        _lib.check(status)
+        grads = [dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
+                 None if ds0 is None else ds0.to(initial_state.dtype)]
+        return (*[gr if need else None for gr, need in zip(grads, ctx.needs_input_grad[:6])], None, None)

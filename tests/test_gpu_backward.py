@@ -1,0 +1,109 @@
+"""GPU parity of the chunkwise backward (kda_chunk_bwd through
+chunkwise_kda's autograd) against the oracle's explicit backward, which is
+itself pinned against autograd through the oracle's forward.
+
+Tolerances (max|x - ref| / max|ref| per gradient): f32 inputs 2e-4 (f32
+arithmetic against the f64 oracle on the same values), bf16 inputs 2e-2
+(gradients computed in f32 and rounded once to bf16).
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import kda
+from oracle import kda_oracle as ora
+from tests._inputs import rel_err, workload
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+TOL = {torch.float32: 2e-4, torch.bfloat16: 2e-2}
+NAMES = ("dq", "dk", "dv", "dg", "dbeta", "ds0")
+
+
+def _case(B, T, H, K, V, dtype, seed):
+    q, k, v, g, beta, s0 = workload(B, T, H, K, V, state_std=0.5, seed=seed, dtype=dtype)
+    gen = torch.Generator().manual_seed(seed + 1)
+    d_out = torch.randn(B, T, H, V, generator=gen).to(dtype)
+    d_final = torch.randn(B, H, K, V, generator=gen)
+    return (q, k, v, g, beta, s0), d_out, d_final
+
+
+def _gpu_grads(inputs, d_out, d_final, mask=None, final=True):
+    leaves = [t.to(DEV).requires_grad_() for t in inputs]
+    res = kda.chunkwise_kda(*leaves, final, None if mask is None else mask.to(DEV))
+    loss = (res.hidden_states.float() * d_out.to(DEV).float()).sum()
+    if final:
+        loss = loss + (res.final_state * d_final.to(DEV)).sum()
+    loss.backward()
+    return [t.grad for t in leaves]
+
+
+def _oracle_grads(inputs, d_out, d_final, final=True):
+    q, k, v, g, beta, s0 = (t.double() for t in inputs)
+    return ora.chunkwise_backward(q, k, v, g, beta, s0, d_out.double(), d_final.double() if final else None,
+                                  chunk_size=64)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+@pytest.mark.parametrize("B,T,H,K,V", [(2, 150, 2, 128, 128), (1, 64, 1, 64, 32), (2, 37, 3, 16, 48),
+                                       (1, 200, 2, 128, 96)])
+def test_backward_matches_oracle(dtype, B, T, H, K, V):
+    inputs, d_out, d_final = _case(B, T, H, K, V, dtype, seed=T + K)
+    got = _gpu_grads(inputs, d_out, d_final)
+    ref = _oracle_grads(inputs, d_out, d_final)
+    for name, a, b, x in zip(NAMES, got, ref, inputs):
+        assert a.dtype == x.dtype and a.shape == x.shape, name
+        assert torch.isfinite(a).all(), name
+        assert rel_err(a, b) < TOL[dtype], (name, rel_err(a, b))
+
+
+def test_backward_without_initial_state_or_final_state():
+    (q, k, v, g, beta, _), d_out, _ = _case(1, 100, 2, 128, 128, torch.float32, seed=3)
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v, g, beta)]
+    res = kda.chunkwise_kda(*leaves)
+    (res.hidden_states * d_out.to(DEV)).sum().backward()
+    ref = ora.chunkwise_backward(*(t.double() for t in (q, k, v, g, beta)), None, d_out.double(), None)
+    for name, a, b in zip(NAMES, [t.grad for t in leaves], ref):
+        assert rel_err(a, b) < TOL[torch.float32], name
+
+
+def test_backward_with_right_padding_mask():
+    B, T, H, K, V = 2, 90, 2, 128, 64
+    inputs, d_out, d_final = _case(B, T, H, K, V, torch.float32, seed=4)
+    mask = torch.arange(T)[None, :] < torch.tensor([T, 53])[:, None]
+    got = _gpu_grads(inputs, d_out, d_final, mask=mask)
+    q, k, v, g, beta, s0 = inputs
+    qm, gm, bm = ora.mask_inputs(q, g, beta, mask)
+    ref = list(_oracle_grads((qm, k, v, gm, bm, s0), d_out, d_final))
+    keep = mask.double()
+    ref[0] = ref[0] * keep[:, :, None, None]
+    ref[3] = ref[3] * keep[:, :, None, None]
+    ref[4] = ref[4] * keep[:, :, None]
+    for name, a, b in zip(NAMES, got, ref):
+        assert rel_err(a, b) < TOL[torch.float32], name
+    assert torch.count_nonzero(got[0][1, 53:]) == 0 and torch.count_nonzero(got[4][1, 53:]) == 0
+
+
+def test_backward_long_context_heads_subset():
+    # B=1 T=8192 H=16 bf16 (the prefill workload); heads are independent, so the
+    # oracle checks heads 0 and 15 of the full-size GPU gradients
+    B, T, H, K, V = 1, 8192, 16, 128, 128
+    inputs, d_out, d_final = _case(B, T, H, K, V, torch.bfloat16, seed=5)
+    got = _gpu_grads(inputs, d_out, d_final)
+    for h in (0, 15):
+        sub = [t[:, :, h:h + 1] for t in inputs[:5]] + [inputs[5][:, h:h + 1]]
+        ref = _oracle_grads(sub, d_out[:, :, h:h + 1], d_final[:, h:h + 1])
+        for name, a, b in zip(NAMES, got, ref):
+            a_h = a[:, h:h + 1] if name == "ds0" else a[:, :, h:h + 1]
+            assert rel_err(a_h, b) < TOL[torch.bfloat16], (name, h, rel_err(a_h, b))
+
+
+def test_backward_refuses_unsupported_cases():
+    q, k, v, g, beta, s0 = (t.to(DEV) for t in workload(1, 8, 1, 16, 16, state_std=0.1, dtype=torch.float64))
+    with pytest.raises(RuntimeError, match="bf16, f16 and f32"):
+        kda.chunkwise_kda(q.requires_grad_(), k, v, g, beta, s0)
+    q2, k2, v2, g2, b2, _ = (t.to(DEV) if t is not None else None for t in workload(1, 8, 1, 16, 16))
+    with pytest.raises(RuntimeError, match="cu_seqlens"):
+        kda.chunkwise_kda(q2.requires_grad_(), k2, v2, g2, b2, cu_seqlens=[0, 4, 8])
