@@ -45,20 +45,14 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 
 // Offsets (floats) of one (sequence, head, chunk) record of the workspace.
 struct Layout {
-  int Kp, Vp;  // K and V rounded up to a power of two >= 16
+  int Kp, Vp;  // K padded to 64 or 128, V to a multiple of 32
   int64_t N, A, Aqk, W, Kt, Qg, Kg, U, D, S, Vt, dS, dVt, dQg, dKt, dKg, dA, dAqk, dD, per;
 };
 
-__host__ __device__ inline int pow2_at_least16(int64_t x) {
-  int p = 16;
-  while (p < x) p *= 2;
-  return p;
-}
-
 __host__ __device__ inline Layout make_layout(int64_t K, int64_t V) {
   Layout L;
-  L.Kp = pow2_at_least16(K);
-  L.Vp = pow2_at_least16(V);
+  L.Kp = K <= 64 ? 64 : 128;
+  L.Vp = static_cast<int>((V + 31) / 32 * 32);
   const int64_t cc = kC * kC, ck = kC * L.Kp, cv = kC * L.Vp, kv = static_cast<int64_t>(L.Kp) * L.Vp;
   int64_t o = 0;
   L.N = o; o += cc;
@@ -96,6 +90,8 @@ struct Args {
   Layout L;
 };
 
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
 // An LDS matrix: element (r, c) at p[r * rs + c * cs] (a transpose swaps rs, cs).
 struct Mat {
   const float* p;
@@ -105,16 +101,48 @@ struct Mat {
 // acc += A[r0:r0+16, 0:kd] * B[0:kd, c0:c0+16] on the f32 MFMA.  Lane
 // (i = lane % 16, g = lane / 16) supplies A[r0+i][kk+g] and B[kk+g][c0+i];
 // the accumulator lane holds D[r0 + 4g + r][c0 + i], r = 0..3.
+// kd is a multiple of 16; each group of four products has its eight operand
+// reads issued before the first product.
 __device__ __forceinline__ f32x4 mma(f32x4 acc, Mat A, int r0, Mat B, int c0, int kd) {
   const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
   const float* a = A.p + (r0 + i) * A.rs + g * A.cs;
   const float* b = B.p + g * B.rs + (c0 + i) * B.cs;
-  for (int kk = 0; kk < kd; kk += 4)
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[kk * A.cs], b[kk * B.rs], acc, 0, 0, 0);
+  for (int k0 = 0; k0 < kd; k0 += 16) {
+    float av[4], bv[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      av[u] = a[(k0 + 4 * u) * A.cs];
+      bv[u] = b[(k0 + 4 * u) * B.rs];
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv[u], acc, 0, 0, 0);
+  }
   return acc;
 }
 
-__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+// The same product for long reductions: alternate groups feed two independent
+// accumulation chains, added at the end.
+__device__ __forceinline__ f32x4 mma_long(f32x4 acc, Mat A, int r0, Mat B, int c0, int kd) {
+  const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  const float* a = A.p + (r0 + i) * A.rs + g * A.cs;
+  const float* b = B.p + g * B.rs + (c0 + i) * B.cs;
+  f32x4 acc2 = zero4();
+  for (int k0 = 0; k0 < kd; k0 += 32) {
+    float av[8], bv[8];
+    const int n = kd - k0 >= 32 ? 8 : 4;
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      av[u] = u < n ? a[(k0 + 4 * u) * A.cs] : 0.f;
+      bv[u] = u < n ? b[(k0 + 4 * u) * B.rs] : 0.f;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv[u], acc, 0, 0, 0);
+      acc2 = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u + 4], bv[u + 4], acc2, 0, 0, 0);
+    }
+  }
+  return acc + acc2;
+}
 
 __device__ __forceinline__ int64_t tok(const int64_t b, const int64_t t, const int64_t T, const int64_t H,
                                        const int64_t h) {
@@ -129,8 +157,71 @@ __device__ __forceinline__ int64_t xcd_block(unsigned b, unsigned nb) {
   return static_cast<int64_t>(x) * per + (x < rem ? x : rem) + b / 8;
 }
 
-// ---- prep_kernel: per-chunk intermediates ----------------------------------
+// Four consecutive elements of an input row, as f32.
 template <class IT>
+__device__ __forceinline__ f32x4 load4(const IT* p) {
+  typedef IT v4 __attribute__((ext_vector_type(4)));
+  const v4 x = *reinterpret_cast<const v4*>(p);
+  return f32x4{to_float(x[0]), to_float(x[1]), to_float(x[2]), to_float(x[3])};
+}
+template <>
+__device__ __forceinline__ f32x4 load4<float>(const float* p) {
+  return *reinterpret_cast<const f32x4*>(p);
+}
+
+// Columns col0 .. col0+NCOL-1 of the chunk's 64 rows of an input [B,T,H,X]
+// into LDS rows of stride RS, zero past T and X.  Every load of a thread is
+// issued before its first LDS store.
+template <class IT, int NCOL, int RS, int NT>
+__device__ __forceinline__ void load_rows(float* dst, const IT* src, int64_t b, int64_t t0, int64_t T, int64_t H,
+                                          int64_t h, int64_t X, int col0, int tid) {
+  constexpr int G = NCOL / 4, PER = kC * G / NT;
+  static_assert(PER * NT == kC * G, "the tile must split evenly over the threads");
+  const bool vec = (X & 3) == 0;
+  f32x4 v[PER];
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+    const int64_t t = t0 + r;
+    const int64_t col = col0 + c4;
+    const IT* p = src + tok(b, t, T, H, h) * X + col;
+    if (t < T && vec && col + 3 < X) {
+      v[it] = load4<IT>(p);
+    } else {
+      f32x4 x = zero4();
+#pragma unroll
+      for (int u = 0; u < 4; ++u) x[u] = (t < T && col + u < X) ? to_float(p[u]) : 0.f;
+      v[it] = x;
+    }
+  }
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+    *reinterpret_cast<f32x4*>(&dst[r * RS + c4]) = v[it];
+  }
+}
+
+// NROW x NCOL f32 from a workspace matrix (row stride ld, from column col0)
+// into LDS rows of stride RS.
+template <int NROW, int NCOL, int RS, int NT>
+__device__ __forceinline__ void load_ws(float* dst, const float* src, int ld, int col0, int tid) {
+  constexpr int G = NCOL / 4, PER = NROW * G / NT;
+  static_assert(PER * NT == NROW * G, "the tile must split evenly over the threads");
+  f32x4 v[PER];
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+    v[it] = *reinterpret_cast<const f32x4*>(src + r * ld + col0 + c4);
+  }
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+    *reinterpret_cast<f32x4*>(&dst[r * RS + c4]) = v[it];
+  }
+}
+
+// ---- prep_kernel: per-chunk intermediates ----------------------------------
+template <class IT, int KP>
 __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
   __shared__ float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS];
   __shared__ float AS[kC * kRC], AqkS[kC * kRC], NS[kC * kRC];
@@ -139,23 +230,13 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
   const int64_t t0 = c * kC;
-  const int Kp = a.L.Kp, Vp = a.L.Vp;
+  constexpr int Kp = KP;
+  const int Vp = a.L.Vp;
   float* ws = a.ws + ch * a.L.per;
 
-  for (int idx = tid; idx < kC * Kp; idx += 256) {
-    const int r = idx / Kp, col = idx % Kp;
-    const int64_t t = t0 + r;
-    float kv = 0.f, qv = 0.f, gv = 0.f;
-    if (t < a.T && col < a.K) {
-      const int64_t off = tok(b, t, a.T, a.H, h) * a.K + col;
-      kv = to_float(a.k[off]);
-      qv = to_float(a.q[off]);
-      gv = to_float(a.g[off]);
-    }
-    kS[r * kRS + col] = kv;
-    qS[r * kRS + col] = qv;
-    lgS[r * kRS + col] = gv;
-  }
+  load_rows<IT, KP, kRS, 256>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_rows<IT, KP, kRS, 256>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_rows<IT, KP, kRS, 256>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid);
   if (tid < kC) {
     const int64_t t = t0 + tid;
     bS[tid] = t < a.T ? to_float(a.beta[tok(b, t, a.T, a.H, h)]) : 0.f;
@@ -182,15 +263,16 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
     const int i0 = 2 * I2, j0 = 2 * J2;
     const bool off_diag = I2 != J2;  // pair (i0, j0 + 1) lies above the diagonal on the diagonal block
     float aa[2][2] = {{0.f, 0.f}, {0.f, 0.f}}, aq[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
+#pragma unroll 2
     for (int kc = 0; kc < Kp; kc += 4) {
-      float4 ki[2], qi[2], li[2], kj[2], lj[2];
+      f32x4 ki[2], qi[2], li[2], kj[2], lj[2];
 #pragma unroll
       for (int x = 0; x < 2; ++x) {
-        ki[x] = *reinterpret_cast<const float4*>(&kS[(i0 + x) * kRS + kc]);
-        qi[x] = *reinterpret_cast<const float4*>(&qS[(i0 + x) * kRS + kc]);
-        li[x] = *reinterpret_cast<const float4*>(&lgS[(i0 + x) * kRS + kc]);
-        kj[x] = *reinterpret_cast<const float4*>(&kS[(j0 + x) * kRS + kc]);
-        lj[x] = *reinterpret_cast<const float4*>(&lgS[(j0 + x) * kRS + kc]);
+        ki[x] = *reinterpret_cast<const f32x4*>(&kS[(i0 + x) * kRS + kc]);
+        qi[x] = *reinterpret_cast<const f32x4*>(&qS[(i0 + x) * kRS + kc]);
+        li[x] = *reinterpret_cast<const f32x4*>(&lgS[(i0 + x) * kRS + kc]);
+        kj[x] = *reinterpret_cast<const f32x4*>(&kS[(j0 + x) * kRS + kc]);
+        lj[x] = *reinterpret_cast<const f32x4*>(&lgS[(j0 + x) * kRS + kc]);
       }
 #pragma unroll
       for (int x = 0; x < 2; ++x)
@@ -215,36 +297,61 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
       }
   }
   __syncthreads();
-  if (w == 0) {
-    // N = (I + diag(b) A)^-1 by forward substitution; lane c holds column c
-    float nc[kC];
-#pragma unroll
-    for (int i = 0; i < kC; ++i) {
-      float s = 0.f;
-#pragma unroll
-      for (int j = 0; j < i; ++j) s += AS[i * kRC + j] * nc[j];
-      nc[i] = (i == lane) ? 1.f : (i > lane ? -bS[i] * s : 0.f);
-    }
-#pragma unroll
-    for (int i = 0; i < kC; ++i) NS[i * kRC + lane] = nc[i];
-  } else {
-    for (int idx = tid - 64; idx < kC * kC; idx += 192) {
-      const int r = idx >> 6, cc = idx & 63;
-      ws[a.L.A + idx] = AS[r * kRC + cc];
-      ws[a.L.Aqk + idx] = AqkS[r * kRC + cc];
-    }
-    for (int idx = tid - 64; idx < kC * Kp; idx += 192) {
-      const int r = idx / Kp, col = idx % Kp;
-      const float lg = lgS[r * kRS + col], last = lgS[(kC - 1) * kRS + col];
-      const float e = fast_exp(lg), kv = kS[r * kRS + col];
-      ws[a.L.Qg + idx] = e * qS[r * kRS + col];
-      ws[a.L.Kt + idx] = fast_exp(last - lg) * kv;
-      ws[a.L.Kg + idx] = e * kv;
-      kS[r * kRS + col] = e * kv;  // Kg, the B operand of W = M Kg
-    }
-    if (tid - 64 < Kp) ws[a.L.D + (tid - 64)] = fast_exp(lgS[(kC - 1) * kRS + (tid - 64)]);
+  for (int idx = tid; idx < kC * kC; idx += 256) {
+    const int r = idx >> 6, cc = idx & 63;
+    ws[a.L.A + idx] = AS[r * kRC + cc];
+    ws[a.L.Aqk + idx] = AqkS[r * kRC + cc];
+  }
+  for (int idx = tid; idx < kC * Kp; idx += 256) {
+    const int r = idx / Kp, col = idx % Kp;
+    const float lg = lgS[r * kRS + col], last = lgS[(kC - 1) * kRS + col];
+    const float e = fast_exp(lg), kv = kS[r * kRS + col];
+    ws[a.L.Qg + idx] = e * qS[r * kRS + col];
+    ws[a.L.Kt + idx] = fast_exp(last - lg) * kv;
+    ws[a.L.Kg + idx] = e * kv;
+    kS[r * kRS + col] = e * kv;  // Kg, the B operand of W = M Kg
+  }
+  if (tid < Kp) ws[a.L.D + tid] = fast_exp(lgS[(kC - 1) * kRS + tid]);
+  __syncthreads();
+  for (int idx = tid; idx < kC * kC; idx += 256) {  // L's strict part b_i A_ij over A; N cleared
+    const int r = idx >> 6, cc = idx & 63;
+    AS[r * kRC + cc] *= bS[r];
+    NS[r * kRC + cc] = 0.f;
   }
   __syncthreads();
+  // N = L^-1 by 16x16 blocks: wave w inverts diagonal block w by forward
+  // substitution (lane c < 16 solves column c), then block rows I = 1..3 follow
+  // N_IJ = -N_II sum_{K=J}^{I-1} L_IK N_KJ on the MFMA.
+  if (lane < 16) {
+    const int base = 16 * w;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float sacc = 0.f;
+#pragma unroll
+      for (int j = 0; j < i; ++j) sacc += AS[(base + i) * kRC + base + j] * x[j];
+      x[i] = i == lane ? 1.f : (i > lane ? -sacc : 0.f);
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) NS[(base + i) * kRC + base + lane] = x[i];
+  }
+  __syncthreads();
+  float* TS = qS + w * 16 * kTS;  // q is no longer read: 16x16 scratch per wave
+  for (int I = 1; I < 4; ++I) {
+    if (w < I) {
+      const f32x4 t = mma(zero4(), Mat{AS + 16 * w, kRC, 1}, 16 * I, Mat{NS + 16 * w * kRC, kRC, 1}, 16 * w,
+                          16 * (I - w));
+#pragma unroll
+      for (int r = 0; r < 4; ++r) TS[(4 * lg4 + r) * kTS + li] = t[r];
+    }
+    __syncthreads();
+    if (w < I) {
+      const f32x4 n = mma(zero4(), Mat{NS + 16 * I, kRC, 1}, 16 * I, Mat{TS, kTS, 1}, 0, 16);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) NS[(16 * I + 4 * lg4 + r) * kRC + 16 * w + li] = -n[r];
+    }
+    __syncthreads();
+  }
   for (int idx = tid; idx < kC * kC; idx += 256) {  // M = N diag(b) over A
     const int r = idx >> 6, cc = idx & 63;
     const float n = NS[r * kRC + cc];
@@ -255,19 +362,16 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
   const int nkt = Kp / 16, nvt = Vp / 16;
   for (int tt = w; tt < 4 * nkt; tt += 4) {  // W = M Kg
     const int rt = tt & 3, ct = tt >> 2;
-    const f32x4 acc = mma(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{kS, kRS, 1}, 16 * ct, kC);
+    const f32x4 acc = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{kS, kRS, 1}, 16 * ct, kC);
 #pragma unroll
     for (int r = 0; r < 4; ++r) ws[a.L.W + (16 * rt + 4 * lg4 + r) * Kp + 16 * ct + li] = acc[r];
   }
-  for (int idx = tid; idx < kC * Vp; idx += 256) {  // v over lg (no longer read)
-    const int r = idx / Vp, col = idx % Vp;
-    const int64_t t = t0 + r;
-    lgS[r * kRS + col] = (t < a.T && col < a.V) ? to_float(a.v[tok(b, t, a.T, a.H, h) * a.V + col]) : 0.f;
-  }
+  for (int s0 = 0; s0 < Vp; s0 += 32)  // v over lg (no longer read)
+    load_rows<IT, 32, kRS, 256>(lgS + s0, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
   __syncthreads();
   for (int tt = w; tt < 4 * nvt; tt += 4) {  // U = M v
     const int rt = tt & 3, ct = tt >> 2;
-    const f32x4 acc = mma(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{lgS, kRS, 1}, 16 * ct, kC);
+    const f32x4 acc = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{lgS, kRS, 1}, 16 * ct, kC);
 #pragma unroll
     for (int r = 0; r < 4; ++r) ws[a.L.U + (16 * rt + 4 * lg4 + r) * Vp + 16 * ct + li] = acc[r];
   }
@@ -278,43 +382,50 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
 //   Vt = U[:, cols] - W S,  S <- D S + Kt^T Vt.
 // The next chunk's W, Kt, U and D are loaded into registers while the current
 // chunk is computed.
-constexpr int kPF = 8;  // float4 per thread of one [64][128] f32 matrix
+constexpr int kPF = 8;  // f32x4 per thread of one [64][128] f32 matrix
 
-template <class IT>
+struct FscanBuf {
+  f32x4 w[kPF], k[kPF];
+  float u[4], d;
+};
+
+template <class IT, int KP>
+__device__ __forceinline__ void fscan_fetch(FscanBuf& p, const Args<IT>& a, int64_t bh, int64_t c, int col0, int tid) {
+  constexpr int nq = kC * KP / 4;
+  const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
+#pragma unroll
+  for (int m = 0; m < kPF; ++m) {
+    const int q4 = tid + 256 * m;
+    if (q4 < nq) {
+      p.w[m] = *reinterpret_cast<const f32x4*>(ws + a.L.W + 4 * q4);
+      p.k[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Kt + 4 * q4);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int idx = tid + 256 * m;  // [64][16]
+    p.u[m] = ws[a.L.U + (idx >> 4) * a.L.Vp + col0 + (idx & 15)];
+  }
+  if (tid < KP) p.d = ws[a.L.D + tid];
+}
+
+template <class IT, int KP>
 __global__ __launch_bounds__(256) void fscan_kernel(const Args<IT> a) {
   __shared__ float WS[kC * kRS], KtS[kC * kRS], SS[128 * kTS], US[kC * kTS], DS[128];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
-  const int Kp = a.L.Kp, Vp = a.L.Vp, ncb = Vp / 16;
+  constexpr int Kp = KP, nq = kC * KP / 4;
+  const int Vp = a.L.Vp, ncb = Vp / 16;
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
   const int col0 = 16 * static_cast<int>(lb % ncb);
-  const int nq = kC * Kp / 4;  // float4 per [64][Kp] matrix
   for (int idx = tid; idx < Kp * 16; idx += 256) {
     const int r = idx >> 4, cc = idx & 15;
     SS[r * kTS + cc] = (a.s0 != nullptr && r < a.K && col0 + cc < a.V)
                            ? a.s0[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
                            : 0.f;
   }
-  float4 pw[kPF], pk[kPF];
-  float pu[4], pd = 0.f;
-  auto fetch = [&](int64_t c) {
-    const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
-#pragma unroll
-    for (int m = 0; m < kPF; ++m) {
-      const int q4 = tid + 256 * m;
-      if (q4 < nq) {
-        pw[m] = *reinterpret_cast<const float4*>(ws + a.L.W + 4 * q4);
-        pk[m] = *reinterpret_cast<const float4*>(ws + a.L.Kt + 4 * q4);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int idx = tid + 256 * m;  // [64][16]
-      pu[m] = ws[a.L.U + (idx >> 4) * Vp + col0 + (idx & 15)];
-    }
-    if (tid < Kp) pd = ws[a.L.D + tid];
-  };
-  fetch(0);
+  FscanBuf pf;
+  fscan_fetch<IT, KP>(pf, a, bh, 0, col0, tid);
   for (int64_t c = 0; c < a.NC; ++c) {
     float* ws = a.ws + (bh * a.NC + c) * a.L.per;
 #pragma unroll
@@ -322,24 +433,24 @@ __global__ __launch_bounds__(256) void fscan_kernel(const Args<IT> a) {
       const int q4 = tid + 256 * m;
       if (q4 < nq) {
         const int e = 4 * q4, r = e / Kp, col = e % Kp;
-        *reinterpret_cast<float4*>(&WS[r * kRS + col]) = pw[m];
-        *reinterpret_cast<float4*>(&KtS[r * kRS + col]) = pk[m];
+        *reinterpret_cast<f32x4*>(&WS[r * kRS + col]) = pf.w[m];
+        *reinterpret_cast<f32x4*>(&KtS[r * kRS + col]) = pf.k[m];
       }
     }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int idx = tid + 256 * m;
-      US[(idx >> 4) * kTS + (idx & 15)] = pu[m];
+      US[(idx >> 4) * kTS + (idx & 15)] = pf.u[m];
     }
-    if (tid < Kp) DS[tid] = pd;
+    if (tid < Kp) DS[tid] = pf.d;
     for (int idx = tid; idx < Kp * 16; idx += 256) {  // the chunk's start state
       const int r = idx >> 4, cc = idx & 15;
       ws[a.L.S + r * Vp + col0 + cc] = SS[r * kTS + cc];
     }
     __syncthreads();
-    if (c + 1 < a.NC) fetch(c + 1);
+    if (c + 1 < a.NC) fscan_fetch<IT, KP>(pf, a, bh, c + 1, col0, tid);
     // Vt = U - W S, rows 16w..16w+15
-    const f32x4 acc = mma(zero4(), Mat{WS, kRS, 1}, 16 * w, Mat{SS, kTS, 1}, 0, Kp);
+    const f32x4 acc = mma_long(zero4(), Mat{WS, kRS, 1}, 16 * w, Mat{SS, kTS, 1}, 0, Kp);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * w + 4 * lg4 + r;
@@ -349,7 +460,7 @@ __global__ __launch_bounds__(256) void fscan_kernel(const Args<IT> a) {
     }
     __syncthreads();
     for (int rt = w; rt < Kp / 16; rt += 4) {  // S <- D S + Kt^T Vt
-      const f32x4 upd = mma(zero4(), Mat{KtS, 1, kRS}, 16 * rt, Mat{US, kTS, 1}, 0, kC);
+      const f32x4 upd = mma_long(zero4(), Mat{KtS, 1, kRS}, 16 * rt, Mat{US, kTS, 1}, 0, kC);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * rt + 4 * lg4 + r;
@@ -362,46 +473,54 @@ __global__ __launch_bounds__(256) void fscan_kernel(const Args<IT> a) {
 
 // ---- bscan_kernel: state gradients backwards through the chunks -------------
 //   dVt = Kt dS + Aqk^T dO[:, cols],  dS <- D dS + Qg^T dO[:, cols] - W^T dVt.
-template <class IT>
+struct BscanBuf {
+  f32x4 k[kPF], q[kPF], w[kPF], a[4];
+  float o[4], d;
+};
+
+template <class IT, int KP>
+__device__ __forceinline__ void bscan_fetch(BscanBuf& p, const Args<IT>& a, int64_t bh, int64_t b, int64_t h,
+                                            int64_t c, int col0, int tid) {
+  constexpr int nq = kC * KP / 4;
+  const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
+#pragma unroll
+  for (int m = 0; m < kPF; ++m) {
+    const int q4 = tid + 256 * m;
+    if (q4 < nq) {
+      p.k[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Kt + 4 * q4);
+      p.q[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Qg + 4 * q4);
+      p.w[m] = *reinterpret_cast<const f32x4*>(ws + a.L.W + 4 * q4);
+    }
+  }
+#pragma unroll
+  for (int m = 0; m < 4; ++m) p.a[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Aqk + 4 * (tid + 256 * m));
+#pragma unroll
+  for (int m = 0; m < 4; ++m) {
+    const int idx = tid + 256 * m, r = idx >> 4, cc = idx & 15;
+    const int64_t t = c * kC + r;
+    p.o[m] = (t < a.T && col0 + cc < a.V) ? to_float(a.dout[tok(b, t, a.T, a.H, h) * a.V + col0 + cc]) : 0.f;
+  }
+  if (tid < KP) p.d = ws[a.L.D + tid];
+}
+
+template <class IT, int KP>
 __global__ __launch_bounds__(256) void bscan_kernel(const Args<IT> a) {
   __shared__ float KtS[kC * kRS], QgS[kC * kRS], WS[kC * kRS], AqkS[kC * kRC];
   __shared__ float dSS[128 * kTS], dOS[kC * kTS], XS[kC * kTS], DS[128];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
-  const int Kp = a.L.Kp, Vp = a.L.Vp, ncb = Vp / 16;
+  constexpr int Kp = KP, nq = kC * KP / 4;
+  const int Vp = a.L.Vp, ncb = Vp / 16;
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
   const int col0 = 16 * static_cast<int>(lb % ncb);
-  const int nq = kC * Kp / 4;
   for (int idx = tid; idx < Kp * 16; idx += 256) {
     const int r = idx >> 4, cc = idx & 15;
     dSS[r * kTS + cc] = (a.dsT != nullptr && r < a.K && col0 + cc < a.V)
                             ? a.dsT[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
                             : 0.f;
   }
-  float4 pk[kPF], pq[kPF], pw[kPF], pa[4];
-  float po[4], pd = 0.f;
-  auto fetch = [&](int64_t c) {
-    const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
-#pragma unroll
-    for (int m = 0; m < kPF; ++m) {
-      const int q4 = tid + 256 * m;
-      if (q4 < nq) {
-        pk[m] = *reinterpret_cast<const float4*>(ws + a.L.Kt + 4 * q4);
-        pq[m] = *reinterpret_cast<const float4*>(ws + a.L.Qg + 4 * q4);
-        pw[m] = *reinterpret_cast<const float4*>(ws + a.L.W + 4 * q4);
-      }
-    }
-#pragma unroll
-    for (int m = 0; m < 4; ++m) pa[m] = *reinterpret_cast<const float4*>(ws + a.L.Aqk + 4 * (tid + 256 * m));
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int idx = tid + 256 * m, r = idx >> 4, cc = idx & 15;
-      const int64_t t = c * kC + r;
-      po[m] = (t < a.T && col0 + cc < a.V) ? to_float(a.dout[tok(b, t, a.T, a.H, h) * a.V + col0 + cc]) : 0.f;
-    }
-    if (tid < Kp) pd = ws[a.L.D + tid];
-  };
-  fetch(a.NC - 1);
+  BscanBuf pf;
+  bscan_fetch<IT, KP>(pf, a, bh, b, h, a.NC - 1, col0, tid);
   for (int64_t c = a.NC - 1; c >= 0; --c) {
     float* ws = a.ws + (bh * a.NC + c) * a.L.per;
 #pragma unroll
@@ -409,31 +528,31 @@ __global__ __launch_bounds__(256) void bscan_kernel(const Args<IT> a) {
       const int q4 = tid + 256 * m;
       if (q4 < nq) {
         const int e = 4 * q4, r = e / Kp, col = e % Kp;
-        *reinterpret_cast<float4*>(&KtS[r * kRS + col]) = pk[m];
-        *reinterpret_cast<float4*>(&QgS[r * kRS + col]) = pq[m];
-        *reinterpret_cast<float4*>(&WS[r * kRS + col]) = pw[m];
+        *reinterpret_cast<f32x4*>(&KtS[r * kRS + col]) = pf.k[m];
+        *reinterpret_cast<f32x4*>(&QgS[r * kRS + col]) = pf.q[m];
+        *reinterpret_cast<f32x4*>(&WS[r * kRS + col]) = pf.w[m];
       }
     }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int e = 4 * (tid + 256 * m), r = e >> 6, cc = e & 63;
-      *reinterpret_cast<float4*>(&AqkS[r * kRC + cc]) = pa[m];
+      *reinterpret_cast<f32x4*>(&AqkS[r * kRC + cc]) = pf.a[m];
     }
 #pragma unroll
     for (int m = 0; m < 4; ++m) {
       const int idx = tid + 256 * m;
-      dOS[(idx >> 4) * kTS + (idx & 15)] = po[m];
+      dOS[(idx >> 4) * kTS + (idx & 15)] = pf.o[m];
     }
-    if (tid < Kp) DS[tid] = pd;
+    if (tid < Kp) DS[tid] = pf.d;
     for (int idx = tid; idx < Kp * 16; idx += 256) {  // gradient of the chunk's end state
       const int r = idx >> 4, cc = idx & 15;
       ws[a.L.dS + r * Vp + col0 + cc] = dSS[r * kTS + cc];
     }
     __syncthreads();
-    if (c > 0) fetch(c - 1);
+    if (c > 0) bscan_fetch<IT, KP>(pf, a, bh, b, h, c - 1, col0, tid);
     // dVt = Kt dS + Aqk^T dO, rows 16w..16w+15
-    f32x4 acc = mma(zero4(), Mat{KtS, kRS, 1}, 16 * w, Mat{dSS, kTS, 1}, 0, Kp);
-    acc = mma(acc, Mat{AqkS, 1, kRC}, 16 * w, Mat{dOS, kTS, 1}, 0, kC);
+    f32x4 acc = mma_long(zero4(), Mat{KtS, kRS, 1}, 16 * w, Mat{dSS, kTS, 1}, 0, Kp);
+    acc = mma_long(acc, Mat{AqkS, 1, kRC}, 16 * w, Mat{dOS, kTS, 1}, 0, kC);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * w + 4 * lg4 + r;
@@ -442,8 +561,8 @@ __global__ __launch_bounds__(256) void bscan_kernel(const Args<IT> a) {
     }
     __syncthreads();
     for (int rt = w; rt < Kp / 16; rt += 4) {  // dS <- D dS + Qg^T dO - W^T dVt
-      const f32x4 p = mma(zero4(), Mat{QgS, 1, kRS}, 16 * rt, Mat{dOS, kTS, 1}, 0, kC);
-      const f32x4 n = mma(zero4(), Mat{WS, 1, kRS}, 16 * rt, Mat{XS, kTS, 1}, 0, kC);
+      const f32x4 p = mma_long(zero4(), Mat{QgS, 1, kRS}, 16 * rt, Mat{dOS, kTS, 1}, 0, kC);
+      const f32x4 n = mma_long(zero4(), Mat{WS, 1, kRS}, 16 * rt, Mat{XS, kTS, 1}, 0, kC);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * rt + 4 * lg4 + r;
@@ -483,7 +602,7 @@ static_assert(kOffX + kC * kRS <= kOffY, "dW must not overlap Kg");
 static_assert(kOffY + kC * kRS <= kGradFloats, "Kg must fit");
 static_assert(kOffDM + kC * kRC <= kOffDN && kOffA + kC * kRC <= kGradFloats, "second-stage tiles must fit");
 
-template <class IT>
+template <class IT, int KP>
 __global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
   __shared__ float sm[kGradFloats];
   __shared__ float bS[kC];
@@ -491,7 +610,8 @@ __global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
   const int64_t t0 = c * kC;
-  const int Kp = a.L.Kp, Vp = a.L.Vp, nkt = Kp / 16;
+  constexpr int Kp = KP, nkt = KP / 16;
+  const int Vp = a.L.Vp;
   float* ws = a.ws + ch * a.L.per;
   float* MS = sm + kOffM;
   if (tid < kC) {
@@ -509,24 +629,14 @@ __global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
   float dd = 0.f;
   float *Ss = sm + kOffSs, *dSn = sm + kOffdSn, *dOs = sm + kOffdOs, *Vts = sm + kOffVts, *dVts = sm + kOffdVts,
         *vs = sm + kOffvs;
-  for (int s0 = 0; s0 < Vp; s0 += kSW) {
-    const int sw = Vp - s0 < kSW ? Vp - s0 : kSW;
-    for (int idx = tid; idx < Kp * kSW; idx += 256) {
-      const int r = idx / kSW, cc = idx % kSW;
-      const bool in = cc < sw;
-      Ss[r * kSS + cc] = in ? ws[a.L.S + r * Vp + s0 + cc] : 0.f;
-      dSn[r * kSS + cc] = in ? ws[a.L.dS + r * Vp + s0 + cc] : 0.f;
-    }
-    for (int idx = tid; idx < kC * kSW; idx += 256) {
-      const int r = idx / kSW, cc = idx % kSW;
-      const int64_t t = t0 + r;
-      const bool in = cc < sw, real = in && t < a.T && s0 + cc < a.V;
-      const int64_t off = tok(b, t, a.T, a.H, h) * a.V + s0 + cc;
-      dOs[r * kSS + cc] = real ? to_float(a.dout[off]) : 0.f;
-      vs[r * kSS + cc] = real ? to_float(a.v[off]) : 0.f;
-      Vts[r * kSS + cc] = in ? ws[a.L.Vt + r * Vp + s0 + cc] : 0.f;
-      dVts[r * kSS + cc] = in ? ws[a.L.dVt + r * Vp + s0 + cc] : 0.f;
-    }
+  for (int s0 = 0; s0 < Vp; s0 += kSW) {  // Vp is a multiple of the slab width
+    constexpr int sw = kSW;
+    load_ws<KP, kSW, kSS, 256>(Ss, ws + a.L.S, Vp, s0, tid);
+    load_ws<KP, kSW, kSS, 256>(dSn, ws + a.L.dS, Vp, s0, tid);
+    load_ws<kC, kSW, kSS, 256>(Vts, ws + a.L.Vt, Vp, s0, tid);
+    load_ws<kC, kSW, kSS, 256>(dVts, ws + a.L.dVt, Vp, s0, tid);
+    load_rows<IT, kSW, kSS, 256>(dOs, a.dout, b, t0, a.T, a.H, h, a.V, s0, tid);
+    load_rows<IT, kSW, kSS, 256>(vs, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
     __syncthreads();
     for (int tt = w; tt < 4 * (sw / 16); tt += 4) {  // dv = M^T dVt
       const int rt = tt & 3, ct = tt >> 2;
@@ -577,28 +687,25 @@ __global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
       const int row = 16 * w + 4 * lg4 + r, col = 16 * ct + li;
       ws[a.L.dAqk + row * kC + col] = col <= row ? aA[ct][r] : 0.f;
     }
-  for (int idx = tid; idx < kC * Kp; idx += 256) Y[(idx / Kp) * kRS + idx % Kp] = ws[a.L.Kg + idx];
+  load_ws<kC, KP, kRS, 256>(Y, ws + a.L.Kg, KP, 0, tid);
   if (tid < Kp) ws[a.L.dD + tid] = dd;
   __syncthreads();
 #pragma unroll
   for (int ct = 0; ct < 8; ++ct) {  // dKg = M^T dW
     if (ct < nkt) {
-      const f32x4 acc = mma(zero4(), Mat{MS, 1, kRC}, 16 * w, Mat{X, kRS, 1}, 16 * ct, kC);
+      const f32x4 acc = mma_long(zero4(), Mat{MS, 1, kRC}, 16 * w, Mat{X, kRS, 1}, 16 * ct, kC);
 #pragma unroll
       for (int r = 0; r < 4; ++r) ws[a.L.dKg + (16 * w + 4 * lg4 + r) * Kp + 16 * ct + li] = acc[r];
     }
   }
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) aM[ct] = mma(aM[ct], Mat{X, kRS, 1}, 16 * w, Mat{Y, 1, kRS}, 16 * ct, Kp);  // dM += dW Kg^T
+  for (int ct = 0; ct < 4; ++ct) aM[ct] = mma_long(aM[ct], Mat{X, kRS, 1}, 16 * w, Mat{Y, 1, kRS}, 16 * ct, Kp);  // dM += dW Kg^T
   __syncthreads();
 
   // dbeta and dA from N: dN = dM diag(b), T1 = N^T dN, dL = -strict(T1 N^T)
   float *NS = sm + kOffN, *DM = sm + kOffDM, *DN = sm + kOffDN, *AS = sm + kOffA;
-  for (int idx = tid; idx < kC * kC; idx += 256) {
-    const int r = idx >> 6, cc = idx & 63;
-    NS[r * kRC + cc] = ws[a.L.N + idx];
-    AS[r * kRC + cc] = ws[a.L.A + idx];
-  }
+  load_ws<kC, kC, kRC, 256>(NS, ws + a.L.N, kC, 0, tid);
+  load_ws<kC, kC, kRC, 256>(AS, ws + a.L.A, kC, 0, tid);
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
@@ -613,7 +720,7 @@ __global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
     for (int r = 0; r < kC; ++r) db += NS[r * kRC + tid] * DM[r * kRC + tid];
   f32x4 t1[4];
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) t1[ct] = mma(zero4(), Mat{NS, 1, kRC}, 16 * w, Mat{DN, kRC, 1}, 16 * ct, kC);
+  for (int ct = 0; ct < 4; ++ct) t1[ct] = mma_long(zero4(), Mat{NS, 1, kRC}, 16 * w, Mat{DN, kRC, 1}, 16 * ct, kC);
   __syncthreads();
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct)
@@ -622,7 +729,7 @@ __global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
   __syncthreads();
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
-    const f32x4 acc = mma(zero4(), Mat{DM, kRC, 1}, 16 * w, Mat{NS, 1, kRC}, 16 * ct, kC);
+    const f32x4 acc = mma_long(zero4(), Mat{DM, kRC, 1}, 16 * w, Mat{NS, 1, kRC}, 16 * ct, kC);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * w + 4 * lg4 + r, col = 16 * ct + li;
@@ -640,42 +747,38 @@ __global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
 }
 
 // ---- pair_kernel: pair sums with exact exponents and the final dq, dk, dg ----
-// Thread (column col, part p) owns rows i = p + P m of its column (P = 256 / Kp)
-// and forms
+// Thread (column col, part p) owns rows i = p + P m of its column (P = NT / Kp,
+// RP = 64 / P rows) and forms
 //   R1_i = sum_j dA_ij k_j E_ij,  R2_i = sum_j dAqk_ij k_j E_ij   (j <= i)
 //   R3_j = sum_i dA_ij k_i E_ij,  R4_j = sum_i dAqk_ij q_i E_ij   (i >= j)
 // then dk = R1 + R3 + R4 + e^lg dKg + e^(lg_last - lg) dKt, dq = R2 + e^lg dQg,
 // d lg = k R1 - k R3 + q R2 - k R4 + Kg dKg + Qg dQg - Kt dKt (+ the last row's
 // sum(Kt dKt) + D dD), and dg as its reverse cumulative sum.
-template <class IT, int RP>
-__global__ __launch_bounds__(256) void pair_kernel(const Args<IT> a) {
+// The sums run over blocks of 4P positions; a block only visits the owned rows
+// it can reach (a compile-time range), and a select drops the pairs on the
+// wrong side of the diagonal inside it, so no branch separates the operand
+// reads.  dA and dAqk are read four positions at a time along their rows, then
+// transposed in place for the second sum.
+template <class IT, int KP, int NT>
+__global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
+  constexpr int RP = kC * KP / NT;  // rows per thread
+  constexpr int P = kC / RP;   // parts per column
+  constexpr int JB = 4 * P;    // positions per block
+  constexpr int NB = kC / JB;  // blocks
+  static_assert(RP % 4 == 0 && NB * JB == kC, "rows per thread must be a multiple of 4");
   __shared__ float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS], dAS[kC * kRC], dQS[kC * kRC];
-  __shared__ float red[16 * 128];
+  __shared__ float red[P * 128];
   const int tid = threadIdx.x;
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
   const int64_t t0 = c * kC;
-  const int Kp = a.L.Kp;
-  constexpr int P = kC / RP;  // parts per column (Kp = 256 / P)
+  constexpr int Kp = KP;
   const float* ws = a.ws + ch * a.L.per;
-  for (int idx = tid; idx < kC * Kp; idx += 256) {
-    const int r = idx / Kp, col = idx % Kp;
-    const int64_t t = t0 + r;
-    float kv = 0.f, qv = 0.f, gv = 0.f;
-    if (t < a.T && col < a.K) {
-      const int64_t off = tok(b, t, a.T, a.H, h) * a.K + col;
-      kv = to_float(a.k[off]);
-      qv = to_float(a.q[off]);
-      gv = to_float(a.g[off]);
-    }
-    kS[r * kRS + col] = kv;
-    qS[r * kRS + col] = qv;
-    lgS[r * kRS + col] = gv;
-  }
-  for (int idx = tid; idx < kC * kC; idx += 256) {
-    dAS[(idx >> 6) * kRC + (idx & 63)] = ws[a.L.dA + idx];
-    dQS[(idx >> 6) * kRC + (idx & 63)] = ws[a.L.dAqk + idx];
-  }
+  load_rows<IT, KP, kRS, NT>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_rows<IT, KP, kRS, NT>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_rows<IT, KP, kRS, NT>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_ws<kC, kC, kRC, NT>(dAS, ws + a.L.dA, kC, 0, tid);
+  load_ws<kC, kC, kRC, NT>(dQS, ws + a.L.dAqk, kC, 0, tid);
   __syncthreads();
   if (tid < Kp) {
     float s = 0.f;
@@ -686,52 +789,114 @@ __global__ __launch_bounds__(256) void pair_kernel(const Args<IT> a) {
   }
   __syncthreads();
   const int col = tid % Kp, part = tid / Kp;
-  float li[RP], ki[RP], qi[RP], R1[RP], R2[RP], R3[RP], R4[RP];
+  float li[RP], R1[RP], R2[RP], R3[RP], R4[RP];
 #pragma unroll
   for (int m = 0; m < RP; ++m) {
-    const int i = part + P * m;
-    li[m] = lgS[i * kRS + col];
-    ki[m] = kS[i * kRS + col];
-    qi[m] = qS[i * kRS + col];
+    li[m] = lgS[(part + P * m) * kRS + col];
     R1[m] = R2[m] = R3[m] = R4[m] = 0.f;
   }
-  for (int j = 0; j < kC; ++j) {  // j-sums: rows i >= j of this thread
-    const float kj = kS[j * kRS + col], lj = lgS[j * kRS + col];
 #pragma unroll
-    for (int m = 0; m < RP; ++m) {
-      const int i = part + P * m;
-      if (i >= j) {
-        const float ke = kj * fast_exp(li[m] - lj);
-        R1[m] += dAS[i * kRC + j] * ke;
-        R2[m] += dQS[i * kRC + j] * ke;
+  for (int jb = 0; jb < NB; ++jb) {  // j-sums: rows i >= j
+#pragma unroll 1
+    for (int j4 = jb * JB; j4 < (jb + 1) * JB; j4 += 4) {
+      f32x4 kj, lj;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        kj[u] = kS[(j4 + u) * kRS + col];
+        lj[u] = lgS[(j4 + u) * kRS + col];
+      }
+#pragma unroll
+      for (int m0 = 4 * jb; m0 < RP; m0 += 4) {  // four rows at a time: reads first
+        f32x4 da[4], dq[4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const int i = part + P * (m0 + x);
+          da[x] = *reinterpret_cast<const f32x4*>(&dAS[i * kRC + j4]);
+          dq[x] = *reinterpret_cast<const f32x4*>(&dQS[i * kRC + j4]);
+        }
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const int m = m0 + x, i = part + P * m;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float e = fast_exp(li[m] - lj[u]);
+            const float ke = j4 + u <= i ? kj[u] * e : 0.f;
+            R1[m] += da[x][u] * ke;
+            R2[m] += dq[x][u] * ke;
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);  // bounds the live operands
       }
     }
   }
-  for (int i = 0; i < kC; ++i) {  // i-sums: rows j <= i of this thread
-    const float kv = kS[i * kRS + col], qv = qS[i * kRS + col], lv = lgS[i * kRS + col];
+  __syncthreads();
+  for (int idx = tid; idx < kC * kC; idx += NT) {  // transpose dA and dAqk in place
+    const int r = idx >> 6, cc = idx & 63;
+    if (r < cc) {
+      const float x = dAS[r * kRC + cc], y = dQS[r * kRC + cc];
+      dAS[r * kRC + cc] = dAS[cc * kRC + r];
+      dQS[r * kRC + cc] = dQS[cc * kRC + r];
+      dAS[cc * kRC + r] = x;
+      dQS[cc * kRC + r] = y;
+    }
+  }
+  __syncthreads();
 #pragma unroll
-    for (int m = 0; m < RP; ++m) {
-      const int j = part + P * m;
-      if (i >= j) {
-        const float e = fast_exp(lv - li[m]);
-        R3[m] += dAS[i * kRC + j] * kv * e;
-        R4[m] += dQS[i * kRC + j] * qv * e;
+  for (int ib = 0; ib < NB; ++ib) {  // i-sums: rows j <= i
+#pragma unroll 1
+    for (int i4 = ib * JB; i4 < (ib + 1) * JB; i4 += 4) {
+      f32x4 ki4, qi4, li4;
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        ki4[u] = kS[(i4 + u) * kRS + col];
+        qi4[u] = qS[(i4 + u) * kRS + col];
+        li4[u] = lgS[(i4 + u) * kRS + col];
+      }
+#pragma unroll
+      for (int m0 = 0; m0 < 4 * (ib + 1) && m0 < RP; m0 += 4) {
+        f32x4 da[4], dq[4];
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const int j = part + P * (m0 + x);
+          da[x] = *reinterpret_cast<const f32x4*>(&dAS[j * kRC + i4]);
+          dq[x] = *reinterpret_cast<const f32x4*>(&dQS[j * kRC + i4]);
+        }
+#pragma unroll
+        for (int x = 0; x < 4; ++x) {
+          const int m = m0 + x, j = part + P * m;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const float e = fast_exp(li4[u] - li[m]);
+            const float w = i4 + u >= j ? e : 0.f;
+            R3[m] += da[x][u] * ki4[u] * w;
+            R4[m] += dq[x][u] * qi4[u] * w;
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
       }
     }
   }
   const float last = lgS[(kC - 1) * kRS + col];
   __syncthreads();  // every read of q ends before d lg overwrites it
   float lastsum = 0.f;
+  float gKg[RP], gKt[RP], gQg[RP];
+#pragma unroll
+  for (int m = 0; m < RP; ++m) {  // every load before the first store
+    const int64_t rec = static_cast<int64_t>(part + P * m) * Kp + col;
+    gKg[m] = ws[a.L.dKg + rec];
+    gKt[m] = ws[a.L.dKt + rec];
+    gQg[m] = ws[a.L.dQg + rec];
+  }
 #pragma unroll
   for (int m = 0; m < RP; ++m) {
     const int i = part + P * m;
-    const int64_t rec = static_cast<int64_t>(i) * Kp + col;
+    const float kv = kS[i * kRS + col], qv = qS[i * kRS + col];
     const float e = fast_exp(li[m]), te = fast_exp(last - li[m]);
-    const float dKg = ws[a.L.dKg + rec], dKt = ws[a.L.dKt + rec], dQg = ws[a.L.dQg + rec];
+    const float dKg = gKg[m], dKt = gKt[m], dQg = gQg[m];
     const float dk = R1[m] + R3[m] + R4[m] + e * dKg + te * dKt;
     const float dq = R2[m] + e * dQg;
-    const float ktd = te * ki[m] * dKt;
-    qS[i * kRS + col] = ki[m] * (R1[m] - R3[m] - R4[m]) + qi[m] * R2[m] + e * ki[m] * dKg + e * qi[m] * dQg - ktd;
+    const float ktd = te * kv * dKt;
+    qS[i * kRS + col] = kv * (R1[m] - R3[m] - R4[m]) + qv * R2[m] + e * kv * dKg + e * qv * dQg - ktd;
     lastsum += ktd;
     const int64_t t = t0 + i;
     if (t < a.T && col < a.K) {
@@ -766,6 +931,15 @@ size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int
   return static_cast<size_t>(B * H * nc * L.per) * sizeof(float);
 }
 
+template <class IT, int KP>
+static void launch_all(const bwd::Args<IT>& a, dim3 chunks, dim3 scans, hipStream_t s) {
+  hipLaunchKernelGGL((bwd::prep_kernel<IT, KP>), chunks, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bwd::fscan_kernel<IT, KP>), scans, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bwd::bscan_kernel<IT, KP>), scans, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bwd::grad_kernel<IT, KP>), chunks, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bwd::pair_kernel<IT, KP, 512>), chunks, dim3(512), 0, s, a);
+}
+
 template <class IT>
 static int run_bwd(const bwd::Args<IT>& a, hipStream_t s) {
   const int64_t chunks = a.B * a.H * a.NC;
@@ -774,16 +948,11 @@ static int run_bwd(const bwd::Args<IT>& a, hipStream_t s) {
     set_detail("chunk backward: grid too large");
     return KDA_ERR_UNSUPPORTED;
   }
-  hipLaunchKernelGGL((bwd::prep_kernel<IT>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a);
-  hipLaunchKernelGGL((bwd::fscan_kernel<IT>), dim3(static_cast<unsigned>(scans)), dim3(256), 0, s, a);
-  hipLaunchKernelGGL((bwd::bscan_kernel<IT>), dim3(static_cast<unsigned>(scans)), dim3(256), 0, s, a);
-  hipLaunchKernelGGL((bwd::grad_kernel<IT>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a);
-  switch (a.L.Kp) {
-    case 16: hipLaunchKernelGGL((bwd::pair_kernel<IT, 4>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a); break;
-    case 32: hipLaunchKernelGGL((bwd::pair_kernel<IT, 8>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a); break;
-    case 64: hipLaunchKernelGGL((bwd::pair_kernel<IT, 16>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a); break;
-    default: hipLaunchKernelGGL((bwd::pair_kernel<IT, 32>), dim3(static_cast<unsigned>(chunks)), dim3(256), 0, s, a); break;
-  }
+  const dim3 gc(static_cast<unsigned>(chunks)), gs(static_cast<unsigned>(scans));
+  if (a.L.Kp == 64)
+    launch_all<IT, 64>(a, gc, gs, s);
+  else
+    launch_all<IT, 128>(a, gc, gs, s);
   return check_launch("chunk backward");
 }
 
