@@ -220,6 +220,58 @@ __device__ __forceinline__ void load_ws(float* dst, const float* src, int ld, in
   }
 }
 
+// Decay products e^(lg_i - lg_j) (j <= i) are formed on the MFMA as
+// (x_i e^(lg_i - r)) (y_j e^(r - lg_j)) with r = lg at the first row of i's
+// 16-row block: for a chunk whose g are all <= 0 (lg falls down the chunk) and
+// whose decay across any 16-row block stays within kMaxBlockDecay, the first
+// factor lies in [e^-80, 1] and the second is <= 1 off the diagonal block (it
+// underflows only where the product itself is negligible) and <= e^80 on it.
+// Other chunks take the exact pairwise path.
+constexpr float kMaxBlockDecay = 80.f;
+
+// True when the chunk needs the exact path; lg in LDS rows of stride kRS,
+// the raw g's sign having been folded into `nonneg` by the caller.
+template <int KP, int NT>
+__device__ __forceinline__ bool needs_exact(const float* lgS, bool nonneg, int tid) {
+  bool risky = nonneg;
+  for (int idx = tid; idx < 4 * KP; idx += NT) {
+    const int I = idx / KP, c = idx % KP;
+    risky |= lgS[16 * I * kRS + c] - lgS[(16 * I + 15) * kRS + c] > kMaxBlockDecay;
+  }
+  return __syncthreads_or(risky);
+}
+
+// accK += sum_c (k_i e^(lg_i - r)) (k_j e^(r - lg_j)) and accQ the same with
+// q_i, for rows i in [r0, r0+16), columns j in [c0, c0+16) and r = lg[rr];
+// the reduction runs over the kd channels.
+__device__ __forceinline__ void decay_product(f32x4& accK, f32x4& accQ, const float* kS, const float* qS,
+                                              const float* lgS, int r0, int c0, int rr, int kd) {
+  const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  for (int k0 = 0; k0 < kd; k0 += 16) {
+    float ka[4], qa[4], kb[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int ch = k0 + 4 * u + g;
+      const float r = lgS[rr * kRS + ch];
+      const float ea = fast_exp(lgS[(r0 + i) * kRS + ch] - r), eb = fast_exp(r - lgS[(c0 + i) * kRS + ch]);
+      ka[u] = kS[(r0 + i) * kRS + ch] * ea;
+      qa[u] = qS[(r0 + i) * kRS + ch] * ea;
+      kb[u] = kS[(c0 + i) * kRS + ch] * eb;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      accK = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[u], kb[u], accK, 0, 0, 0);
+      accQ = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[u], kb[u], accQ, 0, 0, 0);
+    }
+  }
+}
+
+// The ten 16x16 block pairs (I, J <= I) of a chunk.
+__device__ __forceinline__ void block_pair(int p, int& I, int& J) {
+  I = p < 1 ? 0 : (p < 3 ? 1 : (p < 6 ? 2 : 3));
+  J = p - I * (I + 1) / 2;
+}
+
 // ---- prep_kernel: per-chunk intermediates ----------------------------------
 template <class IT, int KP>
 __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
@@ -246,14 +298,32 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
     AqkS[idx] = 0.f;
   }
   __syncthreads();
+  bool rising = false;
   if (tid < Kp) {  // lg = cumsum(g) down the chunk
     float s = 0.f;
     for (int r = 0; r < kC; ++r) {
-      s += lgS[r * kRS + tid];
+      const float gv = lgS[r * kRS + tid];
+      rising |= gv > 0.f;
+      s += gv;
       lgS[r * kRS + tid] = s;
     }
   }
   __syncthreads();
+  if (!needs_exact<KP, 256>(lgS, rising, tid)) {
+    // A and Aqk block by block on the MFMA
+    for (int p = w; p < 10; p += 4) {
+      int I, J;
+      block_pair(p, I, J);
+      f32x4 ak = zero4(), aq = zero4();
+      decay_product(ak, aq, kS, qS, lgS, 16 * I, 16 * J, 16 * I, Kp);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * I + 4 * lg4 + r, col = 16 * J + li;
+        if (col < row) AS[row * kRC + col] = ak[r];
+        if (col <= row) AqkS[row * kRC + col] = aq[r];
+      }
+    }
+  } else
   // A and Aqk with exact pair exponents, 2x2 blocks of (i, j <= i)
   for (int blk = tid; blk < 528; blk += 256) {
     int I2 = static_cast<int>((sqrtf(8.f * blk + 1.f) - 1.f) * 0.5f);
@@ -759,35 +829,18 @@ __global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
 // wrong side of the diagonal inside it, so no branch separates the operand
 // reads.  dA and dAqk are read four positions at a time along their rows, then
 // transposed in place for the second sum.
+// Exact path: thread (column col, part p) owns rows i = p + P m of its column.
+// Leaves d lg in qS and each thread's sum(Kt dKt) in red[p][col].
 template <class IT, int KP, int NT>
-__global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
+__device__ __forceinline__ void pair_exact(const Args<IT>& a, const float* ws, float* kS, float* qS, float* lgS,
+                                           float* dAS, float* dQS, float* red, int64_t b, int64_t h, int64_t t0,
+                                           int tid) {
   constexpr int RP = kC * KP / NT;  // rows per thread
-  constexpr int P = kC / RP;   // parts per column
-  constexpr int JB = 4 * P;    // positions per block
-  constexpr int NB = kC / JB;  // blocks
+  constexpr int P = kC / RP;        // parts per column
+  constexpr int JB = 4 * P;         // positions per block
+  constexpr int NB = kC / JB;       // blocks
   static_assert(RP % 4 == 0 && NB * JB == kC, "rows per thread must be a multiple of 4");
-  __shared__ float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS], dAS[kC * kRC], dQS[kC * kRC];
-  __shared__ float red[P * 128];
-  const int tid = threadIdx.x;
-  const int64_t ch = blockIdx.x;
-  const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
-  const int64_t t0 = c * kC;
   constexpr int Kp = KP;
-  const float* ws = a.ws + ch * a.L.per;
-  load_rows<IT, KP, kRS, NT>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid);
-  load_rows<IT, KP, kRS, NT>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid);
-  load_rows<IT, KP, kRS, NT>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid);
-  load_ws<kC, kC, kRC, NT>(dAS, ws + a.L.dA, kC, 0, tid);
-  load_ws<kC, kC, kRC, NT>(dQS, ws + a.L.dAqk, kC, 0, tid);
-  __syncthreads();
-  if (tid < Kp) {
-    float s = 0.f;
-    for (int r = 0; r < kC; ++r) {
-      s += lgS[r * kRS + tid];
-      lgS[r * kRS + tid] = s;
-    }
-  }
-  __syncthreads();
   const int col = tid % Kp, part = tid / Kp;
   float li[RP], R1[RP], R2[RP], R3[RP], R4[RP];
 #pragma unroll
@@ -906,10 +959,148 @@ __global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
     }
   }
   red[part * 128 + col] = lastsum;
+}
+
+// MFMA path (NT = 512, eight waves): wave w owns rows 16J.. (J = w / 2) and
+// half of the column tiles.  With r_I = lg at row 16I and i in block I,
+//   R1_I = e^(lg - r_I) (dA_I,: (k e^(r_I - lg))),  R2 the same with dAqk,
+//   R3_J = sum_{I >= J} e^(r_I - lg) (dA_IJ^T (k e^(lg - r_I))_I),  R4 with dAqk, q.
+// Leaves d lg in qS and partial sums of Kt dKt in red[4J + g][col].
+template <class IT, int KP>
+__device__ __forceinline__ void pair_mfma(const Args<IT>& a, const float* ws, float* kS, float* qS, float* lgS,
+                                          float* dAS, float* dQS, float* red, int64_t b, int64_t h, int64_t t0,
+                                          int tid) {
+  constexpr int CW = KP / 32;  // column tiles per wave
+  const int w = tid >> 6, lane = tid & 63, li = lane & 15, lg4 = lane >> 4;
+  const int J = w >> 1, ct0 = (w & 1) * CW;
+  f32x4 R1[CW], R2[CW], R3[CW], R4[CW];
+#pragma unroll
+  for (int ct = 0; ct < CW; ++ct) R1[ct] = R2[ct] = R3[ct] = R4[ct] = zero4();
+#pragma unroll
+  for (int ct = 0; ct < CW; ++ct) {  // R1, R2 over j < 16 (J + 1)
+    const int cc = 16 * (ct0 + ct) + li;
+    const float rI = lgS[16 * J * kRS + cc];
+    for (int k0 = 0; k0 < 16 * (J + 1); k0 += 4) {
+      const int j = k0 + lg4;
+      const float bk = kS[j * kRS + cc] * fast_exp(rI - lgS[j * kRS + cc]);
+      R1[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(dAS[(16 * J + li) * kRC + j], bk, R1[ct], 0, 0, 0);
+      R2[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(dQS[(16 * J + li) * kRC + j], bk, R2[ct], 0, 0, 0);
+    }
+  }
+  for (int I = J; I < 4; ++I) {  // R3, R4 over rows i of block I >= J
+#pragma unroll
+    for (int ct = 0; ct < CW; ++ct) {
+      const int cc = 16 * (ct0 + ct) + li;
+      const float rI = lgS[16 * I * kRS + cc];
+      f32x4 t3 = zero4(), t4 = zero4();
+#pragma unroll
+      for (int k0 = 0; k0 < 16; k0 += 4) {
+        const int i = 16 * I + k0 + lg4;
+        const float e = fast_exp(lgS[i * kRS + cc] - rI);
+        t3 = __builtin_amdgcn_mfma_f32_16x16x4f32(dAS[i * kRC + 16 * J + li], kS[i * kRS + cc] * e, t3, 0, 0, 0);
+        t4 = __builtin_amdgcn_mfma_f32_16x16x4f32(dQS[i * kRC + 16 * J + li], qS[i * kRS + cc] * e, t4, 0, 0, 0);
+      }
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float sc = fast_exp(rI - lgS[(16 * J + 4 * lg4 + r) * kRS + cc]);
+        R3[ct][r] += t3[r] * sc;
+        R4[ct][r] += t4[r] * sc;
+      }
+    }
+  }
+  // the element's own inputs and gradient pieces, all loaded before any store
+  float kv[CW][4], qv[CW][4], lv[CW][4], gKg[CW][4], gKt[CW][4], gQg[CW][4];
+#pragma unroll
+  for (int ct = 0; ct < CW; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * J + 4 * lg4 + r, cc = 16 * (ct0 + ct) + li;
+      const int64_t rec = static_cast<int64_t>(row) * KP + cc;
+      gKg[ct][r] = ws[a.L.dKg + rec];
+      gKt[ct][r] = ws[a.L.dKt + rec];
+      gQg[ct][r] = ws[a.L.dQg + rec];
+      kv[ct][r] = kS[row * kRS + cc];
+      qv[ct][r] = qS[row * kRS + cc];
+      lv[ct][r] = lgS[row * kRS + cc];
+    }
+  __syncthreads();  // every read of q ends before d lg overwrites it
+#pragma unroll
+  for (int ct = 0; ct < CW; ++ct) {
+    const int cc = 16 * (ct0 + ct) + li;
+    const float rJ = lgS[16 * J * kRS + cc], last = lgS[(kC - 1) * kRS + cc];
+    float part = 0.f;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * J + 4 * lg4 + r;
+      const float f1 = fast_exp(lv[ct][r] - rJ);
+      const float r1 = R1[ct][r] * f1, r2 = R2[ct][r] * f1, r3 = R3[ct][r], r4 = R4[ct][r];
+      const float e = fast_exp(lv[ct][r]), te = fast_exp(last - lv[ct][r]);
+      const float k_ = kv[ct][r], q_ = qv[ct][r];
+      const float dk = r1 + r3 + r4 + e * gKg[ct][r] + te * gKt[ct][r];
+      const float dq = r2 + e * gQg[ct][r];
+      const float ktd = te * k_ * gKt[ct][r];
+      qS[row * kRS + cc] = k_ * (r1 - r3 - r4) + q_ * r2 + e * k_ * gKg[ct][r] + e * q_ * gQg[ct][r] - ktd;
+      part += ktd;
+      const int64_t t = t0 + row;
+      if (t < a.T && cc < a.K) {
+        const int64_t off = tok(b, t, a.T, a.H, h) * a.K + cc;
+        a.dq[off] = from_compute<IT>(dq);
+        a.dk[off] = from_compute<IT>(dk);
+      }
+    }
+    red[(4 * J + lg4) * 128 + cc] = part;
+  }
+}
+
+// ---- pair_kernel: the pair sums and the final dq, dk, dg ----------------------
+//   R1_i = sum_j dA_ij k_j E_ij,  R2_i = sum_j dAqk_ij k_j E_ij   (j <= i)
+//   R3_j = sum_i dA_ij k_i E_ij,  R4_j = sum_i dAqk_ij q_i E_ij   (i >= j)
+// then dk = R1 + R3 + R4 + e^lg dKg + e^(lg_last - lg) dKt, dq = R2 + e^lg dQg,
+// d lg = k R1 - k R3 + q R2 - k R4 + Kg dKg + Qg dQg - Kt dKt (+ the last row's
+// sum(Kt dKt) + D dD), and dg as its reverse cumulative sum.  The sums run on
+// the MFMA with the block factorisation of the decay unless the chunk needs
+// the exact pairwise path.
+template <class IT, int KP, int NT>
+__global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
+  static_assert(NT == 512, "the MFMA path uses eight waves");
+  __shared__ float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS], dAS[kC * kRC], dQS[kC * kRC];
+  __shared__ float red[16 * 128];
+  const int tid = threadIdx.x;
+  const int64_t ch = blockIdx.x;
+  const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
+  const int64_t t0 = c * kC;
+  constexpr int Kp = KP;
+  const float* ws = a.ws + ch * a.L.per;
+  load_rows<IT, KP, kRS, NT>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_rows<IT, KP, kRS, NT>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_rows<IT, KP, kRS, NT>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_ws<kC, kC, kRC, NT>(dAS, ws + a.L.dA, kC, 0, tid);
+  load_ws<kC, kC, kRC, NT>(dQS, ws + a.L.dAqk, kC, 0, tid);
+  __syncthreads();
+  bool rising = false;
+  if (tid < Kp) {
+    float s = 0.f;
+    for (int r = 0; r < kC; ++r) {
+      const float gv = lgS[r * kRS + tid];
+      rising |= gv > 0.f;
+      s += gv;
+      lgS[r * kRS + tid] = s;
+    }
+  }
+  __syncthreads();
+  int nred;
+  if (!needs_exact<KP, NT>(lgS, rising, tid)) {
+    pair_mfma<IT, KP>(a, ws, kS, qS, lgS, dAS, dQS, red, b, h, t0, tid);
+    nred = 16;
+  } else {
+    pair_exact<IT, KP, NT>(a, ws, kS, qS, lgS, dAS, dQS, red, b, h, t0, tid);
+    nred = kC / (kC * KP / NT);
+  }
   __syncthreads();
   if (tid < Kp) {
+    const float last = lgS[(kC - 1) * kRS + tid];
     float run = fast_exp(last) * ws[a.L.dD + tid];
-    for (int p = 0; p < P; ++p) run += red[p * 128 + tid];
+    for (int p = 0; p < nred; ++p) run += red[p * 128 + tid];
     for (int i = kC - 1; i >= 0; --i) {
       run += qS[i * kRS + tid];
       const int64_t t = t0 + i;

@@ -107,3 +107,24 @@ def test_backward_refuses_unsupported_cases():
     q2, k2, v2, g2, b2, _ = (t.to(DEV) if t is not None else None for t in workload(1, 8, 1, 16, 16))
     with pytest.raises(RuntimeError, match="cu_seqlens"):
         kda.chunkwise_kda(q2.requires_grad_(), k2, v2, g2, b2, cu_seqlens=[0, 4, 8])
+
+
+@pytest.mark.parametrize("regime", ["steep", "rising"])
+def test_backward_exact_path_regimes(regime):
+    # chunks whose decay falls by more than 80 within 16 tokens, or whose g is
+    # positive somewhere, take the exact pairwise path instead of the MFMA
+    # factorisation; both must match the oracle
+    B, T, H, K, V = 1, 128, 2, 128, 64
+    inputs, d_out, d_final = _case(B, T, H, K, V, torch.float32, seed=6)
+    q, k, v, g, beta, s0 = inputs
+    gen = torch.Generator().manual_seed(7)
+    if regime == "steep":
+        g = -6.0 - 6.0 * torch.rand(B, T, H, K, generator=gen)
+    else:
+        g = 0.02 * torch.randn(B, T, H, K, generator=gen)
+    inputs = (q, k, v, g, beta, s0)
+    got = _gpu_grads(inputs, d_out, d_final)
+    ref = _oracle_grads(inputs, d_out, d_final)
+    for name, a, b in zip(NAMES, got, ref):
+        assert torch.isfinite(a).all(), name
+        assert rel_err(a, b) < TOL[torch.float32], (name, rel_err(a, b))
