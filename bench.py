@@ -19,6 +19,8 @@ Metric: "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s".
                workload, on the host cores (thread count reported).
 * fused_stages: the kernels around the operator (kda.fused) on the same
                shape, as HBM GB/s (not part of `value`).
+* backward   : the chunkwise backward (all input gradients) on the prefill
+               workload, ms and tokens/s (not part of `value`).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3]
 """
@@ -241,6 +243,54 @@ def bench_fused(reps=50):
     return res
 
 
+def bench_backward(reps=10):
+    """The chunkwise backward (kda_chunk_bwd) on the prefill workload: all
+    input gradients and dS0 from upstream gradients of the output and the
+    final state.  `reps` back-to-back calls through the C ABI into
+    preallocated outputs, HIP events on the launch stream."""
+    import torch
+
+    from kda import _lib, _prep
+
+    lib = _lib.load()
+    device = torch.device("cuda", 0)
+    q, k, v, g, beta, s0 = _inputs(P_B, P_T, P_H, P_K, P_V, 0.02, 0, device)
+    gen = torch.Generator(device=device).manual_seed(9)
+    d_out = torch.randn(P_B, P_T, P_H, P_V, generator=gen, device=device).to(torch.bfloat16)
+    d_final = torch.randn(P_B, P_H, P_K, P_V, generator=gen, device=device)
+    grads = [torch.empty_like(t) for t in (q, k, v, g, beta)]
+    ds0 = torch.empty_like(s0)
+    nbytes = lib.kda_chunk_bwd_workspace_bytes(P_B, P_T, P_H, P_K, P_V)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    code = _lib.dtype_code(torch.bfloat16)
+    stream = _prep.stream(device)
+
+    def call():
+        _lib.check(lib.kda_chunk_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
+                                     d_out.data_ptr(), code, s0.data_ptr(), d_final.data_ptr(),
+                                     *[t.data_ptr() for t in grads], ds0.data_ptr(), P_B, P_T, P_H, P_K, P_V,
+                                     ws.data_ptr(), nbytes, stream))
+
+    for _ in range(2):
+        call()
+    torch.cuda.synchronize()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        call()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    return {
+        "workload": f"chunkwise backward B={P_B} T={P_T} H={P_H} K=V={P_K}, bf16 inputs, f32 arithmetic "
+                    "(dq, dk, dv, dg, dbeta, dS0)",
+        "ms": round(ms, 4),
+        "tokens_per_s": round(P_B * P_T / (ms * 1e-3), 1),
+        "workspace_bytes": nbytes,
+    }
+
+
 def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
     """The oracle's CPU restatement, timed like benchmarks/benchmark_kda.py:30-40
     (one warm-up, then min over repeats of time.perf_counter, inference_mode)."""
@@ -409,9 +459,10 @@ def main() -> int:
         },
     }
     result["fused_stages"] = {
-        "workload": f"B={P_B} T={P_T} H={P_H} D={P_K} bf16, one call each (median of 20)",
+        "workload": f"B={P_B} T={P_T} H={P_H} D={P_K} bf16, 50 back-to-back C-ABI launches each",
         "kernels": bench_fused(),
     }
+    result["backward"] = bench_backward()
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()
         result["cpu_baseline"] = cpu["prefill"]

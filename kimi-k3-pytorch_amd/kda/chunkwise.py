@@ -60,16 +60,11 @@ def chunkwise_kda(
     )
     _lib.require_gpu(q)
     work_dtype = accumulation_dtype(v.dtype, accumulate_state_in_fp32)
-    if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (q, k, v, g, beta, initial_state)):
+    if needs_grad(q, k, v, g, beta, initial_state):
         if offsets is not None:
             raise RuntimeError("the MI355X KDA backward does not support cu_seqlens; run the documents separately")
-        if work_dtype == torch.float64:
-            raise RuntimeError("the MI355X KDA backward supports bf16, f16 and f32 inputs (f32 arithmetic)")
-        if key_dim > 128 or value_dim > 128:
-            raise RuntimeError("the MI355X KDA backward supports key_dim and value_dim up to 128")
-        qm, gm, bm = _mask_differentiable(q, g, beta, attention_mask)
-        hidden, final = _ChunkwiseFunction.apply(qm, k, v, gm, bm, initial_state, output_final_state, work_dtype)
-        return KDAOperatorOutput(hidden_states=hidden, final_state=final)
+        return differentiable(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype,
+                              recurrent=False)
     return _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype, offsets,
                     batch, tokens, heads, key_dim, value_dim)
 
@@ -107,6 +102,25 @@ def _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask
     return KDAOperatorOutput(hidden_states=hidden, final_state=final)
 
 
+def needs_grad(*tensors) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors)
+
+
+def differentiable(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype, *,
+                   recurrent: bool) -> KDAOperatorOutput:
+    """The operator under autograd: masked inputs, the forward of
+    ``recurrent_kda`` (recurrent=True) or ``chunkwise_kda``, and the HIP chunk
+    backward, whose gradients are those of the exact recurrence either way."""
+    if work_dtype == torch.float64:
+        raise RuntimeError("the MI355X KDA backward supports bf16, f16 and f32 inputs (f32 arithmetic)")
+    if q.shape[-1] > 128 or v.shape[-1] > 128:
+        raise RuntimeError("the MI355X KDA backward supports key_dim and value_dim up to 128")
+    qm, gm, bm = _mask_differentiable(q, g, beta, attention_mask)
+    hidden, final = _ChunkwiseFunction.apply(qm, k, v, gm, bm, initial_state, output_final_state, work_dtype,
+                                             recurrent)
+    return KDAOperatorOutput(hidden_states=hidden, final_state=final)
+
+
 def _mask_differentiable(q, g, beta, attention_mask):
     """Zero q, g and beta at padded positions with tensor ops that autograd
     differentiates (src/kda/utils.py:82-94)."""
@@ -119,14 +133,20 @@ def _mask_differentiable(q, g, beta, attention_mask):
 
 
 class _ChunkwiseFunction(torch.autograd.Function):
-    """chunkwise_kda on masked, dense inputs with the HIP backward."""
+    """The operator on masked, dense inputs with the HIP chunk backward."""
 
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, initial_state, output_final_state, work_dtype):
+    def forward(ctx, q, k, v, g, beta, initial_state, output_final_state, work_dtype, recurrent):
         batch, tokens, heads, key_dim = q.shape
         value_dim = v.shape[-1]
-        out = _forward(q, k, v, g, beta, initial_state, output_final_state, None, work_dtype, None,
-                       batch, tokens, heads, key_dim, value_dim)
+        if recurrent:
+            from .recurrent import recurrent_kda
+
+            out = recurrent_kda(q, k, v, g, beta, initial_state, output_final_state,
+                                accumulate_state_in_fp32=work_dtype != v.dtype)
+        else:
+            out = _forward(q, k, v, g, beta, initial_state, output_final_state, None, work_dtype, None,
+                           batch, tokens, heads, key_dim, value_dim)
         ctx.save_for_backward(q, k, v, g, beta, initial_state)
         ctx.work_dtype = work_dtype
         if out.final_state is None:
@@ -162,4 +182,4 @@ class _ChunkwiseFunction(torch.autograd.Function):
         _lib.check(status)
         grads = [dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
                  None if ds0 is None else ds0.to(initial_state.dtype)]
-        return (*[gr if need else None for gr, need in zip(grads, ctx.needs_input_grad[:6])], None, None)
+        return (*[gr if need else None for gr, need in zip(grads, ctx.needs_input_grad[:6])], None, None, None)

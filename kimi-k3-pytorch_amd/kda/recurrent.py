@@ -60,10 +60,17 @@ def recurrent_kda(
     if return_states_per_token and offsets is not None:
         raise ValueError("return_states_per_token is not supported with cu_seqlens")
     _lib.require_gpu(q)
-    _prep.reject_autograd(q, k, v, g, beta, initial_state)
+    work_dtype = accumulation_dtype(v.dtype, accumulate_state_in_fp32)
+    from .chunkwise import differentiable, needs_grad
+
+    if needs_grad(q, k, v, g, beta, initial_state):
+        if offsets is not None or return_states_per_token or update_state_in_place:
+            raise RuntimeError("the MI355X KDA backward supports dense sequences without return_states_per_token "
+                               "or update_state_in_place")
+        return differentiable(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype,
+                              recurrent=True)
     lib = _lib.load()
 
-    work_dtype = accumulation_dtype(v.dtype, accumulate_state_in_fp32)
     (qc, kc, vc, gc, bc), kernel_dtype, arith = _prep.kernel_inputs(q, k, v, g, beta, work_dtype)
     device = q.device
     n_seq = batch if offsets is None else len(offsets) - 1

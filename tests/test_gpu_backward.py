@@ -128,3 +128,30 @@ def test_backward_exact_path_regimes(regime):
     for name, a, b in zip(NAMES, got, ref):
         assert torch.isfinite(a).all(), name
         assert rel_err(a, b) < TOL[torch.float32], (name, rel_err(a, b))
+
+
+def test_recurrent_kda_gradients_match_oracle():
+    # recurrent_kda under autograd: the recurrent forward, the chunk backward
+    # (the same gradients as the exact recurrence, test_kda_recurrent.py:184-198)
+    inputs, d_out, d_final = _case(2, 40, 2, 64, 32, torch.float32, seed=8)
+    leaves = [t.to(DEV).requires_grad_() for t in inputs]
+    res = kda.recurrent_kda(*leaves, True)
+    ((res.hidden_states * d_out.to(DEV)).sum() + (res.final_state * d_final.to(DEV)).sum()).backward()
+    ref = _oracle_grads(inputs, d_out, d_final)
+    for name, a, b in zip(NAMES, [t.grad for t in leaves], ref):
+        assert rel_err(a, b) < TOL[torch.float32], name
+    with pytest.raises(RuntimeError, match="return_states_per_token"):
+        kda.recurrent_kda(*leaves, True, return_states_per_token=True)
+
+
+def test_decode_step_gradients():
+    # a single decode step (T=1) under autograd
+    inputs, d_out, d_final = _case(3, 1, 2, 128, 128, torch.bfloat16, seed=9)
+    got = []
+    leaves = [t.to(DEV).requires_grad_() for t in inputs]
+    res = kda.recurrent_kda(*leaves, True)
+    ((res.hidden_states.float() * d_out.to(DEV).float()).sum() + (res.final_state * d_final.to(DEV)).sum()).backward()
+    got = [t.grad for t in leaves]
+    ref = _oracle_grads(inputs, d_out, d_final)
+    for name, a, b in zip(NAMES, got, ref):
+        assert rel_err(a, b) < TOL[torch.bfloat16], name
