@@ -157,47 +157,53 @@ __device__ __forceinline__ int64_t xcd_block(unsigned b, unsigned nb) {
   return static_cast<int64_t>(x) * per + (x < rem ? x : rem) + b / 8;
 }
 
-// Four consecutive elements of an input row, as f32.
+// Four consecutive elements of an input row: loaded raw, converted later, so
+// that a batch of loads is in flight before the first conversion waits.
 template <class IT>
-__device__ __forceinline__ f32x4 load4(const IT* p) {
-  typedef IT v4 __attribute__((ext_vector_type(4)));
-  const v4 x = *reinterpret_cast<const v4*>(p);
+struct Raw4 {
+  typedef IT type __attribute__((ext_vector_type(4)));
+};
+
+template <class IT>
+__device__ __forceinline__ f32x4 widen(typename Raw4<IT>::type x) {
   return f32x4{to_float(x[0]), to_float(x[1]), to_float(x[2]), to_float(x[3])};
-}
-template <>
-__device__ __forceinline__ f32x4 load4<float>(const float* p) {
-  return *reinterpret_cast<const f32x4*>(p);
 }
 
 // Columns col0 .. col0+NCOL-1 of the chunk's 64 rows of an input [B,T,H,X]
-// into LDS rows of stride RS, zero past T and X.  Every load of a thread is
-// issued before its first LDS store.
+// into LDS rows of stride RS, zero past T and X.  When the columns lie inside
+// X in whole 4-element groups (the usual case) every load of a thread is
+// issued, from a row clamped into the sequence, before its first conversion.
 template <class IT, int NCOL, int RS, int NT>
 __device__ __forceinline__ void load_rows(float* dst, const IT* src, int64_t b, int64_t t0, int64_t T, int64_t H,
                                           int64_t h, int64_t X, int col0, int tid) {
   constexpr int G = NCOL / 4, PER = kC * G / NT;
   static_assert(PER * NT == kC * G, "the tile must split evenly over the threads");
-  const bool vec = (X & 3) == 0;
-  f32x4 v[PER];
+  typedef typename Raw4<IT>::type raw_t;
+  if ((X & 3) == 0 && col0 + NCOL <= X) {
+    raw_t v[PER];
 #pragma unroll
-  for (int it = 0; it < PER; ++it) {
-    const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
-    const int64_t t = t0 + r;
-    const int64_t col = col0 + c4;
-    const IT* p = src + tok(b, t, T, H, h) * X + col;
-    if (t < T && vec && col + 3 < X) {
-      v[it] = load4<IT>(p);
-    } else {
+    for (int it = 0; it < PER; ++it) {
+      const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+      const int64_t t = t0 + r < T ? t0 + r : T - 1;
+      v[it] = *reinterpret_cast<const raw_t*>(src + tok(b, t, T, H, h) * X + col0 + c4);
+    }
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+      const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+      *reinterpret_cast<f32x4*>(&dst[r * RS + c4]) = t0 + r < T ? widen<IT>(v[it]) : zero4();
+    }
+  } else {
+    for (int it = 0; it < PER; ++it) {
+      const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+      const int64_t t = t0 + r;
       f32x4 x = zero4();
 #pragma unroll
-      for (int u = 0; u < 4; ++u) x[u] = (t < T && col + u < X) ? to_float(p[u]) : 0.f;
-      v[it] = x;
+      for (int u = 0; u < 4; ++u) {
+        const int64_t col = col0 + c4 + u;
+        x[u] = (t < T && col < X) ? to_float(src[tok(b, t, T, H, h) * X + col]) : 0.f;
+      }
+      *reinterpret_cast<f32x4*>(&dst[r * RS + c4]) = x;
     }
-  }
-#pragma unroll
-  for (int it = 0; it < PER; ++it) {
-    const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
-    *reinterpret_cast<f32x4*>(&dst[r * RS + c4]) = v[it];
   }
 }
 
@@ -448,15 +454,17 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
 }
 
 // ---- fscan_kernel: chunk start states and pseudo-values ----------------------
-// Block (sequence, head, 16 columns) carries S[:, cols] through the chunks:
-//   Vt = U[:, cols] - W S,  S <- D S + Kt^T Vt.
-// The next chunk's W, Kt, U and D are loaded into registers while the current
-// chunk is computed.
-constexpr int kPF = 8;  // f32x4 per thread of one [64][128] f32 matrix
+// Block (sequence, head, 16 columns), eight waves, carries S[:, cols] through
+// the chunks:  Vt = U[:, cols] - W S  (the two halves of the channel
+// reduction on waves 0-3 and 4-7),  S <- D S + Kt^T Vt  (one row tile per
+// wave).  The next chunk's W, Kt, U and D are loaded into registers while the
+// current chunk is computed.
+constexpr int kST = 512;  // threads of the scan blocks
+constexpr int kPF = 4;    // f32x4 per thread of one [64][128] f32 matrix
 
 struct FscanBuf {
   f32x4 w[kPF], k[kPF];
-  float u[4], d;
+  float u[2], d;
 };
 
 template <class IT, int KP>
@@ -465,30 +473,31 @@ __device__ __forceinline__ void fscan_fetch(FscanBuf& p, const Args<IT>& a, int6
   const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
 #pragma unroll
   for (int m = 0; m < kPF; ++m) {
-    const int q4 = tid + 256 * m;
+    const int q4 = tid + kST * m;
     if (q4 < nq) {
       p.w[m] = *reinterpret_cast<const f32x4*>(ws + a.L.W + 4 * q4);
       p.k[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Kt + 4 * q4);
     }
   }
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int idx = tid + 256 * m;  // [64][16]
+  for (int m = 0; m < 2; ++m) {
+    const int idx = tid + kST * m;  // [64][16]
     p.u[m] = ws[a.L.U + (idx >> 4) * a.L.Vp + col0 + (idx & 15)];
   }
   if (tid < KP) p.d = ws[a.L.D + tid];
 }
 
 template <class IT, int KP>
-__global__ __launch_bounds__(256) void fscan_kernel(const Args<IT> a) {
-  __shared__ float WS[kC * kRS], KtS[kC * kRS], SS[128 * kTS], US[kC * kTS], DS[128];
+__global__ __launch_bounds__(kST) void fscan_kernel(const Args<IT> a) {
+  __shared__ float WS[kC * kRS], KtS[kC * kRS], SS[128 * kTS], US[kC * kTS], PS[kC * kTS], DS[128];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
-  constexpr int Kp = KP, nq = kC * KP / 4;
+  const int half = w >> 2, wt = w & 3;
+  constexpr int Kp = KP, nq = kC * KP / 4, KH = KP / 2;
   const int Vp = a.L.Vp, ncb = Vp / 16;
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
   const int col0 = 16 * static_cast<int>(lb % ncb);
-  for (int idx = tid; idx < Kp * 16; idx += 256) {
+  for (int idx = tid; idx < Kp * 16; idx += kST) {
     const int r = idx >> 4, cc = idx & 15;
     SS[r * kTS + cc] = (a.s0 != nullptr && r < a.K && col0 + cc < a.V)
                            ? a.s0[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
@@ -500,7 +509,7 @@ __global__ __launch_bounds__(256) void fscan_kernel(const Args<IT> a) {
     float* ws = a.ws + (bh * a.NC + c) * a.L.per;
 #pragma unroll
     for (int m = 0; m < kPF; ++m) {
-      const int q4 = tid + 256 * m;
+      const int q4 = tid + kST * m;
       if (q4 < nq) {
         const int e = 4 * q4, r = e / Kp, col = e % Kp;
         *reinterpret_cast<f32x4*>(&WS[r * kRS + col]) = pf.w[m];
@@ -508,32 +517,39 @@ __global__ __launch_bounds__(256) void fscan_kernel(const Args<IT> a) {
       }
     }
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int idx = tid + 256 * m;
+    for (int m = 0; m < 2; ++m) {
+      const int idx = tid + kST * m;
       US[(idx >> 4) * kTS + (idx & 15)] = pf.u[m];
     }
     if (tid < Kp) DS[tid] = pf.d;
-    for (int idx = tid; idx < Kp * 16; idx += 256) {  // the chunk's start state
+    for (int idx = tid; idx < Kp * 16; idx += kST) {  // the chunk's start state
       const int r = idx >> 4, cc = idx & 15;
       ws[a.L.S + r * Vp + col0 + cc] = SS[r * kTS + cc];
     }
     __syncthreads();
     if (c + 1 < a.NC) fscan_fetch<IT, KP>(pf, a, bh, c + 1, col0, tid);
-    // Vt = U - W S, rows 16w..16w+15
-    const f32x4 acc = mma_long(zero4(), Mat{WS, kRS, 1}, 16 * w, Mat{SS, kTS, 1}, 0, Kp);
+    // W S over one half of the channels, rows 16 wt..
+    const f32x4 acc = mma_long(zero4(), Mat{WS + half * KH, kRS, 1}, 16 * wt, Mat{SS + half * KH * kTS, kTS, 1}, 0, KH);
+    if (half == 1) {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * w + 4 * lg4 + r;
-      const float vt = US[row * kTS + li] - acc[r];
-      US[row * kTS + li] = vt;
-      ws[a.L.Vt + row * Vp + col0 + li] = vt;
+      for (int r = 0; r < 4; ++r) PS[(16 * wt + 4 * lg4 + r) * kTS + li] = acc[r];
     }
     __syncthreads();
-    for (int rt = w; rt < Kp / 16; rt += 4) {  // S <- D S + Kt^T Vt
-      const f32x4 upd = mma_long(zero4(), Mat{KtS, 1, kRS}, 16 * rt, Mat{US, kTS, 1}, 0, kC);
+    if (half == 0) {  // Vt = U - W S
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 16 * rt + 4 * lg4 + r;
+        const int row = 16 * wt + 4 * lg4 + r;
+        const float vt = US[row * kTS + li] - acc[r] - PS[row * kTS + li];
+        US[row * kTS + li] = vt;
+        ws[a.L.Vt + row * Vp + col0 + li] = vt;
+      }
+    }
+    __syncthreads();
+    if (w < Kp / 16) {  // S <- D S + Kt^T Vt, row tile w
+      const f32x4 upd = mma_long(zero4(), Mat{KtS, 1, kRS}, 16 * w, Mat{US, kTS, 1}, 0, kC);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * w + 4 * lg4 + r;
         SS[row * kTS + li] = DS[row] * SS[row * kTS + li] + upd[r];
       }
     }
@@ -542,20 +558,24 @@ __global__ __launch_bounds__(256) void fscan_kernel(const Args<IT> a) {
 }
 
 // ---- bscan_kernel: state gradients backwards through the chunks -------------
-//   dVt = Kt dS + Aqk^T dO[:, cols],  dS <- D dS + Qg^T dO[:, cols] - W^T dVt.
+//   dVt = Kt dS + Aqk^T dO[:, cols]           (waves 0-3, one row tile each)
+//   dS  <- (D dS + Qg^T dO[:, cols]) - W^T dVt  (the bracket on waves 4-7 next
+//                                              to dVt, the product after it)
+template <class IT>
 struct BscanBuf {
-  f32x4 k[kPF], q[kPF], w[kPF], a[4];
-  float o[4], d;
+  f32x4 k[kPF], q[kPF], w[kPF], a[2];
+  IT o[2];  // raw dO, widened when written to LDS
+  float d;
 };
 
 template <class IT, int KP>
-__device__ __forceinline__ void bscan_fetch(BscanBuf& p, const Args<IT>& a, int64_t bh, int64_t b, int64_t h,
+__device__ __forceinline__ void bscan_fetch(BscanBuf<IT>& p, const Args<IT>& a, int64_t bh, int64_t b, int64_t h,
                                             int64_t c, int col0, int tid) {
   constexpr int nq = kC * KP / 4;
   const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
 #pragma unroll
   for (int m = 0; m < kPF; ++m) {
-    const int q4 = tid + 256 * m;
+    const int q4 = tid + kST * m;
     if (q4 < nq) {
       p.k[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Kt + 4 * q4);
       p.q[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Qg + 4 * q4);
@@ -563,39 +583,40 @@ __device__ __forceinline__ void bscan_fetch(BscanBuf& p, const Args<IT>& a, int6
     }
   }
 #pragma unroll
-  for (int m = 0; m < 4; ++m) p.a[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Aqk + 4 * (tid + 256 * m));
+  for (int m = 0; m < 2; ++m) p.a[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Aqk + 4 * (tid + kST * m));
 #pragma unroll
-  for (int m = 0; m < 4; ++m) {
-    const int idx = tid + 256 * m, r = idx >> 4, cc = idx & 15;
-    const int64_t t = c * kC + r;
-    p.o[m] = (t < a.T && col0 + cc < a.V) ? to_float(a.dout[tok(b, t, a.T, a.H, h) * a.V + col0 + cc]) : 0.f;
+  for (int m = 0; m < 2; ++m) {  // clamped into the tensor; masked when widened
+    const int idx = tid + kST * m, r = idx >> 4, cc = idx & 15;
+    const int64_t t = c * kC + r < a.T ? c * kC + r : a.T - 1;
+    const int64_t col = col0 + cc < a.V ? col0 + cc : a.V - 1;
+    p.o[m] = a.dout[tok(b, t, a.T, a.H, h) * a.V + col];
   }
   if (tid < KP) p.d = ws[a.L.D + tid];
 }
 
 template <class IT, int KP>
-__global__ __launch_bounds__(256) void bscan_kernel(const Args<IT> a) {
+__global__ __launch_bounds__(kST) void bscan_kernel(const Args<IT> a) {
   __shared__ float KtS[kC * kRS], QgS[kC * kRS], WS[kC * kRS], AqkS[kC * kRC];
-  __shared__ float dSS[128 * kTS], dOS[kC * kTS], XS[kC * kTS], DS[128];
+  __shared__ float dSS[128 * kTS], dSp[128 * kTS], dOS[kC * kTS], XS[kC * kTS], DS[128];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   constexpr int Kp = KP, nq = kC * KP / 4;
   const int Vp = a.L.Vp, ncb = Vp / 16;
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
   const int col0 = 16 * static_cast<int>(lb % ncb);
-  for (int idx = tid; idx < Kp * 16; idx += 256) {
+  for (int idx = tid; idx < Kp * 16; idx += kST) {
     const int r = idx >> 4, cc = idx & 15;
     dSS[r * kTS + cc] = (a.dsT != nullptr && r < a.K && col0 + cc < a.V)
                             ? a.dsT[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
                             : 0.f;
   }
-  BscanBuf pf;
+  BscanBuf<IT> pf;
   bscan_fetch<IT, KP>(pf, a, bh, b, h, a.NC - 1, col0, tid);
   for (int64_t c = a.NC - 1; c >= 0; --c) {
     float* ws = a.ws + (bh * a.NC + c) * a.L.per;
 #pragma unroll
     for (int m = 0; m < kPF; ++m) {
-      const int q4 = tid + 256 * m;
+      const int q4 = tid + kST * m;
       if (q4 < nq) {
         const int e = 4 * q4, r = e / Kp, col = e % Kp;
         *reinterpret_cast<f32x4*>(&KtS[r * kRS + col]) = pf.k[m];
@@ -604,45 +625,55 @@ __global__ __launch_bounds__(256) void bscan_kernel(const Args<IT> a) {
       }
     }
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int e = 4 * (tid + 256 * m), r = e >> 6, cc = e & 63;
+    for (int m = 0; m < 2; ++m) {
+      const int e = 4 * (tid + kST * m), r = e >> 6, cc = e & 63;
       *reinterpret_cast<f32x4*>(&AqkS[r * kRC + cc]) = pf.a[m];
     }
 #pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      const int idx = tid + 256 * m;
-      dOS[(idx >> 4) * kTS + (idx & 15)] = pf.o[m];
+    for (int m = 0; m < 2; ++m) {
+      const int idx = tid + kST * m, r = idx >> 4, cc = idx & 15;
+      const bool real = c * kC + r < a.T && col0 + cc < a.V;
+      dOS[r * kTS + cc] = real ? to_float(pf.o[m]) : 0.f;
     }
     if (tid < Kp) DS[tid] = pf.d;
-    for (int idx = tid; idx < Kp * 16; idx += 256) {  // gradient of the chunk's end state
+    for (int idx = tid; idx < Kp * 16; idx += kST) {  // gradient of the chunk's end state
       const int r = idx >> 4, cc = idx & 15;
       ws[a.L.dS + r * Vp + col0 + cc] = dSS[r * kTS + cc];
     }
     __syncthreads();
     if (c > 0) bscan_fetch<IT, KP>(pf, a, bh, b, h, c - 1, col0, tid);
-    // dVt = Kt dS + Aqk^T dO, rows 16w..16w+15
-    f32x4 acc = mma_long(zero4(), Mat{KtS, kRS, 1}, 16 * w, Mat{dSS, kTS, 1}, 0, Kp);
-    acc = mma_long(acc, Mat{AqkS, 1, kRC}, 16 * w, Mat{dOS, kTS, 1}, 0, kC);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * w + 4 * lg4 + r;
-      XS[row * kTS + li] = acc[r];
-      ws[a.L.dVt + row * Vp + col0 + li] = acc[r];
-    }
-    __syncthreads();
-    for (int rt = w; rt < Kp / 16; rt += 4) {  // dS <- D dS + Qg^T dO - W^T dVt
-      const f32x4 p = mma_long(zero4(), Mat{QgS, 1, kRS}, 16 * rt, Mat{dOS, kTS, 1}, 0, kC);
-      const f32x4 n = mma_long(zero4(), Mat{WS, 1, kRS}, 16 * rt, Mat{XS, kTS, 1}, 0, kC);
+    if (w < 4) {  // dVt = Kt dS + Aqk^T dO, rows 16w..
+      f32x4 acc = mma_long(zero4(), Mat{KtS, kRS, 1}, 16 * w, Mat{dSS, kTS, 1}, 0, Kp);
+      acc = mma_long(acc, Mat{AqkS, 1, kRC}, 16 * w, Mat{dOS, kTS, 1}, 0, kC);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 16 * rt + 4 * lg4 + r;
-        dSS[row * kTS + li] = DS[row] * dSS[row * kTS + li] + p[r] - n[r];
+        const int row = 16 * w + 4 * lg4 + r;
+        XS[row * kTS + li] = acc[r];
+        ws[a.L.dVt + row * Vp + col0 + li] = acc[r];
+      }
+    } else {  // D dS + Qg^T dO, row tiles w-4 and w
+      for (int rt = w - 4; rt < Kp / 16; rt += 4) {
+        const f32x4 p = mma_long(zero4(), Mat{QgS, 1, kRS}, 16 * rt, Mat{dOS, kTS, 1}, 0, kC);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * rt + 4 * lg4 + r;
+          dSp[row * kTS + li] = DS[row] * dSS[row * kTS + li] + p[r];
+        }
+      }
+    }
+    __syncthreads();
+    if (w < Kp / 16) {  // dS = dSp - W^T dVt, row tile w
+      const f32x4 n = mma_long(zero4(), Mat{WS, 1, kRS}, 16 * w, Mat{XS, kTS, 1}, 0, kC);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * w + 4 * lg4 + r;
+        dSS[row * kTS + li] = dSp[row * kTS + li] - n[r];
       }
     }
     __syncthreads();
   }
   if (a.ds0 != nullptr) {
-    for (int idx = tid; idx < Kp * 16; idx += 256) {
+    for (int idx = tid; idx < Kp * 16; idx += kST) {
       const int r = idx >> 4, cc = idx & 15;
       if (r < a.K && col0 + cc < a.V) a.ds0[((b * a.H + h) * a.K + r) * a.V + col0 + cc] = dSS[r * kTS + cc];
     }
@@ -1125,8 +1156,8 @@ size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int
 template <class IT, int KP>
 static void launch_all(const bwd::Args<IT>& a, dim3 chunks, dim3 scans, hipStream_t s) {
   hipLaunchKernelGGL((bwd::prep_kernel<IT, KP>), chunks, dim3(256), 0, s, a);
-  hipLaunchKernelGGL((bwd::fscan_kernel<IT, KP>), scans, dim3(256), 0, s, a);
-  hipLaunchKernelGGL((bwd::bscan_kernel<IT, KP>), scans, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bwd::fscan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
+  hipLaunchKernelGGL((bwd::bscan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
   hipLaunchKernelGGL((bwd::grad_kernel<IT, KP>), chunks, dim3(256), 0, s, a);
   hipLaunchKernelGGL((bwd::pair_kernel<IT, KP, 512>), chunks, dim3(512), 0, s, a);
 }
