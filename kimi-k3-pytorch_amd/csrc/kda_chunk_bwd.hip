@@ -681,7 +681,8 @@ __global__ __launch_bounds__(kST) void bscan_kernel(const Args<IT> a) {
 }
 
 // ---- grad_kernel: products that reduce over the state columns -----------------
-// Slabs of 32 state columns accumulate dQg, dKt, dW (wave w: rows 16w..),
+// Eight waves; slabs of 32 state columns accumulate dQg, dKt, dW (wave w:
+// row tile w % 4, half w / 4 of the column tiles),
 // dAqk and dM in MFMA accumulators and write dv; then dKg = M^T dW,
 // dM += dW Kg^T, dbeta and dA follow from N.
 constexpr int kOffM = 0;                        // [64][68] M = N diag(b)
@@ -704,14 +705,16 @@ static_assert(kOffY + kC * kRS <= kGradFloats, "Kg must fit");
 static_assert(kOffDM + kC * kRC <= kOffDN && kOffA + kC * kRC <= kGradFloats, "second-stage tiles must fit");
 
 template <class IT, int KP>
-__global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
+__global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
+  constexpr int NT = 512;
+  constexpr int Kp = KP, CH = KP / 32;  // K-wide column tiles per wave
   __shared__ float sm[kGradFloats];
   __shared__ float bS[kC];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
+  const int rt = w & 3, hf = w >> 2;  // wave w: row tile rt, half hf of the column tiles
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
   const int64_t t0 = c * kC;
-  constexpr int Kp = KP, nkt = KP / 16;
   const int Vp = a.L.Vp;
   float* ws = a.ws + ch * a.L.per;
   float* MS = sm + kOffM;
@@ -720,47 +723,46 @@ __global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
     bS[tid] = t < a.T ? to_float(a.beta[tok(b, t, a.T, a.H, h)]) : 0.f;
   }
   __syncthreads();
-  for (int idx = tid; idx < kC * kC; idx += 256) MS[(idx >> 6) * kRC + (idx & 63)] = ws[a.L.N + idx] * bS[idx & 63];
+  for (int idx = tid; idx < kC * kC; idx += NT) MS[(idx >> 6) * kRC + (idx & 63)] = ws[a.L.N + idx] * bS[idx & 63];
 
-  f32x4 aQ[8], aT[8], aW[8], aA[4], aM[4];
+  f32x4 aQ[CH], aT[CH], aW[CH], aA[2], aM[2];
 #pragma unroll
-  for (int m = 0; m < 8; ++m) aQ[m] = aT[m] = aW[m] = zero4();
+  for (int m = 0; m < CH; ++m) aQ[m] = aT[m] = aW[m] = zero4();
 #pragma unroll
-  for (int m = 0; m < 4; ++m) aA[m] = aM[m] = zero4();
+  for (int m = 0; m < 2; ++m) aA[m] = aM[m] = zero4();
   float dd = 0.f;
   float *Ss = sm + kOffSs, *dSn = sm + kOffdSn, *dOs = sm + kOffdOs, *Vts = sm + kOffVts, *dVts = sm + kOffdVts,
         *vs = sm + kOffvs;
   for (int s0 = 0; s0 < Vp; s0 += kSW) {  // Vp is a multiple of the slab width
     constexpr int sw = kSW;
-    load_ws<KP, kSW, kSS, 256>(Ss, ws + a.L.S, Vp, s0, tid);
-    load_ws<KP, kSW, kSS, 256>(dSn, ws + a.L.dS, Vp, s0, tid);
-    load_ws<kC, kSW, kSS, 256>(Vts, ws + a.L.Vt, Vp, s0, tid);
-    load_ws<kC, kSW, kSS, 256>(dVts, ws + a.L.dVt, Vp, s0, tid);
-    load_rows<IT, kSW, kSS, 256>(dOs, a.dout, b, t0, a.T, a.H, h, a.V, s0, tid);
-    load_rows<IT, kSW, kSS, 256>(vs, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
+    load_ws<KP, kSW, kSS, NT>(Ss, ws + a.L.S, Vp, s0, tid);
+    load_ws<KP, kSW, kSS, NT>(dSn, ws + a.L.dS, Vp, s0, tid);
+    load_ws<kC, kSW, kSS, NT>(Vts, ws + a.L.Vt, Vp, s0, tid);
+    load_ws<kC, kSW, kSS, NT>(dVts, ws + a.L.dVt, Vp, s0, tid);
+    load_rows<IT, kSW, kSS, NT>(dOs, a.dout, b, t0, a.T, a.H, h, a.V, s0, tid);
+    load_rows<IT, kSW, kSS, NT>(vs, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
     __syncthreads();
-    for (int tt = w; tt < 4 * (sw / 16); tt += 4) {  // dv = M^T dVt
-      const int rt = tt & 3, ct = tt >> 2;
-      const f32x4 acc = mma(zero4(), Mat{MS, 1, kRC}, 16 * rt, Mat{dVts, kSS, 1}, 16 * ct, kC);
+    {  // dv = M^T dVt, tile (rt, hf) of the slab
+      const f32x4 acc = mma(zero4(), Mat{MS, 1, kRC}, 16 * rt, Mat{dVts, kSS, 1}, 16 * hf, kC);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 16 * rt + 4 * lg4 + r, col = s0 + 16 * ct + li;
+        const int row = 16 * rt + 4 * lg4 + r, col = s0 + 16 * hf + li;
         const int64_t t = t0 + row;
         if (t < a.T && col < a.V) a.dv[tok(b, t, a.T, a.H, h) * a.V + col] = from_compute<IT>(acc[r]);
       }
     }
 #pragma unroll
-    for (int ct = 0; ct < 8; ++ct) {
-      if (ct < nkt) {
-        aQ[ct] = mma(aQ[ct], Mat{dOs, kSS, 1}, 16 * w, Mat{Ss, 1, kSS}, 16 * ct, sw);
-        aT[ct] = mma(aT[ct], Mat{Vts, kSS, 1}, 16 * w, Mat{dSn, 1, kSS}, 16 * ct, sw);
-        aW[ct] = mma(aW[ct], Mat{dVts, kSS, 1}, 16 * w, Mat{Ss, 1, kSS}, 16 * ct, sw);
-      }
+    for (int j = 0; j < CH; ++j) {
+      const int ct = hf * CH + j;
+      aQ[j] = mma(aQ[j], Mat{dOs, kSS, 1}, 16 * rt, Mat{Ss, 1, kSS}, 16 * ct, sw);
+      aT[j] = mma(aT[j], Mat{Vts, kSS, 1}, 16 * rt, Mat{dSn, 1, kSS}, 16 * ct, sw);
+      aW[j] = mma(aW[j], Mat{dVts, kSS, 1}, 16 * rt, Mat{Ss, 1, kSS}, 16 * ct, sw);
     }
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      aA[ct] = mma(aA[ct], Mat{dOs, kSS, 1}, 16 * w, Mat{Vts, 1, kSS}, 16 * ct, sw);
-      aM[ct] = mma(aM[ct], Mat{dVts, kSS, 1}, 16 * w, Mat{vs, 1, kSS}, 16 * ct, sw);
+    for (int j = 0; j < 2; ++j) {
+      const int ct = hf * 2 + j;
+      aA[j] = mma(aA[j], Mat{dOs, kSS, 1}, 16 * rt, Mat{Vts, 1, kSS}, 16 * ct, sw);
+      aM[j] = mma(aM[j], Mat{dVts, kSS, 1}, 16 * rt, Mat{vs, 1, kSS}, 16 * ct, sw);
     }
     if (tid < Kp)
       for (int cc = 0; cc < sw; ++cc) dd += dSn[tid * kSS + cc] * Ss[tid * kSS + cc];
@@ -770,70 +772,69 @@ __global__ __launch_bounds__(256) void grad_kernel(const Args<IT> a) {
   // dW = -(dVt S^T) over the slabs, Kg, and the finished dQg, dKt, dAqk, dD
   float *X = sm + kOffX, *Y = sm + kOffY;
 #pragma unroll
-  for (int ct = 0; ct < 8; ++ct) {
-    if (ct < nkt) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * w + 4 * lg4 + r, col = 16 * ct + li;
-        X[row * kRS + col] = -aW[ct][r];
-        ws[a.L.dQg + row * Kp + col] = aQ[ct][r];
-        ws[a.L.dKt + row * Kp + col] = aT[ct][r];
-      }
-    }
-  }
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct)
+  for (int j = 0; j < CH; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 16 * w + 4 * lg4 + r, col = 16 * ct + li;
-      ws[a.L.dAqk + row * kC + col] = col <= row ? aA[ct][r] : 0.f;
+      const int row = 16 * rt + 4 * lg4 + r, col = 16 * (hf * CH + j) + li;
+      X[row * kRS + col] = -aW[j][r];
+      ws[a.L.dQg + row * Kp + col] = aQ[j][r];
+      ws[a.L.dKt + row * Kp + col] = aT[j][r];
     }
-  load_ws<kC, KP, kRS, 256>(Y, ws + a.L.Kg, KP, 0, tid);
+#pragma unroll
+  for (int j = 0; j < 2; ++j)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * rt + 4 * lg4 + r, col = 16 * (hf * 2 + j) + li;
+      ws[a.L.dAqk + row * kC + col] = col <= row ? aA[j][r] : 0.f;
+    }
+  load_ws<kC, KP, kRS, NT>(Y, ws + a.L.Kg, KP, 0, tid);
   if (tid < Kp) ws[a.L.dD + tid] = dd;
   __syncthreads();
 #pragma unroll
-  for (int ct = 0; ct < 8; ++ct) {  // dKg = M^T dW
-    if (ct < nkt) {
-      const f32x4 acc = mma_long(zero4(), Mat{MS, 1, kRC}, 16 * w, Mat{X, kRS, 1}, 16 * ct, kC);
+  for (int j = 0; j < CH; ++j) {  // dKg = M^T dW
+    const int ct = hf * CH + j;
+    const f32x4 acc = mma_long(zero4(), Mat{MS, 1, kRC}, 16 * rt, Mat{X, kRS, 1}, 16 * ct, kC);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ws[a.L.dKg + (16 * w + 4 * lg4 + r) * Kp + 16 * ct + li] = acc[r];
-    }
+    for (int r = 0; r < 4; ++r) ws[a.L.dKg + (16 * rt + 4 * lg4 + r) * Kp + 16 * ct + li] = acc[r];
   }
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) aM[ct] = mma_long(aM[ct], Mat{X, kRS, 1}, 16 * w, Mat{Y, 1, kRS}, 16 * ct, Kp);  // dM += dW Kg^T
+  for (int j = 0; j < 2; ++j)  // dM += dW Kg^T
+    aM[j] = mma_long(aM[j], Mat{X, kRS, 1}, 16 * rt, Mat{Y, 1, kRS}, 16 * (hf * 2 + j), Kp);
   __syncthreads();
 
   // dbeta and dA from N: dN = dM diag(b), T1 = N^T dN, dL = -strict(T1 N^T)
   float *NS = sm + kOffN, *DM = sm + kOffDM, *DN = sm + kOffDN, *AS = sm + kOffA;
-  load_ws<kC, kC, kRC, 256>(NS, ws + a.L.N, kC, 0, tid);
-  load_ws<kC, kC, kRC, 256>(AS, ws + a.L.A, kC, 0, tid);
+  load_ws<kC, kC, kRC, NT>(NS, ws + a.L.N, kC, 0, tid);
+  load_ws<kC, kC, kRC, NT>(AS, ws + a.L.A, kC, 0, tid);
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 16 * w + 4 * lg4 + r, col = 16 * ct + li;
-      DM[row * kRC + col] = aM[ct][r];
-      DN[row * kRC + col] = aM[ct][r] * bS[col];
+      const int row = 16 * rt + 4 * lg4 + r, col = 16 * (hf * 2 + j) + li;
+      DM[row * kRC + col] = aM[j][r];
+      DN[row * kRC + col] = aM[j][r] * bS[col];
     }
   __syncthreads();
   float db = 0.f;
   if (tid < kC)
     for (int r = 0; r < kC; ++r) db += NS[r * kRC + tid] * DM[r * kRC + tid];
-  f32x4 t1[4];
+  f32x4 t1[2];
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) t1[ct] = mma_long(zero4(), Mat{NS, 1, kRC}, 16 * w, Mat{DN, kRC, 1}, 16 * ct, kC);
+  for (int j = 0; j < 2; ++j)
+    t1[j] = mma_long(zero4(), Mat{NS, 1, kRC}, 16 * rt, Mat{DN, kRC, 1}, 16 * (hf * 2 + j), kC);
   __syncthreads();
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct)
+  for (int j = 0; j < 2; ++j)
 #pragma unroll
-    for (int r = 0; r < 4; ++r) DM[(16 * w + 4 * lg4 + r) * kRC + 16 * ct + li] = t1[ct][r];
+    for (int r = 0; r < 4; ++r) DM[(16 * rt + 4 * lg4 + r) * kRC + 16 * (hf * 2 + j) + li] = t1[j][r];
   __syncthreads();
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const f32x4 acc = mma_long(zero4(), Mat{DM, kRC, 1}, 16 * w, Mat{NS, 1, kRC}, 16 * ct, kC);
+  for (int j = 0; j < 2; ++j) {
+    const int ct = hf * 2 + j;
+    const f32x4 acc = mma_long(zero4(), Mat{DM, kRC, 1}, 16 * rt, Mat{NS, 1, kRC}, 16 * ct, kC);
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int row = 16 * w + 4 * lg4 + r, col = 16 * ct + li;
+      const int row = 16 * rt + 4 * lg4 + r, col = 16 * ct + li;
       const float dl = col < row ? -acc[r] : 0.f;
       DN[row * kRC + col] = dl;
       ws[a.L.dA + row * kC + col] = bS[row] * dl;
@@ -1158,7 +1159,7 @@ static void launch_all(const bwd::Args<IT>& a, dim3 chunks, dim3 scans, hipStrea
   hipLaunchKernelGGL((bwd::prep_kernel<IT, KP>), chunks, dim3(256), 0, s, a);
   hipLaunchKernelGGL((bwd::fscan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
   hipLaunchKernelGGL((bwd::bscan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
-  hipLaunchKernelGGL((bwd::grad_kernel<IT, KP>), chunks, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bwd::grad_kernel<IT, KP>), chunks, dim3(512), 0, s, a);
   hipLaunchKernelGGL((bwd::pair_kernel<IT, KP, 512>), chunks, dim3(512), 0, s, a);
 }
 
