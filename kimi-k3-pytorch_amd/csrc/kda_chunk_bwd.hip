@@ -17,12 +17,12 @@
 //   dA = diag(b) dL, then the pair sums of dA and dAqk with exact exponents,
 //   the exp factors, and dg = reverse cumulative sum of d lg over the chunk.
 //
-// Five kernels, all arithmetic in f32 on the f32 MFMA (v_mfma_f32_16x16x4f32):
+// Four kernels, all arithmetic in f32 on the f32 MFMA (v_mfma_f32_16x16x4f32):
 //   prep_kernel   one block per (sequence, head, chunk): A, Aqk (exact pair
 //                 exponents), N by forward substitution, W, U, Kt, Qg, Kg, D;
-//   fscan_kernel  one block per (sequence, head, 16 state columns): the chunk
-//                 start states S and the pseudo-values Vt, chunk by chunk;
-//   bscan_kernel  the same blocks backwards: dS' and dVt per chunk, dS0;
+//   scan_kernel   one block per (sequence, head, 16 state columns) and
+//                 direction: forward, the chunk start states S and the
+//                 pseudo-values Vt; backward, dS' and dVt per chunk and dS0;
 //   grad_kernel   one block per chunk: dv, dbeta, and dQg, dKt, dKg, dA, dAqk;
 //   pair_kernel   one block per chunk: the pair sums and the final dq, dk, dg.
 // Intermediates live in a caller-owned f32 workspace, one record per
@@ -487,14 +487,18 @@ __device__ __forceinline__ void fscan_fetch(FscanBuf& p, const Args<IT>& a, int6
   if (tid < KP) p.d = ws[a.L.D + tid];
 }
 
+constexpr int kFscanFloats = 2 * kC * kRS + 128 * kTS + 2 * kC * kTS + 128;
+constexpr int kBscanFloats = 3 * kC * kRS + kC * kRC + 2 * 128 * kTS + 2 * kC * kTS + 128;
+constexpr int kScanFloats = kFscanFloats > kBscanFloats ? kFscanFloats : kBscanFloats;
+
 template <class IT, int KP>
-__global__ __launch_bounds__(kST) void fscan_kernel(const Args<IT> a) {
-  __shared__ float WS[kC * kRS], KtS[kC * kRS], SS[128 * kTS], US[kC * kTS], PS[kC * kTS], DS[128];
+__device__ __forceinline__ void fscan_body(const Args<IT>& a, int64_t lb, float* smem) {
+  float *WS = smem, *KtS = WS + kC * kRS, *SS = KtS + kC * kRS, *US = SS + 128 * kTS, *PS = US + kC * kTS,
+        *DS = PS + kC * kTS;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   const int half = w >> 2, wt = w & 3;
   constexpr int Kp = KP, nq = kC * KP / 4, KH = KP / 2;
   const int Vp = a.L.Vp, ncb = Vp / 16;
-  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
   const int col0 = 16 * static_cast<int>(lb % ncb);
   for (int idx = tid; idx < Kp * 16; idx += kST) {
@@ -595,13 +599,12 @@ __device__ __forceinline__ void bscan_fetch(BscanBuf<IT>& p, const Args<IT>& a, 
 }
 
 template <class IT, int KP>
-__global__ __launch_bounds__(kST) void bscan_kernel(const Args<IT> a) {
-  __shared__ float KtS[kC * kRS], QgS[kC * kRS], WS[kC * kRS], AqkS[kC * kRC];
-  __shared__ float dSS[128 * kTS], dSp[128 * kTS], dOS[kC * kTS], XS[kC * kTS], DS[128];
+__device__ __forceinline__ void bscan_body(const Args<IT>& a, int64_t lb, float* smem) {
+  float *KtS = smem, *QgS = KtS + kC * kRS, *WS = QgS + kC * kRS, *AqkS = WS + kC * kRS, *dSS = AqkS + kC * kRC,
+        *dSp = dSS + 128 * kTS, *dOS = dSp + 128 * kTS, *XS = dOS + kC * kTS, *DS = XS + kC * kTS;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   constexpr int Kp = KP, nq = kC * KP / 4;
   const int Vp = a.L.Vp, ncb = Vp / 16;
-  const int64_t lb = xcd_block(blockIdx.x, gridDim.x);
   const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
   const int col0 = 16 * static_cast<int>(lb % ncb);
   for (int idx = tid; idx < Kp * 16; idx += kST) {
@@ -678,6 +681,21 @@ __global__ __launch_bounds__(kST) void bscan_kernel(const Args<IT> a) {
       if (r < a.K && col0 + cc < a.V) a.ds0[((b * a.H + h) * a.K + r) * a.V + col0 + cc] = dSS[r * kTS + cc];
     }
   }
+}
+
+// ---- scan_kernel: both state scans in one launch -------------------------------
+// The backward scan needs only the chunk operands and dO, not the forward
+// scan's states, so the two run side by side: logical blocks [0, n) carry the
+// forward scan and [n, 2n) the backward one (n = heads x column blocks), each
+// XCD owning a contiguous range so the column blocks of a head share its L2.
+template <class IT, int KP>
+__global__ __launch_bounds__(kST) void scan_kernel(const Args<IT> a) {
+  __shared__ __attribute__((aligned(16))) float smem[kScanFloats];
+  const int64_t lb = xcd_block(blockIdx.x, gridDim.x), n = gridDim.x / 2;
+  if (lb < n)
+    fscan_body<IT, KP>(a, lb, smem);
+  else
+    bscan_body<IT, KP>(a, lb - n, smem);
 }
 
 // ---- grad_kernel: products that reduce over the state columns -----------------
@@ -1157,8 +1175,7 @@ size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int
 template <class IT, int KP>
 static void launch_all(const bwd::Args<IT>& a, dim3 chunks, dim3 scans, hipStream_t s) {
   hipLaunchKernelGGL((bwd::prep_kernel<IT, KP>), chunks, dim3(256), 0, s, a);
-  hipLaunchKernelGGL((bwd::fscan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
-  hipLaunchKernelGGL((bwd::bscan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
+  hipLaunchKernelGGL((bwd::scan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
   hipLaunchKernelGGL((bwd::grad_kernel<IT, KP>), chunks, dim3(512), 0, s, a);
   hipLaunchKernelGGL((bwd::pair_kernel<IT, KP, 512>), chunks, dim3(512), 0, s, a);
 }
@@ -1166,7 +1183,7 @@ static void launch_all(const bwd::Args<IT>& a, dim3 chunks, dim3 scans, hipStrea
 template <class IT>
 static int run_bwd(const bwd::Args<IT>& a, hipStream_t s) {
   const int64_t chunks = a.B * a.H * a.NC;
-  const int64_t scans = a.B * a.H * (a.L.Vp / 16);
+  const int64_t scans = 2 * a.B * a.H * (a.L.Vp / 16);  // forward and backward scan blocks
   if (chunks > 0x7fffffffLL || scans > 0x7fffffffLL) {
     set_detail("chunk backward: grid too large");
     return KDA_ERR_UNSUPPORTED;
