@@ -97,3 +97,25 @@ def test_fused_entry_points_reject_unsupported_layouts():
     assert norm(a, 96) == _lib.KDA_ERR_UNSUPPORTED
     assert norm(a, 1024) == _lib.KDA_ERR_UNSUPPORTED
     assert norm(a + 4, 128) == _lib.KDA_ERR_INVALID_ARGUMENT
+
+
+def test_backward_entry_point_rejects_bad_arguments():
+    # host-side checks only: nothing is launched
+    lib = _lib.load()
+    import torch
+
+    bf16, f64 = _lib.dtype_code(torch.bfloat16), _lib.dtype_code(torch.float64)
+    a = 4096
+    ptrs = [a] * 6
+
+    def call(dtype=bf16, K=128, V=128, ws=None, ws_bytes=0, dq=a):
+        return lib.kda_chunk_bwd(*ptrs, dtype, None, None, dq, a, a, a, a, None, 1, 64, 1, K, V, ws, ws_bytes, None)
+
+    assert call(dtype=f64) == _lib.KDA_ERR_UNSUPPORTED
+    assert call(K=256) == _lib.KDA_ERR_UNSUPPORTED
+    assert call(dq=None) == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call() == _lib.KDA_ERR_WORKSPACE  # no workspace
+    need = lib.kda_chunk_bwd_workspace_bytes(1, 64, 1, 128, 128)
+    assert need > 0 and call(ws=a, ws_bytes=need - 1) == _lib.KDA_ERR_WORKSPACE
+    assert call(ws=a + 4, ws_bytes=need) == _lib.KDA_ERR_INVALID_ARGUMENT  # misaligned workspace
+    assert lib.kda_chunk_bwd_workspace_bytes(0, 64, 1, 128, 128) == 0
