@@ -18,7 +18,7 @@ from tests._inputs import rel_err, workload
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
-TOL = {torch.float32: 2e-4, torch.bfloat16: 2e-2}
+TOL = {torch.float32: 2e-4, torch.bfloat16: 2e-2, torch.float16: 2e-2}
 NAMES = ("dq", "dk", "dv", "dg", "dbeta", "ds0")
 
 
@@ -48,7 +48,7 @@ def _oracle_grads(inputs, d_out, d_final, final=True):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,T,H,K,V", [(2, 150, 2, 128, 128), (1, 64, 1, 64, 32), (2, 37, 3, 16, 48),
-                                       (1, 200, 2, 128, 96)])
+                                       (1, 200, 2, 128, 96), (1, 70, 1, 100, 40)])
 def test_backward_matches_oracle(dtype, B, T, H, K, V):
     inputs, d_out, d_final = _case(B, T, H, K, V, dtype, seed=T + K)
     got = _gpu_grads(inputs, d_out, d_final)
@@ -155,3 +155,12 @@ def test_decode_step_gradients():
     ref = _oracle_grads(inputs, d_out, d_final)
     for name, a, b in zip(NAMES, got, ref):
         assert rel_err(a, b) < TOL[torch.bfloat16], name
+
+
+def test_backward_f16_inputs():
+    inputs, d_out, d_final = _case(1, 130, 2, 128, 128, torch.float16, seed=10)
+    got = _gpu_grads(inputs, d_out, d_final)
+    ref = _oracle_grads(inputs, d_out, d_final)
+    for name, a, b, x in zip(NAMES, got, ref, inputs):
+        assert a.dtype == x.dtype, name
+        assert rel_err(a, b) < TOL[torch.float16], (name, rel_err(a, b))
