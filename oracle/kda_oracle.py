@@ -2,7 +2,8 @@
 
 TEST INFRASTRUCTURE ONLY.  Nothing in the product package imports this module;
 only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of
-``bench.py`` may use it, and only as the checker / the timed CPU baseline.
+``bench.py`` may use it, and only as the reference the GPU results are
+compared with, or as the timed CPU baseline.
 
 This is a PyTorch-on-CPU restatement of the reference operator
 (pablo-reyes8/kimi-k3-pytorch, ``src/kda``).  It keeps the reference's

@@ -1,4 +1,4 @@
-"""Pins the CPU oracle (oracle/kda_oracle.py) before it is trusted as the checker.
+"""Pins the CPU oracle (oracle/kda_oracle.py) before the GPU results are compared with it.
 
 Each oracle function is checked against something other than its own formula:
 the reference's literal known-answer tests, closed forms, an explicit matrix
