@@ -46,7 +46,7 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 // Offsets (floats) of one (sequence, head, chunk) record of the workspace.
 struct Layout {
   int Kp, Vp;  // K padded to 64 or 128, V to a multiple of 32
-  int64_t N, A, Aqk, W, Kt, Qg, Kg, U, D, S, Vt, dS, dVt, dQg, dKt, dKg, dA, dAqk, dD, per;
+  int64_t N, A, Aqkt, Wr, Wt, Ktr, Ktt, Qgt, Kg, U, D, S, Vt, dS, dVt, dQg, dKt, dKg, dA, dAqk, dD, per;
 };
 
 __host__ __device__ inline Layout make_layout(int64_t K, int64_t V) {
@@ -57,10 +57,12 @@ __host__ __device__ inline Layout make_layout(int64_t K, int64_t V) {
   int64_t o = 0;
   L.N = o; o += cc;
   L.A = o; o += cc;
-  L.Aqk = o; o += cc;
-  L.W = o; o += ck;
-  L.Kt = o; o += ck;
-  L.Qg = o; o += ck;
+  L.Aqkt = o; o += cc;  // split operands of the scans: bf16 hi plane, then lo plane
+  L.Wr = o; o += ck;
+  L.Wt = o; o += ck;
+  L.Ktr = o; o += ck;
+  L.Ktt = o; o += ck;
+  L.Qgt = o; o += ck;
   L.Kg = o; o += ck;
   L.U = o; o += cv;
   L.D = o; o += L.Kp;
@@ -142,6 +144,73 @@ __device__ __forceinline__ f32x4 mma_long(f32x4 acc, Mat A, int r0, Mat B, int c
     }
   }
   return acc + acc2;
+}
+
+// Split-bf16 products for the state scans: x = hi + lo with hi = bf16(x)
+// and lo = bf16(x - hi) keeps about 16 bits of x, and hi*hi + hi*lo + lo*hi
+// on v_mfma_f32_16x16x32_bf16 (three products per 32-deep slice, against
+// eight f32 MFMAs) loses terms of relative size 2^-17.
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
+  hi = static_cast<__bf16>(x);
+  lo = static_cast<__bf16>(x - static_cast<float>(hi));
+}
+
+// A split matrix in LDS with its reduction index contiguous: element (r, k)
+// at p[r * rs + k] (hi) and p[plane + r * rs + k] (lo); a right operand is
+// held as its transpose (row = output column).
+struct SMat {
+  const __bf16* p;
+  int plane, rs;
+};
+
+// acc += A[r0:r0+16, 0:kd] B[0:kd, c0:c0+16]; lane (i, g) carries k = k0 + 8g ..
+// k0 + 8g + 7 of row r0 + i of A and of column c0 + i of B; kd % 32 == 0.
+__device__ __forceinline__ f32x4 mma3(f32x4 acc, SMat A, int r0, SMat B, int c0, int kd) {
+  const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  const __bf16* pa = A.p + (r0 + i) * A.rs + 8 * g;
+  const __bf16* pb = B.p + (c0 + i) * B.rs + 8 * g;
+  for (int k0 = 0; k0 < kd; k0 += 32) {
+    const bf16x8 ah = *reinterpret_cast<const bf16x8*>(pa + k0), al = *reinterpret_cast<const bf16x8*>(pa + A.plane + k0);
+    const bf16x8 bh = *reinterpret_cast<const bf16x8*>(pb + k0), bl = *reinterpret_cast<const bf16x8*>(pb + B.plane + k0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// Four consecutive split values (an accumulator lane's four rows) into a
+// transposed split tile: row `col`, positions k .. k+3.
+__device__ __forceinline__ void store_split4(__bf16* base, int plane, int rs, int col, int k, f32x4 v) {
+  bf16x4 hi, lo;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    __bf16 h, l;
+    split_bf16(v[r], h, l);
+    hi[r] = h;
+    lo[r] = l;
+  }
+  *reinterpret_cast<bf16x4*>(base + col * rs + k) = hi;
+  *reinterpret_cast<bf16x4*>(base + plane + col * rs + k) = lo;
+}
+
+// Split record in the workspace: n bf16 hi values, then n lo values.  Eight
+// consecutive values from element idx (a multiple of 8) as two 16-byte stores.
+__device__ __forceinline__ void put_split8(float* rec, int n, int idx, const float* x) {
+  bf16x8 hi, lo;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    __bf16 h, l;
+    split_bf16(x[e], h, l);
+    hi[e] = h;
+    lo[e] = l;
+  }
+  __bf16* p = reinterpret_cast<__bf16*>(rec);
+  *reinterpret_cast<bf16x8*>(p + idx) = hi;
+  *reinterpret_cast<bf16x8*>(p + n + idx) = lo;
 }
 
 __device__ __forceinline__ int64_t tok(const int64_t b, const int64_t t, const int64_t T, const int64_t H,
@@ -373,19 +442,43 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
       }
   }
   __syncthreads();
-  for (int idx = tid; idx < kC * kC; idx += 256) {
+  for (int idx = tid; idx < kC * kC; idx += 256) {  // A
     const int r = idx >> 6, cc = idx & 63;
     ws[a.L.A + idx] = AS[r * kRC + cc];
-    ws[a.L.Aqk + idx] = AqkS[r * kRC + cc];
   }
-  for (int idx = tid; idx < kC * Kp; idx += 256) {
+  for (int i8 = tid; i8 < kC * kC / 8; i8 += 256) {  // Aqk^T split, eight positions at a time
+    const int r = (8 * i8) >> 6, c0 = (8 * i8) & 63;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = AqkS[(c0 + e) * kRC + r];
+    put_split8(ws + a.L.Aqkt, kC * kC, 8 * i8, x);
+  }
+  for (int idx = tid; idx < kC * Kp; idx += 256) {  // Kg (f32)
     const int r = idx / Kp, col = idx % Kp;
-    const float lg = lgS[r * kRS + col], last = lgS[(kC - 1) * kRS + col];
-    const float e = fast_exp(lg), kv = kS[r * kRS + col];
-    ws[a.L.Qg + idx] = e * qS[r * kRS + col];
-    ws[a.L.Kt + idx] = fast_exp(last - lg) * kv;
-    ws[a.L.Kg + idx] = e * kv;
-    kS[r * kRS + col] = e * kv;  // Kg, the B operand of W = M Kg
+    ws[a.L.Kg + idx] = fast_exp(lgS[r * kRS + col]) * kS[r * kRS + col];
+  }
+  for (int i8 = tid; i8 < kC * Kp / 8; i8 += 256) {  // Kt split, row-major
+    const int r = (8 * i8) / Kp, c0 = (8 * i8) % Kp;
+    float x[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const int col = c0 + e;
+      x[e] = fast_exp(lgS[(kC - 1) * kRS + col] - lgS[r * kRS + col]) * kS[r * kRS + col];
+    }
+    put_split8(ws + a.L.Ktr, kC * Kp, 8 * i8, x);
+  }
+  for (int i8 = tid; i8 < kC * Kp / 8; i8 += 256) {  // Kt^T and Qg^T split, eight positions at a time
+    const int col = (8 * i8) / kC, r0 = (8 * i8) % kC;
+    const float last = lgS[(kC - 1) * kRS + col];
+    float xk[8], xq[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const float lg = lgS[(r0 + e) * kRS + col];
+      xk[e] = fast_exp(last - lg) * kS[(r0 + e) * kRS + col];
+      xq[e] = fast_exp(lg) * qS[(r0 + e) * kRS + col];
+    }
+    put_split8(ws + a.L.Ktt, kC * Kp, 8 * i8, xk);
+    put_split8(ws + a.L.Qgt, kC * Kp, 8 * i8, xq);
   }
   if (tid < Kp) ws[a.L.D + tid] = fast_exp(lgS[(kC - 1) * kRS + tid]);
   __syncthreads();
@@ -393,6 +486,10 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
     const int r = idx >> 6, cc = idx & 63;
     AS[r * kRC + cc] *= bS[r];
     NS[r * kRC + cc] = 0.f;
+  }
+  for (int idx = tid; idx < kC * Kp; idx += 256) {  // Kg over k: the B operand of W = M Kg
+    const int r = idx / Kp, col = idx % Kp;
+    kS[r * kRS + col] *= fast_exp(lgS[r * kRS + col]);
   }
   __syncthreads();
   // N = L^-1 by 16x16 blocks: wave w inverts diagonal block w by forward
@@ -436,15 +533,27 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
   }
   __syncthreads();
   const int nkt = Kp / 16, nvt = Vp / 16;
-  for (int tt = w; tt < 4 * nkt; tt += 4) {  // W = M Kg
+  for (int tt = w; tt < 4 * nkt; tt += 4) {  // W = M Kg, staged in f32 over q
     const int rt = tt & 3, ct = tt >> 2;
     const f32x4 acc = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{kS, kRS, 1}, 16 * ct, kC);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) ws[a.L.W + (16 * rt + 4 * lg4 + r) * Kp + 16 * ct + li] = acc[r];
+    for (int r = 0; r < 4; ++r) qS[(16 * rt + 4 * lg4 + r) * kRS + 16 * ct + li] = acc[r];
   }
   for (int s0 = 0; s0 < Vp; s0 += 32)  // v over lg (no longer read)
     load_rows<IT, 32, kRS, 256>(lgS + s0, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
   __syncthreads();
+  for (int i8 = tid; i8 < kC * Kp / 8; i8 += 256) {  // W and W^T split
+    float x[8], y[8];
+    const int r = (8 * i8) / Kp, c0 = (8 * i8) % Kp;
+    const int c2 = (8 * i8) / kC, r2 = (8 * i8) % kC;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      x[e] = qS[r * kRS + c0 + e];
+      y[e] = qS[(r2 + e) * kRS + c2];
+    }
+    put_split8(ws + a.L.Wr, kC * Kp, 8 * i8, x);
+    put_split8(ws + a.L.Wt, kC * Kp, 8 * i8, y);
+  }
   for (int tt = w; tt < 4 * nvt; tt += 4) {  // U = M v
     const int rt = tt & 3, ct = tt >> 2;
     const f32x4 acc = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{lgS, kRS, 1}, 16 * ct, kC);
@@ -453,14 +562,45 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
   }
 }
 
-// ---- fscan_kernel: chunk start states and pseudo-values ----------------------
-// Block (sequence, head, 16 columns), eight waves, carries S[:, cols] through
-// the chunks:  Vt = U[:, cols] - W S  (the two halves of the channel
-// reduction on waves 0-3 and 4-7),  S <- D S + Kt^T Vt  (one row tile per
-// wave).  The next chunk's W, Kt, U and D are loaded into registers while the
-// current chunk is computed.
+// ---- state scans ----------------------------------------------------------------
+// Block (sequence, head, 16 state columns), eight waves, with every product
+// on split-bf16 operands (hi + lo) whose f32 masters stay in LDS:
+//   forward:  Vt = U[:, cols] - W S  (the channel reduction split over waves
+//             0-3 and 4-7),  S <- D S + Kt^T Vt  (one row tile per wave);
+//   backward: dVt = Kt dS + Aqk^T dO  (waves 0-3, one row tile each) next to
+//             D dS + Qg^T dO  (waves 4-7, two row tiles each, kept in
+//             registers), then dS = that - W^T dVt  (waves 4-7).
+// The next chunk's operands (stored split by prep_kernel) are loaded into
+// registers while the current chunk is computed.
 constexpr int kST = 512;  // threads of the scan blocks
-constexpr int kPF = 4;    // f32x4 per thread of one [64][128] f32 matrix
+constexpr int kPF = 4;    // f32x4 per thread of one 64 x 128 split record
+constexpr int kRSP(int kp) { return kp + 8; }  // LDS row stride (bf16) of channel-contiguous tiles
+constexpr int kRSC = kC + 8;                    // LDS row stride (bf16) of position-contiguous tiles
+
+// One 64 x KP split record (2 planes) from the workspace into an LDS tile of
+// rows `rows` x `cols` (row stride rs, plane stride plane), f32x4 = 8 bf16.
+template <int KP>
+__device__ __forceinline__ void split_to_lds(__bf16* dst, int plane, int rs, int cols, const f32x4* src, int tid) {
+  constexpr int nq = kC * KP / 4, n = kC * KP;
+#pragma unroll
+  for (int m = 0; m < kPF; ++m) {
+    const int q4 = tid + kST * m;
+    if (q4 < nq) {
+      const int f = 8 * q4, pl = f / n, e = f % n, r = e / cols, c = e % cols;
+      *reinterpret_cast<f32x4*>(dst + pl * plane + r * rs + c) = src[m];
+    }
+  }
+}
+
+template <int KP>
+__device__ __forceinline__ void fetch_split(f32x4* dst, const float* rec, int tid) {
+  constexpr int nq = kC * KP / 4;
+#pragma unroll
+  for (int m = 0; m < kPF; ++m) {
+    const int q4 = tid + kST * m;
+    if (q4 < nq) dst[m] = *reinterpret_cast<const f32x4*>(rec + 4 * q4);
+  }
+}
 
 struct FscanBuf {
   f32x4 w[kPF], k[kPF];
@@ -469,16 +609,9 @@ struct FscanBuf {
 
 template <class IT, int KP>
 __device__ __forceinline__ void fscan_fetch(FscanBuf& p, const Args<IT>& a, int64_t bh, int64_t c, int col0, int tid) {
-  constexpr int nq = kC * KP / 4;
   const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
-#pragma unroll
-  for (int m = 0; m < kPF; ++m) {
-    const int q4 = tid + kST * m;
-    if (q4 < nq) {
-      p.w[m] = *reinterpret_cast<const f32x4*>(ws + a.L.W + 4 * q4);
-      p.k[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Kt + 4 * q4);
-    }
-  }
+  fetch_split<KP>(p.w, ws + a.L.Wr, tid);
+  fetch_split<KP>(p.k, ws + a.L.Ktt, tid);
 #pragma unroll
   for (int m = 0; m < 2; ++m) {
     const int idx = tid + kST * m;  // [64][16]
@@ -487,109 +620,114 @@ __device__ __forceinline__ void fscan_fetch(FscanBuf& p, const Args<IT>& a, int6
   if (tid < KP) p.d = ws[a.L.D + tid];
 }
 
-constexpr int kFscanFloats = 2 * kC * kRS + 128 * kTS + 2 * kC * kTS + 128;
-constexpr int kBscanFloats = 3 * kC * kRS + kC * kRC + 2 * 128 * kTS + 2 * kC * kTS + 128;
-constexpr int kScanFloats = kFscanFloats > kBscanFloats ? kFscanFloats : kBscanFloats;
+// LDS of the forward scan (bytes)
+template <int KP>
+struct FscanLds {
+  static constexpr int rs = kRSP(KP);
+  static constexpr int wr = 0;                                  // W split [64][KP]
+  static constexpr int kt = wr + 2 * kC * rs * 2;               // Kt^T split [KP][64]
+  static constexpr int st = kt + 2 * KP * kRSC * 2;             // S^T split [16][KP]
+  static constexpr int vt = st + 2 * 16 * rs * 2;               // Vt^T split [16][64]
+  static constexpr int ss = vt + 2 * 16 * kRSC * 2;             // S f32 [128][kTS]
+  static constexpr int us = ss + 128 * kTS * 4;                 // U, then Vt, f32 [64][kTS]
+  static constexpr int ps = us + kC * kTS * 4;                  // partial W S f32 [64][kTS]
+  static constexpr int ds = ps + kC * kTS * 4;                  // D f32 [128]
+  static constexpr int bytes = ds + 128 * 4;
+};
 
 template <class IT, int KP>
-__device__ __forceinline__ void fscan_body(const Args<IT>& a, int64_t lb, float* smem) {
-  float *WS = smem, *KtS = WS + kC * kRS, *SS = KtS + kC * kRS, *US = SS + 128 * kTS, *PS = US + kC * kTS,
-        *DS = PS + kC * kTS;
+__device__ __forceinline__ void fscan_body(const Args<IT>& a, int64_t lb, unsigned char* smem) {
+  using LL = FscanLds<KP>;
+  constexpr int rs = LL::rs, KH = KP / 2;
+  __bf16 *WrS = reinterpret_cast<__bf16*>(smem + LL::wr), *KtS = reinterpret_cast<__bf16*>(smem + LL::kt),
+         *StS = reinterpret_cast<__bf16*>(smem + LL::st), *VtS = reinterpret_cast<__bf16*>(smem + LL::vt);
+  float *SS = reinterpret_cast<float*>(smem + LL::ss), *US = reinterpret_cast<float*>(smem + LL::us),
+        *PS = reinterpret_cast<float*>(smem + LL::ps), *DS = reinterpret_cast<float*>(smem + LL::ds);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   const int half = w >> 2, wt = w & 3;
-  constexpr int Kp = KP, nq = kC * KP / 4, KH = KP / 2;
   const int Vp = a.L.Vp, ncb = Vp / 16;
   const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
   const int col0 = 16 * static_cast<int>(lb % ncb);
-  for (int idx = tid; idx < Kp * 16; idx += kST) {
+  for (int idx = tid; idx < KP * 16; idx += kST) {  // S0 and its split transpose
     const int r = idx >> 4, cc = idx & 15;
-    SS[r * kTS + cc] = (a.s0 != nullptr && r < a.K && col0 + cc < a.V)
-                           ? a.s0[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
-                           : 0.f;
+    const float x = (a.s0 != nullptr && r < a.K && col0 + cc < a.V) ? a.s0[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
+                                                                      : 0.f;
+    SS[r * kTS + cc] = x;
+    __bf16 hi, lo;
+    split_bf16(x, hi, lo);
+    StS[cc * rs + r] = hi;
+    StS[16 * rs + cc * rs + r] = lo;
   }
   FscanBuf pf;
   fscan_fetch<IT, KP>(pf, a, bh, 0, col0, tid);
   for (int64_t c = 0; c < a.NC; ++c) {
     float* ws = a.ws + (bh * a.NC + c) * a.L.per;
-#pragma unroll
-    for (int m = 0; m < kPF; ++m) {
-      const int q4 = tid + kST * m;
-      if (q4 < nq) {
-        const int e = 4 * q4, r = e / Kp, col = e % Kp;
-        *reinterpret_cast<f32x4*>(&WS[r * kRS + col]) = pf.w[m];
-        *reinterpret_cast<f32x4*>(&KtS[r * kRS + col]) = pf.k[m];
-      }
-    }
+    split_to_lds<KP>(WrS, kC * rs, rs, KP, pf.w, tid);
+    split_to_lds<KP>(KtS, KP * kRSC, kRSC, kC, pf.k, tid);
 #pragma unroll
     for (int m = 0; m < 2; ++m) {
       const int idx = tid + kST * m;
       US[(idx >> 4) * kTS + (idx & 15)] = pf.u[m];
     }
-    if (tid < Kp) DS[tid] = pf.d;
-    for (int idx = tid; idx < Kp * 16; idx += kST) {  // the chunk's start state
+    if (tid < KP) DS[tid] = pf.d;
+    for (int idx = tid; idx < KP * 16; idx += kST) {  // the chunk's start state
       const int r = idx >> 4, cc = idx & 15;
       ws[a.L.S + r * Vp + col0 + cc] = SS[r * kTS + cc];
     }
     __syncthreads();
     if (c + 1 < a.NC) fscan_fetch<IT, KP>(pf, a, bh, c + 1, col0, tid);
     // W S over one half of the channels, rows 16 wt..
-    const f32x4 acc = mma_long(zero4(), Mat{WS + half * KH, kRS, 1}, 16 * wt, Mat{SS + half * KH * kTS, kTS, 1}, 0, KH);
+    const f32x4 acc = mma3(zero4(), SMat{WrS + half * KH, kC * rs, rs}, 16 * wt, SMat{StS + half * KH, 16 * rs, rs}, 0,
+                           KH);
     if (half == 1) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) PS[(16 * wt + 4 * lg4 + r) * kTS + li] = acc[r];
     }
     __syncthreads();
     if (half == 0) {  // Vt = U - W S
+      f32x4 vt;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * wt + 4 * lg4 + r;
-        const float vt = US[row * kTS + li] - acc[r] - PS[row * kTS + li];
-        US[row * kTS + li] = vt;
-        ws[a.L.Vt + row * Vp + col0 + li] = vt;
+        vt[r] = US[row * kTS + li] - acc[r] - PS[row * kTS + li];
+        ws[a.L.Vt + row * Vp + col0 + li] = vt[r];
       }
+      store_split4(VtS, 16 * kRSC, kRSC, li, 16 * wt + 4 * lg4, vt);
     }
     __syncthreads();
-    if (w < Kp / 16) {  // S <- D S + Kt^T Vt, row tile w
-      const f32x4 upd = mma_long(zero4(), Mat{KtS, 1, kRS}, 16 * w, Mat{US, kTS, 1}, 0, kC);
+    if (w < KP / 16) {  // S <- D S + Kt^T Vt, row tile w
+      const f32x4 upd = mma3(zero4(), SMat{KtS, KP * kRSC, kRSC}, 16 * w, SMat{VtS, 16 * kRSC, kRSC}, 0, kC);
+      f32x4 sn;
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * w + 4 * lg4 + r;
-        SS[row * kTS + li] = DS[row] * SS[row * kTS + li] + upd[r];
+        sn[r] = DS[row] * SS[row * kTS + li] + upd[r];
+        SS[row * kTS + li] = sn[r];
       }
+      store_split4(StS, 16 * rs, rs, li, 16 * w + 4 * lg4, sn);
     }
     __syncthreads();
   }
 }
 
-// ---- bscan_kernel: state gradients backwards through the chunks -------------
-//   dVt = Kt dS + Aqk^T dO[:, cols]           (waves 0-3, one row tile each)
-//   dS  <- (D dS + Qg^T dO[:, cols]) - W^T dVt  (the bracket on waves 4-7 next
-//                                              to dVt, the product after it)
 template <class IT>
 struct BscanBuf {
   f32x4 k[kPF], q[kPF], w[kPF], a[2];
-  IT o[2];  // raw dO, widened when written to LDS
+  IT o[2];  // raw dO, split when written to LDS
   float d;
 };
 
 template <class IT, int KP>
 __device__ __forceinline__ void bscan_fetch(BscanBuf<IT>& p, const Args<IT>& a, int64_t bh, int64_t b, int64_t h,
                                             int64_t c, int col0, int tid) {
-  constexpr int nq = kC * KP / 4;
   const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
+  fetch_split<KP>(p.k, ws + a.L.Ktr, tid);
+  fetch_split<KP>(p.q, ws + a.L.Qgt, tid);
+  fetch_split<KP>(p.w, ws + a.L.Wt, tid);
 #pragma unroll
-  for (int m = 0; m < kPF; ++m) {
-    const int q4 = tid + kST * m;
-    if (q4 < nq) {
-      p.k[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Kt + 4 * q4);
-      p.q[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Qg + 4 * q4);
-      p.w[m] = *reinterpret_cast<const f32x4*>(ws + a.L.W + 4 * q4);
-    }
-  }
+  for (int m = 0; m < 2; ++m) p.a[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Aqkt + 4 * (tid + kST * m));
 #pragma unroll
-  for (int m = 0; m < 2; ++m) p.a[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Aqk + 4 * (tid + kST * m));
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {  // clamped into the tensor; masked when widened
+  for (int m = 0; m < 2; ++m) {  // clamped into the tensor; masked when split
     const int idx = tid + kST * m, r = idx >> 4, cc = idx & 15;
     const int64_t t = c * kC + r < a.T ? c * kC + r : a.T - 1;
     const int64_t col = col0 + cc < a.V ? col0 + cc : a.V - 1;
@@ -598,85 +736,117 @@ __device__ __forceinline__ void bscan_fetch(BscanBuf<IT>& p, const Args<IT>& a, 
   if (tid < KP) p.d = ws[a.L.D + tid];
 }
 
+// LDS of the backward scan (bytes)
+template <int KP>
+struct BscanLds {
+  static constexpr int rs = kRSP(KP);
+  static constexpr int kt = 0;                                  // Kt split [64][KP]
+  static constexpr int qg = kt + 2 * kC * rs * 2;               // Qg^T split [KP][64]
+  static constexpr int wt = qg + 2 * KP * kRSC * 2;             // W^T split [KP][64]
+  static constexpr int aq = wt + 2 * KP * kRSC * 2;             // Aqk^T split [64][64]
+  static constexpr int dst = aq + 2 * kC * kRSC * 2;            // dS^T split [16][KP]
+  static constexpr int dot = dst + 2 * 16 * rs * 2;             // dO^T split [16][64]
+  static constexpr int xt = dot + 2 * 16 * kRSC * 2;            // dVt^T split [16][64]
+  static constexpr int dss = xt + 2 * 16 * kRSC * 2;            // dS f32 [128][kTS]
+  static constexpr int ds = dss + 128 * kTS * 4;                // D f32 [128]
+  static constexpr int bytes = ds + 128 * 4;
+};
+
 template <class IT, int KP>
-__device__ __forceinline__ void bscan_body(const Args<IT>& a, int64_t lb, float* smem) {
-  float *KtS = smem, *QgS = KtS + kC * kRS, *WS = QgS + kC * kRS, *AqkS = WS + kC * kRS, *dSS = AqkS + kC * kRC,
-        *dSp = dSS + 128 * kTS, *dOS = dSp + 128 * kTS, *XS = dOS + kC * kTS, *DS = XS + kC * kTS;
+__device__ __forceinline__ void bscan_body(const Args<IT>& a, int64_t lb, unsigned char* smem) {
+  using LL = BscanLds<KP>;
+  constexpr int rs = LL::rs;
+  __bf16 *KtS = reinterpret_cast<__bf16*>(smem + LL::kt), *QgS = reinterpret_cast<__bf16*>(smem + LL::qg),
+         *WtS = reinterpret_cast<__bf16*>(smem + LL::wt), *AqS = reinterpret_cast<__bf16*>(smem + LL::aq),
+         *dStS = reinterpret_cast<__bf16*>(smem + LL::dst), *dOtS = reinterpret_cast<__bf16*>(smem + LL::dot),
+         *XtS = reinterpret_cast<__bf16*>(smem + LL::xt);
+  float *dSS = reinterpret_cast<float*>(smem + LL::dss), *DS = reinterpret_cast<float*>(smem + LL::ds);
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
-  constexpr int Kp = KP, nq = kC * KP / 4;
   const int Vp = a.L.Vp, ncb = Vp / 16;
   const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
   const int col0 = 16 * static_cast<int>(lb % ncb);
-  for (int idx = tid; idx < Kp * 16; idx += kST) {
+  for (int idx = tid; idx < KP * 16; idx += kST) {  // dS_T and its split transpose
     const int r = idx >> 4, cc = idx & 15;
-    dSS[r * kTS + cc] = (a.dsT != nullptr && r < a.K && col0 + cc < a.V)
-                            ? a.dsT[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
-                            : 0.f;
+    const float x = (a.dsT != nullptr && r < a.K && col0 + cc < a.V)
+                        ? a.dsT[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
+                        : 0.f;
+    dSS[r * kTS + cc] = x;
+    __bf16 hi, lo;
+    split_bf16(x, hi, lo);
+    dStS[cc * rs + r] = hi;
+    dStS[16 * rs + cc * rs + r] = lo;
   }
   BscanBuf<IT> pf;
   bscan_fetch<IT, KP>(pf, a, bh, b, h, a.NC - 1, col0, tid);
   for (int64_t c = a.NC - 1; c >= 0; --c) {
     float* ws = a.ws + (bh * a.NC + c) * a.L.per;
+    split_to_lds<KP>(KtS, kC * rs, rs, KP, pf.k, tid);
+    split_to_lds<KP>(QgS, KP * kRSC, kRSC, kC, pf.q, tid);
+    split_to_lds<KP>(WtS, KP * kRSC, kRSC, kC, pf.w, tid);
 #pragma unroll
-    for (int m = 0; m < kPF; ++m) {
-      const int q4 = tid + kST * m;
-      if (q4 < nq) {
-        const int e = 4 * q4, r = e / Kp, col = e % Kp;
-        *reinterpret_cast<f32x4*>(&KtS[r * kRS + col]) = pf.k[m];
-        *reinterpret_cast<f32x4*>(&QgS[r * kRS + col]) = pf.q[m];
-        *reinterpret_cast<f32x4*>(&WS[r * kRS + col]) = pf.w[m];
-      }
+    for (int m = 0; m < 2; ++m) {  // Aqk^T: 2 x 4096 bf16 = 1024 f32x4
+      const int f = 8 * (tid + kST * m), pl = f / (kC * kC), e = f % (kC * kC);
+      *reinterpret_cast<f32x4*>(AqS + pl * kC * kRSC + (e >> 6) * kRSC + (e & 63)) = pf.a[m];
     }
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int e = 4 * (tid + kST * m), r = e >> 6, cc = e & 63;
-      *reinterpret_cast<f32x4*>(&AqkS[r * kRC + cc]) = pf.a[m];
-    }
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {
+    for (int m = 0; m < 2; ++m) {  // dO^T split
       const int idx = tid + kST * m, r = idx >> 4, cc = idx & 15;
       const bool real = c * kC + r < a.T && col0 + cc < a.V;
-      dOS[r * kTS + cc] = real ? to_float(pf.o[m]) : 0.f;
+      __bf16 hi, lo;
+      split_bf16(real ? to_float(pf.o[m]) : 0.f, hi, lo);
+      dOtS[cc * kRSC + r] = hi;
+      dOtS[16 * kRSC + cc * kRSC + r] = lo;
     }
-    if (tid < Kp) DS[tid] = pf.d;
-    for (int idx = tid; idx < Kp * 16; idx += kST) {  // gradient of the chunk's end state
+    if (tid < KP) DS[tid] = pf.d;
+    for (int idx = tid; idx < KP * 16; idx += kST) {  // gradient of the chunk's end state
       const int r = idx >> 4, cc = idx & 15;
       ws[a.L.dS + r * Vp + col0 + cc] = dSS[r * kTS + cc];
     }
     __syncthreads();
     if (c > 0) bscan_fetch<IT, KP>(pf, a, bh, b, h, c - 1, col0, tid);
+    f32x4 dsp[2];
     if (w < 4) {  // dVt = Kt dS + Aqk^T dO, rows 16w..
-      f32x4 acc = mma_long(zero4(), Mat{KtS, kRS, 1}, 16 * w, Mat{dSS, kTS, 1}, 0, Kp);
-      acc = mma_long(acc, Mat{AqkS, 1, kRC}, 16 * w, Mat{dOS, kTS, 1}, 0, kC);
+      f32x4 acc = mma3(zero4(), SMat{KtS, kC * rs, rs}, 16 * w, SMat{dStS, 16 * rs, rs}, 0, KP);
+      acc = mma3(acc, SMat{AqS, kC * kRSC, kRSC}, 16 * w, SMat{dOtS, 16 * kRSC, kRSC}, 0, kC);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * w + 4 * lg4 + r;
-        XS[row * kTS + li] = acc[r];
-        ws[a.L.dVt + row * Vp + col0 + li] = acc[r];
-      }
+      for (int r = 0; r < 4; ++r) ws[a.L.dVt + (16 * w + 4 * lg4 + r) * Vp + col0 + li] = acc[r];
+      store_split4(XtS, 16 * kRSC, kRSC, li, 16 * w + 4 * lg4, acc);
     } else {  // D dS + Qg^T dO, row tiles w-4 and w
-      for (int rt = w - 4; rt < Kp / 16; rt += 4) {
-        const f32x4 p = mma_long(zero4(), Mat{QgS, 1, kRS}, 16 * rt, Mat{dOS, kTS, 1}, 0, kC);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = 16 * rt + 4 * lg4 + r;
-          dSp[row * kTS + li] = DS[row] * dSS[row * kTS + li] + p[r];
+      for (int j = 0; j < 2; ++j) {
+        const int rt = w - 4 + 4 * j;
+        if (rt < KP / 16) {
+          const f32x4 p = mma3(zero4(), SMat{QgS, KP * kRSC, kRSC}, 16 * rt, SMat{dOtS, 16 * kRSC, kRSC}, 0, kC);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = 16 * rt + 4 * lg4 + r;
+            dsp[j][r] = DS[row] * dSS[row * kTS + li] + p[r];
+          }
         }
       }
     }
     __syncthreads();
-    if (w < Kp / 16) {  // dS = dSp - W^T dVt, row tile w
-      const f32x4 n = mma_long(zero4(), Mat{WS, 1, kRS}, 16 * w, Mat{XS, kTS, 1}, 0, kC);
+    if (w >= 4) {  // dS = dsp - W^T dVt
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * w + 4 * lg4 + r;
-        dSS[row * kTS + li] = dSp[row * kTS + li] - n[r];
+      for (int j = 0; j < 2; ++j) {
+        const int rt = w - 4 + 4 * j;
+        if (rt < KP / 16) {
+          const f32x4 n = mma3(zero4(), SMat{WtS, KP * kRSC, kRSC}, 16 * rt, SMat{XtS, 16 * kRSC, kRSC}, 0, kC);
+          f32x4 dn;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int row = 16 * rt + 4 * lg4 + r;
+            dn[r] = dsp[j][r] - n[r];
+            dSS[row * kTS + li] = dn[r];
+          }
+          store_split4(dStS, 16 * rs, rs, li, 16 * rt + 4 * lg4, dn);
+        }
       }
     }
     __syncthreads();
   }
   if (a.ds0 != nullptr) {
-    for (int idx = tid; idx < Kp * 16; idx += kST) {
+    for (int idx = tid; idx < KP * 16; idx += kST) {
       const int r = idx >> 4, cc = idx & 15;
       if (r < a.K && col0 + cc < a.V) a.ds0[((b * a.H + h) * a.K + r) * a.V + col0 + cc] = dSS[r * kTS + cc];
     }
@@ -690,7 +860,8 @@ __device__ __forceinline__ void bscan_body(const Args<IT>& a, int64_t lb, float*
 // XCD owning a contiguous range so the column blocks of a head share its L2.
 template <class IT, int KP>
 __global__ __launch_bounds__(kST) void scan_kernel(const Args<IT> a) {
-  __shared__ __attribute__((aligned(16))) float smem[kScanFloats];
+  constexpr int bytes = FscanLds<KP>::bytes > BscanLds<KP>::bytes ? FscanLds<KP>::bytes : BscanLds<KP>::bytes;
+  __shared__ __attribute__((aligned(16))) unsigned char smem[bytes];
   const int64_t lb = xcd_block(blockIdx.x, gridDim.x), n = gridDim.x / 2;
   if (lb < n)
     fscan_body<IT, KP>(a, lb, smem);
