@@ -348,8 +348,9 @@ __device__ __forceinline__ void block_pair(int p, int& I, int& J) {
 }
 
 // ---- prep_kernel: per-chunk intermediates ----------------------------------
+constexpr int kPT = 512;  // threads of prep_kernel
 template <class IT, int KP>
-__global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
+__global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
   __shared__ float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS];
   __shared__ float AS[kC * kRC], AqkS[kC * kRC], NS[kC * kRC];
   __shared__ float bS[kC];
@@ -361,14 +362,14 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
   const int Vp = a.L.Vp;
   float* ws = a.ws + ch * a.L.per;
 
-  load_rows<IT, KP, kRS, 256>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid);
-  load_rows<IT, KP, kRS, 256>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid);
-  load_rows<IT, KP, kRS, 256>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_rows<IT, KP, kRS, kPT>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_rows<IT, KP, kRS, kPT>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_rows<IT, KP, kRS, kPT>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid);
   if (tid < kC) {
     const int64_t t = t0 + tid;
     bS[tid] = t < a.T ? to_float(a.beta[tok(b, t, a.T, a.H, h)]) : 0.f;
   }
-  for (int idx = tid; idx < kC * kRC; idx += 256) {
+  for (int idx = tid; idx < kC * kRC; idx += kPT) {
     AS[idx] = 0.f;
     AqkS[idx] = 0.f;
   }
@@ -384,9 +385,9 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
     }
   }
   __syncthreads();
-  if (!needs_exact<KP, 256>(lgS, rising, tid)) {
+  if (!needs_exact<KP, kPT>(lgS, rising, tid)) {
     // A and Aqk block by block on the MFMA
-    for (int p = w; p < 10; p += 4) {
+    for (int p = w; p < 10; p += kPT / 64) {
       int I, J;
       block_pair(p, I, J);
       f32x4 ak = zero4(), aq = zero4();
@@ -400,7 +401,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
     }
   } else
   // A and Aqk with exact pair exponents, 2x2 blocks of (i, j <= i)
-  for (int blk = tid; blk < 528; blk += 256) {
+  for (int blk = tid; blk < 528; blk += kPT) {
     int I2 = static_cast<int>((sqrtf(8.f * blk + 1.f) - 1.f) * 0.5f);
     while (I2 * (I2 + 1) / 2 > blk) --I2;
     while ((I2 + 1) * (I2 + 2) / 2 <= blk) ++I2;
@@ -442,22 +443,22 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
       }
   }
   __syncthreads();
-  for (int idx = tid; idx < kC * kC; idx += 256) {  // A
+  for (int idx = tid; idx < kC * kC; idx += kPT) {  // A
     const int r = idx >> 6, cc = idx & 63;
     ws[a.L.A + idx] = AS[r * kRC + cc];
   }
-  for (int i8 = tid; i8 < kC * kC / 8; i8 += 256) {  // Aqk^T split, eight positions at a time
+  for (int i8 = tid; i8 < kC * kC / 8; i8 += kPT) {  // Aqk^T split, eight positions at a time
     const int r = (8 * i8) >> 6, c0 = (8 * i8) & 63;
     float x[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = AqkS[(c0 + e) * kRC + r];
     put_split8(ws + a.L.Aqkt, kC * kC, 8 * i8, x);
   }
-  for (int idx = tid; idx < kC * Kp; idx += 256) {  // Kg (f32)
+  for (int idx = tid; idx < kC * Kp; idx += kPT) {  // Kg (f32)
     const int r = idx / Kp, col = idx % Kp;
     ws[a.L.Kg + idx] = fast_exp(lgS[r * kRS + col]) * kS[r * kRS + col];
   }
-  for (int i8 = tid; i8 < kC * Kp / 8; i8 += 256) {  // Kt split, row-major
+  for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {  // Kt split, row-major
     const int r = (8 * i8) / Kp, c0 = (8 * i8) % Kp;
     float x[8];
 #pragma unroll
@@ -467,7 +468,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
     }
     put_split8(ws + a.L.Ktr, kC * Kp, 8 * i8, x);
   }
-  for (int i8 = tid; i8 < kC * Kp / 8; i8 += 256) {  // Kt^T and Qg^T split, eight positions at a time
+  for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {  // Kt^T and Qg^T split, eight positions at a time
     const int col = (8 * i8) / kC, r0 = (8 * i8) % kC;
     const float last = lgS[(kC - 1) * kRS + col];
     float xk[8], xq[8];
@@ -482,12 +483,12 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
   }
   if (tid < Kp) ws[a.L.D + tid] = fast_exp(lgS[(kC - 1) * kRS + tid]);
   __syncthreads();
-  for (int idx = tid; idx < kC * kC; idx += 256) {  // L's strict part b_i A_ij over A; N cleared
+  for (int idx = tid; idx < kC * kC; idx += kPT) {  // L's strict part b_i A_ij over A; N cleared
     const int r = idx >> 6, cc = idx & 63;
     AS[r * kRC + cc] *= bS[r];
     NS[r * kRC + cc] = 0.f;
   }
-  for (int idx = tid; idx < kC * Kp; idx += 256) {  // Kg over k: the B operand of W = M Kg
+  for (int idx = tid; idx < kC * Kp; idx += kPT) {  // Kg over k: the B operand of W = M Kg
     const int r = idx / Kp, col = idx % Kp;
     kS[r * kRS + col] *= fast_exp(lgS[r * kRS + col]);
   }
@@ -495,7 +496,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
   // N = L^-1 by 16x16 blocks: wave w inverts diagonal block w by forward
   // substitution (lane c < 16 solves column c), then block rows I = 1..3 follow
   // N_IJ = -N_II sum_{K=J}^{I-1} L_IK N_KJ on the MFMA.
-  if (lane < 16) {
+  if (w < 4 && lane < 16) {
     const int base = 16 * w;
     float x[16];
 #pragma unroll
@@ -525,7 +526,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
     }
     __syncthreads();
   }
-  for (int idx = tid; idx < kC * kC; idx += 256) {  // M = N diag(b) over A
+  for (int idx = tid; idx < kC * kC; idx += kPT) {  // M = N diag(b) over A
     const int r = idx >> 6, cc = idx & 63;
     const float n = NS[r * kRC + cc];
     ws[a.L.N + idx] = n;
@@ -533,16 +534,16 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
   }
   __syncthreads();
   const int nkt = Kp / 16, nvt = Vp / 16;
-  for (int tt = w; tt < 4 * nkt; tt += 4) {  // W = M Kg, staged in f32 over q
+  for (int tt = w; tt < 4 * nkt; tt += kPT / 64) {  // W = M Kg, staged in f32 over q
     const int rt = tt & 3, ct = tt >> 2;
     const f32x4 acc = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{kS, kRS, 1}, 16 * ct, kC);
 #pragma unroll
     for (int r = 0; r < 4; ++r) qS[(16 * rt + 4 * lg4 + r) * kRS + 16 * ct + li] = acc[r];
   }
   for (int s0 = 0; s0 < Vp; s0 += 32)  // v over lg (no longer read)
-    load_rows<IT, 32, kRS, 256>(lgS + s0, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
+    load_rows<IT, 32, kRS, kPT>(lgS + s0, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
   __syncthreads();
-  for (int i8 = tid; i8 < kC * Kp / 8; i8 += 256) {  // W and W^T split
+  for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {  // W and W^T split
     float x[8], y[8];
     const int r = (8 * i8) / Kp, c0 = (8 * i8) % Kp;
     const int c2 = (8 * i8) / kC, r2 = (8 * i8) % kC;
@@ -554,7 +555,7 @@ __global__ __launch_bounds__(256) void prep_kernel(const Args<IT> a) {
     put_split8(ws + a.L.Wr, kC * Kp, 8 * i8, x);
     put_split8(ws + a.L.Wt, kC * Kp, 8 * i8, y);
   }
-  for (int tt = w; tt < 4 * nvt; tt += 4) {  // U = M v
+  for (int tt = w; tt < 4 * nvt; tt += kPT / 64) {  // U = M v
     const int rt = tt & 3, ct = tt >> 2;
     const f32x4 acc = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{lgS, kRS, 1}, 16 * ct, kC);
 #pragma unroll
@@ -1345,7 +1346,7 @@ size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int
 
 template <class IT, int KP>
 static void launch_all(const bwd::Args<IT>& a, dim3 chunks, dim3 scans, hipStream_t s) {
-  hipLaunchKernelGGL((bwd::prep_kernel<IT, KP>), chunks, dim3(256), 0, s, a);
+  hipLaunchKernelGGL((bwd::prep_kernel<IT, KP>), chunks, dim3(bwd::kPT), 0, s, a);
   hipLaunchKernelGGL((bwd::scan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
   hipLaunchKernelGGL((bwd::grad_kernel<IT, KP>), chunks, dim3(512), 0, s, a);
   hipLaunchKernelGGL((bwd::pair_kernel<IT, KP, 512>), chunks, dim3(512), 0, s, a);
