@@ -875,24 +875,93 @@ __global__ __launch_bounds__(kST) void scan_kernel(const Args<IT> a) {
 // row tile w % 4, half w / 4 of the column tiles),
 // dAqk and dM in MFMA accumulators and write dv; then dKg = M^T dW,
 // dM += dW Kg^T, dbeta and dA follow from N.
-constexpr int kOffM = 0;                        // [64][68] M = N diag(b)
-constexpr int kOffSs = kOffM + kC * kRC;        // [128][36] S slab
-constexpr int kOffdSn = kOffSs + 128 * kSS;     // [128][36] dS' slab
-constexpr int kOffdOs = kOffdSn + 128 * kSS;    // [64][36] dO slab
-constexpr int kOffVts = kOffdOs + kC * kSS;     // [64][36] Vt slab
-constexpr int kOffdVts = kOffVts + kC * kSS;    // [64][36] dVt slab
-constexpr int kOffvs = kOffdVts + kC * kSS;     // [64][36] v slab
-constexpr int kGradFloats = kOffvs + kC * kSS;
+constexpr int kSR = kSW + 8;                    // bf16 row stride of the split slab tiles
+constexpr int kOffM = 0;                        // [64][68] f32 M = N diag(b)
+constexpr int kOffSs = kOffM + kC * kRC;        // S slab split [128][kSR] x 2 planes (bf16; offsets in floats)
+constexpr int kOffdSn = kOffSs + 128 * kSR;     // dS' slab split
+constexpr int kOffdOs = kOffdSn + 128 * kSR;    // dO slab split [64][kSR] x 2
+constexpr int kOffVts = kOffdOs + kC * kSR;     // Vt slab split
+constexpr int kOffdVts = kOffVts + kC * kSR;    // dVt slab split
+constexpr int kOffvs = kOffdVts + kC * kSR;     // v slab split
+constexpr int kOffdVf = kOffvs + kC * kSR;      // dVt slab f32 [64][36] (the B operand of dv = M^T dVt)
+constexpr int kGradFloats = kOffdVf + kC * kSS;
 // second stage, over the slabs
-constexpr int kOffX = kOffSs;                   // [64][132] -dW... stored as dW
-constexpr int kOffY = kOffdOs;                  // [64][132] Kg
+constexpr int kOffX = kOffSs;                   // [64][132] dW
+constexpr int kOffY = kOffX + kC * kRS;         // [64][132] Kg
 constexpr int kOffN = kOffSs;                   // [64][68]
 constexpr int kOffDM = kOffN + kC * kRC;        // [64][68] dM, then T1 = N^T dN
-constexpr int kOffDN = kOffdOs;                 // [64][68] dN, then dL
+constexpr int kOffDN = kOffDM + kC * kRC;       // [64][68] dN, then dL
 constexpr int kOffA = kOffDN + kC * kRC;        // [64][68]
-static_assert(kOffX + kC * kRS <= kOffY, "dW must not overlap Kg");
-static_assert(kOffY + kC * kRS <= kGradFloats, "Kg must fit");
-static_assert(kOffDM + kC * kRC <= kOffDN && kOffA + kC * kRC <= kGradFloats, "second-stage tiles must fit");
+static_assert(kOffY + kC * kRS <= kGradFloats, "dW and Kg must fit");
+static_assert(kOffA + kC * kRC <= kGradFloats, "second-stage tiles must fit");
+
+// One slab tile (rows x 32 columns, f32 values v for columns c4..c4+3 of row r)
+// into a split tile of row stride kSR (bf16) and plane `plane`.
+__device__ __forceinline__ void put_split4(__bf16* dst, int plane, int r, int c4, f32x4 v) {
+  bf16x4 hi, lo;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    __bf16 x, y;
+    split_bf16(v[e], x, y);
+    hi[e] = x;
+    lo[e] = y;
+  }
+  *reinterpret_cast<bf16x4*>(dst + r * kSR + c4) = hi;
+  *reinterpret_cast<bf16x4*>(dst + plane + r * kSR + c4) = lo;
+}
+
+// A NROW x 32 workspace slab (row stride ld, from column col0), split into LDS.
+template <int NROW, int NT>
+__device__ __forceinline__ void load_ws_split(__bf16* dst, const float* src, int ld, int col0, int tid) {
+  constexpr int PER = NROW * 8 / NT;
+  static_assert(PER * NT == NROW * 8, "the tile must split evenly over the threads");
+  f32x4 v[PER];
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+    v[it] = *reinterpret_cast<const f32x4*>(src + r * ld + col0 + c4);
+  }
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+    put_split4(dst, NROW * kSR, r, c4, v[it]);
+  }
+}
+
+// Columns col0 .. col0+31 of the chunk's rows of an input [B,T,H,X], split into
+// LDS (zero past T and X); see load_rows.
+template <class IT, int NT>
+__device__ __forceinline__ void load_rows_split(__bf16* dst, const IT* src, int64_t b, int64_t t0, int64_t T,
+                                                int64_t H, int64_t h, int64_t X, int col0, int tid) {
+  constexpr int PER = kC * 8 / NT;
+  typedef typename Raw4<IT>::type raw_t;
+  if ((X & 3) == 0 && col0 + 32 <= X) {
+    raw_t v[PER];
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+      const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+      const int64_t t = t0 + r < T ? t0 + r : T - 1;
+      v[it] = *reinterpret_cast<const raw_t*>(src + tok(b, t, T, H, h) * X + col0 + c4);
+    }
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+      const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+      put_split4(dst, kC * kSR, r, c4, t0 + r < T ? widen<IT>(v[it]) : zero4());
+    }
+  } else {
+    for (int it = 0; it < PER; ++it) {
+      const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+      const int64_t t = t0 + r;
+      f32x4 x = zero4();
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int64_t col = col0 + c4 + u;
+        x[u] = (t < T && col < X) ? to_float(src[tok(b, t, T, H, h) * X + col]) : 0.f;
+      }
+      put_split4(dst, kC * kSR, r, c4, x);
+    }
+  }
+}
 
 template <class IT, int KP>
 __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
@@ -921,19 +990,23 @@ __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
 #pragma unroll
   for (int m = 0; m < 2; ++m) aA[m] = aM[m] = zero4();
   float dd = 0.f;
-  float *Ss = sm + kOffSs, *dSn = sm + kOffdSn, *dOs = sm + kOffdOs, *Vts = sm + kOffVts, *dVts = sm + kOffdVts,
-        *vs = sm + kOffvs;
+  __bf16 *Ss = reinterpret_cast<__bf16*>(sm + kOffSs), *dSn = reinterpret_cast<__bf16*>(sm + kOffdSn),
+         *dOs = reinterpret_cast<__bf16*>(sm + kOffdOs), *Vts = reinterpret_cast<__bf16*>(sm + kOffVts),
+         *dVts = reinterpret_cast<__bf16*>(sm + kOffdVts), *vs = reinterpret_cast<__bf16*>(sm + kOffvs);
+  float* dVf = sm + kOffdVf;
+  const SMat mS{Ss, KP * kSR, kSR}, mdS{dSn, KP * kSR, kSR}, mdO{dOs, kC * kSR, kSR}, mVt{Vts, kC * kSR, kSR},
+      mdVt{dVts, kC * kSR, kSR}, mv{vs, kC * kSR, kSR};
   for (int s0 = 0; s0 < Vp; s0 += kSW) {  // Vp is a multiple of the slab width
-    constexpr int sw = kSW;
-    load_ws<KP, kSW, kSS, NT>(Ss, ws + a.L.S, Vp, s0, tid);
-    load_ws<KP, kSW, kSS, NT>(dSn, ws + a.L.dS, Vp, s0, tid);
-    load_ws<kC, kSW, kSS, NT>(Vts, ws + a.L.Vt, Vp, s0, tid);
-    load_ws<kC, kSW, kSS, NT>(dVts, ws + a.L.dVt, Vp, s0, tid);
-    load_rows<IT, kSW, kSS, NT>(dOs, a.dout, b, t0, a.T, a.H, h, a.V, s0, tid);
-    load_rows<IT, kSW, kSS, NT>(vs, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
+    load_ws_split<KP, NT>(Ss, ws + a.L.S, Vp, s0, tid);
+    load_ws_split<KP, NT>(dSn, ws + a.L.dS, Vp, s0, tid);
+    load_ws_split<kC, NT>(Vts, ws + a.L.Vt, Vp, s0, tid);
+    load_ws_split<kC, NT>(dVts, ws + a.L.dVt, Vp, s0, tid);
+    load_ws<kC, kSW, kSS, NT>(dVf, ws + a.L.dVt, Vp, s0, tid);
+    load_rows_split<IT, NT>(dOs, a.dout, b, t0, a.T, a.H, h, a.V, s0, tid);
+    load_rows_split<IT, NT>(vs, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
     __syncthreads();
     {  // dv = M^T dVt, tile (rt, hf) of the slab
-      const f32x4 acc = mma(zero4(), Mat{MS, 1, kRC}, 16 * rt, Mat{dVts, kSS, 1}, 16 * hf, kC);
+      const f32x4 acc = mma(zero4(), Mat{MS, 1, kRC}, 16 * rt, Mat{dVf, kSS, 1}, 16 * hf, kC);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int row = 16 * rt + 4 * lg4 + r, col = s0 + 16 * hf + li;
@@ -941,21 +1014,26 @@ __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
         if (t < a.T && col < a.V) a.dv[tok(b, t, a.T, a.H, h) * a.V + col] = from_compute<IT>(acc[r]);
       }
     }
+    // products over the slab's 32 state columns on split-bf16 operands
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int ct = hf * CH + j;
-      aQ[j] = mma(aQ[j], Mat{dOs, kSS, 1}, 16 * rt, Mat{Ss, 1, kSS}, 16 * ct, sw);
-      aT[j] = mma(aT[j], Mat{Vts, kSS, 1}, 16 * rt, Mat{dSn, 1, kSS}, 16 * ct, sw);
-      aW[j] = mma(aW[j], Mat{dVts, kSS, 1}, 16 * rt, Mat{Ss, 1, kSS}, 16 * ct, sw);
+      aQ[j] = mma3(aQ[j], mdO, 16 * rt, mS, 16 * ct, kSW);
+      aT[j] = mma3(aT[j], mVt, 16 * rt, mdS, 16 * ct, kSW);
+      aW[j] = mma3(aW[j], mdVt, 16 * rt, mS, 16 * ct, kSW);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int ct = hf * 2 + j;
-      aA[j] = mma(aA[j], Mat{dOs, kSS, 1}, 16 * rt, Mat{Vts, 1, kSS}, 16 * ct, sw);
-      aM[j] = mma(aM[j], Mat{dVts, kSS, 1}, 16 * rt, Mat{vs, 1, kSS}, 16 * ct, sw);
+      aA[j] = mma3(aA[j], mdO, 16 * rt, mVt, 16 * ct, kSW);
+      aM[j] = mma3(aM[j], mdVt, 16 * rt, mv, 16 * ct, kSW);
     }
     if (tid < Kp)
-      for (int cc = 0; cc < sw; ++cc) dd += dSn[tid * kSS + cc] * Ss[tid * kSS + cc];
+      for (int cc = 0; cc < kSW; ++cc) {
+        const float sv = static_cast<float>(Ss[tid * kSR + cc]) + static_cast<float>(Ss[KP * kSR + tid * kSR + cc]);
+        const float dv = static_cast<float>(dSn[tid * kSR + cc]) + static_cast<float>(dSn[KP * kSR + tid * kSR + cc]);
+        dd += dv * sv;
+      }
     __syncthreads();
   }
 
