@@ -21,6 +21,10 @@ Metric: "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s".
                shape, as HBM GB/s (not part of `value`).
 * backward   : the chunkwise backward (all input gradients) on the prefill
                workload, ms and tokens/s (not part of `value`).
+* cache_reorder: the beam-search reorder of a whole decode cache (8 KDA
+               layers at the decode shape) through kda_cache_gather, as HBM
+               GB/s, next to the per-tensor index_select it replaces (not part
+               of `value`).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 3]
 """
@@ -291,6 +295,70 @@ def bench_backward(reps=10):
     }
 
 
+def bench_cache(layers=8, reps=10):
+    """Reorder of a whole decode cache by a random permutation of the batch:
+    `layers` KDA layers at the decode shape (f32 state [256, 32, 128, 128],
+    three bf16 ShortConv histories [256, 3, 4096], int64 offsets [256]), 40
+    tensors in one kda_cache_gather launch into preallocated outputs.
+    Algorithmic bytes = every row read once and written once.  The same
+    reorder as one torch index_select per tensor (what KDAState.reorder does
+    per layer) is timed beside it."""
+    import torch
+
+    from kda import _lib, _prep
+
+    lib = _lib.load()
+    device = torch.device("cuda", 0)
+    B, W = D_B, D_H * D_K
+    tensors = []
+    for _ in range(layers):
+        tensors.append(torch.empty(B, D_H, D_K, D_V, device=device).uniform_())
+        tensors += [torch.empty(B, 3, W, device=device, dtype=torch.bfloat16).uniform_() for _ in range(3)]
+        tensors.append(torch.arange(B, device=device, dtype=torch.long))
+    outs = [torch.empty_like(t) for t in tensors]
+    perm = torch.randperm(B, generator=torch.Generator().manual_seed(3)).to(device)
+    n = len(tensors)
+    src = (ctypes.c_void_p * n)(*[t.data_ptr() for t in tensors])
+    dst = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+    rows = (ctypes.c_int64 * n)(*[t[0].numel() * t.element_size() for t in tensors])
+    status = torch.zeros(1, dtype=torch.int32, device=device)
+    stream = _prep.stream(device)
+    nbytes = 2 * sum(t.numel() * t.element_size() for t in tensors)
+
+    def native():
+        _lib.check(lib.kda_cache_gather(src, dst, rows, n, perm.data_ptr(), B, B, status.data_ptr(), stream))
+
+    def per_tensor():
+        for t, o in zip(tensors, outs):
+            torch.index_select(t, 0, perm, out=o)
+
+    res = {}
+    for name, fn in (("kda_cache_gather", native), ("torch_index_select_per_tensor", per_tensor)):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"ms": round(ms, 4), "achieved_gbs": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    native()
+    torch.cuda.synchronize()
+    if int(status.item()) != 0 or not torch.equal(outs[0], tensors[0][perm]):
+        raise RuntimeError("cache reorder check failed")
+    return {
+        "workload": f"reorder of {layers} KDA layers' decode caches, B={B} H={D_H} K=V={D_K} f32 states + "
+                    f"3 bf16 ShortConv histories [B,3,{W}] + offsets ({n} tensors), random permutation",
+        "algorithmic_bytes": nbytes,
+        **res,
+    }
+
+
 def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
     """The oracle's CPU restatement, timed like benchmarks/benchmark_kda.py:30-40
     (one warm-up, then min over repeats of time.perf_counter, inference_mode)."""
@@ -463,6 +531,7 @@ def main() -> int:
         "kernels": bench_fused(),
     }
     result["backward"] = bench_backward()
+    result["cache_reorder"] = bench_cache()
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()
         result["cpu_baseline"] = cpu["prefill"]

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 4
+#define KDA_ABI_VERSION 5
 
 /* status codes */
 #define KDA_OK 0
@@ -220,6 +220,23 @@ int kda_gates_fwd(const void* decay_logits, const void* decay_bias, const float*
 int kda_rmsnorm_gate_fwd(const void* x, const void* weight, int weight_per_head,
                          const void* gate_logits, void* y, int64_t rows, int64_t heads,
                          int64_t head_dim, double eps, int dtype, void* stream);
+
+/*
+ * Cache plumbing for serving: out_t[i, ...] = src_t[index[i], ...] for every tensor t of a
+ * decode cache, in one launch per 64 tensors.  Replaces the per-tensor index_select of
+ * KDAState.reorder (src/kda/state.py:50-67) and ShortConvState, taken over every layer by
+ * HybridLayerCache/HybridBackboneCache.reorder (src/hybrid_backbone/cache.py:58-61,118-126);
+ * with index == NULL it is the copy of KDAState.clone (src/kda/state.py:41-48).
+ *   src[t], dst[t] : device pointers to batch-major tensors of n_src and n_out rows of
+ *                    row_bytes[t] bytes each (any dtype; 16-byte units when sizes and
+ *                    addresses allow); an output may not overlap any source or other output
+ *   index          : device int64 [n_out], each in [0, n_src), or NULL (n_out == n_src)
+ *   status         : device int32, or NULL; set to 1 (never cleared here) when an index is
+ *                    out of range, whose output row is then left unwritten
+ * The host arrays src, dst and row_bytes are read before the call returns.
+ */
+int kda_cache_gather(const void* const* src, void* const* dst, const int64_t* row_bytes, int n_tensors,
+                     const int64_t* index, int64_t n_src, int64_t n_out, int* status, void* stream);
 
 #ifdef __cplusplus
 }

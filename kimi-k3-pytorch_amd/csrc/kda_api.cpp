@@ -331,4 +331,11 @@ int kda_rmsnorm_gate_fwd(const void* x, const void* weight, int weight_per_head,
                              static_cast<hipStream_t>(stream));
 }
 
+int kda_cache_gather(const void* const* src, void* const* dst, const int64_t* row_bytes, int n_tensors,
+                     const int64_t* index, int64_t n_src, int64_t n_out, int* status, void* stream) {
+  g_detail[0] = '\0';
+  return launch_cache_gather(src, dst, row_bytes, n_tensors, index, n_src, n_out, status,
+                             static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

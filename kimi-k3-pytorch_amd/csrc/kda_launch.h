@@ -55,4 +55,8 @@ int launch_gates(const void* z, const void* zbias, const float* a_log, double g_
 int launch_rmsnorm_gate(const void* x, const void* w, int w_per_head, const void* gl, void* y, int64_t rows,
                         int64_t H, int64_t D, double eps, int dtype, hipStream_t stream);
 
+// Batch-row gather over many cache tensors (csrc/kda_cache.hip).
+int launch_cache_gather(const void* const* src, void* const* dst, const int64_t* row_bytes, int n_tensors,
+                        const int64_t* index, int64_t n_src, int64_t n_out, int* status, hipStream_t stream);
+
 }  // namespace kda_host

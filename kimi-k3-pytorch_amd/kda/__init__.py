@@ -3,12 +3,13 @@
 Mirrors the operator surface of pablo-reyes8/kimi-k3-pytorch ``src/kda``
 (src/kda/__init__.py:1-25): ``chunkwise_kda``, ``recurrent_kda``,
 ``ut_transform``, ``KDAOperatorOutput``, ``UTTransformOutput`` and
-``KDAState``, plus the fused stages around the operator in ``kda.fused``.
+``KDAState``, plus the fused stages around the operator in ``kda.fused`` and the
+whole-cache reorder and clone in ``kda.cache``.
 All arithmetic runs in hand-written HIP kernels in ``libkda_mi355x.so``; see
 include/kda_mi355x.h for the C ABI.
 """
 
-from . import fused
+from . import cache, fused
 from .chunkwise import chunkwise_kda
 from .recurrent import KDAOperatorOutput, recurrent_kda
 from .state import KDAState, ShortConvState
@@ -19,6 +20,7 @@ __all__ = [
     "KDAState",
     "ShortConvState",
     "UTTransformOutput",
+    "cache",
     "chunkwise_kda",
     "fused",
     "recurrent_kda",

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libkda_mi355x.so")
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 KDA_OK = 0
 KDA_ERR_INVALID_ARGUMENT = 1
@@ -66,6 +66,7 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _P, _S, _P],
     ),
+    "kda_cache_gather": (_I, [_P, _P, _P, _I, _P, _L, _L, _P, _P]),
 }
 
 _lock = threading.Lock()

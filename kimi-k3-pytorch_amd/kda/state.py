@@ -6,6 +6,9 @@ state is one plain ``[B,H,K,V]`` tensor (f32 for bf16 models), next to three
 ShortConv buffers ``[B, K_conv-1, width]`` and an int64 ``sequence_offset``.
 The decode kernel reads and writes ``recurrent_state`` in exactly this
 layout, so the byte accounting of inference/cache.py:32-38 is unchanged.
+``clone`` and ``reorder`` of a state held on the GPU run the native batch-row
+gather of ``kda.cache`` (one launch for all five tensors); a state held in
+host memory keeps torch's copies.
 """
 
 from __future__ import annotations
@@ -26,6 +29,10 @@ class ShortConvState:
             raise ValueError("ShortConv state buffer must have shape [B,K-1,C]")
 
     def clone(self) -> "ShortConvState":
+        if self.buffer.is_cuda:
+            from .cache import gather_rows
+
+            return ShortConvState(gather_rows([self.buffer], None)[0])
         return ShortConvState(self.buffer.clone())
 
 
@@ -58,6 +65,10 @@ class KDAState:
             raise ValueError("all ShortConv states must match recurrent batch size")
 
     def clone(self) -> "KDAState":
+        if self.recurrent_state.is_cuda:
+            from .cache import clone_states
+
+            return clone_states([self])[0]
         return KDAState(
             recurrent_state=self.recurrent_state.clone(),
             q_conv_state=self.q_conv_state.clone(),
@@ -71,6 +82,10 @@ class KDAState:
             raise ValueError("indices must be a rank-1 torch.long tensor")
         if indices.device != self.recurrent_state.device:
             raise ValueError("indices and state must be on the same device")
+        if self.recurrent_state.is_cuda:
+            from .cache import reorder_states
+
+            return reorder_states([self], indices)[0]
         pick = lambda t: t.index_select(0, indices)  # noqa: E731
         return KDAState(
             recurrent_state=pick(self.recurrent_state),

@@ -28,6 +28,9 @@ CPU baseline, but the code is written independently:
 * ``beta_gate``            follows ``src/kda/projections.py:207-209``
 * ``rmsnorm_gate``         follows ``src/kimi_primitives/headwise_rmsnorm.py:39-64``
   and the gate product of ``src/kimi_primitives/output_gate.py:62-75``
+* ``gather_rows``          follows ``KDAState.reorder`` / ``clone``
+  (``src/kda/state.py:41-67``) taken over every layer by
+  ``src/hybrid_backbone/cache.py:56-61,112-126``
 
 How each function is pinned (tests/test_oracle_*.py):
 
@@ -52,6 +55,10 @@ How each function is pinned (tests/test_oracle_*.py):
 * ``lower_bounded_decay`` / ``beta_gate``: the sigmoid midpoint, the clamp
   bounds, monotonicity.
 * ``rmsnorm_gate``: unit mean square, scale invariance, the gate midpoint.
+* ``gather_rows``: the reference's reorder test (indices [2, 0, 2] pick those
+  batch rows of every layer, tests/hybrid_backbone/test_hybrid_cache.py:82-101),
+  a permutation followed by its inverse is the identity, and a clone is a
+  byte-equal copy that shares no memory.
 
 Rounding: the reference's bit-level float32/bfloat16 rounding order (einsum /
 BLAS / LAPACK) is not reproduced; parity is judged with tolerances.
@@ -73,6 +80,7 @@ __all__ = [
     "chunkwise_backward",
     "short_conv",
     "conv_silu",
+    "gather_rows",
     "lower_bounded_decay",
     "beta_gate",
     "rmsnorm_gate",
@@ -461,3 +469,28 @@ def rmsnorm_gate(x, weight=None, eps=1e-6, gate_logits=None):
     if gate_logits is not None:
         y = y * torch.sigmoid(gate_logits.to(cd)).reshape(x.shape)
     return y
+
+
+def gather_rows(arrays, index=None):
+    """Batch-row gather of every cache tensor: ``out[i] = a[index[i]]``.
+
+    ``arrays`` are numpy arrays (or CPU tensors) sharing dimension 0; the rows
+    are copied one at a time as bytes, so any dtype is exact.  ``index=None``
+    is the clone (every row in order).  Raises ``IndexError`` for an index
+    outside ``[0, batch)``, like ``index_select``.
+    """
+    import numpy as np
+
+    out = []
+    for a in arrays:
+        a = np.ascontiguousarray(a.numpy() if isinstance(a, torch.Tensor) else a)
+        n = a.shape[0]
+        rows = range(n) if index is None else [int(i) for i in index]
+        src = a.reshape(n, -1).view(np.uint8)
+        dst = np.empty((len(rows), src.shape[1]), dtype=np.uint8)
+        for r, i in enumerate(rows):
+            if not 0 <= i < n:
+                raise IndexError(f"index {i} out of range for a batch of {n}")
+            dst[r] = src[i]
+        out.append(dst.view(a.dtype).reshape((len(rows),) + a.shape[1:]))
+    return out
