@@ -20,7 +20,8 @@ Metric: "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s".
 * fused_stages: the kernels around the operator (kda.fused) on the same
                shape, as HBM GB/s (not part of `value`).
 * backward   : the chunkwise backward (all input gradients) on the prefill
-               workload, ms and tokens/s (not part of `value`).
+               workload, ms and tokens/s (not part of `value`), with the
+               oracle's backward on a T=1024 sample as its CPU baseline.
 * cache_reorder: the beam-search reorder of a whole decode cache (8 KDA
                layers at the decode shape) through kda_cache_gather, as HBM
                GB/s, next to the per-tensor index_select it replaces (not part
@@ -242,8 +243,10 @@ def bench_fused(reps=50):
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / reps
         gbs = nbytes / (ms * 1e-3) / 1e9
+        kernel = {"conv_silu_l2norm": "conv_silu_kernel", "decay_and_beta_gates": "gates_kernel",
+                  "rmsnorm_output_gate": "rmsnorm_gate_kernel"}[name]
         res[name] = {"ms": round(ms, 5), "algorithmic_bytes": nbytes, "achieved_gbs": round(gbs, 1),
-                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kernel)}
     return res
 
 
@@ -286,12 +289,16 @@ def bench_backward(reps=10):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
+    per_kernel = [measured_traffic(f"bwd::{k}_kernel") for k in ("prep", "scan", "grad", "pair")]
+    traffic = None if None in per_kernel else sum(per_kernel)
     return {
         "workload": f"chunkwise backward B={P_B} T={P_T} H={P_H} K=V={P_K}, bf16 inputs, f32 arithmetic "
                     "(dq, dk, dv, dg, dbeta, dS0)",
         "ms": round(ms, 4),
         "tokens_per_s": round(P_B * P_T / (ms * 1e-3), 1),
         "workspace_bytes": nbytes,
+        "traffic": traffic,
+        "traffic_gbs": None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1),
     }
 
 
@@ -355,6 +362,7 @@ def bench_cache(layers=8, reps=10):
         "workload": f"reorder of {layers} KDA layers' decode caches, B={B} H={D_H} K=V={D_K} f32 states + "
                     f"3 bf16 ShortConv histories [B,3,{W}] + offsets ({n} tensors), random permutation",
         "algorithmic_bytes": nbytes,
+        "traffic": measured_traffic("cache_gather_kernel"),
         **res,
     }
 
@@ -385,6 +393,11 @@ def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
     qd, kd, vd, gd, bd, _ = workload(decode_sample_b, 1, D_H, D_K, D_V, seed=2)
     sd = torch.randn(decode_sample_b, D_H, D_K, D_V) * 0.02
     t_dec = timed(lambda: ora.recurrent(qd, kd, vd, gd, bd, sd))
+    bwd_t = prefill_sample_t // 2
+    qb, kb, vb, gb, bb, sb = (t.float() for t in workload(1, bwd_t, P_H, P_K, P_V, state_std=0.02, seed=0))
+    gen = torch.Generator().manual_seed(9)
+    d_out, d_final = torch.randn(1, bwd_t, P_H, P_V, generator=gen), torch.randn(1, P_H, P_K, P_V, generator=gen)
+    t_bwd = timed(lambda: ora.chunkwise_backward(qb, kb, vb, gb, bb, sb, d_out, d_final))
     return {
         "prefill": {
             "value": prefill_sample_t / t_pre, "unit": "tokens/s", "cores": threads, "kind": "port",
@@ -395,6 +408,11 @@ def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
             "value": decode_bytes(decode_sample_b, D_H, D_K, D_V) / t_dec / 1e9, "unit": "GB/s", "cores": threads,
             "kind": "port",
             "sample": f"oracle recurrent one step (torch CPU) B={decode_sample_b} H={D_H} K=V=128, "
+                      f"min of {repeats} after 1 warm-up",
+        },
+        "backward": {
+            "value": bwd_t / t_bwd, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"oracle chunkwise_backward (torch CPU, f32) B=1 T={bwd_t} H={P_H} K=V=128, "
                       f"min of {repeats} after 1 warm-up",
         },
     }
@@ -418,7 +436,9 @@ def measured_traffic(kernel):
 def profile_pass():
     """The workload of the counter runs: after one warm-up round, one prefill at
     the benchmark shape, one in-place decode step at the benchmark shape, and a
-    256 MiB device-to-device copy whose byte counts calibrate the counters."""
+    256 MiB device-to-device copy whose byte counts calibrate the counters;
+    then the fused stages, the backward and the cache reorder legs once each
+    (their warm-up calls included)."""
     import torch
 
     import kda
@@ -435,6 +455,9 @@ def profile_pass():
             kda.recurrent_kda(qd, kd, vd, gd, bd, state, True, update_state_in_place=True)
             dst.copy_(src)
     torch.cuda.synchronize()
+    bench_fused(reps=1)
+    bench_backward(reps=1)
+    bench_cache(reps=1)
     print("profile pass done", flush=True)
 
 
@@ -536,6 +559,7 @@ def main() -> int:
         cpu = cpu_baseline()
         result["cpu_baseline"] = cpu["prefill"]
         result["decode"]["cpu_baseline"] = cpu["decode"]
+        result["backward"]["cpu_baseline"] = cpu["backward"]
     print(json.dumps(result), flush=True)
     return 0
 
