@@ -15,10 +15,13 @@ Additive keyword-only extension: ``cu_seqlens`` (packed documents
 
 Gradients: with autograd enabled and an input that requires grad, the call
 goes through ``_ChunkwiseFunction``, whose backward is the HIP chunk backward
-(``kda_chunk_bwd``) for bf16/f16/f32 inputs, key_dim and value_dim <= 128 and
-the dense layout; the attention mask is applied with differentiable tensor
-ops first (src/kda/utils.py:82-94), so padded positions get zero gradients.
-Other cases raise instead of dropping gradients.
+(``kda_chunk_bwd``) for bf16/f16/f32 inputs and key_dim and value_dim <= 128;
+the attention mask is applied with differentiable tensor ops first
+(src/kda/utils.py:82-94), so padded positions get zero gradients.  Packed
+documents (``cu_seqlens``) are differentiated one document at a time: each is
+a dense batch-1 call on its slice of the packed tensors (pointer offsets into
+the same inputs and gradient buffers, one workspace sized for the longest
+document).  Other cases raise instead of dropping gradients.
 """
 
 from __future__ import annotations
@@ -61,10 +64,8 @@ def chunkwise_kda(
     _lib.require_gpu(q)
     work_dtype = accumulation_dtype(v.dtype, accumulate_state_in_fp32)
     if needs_grad(q, k, v, g, beta, initial_state):
-        if offsets is not None:
-            raise RuntimeError("the MI355X KDA backward does not support cu_seqlens; run the documents separately")
         return differentiable(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype,
-                              recurrent=False)
+                              recurrent=False, offsets=offsets)
     return _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype, offsets,
                     batch, tokens, heads, key_dim, value_dim)
 
@@ -107,17 +108,18 @@ def needs_grad(*tensors) -> bool:
 
 
 def differentiable(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype, *,
-                   recurrent: bool) -> KDAOperatorOutput:
+                   recurrent: bool, offsets: list[int] | None = None) -> KDAOperatorOutput:
     """The operator under autograd: masked inputs, the forward of
     ``recurrent_kda`` (recurrent=True) or ``chunkwise_kda``, and the HIP chunk
-    backward, whose gradients are those of the exact recurrence either way."""
+    backward, whose gradients are those of the exact recurrence either way.
+    ``offsets`` are validated packed-document boundaries (or None)."""
     if work_dtype == torch.float64:
         raise RuntimeError("the MI355X KDA backward supports bf16, f16 and f32 inputs (f32 arithmetic)")
     if q.shape[-1] > 128 or v.shape[-1] > 128:
         raise RuntimeError("the MI355X KDA backward supports key_dim and value_dim up to 128")
     qm, gm, bm = _mask_differentiable(q, g, beta, attention_mask)
     hidden, final = _ChunkwiseFunction.apply(qm, k, v, gm, bm, initial_state, output_final_state, work_dtype,
-                                             recurrent)
+                                             recurrent, offsets)
     return KDAOperatorOutput(hidden_states=hidden, final_state=final)
 
 
@@ -136,19 +138,20 @@ class _ChunkwiseFunction(torch.autograd.Function):
     """The operator on masked, dense inputs with the HIP chunk backward."""
 
     @staticmethod
-    def forward(ctx, q, k, v, g, beta, initial_state, output_final_state, work_dtype, recurrent):
+    def forward(ctx, q, k, v, g, beta, initial_state, output_final_state, work_dtype, recurrent, offsets):
         batch, tokens, heads, key_dim = q.shape
         value_dim = v.shape[-1]
         if recurrent:
             from .recurrent import recurrent_kda
 
             out = recurrent_kda(q, k, v, g, beta, initial_state, output_final_state,
-                                accumulate_state_in_fp32=work_dtype != v.dtype)
+                                accumulate_state_in_fp32=work_dtype != v.dtype, cu_seqlens=offsets)
         else:
-            out = _forward(q, k, v, g, beta, initial_state, output_final_state, None, work_dtype, None,
+            out = _forward(q, k, v, g, beta, initial_state, output_final_state, None, work_dtype, offsets,
                            batch, tokens, heads, key_dim, value_dim)
         ctx.save_for_backward(q, k, v, g, beta, initial_state)
         ctx.work_dtype = work_dtype
+        ctx.offsets = offsets
         if out.final_state is None:
             return out.hidden_states, None
         return out.hidden_states, out.final_state
@@ -168,18 +171,35 @@ class _ChunkwiseFunction(torch.autograd.Function):
         ds_t = None if d_final is None else d_final.to(torch.float32).contiguous()
         dq, dk, dv, dg = (torch.empty_like(t) for t in (qc, kc, vc, gc))
         dbeta = torch.empty_like(bc)
+        n_state = batch if ctx.offsets is None else len(ctx.offsets) - 1
         ds0 = None
         if initial_state is not None and ctx.needs_input_grad[5]:
-            ds0 = torch.empty(batch, heads, key_dim, value_dim, dtype=torch.float32, device=device)
-        ws_bytes = lib.kda_chunk_bwd_workspace_bytes(batch, tokens, heads, key_dim, value_dim)
+            ds0 = torch.empty(n_state, heads, key_dim, value_dim, dtype=torch.float32, device=device)
+        # dense: one call over the batch; packed documents: one batch-1 call per
+        # document on its token range [start, end) of the packed tensors
+        if ctx.offsets is None:
+            spans = [(0, 0, tokens, batch)]
+        else:
+            spans = [(i, ctx.offsets[i], ctx.offsets[i + 1], 1) for i in range(n_state)]
+        longest = max(end - start for _, start, end, _ in spans)
+        n_b = spans[0][3]
+        ws_bytes = lib.kda_chunk_bwd_workspace_bytes(n_b, longest, heads, key_dim, value_dim)
         workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
-        status = lib.kda_chunk_bwd(
-            qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr(), bc.data_ptr(), d_out.data_ptr(),
-            _lib.dtype_code(kernel_dtype), _lib.ptr(s0), _lib.ptr(ds_t), dq.data_ptr(), dk.data_ptr(),
-            dv.data_ptr(), dg.data_ptr(), dbeta.data_ptr(), _lib.ptr(ds0), batch, tokens, heads, key_dim,
-            value_dim, workspace.data_ptr(), ws_bytes, _prep.stream(device),
-        )
-        _lib.check(status)
+        code = _lib.dtype_code(kernel_dtype)
+        stream = _prep.stream(device)
+        state_elems = heads * key_dim * value_dim
+
+        def at(t, elems):
+            return None if t is None else t.data_ptr() + elems * t.element_size()
+
+        for i, start, end, n_b in spans:  # documents are non-empty (validate_cu_seqlens)
+            tk, tv, tb, st = start * heads * key_dim, start * heads * value_dim, start * heads, i * state_elems
+            status = lib.kda_chunk_bwd(
+                at(qc, tk), at(kc, tk), at(vc, tv), at(gc, tk), at(bc, tb), at(d_out, tv), code,
+                at(s0, st), at(ds_t, st), at(dq, tk), at(dk, tk), at(dv, tv), at(dg, tk), at(dbeta, tb),
+                at(ds0, st), n_b, end - start, heads, key_dim, value_dim, _lib.ptr(workspace), ws_bytes, stream,
+            )
+            _lib.check(status)
         grads = [dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
                  None if ds0 is None else ds0.to(initial_state.dtype)]
-        return (*[gr if need else None for gr, need in zip(grads, ctx.needs_input_grad[:6])], None, None, None)
+        return (*[gr if need else None for gr, need in zip(grads, ctx.needs_input_grad[:6])], None, None, None, None)

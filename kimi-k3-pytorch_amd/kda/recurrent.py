@@ -64,11 +64,11 @@ def recurrent_kda(
     from .chunkwise import differentiable, needs_grad
 
     if needs_grad(q, k, v, g, beta, initial_state):
-        if offsets is not None or return_states_per_token or update_state_in_place:
-            raise RuntimeError("the MI355X KDA backward supports dense sequences without return_states_per_token "
-                               "or update_state_in_place")
+        if return_states_per_token or update_state_in_place:
+            raise RuntimeError("the MI355X KDA backward supports neither return_states_per_token "
+                               "nor update_state_in_place")
         return differentiable(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype,
-                              recurrent=True)
+                              recurrent=True, offsets=offsets)
     lib = _lib.load()
 
     (qc, kc, vc, gc, bc), kernel_dtype, arith = _prep.kernel_inputs(q, k, v, g, beta, work_dtype)

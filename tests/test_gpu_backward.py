@@ -104,9 +104,37 @@ def test_backward_refuses_unsupported_cases():
     q, k, v, g, beta, s0 = (t.to(DEV) for t in workload(1, 8, 1, 16, 16, state_std=0.1, dtype=torch.float64))
     with pytest.raises(RuntimeError, match="bf16, f16 and f32"):
         kda.chunkwise_kda(q.requires_grad_(), k, v, g, beta, s0)
-    q2, k2, v2, g2, b2, _ = (t.to(DEV) if t is not None else None for t in workload(1, 8, 1, 16, 16))
-    with pytest.raises(RuntimeError, match="cu_seqlens"):
-        kda.chunkwise_kda(q2.requires_grad_(), k2, v2, g2, b2, cu_seqlens=[0, 4, 8])
+    q2, k2, v2, g2, b2, _ = (t.to(DEV) for t in workload(1, 8, 1, 16, 16, state_std=0.1))
+    with pytest.raises(RuntimeError, match="up to 128"):
+        kda.chunkwise_kda(*(t.repeat(1, 1, 1, 9) for t in (q2.requires_grad_(), k2)), v2, g2.repeat(1, 1, 1, 9), b2)
+
+
+@pytest.mark.parametrize("op", ["chunkwise", "recurrent"])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_packed_documents_gradients_match_per_document_oracle(op, dtype):
+    # cu_seqlens under autograd: every document's slice of the gradients (and
+    # its initial-state gradient) equals the oracle's backward of that document
+    lens = [70, 1, 130, 64]
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    H, K, V = 2, 128, 64
+    q, k, v, g, beta, _ = workload(1, cu[-1], H, K, V, state_std=0.5, seed=12, dtype=dtype)
+    gen = torch.Generator().manual_seed(13)
+    s0 = torch.randn(len(lens), H, K, V, generator=gen) * 0.5
+    d_out = torch.randn(1, cu[-1], H, V, generator=gen).to(dtype)
+    d_final = torch.randn(len(lens), H, K, V, generator=gen)
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v, g, beta, s0)]
+    fn = kda.chunkwise_kda if op == "chunkwise" else kda.recurrent_kda
+    res = fn(*leaves, True, cu_seqlens=torch.tensor(cu, dtype=torch.int32))
+    ((res.hidden_states.float() * d_out.to(DEV).float()).sum() + (res.final_state * d_final.to(DEV)).sum()).backward()
+    for i, (a0, a1) in enumerate(zip(cu[:-1], cu[1:])):
+        doc = [t[:, a0:a1] for t in (q, k, v, g, beta)] + [s0[i:i + 1]]
+        ref = _oracle_grads(doc, d_out[:, a0:a1], d_final[i:i + 1])
+        for name, leaf, b in zip(NAMES, leaves, ref):
+            a = leaf.grad[i:i + 1] if name == "ds0" else leaf.grad[:, a0:a1]
+            assert torch.isfinite(a).all(), (name, i)
+            assert rel_err(a, b) < TOL[dtype], (name, i, rel_err(a, b))
 
 
 @pytest.mark.parametrize("regime", ["steep", "rising"])
