@@ -306,6 +306,38 @@ constexpr float kMaxBlockDecay = 80.f;
 
 // True when the chunk needs the exact path; lg in LDS rows of stride kRS,
 // the raw g's sign having been folded into `nonneg` by the caller.
+// lg = cumsum(g) down the chunk's 64 rows for each of the KP channels, in
+// place in lgS (row stride kRS).  Thread (channel tid % KP, quarter tid / KP)
+// sums its quarter's 16 rows in registers, the quarter totals meet in `tmp`
+// (4 x 128 floats), and each quarter adds the totals above it: a chain of 16
+// additions instead of 64 dependent LDS round trips.  Returns whether one of
+// the thread's own g values is positive; ends with the block synchronised.
+template <int KP>
+__device__ __forceinline__ bool chunk_cumsum(float* lgS, float* tmp, int tid) {
+  bool rising = false;
+  float v[16];
+  const int c = tid % KP, p = tid / KP;
+  if (p < 4) {
+#pragma unroll
+    for (int r = 0; r < 16; ++r) v[r] = lgS[(16 * p + r) * kRS + c];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      rising |= v[r] > 0.f;
+      if (r > 0) v[r] += v[r - 1];
+    }
+    tmp[p * 128 + c] = v[15];
+  }
+  __syncthreads();
+  if (p < 4) {
+    float off = 0.f;
+    for (int q = 0; q < p; ++q) off += tmp[q * 128 + c];
+#pragma unroll
+    for (int r = 0; r < 16; ++r) lgS[(16 * p + r) * kRS + c] = v[r] + off;
+  }
+  __syncthreads();
+  return rising;
+}
+
 template <int KP, int NT>
 __device__ __forceinline__ bool needs_exact(const float* lgS, bool nonneg, int tid) {
   bool risky = nonneg;
@@ -374,17 +406,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     AqkS[idx] = 0.f;
   }
   __syncthreads();
-  bool rising = false;
-  if (tid < Kp) {  // lg = cumsum(g) down the chunk
-    float s = 0.f;
-    for (int r = 0; r < kC; ++r) {
-      const float gv = lgS[r * kRS + tid];
-      rising |= gv > 0.f;
-      s += gv;
-      lgS[r * kRS + tid] = s;
-    }
-  }
-  __syncthreads();
+  const bool rising = chunk_cumsum<KP>(lgS, NS, tid);  // N is formed later
   if (!needs_exact<KP, kPT>(lgS, rising, tid)) {
     // A and Aqk block by block on the MFMA
     for (int p = w; p < 10; p += kPT / 64) {
@@ -1377,17 +1399,7 @@ __global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
   load_ws<kC, kC, kRC, NT>(dAS, ws + a.L.dA, kC, 0, tid);
   load_ws<kC, kC, kRC, NT>(dQS, ws + a.L.dAqk, kC, 0, tid);
   __syncthreads();
-  bool rising = false;
-  if (tid < Kp) {
-    float s = 0.f;
-    for (int r = 0; r < kC; ++r) {
-      const float gv = lgS[r * kRS + tid];
-      rising |= gv > 0.f;
-      s += gv;
-      lgS[r * kRS + tid] = s;
-    }
-  }
-  __syncthreads();
+  const bool rising = chunk_cumsum<KP>(lgS, red, tid);  // red is written later
   int nred;
   if (!needs_exact<KP, NT>(lgS, rising, tid)) {
     pair_mfma<IT, KP>(a, ws, kS, qS, lgS, dAS, dQS, red, b, h, t0, tid);
@@ -1397,14 +1409,24 @@ __global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
     nred = kC / (kC * KP / NT);
   }
   __syncthreads();
-  if (tid < Kp) {
-    const float last = lgS[(kC - 1) * kRS + tid];
-    float run = fast_exp(last) * ws[a.L.dD + tid];
-    for (int p = 0; p < nred; ++p) run += red[p * 128 + tid];
-    for (int i = kC - 1; i >= 0; --i) {
-      run += qS[i * kRS + tid];
-      const int64_t t = t0 + i;
-      if (t < a.T && tid < a.K) a.dg[tok(b, t, a.T, a.H, h) * a.K + tid] = from_compute<IT>(run);
+  {  // dg = reverse cumulative sum of d lg, by quarters of 16 rows (totals through kS)
+    const int cc = tid % KP, p = tid / KP;
+    float v[16];
+    if (p < 4) {
+#pragma unroll
+      for (int r = 15; r >= 0; --r) v[r] = qS[(16 * p + r) * kRS + cc] + (r < 15 ? v[r + 1] : 0.f);
+      kS[p * 128 + cc] = v[0];
+    }
+    __syncthreads();
+    if (p < 4) {
+      float run = fast_exp(lgS[(kC - 1) * kRS + cc]) * ws[a.L.dD + cc];
+      for (int q = 0; q < nred; ++q) run += red[q * 128 + cc];
+      for (int q = p + 1; q < 4; ++q) run += kS[q * 128 + cc];
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int64_t t = t0 + 16 * p + r;
+        if (t < a.T && cc < a.K) a.dg[tok(b, t, a.T, a.H, h) * a.K + cc] = from_compute<IT>(v[r] + run);
+      }
     }
   }
 }
