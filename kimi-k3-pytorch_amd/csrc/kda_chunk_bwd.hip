@@ -1105,9 +1105,13 @@ __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
       DN[row * kRC + col] = aM[j][r] * bS[col];
     }
   __syncthreads();
+  // dbeta_j = sum_i N_ij dM_ij + sum_k dL_jk A_jk: thread (j = tid / 8, p = tid % 8)
+  // takes rows i = p, p + 8, .. of the first sum and columns 8p .. 8p + 7 of
+  // the second; the eight parts of j are neighbouring lanes of one wave
+  const int bj = tid >> 3, bp = tid & 7;
   float db = 0.f;
-  if (tid < kC)
-    for (int r = 0; r < kC; ++r) db += NS[r * kRC + tid] * DM[r * kRC + tid];
+#pragma unroll
+  for (int i = bp; i < kC; i += 8) db += NS[i * kRC + bj] * DM[i * kRC + bj];
   f32x4 t1[2];
 #pragma unroll
   for (int j = 0; j < 2; ++j)
@@ -1131,9 +1135,16 @@ __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
     }
   }
   __syncthreads();
-  if (tid < kC) {
-    for (int j = 0; j < kC; ++j) db += DN[tid * kRC + j] * AS[tid * kRC + j];
-    const int64_t t = t0 + tid;
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(&DN[bj * kRC + 8 * bp + 4 * u]);
+    const f32x4 y = *reinterpret_cast<const f32x4*>(&AS[bj * kRC + 8 * bp + 4 * u]);
+    db += x[0] * y[0] + x[1] * y[1] + x[2] * y[2] + x[3] * y[3];
+  }
+#pragma unroll
+  for (int m = 1; m < 8; m <<= 1) db += __shfl_xor(db, m);
+  if (bp == 0) {
+    const int64_t t = t0 + bj;
     if (t < a.T) a.dbeta[tok(b, t, a.T, a.H, h)] = from_compute<IT>(db);
   }
 }
