@@ -150,13 +150,15 @@ int kda_ut_transform(const void* k, const void* v, const void* g, const void* be
  * (src/kda/chunkwise.py:17-107; its gradients are pinned by
  * tests/kda/test_kda_chunkwise_equivalence.py:92-134).
  *   q, k, g [batch, tokens, heads, key_dim]; v, d_out [batch, tokens, heads, value_dim];
- *   beta [batch, tokens, heads]: dtype bf16, f16 or f32 (inputs already masked);
- *   initial_state, d_final_state : f32 [batch, heads, key_dim, value_dim] or NULL (zero)
+ *   beta [batch, tokens, heads]: dtype bf16, f16, f32 or f64 (inputs already masked);
+ *   initial_state, d_final_state : f32 [batch, heads, key_dim, value_dim] or NULL (zero);
+ *                                  f64 (passed through these pointers) when dtype is f64
  *   dq, dk, dv, dg, dbeta        : outputs, shaped and typed like the inputs
- *   d_initial_state              : f32 [batch, heads, key_dim, value_dim] or NULL
- *   key_dim, value_dim <= 128; dense layout (no packed documents).
- * Arithmetic is f32 throughout.  The workspace (kda_chunk_bwd_workspace_bytes,
- * 16-byte aligned) holds per-chunk intermediates and is fully rewritten.
+ *   d_initial_state              : like initial_state, or NULL
+ *   key_dim, value_dim <= 128; dense layout (packed documents: one call per document).
+ * Arithmetic is f32 for bf16/f16/f32 inputs and f64 for f64 inputs.  The workspace
+ * (kda_chunk_bwd_workspace_bytes, any dtype, 16-byte aligned) holds per-chunk
+ * intermediates and is fully rewritten.
  */
 size_t kda_chunk_bwd_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim,
                                      int64_t value_dim);

@@ -239,9 +239,10 @@ int kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g, co
                   void* dg, void* dbeta, float* d_initial_state, int64_t batch, int64_t tokens, int64_t heads,
                   int64_t key_dim, int64_t value_dim, void* workspace, size_t workspace_bytes, void* stream) {
   g_detail[0] = '\0';
-  if (in_dtype != KDA_DTYPE_BF16 && in_dtype != KDA_DTYPE_F16 && in_dtype != KDA_DTYPE_F32) {
-    set_detail("chunk_bwd: inputs must be bf16, f16 or f32 (dtype %d)", in_dtype);
-    return in_dtype == KDA_DTYPE_F64 ? KDA_ERR_UNSUPPORTED : KDA_ERR_INVALID_ARGUMENT;
+  if (in_dtype != KDA_DTYPE_BF16 && in_dtype != KDA_DTYPE_F16 && in_dtype != KDA_DTYPE_F32 &&
+      in_dtype != KDA_DTYPE_F64) {
+    set_detail("chunk_bwd: inputs must be bf16, f16, f32 or f64 (dtype %d)", in_dtype);
+    return KDA_ERR_INVALID_ARGUMENT;
   }
   if (batch <= 0 || tokens <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) {
     set_detail("chunk_bwd: sizes must be positive");

@@ -1452,7 +1452,9 @@ using namespace kda;
 size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
   const bwd::Layout L = bwd::make_layout(K, V);
   const int64_t nc = (T + bwd::kC - 1) / bwd::kC;
-  return static_cast<size_t>(B * H * nc * L.per) * sizeof(float);
+  const size_t f32 = static_cast<size_t>(B * H * nc * L.per) * sizeof(float);
+  const size_t f64 = chunk_bwd_f64_workspace_bytes(B, T, H, K, V);  // one size serves every dtype
+  return f32 > f64 ? f32 : f64;
 }
 
 template <class IT, int KP>
@@ -1496,6 +1498,14 @@ int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
     set_detail("chunk backward: workspace must be 16-byte aligned");
     return KDA_ERR_INVALID_ARGUMENT;
   }
+  if (in_dtype == KDA_DTYPE_F64)  // f64 arithmetic throughout (kda_chunk_bwd_f64.hip); states are f64 too
+    return launch_chunk_bwd_f64(static_cast<const double*>(q), static_cast<const double*>(k),
+                                static_cast<const double*>(v), static_cast<const double*>(g),
+                                static_cast<const double*>(beta), static_cast<const double*>(dout),
+                                reinterpret_cast<const double*>(s0), reinterpret_cast<const double*>(dsT),
+                                static_cast<double*>(dq), static_cast<double*>(dk), static_cast<double*>(dv),
+                                static_cast<double*>(dg), static_cast<double*>(dbeta), reinterpret_cast<double*>(ds0),
+                                B, T, H, K, V, static_cast<double*>(workspace), stream);
   const bwd::Layout L = bwd::make_layout(K, V);
   const int64_t NC = (T + bwd::kC - 1) / bwd::kC;
   float* ws = static_cast<float*>(workspace);

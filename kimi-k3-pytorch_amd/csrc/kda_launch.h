@@ -44,6 +44,14 @@ int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
                      void* dg, void* dbeta, float* ds0, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
                      void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+// The same backward in f64 arithmetic (csrc/kda_chunk_bwd_f64.hip).
+size_t chunk_bwd_f64_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
+
+int launch_chunk_bwd_f64(const double* q, const double* k, const double* v, const double* g, const double* beta,
+                         const double* dout, const double* s0, const double* dsT, double* dq, double* dk, double* dv,
+                         double* dg, double* dbeta, double* ds0, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
+                         double* ws, hipStream_t stream);
+
 // Fused stages around the operator (csrc/kda_fused.hip).
 int launch_conv_silu(const void* x, const void* w, const void* bias, const void* hist_in, void* y, void* hist_out,
                      const int32_t* valid_lens, int64_t B, int64_t T, int64_t C, int64_t K, int64_t head_dim,

@@ -15,7 +15,8 @@ Additive keyword-only extension: ``cu_seqlens`` (packed documents
 
 Gradients: with autograd enabled and an input that requires grad, the call
 goes through ``_ChunkwiseFunction``, whose backward is the HIP chunk backward
-(``kda_chunk_bwd``) for bf16/f16/f32 inputs and key_dim and value_dim <= 128;
+(``kda_chunk_bwd``: f32 arithmetic for bf16/f16/f32 inputs, f64 for f64
+inputs) with key_dim and value_dim <= 128;
 the attention mask is applied with differentiable tensor ops first
 (src/kda/utils.py:82-94), so padded positions get zero gradients.  Packed
 documents (``cu_seqlens``) are differentiated one document at a time: each is
@@ -113,8 +114,6 @@ def differentiable(q, k, v, g, beta, initial_state, output_final_state, attentio
     ``recurrent_kda`` (recurrent=True) or ``chunkwise_kda``, and the HIP chunk
     backward, whose gradients are those of the exact recurrence either way.
     ``offsets`` are validated packed-document boundaries (or None)."""
-    if work_dtype == torch.float64:
-        raise RuntimeError("the MI355X KDA backward supports bf16, f16 and f32 inputs (f32 arithmetic)")
     if q.shape[-1] > 128 or v.shape[-1] > 128:
         raise RuntimeError("the MI355X KDA backward supports key_dim and value_dim up to 128")
     qm, gm, bm = _mask_differentiable(q, g, beta, attention_mask)
@@ -167,14 +166,15 @@ class _ChunkwiseFunction(torch.autograd.Function):
         if d_hidden is None:
             d_hidden = torch.zeros(batch, tokens, heads, value_dim, dtype=kernel_dtype, device=device)
         d_out = d_hidden.to(kernel_dtype).contiguous()
-        s0 = None if initial_state is None else initial_state.detach().to(torch.float32).contiguous()
-        ds_t = None if d_final is None else d_final.to(torch.float32).contiguous()
+        state_dtype = torch.float64 if kernel_dtype == torch.float64 else torch.float32
+        s0 = None if initial_state is None else initial_state.detach().to(state_dtype).contiguous()
+        ds_t = None if d_final is None else d_final.to(state_dtype).contiguous()
         dq, dk, dv, dg = (torch.empty_like(t) for t in (qc, kc, vc, gc))
         dbeta = torch.empty_like(bc)
         n_state = batch if ctx.offsets is None else len(ctx.offsets) - 1
         ds0 = None
         if initial_state is not None and ctx.needs_input_grad[5]:
-            ds0 = torch.empty(n_state, heads, key_dim, value_dim, dtype=torch.float32, device=device)
+            ds0 = torch.empty(n_state, heads, key_dim, value_dim, dtype=state_dtype, device=device)
         # dense: one call over the batch; packed documents: one batch-1 call per
         # document on its token range [start, end) of the packed tensors
         if ctx.offsets is None:

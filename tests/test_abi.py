@@ -111,7 +111,8 @@ def test_backward_entry_point_rejects_bad_arguments():
     def call(dtype=bf16, K=128, V=128, ws=None, ws_bytes=0, dq=a):
         return lib.kda_chunk_bwd(*ptrs, dtype, None, None, dq, a, a, a, a, None, 1, 64, 1, K, V, ws, ws_bytes, None)
 
-    assert call(dtype=f64) == _lib.KDA_ERR_UNSUPPORTED
+    assert call(dtype=f64) == _lib.KDA_ERR_WORKSPACE  # f64 is computed in f64; no workspace given
+    assert call(dtype=7) == _lib.KDA_ERR_INVALID_ARGUMENT
     assert call(K=256) == _lib.KDA_ERR_UNSUPPORTED
     assert call(dq=None) == _lib.KDA_ERR_INVALID_ARGUMENT
     assert call() == _lib.KDA_ERR_WORKSPACE  # no workspace

@@ -4,7 +4,8 @@ itself pinned against autograd through the oracle's forward.
 
 Tolerances (max|x - ref| / max|ref| per gradient): f32 inputs 2e-4 (f32
 arithmetic against the f64 oracle on the same values), bf16 inputs 2e-2
-(gradients computed in f32 and rounded once to bf16).
+(gradients computed in f32 and rounded once to bf16), f64 inputs 1e-10 (f64
+arithmetic in another order).
 """
 
 from __future__ import annotations
@@ -33,9 +34,9 @@ def _case(B, T, H, K, V, dtype, seed):
 def _gpu_grads(inputs, d_out, d_final, mask=None, final=True):
     leaves = [t.to(DEV).requires_grad_() for t in inputs]
     res = kda.chunkwise_kda(*leaves, final, None if mask is None else mask.to(DEV))
-    loss = (res.hidden_states.float() * d_out.to(DEV).float()).sum()
+    loss = (res.hidden_states.double() * d_out.to(DEV).double()).sum()
     if final:
-        loss = loss + (res.final_state * d_final.to(DEV)).sum()
+        loss = loss + (res.final_state.double() * d_final.to(DEV).double()).sum()
     loss.backward()
     return [t.grad for t in leaves]
 
@@ -100,10 +101,48 @@ def test_backward_long_context_heads_subset():
             assert rel_err(a_h, b) < TOL[torch.bfloat16], (name, h, rel_err(a_h, b))
 
 
+@pytest.mark.parametrize("B,T,H,K,V", [(1, 5, 2, 2, 3), (2, 130, 2, 128, 128), (1, 70, 1, 100, 40)])
+def test_f64_backward_matches_oracle(B, T, H, K, V):
+    # f64 inputs differentiate in f64 arithmetic (kda_chunk_bwd_f64.hip)
+    inputs, d_out, d_final = _case(B, T, H, K, V, torch.float64, seed=T + 1)
+    inputs = tuple(t.double() for t in inputs)  # the initial state too
+    got = _gpu_grads(inputs, d_out, d_final.double())
+    ref = _oracle_grads(inputs, d_out, d_final)
+    for name, a, b in zip(NAMES, got, ref):
+        assert a.dtype == torch.float64, name
+        assert rel_err(a, b) < 1e-10, (name, rel_err(a, b))
+
+
+@pytest.mark.parametrize("op", ["chunkwise", "recurrent"])
+def test_f64_gradcheck_like_the_reference(op):
+    # tests/kda/test_kda_chunkwise_equivalence.py:115-134 and
+    # tests/kda/test_kda_recurrent.py:184-193 (gradcheck; the second derivative
+    # of gradgradcheck is not provided by this backend)
+    inputs, _, _ = _case(1, 3, 1, 2, 2, torch.float64, seed=21)
+    leaves = tuple(t.double().to(DEV).requires_grad_() for t in inputs)
+    fn = kda.chunkwise_kda if op == "chunkwise" else kda.recurrent_kda
+
+    def function(*xs):
+        res = fn(*xs, True)
+        return res.hidden_states, res.final_state
+
+    assert torch.autograd.gradcheck(function, leaves, fast_mode=True)
+
+
+def test_recurrent_and_chunkwise_f64_gradients_agree():
+    # tests/kda/test_kda_chunkwise_equivalence.py:92-112: rtol 2e-10, atol 2e-11
+    inputs, _, _ = _case(1, 5, 2, 2, 3, torch.float64, seed=22)
+    rec = [t.double().to(DEV).requires_grad_() for t in inputs]
+    chk = [t.double().to(DEV).requires_grad_() for t in inputs]
+    r = kda.recurrent_kda(*rec, output_final_state=True)
+    c = kda.chunkwise_kda(*chk, output_final_state=True, chunk_size=3, secondary_tile_size=2)
+    (r.hidden_states.square().sum() + r.final_state.square().sum()).backward()
+    (c.hidden_states.square().sum() + c.final_state.square().sum()).backward()
+    for a, b in zip(rec, chk):
+        torch.testing.assert_close(a.grad, b.grad, rtol=2e-10, atol=2e-11)
+
+
 def test_backward_refuses_unsupported_cases():
-    q, k, v, g, beta, s0 = (t.to(DEV) for t in workload(1, 8, 1, 16, 16, state_std=0.1, dtype=torch.float64))
-    with pytest.raises(RuntimeError, match="bf16, f16 and f32"):
-        kda.chunkwise_kda(q.requires_grad_(), k, v, g, beta, s0)
     q2, k2, v2, g2, b2, _ = (t.to(DEV) for t in workload(1, 8, 1, 16, 16, state_std=0.1))
     with pytest.raises(RuntimeError, match="up to 128"):
         kda.chunkwise_kda(*(t.repeat(1, 1, 1, 9) for t in (q2.requires_grad_(), k2)), v2, g2.repeat(1, 1, 1, 9), b2)
