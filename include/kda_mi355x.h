@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 5
+#define KDA_ABI_VERSION 6
 
 /* status codes */
 #define KDA_OK 0
@@ -222,6 +222,29 @@ int kda_gates_fwd(const void* decay_logits, const void* decay_bias, const float*
 int kda_rmsnorm_gate_fwd(const void* x, const void* weight, int weight_per_head,
                          const void* gate_logits, void* y, int64_t rows, int64_t heads,
                          int64_t head_dim, double eps, int dtype, void* stream);
+
+
+/*
+ * Backward of the token recurrence that returns its per-token states: the
+ * autograd of recurrent_kda(..., return_states_per_token=True)
+ * (src/kda/recurrent.py:61-79), where every intermediate state may carry a gradient.
+ *   q, k, g [batch, tokens, heads, key_dim]; v, d_out [batch, tokens, heads, value_dim];
+ *   beta [batch, tokens, heads]: all of dtype f32 or f64 (the work type), masked already
+ *   initial_state, d_final_state : [batch, heads, key_dim, value_dim] or NULL (zero)
+ *   states, d_states             : the forward's per-token states [tokens, batch, heads,
+ *                                  key_dim, value_dim] and their gradient (or NULL)
+ *   dq, dk, dv, dg, dbeta        : outputs shaped like the inputs; d_initial_state or NULL
+ * One workgroup per (batch, head), serial over the tokens: a debugging path.
+ * Workspace: kda_recurrent_bwd_workspace_bytes(batch, heads, key_dim, value_dim, dtype).
+ */
+size_t kda_recurrent_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t key_dim, int64_t value_dim,
+                                         int dtype);
+
+int kda_recurrent_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                      const void* d_out, const void* initial_state, const void* states, const void* d_states,
+                      const void* d_final_state, void* dq, void* dk, void* dv, void* dg, void* dbeta,
+                      void* d_initial_state, int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim,
+                      int64_t value_dim, int dtype, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Cache plumbing for serving: out_t[i, ...] = src_t[index[i], ...] for every tensor t of a

@@ -339,4 +339,29 @@ int kda_cache_gather(const void* const* src, void* const* dst, const int64_t* ro
                              static_cast<hipStream_t>(stream));
 }
 
+size_t kda_recurrent_bwd_workspace_bytes(int64_t batch, int64_t heads, int64_t key_dim, int64_t value_dim,
+                                         int dtype) {
+  if (batch <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) return 0;
+  return recurrent_bwd_workspace_bytes(batch, heads, key_dim, value_dim, dtype);
+}
+
+int kda_recurrent_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                      const void* d_out, const void* initial_state, const void* states, const void* d_states,
+                      const void* d_final_state, void* dq, void* dk, void* dv, void* dg, void* dbeta,
+                      void* d_initial_state, int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim,
+                      int64_t value_dim, int dtype, void* workspace, size_t workspace_bytes, void* stream) {
+  g_detail[0] = '\0';
+  if (batch <= 0 || tokens <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) {
+    set_detail("recurrent_bwd: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!q || !k || !v || !g || !beta || !d_out || !states || !dq || !dk || !dv || !dg || !dbeta) {
+    set_detail("recurrent_bwd: inputs, d_out, the states and the input gradients must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return launch_recurrent_bwd(q, k, v, g, beta, d_out, initial_state, states, d_states, d_final_state, dq, dk, dv, dg,
+                              dbeta, d_initial_state, batch, tokens, heads, key_dim, value_dim, dtype, workspace,
+                              workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
 }  // extern "C"

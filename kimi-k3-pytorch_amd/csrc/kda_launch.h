@@ -52,6 +52,14 @@ int launch_chunk_bwd_f64(const double* q, const double* k, const double* v, cons
                          double* dg, double* dbeta, double* ds0, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
                          double* ws, hipStream_t stream);
 
+// Backward of the token recurrence with per-token states (csrc/kda_recurrent_bwd.hip).
+size_t recurrent_bwd_workspace_bytes(int64_t B, int64_t H, int64_t K, int64_t V, int dtype);
+
+int launch_recurrent_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                         const void* dout, const void* s0, const void* hist, const void* dhist, const void* dsT,
+                         void* dq, void* dk, void* dv, void* dg, void* dbeta, void* ds0, int64_t B, int64_t T,
+                         int64_t H, int64_t K, int64_t V, int dtype, void* ws, size_t ws_bytes, hipStream_t stream);
+
 // Fused stages around the operator (csrc/kda_fused.hip).
 int launch_conv_silu(const void* x, const void* w, const void* bias, const void* hist_in, void* y, void* hist_out,
                      const int32_t* valid_lens, int64_t B, int64_t T, int64_t C, int64_t K, int64_t head_dim,

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libkda_mi355x.so")
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 KDA_OK = 0
 KDA_ERR_INVALID_ARGUMENT = 1
@@ -67,6 +67,8 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _P, _S, _P],
     ),
     "kda_cache_gather": (_I, [_P, _P, _P, _I, _P, _L, _L, _P, _P]),
+    "kda_recurrent_bwd_workspace_bytes": (_S, [_L, _L, _L, _L, _I]),
+    "kda_recurrent_bwd": (_I, [_P] * 16 + [_L] * 5 + [_I, _P, _S, _P]),
 }
 
 _lock = threading.Lock()

@@ -64,9 +64,16 @@ def recurrent_kda(
     from .chunkwise import differentiable, needs_grad
 
     if needs_grad(q, k, v, g, beta, initial_state):
-        if return_states_per_token or update_state_in_place:
-            raise RuntimeError("the MI355X KDA backward supports neither return_states_per_token "
-                               "nor update_state_in_place")
+        if update_state_in_place:
+            raise RuntimeError("the MI355X KDA backward does not support update_state_in_place")
+        if return_states_per_token:
+            from .chunkwise import _mask_differentiable
+
+            qm, gm, bm = _mask_differentiable(q, g, beta, attention_mask)
+            hidden, final, hist = _RecurrentStatesFunction.apply(qm, k, v, gm, bm, initial_state, output_final_state,
+                                                                 work_dtype)
+            return KDAOperatorOutput(hidden_states=hidden, final_state=final if output_final_state else None,
+                                     states_per_token=tuple(hist.unbind(0)))
         return differentiable(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype,
                               recurrent=True, offsets=offsets)
     lib = _lib.load()
@@ -124,3 +131,47 @@ def recurrent_kda(
     if hist is not None:
         states = tuple(x if x.dtype == work_dtype else x.to(work_dtype) for x in hist.unbind(0))
     return KDAOperatorOutput(hidden_states=hidden, final_state=final, states_per_token=states)
+
+
+class _RecurrentStatesFunction(torch.autograd.Function):
+    """``recurrent_kda`` with its per-token states under autograd: the recurrent
+    kernel forward, and ``kda_recurrent_bwd`` (a token-by-token backward in the
+    work dtype that takes a gradient for every returned state)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, initial_state, output_final_state, work_dtype):
+        out = recurrent_kda(q, k, v, g, beta, initial_state, output_final_state, return_states_per_token=True,
+                            accumulate_state_in_fp32=work_dtype != v.dtype)
+        hist = torch.stack(out.states_per_token)
+        ctx.save_for_backward(q, k, v, g, beta, initial_state, hist)
+        return out.hidden_states, out.final_state, hist
+
+    @staticmethod
+    def backward(ctx, d_hidden, d_final, d_hist):
+        q, k, v, g, beta, initial_state, hist = ctx.saved_tensors
+        lib = _lib.load()
+        batch, tokens, heads, key_dim = q.shape
+        value_dim = v.shape[-1]
+        device = q.device
+        arith = torch.float64 if hist.dtype == torch.float64 else torch.float32
+        cast = lambda t: None if t is None else t.detach().to(arith).contiguous()  # noqa: E731
+        qa, ka, va, ga, ba, s0, ha, dha, dfa = (cast(t) for t in (q, k, v, g, beta, initial_state, hist, d_hist,
+                                                                  d_final))
+        if d_hidden is None:
+            d_hidden = torch.zeros(batch, tokens, heads, value_dim, dtype=arith, device=device)
+        do = cast(d_hidden)
+        dq, dk, dg = (torch.empty_like(qa) for _ in range(3))
+        dv, dbeta = torch.empty_like(va), torch.empty_like(ba)
+        ds0 = torch.empty_like(s0) if s0 is not None and ctx.needs_input_grad[5] else None
+        code = _lib.dtype_code(arith)
+        ws_bytes = lib.kda_recurrent_bwd_workspace_bytes(batch, heads, key_dim, value_dim, code)
+        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        _lib.check(lib.kda_recurrent_bwd(
+            qa.data_ptr(), ka.data_ptr(), va.data_ptr(), ga.data_ptr(), ba.data_ptr(), do.data_ptr(), _lib.ptr(s0),
+            ha.data_ptr(), _lib.ptr(dha), _lib.ptr(dfa), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(),
+            dbeta.data_ptr(), _lib.ptr(ds0), batch, tokens, heads, key_dim, value_dim, code, workspace.data_ptr(),
+            ws_bytes, _prep.stream(device),
+        ))
+        grads = [dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
+                 None if ds0 is None else ds0.to(initial_state.dtype)]
+        return (*[gr if need else None for gr, need in zip(grads, ctx.needs_input_grad[:6])], None, None)

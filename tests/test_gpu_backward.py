@@ -207,8 +207,8 @@ def test_recurrent_kda_gradients_match_oracle():
     ref = _oracle_grads(inputs, d_out, d_final)
     for name, a, b in zip(NAMES, [t.grad for t in leaves], ref):
         assert rel_err(a, b) < TOL[torch.float32], name
-    with pytest.raises(RuntimeError, match="return_states_per_token"):
-        kda.recurrent_kda(*leaves, True, return_states_per_token=True)
+    with pytest.raises(RuntimeError, match="update_state_in_place"):
+        kda.recurrent_kda(*leaves, True, update_state_in_place=True)
 
 
 def test_decode_step_gradients():

@@ -151,3 +151,41 @@ def test_ut_transform_matches_oracle():
     assert rel_err(got.U.transpose(1, 2), ref["U"]) < 1e-10
     assert rel_err(got.log_gamma.transpose(1, 2), ref["log_gamma"]) < 1e-12
     assert rel_err(got.k_gamma.transpose(1, 2), ref["k_gamma"]) < 1e-10
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-10), (torch.float32, 1e-4)])
+def test_states_per_token_gradients_match_oracle_autograd(dtype, tol):
+    # recurrent_kda(return_states_per_token=True) under autograd: every returned
+    # state carries a gradient (kda_recurrent_bwd); the oracle's token loop,
+    # differentiated by torch autograd in f64 on the CPU, is the reference
+    q, k, v, g, beta, state = random_core(batch=2, tokens=6, heads=2, key_dim=3, value_dim=4)
+    mask = torch.tensor([[True] * 6, [True] * 4 + [False] * 2])
+    gen = torch.Generator().manual_seed(5)
+    d_out = torch.randn(2, 6, 2, 4, generator=gen, dtype=torch.float64)
+    d_states = [torch.randn(2, 2, 3, 4, generator=gen, dtype=torch.float64) for _ in range(6)]
+    d_final = torch.randn(2, 2, 3, 4, generator=gen, dtype=torch.float64)
+
+    def loss(out, final, states):
+        total = (out.double() * d_out.to(out.device)).sum() + (final.double() * d_final.to(out.device)).sum()
+        return total + sum((s.double() * d.to(out.device)).sum() for s, d in zip(states, d_states))
+
+    ref_leaves = [t.clone().requires_grad_() for t in (q, k, v, g, beta, state)]
+    ro, rs, rh = ora.recurrent(*ref_leaves, mask, return_states=True)
+    loss(ro, rs, rh).backward()
+    leaves = [t.to(dtype).to(DEV).requires_grad_() for t in (q, k, v, g, beta, state)]
+    got = kda.recurrent_kda(*leaves, True, mask.to(DEV), return_states_per_token=True)
+    loss(got.hidden_states, got.final_state, got.states_per_token).backward()
+    for name, a, b in zip(("dq", "dk", "dv", "dg", "dbeta", "ds0"), leaves, ref_leaves):
+        assert a.grad.dtype == dtype, name
+        assert rel_err(a.grad, b.grad) < tol, (name, rel_err(a.grad, b.grad))
+
+
+def test_states_per_token_gradcheck():
+    q, k, v, g, beta, state = random_core(batch=1, tokens=3, heads=1, key_dim=2, value_dim=2)
+    leaves = tuple(t.to(DEV).requires_grad_() for t in (q, k, v, g, beta, state))
+
+    def function(*xs):
+        res = kda.recurrent_kda(*xs, True, return_states_per_token=True)
+        return (res.hidden_states, res.final_state, *res.states_per_token)
+
+    assert torch.autograd.gradcheck(function, leaves, fast_mode=True)
