@@ -120,3 +120,24 @@ def test_backward_entry_point_rejects_bad_arguments():
     assert need > 0 and call(ws=a, ws_bytes=need - 1) == _lib.KDA_ERR_WORKSPACE
     assert call(ws=a + 4, ws_bytes=need) == _lib.KDA_ERR_INVALID_ARGUMENT  # misaligned workspace
     assert lib.kda_chunk_bwd_workspace_bytes(0, 64, 1, 128, 128) == 0
+
+
+def test_recurrent_backward_entry_point_rejects_bad_arguments():
+    # host-side checks only: nothing is launched
+    lib = _lib.load()
+    import torch
+
+    f32, bf16 = _lib.dtype_code(torch.float32), _lib.dtype_code(torch.bfloat16)
+    a = 4096
+
+    def call(dtype=f32, states=a, ws=None, ws_bytes=0, tokens=4):
+        return lib.kda_recurrent_bwd(a, a, a, a, a, a, None, states, None, None, a, a, a, a, a, None,
+                                     1, tokens, 2, 16, 16, dtype, ws, ws_bytes, None)
+
+    assert call(dtype=bf16) == _lib.KDA_ERR_INVALID_ARGUMENT  # the work type only: f32 or f64
+    assert call(states=None) == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call(tokens=0) == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert call() == _lib.KDA_ERR_WORKSPACE
+    need = lib.kda_recurrent_bwd_workspace_bytes(1, 2, 16, 16, f32)
+    assert need > 0 and call(ws=a, ws_bytes=need - 1) == _lib.KDA_ERR_WORKSPACE
+    assert lib.kda_recurrent_bwd_workspace_bytes(1, 2, 16, 16, _lib.dtype_code(torch.float64)) == 2 * need
