@@ -11,9 +11,16 @@ Metric: "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s".
 * decode     : the memory-bound decode step at B=256, H=32, K=V=128 with the
                512 MiB f32 state updated in place for 64 consecutive steps,
                reported as algorithmic HBM GB/s.
-* roofline   : the dominant kernel of the prefill (per-kernel HIP-event
-               timing) and the decode kernel, against MI355X peaks
-               (HBM 8 TB/s, dense bf16 MFMA 2.5 PFLOP/s).
+* roofline   : the prefill's compulsory HBM bytes (q, k, g, v, beta read,
+               output written, f32 initial and final state: 170.13 MB at
+               this shape) over the dominant kernel's time (per-kernel HIP
+               events on the launch stream), against the MI355X HBM peak
+               (8 TB/s); `roofline_operator` gives the same bytes over the
+               whole operator's time, and the chunk GEMM flops against the
+               dense bf16 MFMA peak (2.5 PFLOP/s).
+* dropin     : the same prefill and decode through the Python drop-in API
+               (kda.chunkwise_kda / kda.recurrent_kda with its validation,
+               casts and per-call allocations), not only the C ABI.
 * cpu_baseline: the oracle's PyTorch-CPU restatement of the reference path
                (oracle/kda_oracle.py) on a bounded sample of the same
                workload, on the host cores (thread count reported).
@@ -67,31 +74,6 @@ def prefill_bytes(B, T, H, K, V, n_state_io=2):
 def prefill_flops(B, T, H, K, V, C=64):
     """Causal-counted chunk GEMM flops: 6KV + (3C+1)K + 2(C+1)V per token per head."""
     return B * T * H * (6 * K * V + (3 * C + 1) * K + 2 * (C + 1) * V)
-
-
-SEGMENT_CHUNKS = 8  # chunks per segment the library picks for the long-context workload on 256 CUs
-MA_BYTES = 12 * 1024  # each chunk's M and Aqk fragments handed from the summary pass to the output pass
-
-
-def summary_bytes(B, T, H, K, V, C=64, L=SEGMENT_CHUNKS):
-    """Bytes the segment-summary pass must move: it reads q, k, g, v (bf16) and
-    beta of every chunk, writes each chunk's M and Aqk fragments, and writes
-    per segment but the last the f32 zero-start end state (or the second
-    segment's start state) and, past the first, the bf16 128x128 transition."""
-    chunks = T // C
-    nseg = (chunks + L - 1) // L
-    reads = 2 * B * T * H * (3 * K + V) + 2 * B * T * H
-    writes = B * H * (chunks * MA_BYTES + (nseg - 1) * 4 * K * V + max(nseg - 2, 0) * 2 * K * K)
-    return reads + writes
-
-
-def kernel_bytes(name, B, T, H, K, V):
-    """Algorithmic HBM bytes one launch of a prefill kernel must move."""
-    if name == "chunk_segment_kernel<output>":
-        return prefill_bytes(B, T, H, K, V)
-    if name == "chunk_segment_kernel<summary>":
-        return summary_bytes(B, T, H, K, V)
-    return 0
 
 
 def decode_bytes(B, H, K, V):
@@ -367,6 +349,20 @@ def bench_cache(layers=8, reps=10):
     }
 
 
+def cpu_threads():
+    """Threads for the CPU baseline: the cores this process may run on, capped by
+    OMP_NUM_THREADS when the environment sets it (the share of the host that a
+    one-GPU job is given).  The host's total count is reported beside it."""
+    try:
+        avail = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        avail = os.cpu_count() or 1
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        avail = min(avail, int(env))
+    return max(1, avail)
+
+
 def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
     """The oracle's CPU restatement, timed like benchmarks/benchmark_kda.py:30-40
     (one warm-up, then min over repeats of time.perf_counter, inference_mode)."""
@@ -375,7 +371,7 @@ def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
     from oracle import kda_oracle as ora
     from tests._inputs import workload
 
-    threads = max(1, min(16, os.cpu_count() or 1))
+    threads = cpu_threads()
     torch.set_num_threads(threads)
 
     def timed(fn):
@@ -401,6 +397,7 @@ def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
     return {
         "prefill": {
             "value": prefill_sample_t / t_pre, "unit": "tokens/s", "cores": threads, "kind": "port",
+            "host_cpu_count": os.cpu_count(),
             "sample": f"oracle chunkwise (torch CPU, f32 work) B=1 T={prefill_sample_t} H={P_H} K=V=128 bf16, "
                       f"min of {repeats} after 1 warm-up",
         },
@@ -418,27 +415,136 @@ def cpu_baseline(prefill_sample_t=2048, decode_sample_b=32, repeats=3):
     }
 
 
-TRAFFIC_FILE = REPO / "profiles" / "hbm_traffic.json"
+COUNTERS_FILE = REPO / "profiles" / "kernel_counters.json"
+CSRC = REPO / "kimi-k3-pytorch_amd" / "csrc"
 
 
-def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the rocprofv3 FETCH_SIZE / WRITE_SIZE
-    runs of `--profile-pass` (calibrated against a device copy of known size), if
-    they have been recorded; None otherwise."""
+def source_sha16():
+    """Hash of the HIP/C++ sources the kernels are built from: a counter record
+    taken from another build is stale and is not reported."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for f in sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")) + list(CSRC.glob("*.h"))):
+        h.update(f.name.encode())
+        h.update(f.read_bytes())
+    return h.hexdigest()[:16]
+
+
+def kernel_key(name):
+    """Short, stable key of a rocprofv3 kernel name (mangled or demangled)."""
+    import re
+
+    base = re.search(r"([A-Za-z0-9_]+_kernel)", name)
+    if base is None:
+        return name
+    key = base.group(1)
+    if key == "chunk_segment_kernel":
+        mode = re.search(r"Li(\d)E", name) or re.search(r",\s*(\d)\s*>", name)
+        key += {"0": "<summary>", "1": "<output, prepared>", "2": "<output>"}.get(mode.group(1) if mode else "", "")
+    if "bwd" in name:
+        key = "bwd::" + key
+    return key
+
+
+def load_counters():
+    """The committed counter record, or None when it is absent or was taken from
+    sources other than the ones in this tree."""
     try:
-        data = json.loads(TRAFFIC_FILE.read_text())
+        data = json.loads(COUNTERS_FILE.read_text())
+    except (OSError, ValueError):
+        return None
+    if data.get("source_sha16") != source_sha16():
+        return None
+    return data
+
+
+def measured_traffic(kernel, counters=None):
+    """HBM bytes per launch of `kernel` from the committed TCC counter record
+    (read + written), or None if there is no current record for it."""
+    data = counters if counters is not None else load_counters()
+    try:
         entry = data["kernels"][kernel]
         return int(entry["read_bytes"] + entry["write_bytes"])
-    except (OSError, KeyError, ValueError, TypeError):
+    except (KeyError, TypeError):
         return None
+
+
+def counters_summary(dirs):
+    """Summarise rocprofv3 --pmc runs over `--profile-pass` (one directory per
+    pass, each with run_counter_collection.csv) into profiles/kernel_counters.json
+    and a markdown table on stdout.  HBM bytes come from the TCC/EA request
+    counts: reads = 128 B x TCC_BUBBLE + 64 B x (TCC_EA0_RDREQ - TCC_BUBBLE -
+    TCC_EA0_RDREQ_32B) + 32 B x TCC_EA0_RDREQ_32B, writes = 64 B x
+    TCC_EA0_WRREQ_64B + 32 B x (TCC_EA0_WRREQ - TCC_EA0_WRREQ_64B); the
+    runtime's 256 MiB device copy in the pass checks them.  MFMA busy % =
+    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs)."""
+    import csv
+    from collections import defaultdict
+
+    per = defaultdict(lambda: defaultdict(list))  # key -> counter -> [value per dispatch]
+    dur = defaultdict(list)
+    names = {}
+    for d in dirs:
+        seen = set()
+        for f in Path(d).rglob("*counter_collection.csv"):
+            for row in csv.DictReader(open(f)):
+                key = kernel_key(row["Kernel_Name"])
+                names.setdefault(key, row["Kernel_Name"])
+                disp = (str(f), row["Dispatch_Id"])
+                per[key][row["Counter_Name"]].append(float(row["Counter_Value"]))
+                if disp not in seen:
+                    seen.add(disp)
+                    dur[key].append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) * 1e-3)
+    mean = lambda xs: sum(xs) / len(xs) if xs else None  # noqa: E731
+    kernels = {}
+    for key, cs in per.items():
+        c = {n: mean(v) for n, v in cs.items()}
+        e = {"dispatches": max(len(v) for v in cs.values())}
+        if "TCC_EA0_RDREQ_sum" in c:
+            bub = c.get("TCC_BUBBLE_sum", 0.0)
+            r32 = c.get("TCC_EA0_RDREQ_32B_sum", 0.0)
+            e["read_bytes"] = int(128 * bub + 64 * (c["TCC_EA0_RDREQ_sum"] - bub - r32) + 32 * r32)
+        if "TCC_EA0_WRREQ_sum" in c:
+            w64 = c.get("TCC_EA0_WRREQ_64B_sum", 0.0)
+            e["write_bytes"] = int(64 * w64 + 32 * (c["TCC_EA0_WRREQ_sum"] - w64))
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in c and "GRBM_GUI_ACTIVE" in c and c["GRBM_GUI_ACTIVE"]:
+            e["mfma_busy_pct"] = round(100 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] * 1024), 2)
+        if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in c:
+            e["mfma_bf16_flop"] = int(512 * c["SQ_INSTS_VALU_MFMA_MOPS_BF16"])
+        if "SQ_INSTS_VALU_MFMA_MOPS_F32" in c:
+            e["mfma_f32_flop"] = int(512 * c["SQ_INSTS_VALU_MFMA_MOPS_F32"])
+        if dur[key]:
+            e["counter_run_us"] = round(mean(dur[key]), 2)
+        e["counters"] = {n: round(v, 1) for n, v in c.items()}
+        kernels[key] = e
+    data = {
+        "source": "rocprofv3 --pmc <counters> --kernel-trace -- python3 bench.py --profile-pass (one MI355X)",
+        "source_sha16": source_sha16(),
+        "byte_rule": counters_summary.__doc__.split("HBM bytes come from")[1].split("MFMA busy")[0].strip(),
+        "kernels": kernels,
+    }
+    copy = kernels.get("__amd_rocclr_copyBuffer") or next(
+        (v for k, v in kernels.items() if "copyBuffer" in k), None)
+    if copy is not None:
+        data["copy_check"] = {"bytes_each_way": 256 * 2**20, "read_bytes": copy.get("read_bytes"),
+                              "write_bytes": copy.get("write_bytes")}
+    COUNTERS_FILE.write_text(json.dumps(data, indent=1, sort_keys=True) + "\n")
+    print("| kernel | dispatches | read MB | written MB | MFMA busy % | bf16 MFMA GFLOP | us (counter run) |")
+    print("|---|---|---|---|---|---|---|")
+    for key in sorted(kernels):
+        e = kernels[key]
+        fmt = lambda x, s=1e6: "—" if x is None else f"{x / s:.1f}"  # noqa: E731
+        print(f"| `{key}` | {e['dispatches']} | {fmt(e.get('read_bytes'))} | {fmt(e.get('write_bytes'))} | "
+              f"{e.get('mfma_busy_pct', '—')} | {fmt(e.get('mfma_bf16_flop'), 1e9)} | {e.get('counter_run_us', '—')} |")
 
 
 def profile_pass():
     """The workload of the counter runs: after one warm-up round, one prefill at
     the benchmark shape, one in-place decode step at the benchmark shape, and a
-    256 MiB device-to-device copy whose byte counts calibrate the counters;
-    then the fused stages, the backward and the cache reorder legs once each
-    (their warm-up calls included)."""
+    256 MiB device-to-device copy whose byte counts check the counters; then
+    the fused stages, the backward and the cache reorder legs once each (their
+    warm-up calls included)."""
     import torch
 
     import kda
@@ -461,6 +567,58 @@ def profile_pass():
     print("profile pass done", flush=True)
 
 
+def bench_dropin(steps, warmup):
+    """The prefill and the decode step through the Python drop-in API, as the
+    reference's callers use them (src/kda/kda.py:133-151): validation, input
+    preparation and per-call output and workspace allocation included."""
+    import torch
+
+    import kda
+
+    device = torch.device("cuda", 0)
+    q, k, v, g, beta, s0 = _inputs(P_B, P_T, P_H, P_K, P_V, 0.02, 0, device)
+    gen = torch.Generator().manual_seed(1)
+    state = (torch.randn(D_B, D_H, D_K, D_V, generator=gen) * 0.02).to(device)
+    dq, dk, dv, dg, db, _ = _inputs(D_B, D_STEPS, D_H, D_K, D_V, None, 2, device)
+    steps_in = [tuple(x[:, t:t + 1].contiguous() for x in (dq, dk, dv, dg, db)) for t in range(D_STEPS)]
+
+    def timed(fn, n):
+        for i in range(warmup):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for i in range(n):
+            fn(i)
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    with torch.no_grad():
+        pre_ms = timed(lambda i: kda.chunkwise_kda(q, k, v, g, beta, s0, True), steps)
+        dec_ms = timed(lambda i: kda.recurrent_kda(*steps_in[i % D_STEPS], state, True, update_state_in_place=True),
+                       D_STEPS)
+    return {
+        "prefill": {"api": "kda.chunkwise_kda(q, k, v, g, beta, initial_state, output_final_state=True)",
+                    "ms": round(pre_ms, 5), "tokens_per_s": round(P_B * P_T / (pre_ms * 1e-3), 1)},
+        "decode": {"api": "kda.recurrent_kda(q, k, v, g, beta, state, True, update_state_in_place=True)",
+                   "ms_per_step": round(dec_ms, 5),
+                   "gbs": round(decode_bytes(D_B, D_H, D_K, D_V) / (dec_ms * 1e-3) / 1e9, 1)},
+    }
+
+
+def prefill_plan():
+    from kda import _lib
+
+    lib = _lib.load()
+    import torch
+
+    L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
+    _lib.check(lib.kda_chunk_fwd_plan(P_B, P_B * P_T, P_H, P_K, P_V, _lib.dtype_code(torch.bfloat16),
+                                      ctypes.byref(L), ctypes.byref(segs)))
+    return {"chunks_per_segment": L.value, "segments": segs.value}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--gpus", type=int, default=1)
@@ -469,7 +627,12 @@ def main() -> int:
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--profile-pass", action="store_true",
                     help="run the counter-collection workload only (for rocprofv3 --pmc)")
+    ap.add_argument("--counters-summary", nargs="+", metavar="DIR",
+                    help="summarise rocprofv3 --pmc output directories into profiles/kernel_counters.json")
     args = ap.parse_args()
+    if args.counters_summary:
+        counters_summary(args.counters_summary)
+        return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the KDA operator has no collective; --gpus {args.gpus} "
               "is not supported: run with --gpus 1)", file=sys.stderr)
@@ -486,16 +649,19 @@ def main() -> int:
 
     ms, per_kernel, ws_bytes = bench_prefill(args.steps, args.warmup)
     dec_ms = bench_decode(args.warmup)
+    counters = load_counters()
 
     tokens_per_s = P_B * P_T / (ms * 1e-3)
     pbytes = prefill_bytes(P_B, P_T, P_H, P_K, P_V)
     pflops = prefill_flops(P_B, P_T, P_H, P_K, P_V)
-    dom = max(PREFILL_KERNELS[1:], key=lambda n: per_kernel[n] if kernel_bytes(n, P_B, P_T, P_H, P_K, P_V) else -1)
-    dom_ms = per_kernel[dom]
-    dom_bytes = kernel_bytes(dom, P_B, P_T, P_H, P_K, P_V)
-    op_ms = ms  # the whole operator, end to end
+    ran = {n: t for n, t in per_kernel.items() if t > 0}
+    dom = max(ran, key=ran.get)
+    dom_ms = ran[dom]
     dbytes = decode_bytes(D_B, D_H, D_K, D_V)
     dec_gbs = dbytes / (dec_ms * 1e-3) / 1e9
+    traffic = {n: measured_traffic(n, counters) for n in ran}
+    op_traffic = None if None in traffic.values() else sum(traffic.values())
+    mfma = {n: (counters or {}).get("kernels", {}).get(n, {}).get("mfma_busy_pct") for n in ran}
 
     result = {
         "metric": METRIC,
@@ -519,21 +685,27 @@ def main() -> int:
         "roofline": {
             "bound": "hbm",
             "kernel": dom,
-            "achieved": round(dom_bytes / (dom_ms * 1e-3) / 1e9, 1),
+            "achieved": round(pbytes / (dom_ms * 1e-3) / 1e9, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
-            "frac": round(dom_bytes / (dom_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "traffic": measured_traffic(dom),
-            "algorithmic_bytes": dom_bytes,
+            "frac": round(pbytes / (dom_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "traffic": op_traffic,
+            "algorithmic_bytes": pbytes,
             "kernel_ms": round(dom_ms, 5),
+            "note": "achieved = the operator's compulsory bytes (q, k, g, v, beta, output, f32 initial and "
+                    "final state) / the dominant kernel's time; traffic = HBM bytes per prefill, all kernels, "
+                    "from the committed TCC counter record of these sources (null if it is stale)",
         },
         "roofline_operator": {
             "bound": "hbm",
+            "plan": prefill_plan(),
             "kernels_ms": {k: round(v, 5) for k, v in per_kernel.items()},
-            "achieved_gbs": round(pbytes / (op_ms * 1e-3) / 1e9, 1),
-            "frac_hbm": round(pbytes / (op_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
-            "achieved_tflops": round(pflops / (op_ms * 1e-3) / 1e12, 2),
-            "frac_bf16_mfma": round(pflops / (op_ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "kernels_traffic": traffic,
+            "kernels_mfma_busy_pct": mfma,
+            "achieved_gbs": round(pbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(pbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "achieved_tflops": round(pflops / (ms * 1e-3) / 1e12, 2),
+            "frac_bf16_mfma": round(pflops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
             "algorithmic_flops": pflops,
             "workspace_bytes": ws_bytes,
         },
@@ -544,11 +716,12 @@ def main() -> int:
             "ms_per_step": round(dec_ms, 5),
             "roofline": {
                 "bound": "hbm", "kernel": "recurrent_kernel", "achieved": round(dec_gbs, 1), "peak": HBM_PEAK_GBS,
-                "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic("recurrent_kernel"),
-                "algorithmic_bytes": dbytes,
+                "unit": "GB/s", "frac": round(dec_gbs / HBM_PEAK_GBS, 4),
+                "traffic": measured_traffic("recurrent_kernel", counters), "algorithmic_bytes": dbytes,
             },
         },
     }
+    result["dropin"] = bench_dropin(args.steps, args.warmup)
     result["fused_stages"] = {
         "workload": f"B={P_B} T={P_T} H={P_H} D={P_K} bf16, 50 back-to-back C-ABI launches each",
         "kernels": bench_fused(),

@@ -35,7 +35,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 6
+#define KDA_ABI_VERSION 7
 
 /* status codes */
 #define KDA_OK 0
@@ -95,6 +95,18 @@ int kda_decode_step(const void* q, const void* k, const void* v, const void* g,
  */
 size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads,
                                      int64_t key_dim, int64_t value_dim, int in_dtype);
+
+/*
+ * The schedule `kda_chunk_fwd` picks for these sizes: *chunks_per_segment is
+ * the number of 64-token chunks per segment (0 when every sequence is one
+ * segment, -1 when the shape runs the exact recurrence kernel) and *segments
+ * the bound on segments it sizes its workspace for.  No reference
+ * counterpart (the reference has one schedule, a Python loop over chunks,
+ * src/kda/chunkwise.py:61-102); benchmarks and tests use it to attribute
+ * time and to cover both schedules.
+ */
+int kda_chunk_fwd_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
+                       int64_t value_dim, int in_dtype, int64_t* chunks_per_segment, int64_t* segments);
 
 /*
  * Chunkwise-parallel KDA prefill (chunk 64): intra-chunk UT transform with a

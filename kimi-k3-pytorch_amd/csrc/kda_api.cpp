@@ -143,6 +143,22 @@ size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int
   return chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype);
 }
 
+int kda_chunk_fwd_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
+                       int in_dtype, int64_t* chunks_per_segment, int64_t* segments) {
+  g_detail[0] = '\0';
+  if (!chunks_per_segment || !segments) {
+    set_detail("chunk_fwd_plan: output pointers must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!is_input_dtype(in_dtype) || num_seqs <= 0 || total_tokens <= 0 || heads <= 0 || key_dim <= 0 ||
+      value_dim <= 0) {
+    set_detail("chunk_fwd_plan: bad sizes or dtype");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  chunk_plan(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype, chunks_per_segment, segments);
+  return KDA_OK;
+}
+
 int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
                   const void* initial_state, void* final_state, int state_dtype, void* out,
                   const int32_t* cu_seqlens, int64_t dense_span, const int32_t* valid_lens, int64_t num_seqs,

@@ -44,13 +44,16 @@
 // written pre-permuted to match.  The raw inputs of the next chunk are loaded
 // into registers while the current chunk is scanned.
 //
-// Numerical scheme for the decays (per-channel, any g <= 0):
+// Numerical scheme for the decays (per-channel g of either sign):
 //   alpha_j = exp(g_j); within each 16-row block J the running products
-//   a_j = exp(lg_j - lg_{16J}) and E_j = exp(lg_{16J+15} - lg_j) are <= 1.
-//   Off-diagonal blocks J < I use (k_i a_i) . (k_j E_j D_IJ) with
-//   D_IJ = exp(lg_{16I} - lg_{16J+15}) <= 1; diagonal blocks use
+//   a_j = exp(lg_j - lg_{16J}) and E_j = exp(lg_{16J+15} - lg_j) (<= 1 for
+//   g <= 0).  Off-diagonal blocks J < I use (k_i a_i) . (k_j E_j D_IJ) with
+//   D_IJ = exp(lg_{16I} - lg_{16J+15}); diagonal blocks use
 //   (k_i a_i) . (k_j E_j / P_I) with P_I = exp(lg_{16I+15} - lg_{16I}).
-//   No factor overflows unless a block decays by more than 2^-100; such
+//   Each factor is a product of at most one chunk's decays, and the product
+//   of two factors is the pairwise exponent exp(lg_i - lg_j) itself, so the
+//   bf16 operands carry the same relative rounding for any g; only a block
+//   whose decay leaves [2^-100, 2^100] could overflow a factor, and such
 //   chunks take an exact pairwise-exponent path for the diagonal blocks (the
 //   reference evaluates every tile with an explicit pairwise exponent,
 //   src/kda/utils.py:128-136).
@@ -71,6 +74,7 @@ constexpr int kKey = 128;
 constexpr int kColGroup = 128;  // value columns per workgroup
 constexpr int kThreads = 512;   // 8 waves
 constexpr float kExtremeDecay = 7.888609052210118e-31f;  // 2^-100
+constexpr float kExtremeGrowth = 1.2676506002282294e30f;  // 2^100
 constexpr int32_t kOneSegment = 0x3fffffff;              // L: every sequence is one segment
 
 constexpr int kSummary = 0;   // phase A: segment summaries, and each chunk's M and Aqk
@@ -567,7 +571,7 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
 #pragma unroll
   for (int ch = 0; ch < 2; ++ch) {
     const float a0 = al[ch][0];
-    ext = ext || !(pj[ch] >= kExtremeDecay);
+    ext = ext || !(pj[ch] >= kExtremeDecay && pj[ch] <= kExtremeGrowth);
     float G[4];
 #pragma unroll
     for (int jb = 0; jb < 4; ++jb) G[jb] = __shfl(a0 * pj[ch], (lane & 15) + 16 * jb);
@@ -1862,6 +1866,18 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
 }  // namespace kda
 
 namespace kda_host {
+
+void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
+                int in_dtype, int64_t* chunks_per_segment, int64_t* segments) {
+  if (!kda::mfma_path(in_dtype, in_dtype == KDA_DTYPE_F64 ? KDA_DTYPE_F64 : KDA_DTYPE_F32, key_dim, value_dim)) {
+    *chunks_per_segment = -1;  // the exact recurrence kernel
+    *segments = num_seqs;
+    return;
+  }
+  const kda::Plan p = kda::make_plan(num_seqs, total_tokens, heads, value_dim);
+  *chunks_per_segment = p.segmented ? p.L : 0;
+  *segments = p.segs_bound;
+}
 
 size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
                              int64_t value_dim, int in_dtype) {

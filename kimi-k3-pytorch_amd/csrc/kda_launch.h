@@ -18,6 +18,11 @@ int launch_recurrent(const void* q, const void* k, const void* v, const void* g,
 size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
                              int64_t value_dim, int in_dtype);
 
+// The schedule launch_chunk picks: chunks per segment (0: one segment per
+// sequence; -1: the exact recurrence kernel) and the bound on segments.
+void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
+                int in_dtype, int64_t* chunks_per_segment, int64_t* segments);
+
 // Optional per-kernel timing: events[i] is recorded before kernel i and
 // events[n] after the last one; *n_launched receives n.  Bit i of `empty`
 // marks a slot whose kernel the call does not need (its time reads zero).

@@ -36,11 +36,20 @@ def gather_rows(tensors: Sequence[torch.Tensor], indices: torch.Tensor | None) -
     ``indices=None`` copies every tensor (a clone).  All tensors share the
     batch size of dimension 0 and live on one GPU; ``indices`` is a rank-1
     ``torch.long`` tensor on that GPU.  An index outside ``[0, batch)`` raises
-    ``IndexError``, as ``index_select`` does.
+    ``IndexError``, as ``index_select`` does.  Like ``index_select`` and
+    ``clone`` (src/kda/state.py:41-67) the result is differentiable: the
+    gradient of a source row is the sum of the gradients of the rows gathered
+    from it.
     """
     tensors = [_rows(t) for t in tensors]
     if not tensors:
         return []
+    if torch.is_grad_enabled() and any(t.requires_grad for t in tensors):
+        return list(_GatherRows.apply(indices, *tensors))
+    return _gather(tensors, indices)
+
+
+def _gather(tensors: list[torch.Tensor], indices: torch.Tensor | None) -> list[torch.Tensor]:
     device = tensors[0].device
     for t in tensors:
         _lib.require_gpu(t)
@@ -77,6 +86,29 @@ def gather_rows(tensors: Sequence[torch.Tensor], indices: torch.Tensor | None) -
     if status is not None and int(status.item()) != 0:
         raise IndexError(f"index out of range for a cache batch of {n_src}")
     return outs
+
+
+class _GatherRows(torch.autograd.Function):
+    """The native gather under autograd.  Backward: a clone passes gradients
+    through; a reorder adds each output row's gradient into the source row it
+    was read from (rows picked several times accumulate)."""
+
+    @staticmethod
+    def forward(ctx, indices, *tensors):
+        ctx.indices = indices
+        ctx.shapes = [t.shape for t in tensors]
+        return tuple(_gather(list(tensors), indices))
+
+    @staticmethod
+    def backward(ctx, *grads):
+        idx = ctx.indices
+        out = []
+        for shape, gr in zip(ctx.shapes, grads):
+            if gr is None or idx is None:
+                out.append(gr)
+            else:
+                out.append(torch.zeros(shape, dtype=gr.dtype, device=gr.device).index_add_(0, idx, gr))
+        return (None, *out)
 
 
 def _flatten(state: KDAState) -> list[torch.Tensor]:

@@ -22,7 +22,8 @@ the attention mask is applied with differentiable tensor ops first
 documents (``cu_seqlens``) are differentiated one document at a time: each is
 a dense batch-1 call on its slice of the packed tensors (pointer offsets into
 the same inputs and gradient buffers, one workspace sized for the longest
-document).  Other cases raise instead of dropping gradients.
+document).  Other cases raise instead of dropping gradients, and so does a
+second derivative (the backward is marked once-differentiable).
 """
 
 from __future__ import annotations
@@ -156,7 +157,11 @@ class _ChunkwiseFunction(torch.autograd.Function):
         return out.hidden_states, out.final_state
 
     @staticmethod
+    @torch.autograd.function.once_differentiable
     def backward(ctx, d_hidden, d_final):
+        # the HIP backward is not itself differentiable: a second derivative
+        # (create_graph=True followed by another backward) raises instead of
+        # treating these gradients as constants
         q, k, v, g, beta, initial_state = ctx.saved_tensors
         lib = _lib.load()
         (qc, kc, vc, gc, bc), kernel_dtype, _ = _prep.kernel_inputs(q, k, v, g, beta, ctx.work_dtype)

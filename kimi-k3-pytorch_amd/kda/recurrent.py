@@ -147,6 +147,7 @@ class _RecurrentStatesFunction(torch.autograd.Function):
         return out.hidden_states, out.final_state, hist
 
     @staticmethod
+    @torch.autograd.function.once_differentiable
     def backward(ctx, d_hidden, d_final, d_hist):
         q, k, v, g, beta, initial_state, hist = ctx.saved_tensors
         lib = _lib.load()

@@ -142,6 +142,22 @@ def test_recurrent_and_chunkwise_f64_gradients_agree():
         torch.testing.assert_close(a.grad, b.grad, rtol=2e-10, atol=2e-11)
 
 
+@pytest.mark.parametrize("op", ["chunkwise", "recurrent_states"])
+def test_second_derivative_raises(op):
+    # The HIP backwards are once-differentiable: a second derivative (the
+    # reference's gradgradcheck, tests/kda/test_kda_recurrent.py:184-198) raises
+    # instead of silently treating the first gradients as constants.
+    q, k, v, g, beta, state = (t.to(DEV).double() for t in workload(1, 6, 1, 16, 16, state_std=0.1, seed=3))
+    q.requires_grad_()
+    if op == "chunkwise":
+        out = kda.chunkwise_kda(q, k, v, g, beta, state, True).hidden_states
+    else:
+        out = kda.recurrent_kda(q, k, v, g, beta, state, True, return_states_per_token=True).hidden_states
+    (gq,) = torch.autograd.grad(out.square().sum(), q, create_graph=True)
+    with pytest.raises(RuntimeError, match="once_differentiable|twice"):
+        gq.sum().backward()
+
+
 def test_backward_refuses_unsupported_cases():
     q2, k2, v2, g2, b2, _ = (t.to(DEV) for t in workload(1, 8, 1, 16, 16, state_std=0.1))
     with pytest.raises(RuntimeError, match="up to 128"):

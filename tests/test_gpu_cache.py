@@ -144,3 +144,24 @@ def test_permutation_round_trip_at_decode_cache_size():
     assert torch.equal(back.q_conv_state.buffer, s.q_conv_state.buffer)
     assert torch.equal(back.sequence_offset, s.sequence_offset)
     assert torch.equal(once.recurrent_state[5], s.recurrent_state[perm[5]])
+
+
+def test_reorder_and_clone_are_differentiable_like_index_select():
+    # KDAState.reorder / clone in the reference are index_select / clone, both
+    # differentiable (src/kda/state.py:41-67): the native gather gives the same
+    # gradients, duplicated indices accumulating
+    gen = torch.Generator().manual_seed(4)
+    src = torch.randn(4, 2, 16, 16, generator=gen).to(DEV).requires_grad_()
+    buf = torch.randn(4, 3, 64, generator=gen).to(DEV).requires_grad_()
+    idx = torch.tensor([3, 0, 3, 1, 3], dtype=torch.long, device=DEV)
+    w1 = torch.randn(5, 2, 16, 16, generator=gen).to(DEV)
+    w2 = torch.randn(5, 3, 64, generator=gen).to(DEV)
+    out = cache.gather_rows([src, buf], idx)
+    ((out[0] * w1).sum() + (out[1] * w2).sum()).backward()
+    ref_src, ref_buf = src.detach().clone().requires_grad_(), buf.detach().clone().requires_grad_()
+    ((ref_src.index_select(0, idx) * w1).sum() + (ref_buf.index_select(0, idx) * w2).sum()).backward()
+    torch.testing.assert_close(src.grad, ref_src.grad, rtol=1e-6, atol=1e-6)
+    torch.testing.assert_close(buf.grad, ref_buf.grad, rtol=1e-6, atol=1e-6)
+    src.grad = None
+    (cache.gather_rows([src], None)[0] * w1[:4]).sum().backward()
+    torch.testing.assert_close(src.grad, w1[:4])

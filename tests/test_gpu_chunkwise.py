@@ -123,6 +123,35 @@ def test_chunkwise_extreme_decay_takes_exact_path():
     _check(got, ro, rs, label="extreme decay")
 
 
+@pytest.mark.parametrize("segment_chunks", [None, "1"])
+@pytest.mark.parametrize("regime", ["mixed_small", "rising_chunk", "rising_block_past_2e100"])
+def test_chunkwise_rising_decays(monkeypatch, regime, segment_chunks):
+    # The reference operator accepts a decay of either sign (src/kda/utils.py:32-71).
+    # mixed_small: g = 0.02 N(0,1) everywhere; rising_chunk: one whole chunk at
+    # g = +0.3 (the chunk grows by e^19.2); rising_block_past_2e100: one 16-row
+    # block at g = +5 (e^80 > 2^100, the exact diagonal path) followed by a
+    # block at g = -5.  Both schedules: one segment per sequence and one chunk
+    # per segment.
+    if segment_chunks is not None:
+        monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", segment_chunks)
+    q, k, v, g, beta, state = workload(1, 200, 2, 128, 128, state_std=0.02, seed=19)
+    gen = torch.Generator().manual_seed(23)
+    if regime == "mixed_small":
+        g = (0.02 * torch.randn(q.shape, generator=gen)).to(torch.bfloat16)
+    elif regime == "rising_chunk":
+        g = g.clone()
+        g[:, 64:128] = 0.3
+    else:
+        g = g.clone()
+        g[:, 80:96] = 5.0
+        g[:, 96:112] = -5.0
+    ro, rs = _oracle_f32(q, k, v, g, beta, state)
+    assert torch.isfinite(ro).all() and torch.isfinite(rs).all()
+    got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True)
+    assert torch.isfinite(got.hidden_states.float()).all() and torch.isfinite(got.final_state).all()
+    _check(got, ro, rs, label=f"{regime} L={segment_chunks}")
+
+
 def test_chunkwise_zero_decay_delta_rule():
     # g = 0 (classic delta rule, no forgetting) over several chunks
     q, k, v, _, beta, state = workload(1, 256, 2, 128, 128, state_std=0.02, seed=18)
