@@ -419,43 +419,80 @@ COUNTERS_FILE = REPO / "profiles" / "kernel_counters.json"
 CSRC = REPO / "kimi-k3-pytorch_amd" / "csrc"
 
 
-def source_sha16():
-    """Hash of the HIP/C++ sources the kernels are built from: a counter record
-    taken from another build is stale and is not reported."""
+def _sha16(data):
     import hashlib
 
-    h = hashlib.sha256()
-    for f in sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")) + list(CSRC.glob("*.h"))):
-        h.update(f.name.encode())
-        h.update(f.read_bytes())
-    return h.hexdigest()[:16]
+    return hashlib.sha256(data).hexdigest()[:16]
+
+
+def source_hashes():
+    """Hash of every HIP/C++ source and header the kernels are built from."""
+    files = sorted(list(CSRC.glob("*.hip")) + list(CSRC.glob("*.cpp")) + list(CSRC.glob("*.h")))
+    return {f.name: _sha16(f.read_bytes()) for f in files}
+
+
+def kernel_source(key):
+    """The source file that defines the kernel behind a counter key (None for
+    kernels that are not this library's)."""
+    import re
+
+    base = key.split("::")[-1].split("<")[0]
+    for f in sorted(CSRC.glob("*.hip")):
+        if re.search(r"__global__[^;{]*\b" + re.escape(base) + r"\s*\(", f.read_text()):
+            return f.name
+    return None
 
 
 def kernel_key(name):
-    """Short, stable key of a rocprofv3 kernel name (mangled or demangled)."""
+    """Short, stable key of a rocprofv3 kernel name (mangled or demangled):
+    the kernel's identifier, the phase of chunk_segment_kernel, and a
+    `bwd::` prefix for the backward's kernels."""
     import re
 
-    base = re.search(r"([A-Za-z0-9_]+_kernel)", name)
-    if base is None:
-        return name
-    key = base.group(1)
+    if name.startswith("_Z"):
+        # length-prefixed identifiers of the mangled name: the first *_kernel one
+        ids, i = [], 2
+        while i < len(name):
+            m = re.match(r"(\d+)", name[i:])
+            if m is None:
+                i += 1
+                continue
+            n = int(m.group(1))
+            start = i + len(m.group(1))
+            ids.append(name[start:start + n])
+            i = start + n
+        base = next((x for x in ids if x.endswith("_kernel")), name)
+        mode = re.search(r"Li(\d)E", name)
+    else:
+        found = re.search(r"([A-Za-z_][A-Za-z0-9_]*_kernel)\b", name) or re.search(r"([A-Za-z_]\w*kernel\w*)", name)
+        base = found.group(1) if found else name
+        mode = re.search(r",\s*(\d)\s*>", name)
+    key = base
     if key == "chunk_segment_kernel":
-        mode = re.search(r"Li(\d)E", name) or re.search(r",\s*(\d)\s*>", name)
         key += {"0": "<summary>", "1": "<output, prepared>", "2": "<output>"}.get(mode.group(1) if mode else "", "")
-    if "bwd" in name:
+    if "bwd" in name and not key.startswith("bwd"):
         key = "bwd::" + key
     return key
 
 
 def load_counters():
-    """The committed counter record, or None when it is absent or was taken from
-    sources other than the ones in this tree."""
+    """The committed counter record with only the kernels whose defining source
+    file (and the shared headers) are unchanged since the counters were taken;
+    None when there is no record."""
     try:
         data = json.loads(COUNTERS_FILE.read_text())
     except (OSError, ValueError):
         return None
-    if data.get("source_sha16") != source_sha16():
-        return None
+    now, then = source_hashes(), data.get("source_hashes", {})
+    shared = [n for n in now if n.endswith(".h")]
+    current = {}
+    for key, entry in data.get("kernels", {}).items():
+        src = entry.get("source")
+        if src is None:
+            continue
+        if all(now.get(n) == then.get(n) for n in [src, *shared]):
+            current[key] = entry
+    data["kernels"] = current
     return data
 
 
@@ -470,73 +507,102 @@ def measured_traffic(kernel, counters=None):
         return None
 
 
-def counters_summary(dirs):
+def counters_summary(dirs, out=None):
     """Summarise rocprofv3 --pmc runs over `--profile-pass` (one directory per
     pass, each with run_counter_collection.csv) into profiles/kernel_counters.json
     and a markdown table on stdout.  HBM bytes come from the TCC/EA request
-    counts: reads = 128 B x TCC_BUBBLE + 64 B x (TCC_EA0_RDREQ - TCC_BUBBLE -
-    TCC_EA0_RDREQ_32B) + 32 B x TCC_EA0_RDREQ_32B, writes = 64 B x
-    TCC_EA0_WRREQ_64B + 32 B x (TCC_EA0_WRREQ - TCC_EA0_WRREQ_64B); the
-    runtime's 256 MiB device copy in the pass checks them.  MFMA busy % =
-    SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE x 1024 SIMDs)."""
+    counts: reads = 128 B x (TCC_EA0_RDREQ - TCC_EA0_RDREQ_32B) + 32 B x
+    TCC_EA0_RDREQ_32B (gfx950 issues 128-byte read requests: the profile
+    pass's 256 MiB device copy shows exactly 2^21 of them), writes = 64 B x
+    TCC_EA0_WRREQ_64B + 32 B x (TCC_EA0_WRREQ - TCC_EA0_WRREQ_64B).  MFMA
+    busy % = SQ_VALU_MFMA_BUSY_CYCLES (summed over the SIMDs) / (GRBM_GUI_ACTIVE
+    per XCC x SIMDs); rocprofv3 sums GRBM_GUI_ACTIVE over the XCCs."""
     import csv
     from collections import defaultdict
 
     per = defaultdict(lambda: defaultdict(list))  # key -> counter -> [value per dispatch]
     dur = defaultdict(list)
-    names = {}
+    n_xcc, n_simd = 8, 1024
     for d in dirs:
-        seen = set()
+        for f in Path(d).rglob("*agent_info.csv"):
+            for row in csv.DictReader(open(f)):
+                if row.get("Name", "").startswith("gfx"):
+                    n_xcc, n_simd = int(row["Num_Xcc"]), int(row["Simd_Count"])
         for f in Path(d).rglob("*counter_collection.csv"):
+            seen = set()
             for row in csv.DictReader(open(f)):
                 key = kernel_key(row["Kernel_Name"])
-                names.setdefault(key, row["Kernel_Name"])
-                disp = (str(f), row["Dispatch_Id"])
                 per[key][row["Counter_Name"]].append(float(row["Counter_Value"]))
-                if disp not in seen:
-                    seen.add(disp)
+                if row["Dispatch_Id"] not in seen:
+                    seen.add(row["Dispatch_Id"])
                     dur[key].append((int(row["End_Timestamp"]) - int(row["Start_Timestamp"])) * 1e-3)
     mean = lambda xs: sum(xs) / len(xs) if xs else None  # noqa: E731
+
+    def read_bytes(c):
+        r32 = c.get("TCC_EA0_RDREQ_32B_sum", 0.0)
+        return int(128 * (c["TCC_EA0_RDREQ_sum"] - r32) + 32 * r32)
+
+    def write_bytes(c):
+        w64 = c.get("TCC_EA0_WRREQ_64B_sum", 0.0)
+        return int(64 * w64 + 32 * (c["TCC_EA0_WRREQ_sum"] - w64))
+
     kernels = {}
     for key, cs in per.items():
         c = {n: mean(v) for n, v in cs.items()}
         e = {"dispatches": max(len(v) for v in cs.values())}
         if "TCC_EA0_RDREQ_sum" in c:
-            bub = c.get("TCC_BUBBLE_sum", 0.0)
-            r32 = c.get("TCC_EA0_RDREQ_32B_sum", 0.0)
-            e["read_bytes"] = int(128 * bub + 64 * (c["TCC_EA0_RDREQ_sum"] - bub - r32) + 32 * r32)
+            e["read_bytes"] = read_bytes(c)
         if "TCC_EA0_WRREQ_sum" in c:
-            w64 = c.get("TCC_EA0_WRREQ_64B_sum", 0.0)
-            e["write_bytes"] = int(64 * w64 + 32 * (c["TCC_EA0_WRREQ_sum"] - w64))
-        if "SQ_VALU_MFMA_BUSY_CYCLES" in c and "GRBM_GUI_ACTIVE" in c and c["GRBM_GUI_ACTIVE"]:
-            e["mfma_busy_pct"] = round(100 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] * 1024), 2)
+            e["write_bytes"] = write_bytes(c)
+        if c.get("SQ_VALU_MFMA_BUSY_CYCLES") is not None and c.get("GRBM_GUI_ACTIVE"):
+            e["mfma_busy_pct"] = round(100 * c["SQ_VALU_MFMA_BUSY_CYCLES"] / (c["GRBM_GUI_ACTIVE"] / n_xcc * n_simd), 2)
         if "SQ_INSTS_VALU_MFMA_MOPS_BF16" in c:
             e["mfma_bf16_flop"] = int(512 * c["SQ_INSTS_VALU_MFMA_MOPS_BF16"])
         if "SQ_INSTS_VALU_MFMA_MOPS_F32" in c:
             e["mfma_f32_flop"] = int(512 * c["SQ_INSTS_VALU_MFMA_MOPS_F32"])
         if dur[key]:
             e["counter_run_us"] = round(mean(dur[key]), 2)
+            if e.get("mfma_bf16_flop"):
+                e["mfma_bf16_frac_of_peak"] = round(e["mfma_bf16_flop"] / (e["counter_run_us"] * 1e-6)
+                                                    / (BF16_PEAK_TFLOPS * 1e12), 4)
         e["counters"] = {n: round(v, 1) for n, v in c.items()}
+        e["source"] = kernel_source(key)
         kernels[key] = e
     data = {
         "source": "rocprofv3 --pmc <counters> --kernel-trace -- python3 bench.py --profile-pass (one MI355X)",
-        "source_sha16": source_sha16(),
-        "byte_rule": counters_summary.__doc__.split("HBM bytes come from")[1].split("MFMA busy")[0].strip(),
+        "source_hashes": source_hashes(),
+        "rules": " ".join(counters_summary.__doc__.split("HBM bytes come from")[1].split()),
         "kernels": kernels,
     }
-    copy = kernels.get("__amd_rocclr_copyBuffer") or next(
-        (v for k, v in kernels.items() if "copyBuffer" in k), None)
-    if copy is not None:
-        data["copy_check"] = {"bytes_each_way": 256 * 2**20, "read_bytes": copy.get("read_bytes"),
-                              "write_bytes": copy.get("write_bytes")}
-    COUNTERS_FILE.write_text(json.dumps(data, indent=1, sort_keys=True) + "\n")
-    print("| kernel | dispatches | read MB | written MB | MFMA busy % | bf16 MFMA GFLOP | us (counter run) |")
-    print("|---|---|---|---|---|---|---|")
+    # the 256 MiB device copy of the profile pass (the runtime's copy kernel also
+    # serves torch's small copies; the largest dispatch is this one)
+    copies = [(r, w) for key, cs in per.items() if "copyBuffer" in key
+              for r, w in zip(cs.get("TCC_EA0_RDREQ_sum", []), cs.get("TCC_EA0_WRREQ_sum", []) or [None] * 999)]
+    rd = max((v for key, cs in per.items() if "copyBuffer" in key for v in cs.get("TCC_EA0_RDREQ_sum", [])),
+             default=None)
+    wr = max((v for key, cs in per.items() if "copyBuffer" in key for v in cs.get("TCC_EA0_WRREQ_sum", [])),
+             default=None)
+    w64 = max((v for key, cs in per.items() if "copyBuffer" in key for v in cs.get("TCC_EA0_WRREQ_64B_sum", [])),
+              default=0.0)
+    del copies
+    if rd is not None:
+        data["copy_check"] = {
+            "bytes_each_way": 256 * 2**20,
+            "read_requests": int(rd),
+            "read_bytes": int(128 * rd),
+            "write_bytes": None if wr is None else int(64 * w64 + 32 * (wr - w64)),
+        }
+    Path(out or COUNTERS_FILE).write_text(json.dumps(data, indent=1, sort_keys=True) + "\n")
+    print("| kernel | dispatches | read MB | written MB | MFMA busy % | bf16 MFMA GFLOP | of bf16 peak | us (counter run) |")
+    print("|---|---|---|---|---|---|---|---|")
     for key in sorted(kernels):
         e = kernels[key]
-        fmt = lambda x, s=1e6: "—" if x is None else f"{x / s:.1f}"  # noqa: E731
+        fmt = lambda x, sc=1e6: "—" if x is None else f"{x / sc:.1f}"  # noqa: E731
         print(f"| `{key}` | {e['dispatches']} | {fmt(e.get('read_bytes'))} | {fmt(e.get('write_bytes'))} | "
-              f"{e.get('mfma_busy_pct', '—')} | {fmt(e.get('mfma_bf16_flop'), 1e9)} | {e.get('counter_run_us', '—')} |")
+              f"{e.get('mfma_busy_pct', '—')} | {fmt(e.get('mfma_bf16_flop'), 1e9)} | "
+              f"{e.get('mfma_bf16_frac_of_peak', '—')} | {e.get('counter_run_us', '—')} |")
+    if "copy_check" in data:
+        print(f"copy check: {data['copy_check']}")
 
 
 def profile_pass():
@@ -629,9 +695,10 @@ def main() -> int:
                     help="run the counter-collection workload only (for rocprofv3 --pmc)")
     ap.add_argument("--counters-summary", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc output directories into profiles/kernel_counters.json")
+    ap.add_argument("--counters-out", default=None, help="where --counters-summary writes its JSON")
     args = ap.parse_args()
     if args.counters_summary:
-        counters_summary(args.counters_summary)
+        counters_summary(args.counters_summary, args.counters_out)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the KDA operator has no collective; --gpus {args.gpus} "
