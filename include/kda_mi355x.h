@@ -130,6 +130,28 @@ int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, co
                   size_t workspace_bytes, void* stream);
 
 /*
+ * `kda_chunk_fwd` for callers that cannot allocate device memory (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * No counterpart in the reference.  Same arguments, checks and kernels as
+ * `kda_chunk_fwd`, minus the workspace: it lives in a static device array of
+ * KDA_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until the
+ * process ends.  A prefill whose `kda_chunk_fwd_workspace_bytes` exceeds it
+ * returns KDA_ERR_WORKSPACE before anything is launched (128 MiB covers one
+ * 8192-token sequence at H=16, which needs 72.5 MB; shapes with
+ * batch * heads >= 192 need only the small chunk maps).  The call performs
+ * no device allocation.  All calls on one GPU share that GPU's array:
+ * calls that overlap on one GPU (two streams, two host threads) race.  The
+ * stream must belong to the current device.
+ */
+#define KDA_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+int kda_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const void* g,
+                          const void* beta, int in_dtype, const void* initial_state,
+                          void* final_state, int state_dtype, void* out,
+                          const int32_t* cu_seqlens, int64_t dense_span,
+                          const int32_t* valid_lens, int64_t num_seqs, int64_t total_tokens,
+                          int64_t heads, int64_t key_dim, int64_t value_dim, void* stream);
+
+/*
  * `kda_chunk_fwd` with a HIP event recorded between its kernels; returns,
  * after synchronising `stream`, the duration of each stage in kernel_ms[0..3]
  * (chunk map, segment summaries, segment combine, chunk outputs; zero for a

@@ -22,6 +22,9 @@ KDA_ERR_UNSUPPORTED = 2
 KDA_ERR_WORKSPACE = 3
 KDA_ERR_LAUNCH = 4
 
+# KDA_NOALLOC_SCRATCH_BYTES: the static device scratch of kda_chunk_fwd_noalloc
+NOALLOC_SCRATCH_BYTES = 128 << 20
+
 DTYPE_CODES = {
     torch.float32: 0,
     torch.float16: 1,
@@ -47,6 +50,10 @@ SIGNATURES = {
     "kda_chunk_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P, _S, _P],
+    ),
+    "kda_chunk_fwd_noalloc": (
+        _I,
+        [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P],
     ),
     "kda_chunk_fwd_profiled": (
         _I,

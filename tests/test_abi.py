@@ -141,3 +141,10 @@ def test_recurrent_backward_entry_point_rejects_bad_arguments():
     need = lib.kda_recurrent_bwd_workspace_bytes(1, 2, 16, 16, f32)
     assert need > 0 and call(ws=a, ws_bytes=need - 1) == _lib.KDA_ERR_WORKSPACE
     assert lib.kda_recurrent_bwd_workspace_bytes(1, 2, 16, 16, _lib.dtype_code(torch.float64)) == 2 * need
+
+
+def test_noalloc_scratch_size_matches_the_header():
+    text = HEADER.read_text()
+    m = re.search(r"#define KDA_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", text)
+    assert m is not None
+    assert int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
