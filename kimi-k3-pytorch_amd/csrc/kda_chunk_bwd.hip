@@ -17,9 +17,16 @@
 //   dA = diag(b) dL, then the pair sums of dA and dAqk with exact exponents,
 //   the exp factors, and dg = reverse cumulative sum of d lg over the chunk.
 //
-// Four kernels, all arithmetic in f32 on the f32 MFMA (v_mfma_f32_16x16x4f32):
-//   prep_kernel   one block per (sequence, head, chunk): A, Aqk (exact pair
-//                 exponents), N by forward substitution, W, U, Kt, Qg, Kg, D;
+// Four kernels with f32 accumulation everywhere.  prep and pair multiply on
+// the f32 MFMA (v_mfma_f32_16x16x4f32); the two state scans and grad's slab
+// products use split-bf16 operands on v_mfma_f32_16x16x32_bf16 (x = hi + lo,
+// hi = bf16(x), lo = bf16(x - hi); hi*hi + hi*lo + lo*hi, dropping terms of
+// relative size 2^-17), which keeps the f32-input gradients within about
+// 1e-5 of the f64 oracle.  Decay products use a 16-row block factorisation
+// on the MFMA, with an exact pairwise-exponent path for chunks whose decays
+// leave its range (any g > 0, or a block decaying past e^-80).
+//   prep_kernel   one block per (sequence, head, chunk): A, Aqk, N by
+//                 forward substitution, W, U, Kt, Qg, Kg, D;
 //   scan_kernel   one block per (sequence, head, 16 state columns) and
 //                 direction: forward, the chunk start states S and the
 //                 pseudo-values Vt; backward, dS' and dVt per chunk and dS0;
