@@ -26,6 +26,8 @@ Metric: "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s".
                workload, on the host cores (thread count reported).
 * fused_stages: the kernels around the operator (kda.fused) on the same
                shape, as HBM GB/s (not part of `value`).
+* decay_fusion: the decay feeding the prefill: gates kernel then chunk
+               kernel, against the chunk kernel forming g from the logits.
 * backward   : the chunkwise backward (all input gradients) on the prefill
                workload, ms and tokens/s (not part of `value`), with the
                oracle's backward on a T=1024 sample as its CPU baseline.
@@ -229,6 +231,60 @@ def bench_fused(reps=50):
                   "rmsnorm_output_gate": "rmsnorm_gate_kernel"}[name]
         res[name] = {"ms": round(ms, 5), "algorithmic_bytes": nbytes, "achieved_gbs": round(gbs, 1),
                      "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kernel)}
+    return res
+
+
+def bench_decay_fusion(reps=20):
+    """The decay feeding the prefill at the long-context shape, two ways:
+    kda_gates_fwd writing g (bf16) followed by kda_chunk_fwd reading it, and
+    kda_chunk_fwd_decay forming g from the logits inside the chunk kernel (g
+    never written or read: 2 x 33.5 MB less traffic).  `reps` back-to-back
+    calls of each through the C ABI, HIP events on the launch stream."""
+    import torch
+
+    from kda import _lib, _prep
+
+    lib = _lib.load()
+    device = torch.device("cuda", 0)
+    q, k, v, _, beta, s0 = _inputs(P_B, P_T, P_H, P_K, P_V, 0.02, 0, device)
+    gen = torch.Generator(device=device).manual_seed(11)
+    z = torch.randn(P_B, P_T, P_H, P_K, generator=gen, device=device).to(torch.bfloat16)
+    zb = (0.5 * torch.randn(P_H, P_K, generator=gen, device=device)).to(torch.bfloat16)
+    a_log = torch.zeros(P_H, device=device)
+    g = torch.empty_like(z)
+    out = torch.empty(P_B, P_T, P_H, P_V, dtype=torch.bfloat16, device=device)
+    s1 = torch.empty(P_B, P_H, P_K, P_V, device=device)
+    code = _lib.dtype_code(torch.bfloat16)
+    total = P_B * P_T
+    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(P_B, total, P_H, P_K, P_V, code)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+    stream = _prep.stream(device)
+    tail = (s0.data_ptr(), s1.data_ptr(), 0, out.data_ptr(), None, P_T, None, P_B, total, P_H, P_K, P_V,
+            ws.data_ptr(), ws_bytes, stream)
+
+    def two_step():
+        _lib.check(lib.kda_gates_fwd(z.data_ptr(), zb.data_ptr(), a_log.data_ptr(), -5.0, g.data_ptr(), None, None,
+                                     None, total, P_H, P_K, code, stream))
+        _lib.check(lib.kda_chunk_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code,
+                                     *tail))
+
+    def fused():
+        _lib.check(lib.kda_chunk_fwd_decay(q.data_ptr(), k.data_ptr(), v.data_ptr(), z.data_ptr(), zb.data_ptr(),
+                                           a_log.data_ptr(), -5.0, beta.data_ptr(), code, *tail))
+
+    res = {"workload": f"decay logits -> prefill B={P_B} T={P_T} H={P_H} K=V={P_K} bf16, f32 state"}
+    for name, fn in (("gates_then_chunk_fwd", two_step), ("chunk_fwd_decay", fused)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        res[name] = {"ms": round(ms, 5), "tokens_per_s": round(total / (ms * 1e-3), 1)}
     return res
 
 
@@ -793,6 +849,7 @@ def main() -> int:
         "workload": f"B={P_B} T={P_T} H={P_H} D={P_K} bf16, 50 back-to-back C-ABI launches each",
         "kernels": bench_fused(),
     }
+    result["decay_fusion"] = bench_decay_fusion()
     result["backward"] = bench_backward()
     result["cache_reorder"] = bench_cache()
     if not args.no_cpu_baseline:

@@ -130,6 +130,30 @@ int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, co
                   size_t workspace_bytes, void* stream);
 
 /*
+ * `kda_chunk_fwd` with the decay formed inside the chunk kernel from the decay
+ * logits, so g never makes a round trip through HBM: the loader waves compute
+ *   g = g_min * clamp(sigmoid(exp(a_log[h]) * (decay_logits + decay_bias[h])), eps, 1 - eps)
+ * (eps of the input type), round it to the input type and take its in-chunk
+ * cumulative sum.  Replaces the chain LowerBoundedDecay.forward
+ * (src/kda/decay.py:36-43, with the bias of src/kda/projections.py:215) ->
+ * chunkwise_kda (src/kda/chunkwise.py:17-107) of KimiDeltaAttention.forward
+ * (src/kda/kda.py:131-151).  The result equals kda_gates_fwd followed by
+ * kda_chunk_fwd bit for bit.
+ *   decay_logits : [tokens, H, K] in in_dtype (in place of g); decay_bias [H, K] or NULL;
+ *   a_log        : f32 [H];  g_min < 0.
+ * The MFMA shapes only (bf16/f16 inputs, K = 128, V a multiple of 16 in
+ * 16..256): other shapes return KDA_ERR_UNSUPPORTED.  Workspace as
+ * kda_chunk_fwd_workspace_bytes.
+ */
+int kda_chunk_fwd_decay(const void* q, const void* k, const void* v, const void* decay_logits,
+                        const void* decay_bias, const float* a_log, double g_min, const void* beta,
+                        int in_dtype, const void* initial_state, void* final_state, int state_dtype,
+                        void* out, const int32_t* cu_seqlens, int64_t dense_span,
+                        const int32_t* valid_lens, int64_t num_seqs, int64_t total_tokens,
+                        int64_t heads, int64_t key_dim, int64_t value_dim, void* workspace,
+                        size_t workspace_bytes, void* stream);
+
+/*
  * `kda_chunk_fwd` for callers that cannot allocate device memory (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * No counterpart in the reference.  Same arguments, checks and kernels as

@@ -180,6 +180,35 @@ int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, co
                       static_cast<hipStream_t>(stream));
 }
 
+int kda_chunk_fwd_decay(const void* q, const void* k, const void* v, const void* decay_logits, const void* decay_bias,
+                        const float* a_log, double g_min, const void* beta, int in_dtype, const void* initial_state,
+                        void* final_state, int state_dtype, void* out, const int32_t* cu_seqlens, int64_t dense_span,
+                        const int32_t* valid_lens, int64_t num_seqs, int64_t total_tokens, int64_t heads,
+                        int64_t key_dim, int64_t value_dim, void* workspace, size_t workspace_bytes, void* stream) {
+  int st = check_common(q, k, v, decay_logits, beta, in_dtype, state_dtype, out, num_seqs, total_tokens, heads,
+                        key_dim, value_dim);
+  if (st != KDA_OK) return st;
+  st = check_seq(cu_seqlens, dense_span, num_seqs, total_tokens);
+  if (st != KDA_OK) return st;
+  if (a_log == nullptr) {
+    set_detail("chunk_fwd_decay: a_log must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!(g_min < 0.0)) {
+    set_detail("chunk_fwd_decay: g_min must be negative");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  const size_t need = chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype);
+  if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
+    set_detail("chunk_fwd_decay needs %zu workspace bytes, got %zu", need, workspace_bytes);
+    return KDA_ERR_WORKSPACE;
+  }
+  kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
+  return launch_chunk_decay(q, k, v, decay_logits, decay_bias, a_log, static_cast<float>(g_min), beta, in_dtype,
+                            initial_state, final_state, state_dtype, out, seq, num_seqs, total_tokens, heads, key_dim,
+                            value_dim, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
+}
+
 int kda_chunk_fwd_profiled(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
                            const void* initial_state, void* final_state, int state_dtype, void* out,
                            const int32_t* cu_seqlens, int64_t dense_span, const int32_t* valid_lens, int64_t num_seqs,

@@ -292,7 +292,48 @@ struct SegArgs {
   bf16* chunk_ma;  // [chunk][h] M and Aqk fragments (kMaBytes), or nullptr
   int64_t N, H, V;
   int32_t L;
+  // kernels that form g from decay logits (DECAY): `g` then points at the
+  // logits z [tokens, H, K], and g = lower_bounded_decay(z + zbias[h],
+  // exp(a_log[h]), g_min, clamp to [g_lo, g_hi]), rounded to the input type
+  const IT* __restrict__ zbias;  // [H, K] or nullptr
+  const float* __restrict__ a_log;  // [H]
+  float g_min, g_lo, g_hi;
 };
+
+// Per-loader constants of the decay formed from logits: the bias of the
+// thread's two channels, the head's scale exp(A_log[h]) and the clamp bounds.
+struct DecayConsts {
+  float b[2];
+  float scale, g_min, lo, hi;
+};
+
+template <class IT, bool DECAY>
+__device__ __forceinline__ DecayConsts decay_consts(const SegArgs<IT>& a, int64_t h, int cp) {
+  DecayConsts d{};
+  if constexpr (DECAY) {
+#pragma unroll
+    for (int ch = 0; ch < 2; ++ch) d.b[ch] = a.zbias ? to_float(a.zbias[h * kKey + 2 * cp + ch]) : 0.f;
+    d.scale = fexp(a.a_log[h]);
+    d.g_min = a.g_min;
+    d.lo = a.g_lo;
+    d.hi = a.g_hi;
+  }
+  return d;
+}
+
+// g of one row and channel: the raw value, or (DECAY) the decay formed from
+// its logit and rounded to the input type, as the gates kernel stores it;
+// rows past the valid tokens decay by nothing (the operator mask,
+// src/kda/utils.py:82-94)
+template <class IT, bool DECAY>
+__device__ __forceinline__ float g_value(float raw, const DecayConsts& d, int ch, bool valid) {
+  if constexpr (DECAY) {
+    const float gg = lower_bounded_decay(raw, d.b[ch], d.scale, d.g_min, d.lo, d.hi);
+    return valid ? to_float(from_compute<IT>(gg)) : 0.f;
+  } else {
+    return raw;
+  }
+}
 
 // Chunk and segment maps: the arrays of chunk_map_kernel for packed
 // documents, a closed form for dense sequences (every sequence has the same
@@ -546,10 +587,12 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, bf16x2_t{(bf16)lo, (bf16)hi});
 }
 
-template <class IT, int MODE>
-__device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const ChunkGeo& cg, int vcg, int tid) {
+template <class IT, int MODE, bool DECAY>
+__device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const ChunkGeo& cg, int vcg, int tid,
+                                        const DecayConsts& dc) {
   // rows past the chunk's valid tokens were read as zero (g = 0, k = q = 0),
-  // so they give a unit decay and zero operands without a test
+  // so they give a unit decay and zero operands without a test (a decay
+  // formed from logits is zeroed there explicitly)
   const int J = loader_block(tid);
   const int lane = tid & 63;
   float al[2][16];
@@ -558,7 +601,7 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
   for (int r = 0; r < 16; ++r) {
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
-      al[ch][r] = fast_exp(to_float(raw.gp[r][ch]));
+      al[ch][r] = fast_exp(g_value<IT, DECAY>(to_float(raw.gp[r][ch]), dc, ch, 16 * J + r < cg.n_valid));
       if (r > 0) pj[ch] *= al[ch][r];
     }
   }
@@ -739,8 +782,9 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
 // with the block products of the other three blocks of its channels taken
 // from the lanes that hold them.  Rows past the chunk's valid tokens were read
 // as zero (g = 0, k = q = 0), so they give zero operands and a unit decay.
-template <class IT>
-__device__ __forceinline__ void p1_math_ma(P1Out& po, const Raw<IT>& raw, int tid) {
+template <class IT, bool DECAY>
+__device__ __forceinline__ void p1_math_ma(P1Out& po, const Raw<IT>& raw, int tid, int n_valid,
+                                           const DecayConsts& dc) {
   const int J = loader_block(tid);
   const int lane = tid & 63;
   float al[2][16];
@@ -749,7 +793,7 @@ __device__ __forceinline__ void p1_math_ma(P1Out& po, const Raw<IT>& raw, int ti
   for (int r = 0; r < 16; ++r) {
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) {
-      al[ch][r] = fast_exp(to_float(raw.gp[r][ch]));
+      al[ch][r] = fast_exp(g_value<IT, DECAY>(to_float(raw.gp[r][ch]), dc, ch, 16 * J + r < n_valid));
       if (r > 0) pj[ch] *= al[ch][r];
     }
   }
@@ -847,7 +891,7 @@ __device__ __forceinline__ void p1_write_ma(unsigned char* sm, const P1Out& po, 
 
 // Everything after P1 (reads only LDS, plus global q/k/g on the rare
 // extreme-decay path).
-template <class IT, int MODE, bool LOADER>
+template <class IT, int MODE, bool LOADER, bool DECAY>
 __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h,
                                             int vcg, int tid, const NextLoads<IT, MODE>& nl) {
   const int lane = tid & 63;
@@ -1054,12 +1098,16 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
     const int64_t krow = a.H * kKey;
     if (wave < 4) {
       const int J = wave, cp = lane;
+      const DecayConsts dc = decay_consts<IT, DECAY>(a, h, cp);
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch) {
         float run = 0.f;
         for (int r = 0; r < 16; ++r) {
           const int tl = 16 * J + r;
-          const float gvv = tl < n_valid ? to_float(a.g[(cg.tok0 + tl) * krow + h * kKey + 2 * cp + ch]) : 0.f;
+          const float gvv =
+              tl < n_valid
+                  ? g_value<IT, DECAY>(to_float(a.g[(cg.tok0 + tl) * krow + h * kKey + 2 * cp + ch]), dc, ch, true)
+                  : 0.f;
           if (r > 0) run += gvv;
           Lr[tl * kKey + 2 * cp + ch] = run;
         }
@@ -1377,7 +1425,7 @@ __device__ __forceinline__ void store_out(const f32x4_t (&O)[2][4], int ntile, I
 // tiles]).  Waves 4-7 (loaders) hold the raw inputs of the next chunk.  The
 // two roles run separate loops with the same barriers, so neither role's
 // registers are live in the other's code.
-template <class IT, int MODE>
+template <class IT, int MODE, bool DECAY>
 __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<IT> a) {
   extern __shared__ __align__(16) unsigned char sm[];
   // one-dimensional grid, segment slowest: the workgroups past the real
@@ -1476,7 +1524,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       // where they would stay live (and spill) next to the state tiles
       const int tid_c = opaque(tid);
       p1_write<MODE, false>(sm, none, nullptr, tid_c);
-      prepare_mid<IT, MODE, false>(sm, a, geo, h, vcg, tid_c, nl);
+      prepare_mid<IT, MODE, false, DECAY>(sm, a, geo, h, vcg, tid_c, nl);
       prepare_m<IT, MODE, false>(sm, tid_c, nl);
 #pragma unroll
       for (int pp = 0; pp < kPairs; ++pp) {
@@ -1500,9 +1548,11 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
     Raw<IT> raw;
     P1Out po;
     const LoaderLanes ll = loader_lanes<IT>(a, vcg, tid);
+    const DecayConsts dc = decay_consts<IT, DECAY>(a, h, loader_pair(tid));
     if (c_begin < c_end) {
-      load_raw<IT, MODE>(raw, chunk_loads<IT>(a, chunk_geo(sr, c_begin - cs), c_begin, h, col0), ll, tid);
-      p1_math_ma<IT>(po, raw, tid);
+      const ChunkGeo g0 = chunk_geo(sr, c_begin - cs);
+      load_raw<IT, MODE>(raw, chunk_loads<IT>(a, g0, c_begin, h, col0), ll, tid);
+      p1_math_ma<IT, DECAY>(po, raw, tid, g0.n_valid, dc);
     }
     for (int64_t c = c_begin; c < c_end; ++c) {
       const int tid_c = opaque(tid);
@@ -1512,7 +1562,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       __syncthreads();
       nl.template load_part<6>();
       nl.template load_part<7>();
-      if (c + 1 < c_end) p1_math_ma<IT>(po, raw, tid_c);
+      if (c + 1 < c_end) p1_math_ma<IT, DECAY>(po, raw, tid_c, chunk_geo(sr, c + 1 - cs).n_valid, dc);
       __syncthreads();
     }
   } else {
@@ -1527,10 +1577,11 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
     Raw<IT> raw;
     P1Out po;
     const LoaderLanes ll = loader_lanes<IT>(a, vcg, tid);
+    const DecayConsts dc = decay_consts<IT, DECAY>(a, h, loader_pair(tid));
     if (c_begin < c_end) {
       const ChunkGeo g0 = chunk_geo(sr, c_begin - cs);
       load_raw<IT, MODE>(raw, chunk_loads<IT>(a, g0, c_begin, h, col0), ll, tid);
-      p1_math<IT, MODE>(po, raw, g0, vcg, tid);
+      p1_math<IT, MODE, DECAY>(po, raw, g0, vcg, tid, dc);
     }
     for (int64_t c = c_begin; c < c_end; ++c) {
       const ChunkGeo geo = chunk_geo(sr, c - cs);
@@ -1538,7 +1589,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       p1_write<MODE, true>(sm, po, &ll, tid_c);
       const NextLoads<IT, MODE> nl{&raw, chunk_loads<IT>(a, chunk_geo(sr, c + 1 - cs), c + 1, h, col0, c + 1 < c_end),
                                    &ll, tid_c};
-      prepare_mid<IT, MODE, true>(sm, a, geo, h, vcg, tid_c, nl);
+      prepare_mid<IT, MODE, true, DECAY>(sm, a, geo, h, vcg, tid_c, nl);
       prepare_m<IT, MODE, true>(sm, tid_c, nl);
       if constexpr (MODE == kSummary) {
         // hand the chunk's M and Aqk fragments to phase C (one column group
@@ -1554,7 +1605,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
           }
         }
       }
-      if (c + 1 < c_end) p1_math<IT, MODE>(po, raw, chunk_geo(sr, c + 1 - cs), vcg, tid_c);
+      if (c + 1 < c_end) p1_math<IT, MODE, DECAY>(po, raw, chunk_geo(sr, c + 1 - cs), vcg, tid_c, dc);
       __syncthreads();
     }
   }
@@ -1778,26 +1829,34 @@ static void mark(kda_host::KernelEvents* ev, int i, hipStream_t stream) {
   }
 }
 
-template <class IT, int MODE>
+template <class IT, int MODE, bool DECAY>
 static int launch_segments(const SegArgs<IT>& sa, const Plan& p, int64_t H, hipStream_t stream) {
   static bool attr_done = false;
   if (!attr_done) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_segment_kernel<IT, MODE>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_segment_kernel<IT, MODE, DECAY>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes) != hipSuccess) {
       kda_host::set_detail("cannot reserve %d bytes of LDS for chunk_segment_kernel", kSmemBytes);
       return KDA_ERR_LAUNCH;
     }
     attr_done = true;
   }
-  hipLaunchKernelGGL((chunk_segment_kernel<IT, MODE>), dim3(static_cast<unsigned>(p.segs_bound * H * p.ncg)),
+  hipLaunchKernelGGL((chunk_segment_kernel<IT, MODE, DECAY>), dim3(static_cast<unsigned>(p.segs_bound * H * p.ncg)),
                      dim3(kThreads), kSmemBytes, stream, sa);
   return kda_host::check_launch(MODE == kSummary ? "chunk_segment_kernel<summary>" : "chunk_segment_kernel<output>");
 }
 
-template <class IT>
+// Decay formed in the kernel from logits (kda_chunk_fwd_decay); null for a g input.
+struct DecayInput {
+  const void* zbias;
+  const float* a_log;
+  float g_min;
+};
+
+template <class IT, bool DECAY>
 static int run_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, const void* s_in,
                      void* s_out, void* out, const SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
-                     int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev) {
+                     int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev,
+                     const DecayInput* decay) {
   const Plan p = make_plan(N, total_tokens, H, V);
   int32_t* chunk_start = static_cast<int32_t*>(workspace);
   int32_t* seg_start = chunk_start + (N + 1);
@@ -1832,6 +1891,19 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
   sa.H = H;
   sa.V = V;
   sa.L = p.L;
+  sa.zbias = nullptr;
+  sa.a_log = nullptr;
+  sa.g_min = 0.f;
+  sa.g_lo = sa.g_hi = 0.f;
+  if (DECAY) {
+    // eps of the input type, as torch.finfo gives it (src/kda/decay.py:40)
+    const float eps = __is_same(IT, bf16) ? 0.0078125f : 0.0009765625f;
+    sa.zbias = static_cast<const IT*>(decay->zbias);
+    sa.a_log = decay->a_log;
+    sa.g_min = decay->g_min;
+    sa.g_lo = eps;
+    sa.g_hi = 1.f - eps;
+  }
 
   mark(ev, 0, stream);
   int st = KDA_OK;
@@ -1843,7 +1915,7 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
   }
   mark(ev, 1, stream);
   if (p.segmented) {
-    st = launch_segments<IT, kSummary>(sa, p, H, stream);
+    st = launch_segments<IT, kSummary, DECAY>(sa, p, H, stream);
     if (st != KDA_OK) return st;
     mark(ev, 2, stream);
     CombineArgs ca{sa.seg_start, sa.dense_segs, sa.seg_state, sa.seg_q, sa.seg_p, N, H, V};
@@ -1858,7 +1930,8 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
     mark(ev, 3, stream);
     if (ev != nullptr) ev->empty |= 6u;  // one segment per sequence: no summaries, no combine
   }
-  st = p.segmented ? launch_segments<IT, kOutputMA>(sa, p, H, stream) : launch_segments<IT, kOutput>(sa, p, H, stream);
+  st = p.segmented ? launch_segments<IT, kOutputMA, DECAY>(sa, p, H, stream)
+                   : launch_segments<IT, kOutput, DECAY>(sa, p, H, stream);
   mark(ev, 4, stream);
   return st;
 }
@@ -1909,8 +1982,37 @@ int launch_chunk(const void* q, const void* k, const void* v, const void* g, con
     return KDA_ERR_UNSUPPORTED;
   }
   if (in_dtype == KDA_DTYPE_BF16)
-    return run_chunk<bf16>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream, ev);
-  return run_chunk<f16>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream, ev);
+    return run_chunk<bf16, false>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream,
+                                  ev, nullptr);
+  return run_chunk<f16, false>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream, ev,
+                               nullptr);
+}
+
+int launch_chunk_decay(const void* q, const void* k, const void* v, const void* z, const void* zbias,
+                       const float* a_log, float g_min, const void* beta, int in_dtype, const void* s_in, void* s_out,
+                       int state_dtype, void* out, const kda::SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
+                       int64_t K, int64_t V, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  using namespace kda;
+  if (!mfma_path(in_dtype, state_dtype, K, V)) {
+    set_detail("chunk_fwd_decay: the fused decay needs the MFMA path (bf16/f16 inputs, f32 state, K = 128, V a "
+               "multiple of 16 in 16..256); form g with kda_gates_fwd and call kda_chunk_fwd");
+    return KDA_ERR_UNSUPPORTED;
+  }
+  if (workspace_bytes < chunk_workspace_bytes(N, total_tokens, H, K, V, in_dtype)) {
+    set_detail("chunk_fwd_decay: workspace too small");
+    return KDA_ERR_WORKSPACE;
+  }
+  const Plan p = make_plan(N, total_tokens, H, V);
+  if (H > 65535 || p.segs_bound * H * p.ncg > 0x7fffffffLL || N > 0x7fffffffLL) {
+    set_detail("chunk_fwd_decay: grid too large (N=%lld, H=%lld)", (long long)N, (long long)H);
+    return KDA_ERR_UNSUPPORTED;
+  }
+  const DecayInput d{zbias, a_log, g_min};
+  if (in_dtype == KDA_DTYPE_BF16)
+    return run_chunk<bf16, true>(q, k, v, z, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream,
+                                 nullptr, &d);
+  return run_chunk<f16, true>(q, k, v, z, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream,
+                              nullptr, &d);
 }
 
 }  // namespace kda_host

@@ -27,6 +27,39 @@ template <> __device__ __forceinline__ f16 from_compute<f16, float>(float x) { r
 __device__ __forceinline__ float fast_exp(float x) { return __expf(x); }
 __device__ __forceinline__ double fast_exp(double x) { return exp(x); }
 
+// exp, reciprocal and reciprocal square root of the gate and norm stages: the
+// hardware's f32 instructions (v_exp_f32 on x*log2(e), v_rcp_f32, v_rsq_f32;
+// about 1 ulp) and the library's correctly rounded routines in f64.
+__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
+__device__ __forceinline__ double fexp(double x) { return exp(x); }
+__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
+__device__ __forceinline__ double frcp(double x) { return 1.0 / x; }
+__device__ __forceinline__ float frsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
+__device__ __forceinline__ double frsqrt(double x) { return 1.0 / sqrt(x); }
+
+template <class C>
+__device__ __forceinline__ C sigmoid(C x) {
+  return frcp(C(1) + fexp(-x));
+}
+
+// The lower-bounded decay of one element (src/kda/decay.py:36-43 with the
+// decay-logit bias of src/kda/projections.py:215):
+//   g = g_min * clamp(sigmoid(scale * (z + b)), lo, hi),  scale = exp(A_log[h]),
+// lo = eps, hi = 1 - eps of the output type.  One definition for the gates
+// kernel and the chunk kernel that forms g from the logits itself, so both
+// produce the same bits.
+template <class C>
+__device__ __forceinline__ C lower_bounded_decay(C z, C b, C scale, C g_min, C lo, C hi) {
+  C p = sigmoid(scale * (z + b));
+  p = p < lo ? lo : (p > hi ? hi : p);
+  C g = g_min * p;
+  // keep the product an f32 value: otherwise the compiler may merge it with
+  // the caller's conversion to f16 into one mixed-precision FMA (a single
+  // rounding) in one kernel and not in another
+  if constexpr (sizeof(C) == 4) asm volatile("" : "+v"(g));
+  return g;
+}
+
 // ---- sequences ------------------------------------------------------------
 // A "sequence" is a run of tokens that share one recurrent state: a batch row
 // of a dense [B,T,...] call (start = s*T) or a packed document

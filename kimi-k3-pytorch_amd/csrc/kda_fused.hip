@@ -19,22 +19,6 @@ struct ComputeOf<double> {
   using type = double;
 };
 
-// exp, reciprocal and reciprocal square root: the hardware's f32
-// instructions (v_exp_f32 on x*log2(e), v_rcp_f32, v_rsq_f32; about 1 ulp,
-// far below the 16-bit output rounding and the f32 tolerance of 1e-5), and
-// the library's correctly rounded routines in f64.
-__device__ __forceinline__ float fexp(float x) { return __builtin_amdgcn_exp2f(x * 1.4426950408889634f); }
-__device__ __forceinline__ double fexp(double x) { return exp(x); }
-__device__ __forceinline__ float frcp(float x) { return __builtin_amdgcn_rcpf(x); }
-__device__ __forceinline__ double frcp(double x) { return 1.0 / x; }
-__device__ __forceinline__ float frsqrt(float x) { return __builtin_amdgcn_rsqf(x); }
-__device__ __forceinline__ double frsqrt(double x) { return 1.0 / sqrt(x); }
-
-template <class C>
-__device__ __forceinline__ C sigmoid(C x) {
-  return frcp(C(1) + fexp(-x));
-}
-
 // Blocks b and b + 8 run on the same XCD (the dispatcher deals blocks to the
 // eight XCDs in turn); this renumbering gives each XCD one contiguous range
 // of logical blocks, so neighbouring tiles share their XCD's L2.
@@ -254,9 +238,7 @@ __global__ __launch_bounds__(256) void gates_kernel(const GateArgs<T> a) {
           vec_t gv, av;
 #pragma unroll
           for (int e = 0; e < VEC; ++e) {
-            C p = sigmoid(scale * (to_compute<C>(zv[u][e]) + to_compute<C>(bv[e])));
-            p = p < lo ? lo : (p > hi ? hi : p);
-            const C gg = C(a.g_min) * p;
+            const C gg = lower_bounded_decay(to_compute<C>(zv[u][e]), to_compute<C>(bv[e]), scale, C(a.g_min), lo, hi);
             gv[e] = from_compute<T>(gg);
             av[e] = from_compute<T>(fexp(gg));
           }

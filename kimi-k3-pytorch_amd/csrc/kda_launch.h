@@ -37,6 +37,13 @@ int launch_chunk(const void* q, const void* k, const void* v, const void* g, con
                  int64_t total_tokens, int64_t H, int64_t K, int64_t V, void* workspace, size_t workspace_bytes,
                  hipStream_t stream, KernelEvents* events = nullptr);
 
+// The prefill with g formed inside the chunk kernel from decay logits
+// (lower-bounded decay of the logits plus bias); MFMA shapes only.
+int launch_chunk_decay(const void* q, const void* k, const void* v, const void* z, const void* zbias,
+                       const float* a_log, float g_min, const void* beta, int in_dtype, const void* s_in, void* s_out,
+                       int state_dtype, void* out, const kda::SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
+                       int64_t K, int64_t V, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 int launch_ut_transform(const void* k, const void* v, const void* g, const void* beta, int in_dtype, void* M,
                         void* U, void* W, void* log_gamma, void* k_gamma, int out_dtype, int64_t batch,
                         int64_t count, int64_t heads, int64_t key_dim, int64_t value_dim, hipStream_t stream);

@@ -51,6 +51,11 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P, _S, _P],
     ),
+    "kda_chunk_fwd_decay": (
+        _I,
+        [_P, _P, _P, _P, _P, _P, ctypes.c_double, _P, _I, _P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P, _S,
+         _P],
+    ),
     "kda_chunk_fwd_noalloc": (
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P],

@@ -8,6 +8,9 @@
 * ``lower_bounded_decay`` / ``beta_gate``: LowerBoundedDecay
   (src/kda/decay.py:30-43, with the decay-logit bias of
   projections.py:211-218) and the beta gate (projections.py:207-209).
+* ``chunkwise_kda_with_decay``: the decay and the chunkwise operator in one
+  pass, g formed from the logits inside the chunk kernel (no HBM round trip
+  of g).
 * ``rmsnorm_gate``: HeadwiseRMSNorm (src/kimi_primitives/headwise_rmsnorm.py:39-64)
   times the sigmoid output gate (src/kimi_primitives/output_gate.py:62-75),
   i.e. the input of the output projection.
@@ -192,6 +195,81 @@ def beta_gate(logits: torch.Tensor) -> torch.Tensor:
     return beta
 
 
+def chunkwise_kda_with_decay(
+    q: torch.Tensor,
+    k: torch.Tensor,
+    v: torch.Tensor,
+    decay_logits: torch.Tensor,
+    a_log: torch.Tensor,
+    beta: torch.Tensor,
+    *,
+    decay_bias: torch.Tensor | None = None,
+    g_min: float = -5.0,
+    initial_state: torch.Tensor | None = None,
+    output_final_state: bool = False,
+    attention_mask: torch.Tensor | None = None,
+    accumulate_state_in_fp32: bool = True,
+    cu_seqlens: torch.Tensor | list[int] | None = None,
+):
+    """``chunkwise_kda(q, k, v, g, beta, ...)`` with ``g = lower_bounded_decay(
+    decay_logits, a_log, g_min, bias=decay_bias)[0]`` (src/kda/decay.py:36-43,
+    src/kda/kda.py:131-151), the decay formed inside the chunk kernel so that g
+    never makes a round trip through HBM.  The result equals the two-step
+    composition bit for bit.  Shapes off the MFMA path (K != 128, V not a
+    multiple of 16 in 16..256, f32/f64 inputs) and calls under autograd run the
+    two steps (both in HIP kernels); so does f16/bf16 work without an f32 state."""
+    from .chunkwise import chunkwise_kda, needs_grad
+    from .recurrent import KDAOperatorOutput
+    from .utils import accumulation_dtype, validate_core_inputs, validate_cu_seqlens
+
+    offsets = None
+    if cu_seqlens is not None:
+        offsets = validate_cu_seqlens(cu_seqlens, q.shape[0] if q.ndim == 4 else -1,
+                                      q.shape[1] if q.ndim == 4 else -1, attention_mask)
+    num_states = None if offsets is None else len(offsets) - 1
+    batch, tokens, heads, key_dim, value_dim = validate_core_inputs(
+        q, k, v, decay_logits, beta, initial_state, attention_mask, num_states=num_states)
+    _lib.require_gpu(q)
+    if a_log.shape != (heads,):
+        raise ValueError(f"A_log must have shape [{heads}], got {tuple(a_log.shape)}")
+    if decay_bias is not None and decay_bias.shape != (heads, key_dim):
+        raise ValueError(f"bias must have shape [{heads},{key_dim}], got {tuple(decay_bias.shape)}")
+    if g_min >= 0:
+        raise ValueError("g_min must be negative")
+    work_dtype = accumulation_dtype(v.dtype, accumulate_state_in_fp32)
+    dtypes = {t.dtype for t in (q, k, v, decay_logits, beta)}
+    fused_ok = (len(dtypes) == 1 and q.dtype in (torch.bfloat16, torch.float16) and work_dtype == torch.float32
+                and key_dim == 128 and value_dim % 16 == 0 and 16 <= value_dim <= 256
+                and not needs_grad(q, k, v, decay_logits, beta, initial_state, a_log, decay_bias))
+    if not fused_ok:
+        g, _ = lower_bounded_decay(decay_logits, a_log, g_min, bias=decay_bias)
+        return chunkwise_kda(q, k, v, g, beta, initial_state, output_final_state, attention_mask,
+                             accumulate_state_in_fp32=accumulate_state_in_fp32, cu_seqlens=cu_seqlens)
+    lib = _lib.load()
+    device = q.device
+    qc, kc, vc, zc, bc = (t.contiguous() for t in (q, k, v, decay_logits, beta))
+    zb = None if decay_bias is None else decay_bias.to(device=device, dtype=q.dtype).contiguous()
+    al = a_log.to(device=device, dtype=torch.float32).contiguous()
+    n_seq = batch if offsets is None else len(offsets) - 1
+    total = batch * tokens
+    s_in = _prep.state_arg(initial_state, torch.float32)
+    s_out = (torch.empty(n_seq, heads, key_dim, value_dim, dtype=torch.float32, device=device)
+             if output_final_state else None)
+    out = torch.empty(batch, tokens, heads, value_dim, dtype=q.dtype, device=device)
+    cu = None if offsets is None else _prep.cu_tensor(offsets, device)
+    valid = _prep.valid_lengths(attention_mask, device)
+    code = _lib.dtype_code(q.dtype)
+    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, total, heads, key_dim, value_dim, code)
+    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+    _lib.check(lib.kda_chunk_fwd_decay(
+        qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), zc.data_ptr(), _lib.ptr(zb), al.data_ptr(), float(g_min),
+        bc.data_ptr(), code, _lib.ptr(s_in), _lib.ptr(s_out), _lib.dtype_code(torch.float32), out.data_ptr(),
+        _lib.ptr(cu), tokens, _lib.ptr(valid), n_seq, total, heads, key_dim, value_dim, _lib.ptr(workspace),
+        ws_bytes, _prep.stream(device)))
+    hidden = out if out.dtype == v.dtype else out.to(v.dtype)
+    return KDAOperatorOutput(hidden_states=hidden, final_state=s_out)
+
+
 def rmsnorm_gate(
     x: torch.Tensor,
     weight: torch.Tensor | None = None,
@@ -238,4 +316,4 @@ def rmsnorm_gate(
     return y
 
 
-__all__ = ["beta_gate", "conv_silu", "lower_bounded_decay", "rmsnorm_gate"]
+__all__ = ["beta_gate", "chunkwise_kda_with_decay", "conv_silu", "lower_bounded_decay", "rmsnorm_gate"]

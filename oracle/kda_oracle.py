@@ -28,6 +28,10 @@ CPU baseline, but the code is written independently:
 * ``beta_gate``            follows ``src/kda/projections.py:207-209``
 * ``rmsnorm_gate``         follows ``src/kimi_primitives/headwise_rmsnorm.py:39-64``
   and the gate product of ``src/kimi_primitives/output_gate.py:62-75``
+* ``kda_layer``            follows ``KimiDeltaAttention.forward`` (``src/kda/kda.py:98-183``)
+  over ``src/kda/projections.py:144-225``: the stages above composed with
+  the operator, in the reference's dtype flow (each stage's result in the
+  activation dtype)
 * ``gather_rows``          follows ``KDAState.reorder`` / ``clone``
   (``src/kda/state.py:41-67``) taken over every layer by
   ``src/hybrid_backbone/cache.py:56-61,112-126``
@@ -494,3 +498,59 @@ def gather_rows(arrays, index=None):
             dst[r] = src[i]
         out.append(dst.view(a.dtype).reshape((len(rows),) + a.shape[1:]))
     return out
+
+
+# ---- the layer around the operator -------------------------------------------
+
+def kda_layer(w, x, attention_mask=None, state=None, mode="chunkwise", output_final_state=False):
+    """KimiDeltaAttention.forward (src/kda/kda.py:98-183, diagnostics left out)
+    with the projections of KDAProjections.forward (src/kda/projections.py:144-225).
+
+    ``w`` is a dict with the fields of ``kda.layer.KDALayerWeights`` (linear
+    weights ``[out, in]``, ShortConv weights ``[C, K_conv]`` in lag order, ...);
+    ``state`` is ``(recurrent [B,H,K,V], q_hist, k_hist, v_hist, offset [B])`` or
+    None.  Each stage's result is rounded to the activation dtype as the
+    reference's modules return it; arithmetic inside a stage is f32 (f64 for
+    f64).  Returns (output [B,T,d_model], next state tuple or None)."""
+    dt = x.dtype
+    cd = _compute_dtype(dt)
+
+    def lin(inp, weight, bias=None):
+        out = torch.nn.functional.linear(inp.to(cd), weight.to(cd), None if bias is None else bias.to(cd))
+        return out.to(dt)
+
+    batch, tokens, _ = x.shape
+    heads, kd, vd = w["num_heads"], w["key_head_dim"], w["value_head_dim"]
+    return_state = output_final_state or mode == "decode"
+    hists = (None, None, None) if state is None else state[1:4]
+    convs = []
+    for name, hist, norm in (("q", hists[0], True), ("k", hists[1], True), ("v", hists[2], False)):
+        y, nxt = conv_silu(lin(x, w[f"{name}_proj"], w.get(f"{name}_proj_bias")), w[f"{name}_conv"].to(dt),
+                           w.get(f"{name}_conv_bias"), hist, attention_mask, num_heads=heads, normalize=norm,
+                           eps=w["eps"])
+        convs.append((y.to(dt).reshape(batch, tokens, heads, -1), nxt))
+    (q, qn), (k, kn), (v, vn) = convs
+    beta = beta_gate(lin(x, w["beta_proj"], w.get("beta_bias"))).to(dt)
+    z = lin(lin(x, w["alpha_down"]), w["alpha_up"]).reshape(batch, tokens, heads, kd)
+    g, _ = lower_bounded_decay(z, w["a_log"], w["g_min"], bias=w["b_alpha"].to(dt))
+    g = g.to(dt)
+    initial = None if state is None else state[0]
+    acc32 = w.get("accumulate_state_in_fp32", True)
+    if mode == "chunkwise":
+        core, final = chunkwise(q, k, v, g, beta, initial, attention_mask, chunk_size=w.get("chunk_size", 64),
+                                secondary_tile_size=w.get("secondary_tile_size", 16), accumulate_state_in_fp32=acc32)
+    else:
+        core, final, _ = recurrent(q, k, v, g, beta, initial, attention_mask, accumulate_state_in_fp32=acc32)
+    norm_w = w.get("norm_weight")
+    gated = rmsnorm_gate(core.to(dt), None if norm_w is None else norm_w.to(dt), w["eps"],
+                         gate_logits=lin(x, w["gate_proj"], w.get("gate_bias"))).to(dt)
+    out = lin(gated.reshape(batch, tokens, heads * vd), w["output_proj"], w.get("output_bias"))
+    if attention_mask is not None:
+        out = out * attention_mask[..., None].to(dt)
+    nxt = None
+    if return_state:
+        lengths = (torch.full((batch,), tokens, dtype=torch.long) if attention_mask is None
+                   else attention_mask.sum(dim=1).to(torch.long))
+        offset = lengths if state is None else state[4] + lengths
+        nxt = (final, qn, kn, vn, offset)
+    return out, nxt

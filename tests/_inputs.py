@@ -47,3 +47,37 @@ def rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
     scale = e.abs().max().item()
     diff = (a - e).abs().max().item()
     return diff / scale if scale > 0 else diff
+
+
+def layer_weights(d_model, heads, key_dim, value_dim, *, conv=4, rank=None, dtype=torch.float64, seed=17, std=0.1,
+                  biases=False):
+    """Seeded parameters of one KDA layer as a dict with the fields of
+    ``kda.layer.KDALayerWeights`` (the reference's layouts,
+    src/kda/projections.py:35-103, src/kda/decay.py:24-26, src/kda/kda.py:50-62).
+    Linear weights N(0, std); ShortConv weights N(0, 0.3); b_alpha by the
+    reference's FLA recipe (log-uniform dt in [1e-3, 1e-1], inverse softplus,
+    projections.py:90-101); A_log = 0.1 N(0,1); RMSNorm weight 1 + 0.1 N(0,1)."""
+    import math
+
+    gen = torch.Generator().manual_seed(seed)
+    rank = value_dim if rank is None else rank
+    kw, vw = heads * key_dim, heads * value_dim
+    rnd = lambda *shape, s=std: (torch.randn(*shape, generator=gen, dtype=torch.float64) * s).to(dtype)  # noqa: E731
+    dt = torch.exp(torch.rand(heads, key_dim, generator=gen, dtype=torch.float64)
+                   * (math.log(0.1) - math.log(0.001)) + math.log(0.001)).clamp_min(1e-4)
+    w = dict(
+        num_heads=heads, key_head_dim=key_dim, value_head_dim=value_dim,
+        q_proj=rnd(kw, d_model), k_proj=rnd(kw, d_model), v_proj=rnd(vw, d_model),
+        q_conv=rnd(kw, conv, s=0.3), k_conv=rnd(kw, conv, s=0.3), v_conv=rnd(vw, conv, s=0.3),
+        beta_proj=rnd(heads, d_model), alpha_down=rnd(rank, d_model), alpha_up=rnd(kw, rank),
+        b_alpha=(dt + torch.log(-torch.expm1(-dt))).to(dtype),
+        a_log=(0.1 * torch.randn(heads, generator=gen, dtype=torch.float64)).float(),
+        norm_weight=(1 + 0.1 * torch.randn(heads, value_dim, generator=gen, dtype=torch.float64)).to(dtype),
+        gate_proj=rnd(d_model, d_model), output_proj=rnd(d_model, d_model),
+        g_min=-5.0, eps=1e-6,
+    )
+    if biases:
+        w.update(q_proj_bias=rnd(kw), k_proj_bias=rnd(kw), v_proj_bias=rnd(vw), q_conv_bias=rnd(kw),
+                 k_conv_bias=rnd(kw), v_conv_bias=rnd(vw), beta_bias=rnd(heads), gate_bias=rnd(d_model),
+                 output_bias=rnd(d_model))
+    return w
