@@ -26,6 +26,7 @@ Metric: "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s".
                workload, on the host cores (thread count reported).
 * fused_stages: the kernels around the operator (kda.fused) on the same
                shape, as HBM GB/s (not part of `value`).
+* prefill_k64: the prefill at the gpu_48gb head shape (K = V = 64).
 * decay_fusion: the decay feeding the prefill: gates kernel then chunk
                kernel, against the chunk kernel forming g from the logits.
 * backward   : the chunkwise backward (all input gradients) on the prefill
@@ -93,24 +94,25 @@ def _inputs(B, T, H, K, V, state_std, seed, device):
     return dev(q), dev(k), dev(v), dev(g), dev(beta), dev(state)
 
 
-def bench_prefill(steps, warmup):
+def bench_prefill(steps, warmup, shape=(P_B, P_T, P_H, P_K, P_V)):
     import torch
 
     from kda import _lib
 
     lib = _lib.load()
     device = torch.device("cuda", 0)
-    q, k, v, g, beta, s0 = _inputs(P_B, P_T, P_H, P_K, P_V, 0.02, 0, device)
-    total = P_B * P_T
-    out = torch.empty(P_B, P_T, P_H, P_V, dtype=torch.bfloat16, device=device)
-    s_out = torch.empty(P_B, P_H, P_K, P_V, dtype=torch.float32, device=device)
+    B, T, H, K, V = shape
+    q, k, v, g, beta, s0 = _inputs(B, T, H, K, V, 0.02, 0, device)
+    total = B * T
+    out = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=device)
+    s_out = torch.empty(B, H, K, V, dtype=torch.float32, device=device)
     code = _lib.dtype_code(torch.bfloat16)
-    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(P_B, total, P_H, P_K, P_V, code)
+    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(B, total, H, K, V, code)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device).cuda_stream
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code,
-            s0.data_ptr(), s_out.data_ptr(), 0, out.data_ptr(), None, P_T, None,
-            P_B, total, P_H, P_K, P_V, ws.data_ptr(), ws_bytes, stream)
+            s0.data_ptr(), s_out.data_ptr(), 0, out.data_ptr(), None, T, None,
+            B, total, H, K, V, ws.data_ptr(), ws_bytes, stream)
 
     def step():
         _lib.check(lib.kda_chunk_fwd(*args))
@@ -848,6 +850,18 @@ def main() -> int:
     result["fused_stages"] = {
         "workload": f"B={P_B} T={P_T} H={P_H} D={P_K} bf16, 50 back-to-back C-ABI launches each",
         "kernels": bench_fused(),
+    }
+    k64_ms, k64_kernels, _ = bench_prefill(args.steps, args.warmup, shape=(1, 8192, 16, 64, 64))
+    k64_bytes = prefill_bytes(1, 8192, 16, 64, 64)
+    result["prefill_k64"] = {
+        "workload": "kda chunkwise prefill B=1 T=8192 H=16 K=V=64 bf16 (the gpu_48gb head shape), f32 state "
+                    "N(0,0.02) in, final state out",
+        "ms": round(k64_ms, 5),
+        "tokens_per_s": round(8192 / (k64_ms * 1e-3), 1),
+        "kernels_ms": {n: round(t, 5) for n, t in k64_kernels.items()},
+        "achieved_gbs": round(k64_bytes / (k64_ms * 1e-3) / 1e9, 1),
+        "frac_hbm": round(k64_bytes / (k64_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "algorithmic_bytes": k64_bytes,
     }
     result["decay_fusion"] = bench_decay_fusion()
     result["backward"] = bench_backward()

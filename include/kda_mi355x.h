@@ -119,8 +119,9 @@ int kda_chunk_fwd_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, in
  * tests/kda/test_kda_ut_transform.py:94-103).  Packed documents via
  * `cu_seqlens` have no reference counterpart: each document equals an
  * independent `chunkwise_kda` call.
- * Shapes the MFMA path does not cover (K != 128, V not a multiple of 16,
- * f32/f64 inputs) run the exact recurrence kernel instead.
+ * The MFMA path covers bf16/f16 inputs with K <= 128 a multiple of 16 (a smaller K is
+ * zero-padded to 128 channels inside the kernel) and V a multiple of 16 in
+ * 16..256; other shapes and f32/f64 inputs run the exact recurrence kernel.
  */
 int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
                   int in_dtype, const void* initial_state, void* final_state, int state_dtype,
@@ -141,8 +142,8 @@ int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, co
  * kda_chunk_fwd bit for bit.
  *   decay_logits : [tokens, H, K] in in_dtype (in place of g); decay_bias [H, K] or NULL;
  *   a_log        : f32 [H];  g_min < 0.
- * The MFMA shapes only (bf16/f16 inputs, K = 128, V a multiple of 16 in
- * 16..256): other shapes return KDA_ERR_UNSUPPORTED.  Workspace as
+ * The MFMA shapes only (bf16/f16 inputs, K <= 128 a multiple of 16, V a multiple of 16
+ * in 16..256): other shapes return KDA_ERR_UNSUPPORTED.  Workspace as
  * kda_chunk_fwd_workspace_bytes.
  */
 int kda_chunk_fwd_decay(const void* q, const void* k, const void* v, const void* decay_logits,

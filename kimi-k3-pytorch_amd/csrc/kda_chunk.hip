@@ -1,4 +1,5 @@
-// Chunkwise KDA prefill on gfx950 bf16 MFMA (chunk C = 64, K = 128, V <= 256).
+// Chunkwise KDA prefill on gfx950 bf16 MFMA (chunk C = 64, K <= 128 zero-padded
+// to 128 channels, V <= 256).
 //
 // Reference algorithm: src/kda/chunkwise.py:61-102 with the UT transform of
 // src/kda/ut_transform.py:23-58.  For one chunk (rows i, j = 0..63, key
@@ -290,7 +291,7 @@ struct SegArgs {
   float* seg_q;
   bf16* seg_p;
   bf16* chunk_ma;  // [chunk][h] M and Aqk fragments (kMaBytes), or nullptr
-  int64_t N, H, V;
+  int64_t N, H, K, V;  // K <= kKey, a multiple of 16: channels K..kKey-1 are zero padding inside the kernel
   int32_t L;
   // kernels that form g from decay logits (DECAY): `g` then points at the
   // logits z [tokens, H, K], and g = lower_bounded_decay(z + zbias[h],
@@ -304,6 +305,7 @@ struct SegArgs {
 // thread's two channels, the head's scale exp(A_log[h]) and the clamp bounds.
 struct DecayConsts {
   float b[2];
+  bool ok[2];  // the channel is a real one (< K), not padding
   float scale, g_min, lo, hi;
 };
 
@@ -312,7 +314,10 @@ __device__ __forceinline__ DecayConsts decay_consts(const SegArgs<IT>& a, int64_
   DecayConsts d{};
   if constexpr (DECAY) {
 #pragma unroll
-    for (int ch = 0; ch < 2; ++ch) d.b[ch] = a.zbias ? to_float(a.zbias[h * kKey + 2 * cp + ch]) : 0.f;
+    for (int ch = 0; ch < 2; ++ch) {
+      d.ok[ch] = 2 * cp + ch < a.K;
+      d.b[ch] = (a.zbias && d.ok[ch]) ? to_float(a.zbias[h * a.K + 2 * cp + ch]) : 0.f;
+    }
     d.scale = fexp(a.a_log[h]);
     d.g_min = a.g_min;
     d.lo = a.g_lo;
@@ -324,12 +329,12 @@ __device__ __forceinline__ DecayConsts decay_consts(const SegArgs<IT>& a, int64_
 // g of one row and channel: the raw value, or (DECAY) the decay formed from
 // its logit and rounded to the input type, as the gates kernel stores it;
 // rows past the valid tokens decay by nothing (the operator mask,
-// src/kda/utils.py:82-94)
+// src/kda/utils.py:82-94), and neither do padding channels
 template <class IT, bool DECAY>
 __device__ __forceinline__ float g_value(float raw, const DecayConsts& d, int ch, bool valid) {
   if constexpr (DECAY) {
     const float gg = lower_bounded_decay(raw, d.b[ch], d.scale, d.g_min, d.lo, d.hi);
-    return valid ? to_float(from_compute<IT>(gg)) : 0.f;
+    return (valid && d.ok[ch]) ? to_float(from_compute<IT>(gg)) : 0.f;
   } else {
     return raw;
   }
@@ -407,9 +412,9 @@ __device__ __forceinline__ ChunkLoads chunk_loads(const SegArgs<IT>& a, const Ch
                                                   int64_t col0, bool active = true) {
   constexpr int64_t kEl = sizeof(IT);
   ChunkLoads cl;
-  cl.krow = static_cast<int>(a.H * kKey * kEl);
+  cl.krow = static_cast<int>(a.H * a.K * kEl);
   const int64_t nv = active ? cg.n_valid : 0;
-  const int64_t kb = (cg.tok0 * a.H + h) * kKey * kEl;
+  const int64_t kb = (cg.tok0 * a.H + h) * a.K * kEl;
   const int64_t kbytes = nv * cl.krow;
   cl.g = buffer_rsrc(reinterpret_cast<const char*>(a.g) + kb, kbytes);
   cl.k = buffer_rsrc(reinterpret_cast<const char*>(a.k) + kb, kbytes);
@@ -428,9 +433,10 @@ struct LoaderLanes {
   int v[4];
   int vlds[4];
   int beta;
+  int kcol;  // byte offset of the thread's channel pair in a q/k/g row, or past every chunk (padding channels)
 };
 
-template <class IT>
+template <class IT, bool PAD>
 __device__ __forceinline__ LoaderLanes loader_lanes(const SegArgs<IT>& a, int vcg, int tid) {
   constexpr int kEl = sizeof(IT);
   const int t2 = tid - 256;
@@ -444,6 +450,10 @@ __device__ __forceinline__ LoaderLanes loader_lanes(const SegArgs<IT>& a, int vc
     ll.vlds[i] = row < kChunk ? (row * kRow + 8 * (u % upr)) * 2 : -1;
   }
   ll.beta = t2 < kChunk ? t2 * static_cast<int>(a.H * kEl) : -1;
+  // a padding channel pair reads at 64 rows past the chunk's first row, beyond
+  // every chunk's resource range, so its loads return zero
+  const int cp = loader_pair(tid);
+  ll.kcol = (!PAD || 2 * cp < a.K) ? 4 * cp : static_cast<int>(kChunk * a.H * a.K * kEl);
   return ll;
 }
 
@@ -457,10 +467,9 @@ template <class IT, int MODE, int PART>
 __device__ __forceinline__ void load_raw_part(Raw<IT>& raw, const ChunkLoads& cl, const LoaderLanes& ll, int tid) {
   typedef typename Raw<IT>::pair_t pair_t;
   const int J = loader_block(tid);
-  const int cp = loader_pair(tid);
 #pragma unroll
   for (int r = 2 * PART; r < 2 * PART + 2; ++r) {
-    const int off = (16 * J + r) * cl.krow + 4 * cp;
+    const int off = (16 * J + r) * cl.krow + ll.kcol;
     raw.gp[r] = __builtin_bit_cast(pair_t, __builtin_amdgcn_raw_buffer_load_b32(cl.g, off, 0, 0));
     raw.kp[r] = __builtin_bit_cast(pair_t, __builtin_amdgcn_raw_buffer_load_b32(cl.k, off, 0, 0));
     raw.qp[r] = __builtin_bit_cast(pair_t, __builtin_amdgcn_raw_buffer_load_b32(cl.q, off, 0, 0));
@@ -1095,7 +1104,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
   // ---- exact diagonal blocks for chunks with extreme decay ----------------
   if (flags[0] | flags[1] | flags[2] | flags[3]) {
     float* Lr = lds<float>(sm, kOffQA);  // [64][128] f32 over the dead q a and k E tiles
-    const int64_t krow = a.H * kKey;
+    const int64_t krow = a.H * a.K;
     if (wave < 4) {
       const int J = wave, cp = lane;
       const DecayConsts dc = decay_consts<IT, DECAY>(a, h, cp);
@@ -1105,8 +1114,8 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
         for (int r = 0; r < 16; ++r) {
           const int tl = 16 * J + r;
           const float gvv =
-              tl < n_valid
-                  ? g_value<IT, DECAY>(to_float(a.g[(cg.tok0 + tl) * krow + h * kKey + 2 * cp + ch]), dc, ch, true)
+              (tl < n_valid && 2 * cp + ch < a.K)
+                  ? g_value<IT, DECAY>(to_float(a.g[(cg.tok0 + tl) * krow + h * a.K + 2 * cp + ch]), dc, ch, true)
                   : 0.f;
           if (r > 0) run += gvv;
           Lr[tl * kKey + 2 * cp + ch] = run;
@@ -1123,9 +1132,9 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
       const int i = 16 * I + il, j = 16 * I + jl;
       float acc_k = 0.f, acc_q = 0.f;
       if (i < n_valid && j < n_valid) {
-        const int64_t oi = (cg.tok0 + i) * krow + h * kKey;
-        const int64_t oj = (cg.tok0 + j) * krow + h * kKey;
-        for (int cc = 0; cc < kKey; ++cc) {
+        const int64_t oi = (cg.tok0 + i) * krow + h * a.K;
+        const int64_t oj = (cg.tok0 + j) * krow + h * a.K;
+        for (int cc = 0; cc < a.K; ++cc) {
           const float e = fast_exp(Lr[i * kKey + cc] - Lr[j * kKey + cc]);
           const float kj = to_float(a.k[oj + cc]);
           acc_k += to_float(a.k[oi + cc]) * kj * e;
@@ -1425,7 +1434,9 @@ __device__ __forceinline__ void store_out(const f32x4_t (&O)[2][4], int ntile, I
 // tiles]).  Waves 4-7 (loaders) hold the raw inputs of the next chunk.  The
 // two roles run separate loops with the same barriers, so neither role's
 // registers are live in the other's code.
-template <class IT, int MODE, bool DECAY>
+// DECAY: g formed from decay logits; PAD: K < 128, channels K..127 are zero
+// padding (K == 128 compiles without any of the padding checks)
+template <class IT, int MODE, bool DECAY, bool PAD>
 __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<IT> a) {
   extern __shared__ __align__(16) unsigned char sm[];
   // one-dimensional grid, segment slowest: the workgroups past the real
@@ -1457,7 +1468,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
   const int nvt = vcg / 16;
   const bool track_p = MODE == kSummary && lg > 0 && cgi == 0;
   const int ntiles = nvt + (track_p ? 8 : 0);
-  const int64_t sbase = (s * a.H + h) * kKey * a.V;
+  const int64_t sbase = (s * a.H + h) * a.K * a.V;
   constexpr int kPairs = MODE == kSummary ? 2 : 1;  // tile pairs per scanner wave
 
   f32x4_t S[kPairs][2][8];
@@ -1472,10 +1483,12 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
         for (int ct = 0; ct < 8; ++ct) {
           if (tile < nvt) {
             if (lg == 0) {
+              // K is a multiple of 16: a row tile is all real or all padding
+              const bool real = a.s_in != nullptr && (!PAD || 16 * ct < a.K);
 #pragma unroll
               for (int r = 0; r < 4; ++r) {
                 const int64_t row = 16 * ct + 4 * g4 + r;
-                S[pp][t][ct][r] = a.s_in ? a.s_in[sbase + row * a.V + col0 + 16 * tile + n16] : 0.f;
+                S[pp][t][ct][r] = real ? a.s_in[sbase + row * a.V + col0 + 16 * tile + n16] : 0.f;
               }
             } else if (kWritesOut<MODE>) {
               const float* p = a.seg_state + (gsg * a.H + h) * seg_state_floats(a.V) +
@@ -1547,7 +1560,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
     // ---------------- loaders, phase C without P2 ----------------
     Raw<IT> raw;
     P1Out po;
-    const LoaderLanes ll = loader_lanes<IT>(a, vcg, tid);
+    const LoaderLanes ll = loader_lanes<IT, PAD>(a, vcg, tid);
     const DecayConsts dc = decay_consts<IT, DECAY>(a, h, loader_pair(tid));
     if (c_begin < c_end) {
       const ChunkGeo g0 = chunk_geo(sr, c_begin - cs);
@@ -1576,7 +1589,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
     // waits for the loads.
     Raw<IT> raw;
     P1Out po;
-    const LoaderLanes ll = loader_lanes<IT>(a, vcg, tid);
+    const LoaderLanes ll = loader_lanes<IT, PAD>(a, vcg, tid);
     const DecayConsts dc = decay_consts<IT, DECAY>(a, h, loader_pair(tid));
     if (c_begin < c_end) {
       const ChunkGeo g0 = chunk_geo(sr, c_begin - cs);
@@ -1619,6 +1632,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
         if (tile >= nvt) continue;
 #pragma unroll
         for (int ct = 0; ct < 8; ++ct) {
+          if (PAD && 16 * ct >= a.K) break;  // padding rows (K is a multiple of 16)
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int64_t row = 16 * ct + 4 * g4 + r;
@@ -1747,7 +1761,8 @@ __global__ __launch_bounds__(512) void segment_combine_kernel(const CombineArgs 
 
 // ---- host side ------------------------------------------------------------
 static bool mfma_path(int in_dtype, int state_dtype, int64_t K, int64_t V) {
-  return (in_dtype == KDA_DTYPE_BF16 || in_dtype == KDA_DTYPE_F16) && state_dtype == KDA_DTYPE_F32 && K == kKey &&
+  return (in_dtype == KDA_DTYPE_BF16 || in_dtype == KDA_DTYPE_F16) && state_dtype == KDA_DTYPE_F32 && K <= kKey &&
+         K % 16 == 0 &&
          V % 16 == 0 && V >= 16 && V <= 256;
 }
 
@@ -1829,18 +1844,18 @@ static void mark(kda_host::KernelEvents* ev, int i, hipStream_t stream) {
   }
 }
 
-template <class IT, int MODE, bool DECAY>
+template <class IT, int MODE, bool DECAY, bool PAD>
 static int launch_segments(const SegArgs<IT>& sa, const Plan& p, int64_t H, hipStream_t stream) {
   static bool attr_done = false;
   if (!attr_done) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_segment_kernel<IT, MODE, DECAY>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_segment_kernel<IT, MODE, DECAY, PAD>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes) != hipSuccess) {
       kda_host::set_detail("cannot reserve %d bytes of LDS for chunk_segment_kernel", kSmemBytes);
       return KDA_ERR_LAUNCH;
     }
     attr_done = true;
   }
-  hipLaunchKernelGGL((chunk_segment_kernel<IT, MODE, DECAY>), dim3(static_cast<unsigned>(p.segs_bound * H * p.ncg)),
+  hipLaunchKernelGGL((chunk_segment_kernel<IT, MODE, DECAY, PAD>), dim3(static_cast<unsigned>(p.segs_bound * H * p.ncg)),
                      dim3(kThreads), kSmemBytes, stream, sa);
   return kda_host::check_launch(MODE == kSummary ? "chunk_segment_kernel<summary>" : "chunk_segment_kernel<output>");
 }
@@ -1852,10 +1867,10 @@ struct DecayInput {
   float g_min;
 };
 
-template <class IT, bool DECAY>
-static int run_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, const void* s_in,
+template <class IT, bool DECAY, bool PAD>
+static int run_chunk_k(const void* q, const void* k, const void* v, const void* g, const void* beta, const void* s_in,
                      void* s_out, void* out, const SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
-                     int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev,
+                     int64_t K, int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev,
                      const DecayInput* decay) {
   const Plan p = make_plan(N, total_tokens, H, V);
   int32_t* chunk_start = static_cast<int32_t*>(workspace);
@@ -1889,6 +1904,7 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
                             : nullptr;
   sa.N = N;
   sa.H = H;
+  sa.K = K;
   sa.V = V;
   sa.L = p.L;
   sa.zbias = nullptr;
@@ -1915,7 +1931,7 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
   }
   mark(ev, 1, stream);
   if (p.segmented) {
-    st = launch_segments<IT, kSummary, DECAY>(sa, p, H, stream);
+    st = launch_segments<IT, kSummary, DECAY, PAD>(sa, p, H, stream);
     if (st != KDA_OK) return st;
     mark(ev, 2, stream);
     CombineArgs ca{sa.seg_start, sa.dense_segs, sa.seg_state, sa.seg_q, sa.seg_p, N, H, V};
@@ -1930,10 +1946,22 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
     mark(ev, 3, stream);
     if (ev != nullptr) ev->empty |= 6u;  // one segment per sequence: no summaries, no combine
   }
-  st = p.segmented ? launch_segments<IT, kOutputMA, DECAY>(sa, p, H, stream)
-                   : launch_segments<IT, kOutput, DECAY>(sa, p, H, stream);
+  st = p.segmented ? launch_segments<IT, kOutputMA, DECAY, PAD>(sa, p, H, stream)
+                   : launch_segments<IT, kOutput, DECAY, PAD>(sa, p, H, stream);
   mark(ev, 4, stream);
   return st;
+}
+
+template <class IT, bool DECAY>
+static int run_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, const void* s_in,
+                     void* s_out, void* out, const SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
+                     int64_t K, int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev,
+                     const DecayInput* decay) {
+  if (K == kKey)
+    return run_chunk_k<IT, DECAY, false>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V, workspace,
+                                         stream, ev, decay);
+  return run_chunk_k<IT, DECAY, true>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V, workspace,
+                                      stream, ev, decay);
 }
 
 }  // namespace kda
@@ -1982,9 +2010,9 @@ int launch_chunk(const void* q, const void* k, const void* v, const void* g, con
     return KDA_ERR_UNSUPPORTED;
   }
   if (in_dtype == KDA_DTYPE_BF16)
-    return run_chunk<bf16, false>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream,
+    return run_chunk<bf16, false>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V, workspace, stream,
                                   ev, nullptr);
-  return run_chunk<f16, false>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream, ev,
+  return run_chunk<f16, false>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V, workspace, stream, ev,
                                nullptr);
 }
 
@@ -1994,8 +2022,8 @@ int launch_chunk_decay(const void* q, const void* k, const void* v, const void* 
                        int64_t K, int64_t V, void* workspace, size_t workspace_bytes, hipStream_t stream) {
   using namespace kda;
   if (!mfma_path(in_dtype, state_dtype, K, V)) {
-    set_detail("chunk_fwd_decay: the fused decay needs the MFMA path (bf16/f16 inputs, f32 state, K = 128, V a "
-               "multiple of 16 in 16..256); form g with kda_gates_fwd and call kda_chunk_fwd");
+    set_detail("chunk_fwd_decay: the fused decay needs the MFMA path (bf16/f16 inputs, f32 state, K <= 128 a multiple of 16, "
+               "V a multiple of 16 in 16..256); form g with kda_gates_fwd and call kda_chunk_fwd");
     return KDA_ERR_UNSUPPORTED;
   }
   if (workspace_bytes < chunk_workspace_bytes(N, total_tokens, H, K, V, in_dtype)) {
@@ -2009,9 +2037,9 @@ int launch_chunk_decay(const void* q, const void* k, const void* v, const void* 
   }
   const DecayInput d{zbias, a_log, g_min};
   if (in_dtype == KDA_DTYPE_BF16)
-    return run_chunk<bf16, true>(q, k, v, z, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream,
+    return run_chunk<bf16, true>(q, k, v, z, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V, workspace, stream,
                                  nullptr, &d);
-  return run_chunk<f16, true>(q, k, v, z, beta, s_in, s_out, out, seq, N, total_tokens, H, V, workspace, stream,
+  return run_chunk<f16, true>(q, k, v, z, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V, workspace, stream,
                               nullptr, &d);
 }
 

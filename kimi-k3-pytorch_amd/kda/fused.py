@@ -215,8 +215,8 @@ def chunkwise_kda_with_decay(
     decay_logits, a_log, g_min, bias=decay_bias)[0]`` (src/kda/decay.py:36-43,
     src/kda/kda.py:131-151), the decay formed inside the chunk kernel so that g
     never makes a round trip through HBM.  The result equals the two-step
-    composition bit for bit.  Shapes off the MFMA path (K != 128, V not a
-    multiple of 16 in 16..256, f32/f64 inputs) and calls under autograd run the
+    composition bit for bit.  Shapes off the MFMA path (K above 128 or not a
+    multiple of 16, V not a multiple of 16 in 16..256, f32/f64 inputs) and calls under autograd run the
     two steps (both in HIP kernels); so does f16/bf16 work without an f32 state."""
     from .chunkwise import chunkwise_kda, needs_grad
     from .recurrent import KDAOperatorOutput
@@ -239,7 +239,7 @@ def chunkwise_kda_with_decay(
     work_dtype = accumulation_dtype(v.dtype, accumulate_state_in_fp32)
     dtypes = {t.dtype for t in (q, k, v, decay_logits, beta)}
     fused_ok = (len(dtypes) == 1 and q.dtype in (torch.bfloat16, torch.float16) and work_dtype == torch.float32
-                and key_dim == 128 and value_dim % 16 == 0 and 16 <= value_dim <= 256
+                and key_dim <= 128 and key_dim % 16 == 0 and value_dim % 16 == 0 and 16 <= value_dim <= 256
                 and not needs_grad(q, k, v, decay_logits, beta, initial_state, a_log, decay_bias))
     if not fused_ok:
         g, _ = lower_bounded_decay(decay_logits, a_log, g_min, bias=decay_bias)

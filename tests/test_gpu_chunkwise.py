@@ -1,5 +1,5 @@
-"""GPU parity of the chunkwise prefill (MFMA path for bf16/f16 with K=128,
-exact-recurrence path otherwise) against the CPU oracle.
+"""GPU parity of the chunkwise prefill (MFMA path for bf16/f16 with K <= 128 a
+multiple of 16, exact-recurrence path otherwise) against the CPU oracle.
 
 Tolerance (max|x - ref| / max|ref|, per tensor): bf16/f16 inputs <= 2e-2
 against the f32 oracle run on the same (exactly upcast) inputs; f32 inputs
@@ -196,11 +196,71 @@ def test_chunkwise_f32_cpu_smoke_config_within_1e4():
     assert rel_err(got.hidden_states, ro) < 1e-4 and rel_err(got.final_state, rs) < 1e-4
 
 
-def test_chunkwise_bf16_small_head_dim_fallback():
+def _plan(B, T, H, K, V, dtype=torch.bfloat16):
+    import ctypes
+
+    from kda import _lib
+
+    L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
+    _lib.check(_lib.load().kda_chunk_fwd_plan(B, B * T, H, K, V, _lib.dtype_code(dtype), ctypes.byref(L),
+                                              ctypes.byref(segs)))
+    return L.value
+
+
+def test_chunkwise_bf16_small_head_dim():
+    # K = 16 runs the MFMA path with channels 16..127 zero-padded in the kernel
+    assert _plan(2, 40, 3, 16, 32) >= 0
     q, k, v, g, beta, state = workload(2, 40, 3, 16, 32, state_std=0.02, seed=20)
     ro, rs = _oracle_f32(q, k, v, g, beta, state)
     got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True)
-    _check(got, ro, rs, label="K=16 fallback")
+    _check(got, ro, rs, label="K=16")
+
+
+@pytest.mark.parametrize("segment_chunks", [None, "1"])
+@pytest.mark.parametrize(
+    "shape",
+    [
+        (1, 300, 2, 64, 64),    # the gpu_48gb profile's head (K = V = 64)
+        (2, 130, 2, 64, 128),   # K = 64, V = 128
+        (1, 200, 3, 32, 48),
+        (1, 150, 2, 96, 128),
+        (2, 70, 2, 16, 16),     # the smallest key dim of the MFMA path
+    ],
+)
+def test_chunkwise_key_dims_below_128(monkeypatch, shape, segment_chunks):
+    # the reference's chunk algorithm runs at any K (src/kda/chunkwise.py:61-102);
+    # K <= 128, a multiple of 16, takes the MFMA path, padded to 128 channels in the kernel
+    if segment_chunks is not None:
+        monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", segment_chunks)
+    assert _plan(*shape) >= 0 and _plan(*shape, dtype=torch.float32) == -1
+    q, k, v, g, beta, state = workload(*shape, state_std=0.02, seed=24)
+    ro, rs = _oracle_f32(q, k, v, g, beta, state)
+    got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True)
+    _check(got, ro, rs, label=f"{shape} L={segment_chunks}")
+
+
+def test_chunkwise_key_dim_off_the_mfma_grid():
+    # K = 40 (not a multiple of 16) runs the exact recurrence kernel
+    assert _plan(1, 100, 2, 40, 32) == -1
+    q, k, v, g, beta, state = workload(1, 100, 2, 40, 32, state_std=0.02, seed=26)
+    ro, rs = _oracle_f32(q, k, v, g, beta, state)
+    _check(kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True), ro, rs, label="K=40")
+
+
+def test_gpu_48gb_shape_full_length():
+    # B=1, T=8192, H=16, K=V=64 bf16 (config/kimi_full_pipeline/gpu_48gb/model.yaml:19,
+    # V = d_model / H): the segmented MFMA schedule; two heads checked at full
+    # length against the oracle
+    assert _plan(1, 8192, 16, 64, 64) > 0
+    q, k, v, g, beta, state = workload(1, 8192, 16, 64, 64, state_std=0.02, seed=25)
+    got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True)
+    for h in (3, 14):
+        sl = slice(h, h + 1)
+        ro, rs = _oracle_f32(q[:, :, sl], k[:, :, sl], v[:, :, sl], g[:, :, sl], beta[:, :, sl], state[:, sl])
+        eo = rel_err(got.hidden_states[:, :, sl], ro)
+        es = rel_err(got.final_state[:, sl], rs)
+        print(f"K=V=64 T=8192 head {h}: output rel err {eo:.2e} state rel err {es:.2e}")
+        assert eo < TOL16 and es < TOL16
 
 
 def test_long_context_full_length_single_head():

@@ -79,6 +79,23 @@ def test_layer_matches_oracle_bf16(mode, biases):
     _check(got.hidden_states, got.state, ref_out, ref_st, label=f"{mode} biases={biases}")
 
 
+def test_layer_key_dim_64_matches_oracle_bf16():
+    # the head shape of the reference's gpu_48gb profile (K = V = 64) on the
+    # MFMA path, chunkwise prefill then decode steps
+    cfg = dict(d_model=128, heads=2, key_dim=64, value_dim=64, conv=4, rank=16)
+    w, gw = _weights(cfg, torch.bfloat16, seed=19)
+    x = _x(cfg, 2, 140, torch.bfloat16, seed=20)
+    ref_out, ref_st = ora.kda_layer(w, x, mode="recurrent", output_final_state=True)
+    xd = x.to(DEV)
+    with torch.no_grad():
+        pre = kda_attention_forward(gw, xd[:, :136], mode="chunkwise", output_final_state=True)
+        state, outs = pre.state, [pre.hidden_states]
+        for t in range(136, 140):
+            step = kda_attention_forward(gw, xd[:, t:t + 1], state=state, mode="decode")
+            state, outs = step.state, outs + [step.hidden_states]
+    _check(torch.cat(outs, 1), state, ref_out, ref_st, label="K=V=64 layer")
+
+
 @pytest.mark.parametrize("in_place", [False, True])
 def test_split_prefill_then_decode_matches_one_shot_bf16(in_place):
     # prefill 100 tokens (chunkwise, fused decay), then 8 decode steps carrying
@@ -183,23 +200,24 @@ def test_cache_bytes_constant_and_equal_to_the_reference_layout():
 
 # ---- the decay fused into the chunk kernel ------------------------------------
 
-def _decay_inputs(B, T, H, V, dtype, seed, z_shift=0.0):
-    q, k, v, _, beta, state = workload(B, T, H, 128, V, state_std=0.02, seed=seed, dtype=dtype)
+def _decay_inputs(B, T, H, K, V, dtype, seed, z_shift=0.0):
+    q, k, v, _, beta, state = workload(B, T, H, K, V, state_std=0.02, seed=seed, dtype=dtype)
     gen = torch.Generator().manual_seed(seed + 100)
-    z = (torch.randn(B, T, H, 128, generator=gen) + z_shift).to(dtype)
-    bias = (0.5 * torch.randn(H, 128, generator=gen)).to(dtype)
+    z = (torch.randn(B, T, H, K, generator=gen) + z_shift).to(dtype)
+    bias = (0.5 * torch.randn(H, K, generator=gen)).to(dtype)
     a_log = 0.3 * torch.randn(H, generator=gen)
     return q, k, v, z, beta, state, bias, a_log
 
 
 @pytest.mark.parametrize(
     "case",
-    ["dense", "masked", "packed", "segmented", "extreme_decay", "f16", "value_64"],
+    ["dense", "masked", "packed", "segmented", "extreme_decay", "f16", "value_64", "key_64"],
 )
 def test_fused_decay_prefill_equals_two_step_and_oracle(monkeypatch, case):
     dtype = torch.float16 if case == "f16" else torch.bfloat16
     B, T, H, V = (1, 260, 2, 128) if case in ("packed", "segmented") else (2, 200, 2, 64 if case == "value_64" else 128)
-    q, k, v, z, beta, state, bias, a_log = _decay_inputs(B, T, H, V, dtype, seed=21,
+    K = 64 if case == "key_64" else 128
+    q, k, v, z, beta, state, bias, a_log = _decay_inputs(B, T, H, K, V, dtype, seed=21,
                                                          z_shift=25.0 if case == "extreme_decay" else 0.0)
     mask = cu = None
     if case == "masked":
@@ -207,7 +225,7 @@ def test_fused_decay_prefill_equals_two_step_and_oracle(monkeypatch, case):
         mask[1, 133:] = False
     if case == "packed":
         cu = [0, 70, 71, 200, 260]
-        state = torch.randn(4, H, 128, V, generator=torch.Generator().manual_seed(5)) * 0.02
+        state = torch.randn(4, H, K, V, generator=torch.Generator().manual_seed(5)) * 0.02
     if case == "segmented":
         monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "1")
     dv = lambda t: None if t is None else t.to(DEV)  # noqa: E731
