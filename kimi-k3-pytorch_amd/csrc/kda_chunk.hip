@@ -1270,17 +1270,19 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
   const int g4 = lane >> 4;
   const int n16 = lane & 15;
   const bf16(*Vn)[kRow] = reinterpret_cast<const bf16(*)[kRow]>(sm + kOffVn);
-  // Y = v - Kgamma S (value columns) or -Kgamma S (transition columns)
+  // Y = v - Kgamma S (value columns) or -Kgamma S (transition columns): the
+  // products start from zero and v is added after them, so that its LDS reads
+  // overlap the MFMA chain instead of delaying its first step
   f32x4_t Y[2][4];
+  bf16 vin[2][4][4];
 #pragma unroll
   for (int t = 0; t < 2; ++t) {
 #pragma unroll
     for (int I = 0; I < 4; ++I) {
+      Y[t][I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
       if (ut[t] >= 0) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) Y[t][I][r] = (float)Vn[16 * I + 4 * g4 + r][16 * ut[t] + n16];
-      } else {
-        Y[t][I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
+        for (int r = 0; r < 4; ++r) vin[t][I][r] = Vn[16 * I + 4 * g4 + r][16 * ut[t] + n16];
       }
       if constexpr (kWritesOut<MODE>) O[t][I] = f32x4_t{0.f, 0.f, 0.f, 0.f};
     }
@@ -1326,6 +1328,15 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
 #pragma unroll
         for (int t = 0; t < 2; ++t) O[t][I] = mfma32(qf[I], sb[t], O[t][I]);
       }
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+    if (ut[t] >= 0) {
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) Y[t][I][r] += (float)vin[t][I][r];
     }
   }
   // lower-triangular 64 x 64 fragments (I, s') with s' <= I / 2 sit in slots 0, 2, 4, 5, 6, 7
