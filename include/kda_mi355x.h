@@ -284,6 +284,48 @@ int kda_rmsnorm_gate_fwd(const void* x, const void* weight, int weight_per_head,
 
 
 /*
+ * Backward of the fused stages: the gradients the reference takes from
+ * autograd through KDAProjections.forward (src/kda/projections.py:164-218),
+ * LowerBoundedDecay.forward (src/kda/decay.py:36-43), HeadwiseRMSNorm.forward
+ * (src/kimi_primitives/headwise_rmsnorm.py:39-64) and the gate product of
+ * FullRankOutputGate.forward (src/kimi_primitives/output_gate.py:62-75).
+ * Arguments mirror the forward entry points; every forward intermediate is
+ * recomputed from the inputs.  Activation gradients have the tensors' dtype.
+ * Parameter gradients (d_weight, d_bias, d_decay_bias, d_a_log) are
+ * ACCUMULATORS in the compute type (f64 for f64 tensors, f32 otherwise) that
+ * the caller zeroes first; each may be NULL to skip it.  They are summed with
+ * float atomics, so their rounding varies from run to run.
+ *
+ * kda_conv_silu_bwd: dy [batch, tokens, channels] (the gradient of y) and
+ *   d_history_out (the gradient of the returned history, or NULL) give dx,
+ *   d_history_in (or NULL), d_weight [channels, kernel_size], d_bias [channels].
+ *   normalize: head_dim a power of two in 16..256 (16..128 for f64).
+ */
+int kda_conv_silu_bwd(const void* x, const void* weight, const void* bias, const void* history_in,
+                      const int32_t* valid_lens, const void* dy, const void* d_history_out, void* dx,
+                      void* d_history_in, void* d_weight, void* d_bias, int64_t batch, int64_t tokens,
+                      int64_t channels, int64_t kernel_size, int64_t head_dim, int normalize, double eps,
+                      int dtype, void* stream);
+
+/*
+ * kda_gates_bwd: d_g (and d_alpha or NULL) give d_decay_logits, d_decay_bias
+ *   [heads, key_dim] and d_a_log [heads]; d_beta gives d_beta_logits.  The
+ *   clamps pass gradient inside [eps, 1 - eps], as torch.clamp does.
+ */
+int kda_gates_bwd(const void* decay_logits, const void* decay_bias, const float* a_log, double g_min,
+                  const void* d_g, const void* d_alpha, void* d_decay_logits, void* d_decay_bias,
+                  void* d_a_log, const void* beta_logits, const void* d_beta, void* d_beta_logits,
+                  int64_t rows, int64_t heads, int64_t key_dim, int dtype, void* stream);
+
+/*
+ * kda_rmsnorm_gate_bwd: dy [rows, heads, head_dim] gives dx, d_gate_logits and
+ *   d_weight (shaped like weight).
+ */
+int kda_rmsnorm_gate_bwd(const void* x, const void* weight, int weight_per_head, const void* gate_logits,
+                         const void* dy, void* dx, void* d_gate_logits, void* d_weight, int64_t rows,
+                         int64_t heads, int64_t head_dim, double eps, int dtype, void* stream);
+
+/*
  * Backward of the token recurrence that returns its per-token states: the
  * autograd of recurrent_kda(..., return_states_per_token=True)
  * (src/kda/recurrent.py:61-79), where every intermediate state may carry a gradient.

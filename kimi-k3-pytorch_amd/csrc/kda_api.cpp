@@ -377,6 +377,84 @@ int kda_rmsnorm_gate_fwd(const void* x, const void* weight, int weight_per_head,
                              static_cast<hipStream_t>(stream));
 }
 
+int kda_conv_silu_bwd(const void* x, const void* weight, const void* bias, const void* history_in,
+                      const int32_t* valid_lens, const void* dy, const void* d_history_out, void* dx,
+                      void* d_history_in, void* d_weight, void* d_bias, int64_t batch, int64_t tokens,
+                      int64_t channels, int64_t kernel_size, int64_t head_dim, int normalize, double eps, int dtype,
+                      void* stream) {
+  g_detail[0] = '\0';
+  if (batch <= 0 || tokens <= 0 || channels <= 0 || kernel_size <= 0 || (normalize && head_dim <= 0)) {
+    set_detail("conv_silu_bwd: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (normalize && channels % head_dim != 0) {
+    set_detail("conv_silu_bwd: channels %lld not a multiple of head_dim %lld", (long long)channels,
+               (long long)head_dim);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!x || !weight || !dy || !dx) {
+    set_detail("conv_silu_bwd: x, weight, dy and dx must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!(eps > 0.0)) {
+    set_detail("conv_silu_bwd: eps must be > 0");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return launch_conv_silu_bwd(x, weight, bias, history_in, valid_lens, dy, d_history_out, dx, d_history_in,
+                              d_weight, d_bias, batch, tokens, channels, kernel_size, head_dim, normalize, eps, dtype,
+                              static_cast<hipStream_t>(stream));
+}
+
+int kda_gates_bwd(const void* decay_logits, const void* decay_bias, const float* a_log, double g_min, const void* d_g,
+                  const void* d_alpha, void* d_decay_logits, void* d_decay_bias, void* d_a_log,
+                  const void* beta_logits, const void* d_beta, void* d_beta_logits, int64_t rows, int64_t heads,
+                  int64_t key_dim, int dtype, void* stream) {
+  g_detail[0] = '\0';
+  if (!is_input_dtype(dtype)) {
+    set_detail("gates_bwd: bad dtype %d", dtype);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (rows <= 0 || heads <= 0 || key_dim <= 0) {
+    set_detail("gates_bwd: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!(g_min < 0.0)) {
+    set_detail("gates_bwd: g_min must be negative");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!decay_logits && !beta_logits) {
+    set_detail("gates_bwd: nothing to do (both logits null)");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return launch_gates_bwd(decay_logits, decay_bias, a_log, g_min, d_g, d_alpha, d_decay_logits, d_decay_bias, d_a_log,
+                          beta_logits, d_beta, d_beta_logits, rows, heads, key_dim, dtype,
+                          static_cast<hipStream_t>(stream));
+}
+
+int kda_rmsnorm_gate_bwd(const void* x, const void* weight, int weight_per_head, const void* gate_logits,
+                         const void* dy, void* dx, void* d_gate_logits, void* d_weight, int64_t rows, int64_t heads,
+                         int64_t head_dim, double eps, int dtype, void* stream) {
+  g_detail[0] = '\0';
+  if (!is_input_dtype(dtype)) {
+    set_detail("rmsnorm_gate_bwd: bad dtype %d", dtype);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (rows <= 0 || heads <= 0 || head_dim <= 0) {
+    set_detail("rmsnorm_gate_bwd: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!x || !dy || !dx || (gate_logits && !d_gate_logits)) {
+    set_detail("rmsnorm_gate_bwd: x, dy, dx (and d_gate_logits with gate_logits) must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!(eps > 0.0)) {
+    set_detail("rmsnorm_gate_bwd: eps must be > 0");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return launch_rmsnorm_gate_bwd(x, weight, weight_per_head, gate_logits, dy, dx, d_gate_logits, weight ? d_weight : nullptr,
+                                 rows, heads, head_dim, eps, dtype, static_cast<hipStream_t>(stream));
+}
+
 int kda_cache_gather(const void* const* src, void* const* dst, const int64_t* row_bytes, int n_tensors,
                      const int64_t* index, int64_t n_src, int64_t n_out, int* status, void* stream) {
   g_detail[0] = '\0';

@@ -83,6 +83,22 @@ int launch_gates(const void* z, const void* zbias, const float* a_log, double g_
 int launch_rmsnorm_gate(const void* x, const void* w, int w_per_head, const void* gl, void* y, int64_t rows,
                         int64_t H, int64_t D, double eps, int dtype, hipStream_t stream);
 
+// Backward of the fused stages (csrc/kda_fused_bwd.hip).  Parameter-gradient
+// buffers are accumulators in the compute type (f64 for f64 tensors, f32
+// otherwise), zeroed by the caller.
+int launch_conv_silu_bwd(const void* x, const void* w, const void* bias, const void* hist_in,
+                         const int32_t* valid_lens, const void* dy, const void* dhist_out, void* dx, void* dhist_in,
+                         void* dw, void* dbias, int64_t B, int64_t T, int64_t C, int64_t K, int64_t head_dim,
+                         int normalize, double eps, int dtype, hipStream_t stream);
+
+int launch_gates_bwd(const void* z, const void* zbias, const float* a_log, double g_min, const void* dg,
+                     const void* dalpha, void* dz, void* dzbias, void* da_log, const void* bl, const void* dbeta,
+                     void* dbl, int64_t rows, int64_t H, int64_t K, int dtype, hipStream_t stream);
+
+int launch_rmsnorm_gate_bwd(const void* x, const void* w, int w_per_head, const void* gl, const void* dy, void* dx,
+                            void* dgl, void* dw, int64_t rows, int64_t H, int64_t D, double eps, int dtype,
+                            hipStream_t stream);
+
 // Batch-row gather over many cache tensors (csrc/kda_cache.hip).
 int launch_cache_gather(const void* const* src, void* const* dst, const int64_t* row_bytes, int n_tensors,
                         const int64_t* index, int64_t n_src, int64_t n_out, int* status, hipStream_t stream);

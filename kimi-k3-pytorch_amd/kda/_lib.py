@@ -74,6 +74,9 @@ SIGNATURES = {
         [_P, _P, _P, ctypes.c_double, _P, _P, _P, _P, _L, _L, _L, _I, _P],
     ),
     "kda_rmsnorm_gate_fwd": (_I, [_P, _P, _I, _P, _P, _L, _L, _L, ctypes.c_double, _I, _P]),
+    "kda_conv_silu_bwd": (_I, [_P] * 11 + [_L] * 5 + [_I, ctypes.c_double, _I, _P]),
+    "kda_gates_bwd": (_I, [_P, _P, _P, ctypes.c_double] + [_P] * 8 + [_L, _L, _L, _I, _P]),
+    "kda_rmsnorm_gate_bwd": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _L, _L, _L, ctypes.c_double, _I, _P]),
     "kda_chunk_bwd_workspace_bytes": (_S, [_L, _L, _L, _L, _L]),
     "kda_chunk_bwd": (
         _I,

@@ -101,29 +101,101 @@ def conv_silu(
         raise ValueError("eps must be > 0")
     validate_attention_mask(attention_mask, batch, tokens)
     _lib.require_gpu(x)
-    _prep.reject_autograd(x, weight, bias, None if state is None else state.buffer)
-    lib = _lib.load()
-
     head_dim = channels // num_heads if num_heads is not None else channels
+    hist = None if state is None else state.buffer
+    valid = _prep.valid_lengths(attention_mask, x.device)
+    cfg = (head_dim, bool(normalize), float(eps), bool(output_final_state))
+    if _needs_grad(x, weight, bias, hist):
+        y, hist_out = _ConvSilu.apply(x, weight, bias, hist, valid, cfg)
+        if not output_final_state:
+            hist_out = None
+    else:
+        y, hist_out = _conv_forward(x, weight, bias, hist, valid, *cfg)
+    if num_heads is not None:
+        y = y.view(batch, tokens, num_heads, head_dim)
+    return y, (ShortConvState(hist_out) if hist_out is not None else None)
+
+
+def _needs_grad(*tensors) -> bool:
+    return torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in tensors)
+
+
+def _conv_forward(x, weight, bias, hist, valid, head_dim, normalize, eps, want_hist):
+    lib = _lib.load()
+    batch, tokens, channels = x.shape
+    kernel_size = weight.shape[1]
     xc = _aligned(x)
     wc = weight.contiguous()
     bc = None if bias is None else bias.contiguous()
-    hist = None if state is None or kernel_size == 1 else _aligned(state.buffer)
+    hc = None if hist is None or kernel_size == 1 else _aligned(hist)
     y = torch.empty_like(xc)
     hist_out = None
-    if output_final_state:
+    if want_hist:
         hist_out = torch.empty(batch, kernel_size - 1, channels, dtype=x.dtype, device=x.device)
-    valid = _prep.valid_lengths(attention_mask, x.device)
     status = lib.kda_conv_silu_fwd(
-        xc.data_ptr(), wc.data_ptr(), _lib.ptr(bc), _lib.ptr(hist), y.data_ptr(),
+        xc.data_ptr(), wc.data_ptr(), _lib.ptr(bc), _lib.ptr(hc), y.data_ptr(),
         _lib.ptr(hist_out) if hist_out is not None and kernel_size > 1 else None, _lib.ptr(valid),
         batch, tokens, channels, kernel_size, head_dim, 1 if normalize else 0, float(eps),
         _lib.dtype_code(x.dtype), _prep.stream(x.device),
     )
     _lib.check(status)
-    if num_heads is not None:
-        y = y.view(batch, tokens, num_heads, head_dim)
-    return y, (ShortConvState(hist_out) if hist_out is not None else None)
+    return y, hist_out
+
+
+def _acc_dtype(dtype: torch.dtype) -> torch.dtype:
+    """Type of the kernels' parameter-gradient accumulators."""
+    return torch.float64 if dtype == torch.float64 else torch.float32
+
+
+class _ConvSilu(torch.autograd.Function):
+    """conv_silu under autograd: the native forward and ``kda_conv_silu_bwd``
+    (input, weight, bias and history gradients; the returned history's own
+    gradient flows back to the inputs it was copied from)."""
+
+    @staticmethod
+    def forward(ctx, x, weight, bias, hist, valid, cfg):
+        y, hist_out = _conv_forward(x, weight, bias, hist, valid, *cfg)
+        ctx.save_for_backward(x, weight, bias, hist, valid)
+        ctx.cfg = cfg
+        if hist_out is None:
+            hist_out = torch.empty(0, dtype=x.dtype, device=x.device)
+            ctx.mark_non_differentiable(hist_out)
+        return y, hist_out
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dy, dhist):
+        x, weight, bias, hist, valid = ctx.saved_tensors
+        head_dim, normalize, eps, want_hist = ctx.cfg
+        lib = _lib.load()
+        batch, tokens, channels = x.shape
+        kernel_size = weight.shape[1]
+        if dy is None:
+            dy = torch.zeros_like(x)
+        dyc = _aligned(dy.to(x.dtype))
+        dh = None
+        if want_hist and dhist is not None and dhist.numel() > 0 and kernel_size > 1:
+            dh = _aligned(dhist.to(x.dtype))
+        xc = _aligned(x)
+        hc = None if hist is None or kernel_size == 1 else _aligned(hist)
+        dx = torch.empty_like(xc)
+        need_w, need_b, need_h = ctx.needs_input_grad[1], ctx.needs_input_grad[2], ctx.needs_input_grad[3]
+        acc = _acc_dtype(x.dtype)
+        dw = torch.zeros(channels, kernel_size, dtype=acc, device=x.device) if need_w else None
+        db = torch.zeros(channels, dtype=acc, device=x.device) if need_b and bias is not None else None
+        dhi = torch.empty_like(hc) if need_h and hc is not None else None
+        _lib.check(lib.kda_conv_silu_bwd(
+            xc.data_ptr(), weight.contiguous().data_ptr(), _lib.ptr(None if bias is None else bias.contiguous()),
+            _lib.ptr(hc), _lib.ptr(valid), dyc.data_ptr(), _lib.ptr(dh), dx.data_ptr(), _lib.ptr(dhi),
+            _lib.ptr(dw), _lib.ptr(db), batch, tokens, channels, kernel_size, head_dim, 1 if normalize else 0,
+            float(eps), _lib.dtype_code(x.dtype), _prep.stream(x.device),
+        ))
+        if need_h and hist is not None and dhi is None:
+            dhi = torch.zeros_like(hist)  # kernel size 1: the history is never read
+        return (dx if ctx.needs_input_grad[0] else None,
+                None if dw is None else dw.to(weight.dtype),
+                None if db is None else db.to(bias.dtype),
+                dhi, None, None)
 
 
 def _gates(decay_logits, a_log, g_min, bias, beta_logits, want_alpha):
@@ -165,7 +237,6 @@ def _gates(decay_logits, a_log, g_min, bias, beta_logits, want_alpha):
             raise ValueError("beta logits must have shape [B,T,H] matching the decay logits")
     else:
         bl = None
-    _prep.reject_autograd(decay_logits, a_log, bias, beta_logits)
     lib = _lib.load()
     status = lib.kda_gates_fwd(
         _lib.ptr(z), _lib.ptr(zb), _lib.ptr(al), float(g_min), _lib.ptr(g), _lib.ptr(alpha),
@@ -184,15 +255,78 @@ def lower_bounded_decay(
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """``(g, exp(g))`` with ``g = g_min * clamp(sigmoid(exp(A_log) * (logits + bias)), eps, 1-eps)``
     for ``logits [B,T,H,K]``, ``A_log [H]`` and an optional bias ``[H,K]``
-    (decay.py:30-43; eps is the dtype's machine epsilon)."""
+    (decay.py:30-43; eps is the dtype's machine epsilon).  Differentiable in
+    the logits, A_log and the bias (``kda_gates_bwd``)."""
+    if _needs_grad(logits, a_log, bias):
+        return _Decay.apply(logits, a_log, bias, float(g_min))
     g, alpha, _ = _gates(logits, a_log, g_min, bias, None, True)
     return g, alpha
 
 
 def beta_gate(logits: torch.Tensor) -> torch.Tensor:
-    """``clamp(sigmoid(logits), eps, 1-eps)`` elementwise (projections.py:207-209)."""
+    """``clamp(sigmoid(logits), eps, 1-eps)`` elementwise (projections.py:207-209);
+    differentiable (``kda_gates_bwd``)."""
+    if _needs_grad(logits):
+        return _Beta.apply(logits)
     _, _, beta = _gates(None, None, -1.0, None, logits, False)
     return beta
+
+
+class _Decay(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, logits, a_log, bias, g_min):
+        g, alpha, _ = _gates(logits, a_log, g_min, bias, None, True)
+        ctx.save_for_backward(logits, a_log, bias)
+        ctx.g_min = g_min
+        return g, alpha
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dg, dalpha):
+        logits, a_log, bias = ctx.saved_tensors
+        lib = _lib.load()
+        batch, tokens, heads, key_dim = logits.shape
+        z = _aligned(logits)
+        zb = None if bias is None else _aligned(bias.to(logits.dtype))
+        al = a_log.to(torch.float32).contiguous()
+        if dg is None:
+            dg = torch.zeros_like(z)
+        dgc = _aligned(dg.to(z.dtype))
+        dac = None if dalpha is None else _aligned(dalpha.to(z.dtype))
+        dz = torch.empty_like(z)
+        acc = _acc_dtype(z.dtype)
+        dzb = torch.zeros(heads, key_dim, dtype=acc, device=z.device) if bias is not None and ctx.needs_input_grad[2] \
+            else None
+        dal = torch.zeros(heads, dtype=acc, device=z.device) if ctx.needs_input_grad[1] else None
+        _lib.check(lib.kda_gates_bwd(
+            z.data_ptr(), _lib.ptr(zb), al.data_ptr(), ctx.g_min, dgc.data_ptr(), _lib.ptr(dac), dz.data_ptr(),
+            _lib.ptr(dzb), _lib.ptr(dal), None, None, None, batch * tokens, heads, key_dim,
+            _lib.dtype_code(z.dtype), _prep.stream(z.device),
+        ))
+        return (dz if ctx.needs_input_grad[0] else None, None if dal is None else dal.to(a_log.dtype),
+                None if dzb is None else dzb.to(bias.dtype), None)
+
+
+class _Beta(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, logits):
+        _, _, beta = _gates(None, None, -1.0, None, logits, False)
+        ctx.save_for_backward(logits)
+        return beta
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dbeta):
+        (logits,) = ctx.saved_tensors
+        lib = _lib.load()
+        bl = logits.contiguous()
+        db = dbeta.to(bl.dtype).contiguous()
+        dl = torch.empty_like(bl)
+        _lib.check(lib.kda_gates_bwd(
+            None, None, None, -1.0, None, None, None, None, None, bl.data_ptr(), db.data_ptr(), dl.data_ptr(),
+            1, bl.numel(), 1, _lib.dtype_code(bl.dtype), _prep.stream(bl.device),
+        ))
+        return dl
 
 
 def chunkwise_kda_with_decay(
@@ -302,8 +436,14 @@ def rmsnorm_gate(
     if eps <= 0:
         raise ValueError("eps must be > 0")
     _lib.require_gpu(x)
-    _prep.reject_autograd(x, weight, gate_logits)
+    if _needs_grad(x, weight, gate_logits):
+        return _RMSNormGate.apply(x, weight, gate_logits, float(eps), per_head)
+    return _norm_forward(x, weight, gate_logits, eps, per_head)
+
+
+def _norm_forward(x, weight, gate_logits, eps, per_head):
     lib = _lib.load()
+    batch, tokens, heads, head_dim = x.shape
     xc = _aligned(x)
     wc = None if weight is None else _aligned(weight.to(x.dtype))
     gc = None if gate_logits is None else _aligned(gate_logits)
@@ -314,6 +454,39 @@ def rmsnorm_gate(
     )
     _lib.check(status)
     return y
+
+
+class _RMSNormGate(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, x, weight, gate_logits, eps, per_head):
+        y = _norm_forward(x, weight, gate_logits, eps, per_head)
+        ctx.save_for_backward(x, weight, gate_logits)
+        ctx.cfg = (eps, per_head)
+        return y
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, dy):
+        x, weight, gate_logits = ctx.saved_tensors
+        eps, per_head = ctx.cfg
+        lib = _lib.load()
+        batch, tokens, heads, head_dim = x.shape
+        xc = _aligned(x)
+        wc = None if weight is None else _aligned(weight.to(x.dtype))
+        gc = None if gate_logits is None else _aligned(gate_logits)
+        dyc = _aligned(dy.to(x.dtype))
+        dx = torch.empty_like(xc)
+        dgl = None if gc is None else torch.empty_like(gc)
+        dw = None
+        if weight is not None and ctx.needs_input_grad[1]:
+            dw = torch.zeros(weight.shape, dtype=_acc_dtype(x.dtype), device=x.device)
+        _lib.check(lib.kda_rmsnorm_gate_bwd(
+            xc.data_ptr(), _lib.ptr(wc), per_head, _lib.ptr(gc), dyc.data_ptr(), dx.data_ptr(), _lib.ptr(dgl),
+            _lib.ptr(dw), batch * tokens, heads, head_dim, float(eps), _lib.dtype_code(x.dtype),
+            _prep.stream(x.device),
+        ))
+        return (dx if ctx.needs_input_grad[0] else None, None if dw is None else dw.to(weight.dtype),
+                dgl if gate_logits is not None and ctx.needs_input_grad[2] else None, None, None)
 
 
 __all__ = ["beta_gate", "chunkwise_kda_with_decay", "conv_silu", "lower_bounded_decay", "rmsnorm_gate"]
