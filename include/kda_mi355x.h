@@ -203,6 +203,25 @@ int kda_ut_transform(const void* k, const void* v, const void* g, const void* be
                      int64_t value_dim, void* stream);
 
 /*
+ * Backward of `kda_ut_transform`: the gradients of a loss through (M, U, W,
+ * log_gamma, k_gamma) with respect to (k, v, g, beta), as autograd takes them
+ * through src/kda/ut_transform.py:23-92 (M = (I + diag(beta) A)^-1 diag(beta)
+ * by triangular solve, W = M k_gamma, U = M v).  The upstream gradients are in
+ * `out_dtype` (f32 for bf16/f16/f32 inputs, f64 for f64), shaped like the
+ * forward outputs, each NULL for zero; dk, dv, dg, dbeta are written in
+ * `out_dtype` with the inputs' shapes.  One workgroup per (batch, head);
+ * workspace: kda_ut_transform_bwd_workspace_bytes.  count <= 1024.
+ */
+size_t kda_ut_transform_bwd_workspace_bytes(int64_t batch, int64_t count, int64_t heads,
+                                            int64_t key_dim, int out_dtype);
+
+int kda_ut_transform_bwd(const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                         const void* dM, const void* dU, const void* dW, const void* d_log_gamma,
+                         const void* d_k_gamma, void* dk, void* dv, void* dg, void* dbeta, int out_dtype,
+                         int64_t batch, int64_t count, int64_t heads, int64_t key_dim, int64_t value_dim,
+                         void* workspace, size_t workspace_bytes, void* stream);
+
+/*
  * Backward of the chunkwise operator: the gradients of a loss through
  * (out, final_state) = chunkwise(q, k, v, g, beta, initial_state) with respect
  * to every input.  Replaces the autograd backward of chunkwise_kda

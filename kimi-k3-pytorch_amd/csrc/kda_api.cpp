@@ -273,6 +273,34 @@ int kda_ut_transform(const void* k, const void* v, const void* g, const void* be
                              key_dim, value_dim, static_cast<hipStream_t>(stream));
 }
 
+size_t kda_ut_transform_bwd_workspace_bytes(int64_t batch, int64_t count, int64_t heads, int64_t key_dim,
+                                            int out_dtype) {
+  if (batch <= 0 || count <= 0 || heads <= 0 || key_dim <= 0) return 0;
+  return ut_transform_bwd_workspace_bytes(batch, count, heads, key_dim, out_dtype);
+}
+
+int kda_ut_transform_bwd(const void* k, const void* v, const void* g, const void* beta, int in_dtype, const void* dM,
+                         const void* dU, const void* dW, const void* d_log_gamma, const void* d_k_gamma, void* dk,
+                         void* dv, void* dg, void* dbeta, int out_dtype, int64_t batch, int64_t count, int64_t heads,
+                         int64_t key_dim, int64_t value_dim, void* workspace, size_t workspace_bytes, void* stream) {
+  g_detail[0] = '\0';
+  if (!is_input_dtype(in_dtype) || out_dtype != expected_state_dtype(in_dtype)) {
+    set_detail("ut_transform_bwd: bad dtypes (in %d, out %d)", in_dtype, out_dtype);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (batch <= 0 || count <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) {
+    set_detail("ut_transform_bwd: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!k || !v || !g || !beta || !dk || !dv || !dg || !dbeta) {
+    set_detail("ut_transform_bwd: inputs and gradients must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  return launch_ut_transform_bwd(k, v, g, beta, in_dtype, dM, dU, dW, d_log_gamma, d_k_gamma, dk, dv, dg, dbeta,
+                                 out_dtype, batch, count, heads, key_dim, value_dim, workspace, workspace_bytes,
+                                 static_cast<hipStream_t>(stream));
+}
+
 size_t kda_chunk_bwd_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim,
                                      int64_t value_dim) {
   if (batch <= 0 || tokens <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) return 0;

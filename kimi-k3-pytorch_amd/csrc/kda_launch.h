@@ -48,6 +48,15 @@ int launch_ut_transform(const void* k, const void* v, const void* g, const void*
                         void* U, void* W, void* log_gamma, void* k_gamma, int out_dtype, int64_t batch,
                         int64_t count, int64_t heads, int64_t key_dim, int64_t value_dim, hipStream_t stream);
 
+// Backward of the public UT transform (csrc/kda_ut_transform.hip).
+size_t ut_transform_bwd_workspace_bytes(int64_t batch, int64_t count, int64_t heads, int64_t key_dim, int out_dtype);
+
+int launch_ut_transform_bwd(const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                            const void* dM, const void* dU, const void* dW, const void* dlg, const void* dkg,
+                            void* dk, void* dv, void* dg, void* dbeta, int out_dtype, int64_t batch, int64_t count,
+                            int64_t heads, int64_t key_dim, int64_t value_dim, void* ws, size_t ws_bytes,
+                            hipStream_t stream);
+
 // Backward of the chunkwise operator (csrc/kda_chunk_bwd.hip).
 size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
 

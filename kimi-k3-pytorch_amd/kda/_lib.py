@@ -77,6 +77,8 @@ SIGNATURES = {
     "kda_conv_silu_bwd": (_I, [_P] * 11 + [_L] * 5 + [_I, ctypes.c_double, _I, _P]),
     "kda_gates_bwd": (_I, [_P, _P, _P, ctypes.c_double] + [_P] * 8 + [_L, _L, _L, _I, _P]),
     "kda_rmsnorm_gate_bwd": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _L, _L, _L, ctypes.c_double, _I, _P]),
+    "kda_ut_transform_bwd_workspace_bytes": (_S, [_L, _L, _L, _L, _I]),
+    "kda_ut_transform_bwd": (_I, [_P, _P, _P, _P, _I] + [_P] * 9 + [_I, _L, _L, _L, _L, _L, _P, _S, _P]),
     "kda_chunk_bwd_workspace_bytes": (_S, [_L, _L, _L, _L, _L]),
     "kda_chunk_bwd": (
         _I,

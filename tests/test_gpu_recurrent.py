@@ -154,6 +154,36 @@ def test_ut_transform_matches_oracle():
 
 
 @pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-10), (torch.float32, 1e-4)])
+@pytest.mark.parametrize("shape", [(2, 9, 2, 5, 3), (1, 64, 2, 128, 64), (1, 37, 3, 16, 128), (2, 1, 1, 8, 4)])
+def test_ut_transform_gradients_match_oracle_autograd(dtype, tol, shape):
+    # ut_transform under autograd (the reference's transform is plain torch,
+    # src/kda/ut_transform.py:23-92): every output carries a gradient
+    B, C, H, K, V = shape
+    _, k, v, g, beta, _ = random_core(batch=B, tokens=C, heads=H, key_dim=K, value_dim=V, dtype=torch.float64,
+                                      seed=C + K)
+    k = torch.nn.functional.normalize(k, dim=-1)
+    leaves = [t.to(dtype) for t in (k, v, g, beta)]
+    gpu = [t.to(DEV).requires_grad_() for t in leaves]
+    cpu = [t.double().requires_grad_() for t in leaves]
+    gen = torch.Generator().manual_seed(3)
+    w_m = torch.randn(B, H, C, C, generator=gen, dtype=torch.float64)
+    w_u = torch.randn(B, C, H, V, generator=gen, dtype=torch.float64)
+    w_w, w_l, w_k = (torch.randn(B, C, H, K, generator=gen, dtype=torch.float64) for _ in range(3))
+    out = kda.ut_transform(*gpu, secondary_tile_size=4)
+    ((out.M.double() * w_m.to(DEV)).sum() + (out.U.double() * w_u.to(DEV)).sum()
+     + (out.W.double() * w_w.to(DEV)).sum() + (out.log_gamma.double() * w_l.to(DEV)).sum()
+     + (out.k_gamma.double() * w_k.to(DEV)).sum()).backward()
+    ki, vi, gi, bi = (t.transpose(1, 2) for t in cpu)
+    ref = ora.ut_transform_internal(ki, vi, gi, bi, 4)
+    ((ref["M"] * w_m).sum() + (ref["U"].transpose(1, 2) * w_u).sum() + (ref["W"].transpose(1, 2) * w_w).sum()
+     + (ref["log_gamma"].transpose(1, 2) * w_l).sum() + (ref["k_gamma"].transpose(1, 2) * w_k).sum()).backward()
+    for name, a, b in zip("kvgb", gpu, cpu):
+        e = rel_err(a.grad, b.grad)
+        print(f"ut_transform {dtype} {shape} d{name}: {e:.2e}")
+        assert e < tol, (name, e)
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float64, 1e-10), (torch.float32, 1e-4)])
 def test_states_per_token_gradients_match_oracle_autograd(dtype, tol):
     # recurrent_kda(return_states_per_token=True) under autograd: every returned
     # state carries a gradient (kda_recurrent_bwd); the oracle's token loop,
