@@ -27,6 +27,8 @@ Metric: "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s".
 * fused_stages: the kernels around the operator (kda.fused) on the same
                shape, as HBM GB/s (not part of `value`).
 * prefill_k64: the prefill at the gpu_48gb head shape (K = V = 64).
+* prefill_f32: f32 inputs at the prefill shape (the split-bf16 chunk path),
+               next to the exact recurrence kernel on the same sequence.
 * decay_fusion: the decay feeding the prefill: gates kernel then chunk
                kernel, against the chunk kernel forming g from the logits.
 * backward   : the chunkwise backward (all input gradients) on the prefill
@@ -731,6 +733,51 @@ def bench_dropin(steps, warmup):
     }
 
 
+def bench_prefill_f32(steps, warmup):
+    """f32 inputs at the long-context shape through kda.chunkwise_kda: the
+    split-bf16 chunk path of a dense call, next to the exact recurrence kernel
+    (the same sequence passed as one packed document, which that path does not
+    take)."""
+    import torch
+
+    import kda
+    from kda import _lib
+
+    device = torch.device("cuda", 0)
+    q, k, v, g, beta, s0 = (t.float() for t in _inputs(P_B, P_T, P_H, P_K, P_V, 0.02, 0, device))
+
+    def timed(fn, n, w):
+        for _ in range(w):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / n
+
+    L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
+    _lib.check(_lib.load().kda_chunk_fwd_plan(P_B, P_B * P_T, P_H, P_K, P_V, _lib.dtype_code(torch.float32),
+                                              ctypes.byref(L), ctypes.byref(segs)))
+    with torch.no_grad():
+        split_ms = timed(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True), steps, warmup)
+        rec_ms = timed(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True, cu_seqlens=[0, P_T]), 2, 1)
+    nbytes = 2 * prefill_bytes(P_B, P_T, P_H, P_K, P_V, n_state_io=1)  # every tensor f32
+    return {
+        "workload": f"kda.chunkwise_kda B={P_B} T={P_T} H={P_H} K=V={P_K} f32 inputs, f32 state N(0,0.02) in, "
+                    "final state out",
+        "plan": L.value,
+        "ms": round(split_ms, 5),
+        "tokens_per_s": round(P_B * P_T / (split_ms * 1e-3), 1),
+        "achieved_gbs": round(nbytes / (split_ms * 1e-3) / 1e9, 1),
+        "algorithmic_bytes": nbytes,
+        "recurrence_kernel_ms": round(rec_ms, 5),
+        "speedup_vs_recurrence": round(rec_ms / split_ms, 2),
+    }
+
+
 def prefill_plan():
     from kda import _lib
 
@@ -863,6 +910,7 @@ def main() -> int:
         "frac_hbm": round(k64_bytes / (k64_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "algorithmic_bytes": k64_bytes,
     }
+    result["prefill_f32"] = bench_prefill_f32(args.steps, args.warmup)
     result["decay_fusion"] = bench_decay_fusion()
     result["backward"] = bench_backward()
     result["cache_reorder"] = bench_cache()

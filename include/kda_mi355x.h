@@ -90,7 +90,9 @@ int kda_decode_step(const void* q, const void* k, const void* v, const void* g,
                     int64_t value_dim, void* stream);
 
 /*
- * Workspace bytes `kda_chunk_fwd` needs for these sizes (0 if none).
+ * Workspace bytes `kda_chunk_fwd` needs for these sizes (0 if none), for
+ * dense sequences of total_tokens / num_seqs tokens; packed documents off the
+ * MFMA path need none, and an f32-state call never needs more.
  * No reference counterpart (the reference allocates per call).
  */
 size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads,
@@ -99,7 +101,8 @@ size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int
 /*
  * The schedule `kda_chunk_fwd` picks for these sizes: *chunks_per_segment is
  * the number of 64-token chunks per segment (0 when every sequence is one
- * segment, -1 when the shape runs the exact recurrence kernel) and *segments
+ * segment, -2 when the shape takes the split-bf16 chunk path for dense
+ * sequences, -1 when it runs the exact recurrence kernel) and *segments
  * the bound on segments it sizes its workspace for.  No reference
  * counterpart (the reference has one schedule, a Python loop over chunks,
  * src/kda/chunkwise.py:61-102); benchmarks and tests use it to attribute
@@ -121,7 +124,14 @@ int kda_chunk_fwd_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, in
  * independent `chunkwise_kda` call.
  * The MFMA path covers bf16/f16 inputs with K <= 128 a multiple of 16 (a smaller K is
  * zero-padded to 128 channels inside the kernel) and V a multiple of 16 in
- * 16..256; other shapes and f32/f64 inputs run the exact recurrence kernel.
+ * 16..256.  Dense calls (no cu_seqlens) of other bf16/f16/f32 inputs with K
+ * and V <= 128 and an f32 state take the split-bf16 chunk path: per-chunk
+ * operands in a chunk-parallel kernel, the state scan with every product on
+ * split operands (x = hi + lo, two bf16 each, relative error about 2^-17) and
+ * the outputs in a second chunk-parallel kernel; its workspace is
+ * B x H x ceil(T/64) records of 593 KiB (K = V = 128).  The rest (packed
+ * documents off the MFMA path, K or V > 128, f64 inputs, a bf16/f16 state)
+ * runs the exact recurrence kernel, which needs no workspace.
  */
 int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
                   int in_dtype, const void* initial_state, void* final_state, int state_dtype,
@@ -160,10 +170,11 @@ int kda_chunk_fwd_decay(const void* q, const void* k, const void* v, const void*
  * No counterpart in the reference.  Same arguments, checks and kernels as
  * `kda_chunk_fwd`, minus the workspace: it lives in a static device array of
  * KDA_NOALLOC_SCRATCH_BYTES that each GPU the library runs on holds until the
- * process ends.  A prefill whose `kda_chunk_fwd_workspace_bytes` exceeds it
- * returns KDA_ERR_WORKSPACE before anything is launched (128 MiB covers one
- * 8192-token sequence at H=16, which needs 72.5 MB; shapes with
- * batch * heads >= 192 need only the small chunk maps).  The call performs
+ * process ends.  A prefill whose workspace exceeds it returns
+ * KDA_ERR_WORKSPACE before anything is launched (128 MiB covers one
+ * 8192-token bf16 sequence at H=16, which needs 72.5 MB; shapes with
+ * batch * heads >= 192 need only the small chunk maps; the split-bf16 path's
+ * records, 593 KiB per 64 tokens and head at K = V = 128, cover 221 of them).  The call performs
  * no device allocation.  All calls on one GPU share that GPU's array:
  * calls that overlap on one GPU (two streams, two host threads) race.  The
  * stream must belong to the current device.

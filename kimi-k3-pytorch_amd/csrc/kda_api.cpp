@@ -169,12 +169,13 @@ int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, co
   if (st != KDA_OK) return st;
   st = check_seq(cu_seqlens, dense_span, num_seqs, total_tokens);
   if (st != KDA_OK) return st;
-  const size_t need = chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype);
+  kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
+  const size_t need = chunk_call_workspace_bytes(seq, num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype,
+                                                 state_dtype);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_detail("chunk_fwd needs %zu workspace bytes, got %zu", need, workspace_bytes);
     return KDA_ERR_WORKSPACE;
   }
-  kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
   return launch_chunk(q, k, v, g, beta, in_dtype, initial_state, final_state, state_dtype, out, seq, num_seqs,
                       total_tokens, heads, key_dim, value_dim, workspace, workspace_bytes,
                       static_cast<hipStream_t>(stream));
@@ -198,12 +199,15 @@ int kda_chunk_fwd_decay(const void* q, const void* k, const void* v, const void*
     set_detail("chunk_fwd_decay: g_min must be negative");
     return KDA_ERR_INVALID_ARGUMENT;
   }
-  const size_t need = chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype);
+  kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
+  int64_t per_segment = 0, segments = 0;  // off the MFMA path the launcher reports the shape unsupported
+  chunk_plan(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype, &per_segment, &segments);
+  const size_t need =
+      per_segment >= 0 ? chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype) : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_detail("chunk_fwd_decay needs %zu workspace bytes, got %zu", need, workspace_bytes);
     return KDA_ERR_WORKSPACE;
   }
-  kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
   return launch_chunk_decay(q, k, v, decay_logits, decay_bias, a_log, static_cast<float>(g_min), beta, in_dtype,
                             initial_state, final_state, state_dtype, out, seq, num_seqs, total_tokens, heads, key_dim,
                             value_dim, workspace, workspace_bytes, static_cast<hipStream_t>(stream));
@@ -224,7 +228,8 @@ int kda_chunk_fwd_profiled(const void* q, const void* k, const void* v, const vo
   if (st != KDA_OK) return st;
   st = check_seq(cu_seqlens, dense_span, num_seqs, total_tokens);
   if (st != KDA_OK) return st;
-  const size_t need = chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype);
+  const size_t need = chunk_call_workspace_bytes(kda::SeqDesc{cu_seqlens, dense_span, valid_lens}, num_seqs,
+                                                 total_tokens, heads, key_dim, value_dim, in_dtype, state_dtype);
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_detail("chunk_fwd needs %zu workspace bytes, got %zu", need, workspace_bytes);
     return KDA_ERR_WORKSPACE;

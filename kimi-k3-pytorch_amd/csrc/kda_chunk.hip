@@ -1982,7 +1982,9 @@ namespace kda_host {
 void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
                 int in_dtype, int64_t* chunks_per_segment, int64_t* segments) {
   if (!kda::mfma_path(in_dtype, in_dtype == KDA_DTYPE_F64 ? KDA_DTYPE_F64 : KDA_DTYPE_F32, key_dim, value_dim)) {
-    *chunks_per_segment = -1;  // the exact recurrence kernel
+    // dense sequences take the split-bf16 chunk path where it applies (-2),
+    // everything else the exact recurrence kernel (-1)
+    *chunks_per_segment = chunk_split_path(in_dtype, KDA_DTYPE_F32, key_dim, value_dim) ? -2 : -1;
     *segments = num_seqs;
     return;
   }
@@ -1993,10 +1995,30 @@ void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t k
 
 size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
                              int64_t value_dim, int in_dtype) {
-  if (!kda::mfma_path(in_dtype, in_dtype == KDA_DTYPE_F64 ? KDA_DTYPE_F64 : KDA_DTYPE_F32, key_dim, value_dim))
-    return 0;
+  if (!kda::mfma_path(in_dtype, in_dtype == KDA_DTYPE_F64 ? KDA_DTYPE_F64 : KDA_DTYPE_F32, key_dim, value_dim)) {
+    // sized for a dense call (num_seqs rows of total_tokens / num_seqs tokens)
+    // on the split-bf16 chunk path; the recurrence kernel needs none
+    if (!chunk_split_path(in_dtype, KDA_DTYPE_F32, key_dim, value_dim) || num_seqs <= 0) return 0;
+    return chunk_split_workspace_bytes(num_seqs, (total_tokens + num_seqs - 1) / num_seqs, heads, key_dim, value_dim);
+  }
   const kda::Plan p = kda::make_plan(num_seqs, total_tokens, heads, value_dim);
   return kda::map_bytes(num_seqs) + kda::segment_bytes(p, heads, value_dim);
+}
+
+// Whether a call off the MFMA path takes the split-bf16 chunk path: dense
+// sequences (no packed documents) of a shape that path covers.
+static bool split_call(const kda::SeqDesc& seq, int64_t N, int64_t total_tokens, int in_dtype, int state_dtype,
+                       int64_t K, int64_t V) {
+  return seq.cu_seqlens == nullptr && seq.dense_span > 0 && N > 0 && N * seq.dense_span == total_tokens &&
+         chunk_split_path(in_dtype, state_dtype, K, V);
+}
+
+size_t chunk_call_workspace_bytes(const kda::SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H, int64_t K,
+                                  int64_t V, int in_dtype, int state_dtype) {
+  if (kda::mfma_path(in_dtype, state_dtype, K, V)) return chunk_workspace_bytes(N, total_tokens, H, K, V, in_dtype);
+  if (split_call(seq, N, total_tokens, in_dtype, state_dtype, K, V))
+    return chunk_split_workspace_bytes(N, seq.dense_span, H, K, V);
+  return 0;
 }
 
 int launch_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
@@ -2005,6 +2027,15 @@ int launch_chunk(const void* q, const void* k, const void* v, const void* g, con
                  hipStream_t stream, KernelEvents* ev) {
   using namespace kda;
   if (!mfma_path(in_dtype, state_dtype, K, V)) {
+    if (split_call(seq, N, total_tokens, in_dtype, state_dtype, K, V)) {
+      // dense sequences: the chunk path of split-bf16 products
+      mark(ev, 0, stream);
+      const int st = launch_chunk_split(q, k, v, g, beta, in_dtype, static_cast<const float*>(s_in),
+                                        static_cast<float*>(s_out), out, seq.valid_lens, N, seq.dense_span, H, K,
+                                        V, workspace, workspace_bytes, stream);
+      mark(ev, 1, stream);
+      return st;
+    }
     mark(ev, 0, stream);
     const int st = launch_recurrent(q, k, v, g, beta, in_dtype, s_in, s_out, state_dtype, out, nullptr, seq, N, H,
                                     K, V, stream, false);

@@ -97,6 +97,10 @@ struct Args {
   float* ws;
   int64_t B, T, H, K, V, NC;
   Layout L;
+  // the forward through these kernels (prep_kernel, fscan_kernel, out_kernel)
+  const int32_t* valid;  // [B] right-padding lengths or null (prep_kernel)
+  float* sT;             // [B,H,K,V] final state or null (fscan_kernel)
+  IT* out;               // [B,T,H,V] (out_kernel)
 };
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
@@ -249,10 +253,12 @@ __device__ __forceinline__ f32x4 widen(typename Raw4<IT>::type x) {
 // into LDS rows of stride RS, zero past T and X.  When the columns lie inside
 // X in whole 4-element groups (the usual case) every load of a thread is
 // issued, from a row clamped into the sequence, before its first conversion.
+// Rows at or past Tv (default T: right padding) read as zero too.
 template <class IT, int NCOL, int RS, int NT>
 __device__ __forceinline__ void load_rows(float* dst, const IT* src, int64_t b, int64_t t0, int64_t T, int64_t H,
-                                          int64_t h, int64_t X, int col0, int tid) {
+                                          int64_t h, int64_t X, int col0, int tid, int64_t Tv = -1) {
   constexpr int G = NCOL / 4, PER = kC * G / NT;
+  if (Tv < 0) Tv = T;
   static_assert(PER * NT == kC * G, "the tile must split evenly over the threads");
   typedef typename Raw4<IT>::type raw_t;
   if ((X & 3) == 0 && col0 + NCOL <= X) {
@@ -266,7 +272,7 @@ __device__ __forceinline__ void load_rows(float* dst, const IT* src, int64_t b, 
 #pragma unroll
     for (int it = 0; it < PER; ++it) {
       const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
-      *reinterpret_cast<f32x4*>(&dst[r * RS + c4]) = t0 + r < T ? widen<IT>(v[it]) : zero4();
+      *reinterpret_cast<f32x4*>(&dst[r * RS + c4]) = t0 + r < Tv ? widen<IT>(v[it]) : zero4();
     }
   } else {
     for (int it = 0; it < PER; ++it) {
@@ -276,7 +282,7 @@ __device__ __forceinline__ void load_rows(float* dst, const IT* src, int64_t b, 
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
         const int64_t col = col0 + c4 + u;
-        x[u] = (t < T && col < X) ? to_float(src[tok(b, t, T, H, h) * X + col]) : 0.f;
+        x[u] = (t < Tv && col < X) ? to_float(src[tok(b, t, T, H, h) * X + col]) : 0.f;
       }
       *reinterpret_cast<f32x4*>(&dst[r * RS + c4]) = x;
     }
@@ -400,13 +406,19 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
   constexpr int Kp = KP;
   const int Vp = a.L.Vp;
   float* ws = a.ws + ch * a.L.per;
+  // padded tokens (t >= Tv) enter as zero rows: no decay, no write, no output
+  int64_t Tv = a.T;
+  if (a.valid != nullptr) {
+    const int64_t n = a.valid[b];
+    Tv = n < 0 ? 0 : (n < a.T ? n : a.T);
+  }
 
-  load_rows<IT, KP, kRS, kPT>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid);
-  load_rows<IT, KP, kRS, kPT>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid);
-  load_rows<IT, KP, kRS, kPT>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid);
+  load_rows<IT, KP, kRS, kPT>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid, Tv);
+  load_rows<IT, KP, kRS, kPT>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid, Tv);
+  load_rows<IT, KP, kRS, kPT>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid, Tv);
   if (tid < kC) {
     const int64_t t = t0 + tid;
-    bS[tid] = t < a.T ? to_float(a.beta[tok(b, t, a.T, a.H, h)]) : 0.f;
+    bS[tid] = t < Tv ? to_float(a.beta[tok(b, t, a.T, a.H, h)]) : 0.f;
   }
   for (int idx = tid; idx < kC * kRC; idx += kPT) {
     AS[idx] = 0.f;
@@ -570,7 +582,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     for (int r = 0; r < 4; ++r) qS[(16 * rt + 4 * lg4 + r) * kRS + 16 * ct + li] = acc[r];
   }
   for (int s0 = 0; s0 < Vp; s0 += 32)  // v over lg (no longer read)
-    load_rows<IT, 32, kRS, kPT>(lgS + s0, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
+    load_rows<IT, 32, kRS, kPT>(lgS + s0, a.v, b, t0, a.T, a.H, h, a.V, s0, tid, Tv);
   __syncthreads();
   for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {  // W and W^T split
     float x[8], y[8];
@@ -738,6 +750,12 @@ __device__ __forceinline__ void fscan_body(const Args<IT>& a, int64_t lb, unsign
     }
     __syncthreads();
   }
+  if (a.sT != nullptr) {  // the final state (the forward through these kernels)
+    for (int idx = tid; idx < KP * 16; idx += kST) {
+      const int r = idx >> 4, cc = idx & 15;
+      if (r < a.K && col0 + cc < a.V) a.sT[((b * a.H + h) * a.K + r) * a.V + col0 + cc] = SS[r * kTS + cc];
+    }
+  }
 }
 
 template <class IT>
@@ -897,6 +915,56 @@ __global__ __launch_bounds__(kST) void scan_kernel(const Args<IT> a) {
     fscan_body<IT, KP>(a, lb, smem);
   else
     bscan_body<IT, KP>(a, lb - n, smem);
+}
+
+// ---- the forward through the same chunk operands ------------------------------
+// prep_kernel, then fscan_kernel (the forward scan alone, which leaves each
+// chunk's start state S and pseudo-values Vt in the workspace and writes the
+// final state), then out_kernel: O = Qg S + Aqk Vt per chunk, all chunks in
+// parallel.  This is the chunkwise prefill for inputs the bf16 MFMA path does
+// not take (f32 inputs, key or value dims off its grid), at the split-bf16
+// accuracy of the scans.
+template <class IT, int KP>
+__global__ __launch_bounds__(kST) void fscan_kernel(const Args<IT> a) {
+  __shared__ __attribute__((aligned(16))) unsigned char smem[FscanLds<KP>::bytes];
+  fscan_body<IT, KP>(a, xcd_block(blockIdx.x, gridDim.x), smem);
+}
+
+constexpr int kOT = 512;  // threads of out_kernel: one 16 x 16 output tile per wave and slab
+template <class IT, int KP>
+__global__ __launch_bounds__(kOT) void out_kernel(const Args<IT> a) {
+  __shared__ float QgT[KP * kRC];  // Qg^T: channel-major, positions contiguous
+  __shared__ float AqT[kC * kRC];  // Aqk^T
+  __shared__ float Ss[KP * kSS];   // S slab [channel][32 columns]
+  __shared__ float Vs[kC * kSS];   // Vt slab [position][32 columns]
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
+  const int64_t ch = blockIdx.x;
+  const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
+  const int64_t t0 = c * kC;
+  const float* ws = a.ws + ch * a.L.per;
+  {  // the split records back to f32: Qgt[col * 64 + r] = Qg[r][col], Aqkt[j * 64 + i] = Aqk[i][j]
+    const __bf16* qg = reinterpret_cast<const __bf16*>(ws + a.L.Qgt);
+    const __bf16* aq = reinterpret_cast<const __bf16*>(ws + a.L.Aqkt);
+    for (int idx = tid; idx < kC * KP; idx += kOT)
+      QgT[(idx >> 6) * kRC + (idx & 63)] = static_cast<float>(qg[idx]) + static_cast<float>(qg[kC * KP + idx]);
+    for (int idx = tid; idx < kC * kC; idx += kOT)
+      AqT[(idx >> 6) * kRC + (idx & 63)] = static_cast<float>(aq[idx]) + static_cast<float>(aq[kC * kC + idx]);
+  }
+  const int rt = w & 3, ct = w >> 2;
+  for (int s0 = 0; s0 < a.L.Vp; s0 += 32) {
+    __syncthreads();  // the previous slab's reads are done
+    load_ws<KP, 32, kSS, kOT>(Ss, ws + a.L.S, a.L.Vp, s0, tid);
+    load_ws<kC, 32, kSS, kOT>(Vs, ws + a.L.Vt, a.L.Vp, s0, tid);
+    __syncthreads();
+    f32x4 acc = mma_long(zero4(), Mat{QgT, 1, kRC}, 16 * rt, Mat{Ss, kSS, 1}, 16 * ct, KP);
+    acc = mma_long(acc, Mat{AqT, 1, kRC}, 16 * rt, Mat{Vs, kSS, 1}, 16 * ct, kC);
+    const int col = s0 + 16 * ct + li;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t t = t0 + 16 * rt + 4 * lg4 + r;
+      if (t < a.T && col < a.V) a.out[tok(b, t, a.T, a.H, h) * a.V + col] = from_compute<IT>(acc[r]);
+    }
+  }
 }
 
 // ---- grad_kernel: products that reduce over the state columns -----------------
@@ -1462,6 +1530,78 @@ size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int
   const size_t f32 = static_cast<size_t>(B * H * nc * L.per) * sizeof(float);
   const size_t f64 = chunk_bwd_f64_workspace_bytes(B, T, H, K, V);  // one size serves every dtype
   return f32 > f64 ? f32 : f64;
+}
+
+size_t chunk_split_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
+  const bwd::Layout L = bwd::make_layout(K, V);
+  const int64_t nc = (T + bwd::kC - 1) / bwd::kC;
+  return static_cast<size_t>(B * H * nc * L.per) * sizeof(float);
+}
+
+bool chunk_split_path(int in_dtype, int state_dtype, int64_t K, int64_t V) {
+  return (in_dtype == KDA_DTYPE_BF16 || in_dtype == KDA_DTYPE_F16 || in_dtype == KDA_DTYPE_F32) &&
+         state_dtype == KDA_DTYPE_F32 && K >= 1 && K <= 128 && V >= 1 && V <= 128;
+}
+
+template <class IT, int KP>
+static void launch_split(const bwd::Args<IT>& a, dim3 chunks, dim3 scans, hipStream_t s) {
+  hipLaunchKernelGGL((bwd::prep_kernel<IT, KP>), chunks, dim3(bwd::kPT), 0, s, a);
+  hipLaunchKernelGGL((bwd::fscan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
+  hipLaunchKernelGGL((bwd::out_kernel<IT, KP>), chunks, dim3(bwd::kOT), 0, s, a);
+}
+
+template <class IT>
+static int run_split(const IT* q, const IT* k, const IT* v, const IT* g, const IT* beta, const float* s0, float* sT,
+                     IT* out, const int32_t* valid, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, float* ws,
+                     hipStream_t s) {
+  bwd::Args<IT> a{};
+  a.q = q, a.k = k, a.v = v, a.g = g, a.beta = beta, a.s0 = s0;
+  a.ws = ws, a.B = B, a.T = T, a.H = H, a.K = K, a.V = V, a.NC = (T + bwd::kC - 1) / bwd::kC;
+  a.L = bwd::make_layout(K, V);
+  a.valid = valid, a.sT = sT, a.out = out;
+  const int64_t chunks = B * H * a.NC, scans = B * H * (a.L.Vp / 16);
+  if (chunks > 0x7fffffffLL || scans > 0x7fffffffLL) {
+    set_detail("chunk_fwd: grid too large");
+    return KDA_ERR_UNSUPPORTED;
+  }
+  const dim3 gc(static_cast<unsigned>(chunks)), gs(static_cast<unsigned>(scans));
+  if (a.L.Kp == 64)
+    launch_split<IT, 64>(a, gc, gs, s);
+  else
+    launch_split<IT, 128>(a, gc, gs, s);
+  return check_launch("chunk_fwd (split-bf16 chunk path)");
+}
+
+int launch_chunk_split(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                       const float* s_in, float* s_out, void* out, const int32_t* valid_lens, int64_t B, int64_t T,
+                       int64_t H, int64_t K, int64_t V, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (!chunk_split_path(in_dtype, KDA_DTYPE_F32, K, V) || B <= 0 || T <= 0 || H <= 0) {
+    set_detail("chunk_fwd: the split-bf16 chunk path needs bf16/f16/f32 inputs, K and V in 1..128 and T > 0");
+    return KDA_ERR_UNSUPPORTED;
+  }
+  if (workspace == nullptr || workspace_bytes < chunk_split_workspace_bytes(B, T, H, K, V)) {
+    set_detail("chunk_fwd: workspace of %zu bytes needed", chunk_split_workspace_bytes(B, T, H, K, V));
+    return KDA_ERR_WORKSPACE;
+  }
+  if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) {
+    set_detail("chunk_fwd: workspace must be 16-byte aligned");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  float* ws = static_cast<float*>(workspace);
+  switch (in_dtype) {
+    case KDA_DTYPE_BF16:
+      return run_split(static_cast<const bf16*>(q), static_cast<const bf16*>(k), static_cast<const bf16*>(v),
+                       static_cast<const bf16*>(g), static_cast<const bf16*>(beta), s_in, s_out, static_cast<bf16*>(out),
+                       valid_lens, B, T, H, K, V, ws, stream);
+    case KDA_DTYPE_F16:
+      return run_split(static_cast<const f16*>(q), static_cast<const f16*>(k), static_cast<const f16*>(v),
+                       static_cast<const f16*>(g), static_cast<const f16*>(beta), s_in, s_out, static_cast<f16*>(out),
+                       valid_lens, B, T, H, K, V, ws, stream);
+    default:
+      return run_split(static_cast<const float*>(q), static_cast<const float*>(k), static_cast<const float*>(v),
+                       static_cast<const float*>(g), static_cast<const float*>(beta), s_in, s_out,
+                       static_cast<float*>(out), valid_lens, B, T, H, K, V, ws, stream);
+  }
 }
 
 template <class IT, int KP>

@@ -32,6 +32,12 @@ struct KernelEvents {
   unsigned empty;
 };
 
+// The workspace one launch_chunk call needs: the MFMA path's maps and
+// segment records, the split-bf16 chunk path's per-chunk records, or none
+// (recurrence kernel).
+size_t chunk_call_workspace_bytes(const kda::SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H, int64_t K,
+                                  int64_t V, int in_dtype, int state_dtype);
+
 int launch_chunk(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
                  const void* s_in, void* s_out, int state_dtype, void* out, const kda::SeqDesc& seq, int64_t N,
                  int64_t total_tokens, int64_t H, int64_t K, int64_t V, void* workspace, size_t workspace_bytes,
@@ -64,6 +70,17 @@ int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
                      const void* dout, int in_dtype, const float* s0, const float* dsT, void* dq, void* dk, void* dv,
                      void* dg, void* dbeta, float* ds0, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+// The chunkwise forward through the backward's chunk operands (prep, forward
+// scan, output kernel; csrc/kda_chunk_bwd.hip): dense sequences with optional
+// right padding, f32 state, K and V up to 128.
+bool chunk_split_path(int in_dtype, int state_dtype, int64_t K, int64_t V);
+
+size_t chunk_split_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
+
+int launch_chunk_split(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
+                       const float* s_in, float* s_out, void* out, const int32_t* valid_lens, int64_t B, int64_t T,
+                       int64_t H, int64_t K, int64_t V, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
 // The same backward in f64 arithmetic (csrc/kda_chunk_bwd_f64.hip).
 size_t chunk_bwd_f64_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);

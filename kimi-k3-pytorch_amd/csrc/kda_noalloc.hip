@@ -79,7 +79,9 @@ extern "C" int kda_chunk_fwd_noalloc(const void* q, const void* k, const void* v
     return KDA_ERR_INVALID_ARGUMENT;
   }
   // the size check comes before any device call: an oversize request launches nothing
-  const size_t need = kda_chunk_fwd_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype);
+  const kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
+  const size_t need = chunk_call_workspace_bytes(seq, num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype,
+                                                 state_dtype);
   if (need > kScratchBytes) {
     set_detail("chunk_fwd_noalloc: this prefill needs %zu workspace bytes; the static scratch holds %zu "
                "(use kda_chunk_fwd with a caller workspace)",

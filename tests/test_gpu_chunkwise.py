@@ -1,5 +1,6 @@
 """GPU parity of the chunkwise prefill (MFMA path for bf16/f16 with K <= 128 a
-multiple of 16, exact-recurrence path otherwise) against the CPU oracle.
+multiple of 16, the split-bf16 chunk path or the exact recurrence otherwise)
+against the CPU oracle.
 
 Tolerance (max|x - ref| / max|ref|, per tensor): bf16/f16 inputs <= 2e-2
 against the f32 oracle run on the same (exactly upcast) inputs; f32 inputs
@@ -232,7 +233,7 @@ def test_chunkwise_key_dims_below_128(monkeypatch, shape, segment_chunks):
     # K <= 128, a multiple of 16, takes the MFMA path, padded to 128 channels in the kernel
     if segment_chunks is not None:
         monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", segment_chunks)
-    assert _plan(*shape) >= 0 and _plan(*shape, dtype=torch.float32) == -1
+    assert _plan(*shape) >= 0 and _plan(*shape, dtype=torch.float32) == -2
     q, k, v, g, beta, state = workload(*shape, state_std=0.02, seed=24)
     ro, rs = _oracle_f32(q, k, v, g, beta, state)
     got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True)
@@ -240,8 +241,8 @@ def test_chunkwise_key_dims_below_128(monkeypatch, shape, segment_chunks):
 
 
 def test_chunkwise_key_dim_off_the_mfma_grid():
-    # K = 40 (not a multiple of 16) runs the exact recurrence kernel
-    assert _plan(1, 100, 2, 40, 32) == -1
+    # K = 40 (not a multiple of 16) runs the split-bf16 chunk path
+    assert _plan(1, 100, 2, 40, 32) == -2
     q, k, v, g, beta, state = workload(1, 100, 2, 40, 32, state_std=0.02, seed=26)
     ro, rs = _oracle_f32(q, k, v, g, beta, state)
     _check(kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True), ro, rs, label="K=40")
