@@ -17,23 +17,24 @@
 //   dA = diag(b) dL, then the pair sums of dA and dAqk with exact exponents,
 //   the exp factors, and dg = reverse cumulative sum of d lg over the chunk.
 //
-// Four kernels with f32 accumulation everywhere.  prep and pair multiply on
-// the f32 MFMA (v_mfma_f32_16x16x4f32); the two state scans and grad's slab
-// products use split-bf16 operands on v_mfma_f32_16x16x32_bf16 (x = hi + lo,
-// hi = bf16(x), lo = bf16(x - hi); hi*hi + hi*lo + lo*hi, dropping terms of
-// relative size 2^-17), which keeps the f32-input gradients within about
-// 1e-5 of the f64 oracle.  Decay products use a 16-row block factorisation
-// on the MFMA, with an exact pairwise-exponent path for chunks whose decays
-// leave its range (any g > 0, or a block decaying past e^-80).
-//   prep_kernel   one block per (sequence, head, chunk): A, Aqk, N by
-//                 forward substitution, W, U, Kt, Qg, Kg, D;
-//   scan_kernel   one block per (sequence, head, 16 state columns) and
-//                 direction: forward, the chunk start states S and the
-//                 pseudo-values Vt; backward, dS' and dVt per chunk and dS0;
-//   grad_kernel   one block per chunk: dv, dbeta, and dQg, dKt, dKg, dA, dAqk;
-//   pair_kernel   one block per chunk: the pair sums and the final dq, dk, dg.
+// f32 accumulation everywhere.  prep and pair multiply on the f32 MFMA
+// (v_mfma_f32_16x16x4f32); the state scans and grad's slab products use
+// split-bf16 operands on v_mfma_f32_16x16x32_bf16 (x = hi + lo, hi = bf16(x),
+// lo = bf16(x - hi); hi*hi + hi*lo + lo*hi, dropping terms of relative size
+// 2^-17), which keeps the f32-input gradients within about 1e-5 of the f64
+// oracle.  Decay products use a 16-row block factorisation on the MFMA, with
+// an exact pairwise-exponent path for chunks whose decays leave its range
+// (any g > 0, or a block decaying past e^-80).
+//   prep_kernel         one block per (sequence, head, chunk): A, Aqk, N by
+//                       forward substitution, W, U, Kt, Qg, Kg, D;
+//   seg_kernel,         the forward scan (chunk start states S, pseudo-values
+//   seg_combine_kernel  Vt) and the backward scan (dS', dVt per chunk, dS0),
+//                       side by side, each cut into segments whose affine
+//                       maps are composed (section "segmented state scans");
+//   grad_kernel         one block per chunk: dv, dbeta, and dQg, dKt, dKg, dA, dAqk;
+//   pair_kernel         one block per chunk: the pair sums and the final dq, dk, dg.
 // Intermediates live in a caller-owned f32 workspace, one record per
-// (sequence, head, chunk).
+// (sequence, head, chunk), followed by the scans' segment records.
 #include <math.h>
 
 #include "kda_launch.h"
@@ -99,8 +100,13 @@ struct Args {
   Layout L;
   // the forward through these kernels (prep_kernel, fscan_kernel, out_kernel)
   const int32_t* valid;  // [B] right-padding lengths or null (prep_kernel)
-  float* sT;             // [B,H,K,V] final state or null (fscan_kernel)
+  float* sT;             // [B,H,K,V] final state or null (forward scan)
   IT* out;               // [B,T,H,V] (out_kernel)
+  // segmented state scans: nseg segments of seglen chunks per sequence,
+  // their records (P, Q, start state) at seg, [direction][B*H][nseg]
+  float* seg;
+  int nseg, seglen;
+  int dir0, ndir;  // the scans launched: directions dir0 .. dir0 + ndir - 1
 };
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
@@ -193,21 +199,6 @@ __device__ __forceinline__ f32x4 mma3(f32x4 acc, SMat A, int r0, SMat B, int c0,
   return acc;
 }
 
-// Four consecutive split values (an accumulator lane's four rows) into a
-// transposed split tile: row `col`, positions k .. k+3.
-__device__ __forceinline__ void store_split4(__bf16* base, int plane, int rs, int col, int k, f32x4 v) {
-  bf16x4 hi, lo;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    __bf16 h, l;
-    split_bf16(v[r], h, l);
-    hi[r] = h;
-    lo[r] = l;
-  }
-  *reinterpret_cast<bf16x4*>(base + col * rs + k) = hi;
-  *reinterpret_cast<bf16x4*>(base + plane + col * rs + k) = lo;
-}
-
 // Split record in the workspace: n bf16 hi values, then n lo values.  Eight
 // consecutive values from element idx (a multiple of 8) as two 16-byte stores.
 __device__ __forceinline__ void put_split8(float* rec, int n, int idx, const float* x) {
@@ -227,14 +218,6 @@ __device__ __forceinline__ void put_split8(float* rec, int n, int idx, const flo
 __device__ __forceinline__ int64_t tok(const int64_t b, const int64_t t, const int64_t T, const int64_t H,
                                        const int64_t h) {
   return (b * T + t) * H + h;
-}
-
-// Blocks b and b + 8 run on the same XCD; renumber so that each XCD owns one
-// contiguous range of logical blocks (the column blocks of one head then
-// share their XCD's L2 for the chunk operands they all read).
-__device__ __forceinline__ int64_t xcd_block(unsigned b, unsigned nb) {
-  const unsigned per = nb / 8, rem = nb % 8, x = b % 8;
-  return static_cast<int64_t>(x) * per + (x < rem ? x : rem) + b / 8;
 }
 
 // Four consecutive elements of an input row: loaded raw, converted later, so
@@ -604,332 +587,488 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
   }
 }
 
-// ---- state scans ----------------------------------------------------------------
-// Block (sequence, head, 16 state columns), eight waves, with every product
-// on split-bf16 operands (hi + lo) whose f32 masters stay in LDS:
-//   forward:  Vt = U[:, cols] - W S  (the channel reduction split over waves
-//             0-3 and 4-7),  S <- D S + Kt^T Vt  (one row tile per wave);
-//   backward: dVt = Kt dS + Aqk^T dO  (waves 0-3, one row tile each) next to
-//             D dS + Qg^T dO  (waves 4-7, two row tiles each, kept in
-//             registers), then dS = that - W^T dVt  (waves 4-7).
-// The next chunk's operands (stored split by prep_kernel) are loaded into
-// registers while the current chunk is computed.
-constexpr int kST = 512;  // threads of the scan blocks
-constexpr int kPF = 4;    // f32x4 per thread of one 64 x 128 split record
-constexpr int kRSP(int kp) { return kp + 8; }  // LDS row stride (bf16) of channel-contiguous tiles
-constexpr int kRSC = kC + 8;                    // LDS row stride (bf16) of position-contiguous tiles
+// ---- segmented state scans ------------------------------------------------------
+// Both scans are affine maps of a K x N state X per chunk:
+//   forward  (chunks 0 .. NC-1):  R = U - W X,               X' = D X + Kt^T R
+//   backward (chunks NC-1 .. 0):  R = -(Kt X + Aqk^T dO),    X' = D X + W^T R + Qg^T dO
+// (forward X = S and R = Vt; backward X = dS', the gradient of the chunk's end
+// state, and R = -dVt).  The chunk chain of each sequence is cut into nseg
+// segments of seglen chunks:
+//   seg_kernel<SUM = true>   one block per (direction, sequence x head, segment
+//                            but the last): the segment's affine map
+//                            X_out = P X_in + Q, by running the chunk maps on
+//                            X = [0 | I] (V value columns, K transition columns);
+//   seg_combine_kernel       X_{g+1} = P_g X_g + Q_g along the segments (f32 MFMA);
+//   seg_kernel<SUM = false>  one block per (direction, sequence x head,
+//                            segment): the segment again from its true start
+//                            state, writing each chunk's X and R (and the final
+//                            state after the last chunk).
+// The state lives in f32 MFMA accumulators, one 16-column tile per wave and
+// kind (value, transition).  Every product uses split-bf16 operands
+// (x = hi + lo; hi*hi + hi*lo + lo*hi).  An accumulator pair (row tiles 2s,
+// 2s+1) is the B operand of reduction step s with the reduction index
+// permuted as perm_k; the A operands are stored in LDS with the same
+// permutation: fragment (J, s) holds, for lane (i, g), elements
+// M[16 J + i][32 s + perm_k(g, e)], e = 0..7, hi lanes then lo lanes (2 KB).
+constexpr int kSC = 512;  // threads of seg_kernel
 
-// One 64 x KP split record (2 planes) from the workspace into an LDS tile of
-// rows `rows` x `cols` (row stride rs, plane stride plane), f32x4 = 8 bf16.
-template <int KP>
-__device__ __forceinline__ void split_to_lds(__bf16* dst, int plane, int rs, int cols, const f32x4* src, int tid) {
-  constexpr int nq = kC * KP / 4, n = kC * KP;
-#pragma unroll
-  for (int m = 0; m < kPF; ++m) {
-    const int q4 = tid + kST * m;
-    if (q4 < nq) {
-      const int f = 8 * q4, pl = f / n, e = f % n, r = e / cols, c = e % cols;
-      *reinterpret_cast<f32x4*>(dst + pl * plane + r * rs + c) = src[m];
-    }
-  }
-}
+__device__ __forceinline__ int perm_k(int g, int e) { return e < 4 ? 4 * g + e : 12 + 4 * g + e; }
 
 template <int KP>
-__device__ __forceinline__ void fetch_split(f32x4* dst, const float* rec, int tid) {
-  constexpr int nq = kC * KP / 4;
-#pragma unroll
-  for (int m = 0; m < kPF; ++m) {
-    const int q4 = tid + kST * m;
-    if (q4 < nq) dst[m] = *reinterpret_cast<const f32x4*>(rec + 4 * q4);
-  }
-}
-
-struct FscanBuf {
-  f32x4 w[kPF], k[kPF];
-  float u[2], d;
+struct SegLds {
+  static constexpr int nrow = 4 * (KP / 32);   // fragments of a [64][KP] record
+  static constexpr int ncol = (KP / 16) * 2;   // fragments of a [KP][64] record
+  static constexpr int fa = 0;                  // forward W, backward Kt        [64][KP]
+  static constexpr int fb = fa + nrow * 2048;   // forward Kt^T, backward W^T    [KP][64]
+  static constexpr int fq = fb + ncol * 2048;   // backward Qg^T                 [KP][64]
+  static constexpr int faq = fq + ncol * 2048;  // backward Aqk^T                [64][64]
+  static constexpr int d = faq + 8 * 2048;      // D f32 [KP]
+  static constexpr int bytes = d + KP * 4;
 };
 
-template <class IT, int KP>
-__device__ __forceinline__ void fscan_fetch(FscanBuf& p, const Args<IT>& a, int64_t bh, int64_t c, int col0, int tid) {
-  const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
-  fetch_split<KP>(p.w, ws + a.L.Wr, tid);
-  fetch_split<KP>(p.k, ws + a.L.Ktt, tid);
+// A split record [R][NC] of the workspace (R x NC bf16 hi, then lo) held in
+// registers as 8-byte groups; thread tid takes the n consecutive groups from
+// tid * n (32 or 16 columns of one row), so its loads and LDS stores share one
+// base address with immediate offsets.
+template <int R, int NC>
+struct Rec {
+  static constexpr int n = R * NC / 2 / kSC;
+  static_assert(n * kSC * 2 == R * NC && (n == 8 || n == 4), "the record must split into runs of 4 or 8 groups");
+  uint2 v[n];
+  __device__ __forceinline__ void fetch(const float* rec, int tid) {
+    const uint4* p = reinterpret_cast<const uint4*>(rec) + tid * (n / 2);
 #pragma unroll
-  for (int m = 0; m < 2; ++m) {
-    const int idx = tid + kST * m;  // [64][16]
-    p.u[m] = ws[a.L.U + (idx >> 4) * a.L.Vp + col0 + (idx & 15)];
+    for (int j = 0; j < n / 2; ++j) {
+      const uint4 x = p[j];
+      v[2 * j] = uint2{x.x, x.y};
+      v[2 * j + 1] = uint2{x.z, x.w};
+    }
   }
-  if (tid < KP) p.d = ws[a.L.D + tid];
-}
-
-// LDS of the forward scan (bytes)
-template <int KP>
-struct FscanLds {
-  static constexpr int rs = kRSP(KP);
-  static constexpr int wr = 0;                                  // W split [64][KP]
-  static constexpr int kt = wr + 2 * kC * rs * 2;               // Kt^T split [KP][64]
-  static constexpr int st = kt + 2 * KP * kRSC * 2;             // S^T split [16][KP]
-  static constexpr int vt = st + 2 * 16 * rs * 2;               // Vt^T split [16][64]
-  static constexpr int ss = vt + 2 * 16 * kRSC * 2;             // S f32 [128][kTS]
-  static constexpr int us = ss + 128 * kTS * 4;                 // U, then Vt, f32 [64][kTS]
-  static constexpr int ps = us + kC * kTS * 4;                  // partial W S f32 [64][kTS]
-  static constexpr int ds = ps + kC * kTS * 4;                  // D f32 [128]
-  static constexpr int bytes = ds + 128 * 4;
+  // into fragment layout at byte offset base of the LDS
+  __device__ __forceinline__ void store(unsigned char* sm, int base, int tid) const {
+    constexpr int per_plane = R * NC / 4;
+    const int q0 = tid * n, plane = q0 / per_plane, el = (q0 % per_plane) * 4;
+    const int r = el / NC, c0 = el % NC;
+    const int f = (r >> 4) * (NC / 32) + (c0 >> 5);
+    unsigned char* dst = sm + base + f * 2048 + plane * 1024 + (r & 15) * 16 + ((c0 & 31) >> 4) * 8;
+#pragma unroll
+    for (int j = 0; j < n; ++j)  // column c0 + 4 j: group g = j % 4 of half j / 4 (of half (c0 & 31) / 16 when n = 4)
+      *reinterpret_cast<uint2*>(dst + (j & 3) * 256 + (j >> 2) * 8) = v[j];
+  }
 };
 
-template <class IT, int KP>
-__device__ __forceinline__ void fscan_body(const Args<IT>& a, int64_t lb, unsigned char* smem) {
-  using LL = FscanLds<KP>;
-  constexpr int rs = LL::rs, KH = KP / 2;
-  __bf16 *WrS = reinterpret_cast<__bf16*>(smem + LL::wr), *KtS = reinterpret_cast<__bf16*>(smem + LL::kt),
-         *StS = reinterpret_cast<__bf16*>(smem + LL::st), *VtS = reinterpret_cast<__bf16*>(smem + LL::vt);
-  float *SS = reinterpret_cast<float*>(smem + LL::ss), *US = reinterpret_cast<float*>(smem + LL::us),
-        *PS = reinterpret_cast<float*>(smem + LL::ps), *DS = reinterpret_cast<float*>(smem + LL::ds);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
-  const int half = w >> 2, wt = w & 3;
-  const int Vp = a.L.Vp, ncb = Vp / 16;
-  const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
-  const int col0 = 16 * static_cast<int>(lb % ncb);
-  for (int idx = tid; idx < KP * 16; idx += kST) {  // S0 and its split transpose
-    const int r = idx >> 4, cc = idx & 15;
-    const float x = (a.s0 != nullptr && r < a.K && col0 + cc < a.V) ? a.s0[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
-                                                                      : 0.f;
-    SS[r * kTS + cc] = x;
-    __bf16 hi, lo;
-    split_bf16(x, hi, lo);
-    StS[cc * rs + r] = hi;
-    StS[16 * rs + cc * rs + r] = lo;
-  }
-  FscanBuf pf;
-  fscan_fetch<IT, KP>(pf, a, bh, 0, col0, tid);
-  for (int64_t c = 0; c < a.NC; ++c) {
-    float* ws = a.ws + (bh * a.NC + c) * a.L.per;
-    split_to_lds<KP>(WrS, kC * rs, rs, KP, pf.w, tid);
-    split_to_lds<KP>(KtS, KP * kRSC, kRSC, kC, pf.k, tid);
+// A per-lane offset the compiler may not hoist out of the chunk loop: keeps
+// the many invariant per-lane addresses of the loop from occupying registers.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
+__device__ __forceinline__ bf16x8 frag_ld(const unsigned char* sm, int base, int f, int plane, int lane) {
+  return *reinterpret_cast<const bf16x8*>(sm + base + f * 2048 + plane * 1024 + lane * 16);
+}
+
+// rows 4g..4g+3 of two accumulator tiles as one split B operand
+__device__ __forceinline__ void split_pair(const f32x4& a, const f32x4& b, bf16x8& hi, bf16x8& lo) {
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {
-      const int idx = tid + kST * m;
-      US[(idx >> 4) * kTS + (idx & 15)] = pf.u[m];
-    }
-    if (tid < KP) DS[tid] = pf.d;
-    for (int idx = tid; idx < KP * 16; idx += kST) {  // the chunk's start state
-      const int r = idx >> 4, cc = idx & 15;
-      ws[a.L.S + r * Vp + col0 + cc] = SS[r * kTS + cc];
-    }
-    __syncthreads();
-    if (c + 1 < a.NC) fscan_fetch<IT, KP>(pf, a, bh, c + 1, col0, tid);
-    // W S over one half of the channels, rows 16 wt..
-    const f32x4 acc = mma3(zero4(), SMat{WrS + half * KH, kC * rs, rs}, 16 * wt, SMat{StS + half * KH, 16 * rs, rs}, 0,
-                           KH);
-    if (half == 1) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) PS[(16 * wt + 4 * lg4 + r) * kTS + li] = acc[r];
-    }
-    __syncthreads();
-    if (half == 0) {  // Vt = U - W S
-      f32x4 vt;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * wt + 4 * lg4 + r;
-        vt[r] = US[row * kTS + li] - acc[r] - PS[row * kTS + li];
-        ws[a.L.Vt + row * Vp + col0 + li] = vt[r];
-      }
-      store_split4(VtS, 16 * kRSC, kRSC, li, 16 * wt + 4 * lg4, vt);
-    }
-    __syncthreads();
-    if (w < KP / 16) {  // S <- D S + Kt^T Vt, row tile w
-      const f32x4 upd = mma3(zero4(), SMat{KtS, KP * kRSC, kRSC}, 16 * w, SMat{VtS, 16 * kRSC, kRSC}, 0, kC);
-      f32x4 sn;
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int row = 16 * w + 4 * lg4 + r;
-        sn[r] = DS[row] * SS[row * kTS + li] + upd[r];
-        SS[row * kTS + li] = sn[r];
-      }
-      store_split4(StS, 16 * rs, rs, li, 16 * w + 4 * lg4, sn);
-    }
-    __syncthreads();
-  }
-  if (a.sT != nullptr) {  // the final state (the forward through these kernels)
-    for (int idx = tid; idx < KP * 16; idx += kST) {
-      const int r = idx >> 4, cc = idx & 15;
-      if (r < a.K && col0 + cc < a.V) a.sT[((b * a.H + h) * a.K + r) * a.V + col0 + cc] = SS[r * kTS + cc];
-    }
+  for (int r = 0; r < 4; ++r) {
+    __bf16 h, l;
+    split_bf16(a[r], h, l);
+    hi[r] = h;
+    lo[r] = l;
+    split_bf16(b[r], h, l);
+    hi[4 + r] = h;
+    lo[4 + r] = l;
   }
 }
 
+__device__ __forceinline__ f32x4 mfma3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh, const bf16x8& bl,
+                                       f32x4 acc) {
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+  acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+}
+
+// dO of a chunk as the split B operand of the two position steps: lane (i, g)
+// element e of step s holds dO[t0 + 32 s + perm_k(g, e)][col]
 template <class IT>
-struct BscanBuf {
-  f32x4 k[kPF], q[kPF], w[kPF], a[2];
-  IT o[2];  // raw dO, split when written to LDS
-  float d;
+struct DoFrag {
+  IT x[2][8];
+  __device__ __forceinline__ void fetch(const Args<IT>& a, int64_t b, int64_t h, int64_t t0, int col, int g) {
+    const int cc = opaque(col < a.V ? col : static_cast<int>(a.V) - 1);
+    const IT* row0 = a.dout + tok(b, 0, a.T, a.H, h) * a.V + cc;
+    const int64_t step = a.H * a.V;
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        int64_t t = t0 + 32 * st + perm_k(g, e);
+        t = t < a.T ? t : a.T - 1;
+        x[st][e] = row0[t * step];
+      }
+  }
+  __device__ __forceinline__ void split(int64_t t0, int64_t T, int col, int64_t V, int g, bf16x8 (&hi)[2],
+                                        bf16x8 (&lo)[2]) const {
+#pragma unroll
+    for (int st = 0; st < 2; ++st)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const bool real = t0 + 32 * st + perm_k(g, e) < T && col < V;
+        __bf16 hh, ll;
+        split_bf16(real ? to_float(x[st][e]) : 0.f, hh, ll);
+        hi[st][e] = hh;
+        lo[st][e] = ll;
+      }
+  }
 };
 
-template <class IT, int KP>
-__device__ __forceinline__ void bscan_fetch(BscanBuf<IT>& p, const Args<IT>& a, int64_t bh, int64_t b, int64_t h,
-                                            int64_t c, int col0, int tid) {
-  const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
-  fetch_split<KP>(p.k, ws + a.L.Ktr, tid);
-  fetch_split<KP>(p.q, ws + a.L.Qgt, tid);
-  fetch_split<KP>(p.w, ws + a.L.Wt, tid);
-#pragma unroll
-  for (int m = 0; m < 2; ++m) p.a[m] = *reinterpret_cast<const f32x4*>(ws + a.L.Aqkt + 4 * (tid + kST * m));
-#pragma unroll
-  for (int m = 0; m < 2; ++m) {  // clamped into the tensor; masked when split
-    const int idx = tid + kST * m, r = idx >> 4, cc = idx & 15;
-    const int64_t t = c * kC + r < a.T ? c * kC + r : a.T - 1;
-    const int64_t col = col0 + cc < a.V ? col0 + cc : a.V - 1;
-    p.o[m] = a.dout[tok(b, t, a.T, a.H, h) * a.V + col];
-  }
-  if (tid < KP) p.d = ws[a.L.D + tid];
-}
+// Block kinds of seg_kernel: the value columns of a segment's map (Q), its
+// transition columns (P), or the rerun of a segment from its start state.
+constexpr int kSumV = 0, kSumT = 1, kRun = 2;
 
-// LDS of the backward scan (bytes)
-template <int KP>
-struct BscanLds {
-  static constexpr int rs = kRSP(KP);
-  static constexpr int kt = 0;                                  // Kt split [64][KP]
-  static constexpr int qg = kt + 2 * kC * rs * 2;               // Qg^T split [KP][64]
-  static constexpr int wt = qg + 2 * KP * kRSC * 2;             // W^T split [KP][64]
-  static constexpr int aq = wt + 2 * KP * kRSC * 2;             // Aqk^T split [64][64]
-  static constexpr int dst = aq + 2 * kC * kRSC * 2;            // dS^T split [16][KP]
-  static constexpr int dot = dst + 2 * 16 * rs * 2;             // dO^T split [16][64]
-  static constexpr int xt = dot + 2 * 16 * kRSC * 2;            // dVt^T split [16][64]
-  static constexpr int dss = xt + 2 * 16 * kRSC * 2;            // dS f32 [128][kTS]
-  static constexpr int ds = dss + 128 * kTS * 4;                // D f32 [128]
-  static constexpr int bytes = ds + 128 * 4;
-};
+template <class IT, int KP, int MODE, int DIR>
+__device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned char* sm) {
+  using SL = SegLds<KP>;
+  constexpr int NKT = KP / 16, NKS = KP / 32;
+  constexpr bool BWD = DIR == 1, TRANS = MODE == kSumT;
+  constexpr bool DO_TERMS = BWD && !TRANS;                            // Aqk^T dO and Qg^T dO
+  constexpr bool EXACT_DO = sizeof(IT) == 2 && !__is_same(IT, f16);  // bf16 dO: its lo part is zero
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g4 = lane >> 4;
+  const int nsb = MODE == kRun ? a.nseg : a.nseg - 1;
+  const int64_t bhn = a.B * a.H;
+  const int64_t bh = id / nsb, b = bh / a.H, h = bh % a.H;
+  const int gseg = static_cast<int>(id % nsb);
+  const int Vp = a.L.Vp;
+  const bool has = w < (TRANS ? NKT : Vp / 16);  // this wave's 16-column tile exists
+  const int col = 16 * w + li;                     // this lane's column (value or transition)
+  float* rec = a.seg + ((static_cast<int64_t>(DIR) * bhn + bh) * a.nseg + gseg) *
+                           (static_cast<int64_t>(KP) * KP + 2 * static_cast<int64_t>(KP) * Vp);
+  const int p0 = gseg * a.seglen;
+  const int p1 = p0 + a.seglen < a.NC ? p0 + a.seglen : static_cast<int>(a.NC);
 
-template <class IT, int KP>
-__device__ __forceinline__ void bscan_body(const Args<IT>& a, int64_t lb, unsigned char* smem) {
-  using LL = BscanLds<KP>;
-  constexpr int rs = LL::rs;
-  __bf16 *KtS = reinterpret_cast<__bf16*>(smem + LL::kt), *QgS = reinterpret_cast<__bf16*>(smem + LL::qg),
-         *WtS = reinterpret_cast<__bf16*>(smem + LL::wt), *AqS = reinterpret_cast<__bf16*>(smem + LL::aq),
-         *dStS = reinterpret_cast<__bf16*>(smem + LL::dst), *dOtS = reinterpret_cast<__bf16*>(smem + LL::dot),
-         *XtS = reinterpret_cast<__bf16*>(smem + LL::xt);
-  float *dSS = reinterpret_cast<float*>(smem + LL::dss), *DS = reinterpret_cast<float*>(smem + LL::ds);
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
-  const int Vp = a.L.Vp, ncb = Vp / 16;
-  const int64_t bh = lb / ncb, b = bh / a.H, h = bh % a.H;
-  const int col0 = 16 * static_cast<int>(lb % ncb);
-  for (int idx = tid; idx < KP * 16; idx += kST) {  // dS_T and its split transpose
-    const int r = idx >> 4, cc = idx & 15;
-    const float x = (a.dsT != nullptr && r < a.K && col0 + cc < a.V)
-                        ? a.dsT[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
-                        : 0.f;
-    dSS[r * kTS + cc] = x;
-    __bf16 hi, lo;
-    split_bf16(x, hi, lo);
-    dStS[cc * rs + r] = hi;
-    dStS[16 * rs + cc * rs + r] = lo;
+  f32x4 X[NKT];
+#pragma unroll
+  for (int ct = 0; ct < NKT; ++ct) {
+    X[ct] = zero4();
+    if constexpr (TRANS) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) X[ct][r] = (16 * ct + 4 * g4 + r == col) ? 1.f : 0.f;
+    } else if constexpr (MODE == kRun) {
+      if (has) {
+        const float* x0 = rec + KP * KP + KP * Vp + opaque(4 * g4 * Vp + col);  // start state from the combine
+#pragma unroll
+        for (int r = 0; r < 4; ++r) X[ct][r] = x0[(16 * ct + r) * Vp];
+      }
+    }
   }
-  BscanBuf<IT> pf;
-  bscan_fetch<IT, KP>(pf, a, bh, b, h, a.NC - 1, col0, tid);
-  for (int64_t c = a.NC - 1; c >= 0; --c) {
+
+  Rec<kC, KP> ra;   // forward W, backward Kt        [64][KP]
+  Rec<KP, kC> rb;   // forward Kt^T, backward W^T    [KP][64]
+  Rec<KP, kC> rq;   // backward Qg^T
+  Rec<kC, kC> raq;  // backward Aqk^T
+  float dval = 0.f;
+  float u[4][4];    // forward value columns: U of the next chunk, accumulator layout
+  DoFrag<IT> dof;   // backward value columns: dO of the next chunk
+  auto chunk_of = [&](int p) -> int64_t { return BWD ? a.NC - 1 - p : p; };
+  auto fetch = [&](int p) {
+    const int64_t c = chunk_of(p);
+    const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
+    if constexpr (!BWD) {
+      ra.fetch(ws + a.L.Wr, tid);
+      rb.fetch(ws + a.L.Ktt, tid);
+      if (!TRANS && has) {
+        const float* up = ws + a.L.U + opaque(4 * g4 * Vp + col);
+#pragma unroll
+        for (int I = 0; I < 4; ++I)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) u[I][r] = up[(16 * I + r) * Vp];
+      }
+    } else {
+      ra.fetch(ws + a.L.Ktr, tid);
+      rb.fetch(ws + a.L.Wt, tid);
+      if constexpr (DO_TERMS) {
+        rq.fetch(ws + a.L.Qgt, tid);
+        raq.fetch(ws + a.L.Aqkt, tid);
+        if (has) dof.fetch(a, b, h, c * kC, col, g4);
+      }
+    }
+    if (tid < KP) dval = ws[a.L.D + tid];
+  };
+  if (p0 < p1) fetch(p0);
+  for (int p = p0; p < p1; ++p) {
+    const int64_t c = chunk_of(p), t0 = c * kC;
     float* ws = a.ws + (bh * a.NC + c) * a.L.per;
-    split_to_lds<KP>(KtS, kC * rs, rs, KP, pf.k, tid);
-    split_to_lds<KP>(QgS, KP * kRSC, kRSC, kC, pf.q, tid);
-    split_to_lds<KP>(WtS, KP * kRSC, kRSC, kC, pf.w, tid);
-#pragma unroll
-    for (int m = 0; m < 2; ++m) {  // Aqk^T: 2 x 4096 bf16 = 1024 f32x4
-      const int f = 8 * (tid + kST * m), pl = f / (kC * kC), e = f % (kC * kC);
-      *reinterpret_cast<f32x4*>(AqS + pl * kC * kRSC + (e >> 6) * kRSC + (e & 63)) = pf.a[m];
+    __syncthreads();  // the previous chunk's fragments are no longer read
+    ra.store(sm, SL::fa, tid);
+    rb.store(sm, SL::fb, tid);
+    if constexpr (DO_TERMS) {
+      rq.store(sm, SL::fq, tid);
+      raq.store(sm, SL::faq, tid);
     }
+    if (tid < KP) reinterpret_cast<float*>(sm + SL::d)[tid] = dval;
+    float uc[4][4];
+    bf16x8 doh[2], dol[2];
+    if (!TRANS && has) {
+      if constexpr (!BWD) {
 #pragma unroll
-    for (int m = 0; m < 2; ++m) {  // dO^T split
-      const int idx = tid + kST * m, r = idx >> 4, cc = idx & 15;
-      const bool real = c * kC + r < a.T && col0 + cc < a.V;
-      __bf16 hi, lo;
-      split_bf16(real ? to_float(pf.o[m]) : 0.f, hi, lo);
-      dOtS[cc * kRSC + r] = hi;
-      dOtS[16 * kRSC + cc * kRSC + r] = lo;
-    }
-    if (tid < KP) DS[tid] = pf.d;
-    for (int idx = tid; idx < KP * 16; idx += kST) {  // gradient of the chunk's end state
-      const int r = idx >> 4, cc = idx & 15;
-      ws[a.L.dS + r * Vp + col0 + cc] = dSS[r * kTS + cc];
-    }
-    __syncthreads();
-    if (c > 0) bscan_fetch<IT, KP>(pf, a, bh, b, h, c - 1, col0, tid);
-    f32x4 dsp[2];
-    if (w < 4) {  // dVt = Kt dS + Aqk^T dO, rows 16w..
-      f32x4 acc = mma3(zero4(), SMat{KtS, kC * rs, rs}, 16 * w, SMat{dStS, 16 * rs, rs}, 0, KP);
-      acc = mma3(acc, SMat{AqS, kC * kRSC, kRSC}, 16 * w, SMat{dOtS, 16 * kRSC, kRSC}, 0, kC);
+        for (int I = 0; I < 4; ++I)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) ws[a.L.dVt + (16 * w + 4 * lg4 + r) * Vp + col0 + li] = acc[r];
-      store_split4(XtS, 16 * kRSC, kRSC, li, 16 * w + 4 * lg4, acc);
-    } else {  // D dS + Qg^T dO, row tiles w-4 and w
-#pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int rt = w - 4 + 4 * j;
-        if (rt < KP / 16) {
-          const f32x4 p = mma3(zero4(), SMat{QgS, KP * kRSC, kRSC}, 16 * rt, SMat{dOtS, 16 * kRSC, kRSC}, 0, kC);
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = 16 * rt + 4 * lg4 + r;
-            dsp[j][r] = DS[row] * dSS[row * kTS + li] + p[r];
-          }
-        }
+          for (int r = 0; r < 4; ++r) uc[I][r] = u[I][r];
+      } else {
+        dof.split(t0, a.T, col, a.V, g4, doh, dol);
       }
     }
     __syncthreads();
-    if (w >= 4) {  // dS = dsp - W^T dVt
+    if (p + 1 < p1) fetch(p + 1);
+    if (!has) continue;  // no barrier below: idle waves go straight to the next chunk's barrier
+
+    // P = B X (forward B = W, backward B = Kt), plus Aqk^T dO (backward value
+    // columns); one fragment pair ahead
+    f32x4 P[4];
 #pragma unroll
-      for (int j = 0; j < 2; ++j) {
-        const int rt = w - 4 + 4 * j;
-        if (rt < KP / 16) {
-          const f32x4 n = mma3(zero4(), SMat{WtS, KP * kRSC, kRSC}, 16 * rt, SMat{XtS, 16 * kRSC, kRSC}, 0, kC);
-          f32x4 dn;
+    for (int I = 0; I < 4; ++I) P[I] = zero4();
+    {
+      bf16x8 xh[NKS], xl[NKS];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int row = 16 * rt + 4 * lg4 + r;
-            dn[r] = dsp[j][r] - n[r];
-            dSS[row * kTS + li] = dn[r];
-          }
-          store_split4(dStS, 16 * rs, rs, li, 16 * rt + 4 * lg4, dn);
+      for (int st = 0; st < NKS; ++st) split_pair(X[2 * st], X[2 * st + 1], xh[st], xl[st]);
+      bf16x8 fh[2], fl[2];
+      fh[0] = frag_ld(sm, SL::fa, 0, 0, lane);
+      fl[0] = frag_ld(sm, SL::fa, 0, 1, lane);
+#pragma unroll
+      for (int k = 0; k < 4 * NKS; ++k) {  // k = I * NKS + st: fragment (I, st)
+        if (k + 1 < 4 * NKS) {
+          fh[(k + 1) & 1] = frag_ld(sm, SL::fa, k + 1, 0, lane);
+          fl[(k + 1) & 1] = frag_ld(sm, SL::fa, k + 1, 1, lane);
+        }
+        P[k / NKS] = mfma3(fh[k & 1], fl[k & 1], xh[k % NKS], xl[k % NKS], P[k / NKS]);
+      }
+    }
+    if constexpr (DO_TERMS) {
+      bf16x8 fh[2], fl[2];
+      fh[0] = frag_ld(sm, SL::faq, 0, 0, lane);
+      fl[0] = frag_ld(sm, SL::faq, 0, 1, lane);
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {  // k = I * 2 + st
+        if (k + 1 < 8) {
+          fh[(k + 1) & 1] = frag_ld(sm, SL::faq, k + 1, 0, lane);
+          fl[(k + 1) & 1] = frag_ld(sm, SL::faq, k + 1, 1, lane);
+        }
+        if constexpr (EXACT_DO) {
+          P[k / 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh[k & 1], doh[k & 1], P[k / 2], 0, 0, 0);
+          P[k / 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl[k & 1], doh[k & 1], P[k / 2], 0, 0, 0);
+        } else {
+          P[k / 2] = mfma3(fh[k & 1], fl[k & 1], doh[k & 1], dol[k & 1], P[k / 2]);
         }
       }
     }
-    __syncthreads();
+    // R = U - P (forward value columns) or -P
+#pragma unroll
+    for (int I = 0; I < 4; ++I)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) P[I][r] = (!BWD && !TRANS ? uc[I][r] : 0.f) - P[I][r];
+    if constexpr (MODE == kRun) {  // this chunk's X and R (the backward stores dVt = -R)
+      const int lo = opaque(4 * g4 * Vp + col);
+      float* xo = ws + (BWD ? a.L.dS : a.L.S) + lo;
+      float* ro = ws + (BWD ? a.L.dVt : a.L.Vt) + lo;
+#pragma unroll
+      for (int ct = 0; ct < NKT; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) xo[(16 * ct + r) * Vp] = X[ct][r];
+#pragma unroll
+      for (int I = 0; I < 4; ++I)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) ro[(16 * I + r) * Vp] = BWD ? -P[I][r] : P[I][r];
+    }
+    // X' = D X + A^T R (forward A = Kt, backward A = W), plus Qg^T dO
+    // (backward value columns); one fragment pair ahead
+    bf16x8 rh[2], rl[2];
+#pragma unroll
+    for (int st = 0; st < 2; ++st) split_pair(P[2 * st], P[2 * st + 1], rh[st], rl[st]);
+    const float* Ds = reinterpret_cast<const float*>(sm + SL::d);
+#pragma unroll
+    for (int ct = 0; ct < NKT; ++ct) X[ct] *= *reinterpret_cast<const f32x4*>(Ds + 16 * ct + 4 * g4);
+    {
+      bf16x8 fh[2], fl[2];
+      fh[0] = frag_ld(sm, SL::fb, 0, 0, lane);
+      fl[0] = frag_ld(sm, SL::fb, 0, 1, lane);
+#pragma unroll
+      for (int k = 0; k < 2 * NKT; ++k) {  // k = ct * 2 + st
+        if (k + 1 < 2 * NKT) {
+          fh[(k + 1) & 1] = frag_ld(sm, SL::fb, k + 1, 0, lane);
+          fl[(k + 1) & 1] = frag_ld(sm, SL::fb, k + 1, 1, lane);
+        }
+        X[k / 2] = mfma3(fh[k & 1], fl[k & 1], rh[k & 1], rl[k & 1], X[k / 2]);
+      }
+    }
+    if constexpr (DO_TERMS) {
+      bf16x8 fh[2], fl[2];
+      fh[0] = frag_ld(sm, SL::fq, 0, 0, lane);
+      fl[0] = frag_ld(sm, SL::fq, 0, 1, lane);
+#pragma unroll
+      for (int k = 0; k < 2 * NKT; ++k) {
+        if (k + 1 < 2 * NKT) {
+          fh[(k + 1) & 1] = frag_ld(sm, SL::fq, k + 1, 0, lane);
+          fl[(k + 1) & 1] = frag_ld(sm, SL::fq, k + 1, 1, lane);
+        }
+        if constexpr (EXACT_DO) {
+          X[k / 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh[k & 1], doh[k & 1], X[k / 2], 0, 0, 0);
+          X[k / 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl[k & 1], doh[k & 1], X[k / 2], 0, 0, 0);
+        } else {
+          X[k / 2] = mfma3(fh[k & 1], fl[k & 1], doh[k & 1], dol[k & 1], X[k / 2]);
+        }
+      }
+    }
   }
-  if (a.ds0 != nullptr) {
-    for (int idx = tid; idx < KP * 16; idx += kST) {
-      const int r = idx >> 4, cc = idx & 15;
-      if (r < a.K && col0 + cc < a.V) a.ds0[((b * a.H + h) * a.K + r) * a.V + col0 + cc] = dSS[r * kTS + cc];
+  if (!has) return;
+  if constexpr (MODE != kRun) {  // the segment's map: P (transition columns) or Q (value columns)
+    float* dst = TRANS ? rec + opaque(4 * g4 * KP + col) : rec + KP * KP + opaque(4 * g4 * Vp + col);
+    const int ld = TRANS ? KP : Vp;
+#pragma unroll
+    for (int ct = 0; ct < NKT; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) dst[(16 * ct + r) * ld] = X[ct][r];
+  } else if (gseg == a.nseg - 1 && col < a.V) {  // the final state
+    float* fin = BWD ? a.ds0 : a.sT;
+    if (fin != nullptr) {
+#pragma unroll
+      for (int ct = 0; ct < NKT; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * ct + 4 * g4 + r;
+          if (row < a.K) fin[((b * a.H + h) * a.K + row) * a.V + col] = X[ct][r];
+        }
     }
   }
 }
 
-// ---- scan_kernel: both state scans in one launch -------------------------------
-// The backward scan needs only the chunk operands and dO, not the forward
-// scan's states, so the two run side by side: logical blocks [0, n) carry the
-// forward scan and [n, 2n) the backward one (n = heads x column blocks), each
-// XCD owning a contiguous range so the column blocks of a head share its L2.
-template <class IT, int KP>
-__global__ __launch_bounds__(kST) void scan_kernel(const Args<IT> a) {
-  constexpr int bytes = FscanLds<KP>::bytes > BscanLds<KP>::bytes ? FscanLds<KP>::bytes : BscanLds<KP>::bytes;
-  __shared__ __attribute__((aligned(16))) unsigned char smem[bytes];
-  const int64_t lb = xcd_block(blockIdx.x, gridDim.x), n = gridDim.x / 2;
-  if (lb < n)
-    fscan_body<IT, KP>(a, lb, smem);
+// Blocks [0, n) run direction dir0, blocks [n, 2n) (when ndir == 2) the
+// backward direction: the two directions are independent and share the launch,
+// each in its own inlined body (registers are those of the larger one).
+template <class IT, int KP, int MODE>
+__global__ __launch_bounds__(kSC) void seg_kernel(const Args<IT> a) {
+  __shared__ __attribute__((aligned(16))) unsigned char sm[SegLds<KP>::bytes];
+  const int64_t n = a.B * a.H * (MODE == kRun ? a.nseg : a.nseg - 1);
+  const int64_t id = blockIdx.x;
+  if (a.dir0 == 0 && id < n)
+    seg_body<IT, KP, MODE, 0>(a, id, sm);
   else
-    bscan_body<IT, KP>(a, lb - n, smem);
+    seg_body<IT, KP, MODE, 1>(a, id - (a.dir0 == 0 ? n : 0), sm);
+}
+
+// X_0 = the initial value (forward S0, backward dS_T; zero when absent), then
+// X_{g+1} = P_g X_g + Q_g for each segment in scan order, one block per
+// (direction, sequence x head, 16 value columns), f32 MFMA; the next
+// segment's P and Q are loaded while the current one multiplies.
+constexpr int kCT = 256;
+template <class IT, int KP, int DIR>
+__device__ __forceinline__ void combine_body(const Args<IT>& a, int64_t id, float* Ps, float* Xs) {
+  constexpr int PS = KP + 4, XS = 20, NP = KP * KP / 4 / kCT;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g4 = lane >> 4;
+  const int Vp = a.L.Vp, nv = Vp / 16;
+  const int64_t bhn = a.B * a.H;
+  const int64_t bh = id / nv, b = bh / a.H, h = bh % a.H;
+  const int col0 = 16 * static_cast<int>(id % nv);
+  const int64_t segf = static_cast<int64_t>(KP) * KP + 2 * static_cast<int64_t>(KP) * Vp;
+  float* base = a.seg + (static_cast<int64_t>(DIR) * bhn + bh) * a.nseg * segf;
+  const float* init = DIR == 1 ? a.dsT : a.s0;
+  for (int idx = tid; idx < KP * 16; idx += kCT) {
+    const int r = idx >> 4, cc = idx & 15;
+    const float x = (init != nullptr && r < a.K && col0 + cc < a.V) ? init[((b * a.H + h) * a.K + r) * a.V + col0 + cc]
+                                                                     : 0.f;
+    Xs[r * XS + cc] = x;
+    base[KP * KP + KP * Vp + r * Vp + col0 + cc] = x;
+  }
+  f32x4 pf[NP];
+  float qf[2][4];
+  auto fetch = [&](int gs) {
+    const float* P = base + gs * segf;
+#pragma unroll
+    for (int j = 0; j < NP; ++j) pf[j] = *reinterpret_cast<const f32x4*>(P + 4 * (tid + kCT * j));
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < KP / 16) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) qf[j][r] = P[KP * KP + (16 * rt + 4 * g4 + r) * Vp + col0 + li];
+      }
+    }
+  };
+  if (a.nseg > 1) fetch(0);
+  for (int gs = 0; gs + 1 < a.nseg; ++gs) {
+    float* Xn = base + (gs + 1) * segf + KP * KP + KP * Vp;
+    __syncthreads();  // the previous step's reads of P are done
+#pragma unroll
+    for (int j = 0; j < NP; ++j) {
+      const int e = 4 * (tid + kCT * j);
+      *reinterpret_cast<f32x4*>(&Ps[(e / KP) * PS + e % KP]) = pf[j];
+    }
+    f32x4 acc[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) acc[j][r] = qf[j][r];
+    __syncthreads();
+    if (gs + 2 < a.nseg) fetch(gs + 1);
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < KP / 16) acc[j] = mma_long(acc[j], Mat{Ps, PS, 1}, 16 * rt, Mat{Xs, XS, 1}, 0, KP);
+    }
+    __syncthreads();  // every read of X_g is done
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int rt = w + 4 * j;
+      if (rt < KP / 16) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = 16 * rt + 4 * g4 + r;
+          Xs[row * XS + li] = acc[j][r];
+          Xn[row * Vp + col0 + li] = acc[j][r];
+        }
+      }
+    }
+  }
+}
+
+template <class IT, int KP>
+__global__ __launch_bounds__(kCT) void seg_combine_kernel(const Args<IT> a) {
+  __shared__ float Ps[KP * (KP + 4)];
+  __shared__ float Xs[KP * 20];
+  const int64_t n = a.B * a.H * (a.L.Vp / 16);
+  const int64_t id = blockIdx.x;
+  if (a.dir0 == 0 && id < n)
+    combine_body<IT, KP, 0>(a, id, Ps, Xs);
+  else
+    combine_body<IT, KP, 1>(a, id - (a.dir0 == 0 ? n : 0), Ps, Xs);
+}
+
+// Chunks per segment and segments per sequence: enough blocks (over the
+// ndir directions that share a launch) to cover the GPU's 256 CUs.
+__host__ __device__ inline int64_t seg_len(int64_t bh, int64_t NC, int ndir) {
+  int64_t want = (256 + ndir * bh - 1) / (ndir * bh);
+  if (want < 1) want = 1;
+  if (want > NC) want = NC;
+  return NC > 0 ? (NC + want - 1) / want : 1;
+}
+__host__ __device__ inline int seg_count(int64_t bh, int64_t NC, int ndir) {
+  const int64_t len = seg_len(bh, NC, ndir);
+  return static_cast<int>((NC + len - 1) / len);
+}
+
+// Segment records of ndir directions: P [KP][KP], Q and the start state [KP][Vp].
+__host__ __device__ inline int64_t seg_floats(int64_t K, int64_t V, int64_t bh, int64_t NC, int ndir) {
+  const Layout L = make_layout(K, V);
+  return static_cast<int64_t>(ndir) * bh * seg_count(bh, NC, ndir) *
+         (static_cast<int64_t>(L.Kp) * L.Kp + 2 * static_cast<int64_t>(L.Kp) * L.Vp);
 }
 
 // ---- the forward through the same chunk operands ------------------------------
-// prep_kernel, then fscan_kernel (the forward scan alone, which leaves each
-// chunk's start state S and pseudo-values Vt in the workspace and writes the
-// final state), then out_kernel: O = Qg S + Aqk Vt per chunk, all chunks in
-// parallel.  This is the chunkwise prefill for inputs the bf16 MFMA path does
-// not take (f32 inputs, key or value dims off its grid), at the split-bf16
-// accuracy of the scans.
-template <class IT, int KP>
-__global__ __launch_bounds__(kST) void fscan_kernel(const Args<IT> a) {
-  __shared__ __attribute__((aligned(16))) unsigned char smem[FscanLds<KP>::bytes];
-  fscan_body<IT, KP>(a, xcd_block(blockIdx.x, gridDim.x), smem);
-}
-
+// prep_kernel, then the forward scan alone (which leaves each chunk's start
+// state S and pseudo-values Vt in the workspace and writes the final state),
+// then out_kernel: O = Qg S + Aqk Vt per chunk, all chunks in parallel.  This
+// is the chunkwise prefill for inputs the bf16 MFMA path does not take (f32
+// inputs, key or value dims off its grid), at the split-bf16 accuracy of the
+// scans.
 constexpr int kOT = 512;  // threads of out_kernel: one 16 x 16 output tile per wave and slab
 template <class IT, int KP>
 __global__ __launch_bounds__(kOT) void out_kernel(const Args<IT> a) {
@@ -1477,7 +1616,6 @@ __global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
   const int64_t t0 = c * kC;
-  constexpr int Kp = KP;
   const float* ws = a.ws + ch * a.L.per;
   load_rows<IT, KP, kRS, NT>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid);
   load_rows<IT, KP, kRS, NT>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid);
@@ -1527,7 +1665,8 @@ using namespace kda;
 size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
   const bwd::Layout L = bwd::make_layout(K, V);
   const int64_t nc = (T + bwd::kC - 1) / bwd::kC;
-  const size_t f32 = static_cast<size_t>(B * H * nc * L.per) * sizeof(float);
+  const size_t f32 =
+      static_cast<size_t>(B * H * nc * L.per + bwd::seg_floats(K, V, B * H, nc, 2)) * sizeof(float);
   const size_t f64 = chunk_bwd_f64_workspace_bytes(B, T, H, K, V);  // one size serves every dtype
   return f32 > f64 ? f32 : f64;
 }
@@ -1535,7 +1674,34 @@ size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int
 size_t chunk_split_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
   const bwd::Layout L = bwd::make_layout(K, V);
   const int64_t nc = (T + bwd::kC - 1) / bwd::kC;
-  return static_cast<size_t>(B * H * nc * L.per) * sizeof(float);
+  return static_cast<size_t>(B * H * nc * L.per + bwd::seg_floats(K, V, B * H, nc, 1)) * sizeof(float);
+}
+
+// The segment geometry and records of the scans (after the chunk records).
+// The scans of directions 0 .. ndir - 1 (forward, then backward) share
+// their launches.
+template <class IT>
+static void set_segments(bwd::Args<IT>& a, int ndir) {
+  a.dir0 = 0;
+  a.ndir = ndir;
+  a.seglen = static_cast<int>(bwd::seg_len(a.B * a.H, a.NC, ndir));
+  a.nseg = bwd::seg_count(a.B * a.H, a.NC, ndir);
+  a.seg = a.ws + a.B * a.H * a.NC * a.L.per;
+}
+
+// Both phases and the combine of the segmented scans.
+template <class IT, int KP>
+static void launch_scans(const bwd::Args<IT>& a, hipStream_t s) {
+  const int64_t bh = a.B * a.H * a.ndir;
+  if (a.nseg > 1) {
+    const dim3 g(static_cast<unsigned>(bh * (a.nseg - 1)));
+    hipLaunchKernelGGL((bwd::seg_kernel<IT, KP, bwd::kSumV>), g, dim3(bwd::kSC), 0, s, a);
+    hipLaunchKernelGGL((bwd::seg_kernel<IT, KP, bwd::kSumT>), g, dim3(bwd::kSC), 0, s, a);
+  }
+  hipLaunchKernelGGL((bwd::seg_combine_kernel<IT, KP>), dim3(static_cast<unsigned>(bh * (a.L.Vp / 16))),
+                     dim3(bwd::kCT), 0, s, a);
+  hipLaunchKernelGGL((bwd::seg_kernel<IT, KP, bwd::kRun>), dim3(static_cast<unsigned>(bh * a.nseg)), dim3(bwd::kSC),
+                     0, s, a);
 }
 
 bool chunk_split_path(int in_dtype, int state_dtype, int64_t K, int64_t V) {
@@ -1544,9 +1710,9 @@ bool chunk_split_path(int in_dtype, int state_dtype, int64_t K, int64_t V) {
 }
 
 template <class IT, int KP>
-static void launch_split(const bwd::Args<IT>& a, dim3 chunks, dim3 scans, hipStream_t s) {
+static void launch_split(const bwd::Args<IT>& a, dim3 chunks, hipStream_t s) {
   hipLaunchKernelGGL((bwd::prep_kernel<IT, KP>), chunks, dim3(bwd::kPT), 0, s, a);
-  hipLaunchKernelGGL((bwd::fscan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
+  launch_scans<IT, KP>(a, s);
   hipLaunchKernelGGL((bwd::out_kernel<IT, KP>), chunks, dim3(bwd::kOT), 0, s, a);
 }
 
@@ -1559,16 +1725,17 @@ static int run_split(const IT* q, const IT* k, const IT* v, const IT* g, const I
   a.ws = ws, a.B = B, a.T = T, a.H = H, a.K = K, a.V = V, a.NC = (T + bwd::kC - 1) / bwd::kC;
   a.L = bwd::make_layout(K, V);
   a.valid = valid, a.sT = sT, a.out = out;
-  const int64_t chunks = B * H * a.NC, scans = B * H * (a.L.Vp / 16);
-  if (chunks > 0x7fffffffLL || scans > 0x7fffffffLL) {
+  set_segments(a, 1);
+  const int64_t chunks = B * H * a.NC;
+  if (chunks > 0x7fffffffLL || B * H * a.nseg > 0x7fffffffLL || B * H * (a.L.Vp / 16) > 0x7fffffffLL) {
     set_detail("chunk_fwd: grid too large");
     return KDA_ERR_UNSUPPORTED;
   }
-  const dim3 gc(static_cast<unsigned>(chunks)), gs(static_cast<unsigned>(scans));
+  const dim3 gc(static_cast<unsigned>(chunks));
   if (a.L.Kp == 64)
-    launch_split<IT, 64>(a, gc, gs, s);
+    launch_split<IT, 64>(a, gc, s);
   else
-    launch_split<IT, 128>(a, gc, gs, s);
+    launch_split<IT, 128>(a, gc, s);
   return check_launch("chunk_fwd (split-bf16 chunk path)");
 }
 
@@ -1605,26 +1772,26 @@ int launch_chunk_split(const void* q, const void* k, const void* v, const void* 
 }
 
 template <class IT, int KP>
-static void launch_all(const bwd::Args<IT>& a, dim3 chunks, dim3 scans, hipStream_t s) {
+static void launch_all(const bwd::Args<IT>& a, dim3 chunks, hipStream_t s) {
   hipLaunchKernelGGL((bwd::prep_kernel<IT, KP>), chunks, dim3(bwd::kPT), 0, s, a);
-  hipLaunchKernelGGL((bwd::scan_kernel<IT, KP>), scans, dim3(bwd::kST), 0, s, a);
+  launch_scans<IT, KP>(a, s);
   hipLaunchKernelGGL((bwd::grad_kernel<IT, KP>), chunks, dim3(512), 0, s, a);
   hipLaunchKernelGGL((bwd::pair_kernel<IT, KP, 512>), chunks, dim3(512), 0, s, a);
 }
 
 template <class IT>
-static int run_bwd(const bwd::Args<IT>& a, hipStream_t s) {
+static int run_bwd(bwd::Args<IT> a, hipStream_t s) {
+  set_segments(a, 2);
   const int64_t chunks = a.B * a.H * a.NC;
-  const int64_t scans = 2 * a.B * a.H * (a.L.Vp / 16);  // forward and backward scan blocks
-  if (chunks > 0x7fffffffLL || scans > 0x7fffffffLL) {
+  if (chunks > 0x7fffffffLL || 2 * a.B * a.H * a.nseg > 0x7fffffffLL || 2 * a.B * a.H * (a.L.Vp / 16) > 0x7fffffffLL) {
     set_detail("chunk backward: grid too large");
     return KDA_ERR_UNSUPPORTED;
   }
-  const dim3 gc(static_cast<unsigned>(chunks)), gs(static_cast<unsigned>(scans));
+  const dim3 gc(static_cast<unsigned>(chunks));
   if (a.L.Kp == 64)
-    launch_all<IT, 64>(a, gc, gs, s);
+    launch_all<IT, 64>(a, gc, s);
   else
-    launch_all<IT, 128>(a, gc, gs, s);
+    launch_all<IT, 128>(a, gc, s);
   return check_launch("chunk backward");
 }
 
