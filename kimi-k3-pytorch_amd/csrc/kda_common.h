@@ -60,6 +60,31 @@ __device__ __forceinline__ C lower_bounded_decay(C z, C b, C scale, C g_min, C l
   return g;
 }
 
+// Sum over aligned groups of G consecutive lanes (G a power of two <= 64).
+// In f32 the steps inside a 16-lane row are DPP moves fused into the adds
+// (quad permutations [1,0,3,2] and [2,3,0,1], then the half-row and row
+// mirrors, each of which pairs the lane with one holding the other half's
+// partial sum); wider groups and f64 use the LDS crossbar (__shfl_xor).
+template <int ctrl>
+__device__ __forceinline__ float dpp_add(float v) {
+  return v + __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), ctrl, 0xf, 0xf, false));
+}
+
+template <int G, class C>
+__device__ __forceinline__ C group_sum(C v) {
+  int off = 1;
+  if constexpr (sizeof(C) == 4) {
+    if constexpr (G >= 2) v = dpp_add<0xb1>(v);   // quad_perm [1,0,3,2]: lane ^ 1
+    if constexpr (G >= 4) v = dpp_add<0x4e>(v);   // quad_perm [2,3,0,1]: lane ^ 2
+    if constexpr (G >= 8) v = dpp_add<0x141>(v);  // row_half_mirror: the other quad of the 8
+    if constexpr (G >= 16) v = dpp_add<0x140>(v); // row_mirror: the other half of the row
+    off = G < 16 ? G : 16;
+  }
+#pragma unroll
+  for (; off < G; off <<= 1) v += __shfl_xor(v, off);
+  return v;
+}
+
 // ---- sequences ------------------------------------------------------------
 // A "sequence" is a run of tokens that share one recurrent state: a batch row
 // of a dense [B,T,...] call (start = s*T) or a packed document

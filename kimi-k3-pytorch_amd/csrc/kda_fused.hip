@@ -35,14 +35,6 @@ struct Vec {
   typedef T type __attribute__((ext_vector_type(VEC)));
 };
 
-// Sum over aligned groups of G consecutive lanes (G a power of two <= 64).
-template <int G, class C>
-__device__ __forceinline__ C group_sum(C v) {
-#pragma unroll
-  for (int off = 1; off < G; off <<= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
 // ---- ShortConv + SiLU (+ L2 normalisation per head) -------------------------
 // Reference: CausalShortConv1D (src/kimi_primitives/short_conv.py:69-98:
 // weight[c, j] multiplies x[t - j]; the history holds the last K-1 inputs,
@@ -51,15 +43,17 @@ __device__ __forceinline__ C group_sum(C v) {
 // the padding never enters the history), then F.silu and, for q and k,
 // F.normalize(p=2, dim=-1, eps) per head (projections.py:185-204).
 //
-// One wave per (batch row, block of 64*VEC channels, tile of 8 tokens).  Lane l owns the VEC channels blk*64*VEC + VEC*l .. (one 16-byte
-// load per token); the wave issues the loads of its whole tile and of the K-1
-// rows before it at once, then forms each token from registers.  With
-// normalisation a head is an aligned group of G = head_dim / VEC lanes, and
-// its sum of squares a G-lane reduction.
+// One wave per (batch row, block of 64*VEC channels, tile of 16 tokens).
+// Lane l owns the VEC channels blk*64*VEC + VEC*l .. (one 16-byte load per
+// token).  The wave streams its tile: eight rows in flight ahead of the one
+// it forms, the K-1 rows before it in a register window, one store per row,
+// so its loads, arithmetic and stores overlap.  With normalisation a head is
+// an aligned group of G = head_dim / VEC lanes, and its sum of squares a
+// G-lane reduction.
 constexpr int kMaxConvK = 8;
 
-// tokens per wave: 8, or 4 when a lane's vector is wider than 16 bytes
-__host__ __device__ constexpr int conv_tile(int vec_bytes) { return vec_bytes > 16 ? 4 : 8; }
+// tokens per wave: 16, or 4 when a lane's vector is wider than 16 bytes
+__host__ __device__ constexpr int conv_tile(int vec_bytes) { return vec_bytes > 16 ? 4 : 16; }
 
 template <class T>
 struct ConvArgs {
@@ -82,42 +76,38 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const ConvArgs<T> a) {
   using C = typename ComputeOf<T>::type;
   typedef typename Vec<T, VEC>::type vec_t;
   constexpr int TT = conv_tile(VEC * sizeof(T));
+  constexpr int D = TT < 8 ? TT : 8;              // rows in flight ahead of the one being formed
   constexpr int KMAX = KT > 0 ? KT : kMaxConvK;  // taps held in registers
   const int lane = threadIdx.x & 63;
-  const int64_t wave = xcd_block(blockIdx.x, gridDim.x) * 4 + (threadIdx.x >> 6);
+  // the wave's tile, batch row and channel block are scalars (the wave index
+  // read through readfirstlane), so row addresses are a scalar base plus the
+  // lane's 32-bit channel offset
+  const int64_t wave = xcd_block(blockIdx.x, gridDim.x) * 4 + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int64_t nblk = (a.nc + 64 * VEC - 1) / (64 * VEC);
   const int64_t ntile = (a.nt + TT - 1) / TT;
   if (wave >= a.nb * nblk * ntile) return;  // uniform over the wave
   const int64_t tile = wave % ntile;
   const int64_t blk = (wave / ntile) % nblk;
   const int64_t b = wave / (ntile * nblk);
-  const int64_t c0 = (blk * 64 + lane) * VEC;
+  const int c0 = static_cast<int>(blk * 64 * VEC) + lane * VEC;
   const bool on = c0 < a.nc;  // lanes past the last channel only join the reductions
   int64_t len = a.nt;
   if (a.valid_lens != nullptr) {
-    const int64_t vl = a.valid_lens[b];
+    const int vl = __builtin_amdgcn_readfirstlane(a.valid_lens[b]);
     len = vl < 0 ? 0 : (vl < a.nt ? vl : a.nt);
   }
   const int K = KT > 0 ? KT : a.K;
   const int H1 = K - 1;
   const int64_t t0 = tile * TT;
   const vec_t zero = {};
+  const T* xb = a.x + b * a.nt * a.nc;  // uniform
   auto row = [&](const T* base, int64_t r) -> vec_t { return *reinterpret_cast<const vec_t*>(base + r * a.nc + c0); };
-  // the tile's inputs and the K-1 before it (position t0 - 1 - j), zero past len
-  vec_t xv[TT], pv[KMAX > 1 ? KMAX - 1 : 1];
-#pragma unroll
-  for (int i = 0; i < TT; ++i) xv[i] = (on && t0 + i < len) ? row(a.x, b * a.nt + t0 + i) : zero;
-#pragma unroll
-  for (int j = 0; j < KMAX - 1; ++j) {
-    const int64_t p = t0 - 1 - j;
-    pv[j] = zero;
-    if (on && j < H1) {
-      if (p >= 0)
-        pv[j] = p < len ? row(a.x, b * a.nt + p) : zero;
-      else if (a.hist_in != nullptr)
-        pv[j] = row(a.hist_in, b * H1 + H1 + p);
-    }
-  }
+  // row t of x for t < nt (the address clamped into the row's span; the
+  // caller masks what lies past the valid prefix), so the loads of the ring
+  // are unconditional and their waits exact; streamed data, so non-temporal
+  auto ld = [&](int64_t t) -> vec_t {
+    return __builtin_nontemporal_load(reinterpret_cast<const vec_t*>(xb + (t < a.nt ? t : a.nt - 1) * a.nc + c0));
+  };
   C wr[KMAX][VEC];
   C br[VEC];
   if constexpr (KT > 0) {
@@ -137,21 +127,54 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const ConvArgs<T> a) {
   }
 #pragma unroll
   for (int e = 0; e < VEC; ++e) br[e] = (on && a.bias != nullptr) ? to_compute<C>(a.bias[c0 + e]) : C(0);
+  // the ring of rows in flight: ring[i % D] holds row t0 + i
+  vec_t ring[D];
+#pragma unroll
+  for (int d = 0; d < D; ++d) ring[d] = on ? ld(t0 + d) : zero;
+  // the window: win[j] = x[t - 1 - j] in the compute type, zero past the valid prefix
+  C win[KMAX > 1 ? KMAX - 1 : 1][VEC];
+#pragma unroll
+  for (int j = 0; j < KMAX - 1; ++j) {
+    const int64_t p = t0 - 1 - j;
+    vec_t v = zero;
+    if (on && j < H1) {
+      if (p >= 0)
+        v = p < len ? row(xb, p) : zero;
+      else if (a.hist_in != nullptr)
+        v = row(a.hist_in, b * H1 + H1 + p);
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) win[j][e] = to_compute<C>(v[e]);
+  }
 #pragma unroll
   for (int i = 0; i < TT; ++i) {
     const int64_t t = t0 + i;
     if (t >= a.nt) break;  // uniform
-    C out[VEC];
+    const vec_t raw = ring[i % D];
+    if (i + D < TT) ring[i % D] = on ? ld(t + D) : zero;
+    const bool valid = t < len;  // uniform
+    C xcur[VEC], out[VEC];
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
-      C acc = br[e];
+    for (int e = 0; e < VEC; ++e) xcur[e] = valid ? to_compute<C>(raw[e]) : C(0);
+    if (valid) {
 #pragma unroll
-      for (int j = 0; j < KMAX; ++j) {
-        const C xin = (i - j >= 0) ? to_compute<C>(xv[i - j >= 0 ? i - j : 0][e])
-                                   : to_compute<C>(pv[j - i - 1 >= 0 && j - i - 1 < KMAX - 1 ? j - i - 1 : 0][e]);
-        acc += wr[j][e] * xin;
+      for (int e = 0; e < VEC; ++e) {
+        C acc = br[e] + wr[0][e] * xcur[e];
+#pragma unroll
+        for (int j = 1; j < KMAX; ++j) acc += wr[j][e] * win[j - 1][e];
+        out[e] = acc * sigmoid(acc);  // SiLU
       }
-      out[e] = t < len ? acc * sigmoid(acc) : C(0);  // SiLU; zero past the valid prefix
+    } else {  // zero past the valid prefix
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) out[e] = C(0);
+    }
+#pragma unroll
+    for (int j = KMAX - 2; j > 0; --j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) win[j][e] = win[j - 1][e];
+    if constexpr (KMAX > 1) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) win[0][e] = xcur[e];
     }
     if constexpr (G > 0) {
       C ss = C(0);
@@ -167,7 +190,8 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const ConvArgs<T> a) {
       vec_t o;
 #pragma unroll
       for (int e = 0; e < VEC; ++e) o[e] = from_compute<T>(out[e]);
-      *reinterpret_cast<vec_t*>(a.y + (b * a.nt + t) * a.nc + c0) = o;
+      T* yrow = a.y + (b * a.nt + t) * a.nc;  // uniform
+      __builtin_nontemporal_store(o, reinterpret_cast<vec_t*>(yrow + c0));
     }
   }
   // next history: the last K-1 rows of [history | valid prefix]
@@ -176,7 +200,7 @@ __global__ __launch_bounds__(256) void conv_silu_kernel(const ConvArgs<T> a) {
       const int64_t p = len + j - H1;  // position relative to the first token
       vec_t val = zero;
       if (p >= 0)
-        val = row(a.x, b * a.nt + p);
+        val = row(xb, p);
       else if (a.hist_in != nullptr)
         val = row(a.hist_in, b * H1 + H1 + p);
       *reinterpret_cast<vec_t*>(a.hist_out + (b * H1 + j) * a.nc + c0) = val;

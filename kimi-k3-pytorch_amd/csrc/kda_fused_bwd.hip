@@ -33,13 +33,6 @@ struct ComputeOf<double> {
   using type = double;
 };
 
-template <int G, class C>
-__device__ __forceinline__ C group_sum(C v) {
-#pragma unroll
-  for (int off = 1; off < G; off <<= 1) v += __shfl_xor(v, off);
-  return v;
-}
-
 __device__ __forceinline__ void atomic_add(float* p, float v) { atomicAdd(p, v); }
 __device__ __forceinline__ void atomic_add(double* p, double v) { atomicAdd(p, v); }
 
