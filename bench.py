@@ -530,6 +530,8 @@ def kernel_key(name):
     key = base
     if key == "chunk_segment_kernel":
         key += {"0": "<summary>", "1": "<output, prepared>", "2": "<output>"}.get(mode.group(1) if mode else "", "")
+    if key == "seg_kernel":  # the segmented state scans: value-column maps, transition maps, rerun
+        key += {"0": "<maps Q>", "1": "<maps P>", "2": "<run>"}.get(mode.group(1) if mode else "", "")
     if "bwd" in name and not key.startswith("bwd"):
         key = "bwd::" + key
     return key

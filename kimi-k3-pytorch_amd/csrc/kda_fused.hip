@@ -320,10 +320,11 @@ __global__ __launch_bounds__(256) void rmsnorm_gate_kernel(const NormArgs<T> a) 
   const int64_t first = ((static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / 64) * GW * kNormPairs + lane / G;
   vec_t xv[kNormPairs], gv[kNormPairs];
 #pragma unroll
-  for (int u = 0; u < kNormPairs; ++u) {  // all loads first
+  for (int u = 0; u < kNormPairs; ++u) {  // all loads first; streamed data, so non-temporal
     const int64_t pair = first + u * GW;
-    xv[u] = pair < n ? *reinterpret_cast<const vec_t*>(a.x + pair * D + k * VEC) : vec_t{};
-    if (a.gl != nullptr) gv[u] = pair < n ? *reinterpret_cast<const vec_t*>(a.gl + pair * D + k * VEC) : vec_t{};
+    xv[u] = pair < n ? __builtin_nontemporal_load(reinterpret_cast<const vec_t*>(a.x + pair * D + k * VEC)) : vec_t{};
+    if (a.gl != nullptr)
+      gv[u] = pair < n ? __builtin_nontemporal_load(reinterpret_cast<const vec_t*>(a.gl + pair * D + k * VEC)) : vec_t{};
   }
 #pragma unroll
   for (int u = 0; u < kNormPairs; ++u) {
@@ -344,7 +345,7 @@ __global__ __launch_bounds__(256) void rmsnorm_gate_kernel(const NormArgs<T> a) 
       if (a.gl != nullptr) v *= sigmoid(to_compute<C>(gv[u][e]));
       o[e] = from_compute<T>(v);
     }
-    *reinterpret_cast<vec_t*>(a.y + pair * D + k * VEC) = o;
+    __builtin_nontemporal_store(o, reinterpret_cast<vec_t*>(a.y + pair * D + k * VEC));
   }
 }
 
