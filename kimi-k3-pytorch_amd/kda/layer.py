@@ -91,22 +91,26 @@ class KDALayerWeights:
         return self.q_conv.shape[1]
 
     @classmethod
-    def from_module(cls, module) -> "KDALayerWeights":
+    def from_module(cls, module, *, detach: bool = True) -> "KDALayerWeights":
         """The parameters of a module with the reference's attribute names
-        (``KimiDeltaAttention``, src/kda/kda.py:45-62)."""
+        (``KimiDeltaAttention``, src/kda/kda.py:45-62).  ``detach=False``
+        keeps the module's parameters themselves, so that a backward through
+        ``kda_attention_forward`` fills their ``.grad`` (training);
+        the default hands over detached views (inference)."""
         cfg, p = module.config, module.projections
-        bias = lambda lin: None if lin.bias is None else lin.bias.detach()  # noqa: E731
-        conv_bias = lambda c: None if c.bias is None else c.bias.detach()  # noqa: E731
+        d = (lambda t: t.detach()) if detach else (lambda t: t)  # noqa: E731
+        bias = lambda lin: None if lin.bias is None else d(lin.bias)  # noqa: E731
+        conv_bias = lambda c: None if c.bias is None else d(c.bias)  # noqa: E731
         norm = module.output_norm.weight
         return cls(
             num_heads=cfg.num_heads, key_head_dim=cfg.key_head_dim, value_head_dim=cfg.value_head_dim,
-            q_proj=p.q_proj.weight.detach(), k_proj=p.k_proj.weight.detach(), v_proj=p.v_proj.weight.detach(),
-            q_conv=p.q_conv.weight.detach(), k_conv=p.k_conv.weight.detach(), v_conv=p.v_conv.weight.detach(),
-            beta_proj=p.beta_proj.weight.detach(), alpha_down=p.alpha_down.weight.detach(),
-            alpha_up=p.alpha_up.weight.detach(), b_alpha=p.b_alpha.detach(), a_log=module.decay.A_log.detach(),
-            norm_weight=None if norm is None else norm.detach(),
-            gate_proj=module.output_gate.gate_proj.weight.detach(),
-            output_proj=module.output_gate.output_proj.weight.detach(),
+            q_proj=d(p.q_proj.weight), k_proj=d(p.k_proj.weight), v_proj=d(p.v_proj.weight),
+            q_conv=d(p.q_conv.weight), k_conv=d(p.k_conv.weight), v_conv=d(p.v_conv.weight),
+            beta_proj=d(p.beta_proj.weight), alpha_down=d(p.alpha_down.weight),
+            alpha_up=d(p.alpha_up.weight), b_alpha=d(p.b_alpha), a_log=d(module.decay.A_log),
+            norm_weight=None if norm is None else d(norm),
+            gate_proj=d(module.output_gate.gate_proj.weight),
+            output_proj=d(module.output_gate.output_proj.weight),
             g_min=cfg.g_min, eps=cfg.eps, accumulate_state_in_fp32=cfg.accumulate_state_in_fp32,
             q_proj_bias=bias(p.q_proj), k_proj_bias=bias(p.k_proj), v_proj_bias=bias(p.v_proj),
             q_conv_bias=conv_bias(p.q_conv), k_conv_bias=conv_bias(p.k_conv), v_conv_bias=conv_bias(p.v_conv),
