@@ -29,6 +29,8 @@ Metric: "KDA prefill tokens/s (T=8192,H=16,d=128 bf16) + decode-step HBM GB/s".
 * prefill_k64: the prefill at the gpu_48gb head shape (K = V = 64).
 * prefill_f32: f32 inputs at the prefill shape (the split-bf16 chunk path),
                next to the exact recurrence kernel on the same sequence.
+* prefill_configs: the other prefill workloads, B=8 T=1024 H=8 and 4 packed
+               documents (65536 tokens) at H=64, tokens/s and roofline.
 * decay_fusion: the decay feeding the prefill: gates kernel then chunk
                kernel, against the chunk kernel forming g from the logits.
 * backward   : the chunkwise backward (all input gradients) on the prefill
@@ -735,6 +737,72 @@ def bench_dropin(steps, warmup):
     }
 
 
+def bench_configs(steps, warmup):
+    """The other prefill configurations the metric reports as tokens/s and
+    roofline: B=8, T=1024, H=8 (zero initial state, final state out) and the
+    packed documents cu_seqlens = [0, 32768, 49152, 61440, 65536] at H=64
+    (per-document final states), K=V=128, bf16, through the C ABI with the
+    workspace preallocated; inputs drawn on the GPU with the distributions of
+    the prefill workload."""
+    import torch
+
+    from kda import _lib
+
+    lib = _lib.load()
+    device = torch.device("cuda", 0)
+    code = _lib.dtype_code(torch.bfloat16)
+    stream = torch.cuda.current_stream(device).cuda_stream
+    out = {}
+    for name, (B, T, H, offsets) in {
+        "b8_t1024_h8": (8, 1024, 8, None),
+        "packed_4docs_t65536_h64": (1, 65536, 64, [0, 32768, 49152, 61440, 65536]),
+    }.items():
+        K = V = 128
+        gen = torch.Generator(device=device).manual_seed(5)
+        shape_k = (B, T, H, K)
+        q = torch.nn.functional.normalize(torch.randn(shape_k, generator=gen, device=device), dim=-1).bfloat16()
+        k = torch.nn.functional.normalize(torch.randn(shape_k, generator=gen, device=device), dim=-1).bfloat16()
+        v = torch.randn(B, T, H, V, generator=gen, device=device).bfloat16()
+        g = (-torch.nn.functional.softplus(torch.randn(shape_k, generator=gen, device=device) + 2)).bfloat16()
+        beta = torch.sigmoid(torch.randn(B, T, H, generator=gen, device=device)).bfloat16()
+        n_seq = B if offsets is None else len(offsets) - 1
+        o = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=device)
+        s_out = torch.empty(n_seq, H, K, V, dtype=torch.float32, device=device)
+        cu = None if offsets is None else torch.tensor(offsets, dtype=torch.int32, device=device)
+        ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, B * T, H, K, V, code)
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+        args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code, None,
+                s_out.data_ptr(), 0, o.data_ptr(), _lib.ptr(cu), T, None, n_seq, B * T, H, K, V, ws.data_ptr(),
+                ws_bytes, stream)
+        for _ in range(warmup):
+            _lib.check(lib.kda_chunk_fwd(*args))
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(steps):
+            _lib.check(lib.kda_chunk_fwd(*args))
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / steps
+        nbytes = 2 * B * T * H * (3 * K + V) + 2 * B * T * H + 2 * B * T * H * V + 4 * n_seq * H * K * V
+        flops = prefill_flops(B, T, H, K, V)
+        L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
+        _lib.check(lib.kda_chunk_fwd_plan(n_seq, B * T, H, K, V, code, ctypes.byref(L), ctypes.byref(segs)))
+        out[name] = {
+            "workload": f"kda chunkwise prefill B={B} T={T} H={H} K=V=128 bf16, zero initial state, "
+                        + ("final state out" if offsets is None else f"cu_seqlens={offsets}, per-document final states"),
+            "ms": round(ms, 5),
+            "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+            "algorithmic_bytes": nbytes,
+            "achieved_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
+            "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+            "frac_bf16_mfma": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
+            "chunks_per_segment": L.value,
+        }
+        del q, k, v, g, beta, o, ws
+    return out
+
+
 def bench_prefill_f32(steps, warmup):
     """f32 inputs at the long-context shape through kda.chunkwise_kda: the
     split-bf16 chunk path of a dense call, next to the exact recurrence kernel
@@ -913,6 +981,7 @@ def main() -> int:
         "algorithmic_bytes": k64_bytes,
     }
     result["prefill_f32"] = bench_prefill_f32(args.steps, args.warmup)
+    result["prefill_configs"] = bench_configs(args.steps, args.warmup)
     result["decay_fusion"] = bench_decay_fusion()
     result["backward"] = bench_backward()
     result["cache_reorder"] = bench_cache()
