@@ -7,15 +7,21 @@ import torch
 from . import _lib
 
 
-def reject_autograd(*tensors: torch.Tensor | None) -> None:
-    """The GPU path is forward-only; refuse to silently drop gradients."""
-    if not torch.is_grad_enabled():
-        return
-    if any(t is not None and t.requires_grad for t in tensors):
+def workspace(nbytes: int, device: torch.device, what: str) -> torch.Tensor | None:
+    """A caller-owned kernel workspace from the torch allocator (None for 0
+    bytes).  A request beyond the device's free memory (what the caching
+    allocator holds in reserve included) raises a RuntimeError that names the
+    call and the size, before the allocator's own out-of-memory error."""
+    if nbytes == 0:
+        return None
+    free, _ = torch.cuda.mem_get_info(device)
+    spare = torch.cuda.memory_reserved(device) - torch.cuda.memory_allocated(device)
+    if nbytes > free + spare:
         raise RuntimeError(
-            "the MI355X KDA backend implements the forward pass only; "
-            "call it under torch.no_grad()/inference_mode() or detach the inputs"
+            f"{what} needs a workspace of {nbytes / 2**30:.2f} GiB and the device has "
+            f"{(free + spare) / 2**30:.2f} GiB free; split the batch or the documents into smaller calls"
         )
+    return torch.empty(nbytes, dtype=torch.uint8, device=device)
 
 
 def kernel_inputs(q, k, v, g, beta, work_dtype: torch.dtype):

@@ -90,7 +90,7 @@ def _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask
     valid = _prep.valid_lengths(attention_mask, device)
     code = _lib.dtype_code(kernel_dtype)
     ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, total, heads, key_dim, value_dim, code)
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+    workspace = _prep.workspace(ws_bytes, device, "chunkwise_kda")
     status = lib.kda_chunk_fwd(
         qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr(), bc.data_ptr(), code,
         _lib.ptr(s_in), _lib.ptr(s_out), _lib.dtype_code(arith), out.data_ptr(),
@@ -189,7 +189,7 @@ class _ChunkwiseFunction(torch.autograd.Function):
         longest = max(end - start for _, start, end, _ in spans)
         n_b = spans[0][3]
         ws_bytes = lib.kda_chunk_bwd_workspace_bytes(n_b, longest, heads, key_dim, value_dim)
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        workspace = _prep.workspace(ws_bytes, device, "the chunkwise_kda backward")
         code = _lib.dtype_code(kernel_dtype)
         stream = _prep.stream(device)
         state_elems = heads * key_dim * value_dim

@@ -394,7 +394,7 @@ def chunkwise_kda_with_decay(
     valid = _prep.valid_lengths(attention_mask, device)
     code = _lib.dtype_code(q.dtype)
     ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, total, heads, key_dim, value_dim, code)
-    workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device) if ws_bytes else None
+    workspace = _prep.workspace(ws_bytes, device, "chunkwise_kda_with_decay")
     _lib.check(lib.kda_chunk_fwd_decay(
         qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), zc.data_ptr(), _lib.ptr(zb), al.data_ptr(), float(g_min),
         bc.data_ptr(), code, _lib.ptr(s_in), _lib.ptr(s_out), _lib.dtype_code(torch.float32), out.data_ptr(),

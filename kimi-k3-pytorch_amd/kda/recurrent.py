@@ -166,11 +166,11 @@ class _RecurrentStatesFunction(torch.autograd.Function):
         ds0 = torch.empty_like(s0) if s0 is not None and ctx.needs_input_grad[5] else None
         code = _lib.dtype_code(arith)
         ws_bytes = lib.kda_recurrent_bwd_workspace_bytes(batch, heads, key_dim, value_dim, code)
-        workspace = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
+        workspace = _prep.workspace(ws_bytes, device, "the recurrent_kda backward")
         _lib.check(lib.kda_recurrent_bwd(
             qa.data_ptr(), ka.data_ptr(), va.data_ptr(), ga.data_ptr(), ba.data_ptr(), do.data_ptr(), _lib.ptr(s0),
             ha.data_ptr(), _lib.ptr(dha), _lib.ptr(dfa), dq.data_ptr(), dk.data_ptr(), dv.data_ptr(), dg.data_ptr(),
-            dbeta.data_ptr(), _lib.ptr(ds0), batch, tokens, heads, key_dim, value_dim, code, workspace.data_ptr(),
+            dbeta.data_ptr(), _lib.ptr(ds0), batch, tokens, heads, key_dim, value_dim, code, _lib.ptr(workspace),
             ws_bytes, _prep.stream(device),
         ))
         grads = [dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),

@@ -114,11 +114,11 @@ class _UTTransformFunction(torch.autograd.Function):
         dk, dg = torch.empty_like(kc, dtype=arith), torch.empty_like(gc, dtype=arith)
         dv, db = torch.empty_like(vc, dtype=arith), torch.empty_like(bc, dtype=arith)
         ws_bytes = lib.kda_ut_transform_bwd_workspace_bytes(batch, count, heads, key_dim, _lib.dtype_code(arith))
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=k.device)
+        ws = _prep.workspace(ws_bytes, k.device, "the ut_transform backward")
         _lib.check(lib.kda_ut_transform_bwd(
             kc.data_ptr(), vc.data_ptr(), gc.data_ptr(), bc.data_ptr(), _lib.dtype_code(kernel_dtype),
             _lib.ptr(dM), _lib.ptr(dU), _lib.ptr(dW), _lib.ptr(dlg), _lib.ptr(dkg), dk.data_ptr(), dv.data_ptr(),
             dg.data_ptr(), db.data_ptr(), _lib.dtype_code(arith), batch, count, heads, key_dim, value_dim,
-            ws.data_ptr(), ws_bytes, _prep.stream(k.device),
+            _lib.ptr(ws), ws_bytes, _prep.stream(k.device),
         ))
         return dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), db.to(beta.dtype)

@@ -247,3 +247,14 @@ def test_backward_f16_inputs():
     for name, a, b, x in zip(NAMES, got, ref, inputs):
         assert a.dtype == x.dtype, name
         assert rel_err(a, b) < TOL[torch.float16], (name, rel_err(a, b))
+
+
+def test_workspace_beyond_free_memory_raises_a_clear_error():
+    # the wrappers check a kernel workspace against the device's free memory
+    # before allocating it (a 32,768-token document at H=64 needs ~20 GB)
+    from kda import _prep
+
+    with pytest.raises(RuntimeError, match="needs a workspace of .* GiB"):
+        _prep.workspace(1 << 50, torch.device(DEV), "the chunkwise_kda backward")
+    assert _prep.workspace(0, torch.device(DEV), "nothing") is None
+    assert _prep.workspace(4096, torch.device(DEV), "a small call").numel() == 4096
