@@ -350,6 +350,7 @@ __device__ __forceinline__ bool needs_exact(const float* lgS, bool nonneg, int t
 __device__ __forceinline__ void decay_product(f32x4& accK, f32x4& accQ, const float* kS, const float* qS,
                                               const float* lgS, int r0, int c0, int rr, int kd) {
   const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  f32x4 accK2 = zero4(), accQ2 = zero4();  // odd steps: four chains instead of two
   for (int k0 = 0; k0 < kd; k0 += 16) {
     float ka[4], qa[4], kb[4];
 #pragma unroll
@@ -362,11 +363,15 @@ __device__ __forceinline__ void decay_product(f32x4& accK, f32x4& accQ, const fl
       kb[u] = kS[(c0 + i) * kRS + ch] * eb;
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < 4; u += 2) {
       accK = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[u], kb[u], accK, 0, 0, 0);
       accQ = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[u], kb[u], accQ, 0, 0, 0);
+      accK2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[u + 1], kb[u + 1], accK2, 0, 0, 0);
+      accQ2 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[u + 1], kb[u + 1], accQ2, 0, 0, 0);
     }
   }
+  accK += accK2;
+  accQ += accQ2;
 }
 
 // The ten 16x16 block pairs (I, J <= I) of a chunk.
@@ -467,7 +472,10 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
       }
   }
   __syncthreads();
-  for (int idx = tid; idx < kC * kC; idx += kPT) {  // A
+  // the records only the gradient kernels read (A, N, Kg, Kt row-major, W^T)
+  // are skipped when the kernels serve the forward alone (no dO)
+  const bool bwd_records = a.dout != nullptr;
+  for (int idx = tid; bwd_records && idx < kC * kC; idx += kPT) {  // A
     const int r = idx >> 6, cc = idx & 63;
     ws[a.L.A + idx] = AS[r * kRC + cc];
   }
@@ -478,11 +486,11 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     for (int e = 0; e < 8; ++e) x[e] = AqkS[(c0 + e) * kRC + r];
     put_split8(ws + a.L.Aqkt, kC * kC, 8 * i8, x);
   }
-  for (int idx = tid; idx < kC * Kp; idx += kPT) {  // Kg (f32)
+  for (int idx = tid; bwd_records && idx < kC * Kp; idx += kPT) {  // Kg (f32)
     const int r = idx / Kp, col = idx % Kp;
     ws[a.L.Kg + idx] = fast_exp(lgS[r * kRS + col]) * kS[r * kRS + col];
   }
-  for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {  // Kt split, row-major
+  for (int i8 = tid; bwd_records && i8 < kC * Kp / 8; i8 += kPT) {  // Kt split, row-major
     const int r = (8 * i8) / Kp, c0 = (8 * i8) % Kp;
     float x[8];
 #pragma unroll
@@ -553,7 +561,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
   for (int idx = tid; idx < kC * kC; idx += kPT) {  // M = N diag(b) over A
     const int r = idx >> 6, cc = idx & 63;
     const float n = NS[r * kRC + cc];
-    ws[a.L.N + idx] = n;
+    if (bwd_records) ws[a.L.N + idx] = n;
     AS[r * kRC + cc] = n * bS[cc];
   }
   __syncthreads();
@@ -577,7 +585,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
       y[e] = qS[(r2 + e) * kRS + c2];
     }
     put_split8(ws + a.L.Wr, kC * Kp, 8 * i8, x);
-    put_split8(ws + a.L.Wt, kC * Kp, 8 * i8, y);
+    if (bwd_records) put_split8(ws + a.L.Wt, kC * Kp, 8 * i8, y);
   }
   for (int tt = w; tt < 4 * nvt; tt += kPT / 64) {  // U = M v
     const int rt = tt & 3, ct = tt >> 2;
@@ -1523,15 +1531,21 @@ __device__ __forceinline__ void pair_mfma(const Args<IT>& a, const float* ws, fl
   f32x4 R1[CW], R2[CW], R3[CW], R4[CW];
 #pragma unroll
   for (int ct = 0; ct < CW; ++ct) R1[ct] = R2[ct] = R3[ct] = R4[ct] = zero4();
+  {  // R1, R2 over j < 16 (J + 1): the column tiles inside the reduction loop,
+     // so 2 CW independent accumulation chains keep the MFMA pipe full
+    float rI[CW];
 #pragma unroll
-  for (int ct = 0; ct < CW; ++ct) {  // R1, R2 over j < 16 (J + 1)
-    const int cc = 16 * (ct0 + ct) + li;
-    const float rI = lgS[16 * J * kRS + cc];
+    for (int ct = 0; ct < CW; ++ct) rI[ct] = lgS[16 * J * kRS + 16 * (ct0 + ct) + li];
     for (int k0 = 0; k0 < 16 * (J + 1); k0 += 4) {
       const int j = k0 + lg4;
-      const float bk = kS[j * kRS + cc] * fast_exp(rI - lgS[j * kRS + cc]);
-      R1[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(dAS[(16 * J + li) * kRC + j], bk, R1[ct], 0, 0, 0);
-      R2[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(dQS[(16 * J + li) * kRC + j], bk, R2[ct], 0, 0, 0);
+      const float ak = dAS[(16 * J + li) * kRC + j], aq = dQS[(16 * J + li) * kRC + j];
+#pragma unroll
+      for (int ct = 0; ct < CW; ++ct) {
+        const int cc = 16 * (ct0 + ct) + li;
+        const float bk = kS[j * kRS + cc] * fast_exp(rI[ct] - lgS[j * kRS + cc]);
+        R1[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(ak, bk, R1[ct], 0, 0, 0);
+        R2[ct] = __builtin_amdgcn_mfma_f32_16x16x4f32(aq, bk, R2[ct], 0, 0, 0);
+      }
     }
   }
   for (int I = J; I < 4; ++I) {  // R3, R4 over rows i of block I >= J
