@@ -601,18 +601,21 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
 //   backward (chunks NC-1 .. 0):  R = -(Kt X + Aqk^T dO),    X' = D X + W^T R + Qg^T dO
 // (forward X = S and R = Vt; backward X = dS', the gradient of the chunk's end
 // state, and R = -dVt).  The chunk chain of each sequence is cut into nseg
-// segments of seglen chunks:
-//   seg_kernel<SUM = true>   one block per (direction, sequence x head, segment
-//                            but the last): the segment's affine map
-//                            X_out = P X_in + Q, by running the chunk maps on
-//                            X = [0 | I] (V value columns, K transition columns);
-//   seg_combine_kernel       X_{g+1} = P_g X_g + Q_g along the segments (f32 MFMA);
-//   seg_kernel<SUM = false>  one block per (direction, sequence x head,
-//                            segment): the segment again from its true start
-//                            state, writing each chunk's X and R (and the final
-//                            state after the last chunk).
-// The state lives in f32 MFMA accumulators, one 16-column tile per wave and
-// kind (value, transition).  Every product uses split-bf16 operands
+// segments of seglen chunks, the same chunks in both directions:
+//   seg_kernel<kSumV>, <kSumT>  the segment's affine map X_out = P X_in + Q, by
+//                               running the chunk maps on X = [0 | I]: Q from
+//                               the V value columns (per direction), P from
+//                               the K transition columns (forward only: the
+//                               backward's chunk transition D - W^T Kt is the
+//                               transpose of the forward's D - Kt^T W, so its
+//                               segment map is the forward map of the same
+//                               chunks, transposed);
+//   seg_combine_kernel          X_{g+1} = P_g X_g + Q_g along the segments (f32 MFMA);
+//   seg_kernel<kRun>            each segment again from its true start state,
+//                               writing each chunk's X and R (and the final
+//                               state after the last chunk).
+// The state lives in f32 MFMA accumulators, one 16-column tile per wave.
+// Every product uses split-bf16 operands
 // (x = hi + lo; hi*hi + hi*lo + lo*hi).  An accumulator pair (row tiles 2s,
 // 2s+1) is the B operand of reduction step s with the reduction index
 // permuted as perm_k; the A operands are stored in LDS with the same
@@ -734,6 +737,18 @@ struct DoFrag {
 // transition columns (P), or the rerun of a segment from its start state.
 constexpr int kSumV = 0, kSumT = 1, kRun = 2;
 
+// Segments per (sequence, head) that a launch of kind MODE runs: every
+// segment for the reruns; all but the last for the value maps; for the
+// transition maps (forward direction only) all but the last when the forward
+// runs alone, and all of them when the backward, which takes their
+// transposes in reverse order, runs too.
+template <class IT>
+__host__ __device__ inline int seg_blocks(const Args<IT>& a, int mode) {
+  if (mode == kRun) return a.nseg;
+  if (mode == kSumT) return a.ndir == 2 ? a.nseg : a.nseg - 1;
+  return a.nseg - 1;
+}
+
 template <class IT, int KP, int MODE, int DIR>
 __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned char* sm) {
   using SL = SegLds<KP>;
@@ -742,7 +757,7 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
   constexpr bool DO_TERMS = BWD && !TRANS;                            // Aqk^T dO and Qg^T dO
   constexpr bool EXACT_DO = sizeof(IT) == 2 && !__is_same(IT, f16);  // bf16 dO: its lo part is zero
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g4 = lane >> 4;
-  const int nsb = MODE == kRun ? a.nseg : a.nseg - 1;
+  const int nsb = seg_blocks(a, MODE);
   const int64_t bhn = a.B * a.H;
   const int64_t bh = id / nsb, b = bh / a.H, h = bh % a.H;
   const int gseg = static_cast<int>(id % nsb);
@@ -751,8 +766,13 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
   const int col = 16 * w + li;                     // this lane's column (value or transition)
   float* rec = a.seg + ((static_cast<int64_t>(DIR) * bhn + bh) * a.nseg + gseg) *
                            (static_cast<int64_t>(KP) * KP + 2 * static_cast<int64_t>(KP) * Vp);
-  const int p0 = gseg * a.seglen;
-  const int p1 = p0 + a.seglen < a.NC ? p0 + a.seglen : static_cast<int>(a.NC);
+  // segment g of the backward scan is the forward's segment nseg - 1 - g, run
+  // from its last chunk down, so that the two directions cut the chain at the
+  // same chunks (the backward's transition maps are then the forward's, transposed)
+  const int fg = BWD ? a.nseg - 1 - gseg : gseg;
+  const int lo = fg * a.seglen;
+  const int hi = lo + a.seglen < a.NC ? lo + a.seglen : static_cast<int>(a.NC);
+  const int p0 = 0, p1 = hi - lo;
 
   f32x4 X[NKT];
 #pragma unroll
@@ -777,7 +797,7 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
   float dval = 0.f;
   float u[4][4];    // forward value columns: U of the next chunk, accumulator layout
   DoFrag<IT> dof;   // backward value columns: dO of the next chunk
-  auto chunk_of = [&](int p) -> int64_t { return BWD ? a.NC - 1 - p : p; };
+  auto chunk_of = [&](int p) -> int64_t { return BWD ? hi - 1 - p : lo + p; };
   auto fetch = [&](int p) {
     const int64_t c = chunk_of(p);
     const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
@@ -955,12 +975,16 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
 template <class IT, int KP, int MODE>
 __global__ __launch_bounds__(kSC) void seg_kernel(const Args<IT> a) {
   __shared__ __attribute__((aligned(16))) unsigned char sm[SegLds<KP>::bytes];
-  const int64_t n = a.B * a.H * (MODE == kRun ? a.nseg : a.nseg - 1);
+  const int64_t n = a.B * a.H * seg_blocks(a, MODE);
   const int64_t id = blockIdx.x;
-  if (a.dir0 == 0 && id < n)
+  if constexpr (MODE == kSumT) {  // the forward's transition maps serve both directions
     seg_body<IT, KP, MODE, 0>(a, id, sm);
-  else
-    seg_body<IT, KP, MODE, 1>(a, id - (a.dir0 == 0 ? n : 0), sm);
+  } else {
+    if (a.dir0 == 0 && id < n)
+      seg_body<IT, KP, MODE, 0>(a, id, sm);
+    else
+      seg_body<IT, KP, MODE, 1>(a, id - (a.dir0 == 0 ? n : 0), sm);
+  }
 }
 
 // X_0 = the initial value (forward S0, backward dS_T; zero when absent), then
@@ -988,8 +1012,13 @@ __device__ __forceinline__ void combine_body(const Args<IT>& a, int64_t id, floa
   }
   f32x4 pf[NP];
   float qf[2][4];
+  // the backward's transition map of its segment g is the transpose of the
+  // forward's map of segment nseg - 1 - g (the same chunks): staged as it is
+  // and read with the strides swapped
+  const float* fwd = a.seg + bh * a.nseg * segf;
   auto fetch = [&](int gs) {
-    const float* P = base + gs * segf;
+    const float* P = DIR == 1 ? fwd + (a.nseg - 1 - gs) * segf : base + gs * segf;
+    const float* Q = base + gs * segf + KP * KP;
 #pragma unroll
     for (int j = 0; j < NP; ++j) pf[j] = *reinterpret_cast<const f32x4*>(P + 4 * (tid + kCT * j));
 #pragma unroll
@@ -997,7 +1026,7 @@ __device__ __forceinline__ void combine_body(const Args<IT>& a, int64_t id, floa
       const int rt = w + 4 * j;
       if (rt < KP / 16) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) qf[j][r] = P[KP * KP + (16 * rt + 4 * g4 + r) * Vp + col0 + li];
+        for (int r = 0; r < 4; ++r) qf[j][r] = Q[(16 * rt + 4 * g4 + r) * Vp + col0 + li];
       }
     }
   };
@@ -1020,7 +1049,8 @@ __device__ __forceinline__ void combine_body(const Args<IT>& a, int64_t id, floa
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int rt = w + 4 * j;
-      if (rt < KP / 16) acc[j] = mma_long(acc[j], Mat{Ps, PS, 1}, 16 * rt, Mat{Xs, XS, 1}, 0, KP);
+      if (rt < KP / 16)
+        acc[j] = mma_long(acc[j], DIR == 1 ? Mat{Ps, 1, PS} : Mat{Ps, PS, 1}, 16 * rt, Mat{Xs, XS, 1}, 0, KP);
     }
     __syncthreads();  // every read of X_g is done
 #pragma unroll
@@ -1708,9 +1738,12 @@ template <class IT, int KP>
 static void launch_scans(const bwd::Args<IT>& a, hipStream_t s) {
   const int64_t bh = a.B * a.H * a.ndir;
   if (a.nseg > 1) {
-    const dim3 g(static_cast<unsigned>(bh * (a.nseg - 1)));
-    hipLaunchKernelGGL((bwd::seg_kernel<IT, KP, bwd::kSumV>), g, dim3(bwd::kSC), 0, s, a);
-    hipLaunchKernelGGL((bwd::seg_kernel<IT, KP, bwd::kSumT>), g, dim3(bwd::kSC), 0, s, a);
+    hipLaunchKernelGGL((bwd::seg_kernel<IT, KP, bwd::kSumV>), dim3(static_cast<unsigned>(bh * (a.nseg - 1))),
+                       dim3(bwd::kSC), 0, s, a);
+    // transition maps: the forward direction's, which the backward reads transposed
+    hipLaunchKernelGGL((bwd::seg_kernel<IT, KP, bwd::kSumT>),
+                       dim3(static_cast<unsigned>(a.B * a.H * bwd::seg_blocks(a, bwd::kSumT))), dim3(bwd::kSC), 0, s,
+                       a);
   }
   hipLaunchKernelGGL((bwd::seg_combine_kernel<IT, KP>), dim3(static_cast<unsigned>(bh * (a.L.Vp / 16))),
                      dim3(bwd::kCT), 0, s, a);
