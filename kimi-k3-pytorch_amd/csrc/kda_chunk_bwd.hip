@@ -798,13 +798,19 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
   float u[4][4];    // forward value columns: U of the next chunk, accumulator layout
   DoFrag<IT> dof;   // backward value columns: dO of the next chunk
   auto chunk_of = [&](int p) -> int64_t { return BWD ? hi - 1 - p : lo + p; };
-  auto fetch = [&](int p) {
+  // the next chunk's records in three parts, issued between the product
+  // phases of this chunk so that each part's requests drain while the MFMAs
+  // of the following phase run
+  auto fetch_part = [&](int p, int part) {
     const int64_t c = chunk_of(p);
     const float* ws = a.ws + (bh * a.NC + c) * a.L.per;
     if constexpr (!BWD) {
-      ra.fetch(ws + a.L.Wr, tid);
-      rb.fetch(ws + a.L.Ktt, tid);
-      if (!TRANS && has) {
+      if (part == 0) ra.fetch(ws + a.L.Wr, tid);
+      if (part == 1) {
+        rb.fetch(ws + a.L.Ktt, tid);
+        if (tid < KP) dval = ws[a.L.D + tid];
+      }
+      if (part == 2 && !TRANS && has) {
         const float* up = ws + a.L.U + opaque(4 * g4 * Vp + col);
 #pragma unroll
         for (int I = 0; I < 4; ++I)
@@ -812,15 +818,24 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
           for (int r = 0; r < 4; ++r) u[I][r] = up[(16 * I + r) * Vp];
       }
     } else {
-      ra.fetch(ws + a.L.Ktr, tid);
-      rb.fetch(ws + a.L.Wt, tid);
+      if (part == 0) ra.fetch(ws + a.L.Ktr, tid);
+      if (part == 1) {
+        rb.fetch(ws + a.L.Wt, tid);
+        if constexpr (DO_TERMS) raq.fetch(ws + a.L.Aqkt, tid);
+        if (tid < KP) dval = ws[a.L.D + tid];
+      }
       if constexpr (DO_TERMS) {
-        rq.fetch(ws + a.L.Qgt, tid);
-        raq.fetch(ws + a.L.Aqkt, tid);
-        if (has) dof.fetch(a, b, h, c * kC, col, g4);
+        if (part == 2) {
+          rq.fetch(ws + a.L.Qgt, tid);
+          if (has) dof.fetch(a, b, h, c * kC, col, g4);
+        }
       }
     }
-    if (tid < KP) dval = ws[a.L.D + tid];
+  };
+  auto fetch = [&](int p) {
+    fetch_part(p, 0);
+    fetch_part(p, 1);
+    fetch_part(p, 2);
   };
   if (p0 < p1) fetch(p0);
   for (int p = p0; p < p1; ++p) {
@@ -847,8 +862,12 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
       }
     }
     __syncthreads();
-    if (p + 1 < p1) fetch(p + 1);
-    if (!has) continue;  // no barrier below: idle waves go straight to the next chunk's barrier
+    const bool more = p + 1 < p1;
+    if (!has) {  // no barrier below: idle waves go straight to the next chunk's barrier
+      if (more) fetch(p + 1);
+      continue;
+    }
+    if (more) fetch_part(p + 1, 0);
 
     // P = B X (forward B = W, backward B = Kt), plus Aqk^T dO (backward value
     // columns); one fragment pair ahead
@@ -889,6 +908,7 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
         }
       }
     }
+    if (more) fetch_part(p + 1, 1);
     // R = U - P (forward value columns) or -P
 #pragma unroll
     for (int I = 0; I < 4; ++I)
@@ -912,6 +932,7 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
     bf16x8 rh[2], rl[2];
 #pragma unroll
     for (int st = 0; st < 2; ++st) split_pair(P[2 * st], P[2 * st + 1], rh[st], rl[st]);
+    if (more) fetch_part(p + 1, 2);
     const float* Ds = reinterpret_cast<const float*>(sm + SL::d);
 #pragma unroll
     for (int ct = 0; ct < NKT; ++ct) X[ct] *= *reinterpret_cast<const f32x4*>(Ds + 16 * ct + 4 * g4);
