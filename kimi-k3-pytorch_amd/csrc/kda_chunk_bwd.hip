@@ -272,6 +272,56 @@ __device__ __forceinline__ void load_rows(float* dst, const IT* src, int64_t b, 
   }
 }
 
+// load_rows split in two: `fetch` issues the loads of the whole-group case
+// (rows_fast) into registers and `store` widens them into LDS, so that the
+// loads of several tiles go out together and their latency is paid once (a
+// load_rows call waits for its own loads before the next call's are issued).
+__device__ __forceinline__ bool rows_fast(int64_t X, int col0, int ncol) {
+  return (X & 3) == 0 && col0 + ncol <= X;
+}
+template <class IT, int NCOL, int NT>
+struct RowTile {
+  static constexpr int G = NCOL / 4, PER = kC * G / NT;
+  static_assert(PER * NT == kC * G, "the tile must split evenly over the threads");
+  typename Raw4<IT>::type v[PER];
+  __device__ __forceinline__ void fetch(const IT* src, int64_t b, int64_t t0, int64_t T, int64_t H, int64_t h,
+                                        int64_t X, int col0, int tid) {
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+      const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+      const int64_t t = t0 + r < T ? t0 + r : T - 1;
+      v[it] = *reinterpret_cast<const typename Raw4<IT>::type*>(src + tok(b, t, T, H, h) * X + col0 + c4);
+    }
+  }
+  template <int RS>
+  __device__ __forceinline__ void store(float* dst, int64_t t0, int64_t Tv, int tid) const {
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+      const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+      *reinterpret_cast<f32x4*>(&dst[r * RS + c4]) = t0 + r < Tv ? widen<IT>(v[it]) : zero4();
+    }
+  }
+};
+
+// k, q and g rows of a chunk into LDS with one round trip to memory
+template <class IT, int KP, int NT>
+__device__ __forceinline__ void load_kqg(float* kS, float* qS, float* lgS, const Args<IT>& a, int64_t b, int64_t t0,
+                                         int64_t h, int tid, int64_t Tv) {
+  if (rows_fast(a.K, 0, KP)) {
+    RowTile<IT, KP, NT> rk, rq, rg;
+    rk.fetch(a.k, b, t0, a.T, a.H, h, a.K, 0, tid);
+    rq.fetch(a.q, b, t0, a.T, a.H, h, a.K, 0, tid);
+    rg.fetch(a.g, b, t0, a.T, a.H, h, a.K, 0, tid);
+    rk.template store<kRS>(kS, t0, Tv, tid);
+    rq.template store<kRS>(qS, t0, Tv, tid);
+    rg.template store<kRS>(lgS, t0, Tv, tid);
+  } else {
+    load_rows<IT, KP, kRS, NT>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid, Tv);
+    load_rows<IT, KP, kRS, NT>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid, Tv);
+    load_rows<IT, KP, kRS, NT>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid, Tv);
+  }
+}
+
 // NROW x NCOL f32 from a workspace matrix (row stride ld, from column col0)
 // into LDS rows of stride RS.
 template <int NROW, int NCOL, int RS, int NT>
@@ -401,9 +451,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     Tv = n < 0 ? 0 : (n < a.T ? n : a.T);
   }
 
-  load_rows<IT, KP, kRS, kPT>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid, Tv);
-  load_rows<IT, KP, kRS, kPT>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid, Tv);
-  load_rows<IT, KP, kRS, kPT>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid, Tv);
+  load_kqg<IT, KP, kPT>(kS, qS, lgS, a, b, t0, h, tid, Tv);
   if (tid < kC) {
     const int64_t t = t0 + tid;
     bS[tid] = t < Tv ? to_float(a.beta[tok(b, t, a.T, a.H, h)]) : 0.f;
@@ -525,6 +573,15 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     kS[r * kRS + col] *= fast_exp(lgS[r * kRS + col]);
   }
   __syncthreads();
+  // v (into lg's rows once W is formed): its loads go out now and land while
+  // N, M and W are formed
+  const bool v_early = (Vp & 31) == 0 && rows_fast(a.V, 0, Vp);
+  RowTile<IT, 32, kPT> rv[4];  // Vp <= 128
+  if (v_early) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (32 * j < Vp) rv[j].fetch(a.v, b, t0, a.T, a.H, h, a.V, 32 * j, tid);
+  }
   // N = L^-1 by 16x16 blocks: wave w inverts diagonal block w by forward
   // substitution (lane c < 16 solves column c), then block rows I = 1..3 follow
   // N_IJ = -N_II sum_{K=J}^{I-1} L_IK N_KJ on the MFMA.
@@ -572,8 +629,14 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) qS[(16 * rt + 4 * lg4 + r) * kRS + 16 * ct + li] = acc[r];
   }
-  for (int s0 = 0; s0 < Vp; s0 += 32)  // v over lg (no longer read)
-    load_rows<IT, 32, kRS, kPT>(lgS + s0, a.v, b, t0, a.T, a.H, h, a.V, s0, tid, Tv);
+  if (v_early) {  // v over lg (no longer read)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (32 * j < Vp) rv[j].template store<kRS>(lgS + 32 * j, t0, Tv, tid);
+  } else {
+    for (int s0 = 0; s0 < Vp; s0 += 32)
+      load_rows<IT, 32, kRS, kPT>(lgS + s0, a.v, b, t0, a.T, a.H, h, a.V, s0, tid, Tv);
+  }
   __syncthreads();
   for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {  // W and W^T split
     float x[8], y[8];
@@ -1682,11 +1745,24 @@ __global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
   const int64_t t0 = c * kC;
   const float* ws = a.ws + ch * a.L.per;
-  load_rows<IT, KP, kRS, NT>(kS, a.k, b, t0, a.T, a.H, h, a.K, 0, tid);
-  load_rows<IT, KP, kRS, NT>(qS, a.q, b, t0, a.T, a.H, h, a.K, 0, tid);
-  load_rows<IT, KP, kRS, NT>(lgS, a.g, b, t0, a.T, a.H, h, a.K, 0, tid);
-  load_ws<kC, kC, kRC, NT>(dAS, ws + a.L.dA, kC, 0, tid);
-  load_ws<kC, kC, kRC, NT>(dQS, ws + a.L.dAqk, kC, 0, tid);
+  {
+    // dA and dAqk go out first (no branch), then k, q, g: one round trip
+    constexpr int PW = kC * (kC / 4) / NT;
+    f32x4 wa[PW], wq[PW];
+#pragma unroll
+    for (int it = 0; it < PW; ++it) {
+      const int item = tid + NT * it, r = item / (kC / 4), c4 = (item % (kC / 4)) * 4;
+      wa[it] = *reinterpret_cast<const f32x4*>(ws + a.L.dA + r * kC + c4);
+      wq[it] = *reinterpret_cast<const f32x4*>(ws + a.L.dAqk + r * kC + c4);
+    }
+    load_kqg<IT, KP, NT>(kS, qS, lgS, a, b, t0, h, tid, a.T);
+#pragma unroll
+    for (int it = 0; it < PW; ++it) {
+      const int item = tid + NT * it, r = item / (kC / 4), c4 = (item % (kC / 4)) * 4;
+      *reinterpret_cast<f32x4*>(&dAS[r * kRC + c4]) = wa[it];
+      *reinterpret_cast<f32x4*>(&dQS[r * kRC + c4]) = wq[it];
+    }
+  }
   __syncthreads();
   const bool rising = chunk_cumsum<KP>(lgS, red, tid);  // red is written later
   int nred;
