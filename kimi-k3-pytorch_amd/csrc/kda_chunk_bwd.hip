@@ -1286,6 +1286,57 @@ __device__ __forceinline__ void load_ws_split(__bf16* dst, const float* src, int
   }
 }
 
+// One 32-column slab of grad_kernel's operands in registers: the S and dS
+// rows (KP x 32), Vt and dVt (64 x 32, f32 from the workspace) and dO and v
+// (64 x 32 from the inputs; the whole-group case of load_rows_split).  The
+// next slab's loads go out while the current one is multiplied.
+template <class IT, int KP, int NT>
+struct GradSlab {
+  static constexpr int PS = KP * 8 / NT, PC = kC * 8 / NT;
+  static_assert(PS * NT == KP * 8 && PC * NT == kC * 8, "the slab must split evenly over the threads");
+  f32x4 s[PS], ds[PS], vt[PC], dvt[PC];
+  typename Raw4<IT>::type dout[PC], v[PC];
+  __device__ __forceinline__ void fetch(const Args<IT>& a, const float* ws, int64_t b, int64_t t0, int64_t h, int s0,
+                                        int tid) {
+    const int Vp = a.L.Vp;
+#pragma unroll
+    for (int it = 0; it < PS; ++it) {
+      const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+      s[it] = *reinterpret_cast<const f32x4*>(ws + a.L.S + r * Vp + s0 + c4);
+      ds[it] = *reinterpret_cast<const f32x4*>(ws + a.L.dS + r * Vp + s0 + c4);
+    }
+#pragma unroll
+    for (int it = 0; it < PC; ++it) {
+      const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+      vt[it] = *reinterpret_cast<const f32x4*>(ws + a.L.Vt + r * Vp + s0 + c4);
+      dvt[it] = *reinterpret_cast<const f32x4*>(ws + a.L.dVt + r * Vp + s0 + c4);
+      const int64_t t = t0 + r < a.T ? t0 + r : a.T - 1;
+      const int64_t row = tok(b, t, a.T, a.H, h) * a.V + s0 + c4;
+      dout[it] = *reinterpret_cast<const typename Raw4<IT>::type*>(a.dout + row);
+      v[it] = *reinterpret_cast<const typename Raw4<IT>::type*>(a.v + row);
+    }
+  }
+  __device__ __forceinline__ void store(__bf16* Ss, __bf16* dSn, __bf16* Vts, __bf16* dVts, float* dVf, __bf16* dOs,
+                                        __bf16* vs, int64_t t0, int64_t T, int tid) const {
+#pragma unroll
+    for (int it = 0; it < PS; ++it) {
+      const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+      put_split4(Ss, KP * kSR, r, c4, s[it]);
+      put_split4(dSn, KP * kSR, r, c4, ds[it]);
+    }
+#pragma unroll
+    for (int it = 0; it < PC; ++it) {
+      const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+      put_split4(Vts, kC * kSR, r, c4, vt[it]);
+      put_split4(dVts, kC * kSR, r, c4, dvt[it]);
+      *reinterpret_cast<f32x4*>(&dVf[r * kSS + c4]) = dvt[it];
+      const bool real = t0 + r < T;
+      put_split4(dOs, kC * kSR, r, c4, real ? widen<IT>(dout[it]) : zero4());
+      put_split4(vs, kC * kSR, r, c4, real ? widen<IT>(v[it]) : zero4());
+    }
+  }
+};
+
 // Columns col0 .. col0+31 of the chunk's rows of an input [B,T,H,X], split into
 // LDS (zero past T and X); see load_rows.
 template <class IT, int NT>
@@ -1354,15 +1405,25 @@ __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
   float* dVf = sm + kOffdVf;
   const SMat mS{Ss, KP * kSR, kSR}, mdS{dSn, KP * kSR, kSR}, mdO{dOs, kC * kSR, kSR}, mVt{Vts, kC * kSR, kSR},
       mdVt{dVts, kC * kSR, kSR}, mv{vs, kC * kSR, kSR};
+  // V a multiple of the slab width: each slab's loads are issued one slab
+  // ahead, into registers; otherwise slab by slab with the edge checks
+  const bool ahead = rows_fast(a.V, 0, Vp);
+  GradSlab<IT, KP, NT> gs;
+  if (ahead) gs.fetch(a, ws, b, t0, h, 0, tid);
   for (int s0 = 0; s0 < Vp; s0 += kSW) {  // Vp is a multiple of the slab width
-    load_ws_split<KP, NT>(Ss, ws + a.L.S, Vp, s0, tid);
-    load_ws_split<KP, NT>(dSn, ws + a.L.dS, Vp, s0, tid);
-    load_ws_split<kC, NT>(Vts, ws + a.L.Vt, Vp, s0, tid);
-    load_ws_split<kC, NT>(dVts, ws + a.L.dVt, Vp, s0, tid);
-    load_ws<kC, kSW, kSS, NT>(dVf, ws + a.L.dVt, Vp, s0, tid);
-    load_rows_split<IT, NT>(dOs, a.dout, b, t0, a.T, a.H, h, a.V, s0, tid);
-    load_rows_split<IT, NT>(vs, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
+    if (ahead) {
+      gs.store(Ss, dSn, Vts, dVts, dVf, dOs, vs, t0, a.T, tid);
+    } else {
+      load_ws_split<KP, NT>(Ss, ws + a.L.S, Vp, s0, tid);
+      load_ws_split<KP, NT>(dSn, ws + a.L.dS, Vp, s0, tid);
+      load_ws_split<kC, NT>(Vts, ws + a.L.Vt, Vp, s0, tid);
+      load_ws_split<kC, NT>(dVts, ws + a.L.dVt, Vp, s0, tid);
+      load_ws<kC, kSW, kSS, NT>(dVf, ws + a.L.dVt, Vp, s0, tid);
+      load_rows_split<IT, NT>(dOs, a.dout, b, t0, a.T, a.H, h, a.V, s0, tid);
+      load_rows_split<IT, NT>(vs, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
+    }
     __syncthreads();
+    if (ahead && s0 + kSW < Vp) gs.fetch(a, ws, b, t0, h, s0 + kSW, tid);
     {  // dv = M^T dVt, tile (rt, hf) of the slab
       const f32x4 acc = mma(zero4(), Mat{MS, 1, kRC}, 16 * rt, Mat{dVf, kSS, 1}, 16 * hf, kC);
 #pragma unroll
