@@ -322,6 +322,30 @@ __device__ __forceinline__ void load_kqg(float* kS, float* qS, float* lgS, const
   }
 }
 
+// load_ws split in two (fetch into registers, store into LDS rows of stride
+// RS), so that the loads can go out ahead of the point where the tile is needed.
+template <int NROW, int NCOL, int NT>
+struct WsTile {
+  static constexpr int G = NCOL / 4, PER = NROW * G / NT;
+  static_assert(PER * NT == NROW * G, "the tile must split evenly over the threads");
+  f32x4 v[PER];
+  __device__ __forceinline__ void fetch(const float* src, int ld, int col0, int tid) {
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+      const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+      v[it] = *reinterpret_cast<const f32x4*>(src + r * ld + col0 + c4);
+    }
+  }
+  template <int RS>
+  __device__ __forceinline__ void store(float* dst, int tid) const {
+#pragma unroll
+    for (int it = 0; it < PER; ++it) {
+      const int item = tid + NT * it, r = item / G, c4 = (item % G) * 4;
+      *reinterpret_cast<f32x4*>(&dst[r * RS + c4]) = v[it];
+    }
+  }
+};
+
 // NROW x NCOL f32 from a workspace matrix (row stride ld, from column col0)
 // into LDS rows of stride RS.
 template <int NROW, int NCOL, int RS, int NT>
@@ -1409,6 +1433,7 @@ __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
   // ahead, into registers; otherwise slab by slab with the edge checks
   const bool ahead = rows_fast(a.V, 0, Vp);
   GradSlab<IT, KP, NT> gs;
+  WsTile<kC, KP, NT> kg;
   if (ahead) gs.fetch(a, ws, b, t0, h, 0, tid);
   for (int s0 = 0; s0 < Vp; s0 += kSW) {  // Vp is a multiple of the slab width
     if (ahead) {
@@ -1422,8 +1447,9 @@ __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
       load_rows_split<IT, NT>(dOs, a.dout, b, t0, a.T, a.H, h, a.V, s0, tid);
       load_rows_split<IT, NT>(vs, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
     }
-    __syncthreads();
     if (ahead && s0 + kSW < Vp) gs.fetch(a, ws, b, t0, h, s0 + kSW, tid);
+    if (s0 + kSW >= Vp) kg.fetch(ws + a.L.Kg, KP, 0, tid);  // for dM += dW Kg^T after the slabs
+    __syncthreads();
     {  // dv = M^T dVt, tile (rt, hf) of the slab
       const f32x4 acc = mma(zero4(), Mat{MS, 1, kRC}, 16 * rt, Mat{dVf, kSS, 1}, 16 * hf, kC);
 #pragma unroll
@@ -1474,9 +1500,13 @@ __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
       const int row = 16 * rt + 4 * lg4 + r, col = 16 * (hf * 2 + j) + li;
       ws[a.L.dAqk + row * kC + col] = col <= row ? aA[j][r] : 0.f;
     }
-  load_ws<kC, KP, kRS, NT>(Y, ws + a.L.Kg, KP, 0, tid);
+  kg.template store<kRS>(Y, tid);
   if (tid < Kp) ws[a.L.dD + tid] = dd;
   __syncthreads();
+  // N and A for dbeta and dA: loaded while dKg and dM are formed
+  WsTile<kC, kC, NT> wn, wa;
+  wn.fetch(ws + a.L.N, kC, 0, tid);
+  wa.fetch(ws + a.L.A, kC, 0, tid);
 #pragma unroll
   for (int j = 0; j < CH; ++j) {  // dKg = M^T dW
     const int ct = hf * CH + j;
@@ -1491,8 +1521,8 @@ __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
 
   // dbeta and dA from N: dN = dM diag(b), T1 = N^T dN, dL = -strict(T1 N^T)
   float *NS = sm + kOffN, *DM = sm + kOffDM, *DN = sm + kOffDN, *AS = sm + kOffA;
-  load_ws<kC, kC, kRC, NT>(NS, ws + a.L.N, kC, 0, tid);
-  load_ws<kC, kC, kRC, NT>(AS, ws + a.L.A, kC, 0, tid);
+  wn.template store<kRC>(NS, tid);
+  wa.template store<kRC>(AS, tid);
 #pragma unroll
   for (int j = 0; j < 2; ++j)
 #pragma unroll
