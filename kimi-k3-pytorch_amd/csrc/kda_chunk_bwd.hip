@@ -1227,6 +1227,11 @@ __global__ __launch_bounds__(kOT) void out_kernel(const Args<IT> a) {
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
   const int64_t t0 = c * kC;
   const float* ws = a.ws + ch * a.L.per;
+  // each slab's S and Vt loads go out one slab ahead (the first before the records)
+  WsTile<KP, 32, kOT> ts;
+  WsTile<kC, 32, kOT> tv;
+  ts.fetch(ws + a.L.S, a.L.Vp, 0, tid);
+  tv.fetch(ws + a.L.Vt, a.L.Vp, 0, tid);
   {  // the split records back to f32: Qgt[col * 64 + r] = Qg[r][col], Aqkt[j * 64 + i] = Aqk[i][j]
     const __bf16* qg = reinterpret_cast<const __bf16*>(ws + a.L.Qgt);
     const __bf16* aq = reinterpret_cast<const __bf16*>(ws + a.L.Aqkt);
@@ -1238,8 +1243,12 @@ __global__ __launch_bounds__(kOT) void out_kernel(const Args<IT> a) {
   const int rt = w & 3, ct = w >> 2;
   for (int s0 = 0; s0 < a.L.Vp; s0 += 32) {
     __syncthreads();  // the previous slab's reads are done
-    load_ws<KP, 32, kSS, kOT>(Ss, ws + a.L.S, a.L.Vp, s0, tid);
-    load_ws<kC, 32, kSS, kOT>(Vs, ws + a.L.Vt, a.L.Vp, s0, tid);
+    ts.template store<kSS>(Ss, tid);
+    tv.template store<kSS>(Vs, tid);
+    if (s0 + 32 < a.L.Vp) {
+      ts.fetch(ws + a.L.S, a.L.Vp, s0 + 32, tid);
+      tv.fetch(ws + a.L.Vt, a.L.Vp, s0 + 32, tid);
+    }
     __syncthreads();
     f32x4 acc = mma_long(zero4(), Mat{QgT, 1, kRC}, 16 * rt, Mat{Ss, kSS, 1}, 16 * ct, KP);
     acc = mma_long(acc, Mat{AqT, 1, kRC}, 16 * rt, Mat{Vs, kSS, 1}, 16 * ct, kC);
