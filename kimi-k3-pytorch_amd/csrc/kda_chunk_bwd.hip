@@ -422,10 +422,10 @@ __device__ __forceinline__ bool needs_exact(const float* lgS, bool nonneg, int t
 // q_i, for rows i in [r0, r0+16), columns j in [c0, c0+16) and r = lg[rr];
 // the reduction runs over the kd channels.
 __device__ __forceinline__ void decay_product(f32x4& accK, f32x4& accQ, const float* kS, const float* qS,
-                                              const float* lgS, int r0, int c0, int rr, int kd) {
+                                              const float* lgS, int r0, int c0, int rr, int kd, int kb = 0) {
   const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
   f32x4 accK2 = zero4(), accQ2 = zero4();  // odd steps: four chains instead of two
-  for (int k0 = 0; k0 < kd; k0 += 16) {
+  for (int k0 = kb; k0 < kb + kd; k0 += 16) {
     float ka[4], qa[4], kb[4];
 #pragma unroll
     for (int u = 0; u < 4; ++u) {
@@ -487,18 +487,42 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
   __syncthreads();
   const bool rising = chunk_cumsum<KP>(lgS, NS, tid);  // N is formed later
   if (!needs_exact<KP, kPT>(lgS, rising, tid)) {
-    // A and Aqk block by block on the MFMA
-    for (int p = w; p < 10; p += kPT / 64) {
-      int I, J;
-      block_pair(p, I, J);
-      f32x4 ak = zero4(), aq = zero4();
-      decay_product(ak, aq, kS, qS, lgS, 16 * I, 16 * J, 16 * I, Kp);
+    static_assert(kPT == 512 && kC * kRC >= 4096, "eight waves; the quarter partials fit in N's tile");
+    // A and Aqk block by block on the MFMA: pair w whole on wave w, and
+    // pairs 8 and 9 in four channel quarters (one per wave), parked over N's
+    // tile and summed in a fixed order after the barrier
+    int I, J;
+    block_pair(w, I, J);
+    f32x4 ak = zero4(), aq = zero4();
+    decay_product(ak, aq, kS, qS, lgS, 16 * I, 16 * J, 16 * I, Kp);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * I + 4 * lg4 + r, col = 16 * J + li;
+      if (col < row) AS[row * kRC + col] = ak[r];
+      if (col <= row) AqkS[row * kRC + col] = aq[r];
+    }
+    {
+      const int pq = w >> 2, qt = w & 3;  // pair 8 + pq, channel quarter qt
+      block_pair(8 + pq, I, J);
+      ak = zero4();
+      aq = zero4();
+      decay_product(ak, aq, kS, qS, lgS, 16 * I, 16 * J, 16 * I, Kp / 4, qt * (Kp / 4));
+      float* part = NS + (pq * 4 + qt) * 512;  // [pair][quarter][A | Aqk][16 x 16]
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
-        const int row = 16 * I + 4 * lg4 + r, col = 16 * J + li;
-        if (col < row) AS[row * kRC + col] = ak[r];
-        if (col <= row) AqkS[row * kRC + col] = aq[r];
+        part[(4 * lg4 + r) * 16 + li] = ak[r];
+        part[256 + (4 * lg4 + r) * 16 + li] = aq[r];
       }
+    }
+    __syncthreads();
+    for (int e = tid; e < 1024; e += kPT) {  // [pair][A | Aqk][16 x 16]
+      const int pq = e >> 9, m = (e >> 8) & 1, idx = e & 255;
+      const float* part = NS + pq * 2048 + m * 256 + idx;
+      const float x = ((part[0] + part[512]) + part[1024]) + part[1536];
+      block_pair(8 + pq, I, J);
+      const int row = 16 * I + (idx >> 4), col = 16 * J + (idx & 15);
+      if (m == 0 && col < row) AS[row * kRC + col] = x;
+      if (m == 1 && col <= row) AqkS[row * kRC + col] = x;
     }
   } else
   // A and Aqk with exact pair exponents, 2x2 blocks of (i, j <= i)
