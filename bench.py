@@ -67,10 +67,17 @@ BF16_PEAK_TFLOPS = 2500.0
 P_B, P_T, P_H, P_K, P_V = 1, 8192, 16, 128, 128
 # decode workload
 D_B, D_H, D_K, D_V, D_STEPS = 256, 32, 128, 128, 64
+# Untimed prefill launches before the headline's warm-up steps: the GPU's
+# clock ramps up over the first ~10 ms of sustained work (per-step times
+# fall from ~131 to ~123 us over the first ~100 prefills and climb back
+# after ~1 s idle), so a few warm-up steps leave every timed step on the ramp.
+SETTLE_MS = 50.0
 
 
 PREFILL_KERNELS = ("chunk_map_kernel", "chunk_segment_kernel<summary>", "segment_combine_kernel",
                    "chunk_segment_kernel<output>")
+BWD_KERNELS = ("bwd::prep_kernel", "bwd::seg_kernel<maps Q>", "bwd::seg_kernel<maps P>", "bwd::seg_combine_kernel",
+               "bwd::seg_kernel<run>", "bwd::grad_kernel", "bwd::pair_kernel")
 
 
 def prefill_bytes(B, T, H, K, V, n_state_io=2):
@@ -98,7 +105,22 @@ def _inputs(B, T, H, K, V, state_std, seed, device):
     return dev(q), dev(k), dev(v), dev(g), dev(beta), dev(state)
 
 
-def bench_prefill(steps, warmup, shape=(P_B, P_T, P_H, P_K, P_V)):
+def _settle(fn, ms=SETTLE_MS):
+    """Untimed calls of `fn` for `ms` milliseconds of sustained GPU work, so
+    that a leg's timed calls run at the settled clock.  Returns the count."""
+    import torch
+
+    n = 0
+    t0 = time.perf_counter()
+    while (time.perf_counter() - t0) * 1e3 < ms:
+        for _ in range(10):
+            fn()
+        torch.cuda.synchronize()
+        n += 10
+    return n
+
+
+def bench_prefill(steps, warmup, shape=(P_B, P_T, P_H, P_K, P_V), settle_ms=0.0):
     import torch
 
     from kda import _lib
@@ -121,6 +143,7 @@ def bench_prefill(steps, warmup, shape=(P_B, P_T, P_H, P_K, P_V)):
     def step():
         _lib.check(lib.kda_chunk_fwd(*args))
 
+    settle = {"ms": settle_ms, "launches": _settle(step, settle_ms) if settle_ms > 0 else 0}
     for _ in range(warmup):
         step()
     torch.cuda.synchronize()
@@ -143,6 +166,8 @@ def bench_prefill(steps, warmup, shape=(P_B, P_T, P_H, P_K, P_V)):
         for i in range(4):
             sums[i] += kms[i]
     per_kernel = {name: sums[i] / reps for i, name in enumerate(PREFILL_KERNELS)}
+    if settle_ms > 0:
+        return ms, per_kernel, ws_bytes, settle
     return ms, per_kernel, ws_bytes
 
 
@@ -322,6 +347,7 @@ def bench_backward(reps=10):
                                      *[t.data_ptr() for t in grads], ds0.data_ptr(), P_B, P_T, P_H, P_K, P_V,
                                      ws.data_ptr(), nbytes, stream))
 
+    _settle(call)
     for _ in range(2):
         call()
     torch.cuda.synchronize()
@@ -333,7 +359,7 @@ def bench_backward(reps=10):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
-    per_kernel = [measured_traffic(f"bwd::{k}_kernel") for k in ("prep", "scan", "grad", "pair")]
+    per_kernel = [measured_traffic(k) for k in BWD_KERNELS]
     traffic = None if None in per_kernel else sum(per_kernel)
     return {
         "workload": f"chunkwise backward B={P_B} T={P_T} H={P_H} K=V={P_K}, bf16 inputs, f32 arithmetic "
@@ -725,6 +751,7 @@ def bench_dropin(steps, warmup):
         return e0.elapsed_time(e1) / n
 
     with torch.no_grad():
+        _settle(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True))
         pre_ms = timed(lambda i: kda.chunkwise_kda(q, k, v, g, beta, s0, True), steps)
         dec_ms = timed(lambda i: kda.recurrent_kda(*steps_in[i % D_STEPS], state, True, update_state_in_place=True),
                        D_STEPS)
@@ -774,6 +801,7 @@ def bench_configs(steps, warmup):
         args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code, None,
                 s_out.data_ptr(), 0, o.data_ptr(), _lib.ptr(cu), T, None, n_seq, B * T, H, K, V, ws.data_ptr(),
                 ws_bytes, stream)
+        _settle(lambda: _lib.check(lib.kda_chunk_fwd(*args)))
         for _ in range(warmup):
             _lib.check(lib.kda_chunk_fwd(*args))
         torch.cuda.synchronize()
@@ -832,6 +860,7 @@ def bench_prefill_f32(steps, warmup):
     _lib.check(_lib.load().kda_chunk_fwd_plan(P_B, P_B * P_T, P_H, P_K, P_V, _lib.dtype_code(torch.float32),
                                               ctypes.byref(L), ctypes.byref(segs)))
     with torch.no_grad():
+        _settle(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True))
         split_ms = timed(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True), steps, warmup)
         rec_ms = timed(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True, cu_seqlens=[0, P_T]), 2, 1)
     nbytes = 2 * prefill_bytes(P_B, P_T, P_H, P_K, P_V, n_state_io=1)  # every tensor f32
@@ -889,7 +918,7 @@ def main() -> int:
         profile_pass()
         return 0
 
-    ms, per_kernel, ws_bytes = bench_prefill(args.steps, args.warmup)
+    ms, per_kernel, ws_bytes, settle = bench_prefill(args.steps, args.warmup, settle_ms=SETTLE_MS)
     dec_ms = bench_decode(args.warmup)
     counters = load_counters()
 
@@ -913,6 +942,9 @@ def main() -> int:
         "steps": args.steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms, 5),
+        "clock_settle": dict(settle, note="untimed prefill launches before the warm-up steps, so that the "
+                             "timed steps run at the GPU's settled clock (from a cold start the first ~100 "
+                             "prefills run up to 7% slower while the clock ramps)"),
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -968,7 +1000,8 @@ def main() -> int:
         "workload": f"B={P_B} T={P_T} H={P_H} D={P_K} bf16, 50 back-to-back C-ABI launches each",
         "kernels": bench_fused(),
     }
-    k64_ms, k64_kernels, _ = bench_prefill(args.steps, args.warmup, shape=(1, 8192, 16, 64, 64))
+    k64_ms, k64_kernels, _, _ = bench_prefill(args.steps, args.warmup, shape=(1, 8192, 16, 64, 64),
+                                              settle_ms=SETTLE_MS)
     k64_bytes = prefill_bytes(1, 8192, 16, 64, 64)
     result["prefill_k64"] = {
         "workload": "kda chunkwise prefill B=1 T=8192 H=16 K=V=64 bf16 (the gpu_48gb head shape), f32 state "
