@@ -1786,6 +1786,18 @@ __device__ __forceinline__ void pair_mfma(const Args<IT>& a, const float* ws, fl
       }
     }
   }
+  // the element's gradient pieces from the grad kernel: their loads go out
+  // now and land while R3 and R4 are formed
+  float gKg[CW][4], gKt[CW][4], gQg[CW][4];
+#pragma unroll
+  for (int ct = 0; ct < CW; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int64_t rec = static_cast<int64_t>(16 * J + 4 * lg4 + r) * KP + 16 * (ct0 + ct) + li;
+      gKg[ct][r] = ws[a.L.dKg + rec];
+      gKt[ct][r] = ws[a.L.dKt + rec];
+      gQg[ct][r] = ws[a.L.dQg + rec];
+    }
   for (int I = J; I < 4; ++I) {  // R3, R4 over rows i of block I >= J
 #pragma unroll
     for (int ct = 0; ct < CW; ++ct) {
@@ -1807,17 +1819,13 @@ __device__ __forceinline__ void pair_mfma(const Args<IT>& a, const float* ws, fl
       }
     }
   }
-  // the element's own inputs and gradient pieces, all loaded before any store
-  float kv[CW][4], qv[CW][4], lv[CW][4], gKg[CW][4], gKt[CW][4], gQg[CW][4];
+  // the element's own inputs, all read before any store
+  float kv[CW][4], qv[CW][4], lv[CW][4];
 #pragma unroll
   for (int ct = 0; ct < CW; ++ct)
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * J + 4 * lg4 + r, cc = 16 * (ct0 + ct) + li;
-      const int64_t rec = static_cast<int64_t>(row) * KP + cc;
-      gKg[ct][r] = ws[a.L.dKg + rec];
-      gKt[ct][r] = ws[a.L.dKt + rec];
-      gQg[ct][r] = ws[a.L.dQg + rec];
       kv[ct][r] = kS[row * kRS + cc];
       qv[ct][r] = qS[row * kRS + cc];
       lv[ct][r] = lgS[row * kRS + cc];
