@@ -193,6 +193,7 @@ def bench_decode(warmup):
                                        code, state.data_ptr(), state.data_ptr(), 0, out.data_ptr(),
                                        D_B, D_H, D_K, D_V, stream))
 
+    _settle(lambda: step(0))
     for t in range(warmup):
         step(t % D_STEPS)
     torch.cuda.synchronize()
@@ -246,6 +247,7 @@ def bench_fused(reps=50):
     }
     res = {}
     for name, (fn, nbytes) in cases.items():
+        _settle(lambda: _lib.check(fn()))
         for _ in range(3):
             _lib.check(fn())
         torch.cuda.synchronize()
@@ -305,6 +307,7 @@ def bench_decay_fusion(reps=20):
 
     res = {"workload": f"decay logits -> prefill B={P_B} T={P_T} H={P_H} K=V={P_K} bf16, f32 state"}
     for name, fn in (("gates_then_chunk_fwd", two_step), ("chunk_fwd_decay", fused)):
+        _settle(fn)
         for _ in range(3):
             fn()
         torch.cuda.synchronize()
@@ -411,6 +414,7 @@ def bench_cache(layers=8, reps=10):
 
     res = {}
     for name, fn in (("kda_cache_gather", native), ("torch_index_select_per_tensor", per_tensor)):
+        _settle(fn)
         for _ in range(2):
             fn()
         torch.cuda.synchronize()
