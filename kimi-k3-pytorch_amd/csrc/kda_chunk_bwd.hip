@@ -458,8 +458,8 @@ __device__ __forceinline__ void block_pair(int p, int& I, int& J) {
 constexpr int kPT = 512;  // threads of prep_kernel
 template <class IT, int KP>
 __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
-  __shared__ float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS];
-  __shared__ float AS[kC * kRC], AqkS[kC * kRC], NS[kC * kRC];
+  __shared__ __attribute__((aligned(16))) float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS];
+  __shared__ __attribute__((aligned(16))) float AS[kC * kRC], AqkS[kC * kRC], NS[kC * kRC];
   __shared__ float bS[kC];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   const int64_t ch = blockIdx.x;
@@ -571,9 +571,9 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
   // the records only the gradient kernels read (A, N, Kg, Kt row-major, W^T)
   // are skipped when the kernels serve the forward alone (no dO)
   const bool bwd_records = a.dout != nullptr;
-  for (int idx = tid; bwd_records && idx < kC * kC; idx += kPT) {  // A
-    const int r = idx >> 6, cc = idx & 63;
-    ws[a.L.A + idx] = AS[r * kRC + cc];
+  for (int i4 = tid; bwd_records && i4 < kC * kC / 4; i4 += kPT) {  // A, four at a time
+    const int r = (4 * i4) >> 6, cc = (4 * i4) & 63;
+    *reinterpret_cast<f32x4*>(ws + a.L.A + 4 * i4) = *reinterpret_cast<const f32x4*>(&AS[r * kRC + cc]);
   }
   for (int i8 = tid; i8 < kC * kC / 8; i8 += kPT) {  // Aqk^T split, eight positions at a time
     const int r = (8 * i8) >> 6, c0 = (8 * i8) & 63;
@@ -582,9 +582,14 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     for (int e = 0; e < 8; ++e) x[e] = AqkS[(c0 + e) * kRC + r];
     put_split8(ws + a.L.Aqkt, kC * kC, 8 * i8, x);
   }
-  for (int idx = tid; bwd_records && idx < kC * Kp; idx += kPT) {  // Kg (f32)
-    const int r = idx / Kp, col = idx % Kp;
-    ws[a.L.Kg + idx] = fast_exp(lgS[r * kRS + col]) * kS[r * kRS + col];
+  for (int i4 = tid; bwd_records && i4 < kC * Kp / 4; i4 += kPT) {  // Kg (f32), four at a time
+    const int r = (4 * i4) / Kp, col = (4 * i4) % Kp;
+    const f32x4 lg = *reinterpret_cast<const f32x4*>(&lgS[r * kRS + col]);
+    const f32x4 kk = *reinterpret_cast<const f32x4*>(&kS[r * kRS + col]);
+    f32x4 x;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = fast_exp(lg[e]) * kk[e];
+    *reinterpret_cast<f32x4*>(ws + a.L.Kg + 4 * i4) = x;
   }
   for (int i8 = tid; bwd_records && i8 < kC * Kp / 8; i8 += kPT) {  // Kt split, row-major
     const int r = (8 * i8) / Kp, c0 = (8 * i8) % Kp;
@@ -1202,8 +1207,8 @@ __device__ __forceinline__ void combine_body(const Args<IT>& a, int64_t id, floa
 
 template <class IT, int KP>
 __global__ __launch_bounds__(kCT) void seg_combine_kernel(const Args<IT> a) {
-  __shared__ float Ps[KP * (KP + 4)];
-  __shared__ float Xs[KP * 20];
+  __shared__ __attribute__((aligned(16))) float Ps[KP * (KP + 4)];
+  __shared__ __attribute__((aligned(16))) float Xs[KP * 20];
   const int64_t n = a.B * a.H * (a.L.Vp / 16);
   const int64_t id = blockIdx.x;
   if (a.dir0 == 0 && id < n)
@@ -1242,10 +1247,10 @@ __host__ __device__ inline int64_t seg_floats(int64_t K, int64_t V, int64_t bh, 
 constexpr int kOT = 512;  // threads of out_kernel: one 16 x 16 output tile per wave and slab
 template <class IT, int KP>
 __global__ __launch_bounds__(kOT) void out_kernel(const Args<IT> a) {
-  __shared__ float QgT[KP * kRC];  // Qg^T: channel-major, positions contiguous
-  __shared__ float AqT[kC * kRC];  // Aqk^T
-  __shared__ float Ss[KP * kSS];   // S slab [channel][32 columns]
-  __shared__ float Vs[kC * kSS];   // Vt slab [position][32 columns]
+  __shared__ __attribute__((aligned(16))) float QgT[KP * kRC];  // Qg^T: channel-major, positions contiguous
+  __shared__ __attribute__((aligned(16))) float AqT[kC * kRC];  // Aqk^T
+  __shared__ __attribute__((aligned(16))) float Ss[KP * kSS];   // S slab [channel][32 columns]
+  __shared__ __attribute__((aligned(16))) float Vs[kC * kSS];   // Vt slab [position][32 columns]
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
@@ -1433,7 +1438,7 @@ template <class IT, int KP>
 __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
   constexpr int NT = 512;
   constexpr int Kp = KP, CH = KP / 32;  // K-wide column tiles per wave
-  __shared__ float sm[kGradFloats];
+  __shared__ __attribute__((aligned(16))) float sm[kGradFloats];
   __shared__ float bS[kC];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   const int rt = w & 3, hf = w >> 2;  // wave w: row tile rt, half hf of the column tiles
@@ -1870,7 +1875,7 @@ __device__ __forceinline__ void pair_mfma(const Args<IT>& a, const float* ws, fl
 template <class IT, int KP, int NT>
 __global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
   static_assert(NT == 512, "the MFMA path uses eight waves");
-  __shared__ float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS], dAS[kC * kRC], dQS[kC * kRC];
+  __shared__ __attribute__((aligned(16))) float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS], dAS[kC * kRC], dQS[kC * kRC];
   __shared__ float red[16 * 128];
   const int tid = threadIdx.x;
   const int64_t ch = blockIdx.x;
