@@ -460,7 +460,7 @@ template <class IT, int KP>
 __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
   __shared__ __attribute__((aligned(16))) float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS];
   __shared__ __attribute__((aligned(16))) float AS[kC * kRC], AqkS[kC * kRC], NS[kC * kRC];
-  __shared__ float bS[kC];
+  __shared__ __attribute__((aligned(16))) float bS[kC];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
@@ -616,14 +616,20 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
   }
   if (tid < Kp) ws[a.L.D + tid] = fast_exp(lgS[(kC - 1) * kRS + tid]);
   __syncthreads();
-  for (int idx = tid; idx < kC * kC; idx += kPT) {  // L's strict part b_i A_ij over A; N cleared
-    const int r = idx >> 6, cc = idx & 63;
-    AS[r * kRC + cc] *= bS[r];
-    NS[r * kRC + cc] = 0.f;
+  for (int i4 = tid; i4 < kC * kC / 4; i4 += kPT) {  // L's strict part b_i A_ij over A; N cleared
+    const int r = (4 * i4) >> 6, cc = (4 * i4) & 63;
+    f32x4* ap = reinterpret_cast<f32x4*>(&AS[r * kRC + cc]);
+    *ap = *ap * bS[r];
+    *reinterpret_cast<f32x4*>(&NS[r * kRC + cc]) = zero4();
   }
-  for (int idx = tid; idx < kC * Kp; idx += kPT) {  // Kg over k: the B operand of W = M Kg
-    const int r = idx / Kp, col = idx % Kp;
-    kS[r * kRS + col] *= fast_exp(lgS[r * kRS + col]);
+  for (int i4 = tid; i4 < kC * Kp / 4; i4 += kPT) {  // Kg over k: the B operand of W = M Kg
+    const int r = (4 * i4) / Kp, col = (4 * i4) % Kp;
+    f32x4* kp = reinterpret_cast<f32x4*>(&kS[r * kRS + col]);
+    const f32x4 lg = *reinterpret_cast<const f32x4*>(&lgS[r * kRS + col]);
+    f32x4 x = *kp;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] *= fast_exp(lg[e]);
+    *kp = x;
   }
   __syncthreads();
   // v (into lg's rows once W is formed): its loads go out now and land while
@@ -668,11 +674,11 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     }
     __syncthreads();
   }
-  for (int idx = tid; idx < kC * kC; idx += kPT) {  // M = N diag(b) over A
-    const int r = idx >> 6, cc = idx & 63;
-    const float n = NS[r * kRC + cc];
-    if (bwd_records) ws[a.L.N + idx] = n;
-    AS[r * kRC + cc] = n * bS[cc];
+  for (int i4 = tid; i4 < kC * kC / 4; i4 += kPT) {  // M = N diag(b) over A, four at a time
+    const int r = (4 * i4) >> 6, cc = (4 * i4) & 63;
+    const f32x4 n = *reinterpret_cast<const f32x4*>(&NS[r * kRC + cc]);
+    if (bwd_records) *reinterpret_cast<f32x4*>(ws + a.L.N + 4 * i4) = n;
+    *reinterpret_cast<f32x4*>(&AS[r * kRC + cc]) = n * *reinterpret_cast<const f32x4*>(&bS[cc]);
   }
   __syncthreads();
   const int nkt = Kp / 16, nvt = Vp / 16;
