@@ -725,6 +725,36 @@ __device__ __forceinline__ void write_kt_frags(unsigned char* sm, const uint32_t
   }
 }
 
+// The part of P1 that only P2 and M read: the k a and q a tiles, the pair
+// scales, the extreme-decay flags and beta.  Phase A, whose state advance
+// reads none of them, writes it while the scanners advance the previous
+// chunk (p1_write_early); the other modes write it with the rest.
+template <int MODE>
+inline constexpr bool kEarlyP1 = MODE == kSummary;
+template <int MODE>
+__device__ __forceinline__ void p1_write_early(unsigned char* sm, const P1Out& po, int tid) {
+  const int J = loader_block(tid);
+  const int cp = loader_pair(tid);
+  float(*Sc)[kKey] = lds<float[kKey]>(sm, kOffTab);
+  float* betas = lds<float>(sm, kOffBeta);
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int tl = 16 * J + r;
+    *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKA, tl) + 2 * cp) = po.ka[r];
+    *reinterpret_cast<uint32_t*>(nat_row(sm, kOffQA, tl) + 2 * cp) = po.qa[r];
+  }
+#pragma unroll
+  for (int ch = 0; ch < 2; ++ch) {
+    const int cc = 2 * cp + ch;
+#pragma unroll
+    for (int jp = 0; jp < 4; ++jp)
+      if (jp <= J) Sc[J * (J + 1) / 2 + jp][cc] = po.sc[jp][ch];
+  }
+  if ((tid & 63) == 0) lds<int>(sm, kOffFlag)[wave_of(tid) - 4] = po.ext;
+  const int t2 = tid - 256;
+  if (t2 < kChunk) betas[t2] = po.bt;
+}
+
 // Writes P1 (loader waves) and joins every wave at the first barrier of the
 // chunk.
 template <int MODE, bool LOADER>
@@ -733,16 +763,13 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
     const int J = loader_block(tid);
     const int cp = loader_pair(tid);
     bf16(*KEt)[kRowT] = lds<bf16[kRowT]>(sm, kOffKEt);
-    float(*Sc)[kKey] = lds<float[kKey]>(sm, kOffTab);
     float(*Gs)[kKey] = lds<float[kKey]>(sm, kOffGs);
     float(*Ge)[kKey] = lds<float[kKey]>(sm, kOffGe);
     float* gam = lds<float>(sm, kOffGam);
-    float* betas = lds<float>(sm, kOffBeta);
+    if constexpr (!kEarlyP1<MODE>) p1_write_early<MODE>(sm, po, tid);
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int tl = 16 * J + r;
-      *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKA, tl) + 2 * cp) = po.ka[r];
-      *reinterpret_cast<uint32_t*>(nat_row(sm, kOffQA, tl) + 2 * cp) = po.qa[r];
       if constexpr (kPrepares<MODE>) *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKE, tl) + 2 * cp) = po.ke[r];
     }
     if constexpr (MODE == kSummary) {
@@ -770,16 +797,10 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
         Ge[J][cc] = po.ge[ch];
       }
       if (J == 0) gam[cc] = po.gam[ch];
-#pragma unroll
-      for (int jp = 0; jp < 4; ++jp)
-        if (jp <= J) Sc[J * (J + 1) / 2 + jp][cc] = po.sc[jp][ch];
     }
-    if ((tid & 63) == 0) lds<int>(sm, kOffFlag)[wave_of(tid) - 4] = po.ext;
 #pragma unroll
     for (int i = 0; i < 4; ++i)
       if (ll->vlds[i] >= 0) *reinterpret_cast<uint4*>(sm + kOffVn + ll->vlds[i]) = po.vv[i];
-    const int t2 = tid - 256;
-    if (t2 < kChunk) betas[t2] = po.bt;
   }
   __syncthreads();
 }
@@ -1606,6 +1627,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       const ChunkGeo g0 = chunk_geo(sr, c_begin - cs);
       load_raw<IT, MODE>(raw, chunk_loads<IT>(a, g0, c_begin, h, col0), ll, tid);
       p1_math<IT, MODE, DECAY>(po, raw, g0, vcg, tid, dc);
+      if constexpr (kEarlyP1<MODE>) p1_write_early<MODE>(sm, po, tid);
     }
     for (int64_t c = c_begin; c < c_end; ++c) {
       const ChunkGeo geo = chunk_geo(sr, c - cs);
@@ -1629,7 +1651,12 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
           }
         }
       }
-      if (c + 1 < c_end) p1_math<IT, MODE, DECAY>(po, raw, chunk_geo(sr, c + 1 - cs), vcg, tid_c, dc);
+      if (c + 1 < c_end) {
+        p1_math<IT, MODE, DECAY>(po, raw, chunk_geo(sr, c + 1 - cs), vcg, tid_c, dc);
+        // the k a and q a tiles, pair scales, flags and beta of chunk c + 1:
+        // P2 and M of chunk c are done, and the state advance reads none of them
+        if constexpr (kEarlyP1<MODE>) p1_write_early<MODE>(sm, po, tid_c);
+      }
       __syncthreads();
     }
   }
