@@ -133,7 +133,7 @@ def bench_prefill(steps, warmup, shape=(P_B, P_T, P_H, P_K, P_V), settle_ms=0.0)
     out = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=device)
     s_out = torch.empty(B, H, K, V, dtype=torch.float32, device=device)
     code = _lib.dtype_code(torch.bfloat16)
-    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(B, total, H, K, V, code)
+    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(B, total, 0, H, K, V, code)
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
     stream = torch.cuda.current_stream(device).cuda_stream
     args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code,
@@ -289,7 +289,7 @@ def bench_decay_fusion(reps=20):
     s1 = torch.empty(P_B, P_H, P_K, P_V, device=device)
     code = _lib.dtype_code(torch.bfloat16)
     total = P_B * P_T
-    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(P_B, total, P_H, P_K, P_V, code)
+    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(P_B, total, 0, P_H, P_K, P_V, code)
     ws = torch.empty(ws_bytes, dtype=torch.uint8, device=device)
     stream = _prep.stream(device)
     tail = (s0.data_ptr(), s1.data_ptr(), 0, out.data_ptr(), None, P_T, None, P_B, total, P_H, P_K, P_V,
@@ -800,10 +800,14 @@ def bench_configs(steps, warmup):
         o = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=device)
         s_out = torch.empty(n_seq, H, K, V, dtype=torch.float32, device=device)
         cu = None if offsets is None else torch.tensor(offsets, dtype=torch.int32, device=device)
-        ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, B * T, H, K, V, code)
+        # dense: tokens per sequence; packed documents: the longest document,
+        # which a caller that packs them knows (the schedule's hint)
+        span = T if offsets is None else max(b - a for a, b in zip(offsets[:-1], offsets[1:]))
+        longest = 0 if offsets is None else span
+        ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, B * T, longest, H, K, V, code)
         ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
         args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code, None,
-                s_out.data_ptr(), 0, o.data_ptr(), _lib.ptr(cu), T, None, n_seq, B * T, H, K, V, ws.data_ptr(),
+                s_out.data_ptr(), 0, o.data_ptr(), _lib.ptr(cu), span, None, n_seq, B * T, H, K, V, ws.data_ptr(),
                 ws_bytes, stream)
         _settle(lambda: _lib.check(lib.kda_chunk_fwd(*args)))
         for _ in range(warmup):
@@ -819,7 +823,7 @@ def bench_configs(steps, warmup):
         nbytes = 2 * B * T * H * (3 * K + V) + 2 * B * T * H + 2 * B * T * H * V + 4 * n_seq * H * K * V
         flops = prefill_flops(B, T, H, K, V)
         L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
-        _lib.check(lib.kda_chunk_fwd_plan(n_seq, B * T, H, K, V, code, ctypes.byref(L), ctypes.byref(segs)))
+        _lib.check(lib.kda_chunk_fwd_plan(n_seq, B * T, longest, H, K, V, code, ctypes.byref(L), ctypes.byref(segs)))
         out[name] = {
             "workload": f"kda chunkwise prefill B={B} T={T} H={H} K=V=128 bf16, zero initial state, "
                         + ("final state out" if offsets is None else f"cu_seqlens={offsets}, per-document final states"),
@@ -861,7 +865,7 @@ def bench_prefill_f32(steps, warmup):
         return e0.elapsed_time(e1) / n
 
     L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
-    _lib.check(_lib.load().kda_chunk_fwd_plan(P_B, P_B * P_T, P_H, P_K, P_V, _lib.dtype_code(torch.float32),
+    _lib.check(_lib.load().kda_chunk_fwd_plan(P_B, P_B * P_T, 0, P_H, P_K, P_V, _lib.dtype_code(torch.float32),
                                               ctypes.byref(L), ctypes.byref(segs)))
     with torch.no_grad():
         _settle(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True))
@@ -888,7 +892,7 @@ def prefill_plan():
     import torch
 
     L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
-    _lib.check(lib.kda_chunk_fwd_plan(P_B, P_B * P_T, P_H, P_K, P_V, _lib.dtype_code(torch.bfloat16),
+    _lib.check(lib.kda_chunk_fwd_plan(P_B, P_B * P_T, 0, P_H, P_K, P_V, _lib.dtype_code(torch.bfloat16),
                                       ctypes.byref(L), ctypes.byref(segs)))
     return {"chunks_per_segment": L.value, "segments": segs.value}
 

@@ -17,7 +17,12 @@
  * tokens each (sequence s owns rows [s*T, (s+1)*T)).  Otherwise
  * `cu_seqlens` is an int32 device array of N+1 monotone offsets (packed
  * documents; the state starts from zero or `initial_state[s]` at each
- * document start).  `valid_lens` (int32 device array [N], or NULL) marks a
+ * document start), and `dense_span` is then the longest document's length in
+ * tokens when the caller knows it, 0 otherwise: a scheduling hint only (the
+ * offsets live in device memory), which lets the chunk prefill cut a
+ * document far longer than the rest into segments instead of leaving the
+ * GPU to its one chain; results do not depend on it beyond rounding.
+ * `valid_lens` (int32 device array [N], or NULL) marks a
  * monotone right-padding: tokens at positions >= valid_lens[s] of sequence s
  * neither decay, write nor read the state and their output rows are zero
  * (src/kda/utils.py:82-94).
@@ -35,7 +40,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 7
+#define KDA_ABI_VERSION 8
 
 /* status codes */
 #define KDA_OK 0
@@ -91,25 +96,30 @@ int kda_decode_step(const void* q, const void* k, const void* v, const void* g,
 
 /*
  * Workspace bytes `kda_chunk_fwd` needs for these sizes (0 if none), for
- * dense sequences of total_tokens / num_seqs tokens; packed documents off the
- * MFMA path need none, and an f32-state call never needs more.
+ * dense sequences of total_tokens / num_seqs tokens (longest_tokens 0) or for
+ * packed documents whose longest is longest_tokens tokens (the value the call
+ * passes in `dense_span`; 0 when unknown); packed documents off the MFMA path
+ * need none, and an f32-state call never needs more.  0 for a longest_tokens
+ * outside 0..total_tokens.
  * No reference counterpart (the reference allocates per call).
  */
-size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads,
-                                     int64_t key_dim, int64_t value_dim, int in_dtype);
+size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t longest_tokens,
+                                     int64_t heads, int64_t key_dim, int64_t value_dim, int in_dtype);
 
 /*
  * The schedule `kda_chunk_fwd` picks for these sizes: *chunks_per_segment is
  * the number of 64-token chunks per segment (0 when every sequence is one
  * segment, -2 when the shape takes the split-bf16 chunk path for dense
  * sequences, -1 when it runs the exact recurrence kernel) and *segments
- * the bound on segments it sizes its workspace for.  No reference
+ * the bound on segments it sizes its workspace for; longest_tokens as for
+ * kda_chunk_fwd_workspace_bytes.  No reference
  * counterpart (the reference has one schedule, a Python loop over chunks,
  * src/kda/chunkwise.py:61-102); benchmarks and tests use it to attribute
  * time and to cover both schedules.
  */
-int kda_chunk_fwd_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
-                       int64_t value_dim, int in_dtype, int64_t* chunks_per_segment, int64_t* segments);
+int kda_chunk_fwd_plan(int64_t num_seqs, int64_t total_tokens, int64_t longest_tokens, int64_t heads,
+                       int64_t key_dim, int64_t value_dim, int in_dtype, int64_t* chunks_per_segment,
+                       int64_t* segments);
 
 /*
  * Chunkwise-parallel KDA prefill (chunk 64): intra-chunk UT transform with a

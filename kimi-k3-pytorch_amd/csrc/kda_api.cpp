@@ -71,6 +71,11 @@ static int check_seq(const int32_t* cu_seqlens, int64_t dense_span, int64_t num_
                  (long long)dense_span, (long long)num_seqs, (long long)total_tokens);
       return KDA_ERR_INVALID_ARGUMENT;
     }
+  } else if (dense_span < 0 || dense_span > total_tokens) {
+    // packed documents: dense_span is the longest document (0 when unknown)
+    set_detail("packed documents take the longest document's length (0 if unknown) in dense_span, got %lld of %lld",
+               (long long)dense_span, (long long)total_tokens);
+    return KDA_ERR_INVALID_ARGUMENT;
   }
   if (total_tokens > 0x7fffffffLL) {
     set_detail("total_tokens %lld exceeds int32 offsets", (long long)total_tokens);
@@ -138,24 +143,27 @@ int kda_decode_step(const void* q, const void* k, const void* v, const void* g, 
                           heads, key_dim, value_dim, static_cast<hipStream_t>(stream), true);
 }
 
-size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
-                                     int64_t value_dim, int in_dtype) {
-  return chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype);
+size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t longest_tokens, int64_t heads,
+                                     int64_t key_dim, int64_t value_dim, int in_dtype) {
+  if (longest_tokens < 0 || longest_tokens > total_tokens) return 0;
+  return chunk_workspace_bytes(num_seqs, total_tokens, longest_tokens, heads, key_dim, value_dim, in_dtype);
 }
 
-int kda_chunk_fwd_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
-                       int in_dtype, int64_t* chunks_per_segment, int64_t* segments) {
+int kda_chunk_fwd_plan(int64_t num_seqs, int64_t total_tokens, int64_t longest_tokens, int64_t heads,
+                       int64_t key_dim, int64_t value_dim, int in_dtype, int64_t* chunks_per_segment,
+                       int64_t* segments) {
   g_detail[0] = '\0';
   if (!chunks_per_segment || !segments) {
     set_detail("chunk_fwd_plan: output pointers must be non-null");
     return KDA_ERR_INVALID_ARGUMENT;
   }
   if (!is_input_dtype(in_dtype) || num_seqs <= 0 || total_tokens <= 0 || heads <= 0 || key_dim <= 0 ||
-      value_dim <= 0) {
+      value_dim <= 0 || longest_tokens < 0 || longest_tokens > total_tokens) {
     set_detail("chunk_fwd_plan: bad sizes or dtype");
     return KDA_ERR_INVALID_ARGUMENT;
   }
-  chunk_plan(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype, chunks_per_segment, segments);
+  chunk_plan(num_seqs, total_tokens, longest_tokens, heads, key_dim, value_dim, in_dtype, chunks_per_segment,
+             segments);
   return KDA_OK;
 }
 
@@ -201,9 +209,11 @@ int kda_chunk_fwd_decay(const void* q, const void* k, const void* v, const void*
   }
   kda::SeqDesc seq{cu_seqlens, dense_span, valid_lens};
   int64_t per_segment = 0, segments = 0;  // off the MFMA path the launcher reports the shape unsupported
-  chunk_plan(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype, &per_segment, &segments);
-  const size_t need =
-      per_segment >= 0 ? chunk_workspace_bytes(num_seqs, total_tokens, heads, key_dim, value_dim, in_dtype) : 0;
+  const int64_t longest = cu_seqlens != nullptr ? dense_span : 0;
+  chunk_plan(num_seqs, total_tokens, longest, heads, key_dim, value_dim, in_dtype, &per_segment, &segments);
+  const size_t need = per_segment >= 0 ? chunk_workspace_bytes(num_seqs, total_tokens, longest, heads, key_dim,
+                                                               value_dim, in_dtype)
+                                       : 0;
   if (need > 0 && (workspace == nullptr || workspace_bytes < need)) {
     set_detail("chunk_fwd_decay needs %zu workspace bytes, got %zu", need, workspace_bytes);
     return KDA_ERR_WORKSPACE;

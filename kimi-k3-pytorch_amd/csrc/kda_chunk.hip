@@ -1837,7 +1837,14 @@ static int64_t segment_override() {
   return v < 0 ? -1 : v;
 }
 
-static Plan make_plan(int64_t N, int64_t total_tokens, int64_t H, int64_t V) {
+// `longest` (packed documents only, 0 when unknown): the longest document in
+// tokens.  Documents of uneven length that alone fill the GPU would leave it
+// idle while the longest runs on (one workgroup per document and head): when
+// the longest document is well past the chunk-steps per CU of a balanced
+// pass, every document is cut into segments of that many chunks (short ones
+// stay one segment), which spreads the long chains over the CUs the short
+// documents free.
+static Plan make_plan(int64_t N, int64_t total_tokens, int64_t H, int64_t V, int64_t longest) {
   Plan p;
   p.ncg = (V + kColGroup - 1) / kColGroup;
   const int64_t cus = device_cus();
@@ -1851,7 +1858,14 @@ static Plan make_plan(int64_t N, int64_t total_tokens, int64_t H, int64_t V) {
     p.segs_bound = chunks_bound / p.L + N + 1;
     return p;
   }
-  if (forced == 0 || N * H * p.ncg * 4 >= cus * 3 || work < 2 * cus) {
+  const int64_t per_cu = (work + cus - 1) / cus;  // chunk-steps per CU of a balanced pass
+  const int64_t longest_chunks = (longest + kChunk - 1) / kChunk;
+  const bool uneven = forced != 0 && N > 1 && per_cu >= 2 && 4 * longest_chunks > 5 * per_cu;
+  if (uneven && work >= 2 * cus) {
+    p.L = static_cast<int32_t>(per_cu < kOneSegment ? per_cu : kOneSegment - 1);
+    p.segmented = true;
+    p.segs_bound = chunks_bound / p.L + N + 1;
+  } else if (forced == 0 || N * H * p.ncg * 4 >= cus * 3 || work < 2 * cus) {
     p.L = kOneSegment;
     p.segmented = false;
     p.segs_bound = N;
@@ -1864,6 +1878,10 @@ static Plan make_plan(int64_t N, int64_t total_tokens, int64_t H, int64_t V) {
   }
   return p;
 }
+
+// The scheduling hint of a call: packed documents carry the longest
+// document's length in `dense_span` (0 when the caller does not know it).
+inline int64_t plan_longest(const SeqDesc& seq) { return seq.cu_seqlens != nullptr ? seq.dense_span : 0; }
 
 static size_t map_bytes(int64_t N) { return static_cast<size_t>(((2 * (N + 1)) * 4 + 255) / 256 * 256); }
 
@@ -1910,7 +1928,7 @@ static int run_chunk_k(const void* q, const void* k, const void* v, const void* 
                      void* s_out, void* out, const SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
                      int64_t K, int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev,
                      const DecayInput* decay) {
-  const Plan p = make_plan(N, total_tokens, H, V);
+  const Plan p = make_plan(N, total_tokens, H, V, plan_longest(seq));
   int32_t* chunk_start = static_cast<int32_t*>(workspace);
   int32_t* seg_start = chunk_start + (N + 1);
   unsigned char* segbuf = static_cast<unsigned char*>(workspace) + map_bytes(N);
@@ -2006,8 +2024,8 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
 
 namespace kda_host {
 
-void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
-                int in_dtype, int64_t* chunks_per_segment, int64_t* segments) {
+void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t longest, int64_t heads, int64_t key_dim,
+                int64_t value_dim, int in_dtype, int64_t* chunks_per_segment, int64_t* segments) {
   if (!kda::mfma_path(in_dtype, in_dtype == KDA_DTYPE_F64 ? KDA_DTYPE_F64 : KDA_DTYPE_F32, key_dim, value_dim)) {
     // dense sequences take the split-bf16 chunk path where it applies (-2),
     // everything else the exact recurrence kernel (-1)
@@ -2015,20 +2033,20 @@ void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t k
     *segments = num_seqs;
     return;
   }
-  const kda::Plan p = kda::make_plan(num_seqs, total_tokens, heads, value_dim);
+  const kda::Plan p = kda::make_plan(num_seqs, total_tokens, heads, value_dim, longest);
   *chunks_per_segment = p.segmented ? p.L : 0;
   *segments = p.segs_bound;
 }
 
-size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
-                             int64_t value_dim, int in_dtype) {
+size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t longest, int64_t heads,
+                             int64_t key_dim, int64_t value_dim, int in_dtype) {
   if (!kda::mfma_path(in_dtype, in_dtype == KDA_DTYPE_F64 ? KDA_DTYPE_F64 : KDA_DTYPE_F32, key_dim, value_dim)) {
     // sized for a dense call (num_seqs rows of total_tokens / num_seqs tokens)
     // on the split-bf16 chunk path; the recurrence kernel needs none
     if (!chunk_split_path(in_dtype, KDA_DTYPE_F32, key_dim, value_dim) || num_seqs <= 0) return 0;
     return chunk_split_workspace_bytes(num_seqs, (total_tokens + num_seqs - 1) / num_seqs, heads, key_dim, value_dim);
   }
-  const kda::Plan p = kda::make_plan(num_seqs, total_tokens, heads, value_dim);
+  const kda::Plan p = kda::make_plan(num_seqs, total_tokens, heads, value_dim, longest);
   return kda::map_bytes(num_seqs) + kda::segment_bytes(p, heads, value_dim);
 }
 
@@ -2042,7 +2060,8 @@ static bool split_call(const kda::SeqDesc& seq, int64_t N, int64_t total_tokens,
 
 size_t chunk_call_workspace_bytes(const kda::SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H, int64_t K,
                                   int64_t V, int in_dtype, int state_dtype) {
-  if (kda::mfma_path(in_dtype, state_dtype, K, V)) return chunk_workspace_bytes(N, total_tokens, H, K, V, in_dtype);
+  if (kda::mfma_path(in_dtype, state_dtype, K, V))
+    return chunk_workspace_bytes(N, total_tokens, kda::plan_longest(seq), H, K, V, in_dtype);
   if (split_call(seq, N, total_tokens, in_dtype, state_dtype, K, V))
     return chunk_split_workspace_bytes(N, seq.dense_span, H, K, V);
   return 0;
@@ -2069,11 +2088,11 @@ int launch_chunk(const void* q, const void* k, const void* v, const void* g, con
     mark(ev, 1, stream);
     return st;
   }
-  if (workspace_bytes < chunk_workspace_bytes(N, total_tokens, H, K, V, in_dtype)) {
+  if (workspace_bytes < chunk_workspace_bytes(N, total_tokens, plan_longest(seq), H, K, V, in_dtype)) {
     set_detail("chunk_fwd: workspace too small");
     return KDA_ERR_WORKSPACE;
   }
-  const Plan p = make_plan(N, total_tokens, H, V);
+  const Plan p = make_plan(N, total_tokens, H, V, plan_longest(seq));
   if (H > 65535 || p.segs_bound * H * p.ncg > 0x7fffffffLL || N > 0x7fffffffLL) {
     set_detail("chunk_fwd: grid too large (N=%lld, H=%lld)", (long long)N, (long long)H);
     return KDA_ERR_UNSUPPORTED;
@@ -2095,11 +2114,11 @@ int launch_chunk_decay(const void* q, const void* k, const void* v, const void* 
                "V a multiple of 16 in 16..256); form g with kda_gates_fwd and call kda_chunk_fwd");
     return KDA_ERR_UNSUPPORTED;
   }
-  if (workspace_bytes < chunk_workspace_bytes(N, total_tokens, H, K, V, in_dtype)) {
+  if (workspace_bytes < chunk_workspace_bytes(N, total_tokens, plan_longest(seq), H, K, V, in_dtype)) {
     set_detail("chunk_fwd_decay: workspace too small");
     return KDA_ERR_WORKSPACE;
   }
-  const Plan p = make_plan(N, total_tokens, H, V);
+  const Plan p = make_plan(N, total_tokens, H, V, plan_longest(seq));
   if (H > 65535 || p.segs_bound * H * p.ncg > 0x7fffffffLL || N > 0x7fffffffLL) {
     set_detail("chunk_fwd_decay: grid too large (N=%lld, H=%lld)", (long long)N, (long long)H);
     return KDA_ERR_UNSUPPORTED;

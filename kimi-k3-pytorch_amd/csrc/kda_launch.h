@@ -15,13 +15,15 @@ int launch_recurrent(const void* q, const void* k, const void* v, const void* g,
                      const kda::SeqDesc& seq, int64_t N, int64_t H, int64_t K, int64_t V, hipStream_t stream,
                      bool streaming_state);
 
-size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim,
-                             int64_t value_dim, int in_dtype);
+// `longest`: the longest packed document in tokens (0 for dense sequences or
+// when unknown), the scheduling hint of make_plan.
+size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t longest, int64_t heads,
+                             int64_t key_dim, int64_t value_dim, int in_dtype);
 
 // The schedule launch_chunk picks: chunks per segment (0: one segment per
 // sequence; -1: the exact recurrence kernel) and the bound on segments.
-void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
-                int in_dtype, int64_t* chunks_per_segment, int64_t* segments);
+void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t longest, int64_t heads, int64_t key_dim,
+                int64_t value_dim, int in_dtype, int64_t* chunks_per_segment, int64_t* segments);
 
 // Optional per-kernel timing: events[i] is recorded before kernel i and
 // events[n] after the last one; *n_launched receives n.  Bit i of `empty`

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libkda_mi355x.so")
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 KDA_OK = 0
 KDA_ERR_INVALID_ARGUMENT = 1
@@ -45,8 +45,8 @@ SIGNATURES = {
         [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P],
     ),
     "kda_decode_step": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _L, _L, _L, _L, _P]),
-    "kda_chunk_fwd_workspace_bytes": (_S, [_L, _L, _L, _L, _L, _I]),
-    "kda_chunk_fwd_plan": (_I, [_L, _L, _L, _L, _L, _I, _P, _P]),
+    "kda_chunk_fwd_workspace_bytes": (_S, [_L, _L, _L, _L, _L, _L, _I]),
+    "kda_chunk_fwd_plan": (_I, [_L, _L, _L, _L, _L, _L, _I, _P, _P]),
     "kda_chunk_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P, _S, _P],

@@ -68,5 +68,14 @@ def cu_tensor(offsets: list[int], device: torch.device) -> torch.Tensor:
     return torch.tensor(offsets, dtype=torch.int32, device=device)
 
 
+def longest_document(offsets: list[int] | None) -> int:
+    """Tokens of the longest packed document (0 for dense sequences): the
+    chunk prefill's scheduling hint, passed in the C ABI's `dense_span` and
+    `longest_tokens` for packed documents."""
+    if offsets is None:
+        return 0
+    return max(b - a for a, b in zip(offsets[:-1], offsets[1:]))
+
+
 def stream(device: torch.device) -> int:
     return _lib.stream_of(device)

@@ -89,12 +89,15 @@ def _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask
     cu = None if offsets is None else _prep.cu_tensor(offsets, device)
     valid = _prep.valid_lengths(attention_mask, device)
     code = _lib.dtype_code(kernel_dtype)
-    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, total, heads, key_dim, value_dim, code)
+    # packed documents: the longest document's length is the schedule's hint
+    longest = _prep.longest_document(offsets)
+    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, total, longest, heads, key_dim, value_dim, code)
     workspace = _prep.workspace(ws_bytes, device, "chunkwise_kda")
     status = lib.kda_chunk_fwd(
         qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr(), bc.data_ptr(), code,
         _lib.ptr(s_in), _lib.ptr(s_out), _lib.dtype_code(arith), out.data_ptr(),
-        _lib.ptr(cu), tokens, _lib.ptr(valid), n_seq, total, heads, key_dim, value_dim,
+        _lib.ptr(cu), tokens if offsets is None else longest, _lib.ptr(valid), n_seq, total, heads, key_dim,
+        value_dim,
         _lib.ptr(workspace), ws_bytes, _prep.stream(device),
     )
     _lib.check(status)

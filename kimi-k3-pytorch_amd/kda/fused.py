@@ -393,13 +393,14 @@ def chunkwise_kda_with_decay(
     cu = None if offsets is None else _prep.cu_tensor(offsets, device)
     valid = _prep.valid_lengths(attention_mask, device)
     code = _lib.dtype_code(q.dtype)
-    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, total, heads, key_dim, value_dim, code)
+    longest = _prep.longest_document(offsets)
+    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, total, longest, heads, key_dim, value_dim, code)
     workspace = _prep.workspace(ws_bytes, device, "chunkwise_kda_with_decay")
     _lib.check(lib.kda_chunk_fwd_decay(
         qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), zc.data_ptr(), _lib.ptr(zb), al.data_ptr(), float(g_min),
         bc.data_ptr(), code, _lib.ptr(s_in), _lib.ptr(s_out), _lib.dtype_code(torch.float32), out.data_ptr(),
-        _lib.ptr(cu), tokens, _lib.ptr(valid), n_seq, total, heads, key_dim, value_dim, _lib.ptr(workspace),
-        ws_bytes, _prep.stream(device)))
+        _lib.ptr(cu), tokens if offsets is None else longest, _lib.ptr(valid), n_seq, total, heads, key_dim,
+        value_dim, _lib.ptr(workspace), ws_bytes, _prep.stream(device)))
     hidden = out if out.dtype == v.dtype else out.to(v.dtype)
     return KDAOperatorOutput(hidden_states=hidden, final_state=s_out)
 

@@ -61,6 +61,39 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert status == _lib.KDA_ERR_INVALID_ARGUMENT
 
 
+def test_plan_cuts_a_dominant_packed_document():
+    """Packed documents that fill the GPU with one chain per (document, head)
+    keep one segment each, unless the longest document (the caller's hint)
+    would run well past a balanced pass: then every document is cut into
+    segments of the balanced pass's chunk-steps per CU.  Without a GPU the
+    planner assumes 256 CUs (the MI355X count)."""
+    lib = _lib.load()
+    code = _lib.dtype_code(__import__("torch").bfloat16)
+
+    def plan(n, total, longest, heads):
+        cps, segs = ctypes.c_int64(0), ctypes.c_int64(0)
+        _lib.check(lib.kda_chunk_fwd_plan(n, total, longest, heads, 128, 128, code, ctypes.byref(cps),
+                                          ctypes.byref(segs)))
+        return cps.value
+
+    # cu_seqlens = [0, 32768, 49152, 61440, 65536] at H=64: 256 chains of which
+    # 64 run 512 chunks, against 256 chunk-steps per CU for a balanced pass
+    assert plan(4, 65536, 32768, 64) == 256
+    assert plan(4, 65536, 0, 64) == 0  # no hint: one segment per document
+    assert plan(4, 65536, 16384, 64) == 0  # four equal documents are already balanced
+    assert plan(4, 65536, 20000, 64) == 0  # within a quarter of balanced
+    # dense sequences ignore the hint argument's absence (0) and keep their plan
+    assert plan(1, 8192, 0, 16) == 8
+    more = lib.kda_chunk_fwd_workspace_bytes(4, 65536, 32768, 64, 128, 128, code)
+    assert more > lib.kda_chunk_fwd_workspace_bytes(4, 65536, 0, 64, 128, 128, code)
+    assert lib.kda_chunk_fwd_workspace_bytes(4, 65536, 65537, 64, 128, 128, code) == 0
+    # a hint past the packed tokens is an invalid argument, rejected before any launch
+    status = lib.kda_chunk_fwd(1, 1, 1, 1, 1, code, None, None, 0, 1, 1, 70000, None, 4, 65536, 64, 128, 128, None,
+                               0, None)
+    assert status == _lib.KDA_ERR_INVALID_ARGUMENT
+    assert "longest document" in lib.kda_status_string(status).decode()
+
+
 def declared_arities() -> dict[str, int]:
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     out = {}

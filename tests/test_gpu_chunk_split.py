@@ -33,7 +33,7 @@ def _dev(*ts):
 
 def _plan(B, T, H, K, V, dtype):
     L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
-    _lib.check(_lib.load().kda_chunk_fwd_plan(B, B * T, H, K, V, _lib.dtype_code(dtype), ctypes.byref(L),
+    _lib.check(_lib.load().kda_chunk_fwd_plan(B, B * T, 0, H, K, V, _lib.dtype_code(dtype), ctypes.byref(L),
                                               ctypes.byref(segs)))
     return L.value
 
@@ -147,7 +147,7 @@ def test_split_path_equals_the_recurrence_kernel():
     for packed in (False, True):
         out = torch.empty(B, T, H, V, device=DEV)
         s_out = torch.empty(B, H, K, V, device=DEV)
-        n = 0 if packed else lib.kda_chunk_fwd_workspace_bytes(B, B * T, H, K, V, code)
+        n = 0 if packed else lib.kda_chunk_fwd_workspace_bytes(B, B * T, 0, H, K, V, code)
         ws = torch.empty(n, dtype=torch.uint8, device=DEV) if n else None
         _lib.check(lib.kda_chunk_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code,
                                      state.data_ptr(), s_out.data_ptr(), code, out.data_ptr(),

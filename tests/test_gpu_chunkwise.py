@@ -112,6 +112,36 @@ def test_chunkwise_varlen_matches_per_document():
         assert rel_err(got.final_state[d:d + 1], solo.final_state) < 1e-6
 
 
+def test_chunkwise_dominant_document_is_cut_into_segments():
+    # three documents at H=64 fill the GPU with one chain per (document, head),
+    # and the first is eight times longer than the others: with the longest
+    # document as the schedule's hint every document is cut into segments
+    # (the plan asserted below); results equal independent per-document calls
+    import ctypes
+
+    from kda import _lib
+
+    cu = [0, 2048, 2304, 2560]
+    H = 64
+    q, k, v, g, beta, _ = workload(1, cu[-1], H, 128, 128, seed=61)
+    init = torch.randn(3, H, 128, 128, generator=torch.Generator().manual_seed(62)) * 0.02
+    cps, segs = ctypes.c_int64(0), ctypes.c_int64(0)
+    _lib.check(_lib.load().kda_chunk_fwd_plan(3, cu[-1], 2048, H, 128, 128, _lib.dtype_code(torch.bfloat16),
+                                              ctypes.byref(cps), ctypes.byref(segs)))
+    assert cps.value > 0  # segmented; without the hint the plan keeps one segment per document
+    got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, init), True, cu_seqlens=cu)
+    for d, (a, b) in enumerate(zip(cu[:-1], cu[1:])):
+        solo = kda.chunkwise_kda(*_dev(q[:, a:b], k[:, a:b], v[:, a:b], g[:, a:b], beta[:, a:b], init[d:d + 1]),
+                                 True)
+        assert rel_err(got.hidden_states[:, a:b], solo.hidden_states) < 1e-2, d
+        assert rel_err(got.final_state[d:d + 1], solo.final_state) < 1e-2, d
+    # two heads of the long document against the oracle
+    hs = [0, 37]
+    ro, rs = _oracle_f32(*(t[:, :2048, hs] for t in (q, k, v, g, beta)), init[0:1, hs])
+    _check(type(got)(hidden_states=got.hidden_states[:, :2048, hs], final_state=got.final_state[0:1, hs]), ro, rs,
+           label="dominant document")
+
+
 def test_chunkwise_extreme_decay_takes_exact_path():
     # g = -4.999 everywhere: a 16-row block decays by e^-75 < 2^-100, so the
     # diagonal blocks use the exact pairwise-exponent path
@@ -203,7 +233,7 @@ def _plan(B, T, H, K, V, dtype=torch.bfloat16):
     from kda import _lib
 
     L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
-    _lib.check(_lib.load().kda_chunk_fwd_plan(B, B * T, H, K, V, _lib.dtype_code(dtype), ctypes.byref(L),
+    _lib.check(_lib.load().kda_chunk_fwd_plan(B, B * T, 0, H, K, V, _lib.dtype_code(dtype), ctypes.byref(L),
                                               ctypes.byref(segs)))
     return L.value
 

@@ -18,10 +18,13 @@ call and separate calls (the same kernels on the same values).
 
 from __future__ import annotations
 
+import ctypes
+
 import pytest
 import torch
 
 import kda
+from kda import _lib
 from oracle import kda_oracle as ora
 from tests._inputs import rel_err, workload
 
@@ -61,6 +64,11 @@ def test_prefill_packed_documents_h64_full_size(monkeypatch):
     cu_t = torch.tensor(cu, dtype=torch.int32, device=DEV)
     got = kda.chunkwise_kda(q, k, v, g, beta, None, True, cu_seqlens=cu_t)
     assert got.final_state.shape == (len(cu) - 1, H, K, V)
+    cps, segs = ctypes.c_int64(0), ctypes.c_int64(0)
+    _lib.check(_lib.load().kda_chunk_fwd_plan(len(cu) - 1, cu[-1], 32768, H, K, V, _lib.dtype_code(torch.bfloat16),
+                                              ctypes.byref(cps), ctypes.byref(segs)))
+    per_segment = cps.value
+    assert per_segment > 0
     heads = [0, 31, 63]
     for d in range(len(cu) - 1):
         s0, s1 = cu[d], cu[d + 1]
@@ -72,10 +80,12 @@ def test_prefill_packed_documents_h64_full_size(monkeypatch):
         es = rel_err(got.final_state[d:d + 1, heads], rs)
         print(f"document {d} ({s1 - s0} tokens): output rel err {eo:.2e} state rel err {es:.2e}")
         assert eo < TOL16 and es < TOL16
-        # the packed call equals a separate call on the document (all heads);
-        # 4 sequences x 64 heads fill the GPU, so the packed call runs one
-        # segment per sequence, and the separate call is held to that schedule
-        monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "0")
+        # the packed call equals a separate call on the document (all heads)
+        # held to the packed call's schedule: 4 documents x 64 heads fill the
+        # GPU, and the first document, twice the chunk-steps per CU of a
+        # balanced pass, has every document cut into segments of that many
+        # chunks (the library's plan for the longest document's hint)
+        monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", str(per_segment))
         alone = kda.chunkwise_kda(q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], g[:, s0:s1], beta[:, s0:s1], None, True)
         monkeypatch.delenv("KDA_MI355X_SEGMENT_CHUNKS")
         assert rel_err(got.hidden_states[:, s0:s1], alone.hidden_states) < 1e-6

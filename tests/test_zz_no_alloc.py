@@ -29,6 +29,8 @@ def _run(lib, noalloc, shape, seed, cu=None):
         s0 = torch.randn(len(cu) - 1, H, K, V, generator=torch.Generator().manual_seed(seed)).mul_(0.02).to(DEV)
     n_seq = B if cu is None else len(cu) - 1
     cu_t = None if cu is None else torch.tensor(cu, dtype=torch.int32, device=DEV)
+    # dense: tokens per sequence; packed documents: the longest document (the schedule's hint)
+    span = T if cu is None else max(b - a for a, b in zip(cu[:-1], cu[1:]))
     code = _lib.dtype_code(torch.bfloat16)
     stream = torch.cuda.current_stream(DEV).cuda_stream
     outs = []
@@ -36,11 +38,11 @@ def _run(lib, noalloc, shape, seed, cu=None):
         out = torch.full((B, T, H, V), float("nan"), dtype=torch.bfloat16, device=DEV)
         s1 = torch.full((n_seq, H, K, V), float("nan"), dtype=torch.float32, device=DEV)
         common = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code, s0.data_ptr(),
-                  s1.data_ptr(), 0, out.data_ptr(), _lib.ptr(cu_t), T, None, n_seq, B * T, H, K, V)
+                  s1.data_ptr(), 0, out.data_ptr(), _lib.ptr(cu_t), span, None, n_seq, B * T, H, K, V)
         if use_noalloc:
             _lib.check(noalloc(*common, stream))
         else:
-            ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, B * T, H, K, V, code)
+            ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, B * T, 0 if cu is None else span, H, K, V, code)
             ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=DEV)
             _lib.check(lib.kda_chunk_fwd(*common, ws.data_ptr(), ws_bytes, stream))
         torch.cuda.synchronize()
@@ -68,7 +70,7 @@ def test_noalloc_refuses_a_prefill_beyond_the_scratch():
     code = _lib.dtype_code(torch.bfloat16)
     # one 262144-token sequence at H=16 needs far more than the 128 MiB scratch;
     # the size check rejects it before any pointer is touched or kernel launched
-    need = lib.kda_chunk_fwd_workspace_bytes(1, 262144, 16, 128, 128, code)
+    need = lib.kda_chunk_fwd_workspace_bytes(1, 262144, 0, 16, 128, 128, code)
     assert need > _lib.NOALLOC_SCRATCH_BYTES
     status = noalloc(1, 1, 1, 1, 1, code, None, None, 0, 1, None, 262144, None, 1, 262144, 16, 128, 128,
                      torch.cuda.current_stream(DEV).cuda_stream)
