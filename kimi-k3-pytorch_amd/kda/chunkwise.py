@@ -19,15 +19,18 @@ goes through ``_ChunkwiseFunction``, whose backward is the HIP chunk backward
 inputs) with key_dim and value_dim <= 128;
 the attention mask is applied with differentiable tensor ops first
 (src/kda/utils.py:82-94), so padded positions get zero gradients.  Packed
-documents (``cu_seqlens``) are differentiated one document at a time: each is
-a dense batch-1 call on its slice of the packed tensors (pointer offsets into
-the same inputs and gradient buffers, one workspace sized for the longest
-document).  Other cases raise instead of dropping gradients, and so does a
-second derivative (the backward is marked once-differentiable).
+documents (``cu_seqlens``) are differentiated in buckets of similar length:
+documents within a fifth of the bucket's longest are stacked into one
+zero-padded dense batch (zero rows are identity steps of the recurrence), a
+lone document runs on its slice of the packed tensors in place, and each
+bucket's workspace stays within max(the longest document's, 1 GiB).  Other
+cases raise instead of dropping gradients, and so does a second derivative
+(the backward is marked once-differentiable).
 """
 
 from __future__ import annotations
 
+import numpy as np
 import torch
 
 from . import _lib, _prep
@@ -137,6 +140,78 @@ def _mask_differentiable(q, g, beta, attention_mask):
             torch.where(keep[:, :, None], beta, torch.zeros((), dtype=beta.dtype, device=beta.device)))
 
 
+def _document_buckets(lengths: list[int], fits) -> list[list[int]]:
+    """Documents (indices) grouped for the backward: sorted by length, each
+    bucket takes the longest remaining document and every next one at least
+    0.8 of its length (at most a fifth of the bucket's rows are padding), as
+    long as fits(count, longest) holds for the workspace."""
+    order = sorted(range(len(lengths)), key=lambda i: -lengths[i])
+    buckets: list[list[int]] = []
+    for i in order:
+        if buckets:
+            head = lengths[buckets[-1][0]]
+            if 5 * lengths[i] >= 4 * head and fits(len(buckets[-1]) + 1, head):
+                buckets[-1].append(i)
+                continue
+        buckets.append([i])
+    return buckets
+
+
+def _packed_backward(lib, offsets, inputs, grads, s0, ds_t, ds0, heads, key_dim, value_dim, device, run):
+    """The chunk backward of packed documents in few calls: documents of
+    similar length are stacked into one zero-padded dense batch [n, T_b, H, *]
+    per bucket.  A zero row (q = k = v = g = beta = 0, dO = 0) neither decays,
+    writes nor reads the state, which is how the kernels treat the rows past a
+    sequence's end, so every document's gradients are those of its own call.
+    A bucket of one document runs on the packed tensors in place."""
+    lengths = [b - a for a, b in zip(offsets[:-1], offsets[1:])]
+    longest = max(lengths)
+    # the workspace a call per document needs anyway (sized for the longest),
+    # or 1 GiB, bounds each bucket's
+    budget = max(lib.kda_chunk_bwd_workspace_bytes(1, longest, heads, key_dim, value_dim), 1 << 30)
+
+    def fits(n, n_tok):
+        return lib.kda_chunk_bwd_workspace_bytes(n, n_tok, heads, key_dim, value_dim) <= budget
+
+    buckets = _document_buckets(lengths, fits)
+    ws_bytes = max(lib.kda_chunk_bwd_workspace_bytes(len(bk), lengths[bk[0]], heads, key_dim, value_dim)
+                   for bk in buckets)
+    workspace = _prep.workspace(ws_bytes, device, "the chunkwise_kda backward")
+    for bk in buckets:
+        if len(bk) == 1:
+            i = bk[0]
+            a = offsets[i]
+            views = [t[:, a:a + lengths[i]] for t in inputs]
+            gviews = [t[:, a:a + lengths[i]] for t in grads]
+            if all(t.is_contiguous() for t in views + gviews):
+                run(views, gviews, None if s0 is None else s0[i:i + 1], None if ds_t is None else ds_t[i:i + 1],
+                    None if ds0 is None else ds0[i:i + 1], 1, lengths[i], workspace, ws_bytes)
+                continue
+        n_tok = lengths[bk[0]]
+        # packed row of each real row of the bucket, and its row in the padded batch
+        lens_b = np.array([lengths[i] for i in bk], dtype=np.int64)
+        starts_b = np.array([offsets[i] for i in bk], dtype=np.int64)
+        doc = np.repeat(np.arange(len(bk)), lens_b)
+        pos = np.arange(int(lens_b.sum())) - np.repeat(np.cumsum(lens_b) - lens_b, lens_b)
+        src_rows = torch.from_numpy(starts_b[doc] + pos).to(device)
+        dst_rows = torch.from_numpy(doc * n_tok + pos).to(device)
+        padded = []
+        for t in inputs:
+            flat = t.new_zeros((len(bk) * n_tok,) + tuple(t.shape[2:]))
+            flat[dst_rows] = t[0].index_select(0, src_rows)
+            padded.append(flat.view((len(bk), n_tok) + tuple(t.shape[2:])))
+        pgrads = [torch.empty_like(p) for p in padded[:5]]
+        idx = torch.tensor(bk, device=device)
+        s_b = None if s0 is None else s0.index_select(0, idx).contiguous()
+        dst_b = None if ds_t is None else ds_t.index_select(0, idx).contiguous()
+        ds0_b = None if ds0 is None else torch.empty_like(s_b)
+        run(padded, pgrads, s_b, dst_b, ds0_b, len(bk), n_tok, workspace, ws_bytes)
+        for dst, src in zip(grads, pgrads):
+            dst[0].index_copy_(0, src_rows, src.view((-1,) + tuple(src.shape[2:])).index_select(0, dst_rows))
+        if ds0 is not None:
+            ds0.index_copy_(0, idx, ds0_b)
+
+
 class _ChunkwiseFunction(torch.autograd.Function):
     """The operator on masked, dense inputs with the HIP chunk backward."""
 
@@ -183,31 +258,25 @@ class _ChunkwiseFunction(torch.autograd.Function):
         ds0 = None
         if initial_state is not None and ctx.needs_input_grad[5]:
             ds0 = torch.empty(n_state, heads, key_dim, value_dim, dtype=state_dtype, device=device)
-        # dense: one call over the batch; packed documents: one batch-1 call per
-        # document on its token range [start, end) of the packed tensors
-        if ctx.offsets is None:
-            spans = [(0, 0, tokens, batch)]
-        else:
-            spans = [(i, ctx.offsets[i], ctx.offsets[i + 1], 1) for i in range(n_state)]
-        longest = max(end - start for _, start, end, _ in spans)
-        n_b = spans[0][3]
-        ws_bytes = lib.kda_chunk_bwd_workspace_bytes(n_b, longest, heads, key_dim, value_dim)
-        workspace = _prep.workspace(ws_bytes, device, "the chunkwise_kda backward")
         code = _lib.dtype_code(kernel_dtype)
         stream = _prep.stream(device)
-        state_elems = heads * key_dim * value_dim
 
-        def at(t, elems):
-            return None if t is None else t.data_ptr() + elems * t.element_size()
-
-        for i, start, end, n_b in spans:  # documents are non-empty (validate_cu_seqlens)
-            tk, tv, tb, st = start * heads * key_dim, start * heads * value_dim, start * heads, i * state_elems
+        def run(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, workspace, ws_bytes):
             status = lib.kda_chunk_bwd(
-                at(qc, tk), at(kc, tk), at(vc, tv), at(gc, tk), at(bc, tb), at(d_out, tv), code,
-                at(s0, st), at(ds_t, st), at(dq, tk), at(dk, tk), at(dv, tv), at(dg, tk), at(dbeta, tb),
-                at(ds0, st), n_b, end - start, heads, key_dim, value_dim, _lib.ptr(workspace), ws_bytes, stream,
+                *(t.data_ptr() for t in tensors), code, _lib.ptr(s_init), _lib.ptr(ds_fin),
+                *(t.data_ptr() for t in grads_out), _lib.ptr(ds_init), n_b, n_tok, heads, key_dim, value_dim,
+                _lib.ptr(workspace), ws_bytes, stream,
             )
             _lib.check(status)
+
+        if ctx.offsets is None:
+            ws_bytes = lib.kda_chunk_bwd_workspace_bytes(batch, tokens, heads, key_dim, value_dim)
+            workspace = _prep.workspace(ws_bytes, device, "the chunkwise_kda backward")
+            run((qc, kc, vc, gc, bc, d_out), (dq, dk, dv, dg, dbeta), s0, ds_t, ds0, batch, tokens, workspace,
+                ws_bytes)
+        else:
+            _packed_backward(lib, ctx.offsets, (qc, kc, vc, gc, bc, d_out), (dq, dk, dv, dg, dbeta), s0, ds_t, ds0,
+                             heads, key_dim, value_dim, device, run)
         grads = [dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
                  None if ds0 is None else ds0.to(initial_state.dtype)]
         return (*[gr if need else None for gr, need in zip(grads, ctx.needs_input_grad[:6])], None, None, None, None)

@@ -192,6 +192,43 @@ def test_packed_documents_gradients_match_per_document_oracle(op, dtype):
             assert rel_err(a, b) < TOL[dtype], (name, i, rel_err(a, b))
 
 
+def test_many_packed_documents_backward_in_length_buckets():
+    # 24 documents of 40..200 tokens: the backward stacks documents within a
+    # fifth of each other's length into zero-padded batches (a few calls instead
+    # of one per document); every document's gradients equal those of its own
+    # call, and two of them the oracle's
+    from kda.chunkwise import _document_buckets
+
+    gen = torch.Generator().manual_seed(70)
+    lens = [int(x) for x in torch.randint(40, 201, (24,), generator=gen)]
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    buckets = _document_buckets(lens, lambda n, t: True)
+    assert len(buckets) < len(lens) and max(len(b) for b in buckets) > 2
+    H, K, V = 2, 128, 64
+    q, k, v, g, beta, _ = workload(1, cu[-1], H, K, V, state_std=0.5, seed=71, dtype=torch.float32)
+    s0 = torch.randn(len(lens), H, K, V, generator=gen) * 0.5
+    d_out = torch.randn(1, cu[-1], H, V, generator=gen)
+    d_final = torch.randn(len(lens), H, K, V, generator=gen)
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v, g, beta, s0)]
+    res = kda.chunkwise_kda(*leaves, True, cu_seqlens=cu)
+    ((res.hidden_states * d_out.to(DEV)).sum() + (res.final_state * d_final.to(DEV)).sum()).backward()
+    for i, (a0, a1) in enumerate(zip(cu[:-1], cu[1:])):
+        doc = [t[:, a0:a1] for t in (q, k, v, g, beta)] + [s0[i:i + 1]]
+        alone = _gpu_grads(doc, d_out[:, a0:a1], d_final[i:i + 1])
+        for name, leaf, b in zip(NAMES, leaves, alone):
+            a = leaf.grad[i:i + 1] if name == "ds0" else leaf.grad[:, a0:a1]
+            assert rel_err(a, b) < 1e-5, (name, i, rel_err(a, b))
+    for i in (0, 17):
+        a0, a1 = cu[i], cu[i + 1]
+        ref = _oracle_grads([t[:, a0:a1] for t in (q, k, v, g, beta)] + [s0[i:i + 1]], d_out[:, a0:a1],
+                            d_final[i:i + 1])
+        for name, leaf, b in zip(NAMES, leaves, ref):
+            a = leaf.grad[i:i + 1] if name == "ds0" else leaf.grad[:, a0:a1]
+            assert rel_err(a, b) < TOL[torch.float32], (name, i)
+
+
 @pytest.mark.parametrize("regime", ["steep", "rising"])
 def test_backward_exact_path_regimes(regime):
     # chunks whose decay falls by more than 80 within 16 tokens, or whose g is

@@ -114,3 +114,19 @@ def test_state_dataclass_contract():
                      torch.tensor([4.0, 6.0]))
     with pytest.raises(ValueError):
         state.reorder(torch.tensor([0.0]))
+
+
+def test_packed_backward_buckets_group_documents_of_similar_length():
+    from kda.chunkwise import _document_buckets
+
+    lens = [70, 1, 130, 64, 128, 100]
+    buckets = _document_buckets(lens, lambda n, tokens: True)
+    # every document exactly once, and within a bucket no document is shorter
+    # than 0.8 of the bucket's first (longest)
+    assert sorted(i for b in buckets for i in b) == list(range(len(lens)))
+    for b in buckets:
+        assert all(5 * lens[i] >= 4 * lens[b[0]] and lens[i] <= lens[b[0]] for i in b)
+    assert [[lens[i] for i in b] for b in buckets] == [[130, 128], [100], [70, 64], [1]]
+    # the workspace bound caps a bucket's size
+    capped = _document_buckets([100] * 5, lambda n, tokens: n <= 2)
+    assert [len(b) for b in capped] == [2, 2, 1]
