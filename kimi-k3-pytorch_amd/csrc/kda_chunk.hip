@@ -921,7 +921,7 @@ __device__ __forceinline__ void p1_write_ma(unsigned char* sm, const P1Out& po, 
 
 // Everything after P1 (reads only LDS, plus global q/k/g on the rare
 // extreme-decay path).
-template <class IT, int MODE, bool LOADER, bool DECAY>
+template <class IT, int MODE, bool LOADER, bool DECAY, int KT>
 __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h,
                                             int vcg, int tid, const NextLoads<IT, MODE>& nl) {
   const int lane = tid & 63;
@@ -1007,7 +1007,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
       f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
       f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
   #pragma unroll
-      for (int half = 0; half < 2; ++half) {
+      for (int half = 0; half < KT / 4; ++half) {
         bf16x8_t ke[2], kb[2], qb[2];
         f32x4_t sc0[2], sc1[2];
   #pragma unroll
@@ -1067,7 +1067,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
       f32x4_t akk = {0.f, 0.f, 0.f, 0.f};
       f32x4_t aqk = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int half = 0; half < 2; ++half) {
+      for (int half = 0; half < KT / 4; ++half) {
         bf16x8_t ke[2], kb[2], qb[2];
         f32x4_t sc0[2], sc1[2];
 #pragma unroll
@@ -1284,8 +1284,10 @@ __device__ __forceinline__ void prepare_m(unsigned char* sm, int tid, const Next
 
 // ---- per-chunk state advance of one wave's pair of 16-column tiles ----------
 // ut[t] >= 0: U tile index of tile t (value columns); -1: a transition column
-// (U = 0).  Phase C also forms O = Q~ S + Aqk V~ for both tiles.
-template <int MODE>
+// (U = 0).  Phase C also forms O = Q~ S + Aqk V~ for both tiles.  KT: the row
+// tiles of the state that carry channels (8, or 4 when K <= 64: the rows past
+// them stay zero, so the products over them are skipped).
+template <int MODE, int KT>
 __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[2][8], const int (&ut)[2], int lane,
                                           f32x4_t (&O)[2][4]) {
   const int g4 = lane >> 4;
@@ -1323,10 +1325,10 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
   bf16x8_t kfa[4], qfa[4], kfb[4], qfb[4];
   load_step(0, kfa, qfa);
 #pragma unroll
-  for (int st = 0; st < 4; ++st) {
+  for (int st = 0; st < KT / 2; ++st) {
     bf16x8_t(&kf)[4] = (st & 1) ? kfb : kfa;
     bf16x8_t(&qf)[4] = (st & 1) ? qfb : qfa;
-    if (st + 1 < 4) {
+    if (st + 1 < KT / 2) {
       if (st & 1)
         load_step(st + 1, kfa, qfa);
       else
@@ -1405,7 +1407,7 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
   // S <- diag(gamma) S + K~^T V~
   const float* gam = reinterpret_cast<const float*>(sm + kOffGam);
 #pragma unroll
-  for (int h4 = 0; h4 < 2; ++h4) {
+  for (int h4 = 0; h4 < KT / 4; ++h4) {
     bf16x8_t kt[4][2];
     f32x4_t gm[4];
 #pragma unroll
@@ -1468,7 +1470,7 @@ __device__ __forceinline__ void store_out(const f32x4_t (&O)[2][4], int ntile, I
 // registers are live in the other's code.
 // DECAY: g formed from decay logits; PAD: K < 128, channels K..127 are zero
 // padding (K == 128 compiles without any of the padding checks)
-template <class IT, int MODE, bool DECAY, bool PAD>
+template <class IT, int MODE, bool DECAY, bool PAD, int KT>
 __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<IT> a) {
   extern __shared__ __align__(16) unsigned char sm[];
   // one-dimensional grid, segment slowest: the workgroups past the real
@@ -1499,7 +1501,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
   const int vcg = static_cast<int>(a.V - col0 < kColGroup ? a.V - col0 : kColGroup);
   const int nvt = vcg / 16;
   const bool track_p = MODE == kSummary && lg > 0 && cgi == 0;
-  const int ntiles = nvt + (track_p ? 8 : 0);
+  const int ntiles = nvt + (track_p ? KT : 0);  // value tiles, then one transition tile per channel row tile
   const int64_t sbase = (s * a.H + h) * a.K * a.V;
   constexpr int kPairs = MODE == kSummary ? 2 : 1;  // tile pairs per scanner wave
 
@@ -1551,7 +1553,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
         const int tile0 = 2 * w;
         f32x4_t O[2][4];
         const int ut[2] = {tile0 < nvt ? tile0 : -1, tile0 + 1 < nvt ? tile0 + 1 : -1};
-        if (tile0 < ntiles) scan_pair<MODE>(sm, S[0], ut, tid_c & 63, O);
+        if (tile0 < ntiles) scan_pair<MODE, KT>(sm, S[0], ut, tid_c & 63, O);
         __syncthreads();
         if (tile0 < ntiles) {
           const int nt = ntiles - tile0 < 2 ? ntiles - tile0 : 2;
@@ -1569,7 +1571,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       // where they would stay live (and spill) next to the state tiles
       const int tid_c = opaque(tid);
       p1_write<MODE, false>(sm, none, nullptr, tid_c);
-      prepare_mid<IT, MODE, false, DECAY>(sm, a, geo, h, vcg, tid_c, nl);
+      prepare_mid<IT, MODE, false, DECAY, KT>(sm, a, geo, h, vcg, tid_c, nl);
       prepare_m<IT, MODE, false>(sm, tid_c, nl);
 #pragma unroll
       for (int pp = 0; pp < kPairs; ++pp) {
@@ -1577,7 +1579,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
         if (tile0 < ntiles && scan_state) {
           const int ut[2] = {tile0 < nvt ? tile0 : -1, tile0 + 1 < nvt ? tile0 + 1 : -1};
           f32x4_t O[2][4];
-          scan_pair<MODE>(sm, S[pp], ut, tid_c & 63, O);
+          scan_pair<MODE, KT>(sm, S[pp], ut, tid_c & 63, O);
           if constexpr (kWritesOut<MODE>) {
             const int nt = ntiles - tile0 < 2 ? ntiles - tile0 : 2;
             store_out<IT>(O, nt, a.out, geo, a.H, h, a.V, col0 + 16 * tile0, tid_c & 63,
@@ -1635,7 +1637,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       p1_write<MODE, true>(sm, po, &ll, tid_c);
       const NextLoads<IT, MODE> nl{&raw, chunk_loads<IT>(a, chunk_geo(sr, c + 1 - cs), c + 1, h, col0, c + 1 < c_end),
                                    &ll, tid_c};
-      prepare_mid<IT, MODE, true, DECAY>(sm, a, geo, h, vcg, tid_c, nl);
+      prepare_mid<IT, MODE, true, DECAY, KT>(sm, a, geo, h, vcg, tid_c, nl);
       prepare_m<IT, MODE, true>(sm, tid_c, nl);
       if constexpr (MODE == kSummary) {
         // hand the chunk's M and Aqk fragments to phase C (one column group
@@ -1713,8 +1715,13 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       for (int f = tid; f < 8 * 4 * 64; f += kThreads) {
         const int I = f >> 8, st = (f >> 6) & 3, fl = f & 63;
         const int i = 16 * I + (fl & 15), gq = fl >> 4;
-        const bf16x4_t lo = *reinterpret_cast<const bf16x4_t*>(&Pn[i][32 * st + 4 * gq]);
-        const bf16x4_t hi = *reinterpret_cast<const bf16x4_t*>(&Pn[i][32 * st + 16 + 4 * gq]);
+        // columns past the KT row tiles have no transition tile (their channels
+        // are padding, and the state rows they would multiply are zero): zeros
+        bf16x4_t lo = bf16x4_t{}, hi = bf16x4_t{};
+        if (st < KT / 2) {
+          lo = *reinterpret_cast<const bf16x4_t*>(&Pn[i][32 * st + 4 * gq]);
+          hi = *reinterpret_cast<const bf16x4_t*>(&Pn[i][32 * st + 16 + 4 * gq]);
+        }
         *reinterpret_cast<bf16x8_t*>(pdst + static_cast<int64_t>(f) * 8) =
             bf16x8_t{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
@@ -1900,18 +1907,18 @@ static void mark(kda_host::KernelEvents* ev, int i, hipStream_t stream) {
   }
 }
 
-template <class IT, int MODE, bool DECAY, bool PAD>
+template <class IT, int MODE, bool DECAY, bool PAD, int KT>
 static int launch_segments(const SegArgs<IT>& sa, const Plan& p, int64_t H, hipStream_t stream) {
   static bool attr_done = false;
   if (!attr_done) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_segment_kernel<IT, MODE, DECAY, PAD>),
+    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_segment_kernel<IT, MODE, DECAY, PAD, KT>),
                             hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes) != hipSuccess) {
       kda_host::set_detail("cannot reserve %d bytes of LDS for chunk_segment_kernel", kSmemBytes);
       return KDA_ERR_LAUNCH;
     }
     attr_done = true;
   }
-  hipLaunchKernelGGL((chunk_segment_kernel<IT, MODE, DECAY, PAD>), dim3(static_cast<unsigned>(p.segs_bound * H * p.ncg)),
+  hipLaunchKernelGGL((chunk_segment_kernel<IT, MODE, DECAY, PAD, KT>), dim3(static_cast<unsigned>(p.segs_bound * H * p.ncg)),
                      dim3(kThreads), kSmemBytes, stream, sa);
   return kda_host::check_launch(MODE == kSummary ? "chunk_segment_kernel<summary>" : "chunk_segment_kernel<output>");
 }
@@ -1923,7 +1930,7 @@ struct DecayInput {
   float g_min;
 };
 
-template <class IT, bool DECAY, bool PAD>
+template <class IT, bool DECAY, bool PAD, int KT>
 static int run_chunk_k(const void* q, const void* k, const void* v, const void* g, const void* beta, const void* s_in,
                      void* s_out, void* out, const SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
                      int64_t K, int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev,
@@ -1987,7 +1994,7 @@ static int run_chunk_k(const void* q, const void* k, const void* v, const void* 
   }
   mark(ev, 1, stream);
   if (p.segmented) {
-    st = launch_segments<IT, kSummary, DECAY, PAD>(sa, p, H, stream);
+    st = launch_segments<IT, kSummary, DECAY, PAD, KT>(sa, p, H, stream);
     if (st != KDA_OK) return st;
     mark(ev, 2, stream);
     CombineArgs ca{sa.seg_start, sa.dense_segs, sa.seg_state, sa.seg_q, sa.seg_p, N, H, V};
@@ -2002,8 +2009,8 @@ static int run_chunk_k(const void* q, const void* k, const void* v, const void* 
     mark(ev, 3, stream);
     if (ev != nullptr) ev->empty |= 6u;  // one segment per sequence: no summaries, no combine
   }
-  st = p.segmented ? launch_segments<IT, kOutputMA, DECAY, PAD>(sa, p, H, stream)
-                   : launch_segments<IT, kOutput, DECAY, PAD>(sa, p, H, stream);
+  st = p.segmented ? launch_segments<IT, kOutputMA, DECAY, PAD, KT>(sa, p, H, stream)
+                   : launch_segments<IT, kOutput, DECAY, PAD, KT>(sa, p, H, stream);
   mark(ev, 4, stream);
   return st;
 }
@@ -2013,11 +2020,16 @@ static int run_chunk(const void* q, const void* k, const void* v, const void* g,
                      void* s_out, void* out, const SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H,
                      int64_t K, int64_t V, void* workspace, hipStream_t stream, kda_host::KernelEvents* ev,
                      const DecayInput* decay) {
+  // K == 128 runs without padding checks; K <= 64 (the reference's shipped
+  // model profiles use 64) carries its channels in four row tiles of the state
   if (K == kKey)
-    return run_chunk_k<IT, DECAY, false>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V, workspace,
-                                         stream, ev, decay);
-  return run_chunk_k<IT, DECAY, true>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V, workspace,
-                                      stream, ev, decay);
+    return run_chunk_k<IT, DECAY, false, 8>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V,
+                                            workspace, stream, ev, decay);
+  if (K <= kKey / 2)
+    return run_chunk_k<IT, DECAY, true, 4>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V,
+                                           workspace, stream, ev, decay);
+  return run_chunk_k<IT, DECAY, true, 8>(q, k, v, g, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V,
+                                         workspace, stream, ev, decay);
 }
 
 }  // namespace kda
