@@ -31,8 +31,9 @@
 //   seg_combine_kernel  Vt) and the backward scan (dS', dVt per chunk, dS0),
 //                       side by side, each cut into segments whose affine
 //                       maps are composed (section "segmented state scans");
-//   grad_kernel         one block per chunk: dv, dbeta, and dQg, dKt, dKg, dA, dAqk;
-//   pair_kernel         one block per chunk: the pair sums and the final dq, dk, dg.
+//   grad_pair_kernel    one block per chunk: grad_body (dv, dbeta, and the records
+//                       dQg, dKt, dKg, dA, dAqk), then pair_body (the pair sums
+//                       and the final dq, dk, dg) on the records just written.
 // Intermediates live in a caller-owned f32 workspace, one record per
 // (sequence, head, chunk), followed by the scans' segment records.
 #include <math.h>
@@ -45,7 +46,7 @@ namespace bwd {
 constexpr int kC = 64;     // chunk rows
 constexpr int kRS = 132;   // LDS row stride of [64][<=128] channel matrices
 constexpr int kRC = 68;    // LDS row stride of [64][64] chunk matrices
-constexpr int kSW = 32;    // state columns per slab in grad_kernel
+constexpr int kSW = 32;    // state columns per slab in grad_body
 constexpr int kSS = 36;    // LDS row stride of slab matrices
 constexpr int kTS = 20;    // LDS row stride of 16-column scan tiles
 
@@ -1296,7 +1297,7 @@ __global__ __launch_bounds__(kOT) void out_kernel(const Args<IT> a) {
   }
 }
 
-// ---- grad_kernel: products that reduce over the state columns -----------------
+// ---- grad_body: products that reduce over the state columns --------------------
 // Eight waves; slabs of 32 state columns accumulate dQg, dKt, dW (wave w:
 // row tile w % 4, half w / 4 of the column tiles),
 // dAqk and dM in MFMA accumulators and write dv; then dKg = M^T dW,
@@ -1354,7 +1355,7 @@ __device__ __forceinline__ void load_ws_split(__bf16* dst, const float* src, int
   }
 }
 
-// One 32-column slab of grad_kernel's operands in registers: the S and dS
+// One 32-column slab of grad_body's operands in registers: the S and dS
 // rows (KP x 32), Vt and dVt (64 x 32, f32 from the workspace) and dO and v
 // (64 x 32 from the inputs; the whole-group case of load_rows_split).  The
 // next slab's loads go out while the current one is multiplied.
@@ -1440,12 +1441,11 @@ __device__ __forceinline__ void load_rows_split(__bf16* dst, const IT* src, int6
   }
 }
 
+// sm: kGradFloats floats of LDS, bS: kC more
 template <class IT, int KP>
-__global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
+__device__ __forceinline__ void grad_body(const Args<IT>& a, float* sm, float* bS) {
   constexpr int NT = 512;
   constexpr int Kp = KP, CH = KP / 32;  // K-wide column tiles per wave
-  __shared__ __attribute__((aligned(16))) float sm[kGradFloats];
-  __shared__ float bS[kC];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   const int rt = w & 3, hf = w >> 2;  // wave w: row tile rt, half hf of the column tiles
   const int64_t ch = blockIdx.x;
@@ -1620,7 +1620,7 @@ __global__ __launch_bounds__(512) void grad_kernel(const Args<IT> a) {
   }
 }
 
-// ---- pair_kernel: pair sums with exact exponents and the final dq, dk, dg ----
+// ---- pair_body: pair sums with exact exponents and the final dq, dk, dg ------
 // Thread (column col, part p) owns rows i = p + P m of its column (P = NT / Kp,
 // RP = 64 / P rows) and forms
 //   R1_i = sum_j dA_ij k_j E_ij,  R2_i = sum_j dAqk_ij k_j E_ij   (j <= i)
@@ -1870,7 +1870,7 @@ __device__ __forceinline__ void pair_mfma(const Args<IT>& a, const float* ws, fl
   }
 }
 
-// ---- pair_kernel: the pair sums and the final dq, dk, dg ----------------------
+// ---- pair_body: the pair sums and the final dq, dk, dg ------------------------
 //   R1_i = sum_j dA_ij k_j E_ij,  R2_i = sum_j dAqk_ij k_j E_ij   (j <= i)
 //   R3_j = sum_i dA_ij k_i E_ij,  R4_j = sum_i dAqk_ij q_i E_ij   (i >= j)
 // then dk = R1 + R3 + R4 + e^lg dKg + e^(lg_last - lg) dKt, dq = R2 + e^lg dQg,
@@ -1878,11 +1878,14 @@ __device__ __forceinline__ void pair_mfma(const Args<IT>& a, const float* ws, fl
 // sum(Kt dKt) + D dD), and dg as its reverse cumulative sum.  The sums run on
 // the MFMA with the block factorisation of the decay unless the chunk needs
 // the exact pairwise path.
+// The pair kernel's LDS: k, q and lg tiles [64][kRS], dA and dAqk [64][kRC],
+// and the partial sums `red` [16][128], kPairFloats floats in this order.
+constexpr int kPairFloats = 3 * kC * kRS + 2 * kC * kRC + 16 * 128;
 template <class IT, int KP, int NT>
-__global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
+__device__ __forceinline__ void pair_body(const Args<IT>& a, float* lds) {
   static_assert(NT == 512, "the MFMA path uses eight waves");
-  __shared__ __attribute__((aligned(16))) float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS], dAS[kC * kRC], dQS[kC * kRC];
-  __shared__ float red[16 * 128];
+  float *kS = lds, *qS = kS + kC * kRS, *lgS = qS + kC * kRS, *dAS = lgS + kC * kRS, *dQS = dAS + kC * kRC;
+  float* red = dQS + kC * kRC;
   const int tid = threadIdx.x;
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
@@ -1937,6 +1940,20 @@ __global__ __launch_bounds__(NT) void pair_kernel(const Args<IT> a) {
       }
     }
   }
+}
+
+// ---- grad_pair_kernel: grad_body, then pair_body on the same chunk ------------
+// The gradient records grad_body writes (dQg, dKt, dKg, dA, dAqk, dD: 128 KB
+// per chunk at K=V=128) are read back by pair_body in the same workgroup right
+// after, while they are still in this XCD's L2, instead of by a second kernel
+// from HBM.  The two bodies use one LDS buffer in turn.
+constexpr int kGradPairFloats = kGradFloats + kC > kPairFloats ? kGradFloats + kC : kPairFloats;
+template <class IT, int KP>
+__global__ __launch_bounds__(512) void grad_pair_kernel(const Args<IT> a) {
+  __shared__ __attribute__((aligned(16))) float lds[kGradPairFloats];
+  grad_body<IT, KP>(a, lds, lds + kGradFloats);
+  __syncthreads();  // every record written and every LDS read of grad_body done
+  pair_body<IT, KP, 512>(a, lds);
 }
 
 }  // namespace bwd
@@ -2062,8 +2079,7 @@ template <class IT, int KP>
 static void launch_all(const bwd::Args<IT>& a, dim3 chunks, hipStream_t s) {
   hipLaunchKernelGGL((bwd::prep_kernel<IT, KP>), chunks, dim3(bwd::kPT), 0, s, a);
   launch_scans<IT, KP>(a, s);
-  hipLaunchKernelGGL((bwd::grad_kernel<IT, KP>), chunks, dim3(512), 0, s, a);
-  hipLaunchKernelGGL((bwd::pair_kernel<IT, KP, 512>), chunks, dim3(512), 0, s, a);
+  hipLaunchKernelGGL((bwd::grad_pair_kernel<IT, KP>), chunks, dim3(512), 0, s, a);
 }
 
 template <class IT>
