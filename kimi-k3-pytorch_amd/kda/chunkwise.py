@@ -23,7 +23,9 @@ documents (``cu_seqlens``) are differentiated in buckets of similar length:
 documents within a fifth of the bucket's longest are stacked into one
 zero-padded dense batch (zero rows are identity steps of the recurrence), a
 lone document runs on its slice of the packed tensors in place, and each
-bucket's workspace stays within max(the longest document's, 1 GiB).  Other
+bucket's workspace stays within max(the longest document's, 1 GiB).  A call
+whose workspace would pass ``BACKWARD_WORKSPACE_LIMIT`` (4 GiB) runs its
+heads in groups, on contiguous copies of the head slices.  Other
 cases raise instead of dropping gradients, and so does a second derivative
 (the backward is marked once-differentiable).
 """
@@ -157,6 +159,75 @@ def _document_buckets(lengths: list[int], fits) -> list[list[int]]:
     return buckets
 
 
+# Most bytes one chunk-backward call may take as workspace before the heads
+# are differentiated in groups (its size is linear in the heads: about
+# 160 KB per token and head at K=V=128).
+BACKWARD_WORKSPACE_LIMIT = 4 << 30
+
+
+def _head_group(lib, n_b, n_tok, heads, key_dim, value_dim) -> int:
+    """Heads per chunk-backward call for an [n_b, n_tok] batch: all of them
+    when the workspace fits BACKWARD_WORKSPACE_LIMIT, else the most that fit
+    (at least one)."""
+    def need(n_h):
+        return lib.kda_chunk_bwd_workspace_bytes(n_b, n_tok, n_h, key_dim, value_dim)
+
+    # the size grows with the heads: the largest count that fits, by bisection
+    lo, hi = 1, heads
+    while lo < hi:
+        mid = (lo + hi + 1) // 2
+        if need(mid) <= BACKWARD_WORKSPACE_LIMIT:
+            lo = mid
+        else:
+            hi = mid - 1
+    return lo
+
+
+class _Workspace:
+    """One workspace for the calls of a backward, grown to the largest
+    request (the torch caching allocator keeps the bytes for reuse)."""
+
+    def __init__(self, device):
+        self.device, self.tensor, self.nbytes = device, None, 0
+
+    def get(self, nbytes):
+        if nbytes > self.nbytes:
+            self.tensor = None
+            self.tensor = _prep.workspace(nbytes, self.device, "the chunkwise_kda backward")
+            self.nbytes = nbytes
+        return self.tensor
+
+
+def _by_head_groups(lib, call, tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, heads, key_dim,
+                    value_dim, workspace):
+    """One chunk-backward over [n_b, n_tok, heads, *] tensors, split into
+    head groups when the whole call's workspace would pass
+    BACKWARD_WORKSPACE_LIMIT.  Heads are independent in KDA (every state,
+    decay and gradient is per head), so a group is the same computation on
+    contiguous copies of its head slices, its gradients copied back."""
+    n_h = _head_group(lib, n_b, n_tok, heads, key_dim, value_dim)
+    ws_bytes = lib.kda_chunk_bwd_workspace_bytes(n_b, n_tok, n_h, key_dim, value_dim)
+    ws = workspace.get(ws_bytes)
+    if n_h == heads:
+        call(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, heads, ws, ws_bytes)
+        return
+
+    def part(t, h0, h1, axis):
+        return None if t is None else t.narrow(axis, h0, h1 - h0).contiguous()
+
+    for h0 in range(0, heads, n_h):
+        h1 = min(heads, h0 + n_h)
+        ins = [part(t, h0, h1, 2) for t in tensors]
+        outs = [torch.empty_like(t) for t in ins[:5]]
+        ds_g = None if ds_init is None else torch.empty_like(part(ds_init, h0, h1, 1))
+        call(ins, outs, part(s_init, h0, h1, 1), part(ds_fin, h0, h1, 1), ds_g, n_b, n_tok, h1 - h0, ws,
+             ws_bytes)
+        for dst, src in zip(grads_out, outs):
+            dst.narrow(2, h0, h1 - h0).copy_(src)
+        if ds_init is not None:
+            ds_init.narrow(1, h0, h1 - h0).copy_(ds_g)
+
+
 def _packed_backward(lib, offsets, inputs, grads, s0, ds_t, ds0, heads, key_dim, value_dim, device, run):
     """The chunk backward of packed documents in few calls: documents of
     similar length are stacked into one zero-padded dense batch [n, T_b, H, *]
@@ -167,16 +238,15 @@ def _packed_backward(lib, offsets, inputs, grads, s0, ds_t, ds0, heads, key_dim,
     lengths = [b - a for a, b in zip(offsets[:-1], offsets[1:])]
     longest = max(lengths)
     # the workspace a call per document needs anyway (sized for the longest),
-    # or 1 GiB, bounds each bucket's
-    budget = max(lib.kda_chunk_bwd_workspace_bytes(1, longest, heads, key_dim, value_dim), 1 << 30)
+    # or 1 GiB, bounds each bucket's, within BACKWARD_WORKSPACE_LIMIT (past it
+    # a bucket's heads go in groups)
+    budget = min(max(lib.kda_chunk_bwd_workspace_bytes(1, longest, heads, key_dim, value_dim), 1 << 30),
+                 BACKWARD_WORKSPACE_LIMIT)
 
     def fits(n, n_tok):
         return lib.kda_chunk_bwd_workspace_bytes(n, n_tok, heads, key_dim, value_dim) <= budget
 
     buckets = _document_buckets(lengths, fits)
-    ws_bytes = max(lib.kda_chunk_bwd_workspace_bytes(len(bk), lengths[bk[0]], heads, key_dim, value_dim)
-                   for bk in buckets)
-    workspace = _prep.workspace(ws_bytes, device, "the chunkwise_kda backward")
     for bk in buckets:
         if len(bk) == 1:
             i = bk[0]
@@ -185,7 +255,7 @@ def _packed_backward(lib, offsets, inputs, grads, s0, ds_t, ds0, heads, key_dim,
             gviews = [t[:, a:a + lengths[i]] for t in grads]
             if all(t.is_contiguous() for t in views + gviews):
                 run(views, gviews, None if s0 is None else s0[i:i + 1], None if ds_t is None else ds_t[i:i + 1],
-                    None if ds0 is None else ds0[i:i + 1], 1, lengths[i], workspace, ws_bytes)
+                    None if ds0 is None else ds0[i:i + 1], 1, lengths[i])
                 continue
         n_tok = lengths[bk[0]]
         # packed row of each real row of the bucket, and its row in the padded batch
@@ -205,7 +275,7 @@ def _packed_backward(lib, offsets, inputs, grads, s0, ds_t, ds0, heads, key_dim,
         s_b = None if s0 is None else s0.index_select(0, idx).contiguous()
         dst_b = None if ds_t is None else ds_t.index_select(0, idx).contiguous()
         ds0_b = None if ds0 is None else torch.empty_like(s_b)
-        run(padded, pgrads, s_b, dst_b, ds0_b, len(bk), n_tok, workspace, ws_bytes)
+        run(padded, pgrads, s_b, dst_b, ds0_b, len(bk), n_tok)
         for dst, src in zip(grads, pgrads):
             dst[0].index_copy_(0, src_rows, src.view((-1,) + tuple(src.shape[2:])).index_select(0, dst_rows))
         if ds0 is not None:
@@ -261,19 +331,22 @@ class _ChunkwiseFunction(torch.autograd.Function):
         code = _lib.dtype_code(kernel_dtype)
         stream = _prep.stream(device)
 
-        def run(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, workspace, ws_bytes):
+        def call(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, n_h, ws, ws_bytes):
             status = lib.kda_chunk_bwd(
                 *(t.data_ptr() for t in tensors), code, _lib.ptr(s_init), _lib.ptr(ds_fin),
-                *(t.data_ptr() for t in grads_out), _lib.ptr(ds_init), n_b, n_tok, heads, key_dim, value_dim,
-                _lib.ptr(workspace), ws_bytes, stream,
+                *(t.data_ptr() for t in grads_out), _lib.ptr(ds_init), n_b, n_tok, n_h, key_dim, value_dim,
+                _lib.ptr(ws), ws_bytes, stream,
             )
             _lib.check(status)
 
+        workspace = _Workspace(device)
+
+        def run(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok):
+            _by_head_groups(lib, call, tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, heads, key_dim,
+                            value_dim, workspace)
+
         if ctx.offsets is None:
-            ws_bytes = lib.kda_chunk_bwd_workspace_bytes(batch, tokens, heads, key_dim, value_dim)
-            workspace = _prep.workspace(ws_bytes, device, "the chunkwise_kda backward")
-            run((qc, kc, vc, gc, bc, d_out), (dq, dk, dv, dg, dbeta), s0, ds_t, ds0, batch, tokens, workspace,
-                ws_bytes)
+            run((qc, kc, vc, gc, bc, d_out), (dq, dk, dv, dg, dbeta), s0, ds_t, ds0, batch, tokens)
         else:
             _packed_backward(lib, ctx.offsets, (qc, kc, vc, gc, bc, d_out), (dq, dk, dv, dg, dbeta), s0, ds_t, ds0,
                              heads, key_dim, value_dim, device, run)

@@ -295,3 +295,58 @@ def test_workspace_beyond_free_memory_raises_a_clear_error():
         _prep.workspace(1 << 50, torch.device(DEV), "the chunkwise_kda backward")
     assert _prep.workspace(0, torch.device(DEV), "nothing") is None
     assert _prep.workspace(4096, torch.device(DEV), "a small call").numel() == 4096
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float64])
+def test_backward_in_head_groups_matches_one_call(monkeypatch, dtype):
+    # a call whose workspace passes BACKWARD_WORKSPACE_LIMIT runs its heads in
+    # groups (here 5 heads in groups of 2, 2 and 1): the gradients are those of
+    # the single call (the groups' segment plans differ, so to rounding) and
+    # the oracle's
+    from kda import chunkwise, _lib
+
+    B, T, H, K, V = 2, 200, 5, 128, 96
+    inputs, d_out, d_final = _case(B, T, H, K, V, dtype, seed=81)
+    if dtype == torch.float64:
+        inputs, d_final = tuple(t.double() for t in inputs), d_final.double()
+    whole = _gpu_grads(inputs, d_out, d_final)
+    lib = _lib.load()
+    limit = lib.kda_chunk_bwd_workspace_bytes(B, T, 2, K, V)
+    assert lib.kda_chunk_bwd_workspace_bytes(B, T, 3, K, V) > limit
+    monkeypatch.setattr(chunkwise, "BACKWARD_WORKSPACE_LIMIT", limit)
+    assert chunkwise._head_group(lib, B, T, H, K, V) == 2
+    grouped = _gpu_grads(inputs, d_out, d_final)
+    ref = _oracle_grads(inputs, d_out, d_final)
+    same = 1e-12 if dtype == torch.float64 else 1e-5
+    for name, a, b, r in zip(NAMES, grouped, whole, ref):
+        assert rel_err(a, b) < same, (name, rel_err(a, b))
+        assert rel_err(a, r) < TOL.get(dtype, 1e-10), (name, rel_err(a, r))
+
+
+def test_packed_backward_in_head_groups(monkeypatch):
+    # packed documents with the head split: each bucket's call goes in head
+    # groups; every document's gradients still equal those of its own call
+    from kda import chunkwise, _lib
+
+    lens = [150, 140, 60]
+    cu = [0, 150, 290, 350]
+    H, K, V = 3, 64, 64
+    q, k, v, g, beta, _ = workload(1, cu[-1], H, K, V, state_std=0.5, seed=91, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(92)
+    s0 = torch.randn(len(lens), H, K, V, generator=gen) * 0.5
+    d_out = torch.randn(1, cu[-1], H, V, generator=gen).bfloat16()
+    d_final = torch.randn(len(lens), H, K, V, generator=gen)
+    lib = _lib.load()
+    monkeypatch.setattr(chunkwise, "BACKWARD_WORKSPACE_LIMIT", lib.kda_chunk_bwd_workspace_bytes(1, 150, 1, K, V))
+    leaves = [t.to(DEV).requires_grad_() for t in (q, k, v, g, beta, s0)]
+    res = kda.chunkwise_kda(*leaves, True, cu_seqlens=cu)
+    ((res.hidden_states.float() * d_out.to(DEV).float()).sum()
+     + (res.final_state * d_final.to(DEV)).sum()).backward()
+    monkeypatch.undo()
+    for i, (a0, a1) in enumerate(zip(cu[:-1], cu[1:])):
+        doc = [t[:, a0:a1] for t in (q, k, v, g, beta)] + [s0[i:i + 1]]
+        alone = _gpu_grads(doc, d_out[:, a0:a1], d_final[i:i + 1])
+        for name, leaf, b in zip(NAMES, leaves, alone):
+            a = leaf.grad[i:i + 1] if name == "ds0" else leaf.grad[:, a0:a1]
+            assert torch.isfinite(a).all(), (name, i)
+            assert rel_err(a, b) < 1e-2, (name, i, rel_err(a, b))
