@@ -23,9 +23,10 @@ documents (``cu_seqlens``) are differentiated in buckets of similar length:
 documents within a fifth of the bucket's longest are stacked into one
 zero-padded dense batch (zero rows are identity steps of the recurrence), a
 lone document runs on its slice of the packed tensors in place, and each
-bucket's workspace stays within max(the longest document's, 1 GiB).  A call
-whose workspace would pass ``BACKWARD_WORKSPACE_LIMIT`` (4 GiB) runs its
-heads in groups, on contiguous copies of the head slices.  Other
+bucket's workspace stays within max(the longest document's, 1 GiB).  A
+backward call, or a dense prefill, whose workspace would pass
+``WORKSPACE_LIMIT`` (4 GiB) runs its heads in groups, on contiguous copies of
+the head slices.  Other
 cases raise instead of dropping gradients, and so does a second derivative
 (the backward is marked once-differentiable).
 """
@@ -77,6 +78,12 @@ def chunkwise_kda(
                     batch, tokens, heads, key_dim, value_dim)
 
 
+# Most bytes one kernel call may take as workspace before its heads run in
+# groups: the chunk backward's (and the split-bf16 prefill's) is linear in
+# the heads, about 160 KB per token and head at K=V=128.
+WORKSPACE_LIMIT = 4 << 30
+
+
 def _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask, work_dtype, offsets,
              batch, tokens, heads, key_dim, value_dim) -> KDAOperatorOutput:
     lib = _lib.load()
@@ -96,16 +103,39 @@ def _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask
     code = _lib.dtype_code(kernel_dtype)
     # packed documents: the longest document's length is the schedule's hint
     longest = _prep.longest_document(offsets)
-    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, total, longest, heads, key_dim, value_dim, code)
+
+    def need(n_h):
+        return lib.kda_chunk_fwd_workspace_bytes(n_seq, total, longest, n_h, key_dim, value_dim, code)
+
+    # a dense prefill whose workspace passes WORKSPACE_LIMIT (f32 inputs and
+    # shapes off the MFMA path take the split-bf16 chunk path, whose workspace
+    # is the backward's) runs its heads in groups
+    n_h = heads if offsets is not None else _head_group(need, heads)
+    ws_bytes = need(n_h)
     workspace = _prep.workspace(ws_bytes, device, "chunkwise_kda")
-    status = lib.kda_chunk_fwd(
-        qc.data_ptr(), kc.data_ptr(), vc.data_ptr(), gc.data_ptr(), bc.data_ptr(), code,
-        _lib.ptr(s_in), _lib.ptr(s_out), _lib.dtype_code(arith), out.data_ptr(),
-        _lib.ptr(cu), tokens if offsets is None else longest, _lib.ptr(valid), n_seq, total, heads, key_dim,
-        value_dim,
-        _lib.ptr(workspace), ws_bytes, _prep.stream(device),
-    )
-    _lib.check(status)
+
+    def call(ins, s_i, s_o, o, n):
+        status = lib.kda_chunk_fwd(
+            *(t.data_ptr() for t in ins), code,
+            _lib.ptr(s_i), _lib.ptr(s_o), _lib.dtype_code(arith), o.data_ptr(),
+            _lib.ptr(cu), tokens if offsets is None else longest, _lib.ptr(valid), n_seq, total, n, key_dim,
+            value_dim,
+            _lib.ptr(workspace), ws_bytes, _prep.stream(device),
+        )
+        _lib.check(status)
+
+    if n_h == heads:
+        call((qc, kc, vc, gc, bc), s_in, s_out, out, heads)
+    else:
+        for h0 in range(0, heads, n_h):
+            n = min(n_h, heads - h0)
+            o = torch.empty(batch, tokens, n, value_dim, dtype=kernel_dtype, device=device)
+            s_o = None if s_out is None else torch.empty(n_seq, n, key_dim, value_dim, dtype=arith, device=device)
+            call([t.narrow(2, h0, n).contiguous() for t in (qc, kc, vc, gc, bc)],
+                 None if s_in is None else s_in.narrow(1, h0, n).contiguous(), s_o, o, n)
+            out.narrow(2, h0, n).copy_(o)
+            if s_out is not None:
+                s_out.narrow(1, h0, n).copy_(s_o)
     hidden = out if out.dtype == v.dtype else out.to(v.dtype)
     final = None
     if s_out is not None:
@@ -159,24 +189,15 @@ def _document_buckets(lengths: list[int], fits) -> list[list[int]]:
     return buckets
 
 
-# Most bytes one chunk-backward call may take as workspace before the heads
-# are differentiated in groups (its size is linear in the heads: about
-# 160 KB per token and head at K=V=128).
-BACKWARD_WORKSPACE_LIMIT = 4 << 30
-
-
-def _head_group(lib, n_b, n_tok, heads, key_dim, value_dim) -> int:
-    """Heads per chunk-backward call for an [n_b, n_tok] batch: all of them
-    when the workspace fits BACKWARD_WORKSPACE_LIMIT, else the most that fit
-    (at least one)."""
-    def need(n_h):
-        return lib.kda_chunk_bwd_workspace_bytes(n_b, n_tok, n_h, key_dim, value_dim)
-
+def _head_group(need, heads) -> int:
+    """Heads per kernel call: all of them when the call's workspace,
+    need(heads) bytes, fits WORKSPACE_LIMIT, else the most that fit (at least
+    one)."""
     # the size grows with the heads: the largest count that fits, by bisection
     lo, hi = 1, heads
     while lo < hi:
         mid = (lo + hi + 1) // 2
-        if need(mid) <= BACKWARD_WORKSPACE_LIMIT:
+        if need(mid) <= WORKSPACE_LIMIT:
             lo = mid
         else:
             hi = mid - 1
@@ -201,12 +222,15 @@ class _Workspace:
 def _by_head_groups(lib, call, tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, heads, key_dim,
                     value_dim, workspace):
     """One chunk-backward over [n_b, n_tok, heads, *] tensors, split into
-    head groups when the whole call's workspace would pass
-    BACKWARD_WORKSPACE_LIMIT.  Heads are independent in KDA (every state,
-    decay and gradient is per head), so a group is the same computation on
-    contiguous copies of its head slices, its gradients copied back."""
-    n_h = _head_group(lib, n_b, n_tok, heads, key_dim, value_dim)
-    ws_bytes = lib.kda_chunk_bwd_workspace_bytes(n_b, n_tok, n_h, key_dim, value_dim)
+    head groups when the whole call's workspace would pass WORKSPACE_LIMIT.
+    Heads are independent in KDA (every state, decay and gradient is per
+    head), so a group is the same computation on contiguous copies of its
+    head slices, its gradients copied back."""
+    def need(n):
+        return lib.kda_chunk_bwd_workspace_bytes(n_b, n_tok, n, key_dim, value_dim)
+
+    n_h = _head_group(need, heads)
+    ws_bytes = need(n_h)
     ws = workspace.get(ws_bytes)
     if n_h == heads:
         call(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, heads, ws, ws_bytes)
@@ -238,10 +262,10 @@ def _packed_backward(lib, offsets, inputs, grads, s0, ds_t, ds0, heads, key_dim,
     lengths = [b - a for a, b in zip(offsets[:-1], offsets[1:])]
     longest = max(lengths)
     # the workspace a call per document needs anyway (sized for the longest),
-    # or 1 GiB, bounds each bucket's, within BACKWARD_WORKSPACE_LIMIT (past it
-    # a bucket's heads go in groups)
+    # or 1 GiB, bounds each bucket's, within WORKSPACE_LIMIT (past it a
+    # bucket's heads go in groups)
     budget = min(max(lib.kda_chunk_bwd_workspace_bytes(1, longest, heads, key_dim, value_dim), 1 << 30),
-                 BACKWARD_WORKSPACE_LIMIT)
+                 WORKSPACE_LIMIT)
 
     def fits(n, n_tok):
         return lib.kda_chunk_bwd_workspace_bytes(n, n_tok, heads, key_dim, value_dim) <= budget

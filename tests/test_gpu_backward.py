@@ -299,7 +299,7 @@ def test_workspace_beyond_free_memory_raises_a_clear_error():
 
 @pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float64])
 def test_backward_in_head_groups_matches_one_call(monkeypatch, dtype):
-    # a call whose workspace passes BACKWARD_WORKSPACE_LIMIT runs its heads in
+    # a call whose workspace passes WORKSPACE_LIMIT runs its heads in
     # groups (here 5 heads in groups of 2, 2 and 1): the gradients are those of
     # the single call (the groups' segment plans differ, so to rounding) and
     # the oracle's
@@ -313,8 +313,8 @@ def test_backward_in_head_groups_matches_one_call(monkeypatch, dtype):
     lib = _lib.load()
     limit = lib.kda_chunk_bwd_workspace_bytes(B, T, 2, K, V)
     assert lib.kda_chunk_bwd_workspace_bytes(B, T, 3, K, V) > limit
-    monkeypatch.setattr(chunkwise, "BACKWARD_WORKSPACE_LIMIT", limit)
-    assert chunkwise._head_group(lib, B, T, H, K, V) == 2
+    monkeypatch.setattr(chunkwise, "WORKSPACE_LIMIT", limit)
+    assert chunkwise._head_group(lambda n: lib.kda_chunk_bwd_workspace_bytes(B, T, n, K, V), H) == 2
     grouped = _gpu_grads(inputs, d_out, d_final)
     ref = _oracle_grads(inputs, d_out, d_final)
     same = 1e-12 if dtype == torch.float64 else 1e-5
@@ -337,7 +337,7 @@ def test_packed_backward_in_head_groups(monkeypatch):
     d_out = torch.randn(1, cu[-1], H, V, generator=gen).bfloat16()
     d_final = torch.randn(len(lens), H, K, V, generator=gen)
     lib = _lib.load()
-    monkeypatch.setattr(chunkwise, "BACKWARD_WORKSPACE_LIMIT", lib.kda_chunk_bwd_workspace_bytes(1, 150, 1, K, V))
+    monkeypatch.setattr(chunkwise, "WORKSPACE_LIMIT", lib.kda_chunk_bwd_workspace_bytes(1, 150, 1, K, V))
     leaves = [t.to(DEV).requires_grad_() for t in (q, k, v, g, beta, s0)]
     res = kda.chunkwise_kda(*leaves, True, cu_seqlens=cu)
     ((res.hidden_states.float() * d_out.to(DEV).float()).sum()

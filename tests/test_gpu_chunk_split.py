@@ -161,3 +161,31 @@ def test_split_path_equals_the_recurrence_kernel():
                                None, None, code, outs[0][0].data_ptr(), None, T, None, B, B * T, H, K, V, None, 0,
                                stream)
     assert status == _lib.KDA_ERR_WORKSPACE
+
+
+@pytest.mark.parametrize("dtype,K", [(torch.float32, 128), (torch.bfloat16, 100)])
+def test_prefill_in_head_groups(monkeypatch, dtype, K):
+    # a dense prefill on the split-bf16 chunk path (f32 inputs, or bf16 off the
+    # MFMA grid) whose workspace passes WORKSPACE_LIMIT runs its heads in
+    # groups (5 heads in groups of 2, 2 and 1, with right padding): output and
+    # final state equal the single call's (to rounding: the groups' plans
+    # differ) and the recurrence's
+    from kda import chunkwise
+
+    B, T, H, V = 2, 150, 5, 64
+    q, k, v, g, beta, state = workload(B, T, H, K, V, state_std=0.02, seed=45, dtype=dtype)
+    mask = torch.ones(B, T, dtype=torch.bool)
+    mask[1, 90:] = False
+    args = (*_dev(q, k, v, g, beta, state), True, mask.to(DEV))
+    whole = kda.chunkwise_kda(*args)
+    lib = _lib.load()
+    code = _lib.dtype_code(dtype)
+    limit = lib.kda_chunk_fwd_workspace_bytes(B, B * T, 0, 2, K, V, code)
+    assert lib.kda_chunk_fwd_workspace_bytes(B, B * T, 0, 3, K, V, code) > limit
+    monkeypatch.setattr(chunkwise, "WORKSPACE_LIMIT", limit)
+    grouped = kda.chunkwise_kda(*args)
+    ro, rs = c_oracle.recurrent_ref(q, k, v, g, beta, state, valid=[T, 90])
+    same = 1e-5 if dtype == torch.float32 else 1e-2
+    assert rel_err(grouped.hidden_states, whole.hidden_states) < same
+    assert rel_err(grouped.final_state, whole.final_state) < same
+    _check(grouped, ro, rs, TOL32 if dtype == torch.float32 else TOL16, f"{dtype} head groups")

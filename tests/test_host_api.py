@@ -132,19 +132,17 @@ def test_packed_backward_buckets_group_documents_of_similar_length():
     assert [len(b) for b in capped] == [2, 2, 1]
 
 
-def test_backward_head_groups_fit_the_workspace_limit(monkeypatch):
-    # the backward splits a call's heads into the largest groups whose
-    # workspace fits BACKWARD_WORKSPACE_LIMIT (at least one head a group)
+def test_head_groups_fit_the_workspace_limit(monkeypatch):
+    # a call whose workspace passes WORKSPACE_LIMIT runs the largest head
+    # groups that fit (at least one head a group)
     from kda import chunkwise
 
-    class Lib:
-        @staticmethod
-        def kda_chunk_bwd_workspace_bytes(B, T, H, K, V):
-            return 1000 + B * T * H * 10
+    def need(B, T):
+        return lambda H: 1000 + B * T * H * 10
 
-    lib = Lib()
-    monkeypatch.setattr(chunkwise, "BACKWARD_WORKSPACE_LIMIT", 1000 + 10 * 64 * 10)
-    assert chunkwise._head_group(lib, 1, 10, 64, 128, 128) == 64
-    assert chunkwise._head_group(lib, 2, 10, 64, 128, 128) == 32
-    assert chunkwise._head_group(lib, 1, 30, 64, 128, 128) == 21
-    assert chunkwise._head_group(lib, 1, 10 ** 6, 64, 128, 128) == 1
+    monkeypatch.setattr(chunkwise, "WORKSPACE_LIMIT", 1000 + 10 * 64 * 10)
+    assert chunkwise._head_group(need(1, 10), 64) == 64
+    assert chunkwise._head_group(need(2, 10), 64) == 32
+    assert chunkwise._head_group(need(1, 30), 64) == 21
+    assert chunkwise._head_group(need(1, 10 ** 6), 64) == 1
+    assert chunkwise._head_group(lambda H: 0, 8) == 8
