@@ -243,7 +243,7 @@ def _by_head_groups(lib, call, tensors, grads_out, s_init, ds_fin, ds_init, n_b,
         h1 = min(heads, h0 + n_h)
         ins = [part(t, h0, h1, 2) for t in tensors]
         outs = [torch.empty_like(t) for t in ins[:5]]
-        ds_g = None if ds_init is None else torch.empty_like(part(ds_init, h0, h1, 1))
+        ds_g = None if ds_init is None else ds_init.new_empty((n_b, h1 - h0) + tuple(ds_init.shape[2:]))
         call(ins, outs, part(s_init, h0, h1, 1), part(ds_fin, h0, h1, 1), ds_g, n_b, n_tok, h1 - h0, ws,
              ws_bytes)
         for dst, src in zip(grads_out, outs):
