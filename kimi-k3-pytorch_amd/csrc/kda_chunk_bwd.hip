@@ -17,9 +17,9 @@
 //   dA = diag(b) dL, then the pair sums of dA and dAqk with exact exponents,
 //   the exp factors, and dg = reverse cumulative sum of d lg over the chunk.
 //
-// f32 accumulation everywhere.  prep and pair multiply on the f32 MFMA
-// (v_mfma_f32_16x16x4f32); the state scans and grad's slab products use
-// split-bf16 operands on v_mfma_f32_16x16x32_bf16 (x = hi + lo, hi = bf16(x),
+// f32 accumulation everywhere.  pair and prep's inverse and W, U products
+// multiply on the f32 MFMA (v_mfma_f32_16x16x4f32); prep's decay products A
+// and Aqk, the state scans and grad's slab products use split-bf16 operands on v_mfma_f32_16x16x32_bf16 (x = hi + lo, hi = bf16(x),
 // lo = bf16(x - hi); hi*hi + hi*lo + lo*hi, dropping terms of relative size
 // 2^-17), which keeps the f32-input gradients within about 1e-5 of the f64
 // oracle.  Decay products use a 16-row block factorisation on the MFMA, with
@@ -421,32 +421,52 @@ __device__ __forceinline__ bool needs_exact(const float* lgS, bool nonneg, int t
 
 // accK += sum_c (k_i e^(lg_i - r)) (k_j e^(r - lg_j)) and accQ the same with
 // q_i, for rows i in [r0, r0+16), columns j in [c0, c0+16) and r = lg[rr];
-// the reduction runs over the kd channels.
+// the reduction runs over the kd channels from kb (kd a multiple of 16).  The
+// decayed operands are split into bf16 hi + lo and multiplied on
+// v_mfma_f32_16x16x32_bf16 (hi*hi + hi*lo + lo*hi, three products per 32
+// channels against eight f32 MFMAs per 16); lane (i, g) carries channels
+// k0 + 8g .. k0 + 8g + 7 of row r0 + i and of column c0 + i, and with 16
+// channels left the lane groups g >= 2 carry zeros.
 __device__ __forceinline__ void decay_product(f32x4& accK, f32x4& accQ, const float* kS, const float* qS,
                                               const float* lgS, int r0, int c0, int rr, int kd, int kb = 0) {
   const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
-  f32x4 accK2 = zero4(), accQ2 = zero4();  // odd steps: four chains instead of two
-  for (int k0 = kb; k0 < kb + kd; k0 += 16) {
-    float ka[4], qa[4], kb[4];
+  for (int k0 = kb; k0 < kb + kd; k0 += 32) {
+    const bool live = 8 * g < kb + kd - k0;
+    bf16x8 kah, kal, qah, qal, kbh, kbl;
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int ch = k0 + 4 * u + g;
-      const float r = lgS[rr * kRS + ch];
-      const float ea = fast_exp(lgS[(r0 + i) * kRS + ch] - r), eb = fast_exp(r - lgS[(c0 + i) * kRS + ch]);
-      ka[u] = kS[(r0 + i) * kRS + ch] * ea;
-      qa[u] = qS[(r0 + i) * kRS + ch] * ea;
-      kb[u] = kS[(c0 + i) * kRS + ch] * eb;
-    }
+    for (int e = 0; e < 8; e += 4) {
+      const int ch = k0 + 8 * g + e;
+      f32x4 r4 = zero4(), la = zero4(), lb = zero4(), ka = zero4(), qa = zero4(), kv = zero4();
+      if (live) {
+        r4 = *reinterpret_cast<const f32x4*>(&lgS[rr * kRS + ch]);
+        la = *reinterpret_cast<const f32x4*>(&lgS[(r0 + i) * kRS + ch]);
+        lb = *reinterpret_cast<const f32x4*>(&lgS[(c0 + i) * kRS + ch]);
+        ka = *reinterpret_cast<const f32x4*>(&kS[(r0 + i) * kRS + ch]);
+        qa = *reinterpret_cast<const f32x4*>(&qS[(r0 + i) * kRS + ch]);
+        kv = *reinterpret_cast<const f32x4*>(&kS[(c0 + i) * kRS + ch]);
+      }
 #pragma unroll
-    for (int u = 0; u < 4; u += 2) {
-      accK = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[u], kb[u], accK, 0, 0, 0);
-      accQ = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[u], kb[u], accQ, 0, 0, 0);
-      accK2 = __builtin_amdgcn_mfma_f32_16x16x4f32(ka[u + 1], kb[u + 1], accK2, 0, 0, 0);
-      accQ2 = __builtin_amdgcn_mfma_f32_16x16x4f32(qa[u + 1], kb[u + 1], accQ2, 0, 0, 0);
+      for (int u = 0; u < 4; ++u) {
+        const float ea = fast_exp(la[u] - r4[u]), eb = fast_exp(r4[u] - lb[u]);
+        __bf16 h, l;
+        split_bf16(ka[u] * ea, h, l);
+        kah[e + u] = h;
+        kal[e + u] = l;
+        split_bf16(qa[u] * ea, h, l);
+        qah[e + u] = h;
+        qal[e + u] = l;
+        split_bf16(kv[u] * eb, h, l);
+        kbh[e + u] = h;
+        kbl[e + u] = l;
+      }
     }
+    accK = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kah, kbh, accK, 0, 0, 0);
+    accQ = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qah, kbh, accQ, 0, 0, 0);
+    accK = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kah, kbl, accK, 0, 0, 0);
+    accQ = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qah, kbl, accQ, 0, 0, 0);
+    accK = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kal, kbh, accK, 0, 0, 0);
+    accQ = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qal, kbh, accQ, 0, 0, 0);
   }
-  accK += accK2;
-  accQ += accQ2;
 }
 
 // The ten 16x16 block pairs (I, J <= I) of a chunk.
