@@ -601,7 +601,7 @@ def measured_traffic(kernel, counters=None):
         return None
 
 
-def counters_summary(dirs, out=None):
+def counters_summary(dirs, out=None, tag=None):
     """Summarise rocprofv3 --pmc runs over `--profile-pass` (one directory per
     pass, each with run_counter_collection.csv) into profiles/kernel_counters.json
     and a markdown table on stdout.  HBM bytes come from the TCC/EA request
@@ -668,6 +668,29 @@ def counters_summary(dirs, out=None):
         "rules": " ".join(counters_summary.__doc__.split("HBM bytes come from")[1].split()),
         "kernels": kernels,
     }
+    if tag is not None:
+        # one prefill configuration: this library's kernels under "<tag>::",
+        # merged into the record of the same sources (a record of other
+        # sources is dropped)
+        kernels = {f"{tag}::{k}": e for k, e in kernels.items() if e["source"] is not None}
+        try:
+            old = json.loads(Path(out or COUNTERS_FILE).read_text())
+        except (OSError, ValueError):
+            old = {}
+        merged = dict(old.get("kernels", {})) if old.get("source_hashes") == data["source_hashes"] else {}
+        merged.update(kernels)
+        data = dict(old or data, source_hashes=data["source_hashes"], kernels=merged)
+        Path(out or COUNTERS_FILE).write_text(json.dumps(data, indent=1, sort_keys=True) + "\n")
+        print("| kernel | dispatches | read MB | written MB | MFMA busy % | bf16 MFMA GFLOP | of bf16 peak | "
+              "us (counter run) |")
+        print("|---|---|---|---|---|---|---|---|")
+        for key in sorted(kernels):
+            e = kernels[key]
+            fmt = lambda x, sc=1e6: "—" if x is None else f"{x / sc:.1f}"  # noqa: E731
+            print(f"| `{key}` | {e['dispatches']} | {fmt(e.get('read_bytes'))} | {fmt(e.get('write_bytes'))} | "
+                  f"{e.get('mfma_busy_pct', '—')} | {fmt(e.get('mfma_bf16_flop'), 1e9)} | "
+                  f"{e.get('mfma_bf16_frac_of_peak', '—')} | {e.get('counter_run_us', '—')} |")
+        return
     # the 256 MiB device copy of the profile pass (the runtime's copy kernel also
     # serves torch's small copies; the largest dispatch is this one)
     copies = [(r, w) for key, cs in per.items() if "copyBuffer" in key
@@ -699,15 +722,24 @@ def counters_summary(dirs, out=None):
         print(f"copy check: {data['copy_check']}")
 
 
-def profile_pass():
+def profile_pass(which="all"):
     """The workload of the counter runs: after one warm-up round, one prefill at
     the benchmark shape, one in-place decode step at the benchmark shape, and a
     256 MiB device-to-device copy whose byte counts check the counters; then
     the fused stages, the backward and the cache reorder legs once each (their
-    warm-up calls included)."""
+    warm-up calls included).  With a configuration name: that prefill only,
+    a warm-up call and a measured one."""
     import torch
 
     import kda
+
+    if which != "all":
+        call, _ = config_call(which)
+        call()
+        call()
+        torch.cuda.synchronize()
+        print(f"profile pass {which} done", flush=True)
+        return
 
     device = torch.device("cuda", 0)
     q, k, v, g, beta, s0 = _inputs(P_B, P_T, P_H, P_K, P_V, 0.02, 0, device)
@@ -768,13 +800,19 @@ def bench_dropin(steps, warmup):
     }
 
 
-def bench_configs(steps, warmup):
-    """The other prefill configurations the metric reports as tokens/s and
-    roofline: B=8, T=1024, H=8 (zero initial state, final state out) and the
-    packed documents cu_seqlens = [0, 32768, 49152, 61440, 65536] at H=64
-    (per-document final states), K=V=128, bf16, through the C ABI with the
-    workspace preallocated; inputs drawn on the GPU with the distributions of
-    the prefill workload."""
+# The other prefill configurations, by the key their counter records carry.
+PREFILL_CONFIGS = {
+    "b8_t1024_h8": (8, 1024, 8, 128, None),
+    "packed_4docs_t65536_h64": (1, 65536, 64, 128, [0, 32768, 49152, 61440, 65536]),
+    "k64_t8192_h16": (1, 8192, 16, 64, None),
+}
+
+
+def config_call(name):
+    """The C-ABI prefill of one configuration with its inputs on the GPU (drawn
+    with the distributions of the prefill workload), its workspace
+    preallocated: (call, metadata).  The K=V=64 shape starts from an
+    N(0, 0.02) state, as the long-context workload does."""
     import torch
 
     from kda import _lib
@@ -783,59 +821,92 @@ def bench_configs(steps, warmup):
     device = torch.device("cuda", 0)
     code = _lib.dtype_code(torch.bfloat16)
     stream = torch.cuda.current_stream(device).cuda_stream
+    B, T, H, K, offsets = PREFILL_CONFIGS[name]
+    V = K
+    gen = torch.Generator(device=device).manual_seed(5)
+    shape_k = (B, T, H, K)
+    q = torch.nn.functional.normalize(torch.randn(shape_k, generator=gen, device=device), dim=-1).bfloat16()
+    k = torch.nn.functional.normalize(torch.randn(shape_k, generator=gen, device=device), dim=-1).bfloat16()
+    v = torch.randn(B, T, H, V, generator=gen, device=device).bfloat16()
+    g = (-torch.nn.functional.softplus(torch.randn(shape_k, generator=gen, device=device) + 2)).bfloat16()
+    beta = torch.sigmoid(torch.randn(B, T, H, generator=gen, device=device)).bfloat16()
+    n_seq = B if offsets is None else len(offsets) - 1
+    s_in = None
+    if name.startswith("k64"):
+        s_in = torch.randn(n_seq, H, K, V, generator=gen, device=device).mul_(0.02)
+    o = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=device)
+    s_out = torch.empty(n_seq, H, K, V, dtype=torch.float32, device=device)
+    cu = None if offsets is None else torch.tensor(offsets, dtype=torch.int32, device=device)
+    # dense: tokens per sequence; packed documents: the longest document,
+    # which a caller that packs them knows (the schedule's hint)
+    span = T if offsets is None else max(b - a for a, b in zip(offsets[:-1], offsets[1:]))
+    longest = 0 if offsets is None else span
+    ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, B * T, longest, H, K, V, code)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
+    keep = (q, k, v, g, beta, s_in, o, s_out, cu, ws)
+    args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code, _lib.ptr(s_in),
+            s_out.data_ptr(), 0, o.data_ptr(), _lib.ptr(cu), span, None, n_seq, B * T, H, K, V, ws.data_ptr(),
+            ws_bytes, stream)
+
+    def call(_keep=keep):
+        _lib.check(lib.kda_chunk_fwd(*args))
+
+    L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
+    _lib.check(lib.kda_chunk_fwd_plan(n_seq, B * T, longest, H, K, V, code, ctypes.byref(L), ctypes.byref(segs)))
+    n_state_io = 1 if s_in is None else 2
+    meta = {
+        "workload": f"kda chunkwise prefill B={B} T={T} H={H} K=V={K} bf16, "
+                    + ("N(0,0.02) initial state, " if s_in is not None else "zero initial state, ")
+                    + ("final state out" if offsets is None else f"cu_seqlens={offsets}, per-document final states"),
+        "tokens": B * T,
+        "algorithmic_bytes": 2 * B * T * H * (3 * K + V) + 2 * B * T * H + 2 * B * T * H * V
+                             + 4 * n_state_io * n_seq * H * K * V,
+        "algorithmic_flops": prefill_flops(B, T, H, K, V),
+        "chunks_per_segment": L.value,
+    }
+    return call, meta
+
+
+def bench_configs(steps, warmup, counters=None):
+    """The other prefill configurations the metric reports as tokens/s and
+    roofline: B=8, T=1024, H=8 (zero initial state, final state out), the
+    packed documents cu_seqlens = [0, 32768, 49152, 61440, 65536] at H=64
+    (per-document final states), both K=V=128, and the reference's shipped
+    head shape K=V=64 at B=1, T=8192, H=16; bf16, through the C ABI with the
+    workspace preallocated.  Each carries the HBM bytes and MFMA busy of its
+    kernels from the committed counter record under its own key."""
+    import torch
+
     out = {}
-    for name, (B, T, H, offsets) in {
-        "b8_t1024_h8": (8, 1024, 8, None),
-        "packed_4docs_t65536_h64": (1, 65536, 64, [0, 32768, 49152, 61440, 65536]),
-    }.items():
-        K = V = 128
-        gen = torch.Generator(device=device).manual_seed(5)
-        shape_k = (B, T, H, K)
-        q = torch.nn.functional.normalize(torch.randn(shape_k, generator=gen, device=device), dim=-1).bfloat16()
-        k = torch.nn.functional.normalize(torch.randn(shape_k, generator=gen, device=device), dim=-1).bfloat16()
-        v = torch.randn(B, T, H, V, generator=gen, device=device).bfloat16()
-        g = (-torch.nn.functional.softplus(torch.randn(shape_k, generator=gen, device=device) + 2)).bfloat16()
-        beta = torch.sigmoid(torch.randn(B, T, H, generator=gen, device=device)).bfloat16()
-        n_seq = B if offsets is None else len(offsets) - 1
-        o = torch.empty(B, T, H, V, dtype=torch.bfloat16, device=device)
-        s_out = torch.empty(n_seq, H, K, V, dtype=torch.float32, device=device)
-        cu = None if offsets is None else torch.tensor(offsets, dtype=torch.int32, device=device)
-        # dense: tokens per sequence; packed documents: the longest document,
-        # which a caller that packs them knows (the schedule's hint)
-        span = T if offsets is None else max(b - a for a, b in zip(offsets[:-1], offsets[1:]))
-        longest = 0 if offsets is None else span
-        ws_bytes = lib.kda_chunk_fwd_workspace_bytes(n_seq, B * T, longest, H, K, V, code)
-        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=device)
-        args = (q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code, None,
-                s_out.data_ptr(), 0, o.data_ptr(), _lib.ptr(cu), span, None, n_seq, B * T, H, K, V, ws.data_ptr(),
-                ws_bytes, stream)
-        _settle(lambda: _lib.check(lib.kda_chunk_fwd(*args)))
+    for name in PREFILL_CONFIGS:
+        call, meta = config_call(name)
+        _settle(call)
         for _ in range(warmup):
-            _lib.check(lib.kda_chunk_fwd(*args))
+            call()
         torch.cuda.synchronize()
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(steps):
-            _lib.check(lib.kda_chunk_fwd(*args))
+            call()
         e1.record()
         torch.cuda.synchronize()
         ms = e0.elapsed_time(e1) / steps
-        nbytes = 2 * B * T * H * (3 * K + V) + 2 * B * T * H + 2 * B * T * H * V + 4 * n_seq * H * K * V
-        flops = prefill_flops(B, T, H, K, V)
-        L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
-        _lib.check(lib.kda_chunk_fwd_plan(n_seq, B * T, longest, H, K, V, code, ctypes.byref(L), ctypes.byref(segs)))
+        nbytes, flops = meta["algorithmic_bytes"], meta["algorithmic_flops"]
+        rec = {k: v for k, v in (counters or {}).get("kernels", {}).items() if k.startswith(name + "::")}
         out[name] = {
-            "workload": f"kda chunkwise prefill B={B} T={T} H={H} K=V=128 bf16, zero initial state, "
-                        + ("final state out" if offsets is None else f"cu_seqlens={offsets}, per-document final states"),
+            "workload": meta["workload"],
             "ms": round(ms, 5),
-            "tokens_per_s": round(B * T / (ms * 1e-3), 1),
+            "tokens_per_s": round(meta["tokens"] / (ms * 1e-3), 1),
             "algorithmic_bytes": nbytes,
             "achieved_gbs": round(nbytes / (ms * 1e-3) / 1e9, 1),
             "frac_hbm": round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
             "frac_bf16_mfma": round(flops / (ms * 1e-3) / 1e12 / BF16_PEAK_TFLOPS, 4),
-            "chunks_per_segment": L.value,
+            "chunks_per_segment": meta["chunks_per_segment"],
+            "traffic": (sum(int(e["read_bytes"] + e["write_bytes"]) for e in rec.values())
+                        if rec and all("read_bytes" in e and "write_bytes" in e for e in rec.values()) else None),
+            "kernels_mfma_busy_pct": {k.split("::", 1)[1]: e.get("mfma_busy_pct") for k, e in rec.items()} or None,
         }
-        del q, k, v, g, beta, o, ws
+        del call
     return out
 
 
@@ -903,14 +974,19 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--no-cpu-baseline", action="store_true")
-    ap.add_argument("--profile-pass", action="store_true",
-                    help="run the counter-collection workload only (for rocprofv3 --pmc)")
+    ap.add_argument("--profile-pass", nargs="?", const="all", default=None,
+                    choices=["all", *PREFILL_CONFIGS],
+                    help="run the counter-collection workload only (for rocprofv3 --pmc): all legs, or one "
+                         "prefill configuration")
     ap.add_argument("--counters-summary", nargs="+", metavar="DIR",
                     help="summarise rocprofv3 --pmc output directories into profiles/kernel_counters.json")
     ap.add_argument("--counters-out", default=None, help="where --counters-summary writes its JSON")
+    ap.add_argument("--counters-tag", default=None, choices=list(PREFILL_CONFIGS),
+                    help="file the summarised kernels under this prefill configuration's key, merged into "
+                         "the existing record")
     args = ap.parse_args()
     if args.counters_summary:
-        counters_summary(args.counters_summary, args.counters_out)
+        counters_summary(args.counters_summary, args.counters_out, args.counters_tag)
         return 0
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (the KDA operator has no collective; --gpus {args.gpus} "
@@ -923,7 +999,7 @@ def main() -> int:
         print("bench.py needs a ROCm GPU", file=sys.stderr)
         return 1
     if args.profile_pass:
-        profile_pass()
+        profile_pass(args.profile_pass)
         return 0
 
     ms, per_kernel, ws_bytes, settle = bench_prefill(args.steps, args.warmup, settle_ms=SETTLE_MS)
@@ -1022,7 +1098,7 @@ def main() -> int:
         "algorithmic_bytes": k64_bytes,
     }
     result["prefill_f32"] = bench_prefill_f32(args.steps, args.warmup)
-    result["prefill_configs"] = bench_configs(args.steps, args.warmup)
+    result["prefill_configs"] = bench_configs(args.steps, args.warmup, counters)
     result["decay_fusion"] = bench_decay_fusion()
     result["backward"] = bench_backward()
     result["cache_reorder"] = bench_cache()

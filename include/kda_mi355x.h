@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 8
+#define KDA_ABI_VERSION 9
 
 /* status codes */
 #define KDA_OK 0
@@ -122,6 +122,17 @@ int kda_chunk_fwd_plan(int64_t num_seqs, int64_t total_tokens, int64_t longest_t
                        int64_t* segments);
 
 /*
+ * Overrides the segment length that kda_chunk_fwd and kda_chunk_fwd_decay
+ * choose for the MFMA prefill (process-wide, every device): a positive value
+ * forces that many chunks per segment, 0 one segment per sequence, -1
+ * restores the library's own plan.  Results do not depend on the schedule;
+ * tests use it to cover the segmented composition at small sizes.  No
+ * reference counterpart (the reference has no schedule).  Returns
+ * KDA_ERR_INVALID_ARGUMENT below -1.
+ */
+int kda_set_segment_chunks(int64_t chunks_per_segment);
+
+/*
  * Chunkwise-parallel KDA prefill (chunk 64): intra-chunk UT transform with a
  * forward-substitution solve, bf16 MFMA chunk products with f32 accumulation
  * and an f32 inter-chunk state scan, cut into segments whose affine state
@@ -189,7 +200,9 @@ int kda_chunk_fwd_decay(const void* q, const void* k, const void* v, const void*
  * calls that overlap on one GPU (two streams, two host threads) race.  The
  * stream must belong to the current device.
  */
+#ifndef KDA_NOALLOC_SCRATCH_BYTES
 #define KDA_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
+#endif
 int kda_chunk_fwd_noalloc(const void* q, const void* k, const void* v, const void* g,
                           const void* beta, int in_dtype, const void* initial_state,
                           void* final_state, int state_dtype, void* out,

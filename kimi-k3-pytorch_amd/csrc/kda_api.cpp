@@ -7,6 +7,9 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
+#include <set>
+#include <utility>
 
 #include "kda_common.h"
 #include "kda_launch.h"
@@ -32,6 +35,18 @@ int check_launch(const char* what) {
     return KDA_ERR_LAUNCH;
   }
   return KDA_OK;
+}
+
+bool reserve_lds(const void* kernel, int bytes) {
+  static std::mutex mu;
+  static std::set<std::pair<const void*, int>> done;  // (kernel, device ordinal)
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return false;
+  std::lock_guard<std::mutex> lock(mu);
+  if (done.count({kernel, dev}) != 0) return true;
+  if (hipFuncSetAttribute(kernel, hipFuncAttributeMaxDynamicSharedMemorySize, bytes) != hipSuccess) return false;
+  done.insert({kernel, dev});
+  return true;
 }
 
 static bool is_input_dtype(int d) {
@@ -91,6 +106,16 @@ using namespace kda_host;
 extern "C" {
 
 int kda_abi_version(void) { return KDA_ABI_VERSION; }
+
+int kda_set_segment_chunks(int64_t chunks_per_segment) {
+  if (chunks_per_segment < -1) {
+    kda_host::set_detail("chunks_per_segment must be -1 (the library's plan), 0 or positive, got %lld",
+                         (long long)chunks_per_segment);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  kda_host::set_segment_override(chunks_per_segment);
+  return KDA_OK;
+}
 
 const char* kda_status_string(int status) {
   const char* base = "unknown status";

@@ -58,6 +58,7 @@
 //   chunks take an exact pairwise-exponent path for the diagonal blocks (the
 //   reference evaluates every tile with an explicit pairwise exponent,
 //   src/kda/utils.py:128-136).
+#include <atomic>
 #include <cstdlib>
 
 #include "kda_launch.h"
@@ -1834,15 +1835,12 @@ struct Plan {
   int64_t chunks_bound;  // upper bound on the total number of chunks
 };
 
-// KDA_MI355X_SEGMENT_CHUNKS=<L> (L >= 1) forces L chunks per segment; 0 forces
-// one segment per sequence.  The result does not depend on it (tests use it
-// to cover both schedules at small sizes).
-static int64_t segment_override() {
-  const char* env = getenv("KDA_MI355X_SEGMENT_CHUNKS");
-  if (env == nullptr || *env == '\0') return -1;
-  const long v = strtol(env, nullptr, 10);
-  return v < 0 ? -1 : v;
-}
+// The schedule override of kda_set_segment_chunks: L >= 1 forces L chunks
+// per segment, 0 one segment per sequence, -1 (the default) the plan below.
+// The result does not depend on it (tests use it to cover both schedules at
+// small sizes); the environment plays no part in the schedule.
+static std::atomic<int64_t> g_segment_override{-1};
+static int64_t segment_override() { return g_segment_override.load(std::memory_order_relaxed); }
 
 // `longest` (packed documents only, 0 when unknown): the longest document in
 // tokens.  Documents of uneven length that alone fill the GPU would leave it
@@ -1909,14 +1907,10 @@ static void mark(kda_host::KernelEvents* ev, int i, hipStream_t stream) {
 
 template <class IT, int MODE, bool DECAY, bool PAD, int KT>
 static int launch_segments(const SegArgs<IT>& sa, const Plan& p, int64_t H, hipStream_t stream) {
-  static bool attr_done = false;
-  if (!attr_done) {
-    if (hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_segment_kernel<IT, MODE, DECAY, PAD, KT>),
-                            hipFuncAttributeMaxDynamicSharedMemorySize, kSmemBytes) != hipSuccess) {
-      kda_host::set_detail("cannot reserve %d bytes of LDS for chunk_segment_kernel", kSmemBytes);
-      return KDA_ERR_LAUNCH;
-    }
-    attr_done = true;
+  if (!kda_host::reserve_lds(reinterpret_cast<const void*>(&chunk_segment_kernel<IT, MODE, DECAY, PAD, KT>),
+                             kSmemBytes)) {
+    kda_host::set_detail("cannot reserve %d bytes of LDS for chunk_segment_kernel", kSmemBytes);
+    return KDA_ERR_LAUNCH;
   }
   hipLaunchKernelGGL((chunk_segment_kernel<IT, MODE, DECAY, PAD, KT>), dim3(static_cast<unsigned>(p.segs_bound * H * p.ncg)),
                      dim3(kThreads), kSmemBytes, stream, sa);
@@ -2142,5 +2136,7 @@ int launch_chunk_decay(const void* q, const void* k, const void* v, const void* 
   return run_chunk<f16, true>(q, k, v, z, beta, s_in, s_out, out, seq, N, total_tokens, H, K, V, workspace, stream,
                               nullptr, &d);
 }
+
+void set_segment_override(int64_t chunks) { kda::g_segment_override.store(chunks, std::memory_order_relaxed); }
 
 }  // namespace kda_host

@@ -126,4 +126,10 @@ namespace kda_host {
 void set_detail(const char* fmt, ...);
 const char* detail();
 int check_launch(const char* what);
+// Raise `kernel`'s dynamic LDS limit to `bytes` on the current device, once
+// per (kernel, device): the attribute belongs to the kernel on each device,
+// and concurrent first calls from several threads set it under one lock.
+bool reserve_lds(const void* kernel, int bytes);
+// Segment-length override of the chunk prefill's plan (kda_set_segment_chunks).
+void set_segment_override(int64_t chunks);
 }  // namespace kda_host

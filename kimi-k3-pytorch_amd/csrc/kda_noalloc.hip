@@ -16,10 +16,6 @@
 
 #include "kda_launch.h"
 
-#ifndef KDA_NOALLOC_SCRATCH_BYTES
-#define KDA_NOALLOC_SCRATCH_BYTES ((size_t)128 << 20)
-#endif
-
 static constexpr size_t kScratchBytes = static_cast<size_t>(KDA_NOALLOC_SCRATCH_BYTES);
 static_assert(kScratchBytes % 256 == 0, "scratch size must keep 256-byte alignment");
 

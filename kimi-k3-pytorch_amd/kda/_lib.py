@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libkda_mi355x.so")
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 KDA_OK = 0
 KDA_ERR_INVALID_ARGUMENT = 1
@@ -47,6 +47,7 @@ SIGNATURES = {
     "kda_decode_step": (_I, [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _L, _L, _L, _L, _P]),
     "kda_chunk_fwd_workspace_bytes": (_S, [_L, _L, _L, _L, _L, _L, _I]),
     "kda_chunk_fwd_plan": (_I, [_L, _L, _L, _L, _L, _L, _I, _P, _P]),
+    "kda_set_segment_chunks": (_I, [_L]),
     "kda_chunk_fwd": (
         _I,
         [_P, _P, _P, _P, _P, _I, _P, _P, _I, _P, _P, _L, _P, _L, _L, _L, _L, _L, _P, _S, _P],
@@ -122,6 +123,12 @@ def check(status: int) -> None:
     if status != KDA_OK:
         text = load().kda_status_string(status).decode(errors="replace")
         raise RuntimeError(f"kda_mi355x: {text}")
+
+
+def set_segment_chunks(chunks_per_segment: int) -> None:
+    """Force the MFMA prefill's segment length (process-wide): L >= 1 chunks
+    per segment, 0 one segment per sequence, -1 the library's own plan."""
+    check(load().kda_set_segment_chunks(int(chunks_per_segment)))
 
 
 def dtype_code(dtype: torch.dtype) -> int:

@@ -28,12 +28,17 @@ def workspace(nbytes: int, device: torch.device, what: str) -> torch.Tensor | No
 def kernel_inputs(q, k, v, g, beta, work_dtype: torch.dtype):
     """Pick the element type the kernels read and make the inputs contiguous.
 
-    The reference upcasts every input to the work dtype before any arithmetic
+    The reference casts every input to the work dtype before any arithmetic
     (src/kda/chunkwise.py:41-45, src/kda/recurrent.py:42-46).  The kernels do
     that upcast on load, so inputs that already share one dtype are passed
     as they are (bf16 stays bf16 in HBM).  Mixed dtypes are cast to the
-    arithmetic type first, which loses nothing.
+    arithmetic type first, which loses nothing.  A bf16/f16 work dtype
+    (``accumulate_state_in_fp32=False``) rounds every input to it first, as
+    the reference's cast does; the kernels then compute in f32 on those
+    rounded values, with results in the work dtype.
     """
+    if work_dtype in (torch.bfloat16, torch.float16):
+        q, k, v, g, beta = (t.to(work_dtype) for t in (q, k, v, g, beta))
     tensors = (q, k, v, g, beta)
     dtypes = {t.dtype for t in tensors}
     arith = torch.float64 if work_dtype == torch.float64 else torch.float32
@@ -58,9 +63,15 @@ def valid_lengths(attention_mask: torch.Tensor | None, device: torch.device) -> 
     return attention_mask.to(device=device).sum(dim=1, dtype=torch.int32).contiguous()
 
 
-def state_arg(initial_state: torch.Tensor | None, arith: torch.dtype) -> torch.Tensor | None:
+def state_arg(initial_state: torch.Tensor | None, arith: torch.dtype,
+              work_dtype: torch.dtype | None = None) -> torch.Tensor | None:
+    """The initial state in the kernels' arithmetic type.  The reference starts
+    from ``initial_state.to(work_dtype)`` (src/kda/chunkwise.py:49-58,
+    src/kda/recurrent.py:50-59), so a bf16/f16 work dtype rounds it first."""
     if initial_state is None:
         return None
+    if work_dtype in (torch.bfloat16, torch.float16):
+        initial_state = initial_state.to(work_dtype)
     return initial_state.to(arith).contiguous()
 
 

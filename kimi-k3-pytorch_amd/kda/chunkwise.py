@@ -91,7 +91,7 @@ def _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask
     device = q.device
     n_seq = batch if offsets is None else len(offsets) - 1
     total = batch * tokens
-    s_in = _prep.state_arg(initial_state, arith)
+    s_in = _prep.state_arg(initial_state, arith, work_dtype)
     s_out = (
         torch.empty(n_seq, heads, key_dim, value_dim, dtype=arith, device=device)
         if output_final_state
@@ -344,7 +344,7 @@ class _ChunkwiseFunction(torch.autograd.Function):
             d_hidden = torch.zeros(batch, tokens, heads, value_dim, dtype=kernel_dtype, device=device)
         d_out = d_hidden.to(kernel_dtype).contiguous()
         state_dtype = torch.float64 if kernel_dtype == torch.float64 else torch.float32
-        s0 = None if initial_state is None else initial_state.detach().to(state_dtype).contiguous()
+        s0 = _prep.state_arg(None if initial_state is None else initial_state.detach(), state_dtype, ctx.work_dtype)
         ds_t = None if d_final is None else d_final.to(state_dtype).contiguous()
         dq, dk, dv, dg = (torch.empty_like(t) for t in (qc, kc, vc, gc))
         dbeta = torch.empty_like(bc)

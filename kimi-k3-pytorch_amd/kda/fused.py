@@ -23,6 +23,8 @@ rounds after each step in the model dtype.
 
 from __future__ import annotations
 
+import warnings
+
 import torch
 
 from . import _lib, _prep
@@ -30,6 +32,22 @@ from .state import ShortConvState
 from .utils import validate_attention_mask
 
 _DTYPES = (torch.float32, torch.float16, torch.bfloat16, torch.float64)
+
+
+def _alert_nondeterministic(what: str) -> None:
+    """The parameter gradients of the fused-stage backwards are summed over
+    workgroups with float atomics, so their rounding can change from run to
+    run.  Under ``torch.use_deterministic_algorithms(True)`` this raises, as
+    torch's own nondeterministic operations do (a warning with
+    ``warn_only=True``); the input gradients are deterministic and unaffected."""
+    if not torch.are_deterministic_algorithms_enabled():
+        return
+    msg = (f"{what} sums its parameter gradients with float atomics and has no deterministic "
+           "implementation; turn off torch.use_deterministic_algorithms or keep the parameters frozen")
+    if torch.is_deterministic_algorithms_warn_only_enabled():
+        warnings.warn(msg)
+    else:
+        raise RuntimeError(msg)
 
 
 def _check_dtype(name: str, tensor: torch.Tensor, dtype: torch.dtype) -> None:
@@ -180,6 +198,8 @@ class _ConvSilu(torch.autograd.Function):
         hc = None if hist is None or kernel_size == 1 else _aligned(hist)
         dx = torch.empty_like(xc)
         need_w, need_b, need_h = ctx.needs_input_grad[1], ctx.needs_input_grad[2], ctx.needs_input_grad[3]
+        if need_w or (need_b and bias is not None):
+            _alert_nondeterministic("the ShortConv+SiLU backward (kda_conv_silu_bwd)")
         acc = _acc_dtype(x.dtype)
         dw = torch.zeros(channels, kernel_size, dtype=acc, device=x.device) if need_w else None
         db = torch.zeros(channels, dtype=acc, device=x.device) if need_b and bias is not None else None
@@ -298,6 +318,8 @@ class _Decay(torch.autograd.Function):
         dzb = torch.zeros(heads, key_dim, dtype=acc, device=z.device) if bias is not None and ctx.needs_input_grad[2] \
             else None
         dal = torch.zeros(heads, dtype=acc, device=z.device) if ctx.needs_input_grad[1] else None
+        if dzb is not None or dal is not None:
+            _alert_nondeterministic("the decay gate backward (kda_gates_bwd)")
         _lib.check(lib.kda_gates_bwd(
             z.data_ptr(), _lib.ptr(zb), al.data_ptr(), ctx.g_min, dgc.data_ptr(), _lib.ptr(dac), dz.data_ptr(),
             _lib.ptr(dzb), _lib.ptr(dal), None, None, None, batch * tokens, heads, key_dim,
@@ -481,6 +503,7 @@ class _RMSNormGate(torch.autograd.Function):
         dw = None
         if weight is not None and ctx.needs_input_grad[1]:
             dw = torch.zeros(weight.shape, dtype=_acc_dtype(x.dtype), device=x.device)
+            _alert_nondeterministic("the RMSNorm x gate backward (kda_rmsnorm_gate_bwd)")
         _lib.check(lib.kda_rmsnorm_gate_bwd(
             xc.data_ptr(), _lib.ptr(wc), per_head, _lib.ptr(gc), dyc.data_ptr(), dx.data_ptr(), _lib.ptr(dgl),
             _lib.ptr(dw), batch * tokens, heads, head_dim, float(eps), _lib.dtype_code(x.dtype),

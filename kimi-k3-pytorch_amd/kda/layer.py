@@ -12,10 +12,10 @@ output gate (kda.py:153-161) and the ``KDAState`` handed to the next call
   reference's ``nn.Linear``), then ``fused.conv_silu`` (ShortConv + SiLU, L2
   norm per head for q and k, right padding and the decode history);
 * beta: the projection, then ``fused.beta_gate``;
-* decay: the low-rank projection; with ``mode="chunkwise"`` on the MFMA
-  shapes the chunk kernel forms g from the logits itself
-  (``fused.chunkwise_kda_with_decay``), otherwise ``fused.lower_bounded_decay``
-  feeds the operator;
+* decay: the low-rank projection, then ``fused.lower_bounded_decay``, which
+  feeds the operator (the chunk kernel can also form g from the logits
+  itself, ``fused.chunkwise_kda_with_decay``, bit-identical but measured
+  slower, so the layer keeps the two launches);
 * output: ``fused.rmsnorm_gate`` (RMSNorm times the sigmoid gate of the gate
   projection), the output projection, and the mask.
 
@@ -33,6 +33,7 @@ import torch
 import torch.nn.functional as F
 
 from . import fused
+from .chunkwise import chunkwise_kda
 from .recurrent import recurrent_kda
 from .state import KDAState
 from .utils import validate_attention_mask
@@ -188,13 +189,14 @@ def kda_attention_forward(
     # the operator (src/kda/kda.py:131-151)
     initial = None if state is None else state.recurrent_state
     keep_state = return_state
+    # the decay kernel, then the operator: measured faster than forming g
+    # inside the chunk kernel (fused.chunkwise_kda_with_decay, bit-identical),
+    # whose extra VALU work lands on the chunk kernel's latency-bound loaders
+    g, _ = fused.lower_bounded_decay(decay_logits, w.a_log, w.g_min, bias=w.b_alpha)
     if mode == "chunkwise":
-        core = fused.chunkwise_kda_with_decay(
-            q, k, v, decay_logits, w.a_log, beta, decay_bias=w.b_alpha, g_min=w.g_min, initial_state=initial,
-            output_final_state=keep_state, attention_mask=attention_mask,
-            accumulate_state_in_fp32=w.accumulate_state_in_fp32)
+        core = chunkwise_kda(q, k, v, g, beta, initial, keep_state, attention_mask,
+                             accumulate_state_in_fp32=w.accumulate_state_in_fp32)
     else:
-        g, _ = fused.lower_bounded_decay(decay_logits, w.a_log, w.g_min, bias=w.b_alpha)
         core = recurrent_kda(q, k, v, g, beta, initial, keep_state, attention_mask,
                              accumulate_state_in_fp32=w.accumulate_state_in_fp32,
                              update_state_in_place=update_state_in_place and mode == "decode" and initial is not None)

@@ -94,7 +94,7 @@ def recurrent_kda(
         s_in = initial_state
         s_out = initial_state
     else:
-        s_in = _prep.state_arg(initial_state, arith)
+        s_in = _prep.state_arg(initial_state, arith, work_dtype)
         need_state = output_final_state or return_states_per_token
         s_out = torch.empty(n_seq, heads, key_dim, value_dim, dtype=arith, device=device) if need_state else None
 

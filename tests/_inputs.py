@@ -40,6 +40,18 @@ def workload(batch, tokens, heads, key_dim, value_dim, *, g_shift=2.0, state_std
     return cast(q), cast(k), cast(v), cast(g), cast(beta), state
 
 
+# Measured parity margins of the full-size tests: (test, tensor, error,
+# tolerance) rows, written at the end of the session to the JSON file that
+# KDA_PARITY_RECORD names (tests/conftest.py), when it is set.
+MARGINS: list[dict] = []
+
+
+def record_margin(case: str, tol: float, **errors: float) -> None:
+    """Keep the measured errors of one parity check for the session record."""
+    for tensor, err in errors.items():
+        MARGINS.append({"case": case, "tensor": tensor, "rel_err": float(err), "tol": float(tol)})
+
+
 def rel_err(actual: torch.Tensor, expected: torch.Tensor) -> float:
     """max |actual - expected| / max |expected| (per-tensor relative error)."""
     a = actual.detach().double().cpu()

@@ -15,7 +15,7 @@ import torch
 
 import kda
 from oracle import kda_oracle as ora
-from tests._inputs import random_core, rel_err, workload
+from tests._inputs import random_core, record_margin, rel_err, workload
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -156,7 +156,7 @@ def test_chunkwise_extreme_decay_takes_exact_path():
 
 @pytest.mark.parametrize("segment_chunks", [None, "1"])
 @pytest.mark.parametrize("regime", ["mixed_small", "rising_chunk", "rising_block_past_2e100"])
-def test_chunkwise_rising_decays(monkeypatch, regime, segment_chunks):
+def test_chunkwise_rising_decays(segments, regime, segment_chunks):
     # The reference operator accepts a decay of either sign (src/kda/utils.py:32-71).
     # mixed_small: g = 0.02 N(0,1) everywhere; rising_chunk: one whole chunk at
     # g = +0.3 (the chunk grows by e^19.2); rising_block_past_2e100: one 16-row
@@ -164,7 +164,7 @@ def test_chunkwise_rising_decays(monkeypatch, regime, segment_chunks):
     # block at g = -5.  Both schedules: one segment per sequence and one chunk
     # per segment.
     if segment_chunks is not None:
-        monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", segment_chunks)
+        segments(int(segment_chunks))
     q, k, v, g, beta, state = workload(1, 200, 2, 128, 128, state_std=0.02, seed=19)
     gen = torch.Generator().manual_seed(23)
     if regime == "mixed_small":
@@ -258,11 +258,11 @@ def test_chunkwise_bf16_small_head_dim():
         (2, 70, 2, 16, 16),     # the smallest key dim of the MFMA path
     ],
 )
-def test_chunkwise_key_dims_below_128(monkeypatch, shape, segment_chunks):
+def test_chunkwise_key_dims_below_128(segments, shape, segment_chunks):
     # the reference's chunk algorithm runs at any K (src/kda/chunkwise.py:61-102);
     # K <= 128, a multiple of 16, takes the MFMA path, padded to 128 channels in the kernel
     if segment_chunks is not None:
-        monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", segment_chunks)
+        segments(int(segment_chunks))
     assert _plan(*shape) >= 0 and _plan(*shape, dtype=torch.float32) == -2
     q, k, v, g, beta, state = workload(*shape, state_std=0.02, seed=24)
     ro, rs = _oracle_f32(q, k, v, g, beta, state)
@@ -291,6 +291,7 @@ def test_gpu_48gb_shape_full_length():
         eo = rel_err(got.hidden_states[:, :, sl], ro)
         es = rel_err(got.final_state[:, sl], rs)
         print(f"K=V=64 T=8192 head {h}: output rel err {eo:.2e} state rel err {es:.2e}")
+        record_margin(f"prefill B=1 T=8192 H=16 K=V=64 bf16, head {h}", TOL16, output=eo, final_state=es)
         assert eo < TOL16 and es < TOL16
 
 
@@ -306,18 +307,20 @@ def test_long_context_full_length_single_head():
         eo = rel_err(got.hidden_states[:, :, sl], ro)
         es = rel_err(got.final_state[:, sl], rs)
         print(f"T=8192 head {h}: output rel err {eo:.2e} state rel err {es:.2e}")
+        record_margin(f"prefill B=1 T=8192 H=16 K=V=128 bf16, N(0,0.02) state, head {h}", TOL16, output=eo,
+                      final_state=es)
         assert eo < TOL16 and es < TOL16
 
 
 # ---------------------------------------------------------------------------
 # Segmented schedule: the chunk chain is cut into segments whose affine state
-# maps are composed (KDA_MI355X_SEGMENT_CHUNKS forces the segment length; the
+# maps are composed (kda_set_segment_chunks forces the segment length; the
 # default plan only segments when batch * heads is small).  The result must
 # match the oracle whatever the segment length.
 
 @pytest.mark.parametrize("chunks_per_segment", ["1", "2", "3"])
-def test_chunkwise_segmented_matches_oracle(monkeypatch, chunks_per_segment):
-    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", chunks_per_segment)
+def test_chunkwise_segmented_matches_oracle(segments, chunks_per_segment):
+    segments(int(chunks_per_segment))
     q, k, v, g, beta, state = workload(2, 64 * 10 + 17, 2, 128, 128, state_std=0.02, seed=31)
     ro, rs = _oracle_f32(q, k, v, g, beta, state)
     got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True)
@@ -325,16 +328,16 @@ def test_chunkwise_segmented_matches_oracle(monkeypatch, chunks_per_segment):
 
 
 @pytest.mark.parametrize("value_dim", [64, 256])
-def test_chunkwise_segmented_value_widths(monkeypatch, value_dim):
-    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "2")
+def test_chunkwise_segmented_value_widths(segments, value_dim):
+    segments(2)
     q, k, v, g, beta, state = workload(1, 64 * 7 + 5, 2, 128, value_dim, state_std=0.02, seed=32)
     ro, rs = _oracle_f32(q, k, v, g, beta, state)
     got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True)
     _check(got, ro, rs, label=f"segmented V={value_dim}")
 
 
-def test_chunkwise_segmented_varlen_and_slow_decay(monkeypatch):
-    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "2")
+def test_chunkwise_segmented_varlen_and_slow_decay(segments):
+    segments(2)
     q, k, v, g, beta, _ = workload(1, 600, 2, 128, 128, g_shift=-2.0, seed=33)
     cu = [0, 100, 164, 165, 600]
     init = torch.randn(4, 2, 128, 128, generator=torch.Generator().manual_seed(34)) * 0.02
@@ -345,8 +348,8 @@ def test_chunkwise_segmented_varlen_and_slow_decay(monkeypatch):
     _check(got, ro, rs, label="segmented varlen, slow decay")
 
 
-def test_chunkwise_segmented_mask_and_zero_decay(monkeypatch):
-    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "1")
+def test_chunkwise_segmented_mask_and_zero_decay(segments):
+    segments(1)
     q, k, v, _, beta, state = workload(2, 300, 2, 128, 128, state_std=0.02, seed=35)
     g = torch.zeros_like(q)
     mask = torch.arange(300)[None, :] < torch.tensor([300, 130])[:, None]
@@ -356,12 +359,12 @@ def test_chunkwise_segmented_mask_and_zero_decay(monkeypatch):
     assert torch.count_nonzero(got.hidden_states[1, 130:]) == 0
 
 
-def test_chunkwise_segmented_equals_single_segment(monkeypatch):
+def test_chunkwise_segmented_equals_single_segment(segments):
     q, k, v, g, beta, state = workload(1, 64 * 12, 3, 128, 128, state_std=0.02, seed=36)
     d = _dev(q, k, v, g, beta, state)
-    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "0")
+    segments(0)
     one = kda.chunkwise_kda(*d, True)
-    monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "4")
+    segments(4)
     seg = kda.chunkwise_kda(*d, True)
     assert rel_err(seg.hidden_states, one.hidden_states.float()) < 1e-2
     assert rel_err(seg.final_state, one.final_state) < 1e-2

@@ -26,7 +26,7 @@ import torch
 import kda
 from kda import _lib
 from oracle import kda_oracle as ora
-from tests._inputs import rel_err, workload
+from tests._inputs import record_margin, rel_err, workload
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -54,10 +54,11 @@ def test_prefill_b8_t1024_h8_full_size():
     eo = rel_err(got.hidden_states, ro)
     es = rel_err(got.final_state, rs)
     print(f"B=8 T=1024 H=8: output rel err {eo:.2e} state rel err {es:.2e}")
+    record_margin("prefill B=8 T=1024 H=8 K=V=128 bf16 (all heads)", TOL16, output=eo, final_state=es)
     assert eo < TOL16 and es < TOL16
 
 
-def test_prefill_packed_documents_h64_full_size(monkeypatch):
+def test_prefill_packed_documents_h64_full_size(segments):
     cu = [0, 32768, 49152, 61440, 65536]
     H, K, V = 64, 128, 128
     q, k, v, g, beta = _gpu_workload(cu[-1], H, K, V, seed=32)
@@ -79,15 +80,17 @@ def test_prefill_packed_documents_h64_full_size(monkeypatch):
         eo = rel_err(got.hidden_states[:, s0:s1, heads], ro)
         es = rel_err(got.final_state[d:d + 1, heads], rs)
         print(f"document {d} ({s1 - s0} tokens): output rel err {eo:.2e} state rel err {es:.2e}")
+        record_margin(f"packed H=64 bf16, document {d} ({s1 - s0} tokens), heads {heads}", TOL16, output=eo,
+                      final_state=es)
         assert eo < TOL16 and es < TOL16
         # the packed call equals a separate call on the document (all heads)
         # held to the packed call's schedule: 4 documents x 64 heads fill the
         # GPU, and the first document, twice the chunk-steps per CU of a
         # balanced pass, has every document cut into segments of that many
         # chunks (the library's plan for the longest document's hint)
-        monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", str(per_segment))
+        segments(per_segment)
         alone = kda.chunkwise_kda(q[:, s0:s1], k[:, s0:s1], v[:, s0:s1], g[:, s0:s1], beta[:, s0:s1], None, True)
-        monkeypatch.delenv("KDA_MI355X_SEGMENT_CHUNKS")
+        segments(-1)
         assert rel_err(got.hidden_states[:, s0:s1], alone.hidden_states) < 1e-6
         assert rel_err(got.final_state[d:d + 1], alone.final_state) < 1e-6
 
@@ -113,4 +116,5 @@ def test_decode_b256_h32_64_steps_in_place():
         eo = rel_err(out[b:b + 1, :, i:i + 1], ro)
         es = rel_err(final[b, h][None, None], rs)
         print(f"decode b={b} h={h}: output rel err {eo:.2e} state rel err {es:.2e}")
+        record_margin(f"decode B=256 H=32 bf16, 64 in-place steps, b={b} h={h}", TOL16, output=eo, final_state=es)
         assert eo < TOL16 and es < TOL16

@@ -55,15 +55,19 @@ def _cmp(label, pairs, dtype):
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("taps", [4, 3])
 @pytest.mark.parametrize("normalize", [True, False])
-def test_conv_silu_gradients(dtype, taps, normalize):
-    B, T, H, D = 2, 37, 4, 64
+@pytest.mark.parametrize("tokens", [37, 300])
+def test_conv_silu_gradients(dtype, taps, normalize, tokens):
+    # T = 37 is one run of one wave; T = 300 spans several runs per wave, the
+    # four waves' LDS reduction of dw and dbias, and blocks of more than one
+    # run group (T > 256)
+    B, T, H, D = 2, tokens, 4, 64
     C = H * D
     x = _rand(B, T, C, seed=1, dtype=dtype)
     w = _rand(C, taps, seed=2, scale=0.3, dtype=dtype)
     b = _rand(C, seed=3, scale=0.1, dtype=dtype)
     hist = _rand(B, taps - 1, C, seed=4, dtype=dtype)
     mask = torch.ones(B, T, dtype=torch.bool)
-    mask[1, 29:] = False
+    mask[1, T - 8:] = False
     (xg, xr), (wg, wr), (bg, br), (hg, hr) = _leaves(x, w, b, hist)
     dy = _rand(B, T, C, seed=5, dtype=torch.float64)
     dh = _rand(B, taps - 1, C, seed=6, dtype=torch.float64)
@@ -72,7 +76,7 @@ def test_conv_silu_gradients(dtype, taps, normalize):
     ((y.double().reshape(B, T, C) * dy.to(DEV)).sum() + (nxt.buffer.double() * dh.to(DEV)).sum()).backward()
     ry, rn = ora.conv_silu(xr, wr, br, hr, mask, num_heads=H, normalize=normalize)
     ((ry * dy).sum() + (rn * dh).sum()).backward()
-    _cmp(f"conv {dtype} K={taps} norm={normalize}", {"x": (xg.grad, xr.grad), "w": (wg.grad, wr.grad),
+    _cmp(f"conv {dtype} T={T} K={taps} norm={normalize}", {"x": (xg.grad, xr.grad), "w": (wg.grad, wr.grad),
                                                       "b": (bg.grad, br.grad), "hist": (hg.grad, hr.grad)}, dtype)
 
 
@@ -183,3 +187,27 @@ def test_layer_trains_through_the_backend_f64():
         worst = max(worst, e)
         print(f"layer d{k}: {e:.2e}")
     assert worst < 1e-8
+
+
+def test_parameter_gradients_under_deterministic_mode():
+    # the parameter gradients are summed with float atomics: deterministic
+    # mode raises for them (as torch's nondeterministic ops do), warns with
+    # warn_only, and leaves input-only gradients alone
+    x = _rand(1, 40, 128, seed=21, dtype=torch.float32).to(DEV).requires_grad_()
+    w = _rand(128, 4, seed=22, scale=0.3, dtype=torch.float32).to(DEV)
+    try:
+        torch.use_deterministic_algorithms(True)
+        y, _ = fused.conv_silu(x, w, num_heads=2, normalize=True)
+        y.sum().backward()  # input gradient only: allowed
+        assert x.grad is not None
+        wg = w.clone().requires_grad_()
+        y, _ = fused.conv_silu(x, wg, num_heads=2, normalize=True)
+        with pytest.raises(RuntimeError, match="deterministic"):
+            y.sum().backward()
+        torch.use_deterministic_algorithms(True, warn_only=True)
+        y, _ = fused.conv_silu(x, wg, num_heads=2, normalize=True)
+        with pytest.warns(UserWarning, match="deterministic"):
+            y.sum().backward()
+        assert wg.grad is not None
+    finally:
+        torch.use_deterministic_algorithms(False)

@@ -213,7 +213,7 @@ def _decay_inputs(B, T, H, K, V, dtype, seed, z_shift=0.0):
     "case",
     ["dense", "masked", "packed", "segmented", "extreme_decay", "f16", "value_64", "key_64"],
 )
-def test_fused_decay_prefill_equals_two_step_and_oracle(monkeypatch, case):
+def test_fused_decay_prefill_equals_two_step_and_oracle(segments, case):
     dtype = torch.float16 if case == "f16" else torch.bfloat16
     B, T, H, V = (1, 260, 2, 128) if case in ("packed", "segmented") else (2, 200, 2, 64 if case == "value_64" else 128)
     K = 64 if case == "key_64" else 128
@@ -227,7 +227,7 @@ def test_fused_decay_prefill_equals_two_step_and_oracle(monkeypatch, case):
         cu = [0, 70, 71, 200, 260]
         state = torch.randn(4, H, K, V, generator=torch.Generator().manual_seed(5)) * 0.02
     if case == "segmented":
-        monkeypatch.setenv("KDA_MI355X_SEGMENT_CHUNKS", "1")
+        segments(1)
     dv = lambda t: None if t is None else t.to(DEV)  # noqa: E731
     kw = dict(initial_state=dv(state), output_final_state=True, attention_mask=dv(mask), cu_seqlens=cu)
     with torch.no_grad():
