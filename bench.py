@@ -912,9 +912,10 @@ def bench_configs(steps, warmup, counters=None):
 
 def bench_prefill_f32(steps, warmup):
     """f32 inputs at the long-context shape through kda.chunkwise_kda: the
-    split-bf16 chunk path of a dense call, next to the exact recurrence kernel
-    (the same sequence passed as one packed document, which that path does not
-    take)."""
+    split-bf16 chunk path of a dense call, the same sequence as one packed
+    document (gathered into a padded batch for the same path), and the exact
+    recurrence kernel (the packed call through the C ABI without the longest
+    document's length, which that path needs)."""
     import torch
 
     import kda
@@ -935,13 +936,25 @@ def bench_prefill_f32(steps, warmup):
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) / n
 
+    lib = _lib.load()
+    code = _lib.dtype_code(torch.float32)
     L, segs = ctypes.c_int64(0), ctypes.c_int64(0)
-    _lib.check(_lib.load().kda_chunk_fwd_plan(P_B, P_B * P_T, 0, P_H, P_K, P_V, _lib.dtype_code(torch.float32),
-                                              ctypes.byref(L), ctypes.byref(segs)))
+    _lib.check(lib.kda_chunk_fwd_plan(P_B, P_B * P_T, 0, P_H, P_K, P_V, code, ctypes.byref(L), ctypes.byref(segs)))
+    out = torch.empty(P_B, P_T, P_H, P_V, device=device)
+    s_out = torch.empty(P_B, P_H, P_K, P_V, device=device)
+    cu = torch.tensor([0, P_T], dtype=torch.int32, device=device)
+    stream = torch.cuda.current_stream(device).cuda_stream
+
+    def recurrence():
+        _lib.check(lib.kda_chunk_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code,
+                                     s0.data_ptr(), s_out.data_ptr(), code, out.data_ptr(), cu.data_ptr(), 0, None, 1,
+                                     P_T, P_H, P_K, P_V, None, 0, stream))
+
     with torch.no_grad():
         _settle(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True))
         split_ms = timed(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True), steps, warmup)
-        rec_ms = timed(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True, cu_seqlens=[0, P_T]), 2, 1)
+        packed_ms = timed(lambda: kda.chunkwise_kda(q, k, v, g, beta, s0, True, cu_seqlens=[0, P_T]), steps, warmup)
+        rec_ms = timed(recurrence, 2, 1)
     nbytes = 2 * prefill_bytes(P_B, P_T, P_H, P_K, P_V, n_state_io=1)  # every tensor f32
     return {
         "workload": f"kda.chunkwise_kda B={P_B} T={P_T} H={P_H} K=V={P_K} f32 inputs, f32 state N(0,0.02) in, "
@@ -951,6 +964,8 @@ def bench_prefill_f32(steps, warmup):
         "tokens_per_s": round(P_B * P_T / (split_ms * 1e-3), 1),
         "achieved_gbs": round(nbytes / (split_ms * 1e-3) / 1e9, 1),
         "algorithmic_bytes": nbytes,
+        "packed_one_document_ms": round(packed_ms, 5),
+        "packed_over_dense": round(packed_ms / split_ms, 3),
         "recurrence_kernel_ms": round(rec_ms, 5),
         "speedup_vs_recurrence": round(rec_ms / split_ms, 2),
     }

@@ -98,9 +98,10 @@ int kda_decode_step(const void* q, const void* k, const void* v, const void* g,
  * Workspace bytes `kda_chunk_fwd` needs for these sizes (0 if none), for
  * dense sequences of total_tokens / num_seqs tokens (longest_tokens 0) or for
  * packed documents whose longest is longest_tokens tokens (the value the call
- * passes in `dense_span`; 0 when unknown); packed documents off the MFMA path
- * need none, and an f32-state call never needs more.  0 for a longest_tokens
- * outside 0..total_tokens.
+ * passes in `dense_span`; 0 when unknown); off the MFMA path packed documents
+ * take a zero-padded batch of num_seqs x longest_tokens tokens, and an
+ * f32-state call never needs more.  0 for a longest_tokens outside
+ * 0..total_tokens.
  * No reference counterpart (the reference allocates per call).
  */
 size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t longest_tokens,
@@ -109,8 +110,8 @@ size_t kda_chunk_fwd_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int
 /*
  * The schedule `kda_chunk_fwd` picks for these sizes: *chunks_per_segment is
  * the number of 64-token chunks per segment (0 when every sequence is one
- * segment, -2 when the shape takes the split-bf16 chunk path for dense
- * sequences, -1 when it runs the exact recurrence kernel) and *segments
+ * segment, -2 when the shape takes the split-bf16 chunk path, -1 when it runs
+ * the exact recurrence kernel: f64 inputs, and K > 128) and *segments
  * the bound on segments it sizes its workspace for; longest_tokens as for
  * kda_chunk_fwd_workspace_bytes.  No reference
  * counterpart (the reference has one schedule, a Python loop over chunks,
@@ -145,14 +146,20 @@ int kda_set_segment_chunks(int64_t chunks_per_segment);
  * independent `chunkwise_kda` call.
  * The MFMA path covers bf16/f16 inputs with K <= 128 a multiple of 16 (a smaller K is
  * zero-padded to 128 channels inside the kernel) and V a multiple of 16 in
- * 16..256.  Dense calls (no cu_seqlens) of other bf16/f16/f32 inputs with K
- * and V <= 128 and an f32 state take the split-bf16 chunk path: per-chunk
- * operands in a chunk-parallel kernel, the state scan with every product on
- * split operands (x = hi + lo, two bf16 each, relative error about 2^-17) and
- * the outputs in a second chunk-parallel kernel; its workspace is
- * B x H x ceil(T/64) records of 593 KiB (K = V = 128).  The rest (packed
- * documents off the MFMA path, K or V > 128, f64 inputs, a bf16/f16 state)
- * runs the exact recurrence kernel, which needs no workspace.
+ * 16..256.  Other bf16/f16/f32 inputs with K <= 128 and an f32 state take
+ * the split-bf16 chunk path: per-chunk operands in a chunk-parallel kernel,
+ * the state scan with every product on split operands (x = hi + lo, two bf16
+ * each, relative error about 2^-17) and the outputs in a second
+ * chunk-parallel kernel; its workspace is B x H x ceil(T/64) records of
+ * 593 KiB (K = V = 128).  Packed documents on that path are gathered into a
+ * zero-padded batch of num_seqs x dense_span tokens (dense_span must be the
+ * longest document's length; a smaller one returns KDA_ERR_INVALID_ARGUMENT
+ * where the host can tell, and drops tokens past it otherwise) and their
+ * outputs scattered back (one document is the dense batch, no copies); value widths past 128 run as
+ * slices of at most 128 columns (state and value columns never interact).
+ * The rest (K > 128, f64 inputs, a bf16/f16 state, packed documents without
+ * their longest length) runs the exact recurrence kernel, which needs no
+ * workspace.
  */
 int kda_chunk_fwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
                   int in_dtype, const void* initial_state, void* final_state, int state_dtype,

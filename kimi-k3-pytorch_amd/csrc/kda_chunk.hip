@@ -2033,9 +2033,10 @@ namespace kda_host {
 void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t longest, int64_t heads, int64_t key_dim,
                 int64_t value_dim, int in_dtype, int64_t* chunks_per_segment, int64_t* segments) {
   if (!kda::mfma_path(in_dtype, in_dtype == KDA_DTYPE_F64 ? KDA_DTYPE_F64 : KDA_DTYPE_F32, key_dim, value_dim)) {
-    // dense sequences take the split-bf16 chunk path where it applies (-2),
-    // everything else the exact recurrence kernel (-1)
-    *chunks_per_segment = chunk_split_path(in_dtype, KDA_DTYPE_F32, key_dim, value_dim) ? -2 : -1;
+    // the split-bf16 chunk path where it applies (-2): dense sequences, and
+    // packed documents whose longest length the caller passes; everything
+    // else (f64 inputs, K past 128) the exact recurrence kernel (-1)
+    *chunks_per_segment = chunk_split_general(in_dtype, KDA_DTYPE_F32, key_dim, value_dim) ? -2 : -1;
     *segments = num_seqs;
     return;
   }
@@ -2047,21 +2048,27 @@ void chunk_plan(int64_t num_seqs, int64_t total_tokens, int64_t longest, int64_t
 size_t chunk_workspace_bytes(int64_t num_seqs, int64_t total_tokens, int64_t longest, int64_t heads,
                              int64_t key_dim, int64_t value_dim, int in_dtype) {
   if (!kda::mfma_path(in_dtype, in_dtype == KDA_DTYPE_F64 ? KDA_DTYPE_F64 : KDA_DTYPE_F32, key_dim, value_dim)) {
-    // sized for a dense call (num_seqs rows of total_tokens / num_seqs tokens)
-    // on the split-bf16 chunk path; the recurrence kernel needs none
-    if (!chunk_split_path(in_dtype, KDA_DTYPE_F32, key_dim, value_dim) || num_seqs <= 0) return 0;
-    return chunk_split_workspace_bytes(num_seqs, (total_tokens + num_seqs - 1) / num_seqs, heads, key_dim, value_dim);
+    // the split-bf16 chunk path: packed documents (longest > 0) as a padded
+    // batch of the longest document's tokens, dense sequences as they are;
+    // the recurrence kernel needs none
+    if (!chunk_split_general(in_dtype, KDA_DTYPE_F32, key_dim, value_dim) || num_seqs <= 0) return 0;
+    if (longest > 0)
+      return chunk_split_general_workspace_bytes(num_seqs, longest, heads, key_dim, value_dim, in_dtype, true);
+    return chunk_split_general_workspace_bytes(num_seqs, (total_tokens + num_seqs - 1) / num_seqs, heads, key_dim,
+                                               value_dim, in_dtype, false);
   }
   const kda::Plan p = kda::make_plan(num_seqs, total_tokens, heads, value_dim, longest);
   return kda::map_bytes(num_seqs) + kda::segment_bytes(p, heads, value_dim);
 }
 
-// Whether a call off the MFMA path takes the split-bf16 chunk path: dense
-// sequences (no packed documents) of a shape that path covers.
+// Whether a call off the MFMA path takes the split-bf16 chunk path: a shape
+// that path covers, as dense sequences or as packed documents whose longest
+// length (dense_span) the caller passes (without it the padded batch cannot
+// be sized, and the exact recurrence runs).
 static bool split_call(const kda::SeqDesc& seq, int64_t N, int64_t total_tokens, int in_dtype, int state_dtype,
                        int64_t K, int64_t V) {
-  return seq.cu_seqlens == nullptr && seq.dense_span > 0 && N > 0 && N * seq.dense_span == total_tokens &&
-         chunk_split_path(in_dtype, state_dtype, K, V);
+  if (!chunk_split_general(in_dtype, state_dtype, K, V) || N <= 0 || seq.dense_span <= 0) return false;
+  return seq.cu_seqlens != nullptr ? seq.valid_lens == nullptr : N * seq.dense_span == total_tokens;
 }
 
 size_t chunk_call_workspace_bytes(const kda::SeqDesc& seq, int64_t N, int64_t total_tokens, int64_t H, int64_t K,
@@ -2069,7 +2076,7 @@ size_t chunk_call_workspace_bytes(const kda::SeqDesc& seq, int64_t N, int64_t to
   if (kda::mfma_path(in_dtype, state_dtype, K, V))
     return chunk_workspace_bytes(N, total_tokens, kda::plan_longest(seq), H, K, V, in_dtype);
   if (split_call(seq, N, total_tokens, in_dtype, state_dtype, K, V))
-    return chunk_split_workspace_bytes(N, seq.dense_span, H, K, V);
+    return chunk_split_general_workspace_bytes(N, seq.dense_span, H, K, V, in_dtype, seq.cu_seqlens != nullptr);
   return 0;
 }
 
@@ -2080,11 +2087,13 @@ int launch_chunk(const void* q, const void* k, const void* v, const void* g, con
   using namespace kda;
   if (!mfma_path(in_dtype, state_dtype, K, V)) {
     if (split_call(seq, N, total_tokens, in_dtype, state_dtype, K, V)) {
-      // dense sequences: the chunk path of split-bf16 products
+      // the chunk path of split-bf16 products (packed documents as a padded
+      // batch, value widths past 128 in column slices)
       mark(ev, 0, stream);
-      const int st = launch_chunk_split(q, k, v, g, beta, in_dtype, static_cast<const float*>(s_in),
-                                        static_cast<float*>(s_out), out, seq.valid_lens, N, seq.dense_span, H, K,
-                                        V, workspace, workspace_bytes, stream);
+      const int st = launch_chunk_split_general(q, k, v, g, beta, in_dtype, static_cast<const float*>(s_in),
+                                                static_cast<float*>(s_out), out, seq.cu_seqlens, seq.valid_lens, N,
+                                                seq.dense_span, total_tokens, H, K, V, workspace, workspace_bytes,
+                                                stream);
       mark(ev, 1, stream);
       return st;
     }

@@ -1976,6 +1976,58 @@ __global__ __launch_bounds__(512) void grad_pair_kernel(const Args<IT> a) {
   pair_body<IT, KP, 512>(a, lds);
 }
 
+
+// ---- rows moved between a caller's tensor and a dense zero-padded batch ------
+// The split-bf16 chunk path runs dense batches [N, T, H, *].  Packed
+// documents are gathered into one (each document a row of T = the longest
+// document's tokens, zero past its length), and value widths past 128 run as
+// independent column slices of at most 128 (state and value columns never
+// interact).  Row d of the dense side is token p = d / R (R rows per token),
+// sub-row j = d % R; with packed offsets, p is (document b = p / T, token
+// t = p % T) and maps to the caller's row (cu[b] + t) R + j, dropped
+// (zero-filled on a gather, skipped on a scatter) when t passes the
+// document's length; without offsets the dense row is the caller's row.
+struct RowMove {
+  const char* src;
+  char* dst;
+  int64_t src_stride, dst_stride;  // bytes between consecutive rows
+  int64_t n_rows;                  // rows of the dense side
+  int64_t T, R;
+  const int32_t* cu;               // [N+1] packed offsets, or null
+  int64_t upr;                     // units per row
+  int scatter;                     // 0: caller -> dense, 1: dense -> caller
+};
+
+template <class U>
+__global__ __launch_bounds__(256) void move_rows_kernel(const RowMove m) {
+  const int64_t i = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (i >= m.n_rows * m.upr) return;
+  const int64_t d = i / m.upr;
+  const int64_t u = i - d * m.upr;
+  int64_t r = d;
+  bool live = true;
+  if (m.cu != nullptr) {
+    const int64_t p = d / m.R, j = d - p * m.R;
+    const int64_t b = p / m.T, t = p - b * m.T;
+    const int64_t start = m.cu[b];
+    live = t < static_cast<int64_t>(m.cu[b + 1]) - start;
+    r = (start + t) * m.R + j;
+  }
+  if (!m.scatter) {
+    U x{};
+    if (live) x = reinterpret_cast<const U*>(m.src + r * m.src_stride)[u];
+    reinterpret_cast<U*>(m.dst + d * m.dst_stride)[u] = x;
+  } else if (live) {
+    reinterpret_cast<U*>(m.dst + r * m.dst_stride)[u] = reinterpret_cast<const U*>(m.src + d * m.src_stride)[u];
+  }
+}
+
+// Document lengths from packed offsets.
+__global__ __launch_bounds__(256) void doc_lengths_kernel(const int32_t* cu, int64_t N, int32_t* len) {
+  const int64_t b = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+  if (b < N) len[b] = cu[b + 1] - cu[b];
+}
+
 }  // namespace bwd
 }  // namespace kda
 
@@ -2173,6 +2225,148 @@ int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
       set_detail("chunk backward: inputs must be bf16, f16 or f32 (dtype %d)", in_dtype);
       return KDA_ERR_UNSUPPORTED;
   }
+}
+
+
+// ---- the split path over packed documents and value slices -----------------
+static int64_t align256(int64_t b) { return (b + 255) / 256 * 256; }
+static int64_t elem_bytes(int in_dtype) { return in_dtype == KDA_DTYPE_F32 ? 4 : 2; }
+static constexpr int64_t kSliceCols = 128;  // value columns per slice of the split path
+
+bool chunk_split_general(int in_dtype, int state_dtype, int64_t K, int64_t V) {
+  return (in_dtype == KDA_DTYPE_BF16 || in_dtype == KDA_DTYPE_F16 || in_dtype == KDA_DTYPE_F32) &&
+         state_dtype == KDA_DTYPE_F32 && K >= 1 && K <= 128 && V >= 1;
+}
+
+size_t chunk_split_general_workspace_bytes(int64_t N, int64_t T, int64_t H, int64_t K, int64_t V, int in_dtype,
+                                           bool packed) {
+  const int64_t e = elem_bytes(in_dtype);
+  const bool sliced = V > kSliceCols;
+  const int64_t w = sliced ? kSliceCols : V;
+  int64_t bytes = static_cast<int64_t>(chunk_split_workspace_bytes(N, T, H, K, w));
+  if (packed) bytes += 3 * align256(N * T * H * K * e) + align256(N * T * H * e) + align256(N * 4);
+  if (packed || sliced) bytes += 2 * align256(N * T * H * w * e);
+  if (sliced) bytes += 2 * align256(N * H * K * w * 4);
+  return static_cast<size_t>(bytes);
+}
+
+// Moves n_rows rows of row_bytes bytes (see bwd::RowMove), in the widest unit
+// that divides the row, both strides and both addresses.
+static int move_rows(const void* src, int64_t src_stride, void* dst, int64_t dst_stride, int64_t row_bytes,
+                     int64_t n_rows, int64_t T, int64_t R, const int32_t* cu, bool scatter, hipStream_t s) {
+  if (n_rows <= 0 || row_bytes <= 0) return KDA_OK;
+  const uintptr_t all = reinterpret_cast<uintptr_t>(src) | reinterpret_cast<uintptr_t>(dst) |
+                        static_cast<uintptr_t>(src_stride) | static_cast<uintptr_t>(dst_stride) |
+                        static_cast<uintptr_t>(row_bytes);
+  const int unit = all % 16 == 0 ? 16 : all % 4 == 0 ? 4 : 2;
+  bwd::RowMove m{static_cast<const char*>(src), static_cast<char*>(dst), src_stride, dst_stride, n_rows, T, R, cu,
+                 row_bytes / unit, scatter ? 1 : 0};
+  const int64_t blocks = (n_rows * m.upr + 255) / 256;
+  if (blocks > 0x7fffffffLL) {
+    set_detail("chunk_fwd: gather grid too large");
+    return KDA_ERR_UNSUPPORTED;
+  }
+  const dim3 grid(static_cast<unsigned>(blocks));
+  if (unit == 16)
+    hipLaunchKernelGGL(bwd::move_rows_kernel<uint4>, grid, dim3(256), 0, s, m);
+  else if (unit == 4)
+    hipLaunchKernelGGL(bwd::move_rows_kernel<uint32_t>, grid, dim3(256), 0, s, m);
+  else
+    hipLaunchKernelGGL(bwd::move_rows_kernel<uint16_t>, grid, dim3(256), 0, s, m);
+  return check_launch("move_rows_kernel");
+}
+
+int launch_chunk_split_general(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                               int in_dtype, const float* s_in, float* s_out, void* out, const int32_t* cu_seqlens,
+                               const int32_t* valid_lens, int64_t N, int64_t T, int64_t total_tokens, int64_t H,
+                               int64_t K, int64_t V, void* workspace, size_t workspace_bytes, hipStream_t stream) {
+  if (cu_seqlens != nullptr && (T * N < total_tokens || (N == 1 && T != total_tokens))) {
+    // the padded batch holds N x T tokens: T must be the longest document
+    set_detail("chunk_fwd: packed documents off the MFMA path need the longest document's length in dense_span "
+               "(got %lld for %lld documents of %lld tokens)", (long long)T, (long long)N, (long long)total_tokens);
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  // one packed document spanning every token is the dense batch itself
+  if (cu_seqlens != nullptr && N == 1) cu_seqlens = nullptr;
+  const bool packed = cu_seqlens != nullptr;
+  const bool sliced = V > kSliceCols;
+  if (!packed && !sliced)
+    return launch_chunk_split(q, k, v, g, beta, in_dtype, s_in, s_out, out, valid_lens, N, T, H, K, V, workspace,
+                              workspace_bytes, stream);
+  if (!chunk_split_general(in_dtype, KDA_DTYPE_F32, K, V) || N <= 0 || T <= 0 || H <= 0) {
+    set_detail("chunk_fwd: the split-bf16 chunk path needs bf16/f16/f32 inputs, K in 1..128 and T > 0");
+    return KDA_ERR_UNSUPPORTED;
+  }
+  if (packed && valid_lens != nullptr) {
+    set_detail("chunk_fwd: packed documents take no right-padding lengths");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (workspace == nullptr || workspace_bytes < chunk_split_general_workspace_bytes(N, T, H, K, V, in_dtype, packed)) {
+    set_detail("chunk_fwd: workspace of %zu bytes needed",
+               chunk_split_general_workspace_bytes(N, T, H, K, V, in_dtype, packed));
+    return KDA_ERR_WORKSPACE;
+  }
+  const int64_t e = elem_bytes(in_dtype);
+  const int64_t w = sliced ? kSliceCols : V;
+  char* p = static_cast<char*>(workspace);
+  auto take = [&](int64_t bytes) {
+    char* r = p;
+    p += align256(bytes);
+    return r;
+  };
+  char* split_ws = take(static_cast<int64_t>(chunk_split_workspace_bytes(N, T, H, K, w)));
+  const int64_t rows = N * T;  // dense tokens
+  const void *dq = q, *dk = k, *dg = g, *db = beta;
+  const int32_t* valid = valid_lens;
+  int st = KDA_OK;
+  if (packed) {
+    char* gq = take(rows * H * K * e);
+    char* gk = take(rows * H * K * e);
+    char* gg = take(rows * H * K * e);
+    char* gb = take(rows * H * e);
+    int32_t* len = reinterpret_cast<int32_t*>(take(N * 4));
+    const int64_t kb = H * K * e;
+    if ((st = move_rows(q, kb, gq, kb, kb, rows, T, 1, cu_seqlens, false, stream)) != KDA_OK) return st;
+    if ((st = move_rows(k, kb, gk, kb, kb, rows, T, 1, cu_seqlens, false, stream)) != KDA_OK) return st;
+    if ((st = move_rows(g, kb, gg, kb, kb, rows, T, 1, cu_seqlens, false, stream)) != KDA_OK) return st;
+    if ((st = move_rows(beta, H * e, gb, H * e, H * e, rows, T, 1, cu_seqlens, false, stream)) != KDA_OK) return st;
+    hipLaunchKernelGGL(bwd::doc_lengths_kernel, dim3(static_cast<unsigned>((N + 255) / 256)), dim3(256), 0, stream,
+                       cu_seqlens, N, len);
+    if ((st = check_launch("doc_lengths_kernel")) != KDA_OK) return st;
+    dq = gq, dk = gk, dg = gg, db = gb, valid = len;
+  }
+  char* gv = take(rows * H * w * e);
+  char* go = take(rows * H * w * e);
+  char* gs_in = sliced ? take(N * H * K * w * 4) : nullptr;
+  char* gs_out = sliced ? take(N * H * K * w * 4) : nullptr;
+  const size_t split_bytes = chunk_split_workspace_bytes(N, T, H, K, w);
+  for (int64_t c0 = 0; c0 < V; c0 += w) {
+    const int64_t wc = V - c0 < w ? V - c0 : w;
+    // value rows of this slice: one per (token, head), wc columns of V
+    if ((st = move_rows(static_cast<const char*>(v) + c0 * e, V * e, gv, wc * e, wc * e, rows * H, T, H,
+                        cu_seqlens, false, stream)) != KDA_OK)
+      return st;
+    const float* si = s_in;
+    float* so = s_out;
+    if (sliced) {
+      // state rows of this slice: one per (sequence, head, key), wc columns of V
+      if (s_in != nullptr &&
+          (st = move_rows(s_in + c0, V * 4, gs_in, wc * 4, wc * 4, N * H * K, 1, 1, nullptr, false, stream)) != KDA_OK)
+        return st;
+      si = s_in != nullptr ? reinterpret_cast<const float*>(gs_in) : nullptr;
+      so = s_out != nullptr ? reinterpret_cast<float*>(gs_out) : nullptr;
+    }
+    if ((st = launch_chunk_split(dq, dk, gv, dg, db, in_dtype, si, so, go, valid, N, T, H, K, wc, split_ws,
+                                 split_bytes, stream)) != KDA_OK)
+      return st;
+    if ((st = move_rows(go, wc * e, static_cast<char*>(out) + c0 * e, V * e, wc * e, rows * H, T, H, cu_seqlens,
+                        true, stream)) != KDA_OK)
+      return st;
+    if (sliced && s_out != nullptr &&
+        (st = move_rows(gs_out, wc * 4, s_out + c0, V * 4, wc * 4, N * H * K, 1, 1, nullptr, true, stream)) != KDA_OK)
+      return st;
+  }
+  return KDA_OK;
 }
 
 }  // namespace kda_host

@@ -84,6 +84,19 @@ int launch_chunk_split(const void* q, const void* k, const void* v, const void* 
                        const float* s_in, float* s_out, void* out, const int32_t* valid_lens, int64_t B, int64_t T,
                        int64_t H, int64_t K, int64_t V, void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+// The same path for packed documents (gathered into a zero-padded dense batch
+// of T = the longest document's tokens, outputs scattered back) and for any
+// value width (slices of at most 128 columns): K up to 128, f32 state.
+bool chunk_split_general(int in_dtype, int state_dtype, int64_t K, int64_t V);
+
+size_t chunk_split_general_workspace_bytes(int64_t N, int64_t T, int64_t H, int64_t K, int64_t V, int in_dtype,
+                                           bool packed);
+
+int launch_chunk_split_general(const void* q, const void* k, const void* v, const void* g, const void* beta,
+                               int in_dtype, const float* s_in, float* s_out, void* out, const int32_t* cu_seqlens,
+                               const int32_t* valid_lens, int64_t N, int64_t T, int64_t total_tokens, int64_t H,
+                               int64_t K, int64_t V, void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 // The same backward in f64 arithmetic (csrc/kda_chunk_bwd_f64.hip).
 size_t chunk_bwd_f64_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
 

@@ -107,10 +107,11 @@ def _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask
     def need(n_h):
         return lib.kda_chunk_fwd_workspace_bytes(n_seq, total, longest, n_h, key_dim, value_dim, code)
 
-    # a dense prefill whose workspace passes WORKSPACE_LIMIT (f32 inputs and
-    # shapes off the MFMA path take the split-bf16 chunk path, whose workspace
-    # is the backward's) runs its heads in groups
-    n_h = heads if offsets is not None else _head_group(need, heads)
+    # a prefill whose workspace passes WORKSPACE_LIMIT (f32 inputs and shapes
+    # off the MFMA path take the split-bf16 chunk path, whose workspace is the
+    # backward's; packed documents there are a zero-padded batch) runs its
+    # heads in groups
+    n_h = _head_group(need, heads)
     ws_bytes = need(n_h)
     workspace = _prep.workspace(ws_bytes, device, "chunkwise_kda")
 
@@ -153,8 +154,8 @@ def differentiable(q, k, v, g, beta, initial_state, output_final_state, attentio
     ``recurrent_kda`` (recurrent=True) or ``chunkwise_kda``, and the HIP chunk
     backward, whose gradients are those of the exact recurrence either way.
     ``offsets`` are validated packed-document boundaries (or None)."""
-    if q.shape[-1] > 128 or v.shape[-1] > 128:
-        raise RuntimeError("the MI355X KDA backward supports key_dim and value_dim up to 128")
+    if q.shape[-1] > 128:
+        raise RuntimeError("the MI355X KDA backward supports key_dim up to 128")
     qm, gm, bm = _mask_differentiable(q, g, beta, attention_mask)
     hidden, final = _ChunkwiseFunction.apply(qm, k, v, gm, bm, initial_state, output_final_state, work_dtype,
                                              recurrent, offsets)
@@ -355,25 +356,52 @@ class _ChunkwiseFunction(torch.autograd.Function):
         code = _lib.dtype_code(kernel_dtype)
         stream = _prep.stream(device)
 
-        def call(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, n_h, ws, ws_bytes):
+        def call(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, n_h, ws, ws_bytes, vdim):
             status = lib.kda_chunk_bwd(
                 *(t.data_ptr() for t in tensors), code, _lib.ptr(s_init), _lib.ptr(ds_fin),
-                *(t.data_ptr() for t in grads_out), _lib.ptr(ds_init), n_b, n_tok, n_h, key_dim, value_dim,
+                *(t.data_ptr() for t in grads_out), _lib.ptr(ds_init), n_b, n_tok, n_h, key_dim, vdim,
                 _lib.ptr(ws), ws_bytes, stream,
             )
             _lib.check(status)
 
         workspace = _Workspace(device)
 
-        def run(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok):
-            _by_head_groups(lib, call, tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, heads, key_dim,
-                            value_dim, workspace)
+        def backward_of(vc, d_out, s0, ds_t, grads, ds0):
+            """The kernels' backward over one value slice (at most 128 columns)."""
+            vdim = vc.shape[-1]
 
-        if ctx.offsets is None:
-            run((qc, kc, vc, gc, bc, d_out), (dq, dk, dv, dg, dbeta), s0, ds_t, ds0, batch, tokens)
+            def run(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok):
+                _by_head_groups(lib, lambda *a: call(*a, vdim), tensors, grads_out, s_init, ds_fin, ds_init, n_b,
+                                n_tok, heads, key_dim, vdim, workspace)
+
+            if ctx.offsets is None:
+                run((qc, kc, vc, gc, bc, d_out), grads, s0, ds_t, ds0, batch, tokens)
+            else:
+                _packed_backward(lib, ctx.offsets, (qc, kc, vc, gc, bc, d_out), grads, s0, ds_t, ds0, heads,
+                                 key_dim, vdim, device, run)
+
+        if value_dim <= 128:
+            backward_of(vc, d_out, s0, ds_t, (dq, dk, dv, dg, dbeta), ds0)
         else:
-            _packed_backward(lib, ctx.offsets, (qc, kc, vc, gc, bc, d_out), (dq, dk, dv, dg, dbeta), s0, ds_t, ds0,
-                             heads, key_dim, value_dim, device, run)
+            # value columns never interact: the operator over V columns is the
+            # operators over column slices sharing q, k, g and beta, whose
+            # gradients add up over the slices; v and the state get theirs per slice
+            acc = [torch.zeros(t.shape, dtype=torch.float64 if kernel_dtype == torch.float64 else torch.float32,
+                               device=device) for t in (dq, dk, dg, dbeta)]
+            for c0 in range(0, value_dim, 128):
+                c1 = min(c0 + 128, value_dim)
+                part = (lambda t: None if t is None else t[..., c0:c1].contiguous())  # noqa: E731
+                g_s = [torch.empty_like(t) for t in (dq, dk)] + [torch.empty_like(part(vc))] + \
+                    [torch.empty_like(t) for t in (dg, dbeta)]
+                ds0_s = None if ds0 is None else torch.empty_like(part(ds0))
+                backward_of(part(vc), part(d_out), part(s0), part(ds_t), g_s, ds0_s)
+                for a, gs in zip(acc, (g_s[0], g_s[1], g_s[3], g_s[4])):
+                    a += gs
+                dv[..., c0:c1] = g_s[2]
+                if ds0 is not None:
+                    ds0[..., c0:c1] = ds0_s
+            for dst, a in zip((dq, dk, dg, dbeta), acc):
+                dst.copy_(a)
         grads = [dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
                  None if ds0 is None else ds0.to(initial_state.dtype)]
         return (*[gr if need else None for gr, need in zip(grads, ctx.needs_input_grad[:6])], None, None, None, None)

@@ -94,6 +94,34 @@ def test_plan_cuts_a_dominant_packed_document():
     assert "longest document" in lib.kda_status_string(status).decode()
 
 
+def test_plan_takes_a_chunk_path_for_every_float_input_up_to_key_dim_128():
+    """bf16, f16 and f32 inputs with K <= 128 never run the token recurrence:
+    the MFMA path (bf16/f16 on its grid) or the split-bf16 chunk path (>= 0 or
+    -2), dense or packed, any value width; K past 128 and f64 inputs run the
+    exact recurrence (-1)."""
+    torch = __import__("torch")
+    lib = _lib.load()
+
+    def plan(n, total, longest, heads, K, V, dtype):
+        cps, segs = ctypes.c_int64(0), ctypes.c_int64(0)
+        _lib.check(lib.kda_chunk_fwd_plan(n, total, longest, heads, K, V, _lib.dtype_code(dtype), ctypes.byref(cps),
+                                          ctypes.byref(segs)))
+        return cps.value
+
+    for dtype in (torch.bfloat16, torch.float16, torch.float32):
+        for K in (1, 3, 40, 64, 100, 128):
+            for V in (1, 5, 48, 128, 129, 200, 256, 300, 512):
+                for n, total, longest in ((1, 8192, 0), (4, 4096, 0), (3, 1000, 700)):
+                    assert plan(n, total, longest, 4, K, V, dtype) != -1, (dtype, K, V, n, longest)
+        assert plan(1, 8192, 0, 4, 129, 128, dtype) == -1
+        assert plan(3, 1000, 700, 4, 256, 64, dtype) == -1
+    assert plan(1, 8192, 0, 4, 128, 128, torch.float64) == -1
+    # the packed split path's workspace is a padded batch of the longest document
+    code = _lib.dtype_code(torch.float32)
+    packed = lib.kda_chunk_fwd_workspace_bytes(3, 1000, 700, 4, 128, 128, code)
+    assert packed > lib.kda_chunk_fwd_workspace_bytes(1, 3 * 700, 0, 4, 128, 128, code)
+
+
 def declared_arities() -> dict[str, int]:
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     out = {}

@@ -137,8 +137,10 @@ def test_bf16_off_grid_key_dim():
 
 
 def test_split_path_equals_the_recurrence_kernel():
-    # the same sequences as packed documents (cu_seqlens) run the recurrence
-    # kernel: both paths agree, and the split path refuses a missing workspace
+    # the same sequences dense, as packed documents with their longest length
+    # (gathered into a padded batch on the split path) and as packed documents
+    # without it (the exact recurrence kernel): the three agree, and the split
+    # path refuses a missing workspace
     B, T, H, K, V = 2, 150, 2, 64, 32
     q, k, v, g, beta, state = _dev(*workload(B, T, H, K, V, state_std=0.02, seed=48, dtype=torch.float32))
     lib = _lib.load()
@@ -146,23 +148,89 @@ def test_split_path_equals_the_recurrence_kernel():
     stream = _lib.stream_of(q.device)
     cu = torch.tensor([0, T, 2 * T], dtype=torch.int32, device=DEV)
     outs = []
-    for packed in (False, True):
+    for packed, span in ((False, T), (True, T), (True, 0)):
         out = torch.empty(B, T, H, V, device=DEV)
         s_out = torch.empty(B, H, K, V, device=DEV)
-        n = 0 if packed else lib.kda_chunk_fwd_workspace_bytes(B, B * T, 0, H, K, V, code)
+        # (packed documents without their longest length need no workspace)
+        n = 0 if packed and span == 0 else lib.kda_chunk_fwd_workspace_bytes(B, B * T, span if packed else 0, H, K,
+                                                                             V, code)
         ws = torch.empty(n, dtype=torch.uint8, device=DEV) if n else None
         _lib.check(lib.kda_chunk_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code,
                                      state.data_ptr(), s_out.data_ptr(), code, out.data_ptr(),
-                                     cu.data_ptr() if packed else None, T, None, B, B * T, H, K, V, _lib.ptr(ws), n,
-                                     stream))
+                                     cu.data_ptr() if packed else None, span, None, B, B * T, H, K, V, _lib.ptr(ws),
+                                     n, stream))
         outs.append((out, s_out))
     torch.cuda.synchronize()
     # each path is within about 1e-5 of the f64 oracle (the split products keep ~2^-17)
-    assert rel_err(outs[0][0], outs[1][0]) < TOL32 and rel_err(outs[0][1], outs[1][1]) < TOL32
+    for o, s in outs[1:]:
+        assert rel_err(outs[0][0], o) < TOL32 and rel_err(outs[0][1], s) < TOL32
+    # the padded batch runs the same kernels on the same values as the dense call
+    assert torch.equal(outs[0][0], outs[1][0]) and torch.equal(outs[0][1], outs[1][1])
     status = lib.kda_chunk_fwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(), code,
                                None, None, code, outs[0][0].data_ptr(), None, T, None, B, B * T, H, K, V, None, 0,
                                stream)
     assert status == _lib.KDA_ERR_WORKSPACE
+
+
+def _packed(lens, H, K, V, dtype, seed):
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    q, k, v, g, beta, _ = workload(1, cu[-1], H, K, V, seed=seed, dtype=dtype)
+    s0 = torch.randn(len(lens), H, K, V, generator=torch.Generator().manual_seed(seed)) * 0.02
+    return cu, (q, k, v, g, beta), s0
+
+
+@pytest.mark.parametrize("dtype,K,V", [(torch.float32, 128, 128), (torch.float32, 64, 200), (torch.bfloat16, 40, 72),
+                                       (torch.float16, 128, 40), (torch.bfloat16, 128, 320)])
+def test_packed_documents_off_the_mfma_path(dtype, K, V):
+    # packed documents that the bf16 MFMA path does not take (f32 inputs, key
+    # or value dims off its grid, V past 256) run the split-bf16 chunk path on
+    # a zero-padded batch: every document against the f64 scalar recurrence
+    lens = [130, 1, 64, 257]
+    H = 2
+    cu, ins, s0 = _packed(lens, H, K, V, dtype, seed=50 + K + V)
+    assert _plan(len(lens), cu[-1], H, K, V, dtype) == -2
+    got = kda.chunkwise_kda(*_dev(*ins, s0), True, cu_seqlens=cu)
+    assert got.hidden_states.dtype == dtype and got.final_state.shape == (len(lens), H, K, V)
+    tol = TOL32 if dtype == torch.float32 else TOL16
+    for d in range(len(lens)):
+        a, b = cu[d], cu[d + 1]
+        ro, rs = c_oracle.recurrent_ref(*(t[:, a:b] for t in ins), s0[d:d + 1])
+        _check(kda.KDAOperatorOutput(got.hidden_states[:, a:b], got.final_state[d:d + 1]), ro, rs, tol,
+               f"packed {dtype} K={K} V={V} document {d} ({b - a} tokens)")
+
+
+@pytest.mark.parametrize("dtype,V", [(torch.float32, 200), (torch.bfloat16, 272)])
+def test_value_dims_past_the_slices(dtype, V):
+    # dense calls with V past 128 (f32) or past 256 (bf16) run in column slices
+    # of at most 128: right padding, an initial state, against the f64 recurrence
+    B, T, H, K = 2, 150, 2, 64
+    q, k, v, g, beta, state = workload(B, T, H, K, V, state_std=0.02, seed=52, dtype=dtype)
+    assert _plan(B, T, H, K, V, dtype) == -2
+    mask = torch.ones(B, T, dtype=torch.bool)
+    mask[0, 120:] = False
+    got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True, mask.to(DEV))
+    ro, rs = c_oracle.recurrent_ref(q, k, v, g, beta, state, valid=[120, T])
+    _check(got, ro, rs, TOL32 if dtype == torch.float32 else TOL16, f"{dtype} V={V} slices")
+
+
+def test_packed_f32_long_document():
+    # one 8192-token f32 document at H=16 (the long-context shape) through the
+    # packed path equals the dense call bit for bit (the padded batch is the
+    # dense batch), two heads checked against the f64 recurrence
+    q, k, v, g, beta, state = workload(1, 8192, 16, 128, 128, state_std=0.02, seed=53, dtype=torch.float32)
+    args = _dev(q, k, v, g, beta, state)
+    dense = kda.chunkwise_kda(*args, True)
+    packed = kda.chunkwise_kda(*args, True, cu_seqlens=[0, 8192])
+    assert torch.equal(dense.hidden_states, packed.hidden_states)
+    assert torch.equal(dense.final_state, packed.final_state)
+    for h in (4, 9):
+        sl = slice(h, h + 1)
+        ro, rs = c_oracle.recurrent_ref(q[:, :, sl], k[:, :, sl], v[:, :, sl], g[:, :, sl], beta[:, :, sl],
+                                        state[:, sl])
+        _check(kda.KDAOperatorOutput(packed.hidden_states[:, :, sl], packed.final_state[:, sl]), ro, rs, TOL32,
+               f"packed f32 T=8192 head {h}")
 
 
 @pytest.mark.parametrize("dtype,K", [(torch.float32, 128), (torch.bfloat16, 100)])
