@@ -289,6 +289,35 @@ int kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g, co
                   void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Directional derivative of the chunkwise backward, for second derivatives.
+ * For f64 values x = (q, k, v, g, beta, initial_state), the output cotangent
+ * d_out and the final-state cotangent d_final_state (NULL = zero), and
+ * tangents tx of x (same shapes; each NULL = zero), writes
+ *   t_d*     = d/de of kda_chunk_bwd's gradients (dq, dk, dv, dg, dbeta,
+ *              d_initial_state) at x + e tx,
+ *   t_out    = d/de of the output [B,T,H,V] at x + e tx,
+ *   t_final  = d/de of the final state [B,H,K,V] at x + e tx
+ * (every output pointer may be NULL).  The second derivatives are symmetric,
+ * so with tx the cotangent of the gradients these are the double backward:
+ * the cotangent of x is t_d*, that of d_out is t_out and that of
+ * d_final_state is t_final.  f64 arithmetic (the f64 backward kernel on
+ * value-and-derivative pairs), one workgroup per (sequence, head): for
+ * second-order gradients and gradient checks, not for speed.  No reference
+ * counterpart: the reference differentiates twice through autograd
+ * (tests/kda/test_kda_recurrent.py:184-198).
+ */
+size_t kda_chunk_grad_tangent_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim,
+                                              int64_t value_dim);
+int kda_chunk_grad_tangent(const double* q, const double* k, const double* v, const double* g,
+                           const double* beta, const double* initial_state, const double* d_out,
+                           const double* d_final_state, const double* tq, const double* tk, const double* tv,
+                           const double* tg, const double* tbeta, const double* t_initial_state, double* t_dq,
+                           double* t_dk, double* t_dv, double* t_dg, double* t_dbeta,
+                           double* t_d_initial_state, double* t_out, double* t_final_state, int64_t batch,
+                           int64_t tokens, int64_t heads, int64_t key_dim, int64_t value_dim, void* workspace,
+                           size_t workspace_bytes, void* stream);
+
+/*
  * Fused stages around the operator.  Tensors are contiguous, of one dtype
  * (`dtype`: f32, f16, bf16 or f64); arithmetic is f32 (f64 for f64) with one
  * rounding to the output type.

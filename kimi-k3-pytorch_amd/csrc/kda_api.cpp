@@ -370,6 +370,44 @@ int kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g, co
                           static_cast<hipStream_t>(stream));
 }
 
+size_t kda_chunk_grad_tangent_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim,
+                                              int64_t value_dim) {
+  if (batch <= 0 || tokens <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) return 0;
+  return chunk_grad_tangent_workspace_bytes(batch, tokens, heads, key_dim, value_dim);
+}
+
+int kda_chunk_grad_tangent(const double* q, const double* k, const double* v, const double* g, const double* beta,
+                           const double* initial_state, const double* d_out, const double* d_final_state,
+                           const double* tq, const double* tk, const double* tv, const double* tg, const double* tbeta,
+                           const double* t_initial_state, double* t_dq, double* t_dk, double* t_dv, double* t_dg,
+                           double* t_dbeta, double* t_d_initial_state, double* t_out, double* t_final_state,
+                           int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim, int64_t value_dim,
+                           void* workspace, size_t workspace_bytes, void* stream) {
+  g_detail[0] = '\0';
+  if (batch <= 0 || tokens <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) {
+    set_detail("chunk_grad_tangent: sizes must be positive");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (!q || !k || !v || !g || !beta || !d_out) {
+    set_detail("chunk_grad_tangent: q, k, v, g, beta and d_out must be non-null");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  if (t_d_initial_state && !initial_state) {
+    set_detail("chunk_grad_tangent: the initial-state gradient needs an initial state");
+    return KDA_ERR_INVALID_ARGUMENT;
+  }
+  const size_t need = chunk_grad_tangent_workspace_bytes(batch, tokens, heads, key_dim, value_dim);
+  if (workspace == nullptr || workspace_bytes < need || reinterpret_cast<uintptr_t>(workspace) % 16 != 0) {
+    set_detail("chunk_grad_tangent needs %zu bytes of 16-byte aligned workspace, got %zu", need, workspace_bytes);
+    return KDA_ERR_WORKSPACE;
+  }
+  const double* in[6] = {q, k, v, g, beta, initial_state};
+  const double* tan[6] = {tq, tk, tv, tg, tbeta, initial_state ? t_initial_state : nullptr};
+  double* tgrad[6] = {t_dq, t_dk, t_dv, t_dg, t_dbeta, t_d_initial_state};
+  return launch_chunk_grad_tangent(in, tan, d_out, d_final_state, tgrad, t_out, t_final_state, batch, tokens, heads,
+                                   key_dim, value_dim, workspace, static_cast<hipStream_t>(stream));
+}
+
 int kda_conv_silu_fwd(const void* x, const void* weight, const void* bias, const void* history_in, void* y,
                       void* history_out, const int32_t* valid_lens, int64_t batch, int64_t tokens, int64_t channels,
                       int64_t kernel_size, int64_t head_dim, int normalize, double eps, int dtype, void* stream) {

@@ -74,11 +74,60 @@ __host__ __device__ inline Layout64 make_layout64(int64_t NC, int64_t K, int64_t
   return L;
 }
 
+// A value and its derivative along one direction (forward-mode
+// differentiation): the kernel below, instantiated on Dual, gives the
+// directional derivative of everything it computes.
+struct Dual {
+  double v, d;
+};
+__device__ __forceinline__ Dual operator+(Dual a, Dual b) { return {a.v + b.v, a.d + b.d}; }
+__device__ __forceinline__ Dual operator-(Dual a, Dual b) { return {a.v - b.v, a.d - b.d}; }
+__device__ __forceinline__ Dual operator-(Dual a) { return {-a.v, -a.d}; }
+__device__ __forceinline__ Dual operator*(Dual a, Dual b) { return {a.v * b.v, a.d * b.v + a.v * b.d}; }
+__device__ __forceinline__ Dual operator*(double a, Dual b) { return {a * b.v, a * b.d}; }
+__device__ __forceinline__ Dual operator/(Dual a, Dual b) { return {a.v / b.v, (a.d * b.v - a.v * b.d) / (b.v * b.v)}; }
+__device__ __forceinline__ Dual& operator+=(Dual& a, Dual b) { return a = a + b; }
+__device__ __forceinline__ Dual& operator-=(Dual& a, Dual b) { return a = a - b; }
+__device__ __forceinline__ Dual dexp(Dual a) {
+  const double e = exp(a.v);
+  return {e, e * a.d};
+}
+__device__ __forceinline__ double dexp(double a) { return exp(a); }
+__device__ __forceinline__ double value(double a) { return a; }
+__device__ __forceinline__ double value(Dual a) { return a.v; }
+template <class T>
+__device__ __forceinline__ T cst(double x) {
+  if constexpr (__is_same(T, Dual))
+    return Dual{x, 0.0};
+  else
+    return x;
+}
+
+// Inputs and outputs: values, and for the Dual instantiation the direction
+// (tangents of the inputs; null = 0) and the derivatives it produces along it
+// (null = not wanted): of the gradients, of the output and of the final state.
 struct Args64 {
   const double *q, *k, *v, *g, *beta, *dout, *s0, *dsT;
-  double *dq, *dk, *dv, *dg, *dbeta, *ds0, *ws;
+  double *dq, *dk, *dv, *dg, *dbeta, *ds0;
+  void* ws;
   int64_t B, T, H, K, V, NC;
+  const double *tq, *tk, *tv, *tg, *tbeta, *ts0;
+  double *tdq, *tdk, *tdv, *tdg, *tdbeta, *tds0, *tout, *tsT;
 };
+
+template <class T>
+__device__ __forceinline__ T ld(const double* p, const double* tp, int64_t off) {
+  if constexpr (__is_same(T, Dual))
+    return Dual{p[off], tp ? tp[off] : 0.0};
+  else
+    return p[off];
+}
+template <class T>
+__device__ __forceinline__ void st(double* p, double* tp, int64_t off, T x) {
+  if (p) p[off] = value(x);
+  if constexpr (__is_same(T, Dual))
+    if (tp) tp[off] = x.d;
+}
 
 __device__ __forceinline__ int64_t tok64(int64_t b, int64_t t, int64_t T, int64_t H, int64_t h) {
   return (b * T + t) * H + h;
@@ -86,11 +135,12 @@ __device__ __forceinline__ int64_t tok64(int64_t b, int64_t t, int64_t T, int64_
 
 // C[m][n] (row stride ldc) = sum_k A(m, k) B(k, n) (+ C when acc), with
 // A(m, k) = A[m * ars + k * acs] and B(k, n) = B[k * brs + n * bcs].
-__device__ void gemm(double* C, int64_t ldc, const double* A, int64_t ars, int64_t acs, const double* B, int64_t brs,
-                     int64_t bcs, int64_t M, int64_t N, int64_t Kd, double alpha, bool acc) {
+template <class T>
+__device__ void gemm(T* C, int64_t ldc, const T* A, int64_t ars, int64_t acs, const T* B, int64_t brs, int64_t bcs,
+                     int64_t M, int64_t N, int64_t Kd, double alpha, bool acc) {
   for (int64_t idx = threadIdx.x; idx < M * N; idx += kNT) {
     const int64_t m = idx / N, n = idx % N;
-    double s = 0.0;
+    T s = cst<T>(0.0);
     for (int64_t kk = 0; kk < Kd; ++kk) s += A[m * ars + kk * acs] * B[kk * brs + n * bcs];
     C[m * ldc + n] = acc ? C[m * ldc + n] + alpha * s : alpha * s;
   }
@@ -98,65 +148,66 @@ __device__ void gemm(double* C, int64_t ldc, const double* A, int64_t ars, int64
 }
 
 // The chunk's inputs (zero past T), lg, Kg, Kt, Qg, D, A, Aqk, N and M.
-__device__ void chunk_locals(const Args64& a, const Layout64& L, double* w, int64_t b, int64_t h, int64_t c) {
+template <class T>
+__device__ void chunk_locals(const Args64& a, const Layout64& L, T* w, int64_t b, int64_t h, int64_t c) {
   const int64_t K = a.K, V = a.V, t0 = c * kC;
   for (int64_t idx = threadIdx.x; idx < kC * K; idx += kNT) {
     const int64_t r = idx / K, j = idx % K, t = t0 + r;
     const bool in = t < a.T;
     const int64_t off = tok64(b, in ? t : 0, a.T, a.H, h) * K + j;
-    w[L.q + idx] = in ? a.q[off] : 0.0;
-    w[L.k + idx] = in ? a.k[off] : 0.0;
-    w[L.lg + idx] = in ? a.g[off] : 0.0;
+    w[L.q + idx] = in ? ld<T>(a.q, a.tq, off) : cst<T>(0.0);
+    w[L.k + idx] = in ? ld<T>(a.k, a.tk, off) : cst<T>(0.0);
+    w[L.lg + idx] = in ? ld<T>(a.g, a.tg, off) : cst<T>(0.0);
   }
   for (int64_t idx = threadIdx.x; idx < kC * V; idx += kNT) {
     const int64_t r = idx / V, j = idx % V, t = t0 + r;
     const bool in = t < a.T;
     const int64_t off = tok64(b, in ? t : 0, a.T, a.H, h) * V + j;
-    w[L.v + idx] = in ? a.v[off] : 0.0;
-    w[L.dO + idx] = in ? a.dout[off] : 0.0;
+    w[L.v + idx] = in ? ld<T>(a.v, a.tv, off) : cst<T>(0.0);
+    w[L.dO + idx] = cst<T>(in ? a.dout[off] : 0.0);
   }
   for (int64_t r = threadIdx.x; r < kC; r += kNT) {
     const int64_t t = t0 + r;
-    w[L.b + r] = t < a.T ? a.beta[tok64(b, t, a.T, a.H, h)] : 0.0;
+    w[L.b + r] = t < a.T ? ld<T>(a.beta, a.tbeta, tok64(b, t, a.T, a.H, h)) : cst<T>(0.0);
   }
   __syncthreads();
   for (int64_t j = threadIdx.x; j < K; j += kNT) {  // lg = cumsum(g) down the chunk
-    double s = 0.0;
+    T s = cst<T>(0.0);
     for (int64_t r = 0; r < kC; ++r) {
       s += w[L.lg + r * K + j];
       w[L.lg + r * K + j] = s;
     }
-    w[L.D + j] = exp(s);
+    w[L.D + j] = dexp(s);
   }
   __syncthreads();
   for (int64_t idx = threadIdx.x; idx < kC * K; idx += kNT) {
     const int64_t j = idx % K;
-    const double l = w[L.lg + idx], last = w[L.lg + (kC - 1) * K + j];
-    w[L.Kg + idx] = exp(l) * w[L.k + idx];
-    w[L.Kt + idx] = exp(last - l) * w[L.k + idx];
-    w[L.Qg + idx] = exp(l) * w[L.q + idx];
+    const T l = w[L.lg + idx], last = w[L.lg + (kC - 1) * K + j];
+    w[L.Kg + idx] = dexp(l) * w[L.k + idx];
+    w[L.Kt + idx] = dexp(last - l) * w[L.k + idx];
+    w[L.Qg + idx] = dexp(l) * w[L.q + idx];
   }
   // A_ij = sum_c k_i k_j e^(lg_i - lg_j) (j < i), Aqk_ij the same with q_i (j <= i)
   for (int64_t idx = threadIdx.x; idx < kC * kC; idx += kNT) {
     const int64_t i = idx / kC, j = idx % kC;
-    double sa = 0.0, sq = 0.0;
+    T sa = cst<T>(0.0), sq = cst<T>(0.0);
     if (j <= i)
       for (int64_t x = 0; x < K; ++x) {
-        const double e = exp(w[L.lg + i * K + x] - w[L.lg + j * K + x]) * w[L.k + j * K + x];
+        const T e = dexp(w[L.lg + i * K + x] - w[L.lg + j * K + x]) * w[L.k + j * K + x];
         sa += w[L.k + i * K + x] * e;
         sq += w[L.q + i * K + x] * e;
       }
-    w[L.A + idx] = j < i ? sa : 0.0;
-    w[L.Aqk + idx] = j <= i ? sq : 0.0;
+    w[L.A + idx] = j < i ? sa : cst<T>(0.0);
+    w[L.Aqk + idx] = j <= i ? sq : cst<T>(0.0);
   }
   __syncthreads();
   // N = (I + diag(b) A)^-1 by forward substitution, row by row
   for (int64_t i = 0; i < kC; ++i) {
     for (int64_t j = threadIdx.x; j < kC; j += kNT) {
-      double s = i == j ? 1.0 : 0.0;
+      T s = cst<T>(i == j ? 1.0 : 0.0);
       if (j < i)
         for (int64_t x = j; x < i; ++x) s -= w[L.b + i] * w[L.A + i * kC + x] * w[L.N + x * kC + j];
-      w[L.N + i * kC + j] = j <= i ? s : 0.0;
+      w[L.N + i * kC + j] = j <= i ? s : cst<T>(0.0);
     }
     __syncthreads();
   }
@@ -164,33 +215,46 @@ __device__ void chunk_locals(const Args64& a, const Layout64& L, double* w, int6
   __syncthreads();
 }
 
+template <class T>
 __global__ __launch_bounds__(kNT) void chunk_bwd_f64_kernel(const Args64 a) {
   const int64_t bh = blockIdx.x, b = bh / a.H, h = bh % a.H;
   const int64_t K = a.K, V = a.V, kv = K * V;
   const Layout64 L = make_layout64(a.NC, K, V);
-  double* w = a.ws + bh * L.per;
-  // ---- forward: start states and Vt of every chunk
-  for (int64_t idx = threadIdx.x; idx < kv; idx += kNT) w[L.dS + idx] = a.s0 ? a.s0[bh * kv + idx] : 0.0;
+  T* w = static_cast<T*>(a.ws) + bh * L.per;
+  // ---- forward: start states and Vt of every chunk (and, when asked for,
+  // the output O = Qg S + Aqk Vt and the final state)
+  for (int64_t idx = threadIdx.x; idx < kv; idx += kNT)
+    w[L.dS + idx] = a.s0 ? ld<T>(a.s0, a.ts0, bh * kv + idx) : cst<T>(0.0);
   __syncthreads();
   for (int64_t c = 0; c < a.NC; ++c) {
     chunk_locals(a, L, w, b, h, c);
-    double *S = w + L.S + c * kv, *Vt = w + L.Vt + c * kC * V;
+    T *S = w + L.S + c * kv, *Vt = w + L.Vt + c * kC * V;
     for (int64_t idx = threadIdx.x; idx < kv; idx += kNT) S[idx] = w[L.dS + idx];  // dS holds the running state
     gemm(w + L.W, K, w + L.M, kC, 1, w + L.Kg, K, 1, kC, K, kC, 1.0, false);  // W = M Kg
     gemm(w + L.U, V, w + L.M, kC, 1, w + L.v, V, 1, kC, V, kC, 1.0, false);   // U = M v
     for (int64_t idx = threadIdx.x; idx < kC * V; idx += kNT) Vt[idx] = w[L.U + idx];
     __syncthreads();
     gemm(Vt, V, w + L.W, K, 1, S, V, 1, kC, V, K, -1.0, true);  // Vt = U - W S
+    if (a.tout != nullptr) {  // O = Qg S + Aqk Vt, over U (free now)
+      gemm(w + L.U, V, w + L.Qg, K, 1, S, V, 1, kC, V, K, 1.0, false);
+      gemm(w + L.U, V, w + L.Aqk, kC, 1, Vt, V, 1, kC, V, kC, 1.0, true);
+      for (int64_t idx = threadIdx.x; idx < kC * V; idx += kNT) {
+        const int64_t t = c * kC + idx / V;
+        if (t < a.T) st<T>(nullptr, a.tout, tok64(b, t, a.T, a.H, h) * V + idx % V, w[L.U + idx]);
+      }
+    }
     for (int64_t idx = threadIdx.x; idx < kv; idx += kNT) w[L.dS + idx] = w[L.D + idx / V] * S[idx];
     __syncthreads();
     gemm(w + L.dS, V, w + L.Kt, 1, K, Vt, V, 1, K, V, kC, 1.0, true);  // S' = D S + Kt^T Vt
   }
+  if (a.tsT != nullptr)
+    for (int64_t idx = threadIdx.x; idx < kv; idx += kNT) st<T>(nullptr, a.tsT, bh * kv + idx, w[L.dS + idx]);
   // ---- backward from the last chunk
-  for (int64_t idx = threadIdx.x; idx < kv; idx += kNT) w[L.dS + idx] = a.dsT ? a.dsT[bh * kv + idx] : 0.0;
+  for (int64_t idx = threadIdx.x; idx < kv; idx += kNT) w[L.dS + idx] = cst<T>(a.dsT ? a.dsT[bh * kv + idx] : 0.0);
   __syncthreads();
   for (int64_t c = a.NC - 1; c >= 0; --c) {
     chunk_locals(a, L, w, b, h, c);
-    const double *S = w + L.S + c * kv, *Vt = w + L.Vt + c * kC * V;
+    const T *S = w + L.S + c * kv, *Vt = w + L.Vt + c * kC * V;
     const int64_t t0 = c * kC;
     gemm(w + L.W, K, w + L.M, kC, 1, w + L.Kg, K, 1, kC, K, kC, 1.0, false);          // W = M Kg
     gemm(w + L.dVt, V, w + L.Kt, K, 1, w + L.dS, V, 1, kC, V, K, 1.0, false);         // Kt dS'
@@ -200,7 +264,7 @@ __global__ __launch_bounds__(kNT) void chunk_bwd_f64_kernel(const Args64 a) {
     gemm(w + L.dKt, K, Vt, V, 1, w + L.dS, 1, V, kC, K, V, 1.0, false);               // dKt = Vt dS'^T
     gemm(w + L.dW, K, w + L.dVt, V, 1, S, 1, V, kC, K, V, -1.0, false);               // dW = -dVt S^T
     for (int64_t j = threadIdx.x; j < K; j += kNT) {                                  // dD = rowsum(dS' * S)
-      double s = 0.0;
+      T s = cst<T>(0.0);
       for (int64_t x = 0; x < V; ++x) s += w[L.dS + j * V + x] * S[j * V + x];
       w[L.dD + j] = s;
     }
@@ -211,9 +275,9 @@ __global__ __launch_bounds__(kNT) void chunk_bwd_f64_kernel(const Args64 a) {
     // dv = M^T dVt
     for (int64_t idx = threadIdx.x; idx < kC * V; idx += kNT) {
       const int64_t i = idx / V, x = idx % V, t = t0 + i;
-      double s = 0.0;
+      T s = cst<T>(0.0);
       for (int64_t r = 0; r < kC; ++r) s += w[L.M + r * kC + i] * w[L.dVt + r * V + x];
-      if (t < a.T) a.dv[tok64(b, t, a.T, a.H, h) * V + x] = s;
+      if (t < a.T) st<T>(a.dv, a.tdv, tok64(b, t, a.T, a.H, h) * V + x, s);
     }
     gemm(w + L.dM, kC, w + L.dVt, V, 1, w + L.v, 1, V, kC, kC, V, 1.0, false);        // dM = dVt v^T
     gemm(w + L.dM, kC, w + L.dW, K, 1, w + L.Kg, 1, K, kC, kC, K, 1.0, true);         // + dW Kg^T
@@ -221,76 +285,76 @@ __global__ __launch_bounds__(kNT) void chunk_bwd_f64_kernel(const Args64 a) {
     // dL = -strict(N^T (dM diag b) N^T): T1 = N^T (dM diag b), then -T1 N^T
     for (int64_t idx = threadIdx.x; idx < kC * kC; idx += kNT) {
       const int64_t i = idx / kC, j = idx % kC;
-      double s = 0.0;
+      T s = cst<T>(0.0);
       for (int64_t r = 0; r < kC; ++r) s += w[L.N + r * kC + i] * w[L.dM + r * kC + j] * w[L.b + j];
       w[L.T1 + idx] = s;
     }
     __syncthreads();
     for (int64_t idx = threadIdx.x; idx < kC * kC; idx += kNT) {
       const int64_t i = idx / kC, j = idx % kC;
-      double s = 0.0;
+      T s = cst<T>(0.0);
       for (int64_t r = 0; r < kC; ++r) s += w[L.T1 + i * kC + r] * w[L.N + j * kC + r];
-      w[L.dA + idx] = j < i ? -s * w[L.b + i] : 0.0;  // dA = diag(b) dL
-      w[L.dAqk + idx] = j <= i ? w[L.dAqk + idx] : 0.0;
+      w[L.dA + idx] = j < i ? -s * w[L.b + i] : cst<T>(0.0);  // dA = diag(b) dL
+      w[L.dAqk + idx] = j <= i ? w[L.dAqk + idx] : cst<T>(0.0);
     }
     __syncthreads();
     for (int64_t j = threadIdx.x; j < kC; j += kNT) {  // dbeta
-      double s = 0.0;
+      T s = cst<T>(0.0);
       for (int64_t i = 0; i < kC; ++i) s += w[L.N + i * kC + j] * w[L.dM + i * kC + j];
-      const double bj = w[L.b + j];
-      if (bj != 0.0)  // sum_k dL_jk A_jk with dL = dA / b
+      const T bj = w[L.b + j];
+      if (value(bj) != 0.0)  // sum_k dL_jk A_jk with dL = dA / b
         for (int64_t x = 0; x < j; ++x) s += w[L.dA + j * kC + x] / bj * w[L.A + j * kC + x];
       else
         for (int64_t x = 0; x < j; ++x) {
-          double t = 0.0;
+          T t = cst<T>(0.0);
           for (int64_t r = 0; r < kC; ++r) t += w[L.T1 + j * kC + r] * w[L.N + x * kC + r];
           s -= t * w[L.A + j * kC + x];
         }
       const int64_t t = t0 + j;
-      if (t < a.T) a.dbeta[tok64(b, t, a.T, a.H, h)] = s;
+      if (t < a.T) st<T>(a.dbeta, a.tdbeta, tok64(b, t, a.T, a.H, h), s);
     }
     // per channel: the pair sums, dq, dk and d lg
     for (int64_t idx = threadIdx.x; idx < kC * K; idx += kNT) {
       const int64_t i = idx / K, x = idx % K;
-      const double li = w[L.lg + idx], ki = w[L.k + idx], qi = w[L.q + idx];
-      double r1 = 0.0, r2 = 0.0, r3 = 0.0, r4 = 0.0;
+      const T li = w[L.lg + idx], ki = w[L.k + idx], qi = w[L.q + idx];
+      T r1 = cst<T>(0.0), r2 = cst<T>(0.0), r3 = cst<T>(0.0), r4 = cst<T>(0.0);
       for (int64_t j = 0; j <= i; ++j) {  // R1, R2 over j <= i
-        const double e = exp(li - w[L.lg + j * K + x]) * w[L.k + j * K + x];
+        const T e = dexp(li - w[L.lg + j * K + x]) * w[L.k + j * K + x];
         r1 += w[L.dA + i * kC + j] * e;
         r2 += w[L.dAqk + i * kC + j] * e;
       }
       for (int64_t r = i; r < kC; ++r) {  // R3, R4 over rows r >= i
-        const double e = exp(w[L.lg + r * K + x] - li);
+        const T e = dexp(w[L.lg + r * K + x] - li);
         r3 += w[L.dA + r * kC + i] * w[L.k + r * K + x] * e;
         r4 += w[L.dAqk + r * kC + i] * w[L.q + r * K + x] * e;
       }
-      const double el = exp(li), te = exp(w[L.lg + (kC - 1) * K + x] - li);
-      const double dk = r1 + r3 + r4 + el * w[L.dKg + idx] + te * w[L.dKt + idx];
-      const double dq = r2 + el * w[L.dQg + idx];
+      const T el = dexp(li), te = dexp(w[L.lg + (kC - 1) * K + x] - li);
+      const T dk = r1 + r3 + r4 + el * w[L.dKg + idx] + te * w[L.dKt + idx];
+      const T dq = r2 + el * w[L.dQg + idx];
       w[L.dlg + idx] = ki * (r1 - r3 - r4) + qi * r2 + w[L.Kg + idx] * w[L.dKg + idx] +
                        w[L.Qg + idx] * w[L.dQg + idx] - w[L.Kt + idx] * w[L.dKt + idx];
       const int64_t t = t0 + i;
       if (t < a.T) {
         const int64_t off = tok64(b, t, a.T, a.H, h) * K + x;
-        a.dq[off] = dq;
-        a.dk[off] = dk;
+        st<T>(a.dq, a.tdq, off, dq);
+        st<T>(a.dk, a.tdk, off, dk);
       }
     }
     __syncthreads();
     for (int64_t x = threadIdx.x; x < K; x += kNT) {  // dg = reverse cumsum of d lg (+ the last row's terms)
-      double run = w[L.D + x] * w[L.dD + x];
+      T run = w[L.D + x] * w[L.dD + x];
       for (int64_t r = 0; r < kC; ++r) run += w[L.Kt + r * K + x] * w[L.dKt + r * K + x];
       for (int64_t i = kC - 1; i >= 0; --i) {
         run += w[L.dlg + i * K + x];
         const int64_t t = t0 + i;
-        if (t < a.T) a.dg[tok64(b, t, a.T, a.H, h) * K + x] = run;
+        if (t < a.T) st<T>(a.dg, a.tdg, tok64(b, t, a.T, a.H, h) * K + x, run);
       }
     }
     for (int64_t idx = threadIdx.x; idx < kv; idx += kNT) w[L.dS + idx] = w[L.dSn + idx];
     __syncthreads();
   }
-  if (a.ds0)
-    for (int64_t idx = threadIdx.x; idx < kv; idx += kNT) a.ds0[bh * kv + idx] = w[L.dS + idx];
+  if (a.ds0 || a.tds0)
+    for (int64_t idx = threadIdx.x; idx < kv; idx += kNT) st<T>(a.ds0, a.tds0, bh * kv + idx, w[L.dS + idx]);
 }
 
 }  // namespace bwd64
@@ -312,10 +376,36 @@ int launch_chunk_bwd_f64(const double* q, const double* k, const double* v, cons
     set_detail("chunk backward (f64): grid too large");
     return KDA_ERR_UNSUPPORTED;
   }
-  const kda::bwd64::Args64 a{q, k, v, g, beta, dout, s0, dsT, dq, dk, dv, dg, dbeta, ds0, ws, B, T, H, K, V, NC};
-  hipLaunchKernelGGL(kda::bwd64::chunk_bwd_f64_kernel, dim3(static_cast<unsigned>(B * H)), dim3(kda::bwd64::kNT), 0,
-                     stream, a);
+  kda::bwd64::Args64 a{};
+  a.q = q, a.k = k, a.v = v, a.g = g, a.beta = beta, a.dout = dout, a.s0 = s0, a.dsT = dsT;
+  a.dq = dq, a.dk = dk, a.dv = dv, a.dg = dg, a.dbeta = dbeta, a.ds0 = ds0, a.ws = ws;
+  a.B = B, a.T = T, a.H = H, a.K = K, a.V = V, a.NC = NC;
+  hipLaunchKernelGGL(kda::bwd64::chunk_bwd_f64_kernel<double>, dim3(static_cast<unsigned>(B * H)),
+                     dim3(kda::bwd64::kNT), 0, stream, a);
   return check_launch("chunk_bwd_f64_kernel");
+}
+
+size_t chunk_grad_tangent_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
+  return 2 * chunk_bwd_f64_workspace_bytes(B, T, H, K, V);
+}
+
+int launch_chunk_grad_tangent(const double* const* in, const double* const* tan, const double* dout,
+                              const double* dsT, double* const* tgrad, double* tout, double* tsT, int64_t B, int64_t T,
+                              int64_t H, int64_t K, int64_t V, void* ws, hipStream_t stream) {
+  const int64_t NC = (T + kda::bwd64::kC - 1) / kda::bwd64::kC;
+  if (B * H > 0x7fffffffLL) {
+    set_detail("chunk gradient tangent: grid too large");
+    return KDA_ERR_UNSUPPORTED;
+  }
+  kda::bwd64::Args64 a{};
+  a.q = in[0], a.k = in[1], a.v = in[2], a.g = in[3], a.beta = in[4], a.s0 = in[5], a.dout = dout, a.dsT = dsT;
+  a.tq = tan[0], a.tk = tan[1], a.tv = tan[2], a.tg = tan[3], a.tbeta = tan[4], a.ts0 = tan[5];
+  a.tdq = tgrad[0], a.tdk = tgrad[1], a.tdv = tgrad[2], a.tdg = tgrad[3], a.tdbeta = tgrad[4], a.tds0 = tgrad[5];
+  a.tout = tout, a.tsT = tsT, a.ws = ws;
+  a.B = B, a.T = T, a.H = H, a.K = K, a.V = V, a.NC = NC;
+  hipLaunchKernelGGL(kda::bwd64::chunk_bwd_f64_kernel<kda::bwd64::Dual>, dim3(static_cast<unsigned>(B * H)),
+                     dim3(kda::bwd64::kNT), 0, stream, a);
+  return check_launch("chunk_bwd_f64_kernel<tangent>");
 }
 
 }  // namespace kda_host

@@ -105,6 +105,17 @@ int launch_chunk_bwd_f64(const double* q, const double* k, const double* v, cons
                          double* dg, double* dbeta, double* ds0, int64_t B, int64_t T, int64_t H, int64_t K, int64_t V,
                          double* ws, hipStream_t stream);
 
+// Directional derivative of the chunk backward, of the output and of the
+// final state along tangents of the inputs (f64 arithmetic; the f64 kernel on
+// dual numbers, csrc/kda_chunk_bwd_f64.hip).  in / tan: q, k, v, g, beta,
+// s0 (tangent entries may be null); tgrad: dq, dk, dv, dg, dbeta, ds0
+// tangents (entries may be null).
+size_t chunk_grad_tangent_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
+
+int launch_chunk_grad_tangent(const double* const* in, const double* const* tan, const double* dout,
+                              const double* dsT, double* const* tgrad, double* tout, double* tsT, int64_t B, int64_t T,
+                              int64_t H, int64_t K, int64_t V, void* ws, hipStream_t stream);
+
 // Backward of the token recurrence with per-token states (csrc/kda_recurrent_bwd.hip).
 size_t recurrent_bwd_workspace_bytes(int64_t B, int64_t H, int64_t K, int64_t V, int dtype);
 

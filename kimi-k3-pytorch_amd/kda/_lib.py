@@ -85,6 +85,8 @@ SIGNATURES = {
         _I,
         [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _P, _S, _P],
     ),
+    "kda_chunk_grad_tangent_workspace_bytes": (_S, [_L, _L, _L, _L, _L]),
+    "kda_chunk_grad_tangent": (_I, [_P] * 22 + [_L] * 5 + [_P, _S, _P]),
     "kda_cache_gather": (_I, [_P, _P, _P, _I, _P, _L, _L, _P, _P]),
     "kda_recurrent_bwd_workspace_bytes": (_S, [_L, _L, _L, _L, _I]),
     "kda_recurrent_bwd": (_I, [_P] * 16 + [_L] * 5 + [_I, _P, _S, _P]),

@@ -16,19 +16,21 @@ Additive keyword-only extension: ``cu_seqlens`` (packed documents
 Gradients: with autograd enabled and an input that requires grad, the call
 goes through ``_ChunkwiseFunction``, whose backward is the HIP chunk backward
 (``kda_chunk_bwd``: f32 arithmetic for bf16/f16/f32 inputs, f64 for f64
-inputs) with key_dim and value_dim <= 128;
-the attention mask is applied with differentiable tensor ops first
-(src/kda/utils.py:82-94), so padded positions get zero gradients.  Packed
+inputs) with key_dim <= 128; the attention mask is applied with
+differentiable tensor ops first (src/kda/utils.py:82-94), so padded positions
+get zero gradients.  With ``create_graph=True`` the gradients are themselves
+differentiable (dense inputs): the double backward is
+``kda_chunk_grad_tangent``, in f64 arithmetic.  Packed
 documents (``cu_seqlens``) are differentiated in buckets of similar length:
 documents within a fifth of the bucket's longest are stacked into one
 zero-padded dense batch (zero rows are identity steps of the recurrence), a
 lone document runs on its slice of the packed tensors in place, and each
 bucket's workspace stays within max(the longest document's, 1 GiB).  A
-backward call, or a dense prefill, whose workspace would pass
+backward call, or a prefill, whose workspace would pass
 ``WORKSPACE_LIMIT`` (4 GiB) runs its heads in groups, on contiguous copies of
-the head slices.  Other
-cases raise instead of dropping gradients, and so does a second derivative
-(the backward is marked once-differentiable).
+the head slices.  Value dims past 128 differentiate in column slices.  Key
+dims past 128, second derivatives of packed documents and third derivatives
+raise instead of dropping gradients.
 """
 
 from __future__ import annotations
@@ -330,78 +332,150 @@ class _ChunkwiseFunction(torch.autograd.Function):
         return out.hidden_states, out.final_state
 
     @staticmethod
-    @torch.autograd.function.once_differentiable
     def backward(ctx, d_hidden, d_final):
-        # the HIP backward is not itself differentiable: a second derivative
-        # (create_graph=True followed by another backward) raises instead of
-        # treating these gradients as constants
         q, k, v, g, beta, initial_state = ctx.saved_tensors
+        needs = ctx.needs_input_grad[:6]
+        if torch.is_grad_enabled():
+            # create_graph: the gradients themselves are differentiable (second
+            # derivatives through kda_chunk_grad_tangent)
+            if ctx.offsets is not None:
+                raise RuntimeError("second derivatives of the MI355X KDA operator need dense inputs (no cu_seqlens)")
+            if d_hidden is None:
+                d_hidden = torch.zeros(v.shape[:3] + v.shape[3:], dtype=v.dtype, device=v.device)
+            grads = _ChunkwiseGrad.apply(q, k, v, g, beta, initial_state, d_hidden, d_final, ctx.work_dtype, needs)
+        else:
+            grads = _chunk_gradients(q, k, v, g, beta, initial_state, d_hidden, d_final, ctx.work_dtype,
+                                     ctx.offsets, needs)
+        return (*[gr if need else None for gr, need in zip(grads, needs)], None, None, None, None)
+
+
+class _ChunkwiseGrad(torch.autograd.Function):
+    """The chunk backward as a differentiable function of the operator's
+    inputs and of its output and final-state cotangents (second derivatives,
+    dense inputs).  Forward: the HIP backward (``_chunk_gradients``).
+    Backward: ``kda_chunk_grad_tangent``, the f64 backward kernel run on
+    value-and-derivative pairs along the incoming cotangents of the
+    gradients.  Second derivatives are symmetric, so that directional
+    derivative is the cotangent of the inputs, and the directional
+    derivatives of the output and of the final state are the cotangents of
+    their own cotangents: the double backward, in f64 arithmetic for every
+    input dtype.  (A third derivative raises.)"""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, beta, initial_state, d_hidden, d_final, work_dtype, needs):
+        grads = _chunk_gradients(q, k, v, g, beta, initial_state, d_hidden, d_final, work_dtype, None, needs)
+        ctx.save_for_backward(q, k, v, g, beta, initial_state, d_hidden, d_final)
+        ctx.work_dtype = work_dtype
+        return tuple(grads)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, wq, wk, wv, wg, wb, ws0):
+        q, k, v, g, beta, s0, d_hidden, d_final = ctx.saved_tensors
         lib = _lib.load()
-        (qc, kc, vc, gc, bc), kernel_dtype, _ = _prep.kernel_inputs(q, k, v, g, beta, ctx.work_dtype)
+        f64 = torch.float64
+        device = q.device
         batch, tokens, heads, key_dim = q.shape
         value_dim = v.shape[-1]
-        device = q.device
-        if d_hidden is None:
-            d_hidden = torch.zeros(batch, tokens, heads, value_dim, dtype=kernel_dtype, device=device)
-        d_out = d_hidden.to(kernel_dtype).contiguous()
-        state_dtype = torch.float64 if kernel_dtype == torch.float64 else torch.float32
-        s0 = _prep.state_arg(None if initial_state is None else initial_state.detach(), state_dtype, ctx.work_dtype)
-        ds_t = None if d_final is None else d_final.to(state_dtype).contiguous()
-        dq, dk, dv, dg = (torch.empty_like(t) for t in (qc, kc, vc, gc))
-        dbeta = torch.empty_like(bc)
-        n_state = batch if ctx.offsets is None else len(ctx.offsets) - 1
-        ds0 = None
-        if initial_state is not None and ctx.needs_input_grad[5]:
-            ds0 = torch.empty(n_state, heads, key_dim, value_dim, dtype=state_dtype, device=device)
-        code = _lib.dtype_code(kernel_dtype)
-        stream = _prep.stream(device)
+        # the values the forward and the first backward computed on (rounded
+        # to the work dtype as they were), in f64
+        ins, _, _ = _prep.kernel_inputs(q, k, v, g, beta, ctx.work_dtype)
+        x = [t.to(f64).contiguous() for t in ins]
+        s0d = _prep.state_arg(None if s0 is None else s0.detach(), f64, ctx.work_dtype)
+        d_out = d_hidden.to(f64).contiguous()
+        ds_t = None if d_final is None else d_final.to(f64).contiguous()
+        tan = [None if w is None else w.to(f64).contiguous() for w in (wq, wk, wv, wg, wb)]
+        t_s0 = None if ws0 is None or s0 is None else ws0.to(f64).contiguous()
+        need = ctx.needs_input_grad
+        outs = [torch.empty_like(t) if need[i] else None for i, t in enumerate(x)]
+        g_s0 = torch.empty_like(s0d) if s0 is not None and need[5] else None
+        t_out = torch.empty(batch, tokens, heads, value_dim, dtype=f64, device=device) if need[6] else None
+        t_fin = (torch.empty(batch, heads, key_dim, value_dim, dtype=f64, device=device)
+                 if d_final is not None and need[7] else None)
+        ws_bytes = lib.kda_chunk_grad_tangent_workspace_bytes(batch, tokens, heads, key_dim, value_dim)
+        ws = _prep.workspace(ws_bytes, device, "the chunkwise_kda second derivative")
+        _lib.check(lib.kda_chunk_grad_tangent(
+            *(t.data_ptr() for t in x), _lib.ptr(s0d), d_out.data_ptr(), _lib.ptr(ds_t),
+            *(_lib.ptr(t) for t in tan), _lib.ptr(t_s0), *(_lib.ptr(o) for o in outs), _lib.ptr(g_s0),
+            _lib.ptr(t_out), _lib.ptr(t_fin), batch, tokens, heads, key_dim, value_dim, _lib.ptr(ws), ws_bytes,
+            _prep.stream(device),
+        ))
+        grads = [None if o is None else o.to(t.dtype) for o, t in zip(outs, (q, k, v, g, beta))]
+        return (*grads, None if g_s0 is None else g_s0.to(s0.dtype),
+                None if t_out is None else t_out.to(d_hidden.dtype),
+                None if t_fin is None else t_fin.to(d_final.dtype), None, None)
 
-        def call(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, n_h, ws, ws_bytes, vdim):
-            status = lib.kda_chunk_bwd(
-                *(t.data_ptr() for t in tensors), code, _lib.ptr(s_init), _lib.ptr(ds_fin),
-                *(t.data_ptr() for t in grads_out), _lib.ptr(ds_init), n_b, n_tok, n_h, key_dim, vdim,
-                _lib.ptr(ws), ws_bytes, stream,
-            )
-            _lib.check(status)
 
-        workspace = _Workspace(device)
+def _chunk_gradients(q, k, v, g, beta, initial_state, d_hidden, d_final, work_dtype, offsets, needs):
+    """The HIP chunk backward: gradients of the output and final state's
+    loss with respect to q, k, v, g, beta and the initial state."""
+    lib = _lib.load()
+    (qc, kc, vc, gc, bc), kernel_dtype, _ = _prep.kernel_inputs(q, k, v, g, beta, work_dtype)
+    batch, tokens, heads, key_dim = q.shape
+    value_dim = v.shape[-1]
+    device = q.device
+    if d_hidden is None:
+        d_hidden = torch.zeros(batch, tokens, heads, value_dim, dtype=kernel_dtype, device=device)
+    d_out = d_hidden.to(kernel_dtype).contiguous()
+    state_dtype = torch.float64 if kernel_dtype == torch.float64 else torch.float32
+    s0 = _prep.state_arg(None if initial_state is None else initial_state.detach(), state_dtype, work_dtype)
+    ds_t = None if d_final is None else d_final.to(state_dtype).contiguous()
+    dq, dk, dv, dg = (torch.empty_like(t) for t in (qc, kc, vc, gc))
+    dbeta = torch.empty_like(bc)
+    n_state = batch if offsets is None else len(offsets) - 1
+    ds0 = None
+    if initial_state is not None and needs[5]:
+        ds0 = torch.empty(n_state, heads, key_dim, value_dim, dtype=state_dtype, device=device)
+    code = _lib.dtype_code(kernel_dtype)
+    stream = _prep.stream(device)
 
-        def backward_of(vc, d_out, s0, ds_t, grads, ds0):
-            """The kernels' backward over one value slice (at most 128 columns)."""
-            vdim = vc.shape[-1]
+    def call(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, n_h, ws, ws_bytes, vdim):
+        status = lib.kda_chunk_bwd(
+            *(t.data_ptr() for t in tensors), code, _lib.ptr(s_init), _lib.ptr(ds_fin),
+            *(t.data_ptr() for t in grads_out), _lib.ptr(ds_init), n_b, n_tok, n_h, key_dim, vdim,
+            _lib.ptr(ws), ws_bytes, stream,
+        )
+        _lib.check(status)
 
-            def run(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok):
-                _by_head_groups(lib, lambda *a: call(*a, vdim), tensors, grads_out, s_init, ds_fin, ds_init, n_b,
-                                n_tok, heads, key_dim, vdim, workspace)
+    workspace = _Workspace(device)
 
-            if ctx.offsets is None:
-                run((qc, kc, vc, gc, bc, d_out), grads, s0, ds_t, ds0, batch, tokens)
-            else:
-                _packed_backward(lib, ctx.offsets, (qc, kc, vc, gc, bc, d_out), grads, s0, ds_t, ds0, heads,
-                                 key_dim, vdim, device, run)
+    def backward_of(vc, d_out, s0, ds_t, grads, ds0):
+        """The kernels' backward over one value slice (at most 128 columns)."""
+        vdim = vc.shape[-1]
 
-        if value_dim <= 128:
-            backward_of(vc, d_out, s0, ds_t, (dq, dk, dv, dg, dbeta), ds0)
+        def run(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok):
+            _by_head_groups(lib, lambda *a: call(*a, vdim), tensors, grads_out, s_init, ds_fin, ds_init, n_b,
+                            n_tok, heads, key_dim, vdim, workspace)
+
+        if offsets is None:
+            run((qc, kc, vc, gc, bc, d_out), grads, s0, ds_t, ds0, batch, tokens)
         else:
-            # value columns never interact: the operator over V columns is the
-            # operators over column slices sharing q, k, g and beta, whose
-            # gradients add up over the slices; v and the state get theirs per slice
-            acc = [torch.zeros(t.shape, dtype=torch.float64 if kernel_dtype == torch.float64 else torch.float32,
-                               device=device) for t in (dq, dk, dg, dbeta)]
-            for c0 in range(0, value_dim, 128):
-                c1 = min(c0 + 128, value_dim)
-                part = (lambda t: None if t is None else t[..., c0:c1].contiguous())  # noqa: E731
-                g_s = [torch.empty_like(t) for t in (dq, dk)] + [torch.empty_like(part(vc))] + \
-                    [torch.empty_like(t) for t in (dg, dbeta)]
-                ds0_s = None if ds0 is None else torch.empty_like(part(ds0))
-                backward_of(part(vc), part(d_out), part(s0), part(ds_t), g_s, ds0_s)
-                for a, gs in zip(acc, (g_s[0], g_s[1], g_s[3], g_s[4])):
-                    a += gs
-                dv[..., c0:c1] = g_s[2]
-                if ds0 is not None:
-                    ds0[..., c0:c1] = ds0_s
-            for dst, a in zip((dq, dk, dg, dbeta), acc):
-                dst.copy_(a)
-        grads = [dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
-                 None if ds0 is None else ds0.to(initial_state.dtype)]
-        return (*[gr if need else None for gr, need in zip(grads, ctx.needs_input_grad[:6])], None, None, None, None)
+            _packed_backward(lib, offsets, (qc, kc, vc, gc, bc, d_out), grads, s0, ds_t, ds0, heads,
+                             key_dim, vdim, device, run)
+
+    if value_dim <= 128:
+        backward_of(vc, d_out, s0, ds_t, (dq, dk, dv, dg, dbeta), ds0)
+    else:
+        # value columns never interact: the operator over V columns is the
+        # operators over column slices sharing q, k, g and beta, whose
+        # gradients add up over the slices; v and the state get theirs per slice
+        acc = [torch.zeros(t.shape, dtype=torch.float64 if kernel_dtype == torch.float64 else torch.float32,
+                           device=device) for t in (dq, dk, dg, dbeta)]
+        for c0 in range(0, value_dim, 128):
+            c1 = min(c0 + 128, value_dim)
+            part = (lambda t: None if t is None else t[..., c0:c1].contiguous())  # noqa: E731
+            g_s = [torch.empty_like(t) for t in (dq, dk)] + [torch.empty_like(part(vc))] + \
+                [torch.empty_like(t) for t in (dg, dbeta)]
+            ds0_s = None if ds0 is None else torch.empty_like(part(ds0))
+            backward_of(part(vc), part(d_out), part(s0), part(ds_t), g_s, ds0_s)
+            for a, gs in zip(acc, (g_s[0], g_s[1], g_s[3], g_s[4])):
+                a += gs
+            dv[..., c0:c1] = g_s[2]
+            if ds0 is not None:
+                ds0[..., c0:c1] = ds0_s
+        for dst, a in zip((dq, dk, dg, dbeta), acc):
+            dst.copy_(a)
+    grads = [dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), dg.to(g.dtype), dbeta.to(beta.dtype),
+             None if ds0 is None else ds0.to(initial_state.dtype)]
+    return grads
+

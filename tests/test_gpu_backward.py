@@ -16,7 +16,7 @@ import torch
 
 import kda
 from oracle import kda_oracle as ora
-from tests._inputs import rel_err, workload
+from tests._inputs import random_core, rel_err, workload
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -143,20 +143,75 @@ def test_recurrent_and_chunkwise_f64_gradients_agree():
         torch.testing.assert_close(a.grad, b.grad, rtol=2e-10, atol=2e-11)
 
 
-@pytest.mark.parametrize("op", ["chunkwise", "recurrent_states"])
-def test_second_derivative_raises(op):
-    # The HIP backwards are once-differentiable: a second derivative (the
-    # reference's gradgradcheck, tests/kda/test_kda_recurrent.py:184-198) raises
-    # instead of silently treating the first gradients as constants.
+@pytest.mark.parametrize("op", ["chunkwise", "recurrent"])
+def test_gradgradcheck_like_the_reference(op):
+    # the reference's test_recurrent_gradcheck_and_gradgradcheck
+    # (tests/kda/test_kda_recurrent.py:184-198): f64, B=1, T=2, H=1, K=V=2,
+    # gradcheck of output and final state, gradgradcheck of the output; the
+    # second derivatives come from kda_chunk_grad_tangent
+    fn_op = kda.chunkwise_kda if op == "chunkwise" else kda.recurrent_kda
+    inputs = tuple(t.to(DEV).requires_grad_() for t in random_core(batch=1, tokens=2, heads=1, key_dim=2,
+                                                                    value_dim=2))
+    both = lambda *xs: (fn_op(*xs, output_final_state=True).hidden_states,  # noqa: E731
+                        fn_op(*xs, output_final_state=True).final_state)
+    assert torch.autograd.gradcheck(both, inputs, fast_mode=True)
+    assert torch.autograd.gradgradcheck(lambda *xs: fn_op(*xs).hidden_states, inputs, fast_mode=True)
+
+
+@pytest.mark.parametrize("B,T,H,K,V", [(2, 70, 2, 5, 3), (1, 130, 1, 16, 8)])
+def test_gradgradcheck_across_chunks_with_mask(B, T, H, K, V):
+    # several chunks, right padding, the final state in the loss, every input
+    # (initial state included) and both cotangents differentiated twice
+    q, k, v, g, beta, state = random_core(batch=B, tokens=T, heads=H, key_dim=K, value_dim=V, seed=T)
+    g = g * 0.1  # a slow decay keeps every chunk's terms in play
+    mask = torch.ones(B, T, dtype=torch.bool)
+    mask[-1, T - 11:] = False
+    inputs = tuple(t.to(DEV).requires_grad_() for t in (q, k, v, g, beta, state))
+
+    def fn(*xs):
+        r = kda.chunkwise_kda(*xs, True, mask.to(DEV))
+        return r.hidden_states, r.final_state
+
+    assert torch.autograd.gradgradcheck(fn, inputs, fast_mode=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_second_derivative_in_lower_precision_inputs(dtype):
+    # the double backward of f32/bf16 inputs runs in f64 on the same (rounded)
+    # values: a Hessian-vector product through the f32 first backward agrees
+    # with the f64 one to the first backward's precision
+    q, k, v, g, beta, state = workload(1, 90, 2, 32, 16, state_std=0.3, seed=8, dtype=dtype)
+    gen = torch.Generator().manual_seed(9)
+    u = [torch.randn(t.shape, generator=gen, dtype=torch.float64) for t in (q, k, v, g, beta)]
+
+    def hvp(tensors, st):
+        leaves = [t.to(DEV).requires_grad_() for t in tensors]
+        s0 = st.to(DEV).requires_grad_()
+        r = kda.chunkwise_kda(*leaves, s0, True)
+        loss = r.hidden_states.double().square().sum() + r.final_state.double().square().sum()
+        grads = torch.autograd.grad(loss, leaves + [s0], create_graph=True)
+        dot = sum((gr.double() * w.to(DEV)).sum() for gr, w in zip(grads[:5], u))
+        return torch.autograd.grad(dot, leaves + [s0])
+
+    got = hvp((q, k, v, g, beta), state)
+    ref = hvp([t.double() for t in (q, k, v, g, beta)], state.double())
+    for name, a, b in zip(NAMES, got, ref):
+        e = rel_err(a, b)
+        print(f"{dtype} Hessian-vector product {name}: {e:.2e}")
+        assert e < TOL[dtype], (name, e)
+
+
+def test_third_derivative_and_packed_second_derivative_raise():
     q, k, v, g, beta, state = (t.to(DEV).double() for t in workload(1, 6, 1, 16, 16, state_std=0.1, seed=3))
     q.requires_grad_()
-    if op == "chunkwise":
-        out = kda.chunkwise_kda(q, k, v, g, beta, state, True).hidden_states
-    else:
-        out = kda.recurrent_kda(q, k, v, g, beta, state, True, return_states_per_token=True).hidden_states
+    out = kda.chunkwise_kda(q, k, v, g, beta, state, True).hidden_states
     (gq,) = torch.autograd.grad(out.square().sum(), q, create_graph=True)
+    (hq,) = torch.autograd.grad(gq.square().sum(), q, create_graph=True)
     with pytest.raises(RuntimeError, match="once_differentiable|twice"):
-        gq.sum().backward()
+        hq.sum().backward()
+    out = kda.chunkwise_kda(q, k, v, g, beta, None, True, cu_seqlens=[0, 2, 6]).hidden_states
+    with pytest.raises(RuntimeError, match="dense inputs"):
+        torch.autograd.grad(out.square().sum(), q, create_graph=True)
 
 
 def test_backward_refuses_unsupported_cases():
