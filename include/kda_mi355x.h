@@ -274,7 +274,10 @@ int kda_ut_transform_bwd(const void* k, const void* v, const void* g, const void
  *                                  f64 (passed through these pointers) when dtype is f64
  *   dq, dk, dv, dg, dbeta        : outputs, shaped and typed like the inputs
  *   d_initial_state              : like initial_state, or NULL
- *   key_dim, value_dim <= 128; dense layout (packed documents: one call per document).
+ *   key_dim, value_dim <= 128; dense layout.  Packed documents are differentiated as
+ *   dense batches of similar-length documents, zero-padded (a zero row is an
+ *   identity step), by the caller (the Python wrapper's length buckets); wider
+ *   values as column slices whose dq, dk, dg, dbeta add up.
  * Arithmetic is f32 for bf16/f16/f32 inputs and f64 for f64 inputs.  The workspace
  * (kda_chunk_bwd_workspace_bytes, any dtype, 16-byte aligned) holds per-chunk
  * intermediates and is fully rewritten.
