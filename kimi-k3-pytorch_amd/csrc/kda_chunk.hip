@@ -1738,8 +1738,16 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
 // step loop is unrolled by kCombineDepth with every load unconditional (the
 // segment index clamped) and the last group padded with steps whose results
 // are dropped, so each register set is reloaded at one fixed place and the
-// waits for a step's operands cover only that step's loads.
-constexpr int kCombineDepth = 4;
+// waits for a step's operands cover only that step's loads (an early exit
+// from the unrolled group would join the loop's back edge, where the compiler
+// then waits for every load in flight).  The start state is loaded before the
+// prefetches, so the first step waits for its own operands only.  Each step
+// moves 40 KB through the CU's vector memory path (the 32 KB of P_g this
+// column tile needs whole, Q_g's slice and the stored state), which sets its
+// pace more than load latency does: two steps ahead measured fastest (13.1 us
+// for 14 steps at T=8192, H=16 against 14.8 us four ahead, whose prologue
+// burst and padded steps cost more than the shorter lead).
+constexpr int kCombineDepth = 2;
 
 struct CombineArgs {
   const int32_t* seg_start;  // [N+1], or nullptr for dense sequences
@@ -1777,12 +1785,10 @@ __global__ __launch_bounds__(512) void segment_combine_kernel(const CombineArgs 
     for (int st = 0; st < 4; ++st) Pf[d][st] = *reinterpret_cast<const bf16x8_t*>(p_base + g * p_stride + st * 64 * 8);
     Qv[d] = *reinterpret_cast<const f32x4_t*>(q_base + g * st_stride);
   };
+  const f32x4_t x = *reinterpret_cast<const f32x4_t*>(s_base + st_stride);
 #pragma unroll
   for (int d = 0; d < kCombineDepth; ++d) load_step(d, 1 + d);
-  {
-    const f32x4_t x = *reinterpret_cast<const f32x4_t*>(s_base + st_stride);
-    Sh[0][ct][lane] = bf16x4_t{(bf16)x[0], (bf16)x[1], (bf16)x[2], (bf16)x[3]};
-  }
+  Sh[0][ct][lane] = bf16x4_t{(bf16)x[0], (bf16)x[1], (bf16)x[2], (bf16)x[3]};
   __syncthreads();
   for (int lg0 = 1; lg0 <= last; lg0 += kCombineDepth) {
 #pragma unroll
