@@ -774,9 +774,7 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
       if constexpr (kPrepares<MODE>) *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKE, tl) + 2 * cp) = po.ke[r];
     }
     if constexpr (MODE == kSummary) {
-      // phase A: -Kgamma and K~^T fragments straight from the registers
-      write_channel_frags<MODE>(sm + kgf_off<MODE>(J, wave_of(tid) - 4), po.kg, J, tid & 63);
-      write_kt_frags<MODE>(sm, po.kt, J, cp);
+      // phase A: the state advance's operands wait for p1_write_late
     } else {
       // channel-major k E: rows 16 J .. 16 J + 15 of channels 2 cp, 2 cp + 1
 #pragma unroll
@@ -790,20 +788,43 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
         *reinterpret_cast<uint4*>(&KEt[2 * cp + ch][16 * J + 8]) = uint4{w[4], w[5], w[6], w[7]};
       }
     }
+    if constexpr (MODE != kSummary) {
 #pragma unroll
-    for (int ch = 0; ch < 2; ++ch) {
-      const int cc = 2 * cp + ch;
-      if constexpr (MODE == kOutput) {
-        Gs[J][cc] = po.gs[ch];
-        Ge[J][cc] = po.ge[ch];
+      for (int ch = 0; ch < 2; ++ch) {
+        const int cc = 2 * cp + ch;
+        if constexpr (MODE == kOutput) {
+          Gs[J][cc] = po.gs[ch];
+          Ge[J][cc] = po.ge[ch];
+        }
+        if (J == 0) gam[cc] = po.gam[ch];
       }
-      if (J == 0) gam[cc] = po.gam[ch];
-    }
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (ll->vlds[i] >= 0) *reinterpret_cast<uint4*>(sm + kOffVn + ll->vlds[i]) = po.vv[i];
+      for (int i = 0; i < 4; ++i)
+        if (ll->vlds[i] >= 0) *reinterpret_cast<uint4*>(sm + kOffVn + ll->vlds[i]) = po.vv[i];
+    }
   }
   __syncthreads();
+}
+
+// Phase A: the operands that only the state advance reads (-Kgamma and K~^T
+// fragments straight from the registers, gamma, the v tile), written by the
+// loader waves while waves 0-3 form the diagonal-block inverses, so that the
+// first barrier of the chunk waits for the k E tile alone.  None of these
+// tiles is touched between the previous chunk's state advance and this one's.
+template <int MODE>
+__device__ __forceinline__ void p1_write_late(unsigned char* sm, const P1Out& po, const LoaderLanes& ll, int tid) {
+  const int J = loader_block(tid);
+  const int cp = loader_pair(tid);
+  write_channel_frags<MODE>(sm + kgf_off<MODE>(J, wave_of(tid) - 4), po.kg, J, tid & 63);
+  write_kt_frags<MODE>(sm, po.kt, J, cp);
+  float* gam = lds<float>(sm, kOffGam);
+  if (J == 0) {
+    gam[2 * cp] = po.gam[0];
+    gam[2 * cp + 1] = po.gam[1];
+  }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    if (ll.vlds[i] >= 0) *reinterpret_cast<uint4*>(sm + kOffVn + ll.vlds[i]) = po.vv[i];
 }
 
 // P1 of phase C without P2, which needs no natural tiles: the loader thread
@@ -924,7 +945,8 @@ __device__ __forceinline__ void p1_write_ma(unsigned char* sm, const P1Out& po, 
 // extreme-decay path).
 template <class IT, int MODE, bool LOADER, bool DECAY, int KT>
 __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h,
-                                            int vcg, int tid, const NextLoads<IT, MODE>& nl) {
+                                            int vcg, int tid, const NextLoads<IT, MODE>& nl,
+                                            const P1Out* po = nullptr, const LoaderLanes* ll = nullptr) {
   const int lane = tid & 63;
   const int wave = wave_of(tid);
   const int n16 = lane & 15;
@@ -1253,6 +1275,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
         *lds<bf16x8_t>(sm, kgf_off<MODE>(0, 0) + (tid - 256 + 256 * k) * 16) = o;
       }
     }
+    if constexpr (LOADER && MODE == kSummary) p1_write_late<MODE>(sm, *po, *ll, tid);
     if constexpr (LOADER) nl.template load_part<6>();
   }
   __syncthreads();
@@ -1638,7 +1661,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       p1_write<MODE, true>(sm, po, &ll, tid_c);
       const NextLoads<IT, MODE> nl{&raw, chunk_loads<IT>(a, chunk_geo(sr, c + 1 - cs), c + 1, h, col0, c + 1 < c_end),
                                    &ll, tid_c};
-      prepare_mid<IT, MODE, true, DECAY, KT>(sm, a, geo, h, vcg, tid_c, nl);
+      prepare_mid<IT, MODE, true, DECAY, KT>(sm, a, geo, h, vcg, tid_c, nl, &po, &ll);
       prepare_m<IT, MODE, true>(sm, tid_c, nl);
       if constexpr (MODE == kSummary) {
         // hand the chunk's M and Aqk fragments to phase C (one column group
