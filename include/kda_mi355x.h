@@ -151,7 +151,8 @@ int kda_set_segment_chunks(int64_t chunks_per_segment);
  * the state scan with every product on split operands (x = hi + lo, two bf16
  * each, relative error about 2^-17) and the outputs in a second
  * chunk-parallel kernel; its workspace is B x H x ceil(T/64) records of
- * 593 KiB (K = V = 128).  Packed documents on that path are gathered into a
+ * 240.5 KiB (K = V = 128: the operands the forward scan and the output
+ * kernel read, and each chunk's start state and pseudo-values).  Packed documents on that path are gathered into a
  * zero-padded batch of num_seqs x dense_span tokens (dense_span must be the
  * longest document's length; a smaller one returns KDA_ERR_INVALID_ARGUMENT
  * where the host can tell, and drops tokens past it otherwise) and their
@@ -202,7 +203,8 @@ int kda_chunk_fwd_decay(const void* q, const void* k, const void* v, const void*
  * KDA_ERR_WORKSPACE before anything is launched (128 MiB covers one
  * 8192-token bf16 sequence at H=16, which needs 72.5 MB; shapes with
  * batch * heads >= 192 need only the small chunk maps; the split-bf16 path's
- * records, 593 KiB per 64 tokens and head at K = V = 128, cover 221 of them).  The call performs
+ * records, 240.5 KiB per 64 tokens and head at K = V = 128, cover about 390
+ * of them).  The call performs
  * no device allocation.  All calls on one GPU share that GPU's array:
  * calls that overlap on one GPU (two streams, two host threads) race.  The
  * stream must belong to the current device.

@@ -58,12 +58,30 @@ struct Layout {
   int64_t N, A, Aqkt, Wr, Wt, Ktr, Ktt, Qgt, Kg, U, D, S, Vt, dS, dVt, dQg, dKt, dKg, dA, dAqk, dD, per;
 };
 
-__host__ __device__ inline Layout make_layout(int64_t K, int64_t V) {
+// `backward` false: the record of the forward through these kernels (the
+// split-bf16 chunk path), which holds only what prep_kernel writes without dO,
+// the forward scan and out_kernel read (Aqk^T, W, K~^T, Qg^T, U, D, S, Vt:
+// 41% of the backward's record); the offsets of the other records are 0 and
+// nothing of the forward touches them.
+__host__ __device__ inline Layout make_layout(int64_t K, int64_t V, bool backward = true) {
   Layout L;
   L.Kp = K <= 64 ? 64 : 128;
   L.Vp = static_cast<int>((V + 31) / 32 * 32);
   const int64_t cc = kC * kC, ck = kC * L.Kp, cv = kC * L.Vp, kv = static_cast<int64_t>(L.Kp) * L.Vp;
   int64_t o = 0;
+  if (!backward) {
+    L.N = L.A = L.Wt = L.Ktr = L.Kg = L.dS = L.dVt = L.dQg = L.dKt = L.dKg = L.dA = L.dAqk = L.dD = 0;
+    L.Aqkt = o; o += cc;
+    L.Wr = o; o += ck;
+    L.Ktt = o; o += ck;
+    L.Qgt = o; o += ck;
+    L.U = o; o += cv;
+    L.D = o; o += L.Kp;
+    L.S = o; o += kv;
+    L.Vt = o; o += cv;
+    L.per = (o + 63) / 64 * 64;
+    return L;
+  }
   L.N = o; o += cc;
   L.A = o; o += cc;
   L.Aqkt = o; o += cc;  // split operands of the scans: bf16 hi plane, then lo plane
@@ -2045,7 +2063,7 @@ size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int
 }
 
 size_t chunk_split_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
-  const bwd::Layout L = bwd::make_layout(K, V);
+  const bwd::Layout L = bwd::make_layout(K, V, false);
   const int64_t nc = (T + bwd::kC - 1) / bwd::kC;
   return static_cast<size_t>(B * H * nc * L.per + bwd::seg_floats(K, V, B * H, nc, 1)) * sizeof(float);
 }
@@ -2099,7 +2117,7 @@ static int run_split(const IT* q, const IT* k, const IT* v, const IT* g, const I
   bwd::Args<IT> a{};
   a.q = q, a.k = k, a.v = v, a.g = g, a.beta = beta, a.s0 = s0;
   a.ws = ws, a.B = B, a.T = T, a.H = H, a.K = K, a.V = V, a.NC = (T + bwd::kC - 1) / bwd::kC;
-  a.L = bwd::make_layout(K, V);
+  a.L = bwd::make_layout(K, V, false);  // the forward's records only (no dO)
   a.valid = valid, a.sT = sT, a.out = out;
   set_segments(a, 1);
   const int64_t chunks = B * H * a.NC;

@@ -110,9 +110,9 @@ def _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask
         return lib.kda_chunk_fwd_workspace_bytes(n_seq, total, longest, n_h, key_dim, value_dim, code)
 
     # a prefill whose workspace passes WORKSPACE_LIMIT (f32 inputs and shapes
-    # off the MFMA path take the split-bf16 chunk path, whose workspace is the
-    # backward's; packed documents there are a zero-padded batch) runs its
-    # heads in groups
+    # off the MFMA path take the split-bf16 chunk path, whose per-chunk records
+    # are 240 KiB per head at K = V = 128; packed documents there are a
+    # zero-padded batch) runs its heads in groups
     n_h = _head_group(need, heads)
     ws_bytes = need(n_h)
     workspace = _prep.workspace(ws_bytes, device, "chunkwise_kda")
