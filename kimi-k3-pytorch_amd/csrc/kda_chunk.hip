@@ -1426,8 +1426,31 @@ __device__ __forceinline__ void scan_pair(const unsigned char* sm, f32x4_t (&S)[
   lower_product(mf_off<MODE>(), Yb, Vt);
   bf16x8_t Vb[2][2];
   pack(Vt, Vb);
+  // the output product takes V~ as hi + lo (x = bf16(x) + bf16(x - bf16(x)),
+  // about 16 bits): V~'s rounding is the largest operand error of the output
+  // (measured at B=1, T=8192, H=16, K=V=128: 5.7e-3 -> 4.5e-3 against the
+  // f32 oracle, for 12 more MFMAs per tile pair; at K <= 64 it left the
+  // error unchanged, so those shapes skip it).  The state update keeps the
+  // bf16 V~: splitting it too cut the state's error from 1.9e-3 to 4e-4 but
+  // cost 2.5% of the prefill.
+  constexpr bool kSplitV = kWritesOut<MODE> && KT == 8;
+  bf16x8_t Vl[2][2];
+  if constexpr (kSplitV) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int st = 0; st < 2; ++st)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          Vl[t][st][r] = (bf16)(Vt[t][2 * st][r] - (float)Vb[t][st][r]);
+          Vl[t][st][4 + r] = (bf16)(Vt[t][2 * st + 1][r] - (float)Vb[t][st][4 + r]);
+        }
+  }
   // O += Aqk V~
-  if constexpr (kWritesOut<MODE>) lower_product(kOffAf, Vb, O);
+  if constexpr (kWritesOut<MODE>) {
+    lower_product(kOffAf, Vb, O);
+    if constexpr (kSplitV) lower_product(kOffAf, Vl, O);
+  }
   // S <- diag(gamma) S + K~^T V~
   const float* gam = reinterpret_cast<const float*>(sm + kOffGam);
 #pragma unroll
