@@ -1290,12 +1290,21 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
 }
 
 // ---- P4: M, block row I by wave I < 4 (the loader waves are free here) ------
-template <class IT, int MODE, bool LOADER>
-__device__ __forceinline__ void prepare_m(unsigned char* sm, int tid, const NextLoads<IT, MODE>& nl) {
+struct NoWork {
+  __device__ __forceinline__ void operator()() const {}
+};
+// `loader_work` runs on the loader waves, which M does not need, before the
+// barrier.
+template <class IT, int MODE, bool LOADER, class F = NoWork>
+__device__ __forceinline__ void prepare_m(unsigned char* sm, int tid, const NextLoads<IT, MODE>& nl,
+                                          const F& loader_work = F{}) {
   if constexpr (!kPrepares<MODE>) return;  // M comes with the chunk's loads
   const int lane = tid & 63;
   const int wave = wave_of(tid);
-  if constexpr (LOADER) nl.template load_part<7>();
+  if constexpr (LOADER) {
+    nl.template load_part<7>();
+    loader_work();
+  }
   switch (wave) {
     case 0: m_block_row<0>(sm, lane); break;
     case 1: m_block_row<1>(sm, lane); break;
@@ -1685,21 +1694,27 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       const NextLoads<IT, MODE> nl{&raw, chunk_loads<IT>(a, chunk_geo(sr, c + 1 - cs), c + 1, h, col0, c + 1 < c_end),
                                    &ll, tid_c};
       prepare_mid<IT, MODE, true, DECAY, KT>(sm, a, geo, h, vcg, tid_c, nl, &po, &ll);
-      prepare_m<IT, MODE, true>(sm, tid_c, nl);
-      if constexpr (MODE == kSummary) {
-        // hand the chunk's M and Aqk fragments to phase C (one column group
-        // writes them); the scanners only read these tiles meanwhile
-        if (a.chunk_ma != nullptr && cgi == 0) {
-          unsigned char* dst = reinterpret_cast<unsigned char*>(a.chunk_ma) + (c * a.H + h) * kMaBytes;
+      // hand the chunk's M and Aqk fragments to phase C (one column group
+      // writes them, 16-byte units [M | Aqk][j][lane]): Aqk, final since P2,
+      // while waves 0-3 form M; M after it, while the scanners only read it
+      const bool hand_off = MODE == kSummary && a.chunk_ma != nullptr && cgi == 0;
+      unsigned char* ma_dst = hand_off ? reinterpret_cast<unsigned char*>(a.chunk_ma) + (c * a.H + h) * kMaBytes
+                                       : nullptr;
+      auto hand_units = [&](bool aqk) {
 #pragma unroll
-          for (int k = 0; k < 3; ++k) {
-            const int u = (tid_c - 256) + 256 * k;  // [M | Aqk][j][lane]
+        for (int k = 0; k < 3; ++k) {
+          const int u = (tid_c - 256) + 256 * k;
+          if ((u >= 384) == aqk) {
             const int slot = lower_slot((u >> 6) % 6);
-            *reinterpret_cast<uint4*>(dst + u * 16) =
-                *reinterpret_cast<const uint4*>(sm + (u < 384 ? mf_off<MODE>() : kOffAf) + (slot * 64 + (u & 63)) * 16);
+            *reinterpret_cast<uint4*>(ma_dst + u * 16) =
+                *reinterpret_cast<const uint4*>(sm + (aqk ? kOffAf : mf_off<MODE>()) + (slot * 64 + (u & 63)) * 16);
           }
         }
-      }
+      };
+      prepare_m<IT, MODE, true>(sm, tid_c, nl, [&] {
+        if (hand_off) hand_units(true);
+      });
+      if (hand_off) hand_units(false);
       if (c + 1 < c_end) {
         p1_math<IT, MODE, DECAY>(po, raw, chunk_geo(sr, c + 1 - cs), vcg, tid_c, dc);
         // the k a and q a tiles, pair scales, flags and beta of chunk c + 1:
