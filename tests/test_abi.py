@@ -8,6 +8,7 @@ import re
 from pathlib import Path
 
 import pytest
+import torch
 
 from kda import _lib
 
@@ -209,3 +210,24 @@ def test_noalloc_scratch_size_matches_the_header():
     m = re.search(r"#define KDA_NOALLOC_SCRATCH_BYTES \(\(size_t\)(\d+) << (\d+)\)", text)
     assert m is not None
     assert int(m.group(1)) << int(m.group(2)) == _lib.NOALLOC_SCRATCH_BYTES
+
+
+@pytest.mark.parametrize("B,T,H,K,V", [(1, 8192, 16, 128, 128), (2, 1000, 3, 64, 48), (4, 130, 2, 100, 5)])
+def test_split_path_forward_workspace_is_its_own_records(B, T, H, K, V):
+    # f32 inputs take the split-bf16 chunk path: one record of the forward's
+    # operands per (sequence, head, chunk) plus the forward scan's segment
+    # records, smaller than the backward's workspace at every shape
+    lib = _lib.load()
+    kp, vp = (64 if K <= 64 else 128), (V + 31) // 32 * 32
+    nc = (T + 63) // 64
+    record = 64 * 64 + 3 * 64 * kp + 2 * 64 * vp + kp + kp * vp
+    record = (record + 63) // 64 * 64
+    want_segs = min(max(-(-256 // (B * H)), 1), nc)
+    seg_len = -(-nc // want_segs)
+    segs = -(-nc // seg_len)
+    expect = 4 * (B * H * nc * record + B * H * segs * (kp * kp + 2 * kp * vp))
+    got = lib.kda_chunk_fwd_workspace_bytes(B, B * T, 0, H, K, V, _lib.dtype_code(torch.float32))
+    assert got == expect
+    assert got < lib.kda_chunk_bwd_workspace_bytes(B, T, H, K, V)
+    if (B, T, H, K, V) == (1, 8192, 16, 128, 128):
+        assert record == 61568 and got == 554696704
