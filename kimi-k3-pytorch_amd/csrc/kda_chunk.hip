@@ -773,9 +773,8 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
       const int tl = 16 * J + r;
       if constexpr (kPrepares<MODE>) *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKE, tl) + 2 * cp) = po.ke[r];
     }
-    if constexpr (MODE == kSummary) {
-      // phase A: the state advance's operands wait for p1_write_late
-    } else {
+    // phase A writes the state advance's operands later (p1_write_late)
+    if constexpr (MODE != kSummary) {
       // channel-major k E: rows 16 J .. 16 J + 15 of channels 2 cp, 2 cp + 1
 #pragma unroll
       for (int ch = 0; ch < 2; ++ch) {
