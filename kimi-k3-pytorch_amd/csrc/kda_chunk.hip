@@ -381,6 +381,15 @@ __device__ __forceinline__ ChunkGeo chunk_geo(const SeqRange& sr, int64_t lc) {
 // slice of this column group and beta.
 __device__ __forceinline__ int loader_block(int tid) { return (tid & 63) >> 4; }
 __device__ __forceinline__ int loader_pair(int tid) { return 16 * (wave_of(tid) - 4) + (tid & 15); }
+// Whether loader wave w holds channels the chunk reads.  With K <= 64 (four
+// state row tiles) waves 6 and 7 hold channels 64..127, all padding, and no
+// product reads them (P2, the state advance and the output reduce over the
+// first 64 channels only): those waves skip the channel work of P1 and keep
+// only their share of v, beta and the M/Aqk units.  With eight row tiles
+// every channel's operands are read, the padding ones as zeros, so every
+// wave forms them.
+template <bool PAD, int KT>
+__device__ __forceinline__ bool kChanWave(int w) { return !(PAD && KT == 4) || w < 6; }
 
 template <class IT>
 struct Raw {
@@ -599,12 +608,15 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 template <class IT, int MODE, bool DECAY>
 __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const ChunkGeo& cg, int vcg, int tid,
-                                        const DecayConsts& dc) {
+                                        const DecayConsts& dc, bool chan = true) {
   // rows past the chunk's valid tokens were read as zero (g = 0, k = q = 0),
   // so they give a unit decay and zero operands without a test (a decay
-  // formed from logits is zeroed there explicitly)
+  // formed from logits is zeroed there explicitly).  `chan` false (a loader
+  // wave whose channels are all padding and never read): only v and beta.
   const int J = loader_block(tid);
   const int lane = tid & 63;
+  po.ext = 0;
+  if (chan) {
   float al[2][16];
   float pj[2] = {1.f, 1.f};  // P_J = exp(lg_{16J+15} - lg_{16J})
 #pragma unroll
@@ -672,6 +684,7 @@ __device__ __forceinline__ void p1_math(P1Out& po, const Raw<IT>& raw, const Chu
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) suf[ch] *= al[ch][r];
   }
+  }  // chan
   const int t2 = tid - 256;
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -733,23 +746,25 @@ __device__ __forceinline__ void write_kt_frags(unsigned char* sm, const uint32_t
 template <int MODE>
 inline constexpr bool kEarlyP1 = MODE == kSummary;
 template <int MODE>
-__device__ __forceinline__ void p1_write_early(unsigned char* sm, const P1Out& po, int tid) {
+__device__ __forceinline__ void p1_write_early(unsigned char* sm, const P1Out& po, int tid, bool chan = true) {
   const int J = loader_block(tid);
   const int cp = loader_pair(tid);
   float(*Sc)[kKey] = lds<float[kKey]>(sm, kOffTab);
   float* betas = lds<float>(sm, kOffBeta);
+  if (chan) {
 #pragma unroll
-  for (int r = 0; r < 16; ++r) {
-    const int tl = 16 * J + r;
-    *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKA, tl) + 2 * cp) = po.ka[r];
-    *reinterpret_cast<uint32_t*>(nat_row(sm, kOffQA, tl) + 2 * cp) = po.qa[r];
-  }
+    for (int r = 0; r < 16; ++r) {
+      const int tl = 16 * J + r;
+      *reinterpret_cast<uint32_t*>(nat_row(sm, kOffKA, tl) + 2 * cp) = po.ka[r];
+      *reinterpret_cast<uint32_t*>(nat_row(sm, kOffQA, tl) + 2 * cp) = po.qa[r];
+    }
 #pragma unroll
-  for (int ch = 0; ch < 2; ++ch) {
-    const int cc = 2 * cp + ch;
+    for (int ch = 0; ch < 2; ++ch) {
+      const int cc = 2 * cp + ch;
 #pragma unroll
-    for (int jp = 0; jp < 4; ++jp)
-      if (jp <= J) Sc[J * (J + 1) / 2 + jp][cc] = po.sc[jp][ch];
+      for (int jp = 0; jp < 4; ++jp)
+        if (jp <= J) Sc[J * (J + 1) / 2 + jp][cc] = po.sc[jp][ch];
+    }
   }
   if ((tid & 63) == 0) lds<int>(sm, kOffFlag)[wave_of(tid) - 4] = po.ext;
   const int t2 = tid - 256;
@@ -759,7 +774,8 @@ __device__ __forceinline__ void p1_write_early(unsigned char* sm, const P1Out& p
 // Writes P1 (loader waves) and joins every wave at the first barrier of the
 // chunk.
 template <int MODE, bool LOADER>
-__device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, const LoaderLanes* ll, int tid) {
+__device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, const LoaderLanes* ll, int tid,
+                                         bool chan = true) {
   if constexpr (LOADER) {
     const int J = loader_block(tid);
     const int cp = loader_pair(tid);
@@ -767,7 +783,8 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
     float(*Gs)[kKey] = lds<float[kKey]>(sm, kOffGs);
     float(*Ge)[kKey] = lds<float[kKey]>(sm, kOffGe);
     float* gam = lds<float>(sm, kOffGam);
-    if constexpr (!kEarlyP1<MODE>) p1_write_early<MODE>(sm, po, tid);
+    if constexpr (!kEarlyP1<MODE>) p1_write_early<MODE>(sm, po, tid, chan);
+    if (chan) {
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       const int tl = 16 * J + r;
@@ -797,6 +814,9 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
         }
         if (J == 0) gam[cc] = po.gam[ch];
       }
+    }
+    }  // chan
+    if constexpr (MODE != kSummary) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         if (ll->vlds[i] >= 0) *reinterpret_cast<uint4*>(sm + kOffVn + ll->vlds[i]) = po.vv[i];
@@ -811,15 +831,18 @@ __device__ __forceinline__ void p1_write(unsigned char* sm, const P1Out& po, con
 // first barrier of the chunk waits for the k E tile alone.  None of these
 // tiles is touched between the previous chunk's state advance and this one's.
 template <int MODE>
-__device__ __forceinline__ void p1_write_late(unsigned char* sm, const P1Out& po, const LoaderLanes& ll, int tid) {
+__device__ __forceinline__ void p1_write_late(unsigned char* sm, const P1Out& po, const LoaderLanes& ll, int tid,
+                                              bool chan = true) {
   const int J = loader_block(tid);
   const int cp = loader_pair(tid);
-  write_channel_frags<MODE>(sm + kgf_off<MODE>(J, wave_of(tid) - 4), po.kg, J, tid & 63);
-  write_kt_frags<MODE>(sm, po.kt, J, cp);
-  float* gam = lds<float>(sm, kOffGam);
-  if (J == 0) {
-    gam[2 * cp] = po.gam[0];
-    gam[2 * cp + 1] = po.gam[1];
+  if (chan) {
+    write_channel_frags<MODE>(sm + kgf_off<MODE>(J, wave_of(tid) - 4), po.kg, J, tid & 63);
+    write_kt_frags<MODE>(sm, po.kt, J, cp);
+    float* gam = lds<float>(sm, kOffGam);
+    if (J == 0) {
+      gam[2 * cp] = po.gam[0];
+      gam[2 * cp + 1] = po.gam[1];
+    }
   }
 #pragma unroll
   for (int i = 0; i < 4; ++i)
@@ -835,9 +858,10 @@ __device__ __forceinline__ void p1_write_late(unsigned char* sm, const P1Out& po
 // as zero (g = 0, k = q = 0), so they give zero operands and a unit decay.
 template <class IT, bool DECAY>
 __device__ __forceinline__ void p1_math_ma(P1Out& po, const Raw<IT>& raw, int tid, int n_valid,
-                                           const DecayConsts& dc) {
+                                           const DecayConsts& dc, bool chan = true) {
   const int J = loader_block(tid);
   const int lane = tid & 63;
+  if (chan) {  // false: a loader wave whose channels are all padding and never read (v and M, Aqk only)
   float al[2][16];
   float pj[2] = {1.f, 1.f};
 #pragma unroll
@@ -883,6 +907,7 @@ __device__ __forceinline__ void p1_math_ma(P1Out& po, const Raw<IT>& raw, int ti
 #pragma unroll
     for (int ch = 0; ch < 2; ++ch) y[ch] *= al[ch][r];
   }
+  }  // chan
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     uint4 val = raw.vv[i];
@@ -910,21 +935,23 @@ __device__ __forceinline__ void p1_math_ma(P1Out& po, const Raw<IT>& raw, int ti
 // of reduction step J / 2.
 template <class IT, int MODE>
 __device__ __forceinline__ void p1_write_ma(unsigned char* sm, const P1Out& po, const LoaderLanes& ll, int tid,
-                                            const NextLoads<IT, MODE>& nl) {
+                                            const NextLoads<IT, MODE>& nl, bool chan = true) {
   const int lane = tid & 63;
   const int J = loader_block(tid);
   const int cp = loader_pair(tid);
   const int s = wave_of(tid) - 4;
   nl.template load_part<0>();
   nl.template load_part<1>();
-  write_channel_frags<MODE>(sm + kOffQf + (J * 4 + s) * 1024, po.qa, J, lane);
-  write_channel_frags<MODE>(sm + kgf_off<MODE>(J, s), po.ka, J, lane);
+  if (chan) {
+    write_channel_frags<MODE>(sm + kOffQf + (J * 4 + s) * 1024, po.qa, J, lane);
+    write_channel_frags<MODE>(sm + kgf_off<MODE>(J, s), po.ka, J, lane);
+  }
   nl.template load_part<2>();
   nl.template load_part<3>();
-  write_kt_frags<MODE>(sm, po.ke, J, cp);
+  if (chan) write_kt_frags<MODE>(sm, po.ke, J, cp);
   nl.template load_part<4>();
   nl.template load_part<5>();
-  if (J == 0) {
+  if (chan && J == 0) {
     float* gam = lds<float>(sm, kOffGam);
     gam[2 * cp] = po.gam[0];
     gam[2 * cp + 1] = po.gam[1];
@@ -945,7 +972,8 @@ __device__ __forceinline__ void p1_write_ma(unsigned char* sm, const P1Out& po, 
 template <class IT, int MODE, bool LOADER, bool DECAY, int KT>
 __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>& a, const ChunkGeo& cg, int64_t h,
                                             int vcg, int tid, const NextLoads<IT, MODE>& nl,
-                                            const P1Out* po = nullptr, const LoaderLanes* ll = nullptr) {
+                                            const P1Out* po = nullptr, const LoaderLanes* ll = nullptr,
+                                            bool chan = true) {
   const int lane = tid & 63;
   const int wave = wave_of(tid);
   const int n16 = lane & 15;
@@ -1274,7 +1302,7 @@ __device__ __forceinline__ void prepare_mid(unsigned char* sm, const SegArgs<IT>
         *lds<bf16x8_t>(sm, kgf_off<MODE>(0, 0) + (tid - 256 + 256 * k) * 16) = o;
       }
     }
-    if constexpr (LOADER && MODE == kSummary) p1_write_late<MODE>(sm, *po, *ll, tid);
+    if constexpr (LOADER && MODE == kSummary) p1_write_late<MODE>(sm, *po, *ll, tid, chan);
     if constexpr (LOADER) nl.template load_part<6>();
   }
   __syncthreads();
@@ -1550,6 +1578,11 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int w = wave_of(tid);
+  // scanner slot: with K <= 64 the output phases put their value tiles on
+  // scanners 2 and 3, which share SIMDs with loader waves 6 and 7 (their
+  // channels all padding, kChanWave), so that no SIMD runs a busy scanner
+  // and a busy loader
+  const int sw = (KT == 4 && kWritesOut<MODE>) ? (w ^ 2) : w;
   const int n16 = lane & 15;
   const int g4 = lane >> 4;
   const int64_t col0 = cgi * kColGroup;
@@ -1567,7 +1600,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
     for (int pp = 0; pp < kPairs; ++pp) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const int tile = 2 * w + 8 * pp + t;
+        const int tile = 2 * sw + 8 * pp + t;
 #pragma unroll
         for (int ct = 0; ct < 8; ++ct) {
           if (tile < nvt) {
@@ -1605,7 +1638,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
         const ChunkGeo geo = chunk_geo(sr, c - cs);
         const int tid_c = opaque(tid);
         __syncthreads();
-        const int tile0 = 2 * w;
+        const int tile0 = 2 * sw;
         f32x4_t O[2][4];
         const int ut[2] = {tile0 < nvt ? tile0 : -1, tile0 + 1 < nvt ? tile0 + 1 : -1};
         if (tile0 < ntiles) scan_pair<MODE, KT>(sm, S[0], ut, tid_c & 63, O);
@@ -1630,7 +1663,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       prepare_m<IT, MODE, false>(sm, tid_c, nl);
 #pragma unroll
       for (int pp = 0; pp < kPairs; ++pp) {
-        const int tile0 = 2 * w + 8 * pp;
+        const int tile0 = 2 * sw + 8 * pp;
         if (tile0 < ntiles && scan_state) {
           const int ut[2] = {tile0 < nvt ? tile0 : -1, tile0 + 1 < nvt ? tile0 + 1 : -1};
           f32x4_t O[2][4];
@@ -1651,20 +1684,21 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
     P1Out po;
     const LoaderLanes ll = loader_lanes<IT, PAD>(a, vcg, tid);
     const DecayConsts dc = decay_consts<IT, DECAY>(a, h, loader_pair(tid));
+    const bool chan = kChanWave<PAD, KT>(w);
     if (c_begin < c_end) {
       const ChunkGeo g0 = chunk_geo(sr, c_begin - cs);
       load_raw<IT, MODE>(raw, chunk_loads<IT>(a, g0, c_begin, h, col0), ll, tid);
-      p1_math_ma<IT, DECAY>(po, raw, tid, g0.n_valid, dc);
+      p1_math_ma<IT, DECAY>(po, raw, tid, g0.n_valid, dc, chan);
     }
     for (int64_t c = c_begin; c < c_end; ++c) {
       const int tid_c = opaque(tid);
       const NextLoads<IT, MODE> nl{&raw, chunk_loads<IT>(a, chunk_geo(sr, c + 1 - cs), c + 1, h, col0, c + 1 < c_end),
                                    &ll, tid_c};
-      p1_write_ma<IT, MODE>(sm, po, ll, tid_c, nl);
+      p1_write_ma<IT, MODE>(sm, po, ll, tid_c, nl, chan);
       __syncthreads();
       nl.template load_part<6>();
       nl.template load_part<7>();
-      if (c + 1 < c_end) p1_math_ma<IT, DECAY>(po, raw, tid_c, chunk_geo(sr, c + 1 - cs).n_valid, dc);
+      if (c + 1 < c_end) p1_math_ma<IT, DECAY>(po, raw, tid_c, chunk_geo(sr, c + 1 - cs).n_valid, dc, chan);
       __syncthreads();
     }
   } else {
@@ -1680,19 +1714,20 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
     P1Out po;
     const LoaderLanes ll = loader_lanes<IT, PAD>(a, vcg, tid);
     const DecayConsts dc = decay_consts<IT, DECAY>(a, h, loader_pair(tid));
+    const bool chan = kChanWave<PAD, KT>(w);
     if (c_begin < c_end) {
       const ChunkGeo g0 = chunk_geo(sr, c_begin - cs);
       load_raw<IT, MODE>(raw, chunk_loads<IT>(a, g0, c_begin, h, col0), ll, tid);
-      p1_math<IT, MODE, DECAY>(po, raw, g0, vcg, tid, dc);
-      if constexpr (kEarlyP1<MODE>) p1_write_early<MODE>(sm, po, tid);
+      p1_math<IT, MODE, DECAY>(po, raw, g0, vcg, tid, dc, chan);
+      if constexpr (kEarlyP1<MODE>) p1_write_early<MODE>(sm, po, tid, chan);
     }
     for (int64_t c = c_begin; c < c_end; ++c) {
       const ChunkGeo geo = chunk_geo(sr, c - cs);
       const int tid_c = opaque(tid);
-      p1_write<MODE, true>(sm, po, &ll, tid_c);
+      p1_write<MODE, true>(sm, po, &ll, tid_c, chan);
       const NextLoads<IT, MODE> nl{&raw, chunk_loads<IT>(a, chunk_geo(sr, c + 1 - cs), c + 1, h, col0, c + 1 < c_end),
                                    &ll, tid_c};
-      prepare_mid<IT, MODE, true, DECAY, KT>(sm, a, geo, h, vcg, tid_c, nl, &po, &ll);
+      prepare_mid<IT, MODE, true, DECAY, KT>(sm, a, geo, h, vcg, tid_c, nl, &po, &ll, chan);
       // hand the chunk's M and Aqk fragments to phase C (one column group
       // writes them, 16-byte units [M | Aqk][j][lane]): Aqk, final since P2,
       // while waves 0-3 form M; M after it, while the scanners only read it
@@ -1715,10 +1750,10 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       });
       if (hand_off) hand_units(false);
       if (c + 1 < c_end) {
-        p1_math<IT, MODE, DECAY>(po, raw, chunk_geo(sr, c + 1 - cs), vcg, tid_c, dc);
+        p1_math<IT, MODE, DECAY>(po, raw, chunk_geo(sr, c + 1 - cs), vcg, tid_c, dc, chan);
         // the k a and q a tiles, pair scales, flags and beta of chunk c + 1:
         // P2 and M of chunk c are done, and the state advance reads none of them
-        if constexpr (kEarlyP1<MODE>) p1_write_early<MODE>(sm, po, tid_c);
+        if constexpr (kEarlyP1<MODE>) p1_write_early<MODE>(sm, po, tid_c, chan);
       }
       __syncthreads();
     }
@@ -1729,7 +1764,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
     if (w < 4 && lg == nseg - 1 && a.s_out != nullptr) {
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
-        const int tile = 2 * w + t;
+        const int tile = 2 * sw + t;
         if (tile >= nvt) continue;
 #pragma unroll
         for (int ct = 0; ct < 8; ++ct) {
@@ -1753,7 +1788,7 @@ __global__ __launch_bounds__(kThreads) void chunk_segment_kernel(const SegArgs<I
       for (int pp = 0; pp < kPairs; ++pp) {
 #pragma unroll
         for (int t = 0; t < 2; ++t) {
-          const int tile = 2 * w + 8 * pp + t;
+          const int tile = 2 * sw + 8 * pp + t;
           if (tile < nvt) {
 #pragma unroll
             for (int ct = 0; ct < 8; ++ct)
