@@ -256,6 +256,8 @@ def test_chunkwise_bf16_small_head_dim():
         (1, 200, 3, 32, 48),
         (1, 150, 2, 96, 128),
         (2, 70, 2, 16, 16),     # the smallest key dim of the MFMA path
+        (1, 150, 2, 64, 256),   # K = 64 with two full column groups
+        (2, 100, 3, 32, 176),   # K = 32, the second column group 48 columns wide
     ],
 )
 def test_chunkwise_key_dims_below_128(segments, shape, segment_chunks):
