@@ -22,7 +22,9 @@
 // and Aqk, the state scans and grad's slab products use split-bf16 operands on v_mfma_f32_16x16x32_bf16 (x = hi + lo, hi = bf16(x),
 // lo = bf16(x - hi); hi*hi + hi*lo + lo*hi, dropping terms of relative size
 // 2^-17), which keeps the f32-input gradients within about 1e-5 of the f64
-// oracle.  Decay products use a 16-row block factorisation on the MFMA, with
+// oracle.  For bf16 and f16 inputs the scans and grad's slab products take
+// single bf16 operands (kSplitOps): their gradients, rounded to the input
+// type, stay within about 5e-3 of the oracle.  Decay products use a 16-row block factorisation on the MFMA, with
 // an exact pairwise-exponent path for chunks whose decays leave its range
 // (any g > 0, or a block decaying past e^-80).
 //   prep_kernel         one block per (sequence, head, chunk): A, Aqk, N by
@@ -194,6 +196,14 @@ __device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
   lo = static_cast<__bf16>(x - static_cast<float>(hi));
 }
 
+// bf16 and f16 inputs, held to 2e-2 of the f32 oracle, take the scans' and
+// the gradient slabs' products on single bf16 operands (hi*hi, one MFMA per
+// 32-deep slice, the records' lo planes neither written nor read); f32
+// inputs keep the split pairs.  prep's decay products A and Aqk stay split
+// for every input type.
+template <class IT>
+constexpr bool kSplitOps = sizeof(IT) == 4;
+
 // A split matrix in LDS with its reduction index contiguous: element (r, k)
 // at p[r * rs + k] (hi) and p[plane + r * rs + k] (lo); a right operand is
 // held as its transpose (row = output column).
@@ -204,22 +214,30 @@ struct SMat {
 
 // acc += A[r0:r0+16, 0:kd] B[0:kd, c0:c0+16]; lane (i, g) carries k = k0 + 8g ..
 // k0 + 8g + 7 of row r0 + i of A and of column c0 + i of B; kd % 32 == 0.
+// SPLIT false: hi*hi alone (the lo planes are not read).
+template <bool SPLIT = true>
 __device__ __forceinline__ f32x4 mma3(f32x4 acc, SMat A, int r0, SMat B, int c0, int kd) {
   const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
   const __bf16* pa = A.p + (r0 + i) * A.rs + 8 * g;
   const __bf16* pb = B.p + (c0 + i) * B.rs + 8 * g;
   for (int k0 = 0; k0 < kd; k0 += 32) {
-    const bf16x8 ah = *reinterpret_cast<const bf16x8*>(pa + k0), al = *reinterpret_cast<const bf16x8*>(pa + A.plane + k0);
-    const bf16x8 bh = *reinterpret_cast<const bf16x8*>(pb + k0), bl = *reinterpret_cast<const bf16x8*>(pb + B.plane + k0);
+    const bf16x8 ah = *reinterpret_cast<const bf16x8*>(pa + k0);
+    const bf16x8 bh = *reinterpret_cast<const bf16x8*>(pb + k0);
     acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
-    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+    if constexpr (SPLIT) {
+      const bf16x8 al = *reinterpret_cast<const bf16x8*>(pa + A.plane + k0);
+      const bf16x8 bl = *reinterpret_cast<const bf16x8*>(pb + B.plane + k0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
+      acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
+    }
   }
   return acc;
 }
 
 // Split record in the workspace: n bf16 hi values, then n lo values.  Eight
-// consecutive values from element idx (a multiple of 8) as two 16-byte stores.
+// consecutive values from element idx (a multiple of 8) as two 16-byte stores
+// (SPLIT false: the hi store alone).
+template <bool SPLIT = true>
 __device__ __forceinline__ void put_split8(float* rec, int n, int idx, const float* x) {
   bf16x8 hi, lo;
 #pragma unroll
@@ -231,7 +249,7 @@ __device__ __forceinline__ void put_split8(float* rec, int n, int idx, const flo
   }
   __bf16* p = reinterpret_cast<__bf16*>(rec);
   *reinterpret_cast<bf16x8*>(p + idx) = hi;
-  *reinterpret_cast<bf16x8*>(p + n + idx) = lo;
+  if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(p + n + idx) = lo;
 }
 
 __device__ __forceinline__ int64_t tok(const int64_t b, const int64_t t, const int64_t T, const int64_t H,
@@ -619,7 +637,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     float x[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) x[e] = AqkS[(c0 + e) * kRC + r];
-    put_split8(ws + a.L.Aqkt, kC * kC, 8 * i8, x);
+    put_split8<kSplitOps<IT>>(ws + a.L.Aqkt, kC * kC, 8 * i8, x);
   }
   for (int i4 = tid; bwd_records && i4 < kC * Kp / 4; i4 += kPT) {  // Kg (f32), four at a time
     const int r = (4 * i4) / Kp, col = (4 * i4) % Kp;
@@ -638,7 +656,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
       const int col = c0 + e;
       x[e] = fast_exp(lgS[(kC - 1) * kRS + col] - lgS[r * kRS + col]) * kS[r * kRS + col];
     }
-    put_split8(ws + a.L.Ktr, kC * Kp, 8 * i8, x);
+    put_split8<kSplitOps<IT>>(ws + a.L.Ktr, kC * Kp, 8 * i8, x);
   }
   for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {  // Kt^T and Qg^T split, eight positions at a time
     const int col = (8 * i8) / kC, r0 = (8 * i8) % kC;
@@ -650,8 +668,8 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
       xk[e] = fast_exp(last - lg) * kS[(r0 + e) * kRS + col];
       xq[e] = fast_exp(lg) * qS[(r0 + e) * kRS + col];
     }
-    put_split8(ws + a.L.Ktt, kC * Kp, 8 * i8, xk);
-    put_split8(ws + a.L.Qgt, kC * Kp, 8 * i8, xq);
+    put_split8<kSplitOps<IT>>(ws + a.L.Ktt, kC * Kp, 8 * i8, xk);
+    put_split8<kSplitOps<IT>>(ws + a.L.Qgt, kC * Kp, 8 * i8, xq);
   }
   if (tid < Kp) ws[a.L.D + tid] = fast_exp(lgS[(kC - 1) * kRS + tid]);
   __syncthreads();
@@ -745,8 +763,8 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
       x[e] = qS[r * kRS + c0 + e];
       y[e] = qS[(r2 + e) * kRS + c2];
     }
-    put_split8(ws + a.L.Wr, kC * Kp, 8 * i8, x);
-    if (bwd_records) put_split8(ws + a.L.Wt, kC * Kp, 8 * i8, y);
+    put_split8<kSplitOps<IT>>(ws + a.L.Wr, kC * Kp, 8 * i8, x);
+    if (bwd_records) put_split8<kSplitOps<IT>>(ws + a.L.Wt, kC * Kp, 8 * i8, y);
   }
   for (int tt = w; tt < 4 * nvt; tt += kPT / 64) {  // U = M v
     const int rt = tt & 3, ct = tt >> 2;
@@ -776,8 +794,9 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
 //                               writing each chunk's X and R (and the final
 //                               state after the last chunk).
 // The state lives in f32 MFMA accumulators, one 16-column tile per wave.
-// Every product uses split-bf16 operands
-// (x = hi + lo; hi*hi + hi*lo + lo*hi).  An accumulator pair (row tiles 2s,
+// Every product uses split-bf16 operands for f32 inputs
+// (x = hi + lo; hi*hi + hi*lo + lo*hi) and single bf16 operands otherwise
+// (kSplitOps: the records' lo planes are then neither written nor read).  An accumulator pair (row tiles 2s,
 // 2s+1) is the B operand of reduction step s with the reduction index
 // permuted as perm_k; the A operands are stored in LDS with the same
 // permutation: fragment (J, s) holds, for lane (i, g), elements
@@ -798,14 +817,17 @@ struct SegLds {
   static constexpr int bytes = d + KP * 4;
 };
 
-// A split record [R][NC] of the workspace (R x NC bf16 hi, then lo) held in
-// registers as 8-byte groups; thread tid takes the n consecutive groups from
-// tid * n (32 or 16 columns of one row), so its loads and LDS stores share one
-// base address with immediate offsets.
-template <int R, int NC>
+// A split record [R][NC] of the workspace (R x NC bf16 hi, then lo; the hi
+// plane alone when SPLIT is false) held in registers as 8-byte groups; thread
+// tid takes the n consecutive groups from tid * n (8, 16 or 32 columns of one
+// row), so its loads and LDS stores share one base address with immediate
+// offsets.
+template <int R, int NC, bool SPLIT = true>
 struct Rec {
-  static constexpr int n = R * NC / 2 / kSC;
-  static_assert(n * kSC * 2 == R * NC && (n == 8 || n == 4), "the record must split into runs of 4 or 8 groups");
+  static constexpr int planes = SPLIT ? 2 : 1;
+  static constexpr int n = R * NC * planes / 4 / kSC;
+  static_assert(n * kSC * 4 == R * NC * planes && (n == 8 || n == 4 || n == 2),
+                "the record must split into runs of 2, 4 or 8 groups");
   uint2 v[n];
   __device__ __forceinline__ void fetch(const float* rec, int tid) {
     const uint4* p = reinterpret_cast<const uint4*>(rec) + tid * (n / 2);
@@ -816,16 +838,19 @@ struct Rec {
       v[2 * j + 1] = uint2{x.z, x.w};
     }
   }
-  // into fragment layout at byte offset base of the LDS
+  // into fragment layout at byte offset base of the LDS: the group at column
+  // c of a 32-column slice is group (c % 16) / 4 of half c / 16
   __device__ __forceinline__ void store(unsigned char* sm, int base, int tid) const {
     constexpr int per_plane = R * NC / 4;
     const int q0 = tid * n, plane = q0 / per_plane, el = (q0 % per_plane) * 4;
     const int r = el / NC, c0 = el % NC;
     const int f = (r >> 4) * (NC / 32) + (c0 >> 5);
-    unsigned char* dst = sm + base + f * 2048 + plane * 1024 + (r & 15) * 16 + ((c0 & 31) >> 4) * 8;
+    unsigned char* dst = sm + base + f * 2048 + plane * 1024 + (r & 15) * 16;
 #pragma unroll
-    for (int j = 0; j < n; ++j)  // column c0 + 4 j: group g = j % 4 of half j / 4 (of half (c0 & 31) / 16 when n = 4)
-      *reinterpret_cast<uint2*>(dst + (j & 3) * 256 + (j >> 2) * 8) = v[j];
+    for (int j = 0; j < n; ++j) {
+      const int c = (c0 & 31) + 4 * j;
+      *reinterpret_cast<uint2*>(dst + ((c & 15) >> 2) * 256 + (c >> 4) * 8) = v[j];
+    }
   }
 };
 
@@ -840,23 +865,33 @@ __device__ __forceinline__ bf16x8 frag_ld(const unsigned char* sm, int base, int
   return *reinterpret_cast<const bf16x8*>(sm + base + f * 2048 + plane * 1024 + lane * 16);
 }
 
-// rows 4g..4g+3 of two accumulator tiles as one split B operand
+// rows 4g..4g+3 of two accumulator tiles as one split B operand (SPLIT
+// false: hi alone, lo left unset)
+template <bool SPLIT = true>
 __device__ __forceinline__ void split_pair(const f32x4& a, const f32x4& b, bf16x8& hi, bf16x8& lo) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
-    __bf16 h, l;
-    split_bf16(a[r], h, l);
-    hi[r] = h;
-    lo[r] = l;
-    split_bf16(b[r], h, l);
-    hi[4 + r] = h;
-    lo[4 + r] = l;
+    if constexpr (SPLIT) {
+      __bf16 h, l;
+      split_bf16(a[r], h, l);
+      hi[r] = h;
+      lo[r] = l;
+      split_bf16(b[r], h, l);
+      hi[4 + r] = h;
+      lo[4 + r] = l;
+    } else {
+      hi[r] = static_cast<__bf16>(a[r]);
+      hi[4 + r] = static_cast<__bf16>(b[r]);
+    }
   }
 }
 
+// SPLIT false: hi*hi alone (the lo parts are not read)
+template <bool SPLIT = true>
 __device__ __forceinline__ f32x4 mfma3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh, const bf16x8& bl,
                                        f32x4 acc) {
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+  if constexpr (!SPLIT) return acc;
   acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);
 }
@@ -879,6 +914,7 @@ struct DoFrag {
         x[st][e] = row0[t * step];
       }
   }
+  template <bool SPLIT>
   __device__ __forceinline__ void split(int64_t t0, int64_t T, int col, int64_t V, int g, bf16x8 (&hi)[2],
                                         bf16x8 (&lo)[2]) const {
 #pragma unroll
@@ -889,7 +925,7 @@ struct DoFrag {
         __bf16 hh, ll;
         split_bf16(real ? to_float(x[st][e]) : 0.f, hh, ll);
         hi[st][e] = hh;
-        lo[st][e] = ll;
+        if constexpr (SPLIT) lo[st][e] = ll;
       }
   }
 };
@@ -917,6 +953,7 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
   constexpr bool BWD = DIR == 1, TRANS = MODE == kSumT;
   constexpr bool DO_TERMS = BWD && !TRANS;                            // Aqk^T dO and Qg^T dO
   constexpr bool EXACT_DO = sizeof(IT) == 2 && !__is_same(IT, f16);  // bf16 dO: its lo part is zero
+  constexpr bool SPLIT = kSplitOps<IT>;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g4 = lane >> 4;
   const int nsb = seg_blocks(a, MODE);
   const int64_t bhn = a.B * a.H;
@@ -951,10 +988,10 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
     }
   }
 
-  Rec<kC, KP> ra;   // forward W, backward Kt        [64][KP]
-  Rec<KP, kC> rb;   // forward Kt^T, backward W^T    [KP][64]
-  Rec<KP, kC> rq;   // backward Qg^T
-  Rec<kC, kC> raq;  // backward Aqk^T
+  Rec<kC, KP, SPLIT> ra;   // forward W, backward Kt        [64][KP]
+  Rec<KP, kC, SPLIT> rb;   // forward Kt^T, backward W^T    [KP][64]
+  Rec<KP, kC, SPLIT> rq;   // backward Qg^T
+  Rec<kC, kC, SPLIT> raq;  // backward Aqk^T
   float dval = 0.f;
   float u[4][4];    // forward value columns: U of the next chunk, accumulator layout
   DoFrag<IT> dof;   // backward value columns: dO of the next chunk
@@ -1019,7 +1056,7 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
 #pragma unroll
           for (int r = 0; r < 4; ++r) uc[I][r] = u[I][r];
       } else {
-        dof.split(t0, a.T, col, a.V, g4, doh, dol);
+        dof.template split<SPLIT>(t0, a.T, col, a.V, g4, doh, dol);
       }
     }
     __syncthreads();
@@ -1038,34 +1075,35 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
     {
       bf16x8 xh[NKS], xl[NKS];
 #pragma unroll
-      for (int st = 0; st < NKS; ++st) split_pair(X[2 * st], X[2 * st + 1], xh[st], xl[st]);
+      for (int st = 0; st < NKS; ++st) split_pair<SPLIT>(X[2 * st], X[2 * st + 1], xh[st], xl[st]);
       bf16x8 fh[2], fl[2];
       fh[0] = frag_ld(sm, SL::fa, 0, 0, lane);
-      fl[0] = frag_ld(sm, SL::fa, 0, 1, lane);
+      if constexpr (SPLIT) fl[0] = frag_ld(sm, SL::fa, 0, 1, lane);
 #pragma unroll
       for (int k = 0; k < 4 * NKS; ++k) {  // k = I * NKS + st: fragment (I, st)
         if (k + 1 < 4 * NKS) {
           fh[(k + 1) & 1] = frag_ld(sm, SL::fa, k + 1, 0, lane);
-          fl[(k + 1) & 1] = frag_ld(sm, SL::fa, k + 1, 1, lane);
+          if constexpr (SPLIT) fl[(k + 1) & 1] = frag_ld(sm, SL::fa, k + 1, 1, lane);
         }
-        P[k / NKS] = mfma3(fh[k & 1], fl[k & 1], xh[k % NKS], xl[k % NKS], P[k / NKS]);
+        P[k / NKS] = mfma3<SPLIT>(fh[k & 1], fl[k & 1], xh[k % NKS], xl[k % NKS], P[k / NKS]);
       }
     }
     if constexpr (DO_TERMS) {
       bf16x8 fh[2], fl[2];
       fh[0] = frag_ld(sm, SL::faq, 0, 0, lane);
-      fl[0] = frag_ld(sm, SL::faq, 0, 1, lane);
+      if constexpr (SPLIT) fl[0] = frag_ld(sm, SL::faq, 0, 1, lane);
 #pragma unroll
       for (int k = 0; k < 8; ++k) {  // k = I * 2 + st
         if (k + 1 < 8) {
           fh[(k + 1) & 1] = frag_ld(sm, SL::faq, k + 1, 0, lane);
-          fl[(k + 1) & 1] = frag_ld(sm, SL::faq, k + 1, 1, lane);
+          if constexpr (SPLIT) fl[(k + 1) & 1] = frag_ld(sm, SL::faq, k + 1, 1, lane);
         }
         if constexpr (EXACT_DO) {
           P[k / 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh[k & 1], doh[k & 1], P[k / 2], 0, 0, 0);
-          P[k / 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl[k & 1], doh[k & 1], P[k / 2], 0, 0, 0);
+          if constexpr (SPLIT)
+            P[k / 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl[k & 1], doh[k & 1], P[k / 2], 0, 0, 0);
         } else {
-          P[k / 2] = mfma3(fh[k & 1], fl[k & 1], doh[k & 1], dol[k & 1], P[k / 2]);
+          P[k / 2] = mfma3<SPLIT>(fh[k & 1], fl[k & 1], doh[k & 1], dol[k & 1], P[k / 2]);
         }
       }
     }
@@ -1092,7 +1130,7 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
     // (backward value columns); one fragment pair ahead
     bf16x8 rh[2], rl[2];
 #pragma unroll
-    for (int st = 0; st < 2; ++st) split_pair(P[2 * st], P[2 * st + 1], rh[st], rl[st]);
+    for (int st = 0; st < 2; ++st) split_pair<SPLIT>(P[2 * st], P[2 * st + 1], rh[st], rl[st]);
     if (more) fetch_part(p + 1, 2);
     const float* Ds = reinterpret_cast<const float*>(sm + SL::d);
 #pragma unroll
@@ -1100,31 +1138,32 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
     {
       bf16x8 fh[2], fl[2];
       fh[0] = frag_ld(sm, SL::fb, 0, 0, lane);
-      fl[0] = frag_ld(sm, SL::fb, 0, 1, lane);
+      if constexpr (SPLIT) fl[0] = frag_ld(sm, SL::fb, 0, 1, lane);
 #pragma unroll
       for (int k = 0; k < 2 * NKT; ++k) {  // k = ct * 2 + st
         if (k + 1 < 2 * NKT) {
           fh[(k + 1) & 1] = frag_ld(sm, SL::fb, k + 1, 0, lane);
-          fl[(k + 1) & 1] = frag_ld(sm, SL::fb, k + 1, 1, lane);
+          if constexpr (SPLIT) fl[(k + 1) & 1] = frag_ld(sm, SL::fb, k + 1, 1, lane);
         }
-        X[k / 2] = mfma3(fh[k & 1], fl[k & 1], rh[k & 1], rl[k & 1], X[k / 2]);
+        X[k / 2] = mfma3<SPLIT>(fh[k & 1], fl[k & 1], rh[k & 1], rl[k & 1], X[k / 2]);
       }
     }
     if constexpr (DO_TERMS) {
       bf16x8 fh[2], fl[2];
       fh[0] = frag_ld(sm, SL::fq, 0, 0, lane);
-      fl[0] = frag_ld(sm, SL::fq, 0, 1, lane);
+      if constexpr (SPLIT) fl[0] = frag_ld(sm, SL::fq, 0, 1, lane);
 #pragma unroll
       for (int k = 0; k < 2 * NKT; ++k) {
         if (k + 1 < 2 * NKT) {
           fh[(k + 1) & 1] = frag_ld(sm, SL::fq, k + 1, 0, lane);
-          fl[(k + 1) & 1] = frag_ld(sm, SL::fq, k + 1, 1, lane);
+          if constexpr (SPLIT) fl[(k + 1) & 1] = frag_ld(sm, SL::fq, k + 1, 1, lane);
         }
         if constexpr (EXACT_DO) {
           X[k / 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fh[k & 1], doh[k & 1], X[k / 2], 0, 0, 0);
-          X[k / 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl[k & 1], doh[k & 1], X[k / 2], 0, 0, 0);
+          if constexpr (SPLIT)
+            X[k / 2] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fl[k & 1], doh[k & 1], X[k / 2], 0, 0, 0);
         } else {
-          X[k / 2] = mfma3(fh[k & 1], fl[k & 1], doh[k & 1], dol[k & 1], X[k / 2]);
+          X[k / 2] = mfma3<SPLIT>(fh[k & 1], fl[k & 1], doh[k & 1], dol[k & 1], X[k / 2]);
         }
       }
     }
@@ -1310,9 +1349,11 @@ __global__ __launch_bounds__(kOT) void out_kernel(const Args<IT> a) {
     const __bf16* qg = reinterpret_cast<const __bf16*>(ws + a.L.Qgt);
     const __bf16* aq = reinterpret_cast<const __bf16*>(ws + a.L.Aqkt);
     for (int idx = tid; idx < kC * KP; idx += kOT)
-      QgT[(idx >> 6) * kRC + (idx & 63)] = static_cast<float>(qg[idx]) + static_cast<float>(qg[kC * KP + idx]);
+      QgT[(idx >> 6) * kRC + (idx & 63)] =
+          static_cast<float>(qg[idx]) + (kSplitOps<IT> ? static_cast<float>(qg[kC * KP + idx]) : 0.f);
     for (int idx = tid; idx < kC * kC; idx += kOT)
-      AqT[(idx >> 6) * kRC + (idx & 63)] = static_cast<float>(aq[idx]) + static_cast<float>(aq[kC * kC + idx]);
+      AqT[(idx >> 6) * kRC + (idx & 63)] =
+          static_cast<float>(aq[idx]) + (kSplitOps<IT> ? static_cast<float>(aq[kC * kC + idx]) : 0.f);
   }
   const int rt = w & 3, ct = w >> 2;
   for (int s0 = 0; s0 < a.L.Vp; s0 += 32) {
@@ -1361,7 +1402,9 @@ static_assert(kOffY + kC * kRS <= kGradFloats, "dW and Kg must fit");
 static_assert(kOffA + kC * kRC <= kGradFloats, "second-stage tiles must fit");
 
 // One slab tile (rows x 32 columns, f32 values v for columns c4..c4+3 of row r)
-// into a split tile of row stride kSR (bf16) and plane `plane`.
+// into a split tile of row stride kSR (bf16) and plane `plane` (SPLIT false:
+// the hi values alone).
+template <bool SPLIT = true>
 __device__ __forceinline__ void put_split4(__bf16* dst, int plane, int r, int c4, f32x4 v) {
   bf16x4 hi, lo;
 #pragma unroll
@@ -1372,11 +1415,11 @@ __device__ __forceinline__ void put_split4(__bf16* dst, int plane, int r, int c4
     lo[e] = y;
   }
   *reinterpret_cast<bf16x4*>(dst + r * kSR + c4) = hi;
-  *reinterpret_cast<bf16x4*>(dst + plane + r * kSR + c4) = lo;
+  if constexpr (SPLIT) *reinterpret_cast<bf16x4*>(dst + plane + r * kSR + c4) = lo;
 }
 
 // A NROW x 32 workspace slab (row stride ld, from column col0), split into LDS.
-template <int NROW, int NT>
+template <int NROW, int NT, bool SPLIT>
 __device__ __forceinline__ void load_ws_split(__bf16* dst, const float* src, int ld, int col0, int tid) {
   constexpr int PER = NROW * 8 / NT;
   static_assert(PER * NT == NROW * 8, "the tile must split evenly over the threads");
@@ -1389,7 +1432,7 @@ __device__ __forceinline__ void load_ws_split(__bf16* dst, const float* src, int
 #pragma unroll
   for (int it = 0; it < PER; ++it) {
     const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
-    put_split4(dst, NROW * kSR, r, c4, v[it]);
+    put_split4<SPLIT>(dst, NROW * kSR, r, c4, v[it]);
   }
 }
 
@@ -1428,18 +1471,18 @@ struct GradSlab {
 #pragma unroll
     for (int it = 0; it < PS; ++it) {
       const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
-      put_split4(Ss, KP * kSR, r, c4, s[it]);
-      put_split4(dSn, KP * kSR, r, c4, ds[it]);
+      put_split4<kSplitOps<IT>>(Ss, KP * kSR, r, c4, s[it]);
+      put_split4<kSplitOps<IT>>(dSn, KP * kSR, r, c4, ds[it]);
     }
 #pragma unroll
     for (int it = 0; it < PC; ++it) {
       const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
-      put_split4(Vts, kC * kSR, r, c4, vt[it]);
-      put_split4(dVts, kC * kSR, r, c4, dvt[it]);
+      put_split4<kSplitOps<IT>>(Vts, kC * kSR, r, c4, vt[it]);
+      put_split4<kSplitOps<IT>>(dVts, kC * kSR, r, c4, dvt[it]);
       *reinterpret_cast<f32x4*>(&dVf[r * kSS + c4]) = dvt[it];
       const bool real = t0 + r < T;
-      put_split4(dOs, kC * kSR, r, c4, real ? widen<IT>(dout[it]) : zero4());
-      put_split4(vs, kC * kSR, r, c4, real ? widen<IT>(v[it]) : zero4());
+      put_split4<kSplitOps<IT>>(dOs, kC * kSR, r, c4, real ? widen<IT>(dout[it]) : zero4());
+      put_split4<kSplitOps<IT>>(vs, kC * kSR, r, c4, real ? widen<IT>(v[it]) : zero4());
     }
   }
 };
@@ -1462,7 +1505,7 @@ __device__ __forceinline__ void load_rows_split(__bf16* dst, const IT* src, int6
 #pragma unroll
     for (int it = 0; it < PER; ++it) {
       const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
-      put_split4(dst, kC * kSR, r, c4, t0 + r < T ? widen<IT>(v[it]) : zero4());
+      put_split4<kSplitOps<IT>>(dst, kC * kSR, r, c4, t0 + r < T ? widen<IT>(v[it]) : zero4());
     }
   } else {
     for (int it = 0; it < PER; ++it) {
@@ -1474,7 +1517,7 @@ __device__ __forceinline__ void load_rows_split(__bf16* dst, const IT* src, int6
         const int64_t col = col0 + c4 + u;
         x[u] = (t < T && col < X) ? to_float(src[tok(b, t, T, H, h) * X + col]) : 0.f;
       }
-      put_split4(dst, kC * kSR, r, c4, x);
+      put_split4<kSplitOps<IT>>(dst, kC * kSR, r, c4, x);
     }
   }
 }
@@ -1521,10 +1564,10 @@ __device__ __forceinline__ void grad_body(const Args<IT>& a, float* sm, float* b
     if (ahead) {
       gs.store(Ss, dSn, Vts, dVts, dVf, dOs, vs, t0, a.T, tid);
     } else {
-      load_ws_split<KP, NT>(Ss, ws + a.L.S, Vp, s0, tid);
-      load_ws_split<KP, NT>(dSn, ws + a.L.dS, Vp, s0, tid);
-      load_ws_split<kC, NT>(Vts, ws + a.L.Vt, Vp, s0, tid);
-      load_ws_split<kC, NT>(dVts, ws + a.L.dVt, Vp, s0, tid);
+      load_ws_split<KP, NT, kSplitOps<IT>>(Ss, ws + a.L.S, Vp, s0, tid);
+      load_ws_split<KP, NT, kSplitOps<IT>>(dSn, ws + a.L.dS, Vp, s0, tid);
+      load_ws_split<kC, NT, kSplitOps<IT>>(Vts, ws + a.L.Vt, Vp, s0, tid);
+      load_ws_split<kC, NT, kSplitOps<IT>>(dVts, ws + a.L.dVt, Vp, s0, tid);
       load_ws<kC, kSW, kSS, NT>(dVf, ws + a.L.dVt, Vp, s0, tid);
       load_rows_split<IT, NT>(dOs, a.dout, b, t0, a.T, a.H, h, a.V, s0, tid);
       load_rows_split<IT, NT>(vs, a.v, b, t0, a.T, a.H, h, a.V, s0, tid);
@@ -1545,20 +1588,23 @@ __device__ __forceinline__ void grad_body(const Args<IT>& a, float* sm, float* b
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int ct = hf * CH + j;
-      aQ[j] = mma3(aQ[j], mdO, 16 * rt, mS, 16 * ct, kSW);
-      aT[j] = mma3(aT[j], mVt, 16 * rt, mdS, 16 * ct, kSW);
-      aW[j] = mma3(aW[j], mdVt, 16 * rt, mS, 16 * ct, kSW);
+      aQ[j] = mma3<kSplitOps<IT>>(aQ[j], mdO, 16 * rt, mS, 16 * ct, kSW);
+      aT[j] = mma3<kSplitOps<IT>>(aT[j], mVt, 16 * rt, mdS, 16 * ct, kSW);
+      aW[j] = mma3<kSplitOps<IT>>(aW[j], mdVt, 16 * rt, mS, 16 * ct, kSW);
     }
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
       const int ct = hf * 2 + j;
-      aA[j] = mma3(aA[j], mdO, 16 * rt, mVt, 16 * ct, kSW);
-      aM[j] = mma3(aM[j], mdVt, 16 * rt, mv, 16 * ct, kSW);
+      aA[j] = mma3<kSplitOps<IT>>(aA[j], mdO, 16 * rt, mVt, 16 * ct, kSW);
+      aM[j] = mma3<kSplitOps<IT>>(aM[j], mdVt, 16 * rt, mv, 16 * ct, kSW);
     }
     if (tid < Kp)
       for (int cc = 0; cc < kSW; ++cc) {
-        const float sv = static_cast<float>(Ss[tid * kSR + cc]) + static_cast<float>(Ss[KP * kSR + tid * kSR + cc]);
-        const float dv = static_cast<float>(dSn[tid * kSR + cc]) + static_cast<float>(dSn[KP * kSR + tid * kSR + cc]);
+        float sv = static_cast<float>(Ss[tid * kSR + cc]), dv = static_cast<float>(dSn[tid * kSR + cc]);
+        if constexpr (kSplitOps<IT>) {
+          sv += static_cast<float>(Ss[KP * kSR + tid * kSR + cc]);
+          dv += static_cast<float>(dSn[KP * kSR + tid * kSR + cc]);
+        }
         dd += dv * sv;
       }
     __syncthreads();
