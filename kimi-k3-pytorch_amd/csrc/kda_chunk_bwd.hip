@@ -58,25 +58,32 @@ typedef float f32x4 __attribute__((ext_vector_type(4)));
 struct Layout {
   int Kp, Vp;  // K padded to 64 or 128, V to a multiple of 32
   int64_t N, A, Aqkt, Wr, Wt, Ktr, Ktt, Qgt, Kg, U, D, S, Vt, dS, dVt, dQg, dKt, dKg, dA, dAqk, dD, per;
+  int hs;  // S, dS and Vt of the backward stored as bf16 (single-operand inputs)
 };
 
 // `backward` false: the record of the forward through these kernels (the
 // split-bf16 chunk path), which holds only what prep_kernel writes without dO,
 // the forward scan and out_kernel read (Aqk^T, W, K~^T, Qg^T, U, D, S, Vt:
 // 41% of the backward's record); the offsets of the other records are 0 and
-// nothing of the forward touches them.
-__host__ __device__ inline Layout make_layout(int64_t K, int64_t V, bool backward = true) {
+// nothing of the forward touches them.  `split` false (bf16 and f16 inputs,
+// kSplitOps): the scans' operand records hold their hi plane alone and, in
+// the backward, S, dS and Vt are bf16 (the gradient kernel reads them as bf16
+// operands), which takes the backward's record from 593 to 425 KiB at
+// K = V = 128.
+__host__ __device__ inline Layout make_layout(int64_t K, int64_t V, bool backward = true, bool split = true) {
   Layout L;
   L.Kp = K <= 64 ? 64 : 128;
   L.Vp = static_cast<int>((V + 31) / 32 * 32);
   const int64_t cc = kC * kC, ck = kC * L.Kp, cv = kC * L.Vp, kv = static_cast<int64_t>(L.Kp) * L.Vp;
+  const int64_t sc = split ? cc : cc / 2, sk = split ? ck : ck / 2;  // split records in floats
   int64_t o = 0;
+  L.hs = 0;
   if (!backward) {
     L.N = L.A = L.Wt = L.Ktr = L.Kg = L.dS = L.dVt = L.dQg = L.dKt = L.dKg = L.dA = L.dAqk = L.dD = 0;
-    L.Aqkt = o; o += cc;
-    L.Wr = o; o += ck;
-    L.Ktt = o; o += ck;
-    L.Qgt = o; o += ck;
+    L.Aqkt = o; o += sc;
+    L.Wr = o; o += sk;
+    L.Ktt = o; o += sk;
+    L.Qgt = o; o += sk;
     L.U = o; o += cv;
     L.D = o; o += L.Kp;
     L.S = o; o += kv;
@@ -84,20 +91,22 @@ __host__ __device__ inline Layout make_layout(int64_t K, int64_t V, bool backwar
     L.per = (o + 63) / 64 * 64;
     return L;
   }
+  L.hs = split ? 0 : 1;
+  const int64_t hv = split ? kv : kv / 2, hc = split ? cv : cv / 2;  // S, dS and Vt in floats
   L.N = o; o += cc;
   L.A = o; o += cc;
-  L.Aqkt = o; o += cc;  // split operands of the scans: bf16 hi plane, then lo plane
-  L.Wr = o; o += ck;
-  L.Wt = o; o += ck;
-  L.Ktr = o; o += ck;
-  L.Ktt = o; o += ck;
-  L.Qgt = o; o += ck;
+  L.Aqkt = o; o += sc;  // split operands of the scans: bf16 hi plane, then lo plane
+  L.Wr = o; o += sk;
+  L.Wt = o; o += sk;
+  L.Ktr = o; o += sk;
+  L.Ktt = o; o += sk;
+  L.Qgt = o; o += sk;
   L.Kg = o; o += ck;
   L.U = o; o += cv;
   L.D = o; o += L.Kp;
-  L.S = o; o += kv;
-  L.Vt = o; o += cv;
-  L.dS = o; o += kv;
+  L.S = o; o += hv;
+  L.Vt = o; o += hc;
+  L.dS = o; o += hv;
   L.dVt = o; o += cv;
   L.dQg = o; o += ck;
   L.dKt = o; o += ck;
@@ -203,6 +212,15 @@ __device__ __forceinline__ void split_bf16(float x, __bf16& hi, __bf16& lo) {
 // for every input type.
 template <class IT>
 constexpr bool kSplitOps = sizeof(IT) == 4;
+
+template <bool B, class T, class F>
+struct Pick {
+  typedef T type;
+};
+template <class T, class F>
+struct Pick<false, T, F> {
+  typedef F type;
+};
 
 // A split matrix in LDS with its reduction index contiguous: element (r, k)
 // at p[r * rs + k] (hi) and p[plane + r * rs + k] (lo); a right operand is
@@ -1115,16 +1133,37 @@ __device__ __forceinline__ void seg_body(const Args<IT>& a, int64_t id, unsigned
       for (int r = 0; r < 4; ++r) P[I][r] = (!BWD && !TRANS ? uc[I][r] : 0.f) - P[I][r];
     if constexpr (MODE == kRun) {  // this chunk's X and R (the backward stores dVt = -R)
       const int lo = opaque(4 * g4 * Vp + col);
-      float* xo = ws + (BWD ? a.L.dS : a.L.S) + lo;
-      float* ro = ws + (BWD ? a.L.dVt : a.L.Vt) + lo;
+      if (!SPLIT && a.L.hs) {  // S, dS and Vt as bf16 (dVt stays f32)
+        __bf16* xo = reinterpret_cast<__bf16*>(ws + (BWD ? a.L.dS : a.L.S)) + lo;
 #pragma unroll
-      for (int ct = 0; ct < NKT; ++ct)
+        for (int ct = 0; ct < NKT; ++ct)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) xo[(16 * ct + r) * Vp] = X[ct][r];
+          for (int r = 0; r < 4; ++r) xo[(16 * ct + r) * Vp] = static_cast<__bf16>(X[ct][r]);
+        if constexpr (BWD) {
+          float* ro = ws + a.L.dVt + lo;
 #pragma unroll
-      for (int I = 0; I < 4; ++I)
+          for (int I = 0; I < 4; ++I)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) ro[(16 * I + r) * Vp] = BWD ? -P[I][r] : P[I][r];
+            for (int r = 0; r < 4; ++r) ro[(16 * I + r) * Vp] = -P[I][r];
+        } else {
+          __bf16* ro = reinterpret_cast<__bf16*>(ws + a.L.Vt) + lo;
+#pragma unroll
+          for (int I = 0; I < 4; ++I)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) ro[(16 * I + r) * Vp] = static_cast<__bf16>(P[I][r]);
+        }
+      } else {
+        float* xo = ws + (BWD ? a.L.dS : a.L.S) + lo;
+        float* ro = ws + (BWD ? a.L.dVt : a.L.Vt) + lo;
+#pragma unroll
+        for (int ct = 0; ct < NKT; ++ct)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) xo[(16 * ct + r) * Vp] = X[ct][r];
+#pragma unroll
+        for (int I = 0; I < 4; ++I)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) ro[(16 * I + r) * Vp] = BWD ? -P[I][r] : P[I][r];
+      }
     }
     // X' = D X + A^T R (forward A = Kt, backward A = W), plus Qg^T dO
     // (backward value columns); one fragment pair ahead
@@ -1436,6 +1475,26 @@ __device__ __forceinline__ void load_ws_split(__bf16* dst, const float* src, int
   }
 }
 
+// A NROW x 32 bf16 workspace slab (row stride ld, from column col0) into the
+// hi plane of a split tile.
+template <int NROW, int NT>
+__device__ __forceinline__ void load_ws_half(__bf16* dst, const float* src, int ld, int col0, int tid) {
+  constexpr int PER = NROW * 8 / NT;
+  static_assert(PER * NT == NROW * 8, "the tile must split evenly over the threads");
+  const __bf16* p = reinterpret_cast<const __bf16*>(src);
+  bf16x4 v[PER];
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+    v[it] = *reinterpret_cast<const bf16x4*>(p + r * ld + col0 + c4);
+  }
+#pragma unroll
+  for (int it = 0; it < PER; ++it) {
+    const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
+    *reinterpret_cast<bf16x4*>(dst + r * kSR + c4) = v[it];
+  }
+}
+
 // One 32-column slab of grad_body's operands in registers: the S and dS
 // rows (KP x 32), Vt and dVt (64 x 32, f32 from the workspace) and dO and v
 // (64 x 32 from the inputs; the whole-group case of load_rows_split).  The
@@ -1444,21 +1503,34 @@ template <class IT, int KP, int NT>
 struct GradSlab {
   static constexpr int PS = KP * 8 / NT, PC = kC * 8 / NT;
   static_assert(PS * NT == KP * 8 && PC * NT == kC * 8, "the slab must split evenly over the threads");
-  f32x4 s[PS], ds[PS], vt[PC], dvt[PC];
+  // S, dS and Vt as the workspace holds them: f32 for f32 inputs, bf16 otherwise
+  // (the backward's layout for single-operand inputs, Layout::hs)
+  static constexpr bool W32 = kSplitOps<IT>;
+  typedef typename Pick<W32, f32x4, bf16x4>::type st_t;
+  st_t s[PS], ds[PS], vt[PC];
+  f32x4 dvt[PC];
   typename Raw4<IT>::type dout[PC], v[PC];
+  __device__ __forceinline__ static st_t ld(const float* base, int idx) {
+    if constexpr (W32) return *reinterpret_cast<const f32x4*>(base + idx);
+    else return *reinterpret_cast<const bf16x4*>(reinterpret_cast<const __bf16*>(base) + idx);
+  }
+  __device__ __forceinline__ static void put(__bf16* dst, int plane, int r, int c4, const st_t& x) {
+    if constexpr (W32) put_split4<true>(dst, plane, r, c4, x);
+    else *reinterpret_cast<bf16x4*>(dst + r * kSR + c4) = x;
+  }
   __device__ __forceinline__ void fetch(const Args<IT>& a, const float* ws, int64_t b, int64_t t0, int64_t h, int s0,
                                         int tid) {
     const int Vp = a.L.Vp;
 #pragma unroll
     for (int it = 0; it < PS; ++it) {
       const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
-      s[it] = *reinterpret_cast<const f32x4*>(ws + a.L.S + r * Vp + s0 + c4);
-      ds[it] = *reinterpret_cast<const f32x4*>(ws + a.L.dS + r * Vp + s0 + c4);
+      s[it] = ld(ws + a.L.S, r * Vp + s0 + c4);
+      ds[it] = ld(ws + a.L.dS, r * Vp + s0 + c4);
     }
 #pragma unroll
     for (int it = 0; it < PC; ++it) {
       const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
-      vt[it] = *reinterpret_cast<const f32x4*>(ws + a.L.Vt + r * Vp + s0 + c4);
+      vt[it] = ld(ws + a.L.Vt, r * Vp + s0 + c4);
       dvt[it] = *reinterpret_cast<const f32x4*>(ws + a.L.dVt + r * Vp + s0 + c4);
       const int64_t t = t0 + r < a.T ? t0 + r : a.T - 1;
       const int64_t row = tok(b, t, a.T, a.H, h) * a.V + s0 + c4;
@@ -1471,18 +1543,18 @@ struct GradSlab {
 #pragma unroll
     for (int it = 0; it < PS; ++it) {
       const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
-      put_split4<kSplitOps<IT>>(Ss, KP * kSR, r, c4, s[it]);
-      put_split4<kSplitOps<IT>>(dSn, KP * kSR, r, c4, ds[it]);
+      put(Ss, KP * kSR, r, c4, s[it]);
+      put(dSn, KP * kSR, r, c4, ds[it]);
     }
 #pragma unroll
     for (int it = 0; it < PC; ++it) {
       const int item = tid + NT * it, r = item >> 3, c4 = (item & 7) * 4;
-      put_split4<kSplitOps<IT>>(Vts, kC * kSR, r, c4, vt[it]);
-      put_split4<kSplitOps<IT>>(dVts, kC * kSR, r, c4, dvt[it]);
+      put(Vts, kC * kSR, r, c4, vt[it]);
+      put_split4<W32>(dVts, kC * kSR, r, c4, dvt[it]);
       *reinterpret_cast<f32x4*>(&dVf[r * kSS + c4]) = dvt[it];
       const bool real = t0 + r < T;
-      put_split4<kSplitOps<IT>>(dOs, kC * kSR, r, c4, real ? widen<IT>(dout[it]) : zero4());
-      put_split4<kSplitOps<IT>>(vs, kC * kSR, r, c4, real ? widen<IT>(v[it]) : zero4());
+      put_split4<W32>(dOs, kC * kSR, r, c4, real ? widen<IT>(dout[it]) : zero4());
+      put_split4<W32>(vs, kC * kSR, r, c4, real ? widen<IT>(v[it]) : zero4());
     }
   }
 };
@@ -1564,9 +1636,15 @@ __device__ __forceinline__ void grad_body(const Args<IT>& a, float* sm, float* b
     if (ahead) {
       gs.store(Ss, dSn, Vts, dVts, dVf, dOs, vs, t0, a.T, tid);
     } else {
-      load_ws_split<KP, NT, kSplitOps<IT>>(Ss, ws + a.L.S, Vp, s0, tid);
-      load_ws_split<KP, NT, kSplitOps<IT>>(dSn, ws + a.L.dS, Vp, s0, tid);
-      load_ws_split<kC, NT, kSplitOps<IT>>(Vts, ws + a.L.Vt, Vp, s0, tid);
+      if constexpr (kSplitOps<IT>) {
+        load_ws_split<KP, NT, true>(Ss, ws + a.L.S, Vp, s0, tid);
+        load_ws_split<KP, NT, true>(dSn, ws + a.L.dS, Vp, s0, tid);
+        load_ws_split<kC, NT, true>(Vts, ws + a.L.Vt, Vp, s0, tid);
+      } else {  // bf16 S, dS and Vt
+        load_ws_half<KP, NT>(Ss, ws + a.L.S, Vp, s0, tid);
+        load_ws_half<KP, NT>(dSn, ws + a.L.dS, Vp, s0, tid);
+        load_ws_half<kC, NT>(Vts, ws + a.L.Vt, Vp, s0, tid);
+      }
       load_ws_split<kC, NT, kSplitOps<IT>>(dVts, ws + a.L.dVt, Vp, s0, tid);
       load_ws<kC, kSW, kSS, NT>(dVf, ws + a.L.dVt, Vp, s0, tid);
       load_rows_split<IT, NT>(dOs, a.dout, b, t0, a.T, a.H, h, a.V, s0, tid);
@@ -2163,7 +2241,7 @@ static int run_split(const IT* q, const IT* k, const IT* v, const IT* g, const I
   bwd::Args<IT> a{};
   a.q = q, a.k = k, a.v = v, a.g = g, a.beta = beta, a.s0 = s0;
   a.ws = ws, a.B = B, a.T = T, a.H = H, a.K = K, a.V = V, a.NC = (T + bwd::kC - 1) / bwd::kC;
-  a.L = bwd::make_layout(K, V, false);  // the forward's records only (no dO)
+  a.L = bwd::make_layout(K, V, false, bwd::kSplitOps<IT>);  // the forward's records only (no dO)
   a.valid = valid, a.sT = sT, a.out = out;
   set_segments(a, 1);
   const int64_t chunks = B * H * a.NC;
@@ -2259,7 +2337,8 @@ int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
                                 static_cast<double*>(dq), static_cast<double*>(dk), static_cast<double*>(dv),
                                 static_cast<double*>(dg), static_cast<double*>(dbeta), reinterpret_cast<double*>(ds0),
                                 B, T, H, K, V, static_cast<double*>(workspace), stream);
-  const bwd::Layout L = bwd::make_layout(K, V);
+  // single-operand records for bf16 and f16 inputs (within the f32 size queried)
+  const bwd::Layout L = bwd::make_layout(K, V, true, in_dtype == KDA_DTYPE_F32);
   const int64_t NC = (T + bwd::kC - 1) / bwd::kC;
   float* ws = static_cast<float*>(workspace);
   switch (in_dtype) {
