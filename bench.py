@@ -339,9 +339,9 @@ def bench_backward(reps=10):
     d_final = torch.randn(P_B, P_H, P_K, P_V, generator=gen, device=device)
     grads = [torch.empty_like(t) for t in (q, k, v, g, beta)]
     ds0 = torch.empty_like(s0)
-    nbytes = lib.kda_chunk_bwd_workspace_bytes(P_B, P_T, P_H, P_K, P_V)
-    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
     code = _lib.dtype_code(torch.bfloat16)
+    nbytes = lib.kda_chunk_bwd_workspace_bytes(P_B, P_T, P_H, P_K, P_V, code)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
     stream = _prep.stream(device)
 
     def call():

@@ -40,7 +40,7 @@
 extern "C" {
 #endif
 
-#define KDA_ABI_VERSION 9
+#define KDA_ABI_VERSION 10
 
 /* status codes */
 #define KDA_OK 0
@@ -280,12 +280,14 @@ int kda_ut_transform_bwd(const void* k, const void* v, const void* g, const void
  *   dense batches of similar-length documents, zero-padded (a zero row is an
  *   identity step), by the caller (the Python wrapper's length buckets); wider
  *   values as column slices whose dq, dk, dg, dbeta add up.
- * Arithmetic is f32 for bf16/f16/f32 inputs and f64 for f64 inputs.  The workspace
- * (kda_chunk_bwd_workspace_bytes, any dtype, 16-byte aligned) holds per-chunk
- * intermediates and is fully rewritten.
+ * Arithmetic is f32 for bf16/f16/f32 inputs and f64 for f64 inputs; the state
+ * scans and the gradient slabs multiply split-bf16 operands for f32 inputs and
+ * single bf16 operands for bf16/f16 inputs.  The workspace
+ * (kda_chunk_bwd_workspace_bytes for the same dtype, 16-byte aligned; 0 for an
+ * unknown dtype) holds per-chunk intermediates and is fully rewritten.
  */
 size_t kda_chunk_bwd_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim,
-                                     int64_t value_dim);
+                                     int64_t value_dim, int dtype);
 
 int kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
                   const void* d_out, int dtype, const float* initial_state, const float* d_final_state,

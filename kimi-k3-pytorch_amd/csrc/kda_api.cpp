@@ -342,9 +342,10 @@ int kda_ut_transform_bwd(const void* k, const void* v, const void* g, const void
 }
 
 size_t kda_chunk_bwd_workspace_bytes(int64_t batch, int64_t tokens, int64_t heads, int64_t key_dim,
-                                     int64_t value_dim) {
+                                     int64_t value_dim, int dtype) {
   if (batch <= 0 || tokens <= 0 || heads <= 0 || key_dim <= 0 || value_dim <= 0) return 0;
-  return chunk_bwd_workspace_bytes(batch, tokens, heads, key_dim, value_dim);
+  if (dtype != KDA_DTYPE_BF16 && dtype != KDA_DTYPE_F16 && dtype != KDA_DTYPE_F32 && dtype != KDA_DTYPE_F64) return 0;
+  return chunk_bwd_workspace_bytes(batch, tokens, heads, key_dim, value_dim, dtype);
 }
 
 int kda_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta, const void* d_out,

@@ -2177,17 +2177,16 @@ namespace kda_host {
 
 using namespace kda;
 
-size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
-  const bwd::Layout L = bwd::make_layout(K, V);
+size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int in_dtype) {
+  if (in_dtype == KDA_DTYPE_F64) return chunk_bwd_f64_workspace_bytes(B, T, H, K, V);
+  // bf16 and f16 inputs keep the single-operand records (bwd::kSplitOps)
+  const bwd::Layout L = bwd::make_layout(K, V, true, in_dtype == KDA_DTYPE_F32);
   const int64_t nc = (T + bwd::kC - 1) / bwd::kC;
-  const size_t f32 =
-      static_cast<size_t>(B * H * nc * L.per + bwd::seg_floats(K, V, B * H, nc, 2)) * sizeof(float);
-  const size_t f64 = chunk_bwd_f64_workspace_bytes(B, T, H, K, V);  // one size serves every dtype
-  return f32 > f64 ? f32 : f64;
+  return static_cast<size_t>(B * H * nc * L.per + bwd::seg_floats(K, V, B * H, nc, 2)) * sizeof(float);
 }
 
-size_t chunk_split_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V) {
-  const bwd::Layout L = bwd::make_layout(K, V, false);
+size_t chunk_split_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int in_dtype) {
+  const bwd::Layout L = bwd::make_layout(K, V, false, in_dtype == KDA_DTYPE_F32);
   const int64_t nc = (T + bwd::kC - 1) / bwd::kC;
   return static_cast<size_t>(B * H * nc * L.per + bwd::seg_floats(K, V, B * H, nc, 1)) * sizeof(float);
 }
@@ -2264,8 +2263,8 @@ int launch_chunk_split(const void* q, const void* k, const void* v, const void* 
     set_detail("chunk_fwd: the split-bf16 chunk path needs bf16/f16/f32 inputs, K and V in 1..128 and T > 0");
     return KDA_ERR_UNSUPPORTED;
   }
-  if (workspace == nullptr || workspace_bytes < chunk_split_workspace_bytes(B, T, H, K, V)) {
-    set_detail("chunk_fwd: workspace of %zu bytes needed", chunk_split_workspace_bytes(B, T, H, K, V));
+  if (workspace == nullptr || workspace_bytes < chunk_split_workspace_bytes(B, T, H, K, V, in_dtype)) {
+    set_detail("chunk_fwd: workspace of %zu bytes needed", chunk_split_workspace_bytes(B, T, H, K, V, in_dtype));
     return KDA_ERR_WORKSPACE;
   }
   if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0) {
@@ -2320,7 +2319,7 @@ int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
     set_detail("chunk backward: key_dim and value_dim must be <= 128 (got %lld, %lld)", (long long)K, (long long)V);
     return KDA_ERR_UNSUPPORTED;
   }
-  const size_t need = chunk_bwd_workspace_bytes(B, T, H, K, V);
+  const size_t need = chunk_bwd_workspace_bytes(B, T, H, K, V, in_dtype);
   if (workspace == nullptr || workspace_bytes < need) {
     set_detail("chunk backward: workspace of %zu bytes needed", need);
     return KDA_ERR_WORKSPACE;
@@ -2337,7 +2336,7 @@ int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
                                 static_cast<double*>(dq), static_cast<double*>(dk), static_cast<double*>(dv),
                                 static_cast<double*>(dg), static_cast<double*>(dbeta), reinterpret_cast<double*>(ds0),
                                 B, T, H, K, V, static_cast<double*>(workspace), stream);
-  // single-operand records for bf16 and f16 inputs (within the f32 size queried)
+  // single-operand records for bf16 and f16 inputs
   const bwd::Layout L = bwd::make_layout(K, V, true, in_dtype == KDA_DTYPE_F32);
   const int64_t NC = (T + bwd::kC - 1) / bwd::kC;
   float* ws = static_cast<float*>(workspace);
@@ -2386,7 +2385,7 @@ size_t chunk_split_general_workspace_bytes(int64_t N, int64_t T, int64_t H, int6
   const int64_t e = elem_bytes(in_dtype);
   const bool sliced = V > kSliceCols;
   const int64_t w = sliced ? kSliceCols : V;
-  int64_t bytes = static_cast<int64_t>(chunk_split_workspace_bytes(N, T, H, K, w));
+  int64_t bytes = static_cast<int64_t>(chunk_split_workspace_bytes(N, T, H, K, w, in_dtype));
   if (packed) bytes += 3 * align256(N * T * H * K * e) + align256(N * T * H * e) + align256(N * 4);
   if (packed || sliced) bytes += 2 * align256(N * T * H * w * e);
   if (sliced) bytes += 2 * align256(N * H * K * w * 4);
@@ -2457,7 +2456,7 @@ int launch_chunk_split_general(const void* q, const void* k, const void* v, cons
     p += align256(bytes);
     return r;
   };
-  char* split_ws = take(static_cast<int64_t>(chunk_split_workspace_bytes(N, T, H, K, w)));
+  char* split_ws = take(static_cast<int64_t>(chunk_split_workspace_bytes(N, T, H, K, w, in_dtype)));
   const int64_t rows = N * T;  // dense tokens
   const void *dq = q, *dk = k, *dg = g, *db = beta;
   const int32_t* valid = valid_lens;
@@ -2482,7 +2481,7 @@ int launch_chunk_split_general(const void* q, const void* k, const void* v, cons
   char* go = take(rows * H * w * e);
   char* gs_in = sliced ? take(N * H * K * w * 4) : nullptr;
   char* gs_out = sliced ? take(N * H * K * w * 4) : nullptr;
-  const size_t split_bytes = chunk_split_workspace_bytes(N, T, H, K, w);
+  const size_t split_bytes = chunk_split_workspace_bytes(N, T, H, K, w, in_dtype);
   for (int64_t c0 = 0; c0 < V; c0 += w) {
     const int64_t wc = V - c0 < w ? V - c0 : w;
     // value rows of this slice: one per (token, head), wc columns of V

@@ -66,7 +66,7 @@ int launch_ut_transform_bwd(const void* k, const void* v, const void* g, const v
                             hipStream_t stream);
 
 // Backward of the chunkwise operator (csrc/kda_chunk_bwd.hip).
-size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
+size_t chunk_bwd_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int in_dtype);
 
 int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g, const void* beta,
                      const void* dout, int in_dtype, const float* s0, const float* dsT, void* dq, void* dk, void* dv,
@@ -78,7 +78,7 @@ int launch_chunk_bwd(const void* q, const void* k, const void* v, const void* g,
 // right padding, f32 state, K and V up to 128.
 bool chunk_split_path(int in_dtype, int state_dtype, int64_t K, int64_t V);
 
-size_t chunk_split_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V);
+size_t chunk_split_workspace_bytes(int64_t B, int64_t T, int64_t H, int64_t K, int64_t V, int in_dtype);
 
 int launch_chunk_split(const void* q, const void* k, const void* v, const void* g, const void* beta, int in_dtype,
                        const float* s_in, float* s_out, void* out, const int32_t* valid_lens, int64_t B, int64_t T,

@@ -14,7 +14,7 @@ from pathlib import Path
 import torch
 
 LIB_PATH = Path(__file__).resolve().with_name("libkda_mi355x.so")
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 KDA_OK = 0
 KDA_ERR_INVALID_ARGUMENT = 1
@@ -80,7 +80,7 @@ SIGNATURES = {
     "kda_rmsnorm_gate_bwd": (_I, [_P, _P, _I, _P, _P, _P, _P, _P, _L, _L, _L, ctypes.c_double, _I, _P]),
     "kda_ut_transform_bwd_workspace_bytes": (_S, [_L, _L, _L, _L, _I]),
     "kda_ut_transform_bwd": (_I, [_P, _P, _P, _P, _I] + [_P] * 9 + [_I, _L, _L, _L, _L, _L, _P, _S, _P]),
-    "kda_chunk_bwd_workspace_bytes": (_S, [_L, _L, _L, _L, _L]),
+    "kda_chunk_bwd_workspace_bytes": (_S, [_L, _L, _L, _L, _L, _I]),
     "kda_chunk_bwd": (
         _I,
         [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _P, _S, _P],

@@ -223,14 +223,14 @@ class _Workspace:
 
 
 def _by_head_groups(lib, call, tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok, heads, key_dim,
-                    value_dim, workspace):
+                    value_dim, workspace, code):
     """One chunk-backward over [n_b, n_tok, heads, *] tensors, split into
     head groups when the whole call's workspace would pass WORKSPACE_LIMIT.
     Heads are independent in KDA (every state, decay and gradient is per
     head), so a group is the same computation on contiguous copies of its
     head slices, its gradients copied back."""
     def need(n):
-        return lib.kda_chunk_bwd_workspace_bytes(n_b, n_tok, n, key_dim, value_dim)
+        return lib.kda_chunk_bwd_workspace_bytes(n_b, n_tok, n, key_dim, value_dim, code)
 
     n_h = _head_group(need, heads)
     ws_bytes = need(n_h)
@@ -255,7 +255,7 @@ def _by_head_groups(lib, call, tensors, grads_out, s_init, ds_fin, ds_init, n_b,
             ds_init.narrow(1, h0, h1 - h0).copy_(ds_g)
 
 
-def _packed_backward(lib, offsets, inputs, grads, s0, ds_t, ds0, heads, key_dim, value_dim, device, run):
+def _packed_backward(lib, offsets, inputs, grads, s0, ds_t, ds0, heads, key_dim, value_dim, device, run, code):
     """The chunk backward of packed documents in few calls: documents of
     similar length are stacked into one zero-padded dense batch [n, T_b, H, *]
     per bucket.  A zero row (q = k = v = g = beta = 0, dO = 0) neither decays,
@@ -267,11 +267,11 @@ def _packed_backward(lib, offsets, inputs, grads, s0, ds_t, ds0, heads, key_dim,
     # the workspace a call per document needs anyway (sized for the longest),
     # or 1 GiB, bounds each bucket's, within WORKSPACE_LIMIT (past it a
     # bucket's heads go in groups)
-    budget = min(max(lib.kda_chunk_bwd_workspace_bytes(1, longest, heads, key_dim, value_dim), 1 << 30),
+    budget = min(max(lib.kda_chunk_bwd_workspace_bytes(1, longest, heads, key_dim, value_dim, code), 1 << 30),
                  WORKSPACE_LIMIT)
 
     def fits(n, n_tok):
-        return lib.kda_chunk_bwd_workspace_bytes(n, n_tok, heads, key_dim, value_dim) <= budget
+        return lib.kda_chunk_bwd_workspace_bytes(n, n_tok, heads, key_dim, value_dim, code) <= budget
 
     buckets = _document_buckets(lengths, fits)
     for bk in buckets:
@@ -445,13 +445,13 @@ def _chunk_gradients(q, k, v, g, beta, initial_state, d_hidden, d_final, work_dt
 
         def run(tensors, grads_out, s_init, ds_fin, ds_init, n_b, n_tok):
             _by_head_groups(lib, lambda *a: call(*a, vdim), tensors, grads_out, s_init, ds_fin, ds_init, n_b,
-                            n_tok, heads, key_dim, vdim, workspace)
+                            n_tok, heads, key_dim, vdim, workspace, code)
 
         if offsets is None:
             run((qc, kc, vc, gc, bc, d_out), grads, s0, ds_t, ds0, batch, tokens)
         else:
             _packed_backward(lib, offsets, (qc, kc, vc, gc, bc, d_out), grads, s0, ds_t, ds0, heads,
-                             key_dim, vdim, device, run)
+                             key_dim, vdim, device, run, code)
 
     if value_dim <= 128:
         backward_of(vc, d_out, s0, ds_t, (dq, dk, dv, dg, dbeta), ds0)

@@ -178,10 +178,41 @@ def test_backward_entry_point_rejects_bad_arguments():
     assert call(K=256) == _lib.KDA_ERR_UNSUPPORTED
     assert call(dq=None) == _lib.KDA_ERR_INVALID_ARGUMENT
     assert call() == _lib.KDA_ERR_WORKSPACE  # no workspace
-    need = lib.kda_chunk_bwd_workspace_bytes(1, 64, 1, 128, 128)
+    need = lib.kda_chunk_bwd_workspace_bytes(1, 64, 1, 128, 128, bf16)
     assert need > 0 and call(ws=a, ws_bytes=need - 1) == _lib.KDA_ERR_WORKSPACE
     assert call(ws=a + 4, ws_bytes=need) == _lib.KDA_ERR_INVALID_ARGUMENT  # misaligned workspace
-    assert lib.kda_chunk_bwd_workspace_bytes(0, 64, 1, 128, 128) == 0
+    assert lib.kda_chunk_bwd_workspace_bytes(0, 64, 1, 128, 128, bf16) == 0
+    assert lib.kda_chunk_bwd_workspace_bytes(1, 64, 1, 128, 128, 7) == 0  # unknown dtype
+
+
+@pytest.mark.parametrize("B,T,H,K,V", [(1, 8192, 16, 128, 128), (2, 1000, 3, 64, 48), (4, 130, 2, 100, 5)])
+def test_backward_workspace_per_dtype(B, T, H, K, V):
+    # one record per (sequence, head, chunk) plus the segment records of both
+    # scans; f32 inputs keep split-bf16 operand records (hi and lo planes) and
+    # f32 states, bf16/f16 inputs single-operand records and bf16 S, dS, Vt
+    import torch
+
+    lib = _lib.load()
+    kp, vp = (64 if K <= 64 else 128), (V + 31) // 32 * 32
+    nc = (T + 63) // 64
+    cc, ck, cv, kv = 64 * 64, 64 * kp, 64 * vp, kp * vp
+
+    def record(split):
+        s = 1 if split else 2
+        rec = 2 * cc + cc // s + 5 * ck // s + ck + cv + kp + 2 * (kv // s) + cv // s + cv + 3 * ck + 2 * cc + kp
+        return (rec + 63) // 64 * 64
+
+    want_segs = min(max(-(-256 // (2 * B * H)), 1), nc)
+    seg_len = -(-nc // want_segs)
+    segs = -(-nc // seg_len)
+    seg = 2 * B * H * segs * (kp * kp + 2 * kp * vp)
+    for dtype, split in ((torch.float32, True), (torch.bfloat16, False), (torch.float16, False)):
+        got = lib.kda_chunk_bwd_workspace_bytes(B, T, H, K, V, _lib.dtype_code(dtype))
+        assert got == 4 * (B * H * nc * record(split) + seg), dtype
+    f64 = lib.kda_chunk_bwd_workspace_bytes(B, T, H, K, V, _lib.dtype_code(torch.float64))
+    assert f64 > 0
+    if (B, T, H, K, V) == (1, 8192, 16, 128, 128):
+        assert record(True) == 151808 and record(False) == 108800  # 593 and 425 KiB
 
 
 def test_recurrent_backward_entry_point_rejects_bad_arguments():
@@ -228,6 +259,6 @@ def test_split_path_forward_workspace_is_its_own_records(B, T, H, K, V):
     expect = 4 * (B * H * nc * record + B * H * segs * (kp * kp + 2 * kp * vp))
     got = lib.kda_chunk_fwd_workspace_bytes(B, B * T, 0, H, K, V, _lib.dtype_code(torch.float32))
     assert got == expect
-    assert got < lib.kda_chunk_bwd_workspace_bytes(B, T, H, K, V)
+    assert got < lib.kda_chunk_bwd_workspace_bytes(B, T, H, K, V, _lib.dtype_code(torch.float32))
     if (B, T, H, K, V) == (1, 8192, 16, 128, 128):
         assert record == 61568 and got == 554696704

@@ -372,10 +372,11 @@ def test_backward_in_head_groups_matches_one_call(monkeypatch, dtype):
         inputs, d_final = tuple(t.double() for t in inputs), d_final.double()
     whole = _gpu_grads(inputs, d_out, d_final)
     lib = _lib.load()
-    limit = lib.kda_chunk_bwd_workspace_bytes(B, T, 2, K, V)
-    assert lib.kda_chunk_bwd_workspace_bytes(B, T, 3, K, V) > limit
+    code = _lib.dtype_code(dtype)
+    limit = lib.kda_chunk_bwd_workspace_bytes(B, T, 2, K, V, code)
+    assert lib.kda_chunk_bwd_workspace_bytes(B, T, 3, K, V, code) > limit
     monkeypatch.setattr(chunkwise, "WORKSPACE_LIMIT", limit)
-    assert chunkwise._head_group(lambda n: lib.kda_chunk_bwd_workspace_bytes(B, T, n, K, V), H) == 2
+    assert chunkwise._head_group(lambda n: lib.kda_chunk_bwd_workspace_bytes(B, T, n, K, V, code), H) == 2
     grouped = _gpu_grads(inputs, d_out, d_final)
     ref = _oracle_grads(inputs, d_out, d_final)
     same = 1e-12 if dtype == torch.float64 else 1e-5
@@ -398,7 +399,8 @@ def test_packed_backward_in_head_groups(monkeypatch):
     d_out = torch.randn(1, cu[-1], H, V, generator=gen).bfloat16()
     d_final = torch.randn(len(lens), H, K, V, generator=gen)
     lib = _lib.load()
-    monkeypatch.setattr(chunkwise, "WORKSPACE_LIMIT", lib.kda_chunk_bwd_workspace_bytes(1, 150, 1, K, V))
+    monkeypatch.setattr(chunkwise, "WORKSPACE_LIMIT",
+                        lib.kda_chunk_bwd_workspace_bytes(1, 150, 1, K, V, _lib.dtype_code(torch.bfloat16)))
     leaves = [t.to(DEV).requires_grad_() for t in (q, k, v, g, beta, s0)]
     res = kda.chunkwise_kda(*leaves, True, cu_seqlens=cu)
     ((res.hidden_states.float() * d_out.to(DEV).float()).sum()
