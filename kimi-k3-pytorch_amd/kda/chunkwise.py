@@ -82,7 +82,8 @@ def chunkwise_kda(
 
 # Most bytes one kernel call may take as workspace before its heads run in
 # groups: the chunk backward's (and the split-bf16 prefill's) is linear in
-# the heads, about 160 KB per token and head at K=V=128.
+# the heads, about 115 KB per token and head at K=V=128 for bf16/f16 inputs
+# and 160 KB for f32 inputs.
 WORKSPACE_LIMIT = 4 << 30
 
 
