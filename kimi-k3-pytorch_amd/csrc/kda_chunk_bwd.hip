@@ -1250,16 +1250,25 @@ __global__ __launch_bounds__(kSC) void seg_kernel(const Args<IT> a) {
 // X_0 = the initial value (forward S0, backward dS_T; zero when absent), then
 // X_{g+1} = P_g X_g + Q_g for each segment in scan order, one block per
 // (direction, sequence x head, 16 value columns), f32 MFMA; the next
-// segment's P and Q are loaded while the current one multiplies.
+// segment's P and Q are loaded while the current one multiplies.  Every
+// column block reads the whole P_g, so the blocks of one (sequence, head)
+// take block indices equal mod 8: they run on one XCD, whose L2 serves P_g to
+// all but the first (blocks go to the XCDs round-robin by index; the grid is
+// padded to whole groups of 8 sequence x heads).
 constexpr int kCT = 256;
+template <class IT>
+__host__ __device__ inline int64_t combine_blocks(const Args<IT>& a) {
+  return (a.B * a.H + 7) / 8 * 8 * (a.L.Vp / 16);
+}
 template <class IT, int KP, int DIR>
 __device__ __forceinline__ void combine_body(const Args<IT>& a, int64_t id, float* Ps, float* Xs) {
   constexpr int PS = KP + 4, XS = 20, NP = KP * KP / 4 / kCT;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, g4 = lane >> 4;
   const int Vp = a.L.Vp, nv = Vp / 16;
   const int64_t bhn = a.B * a.H;
-  const int64_t bh = id / nv, b = bh / a.H, h = bh % a.H;
-  const int col0 = 16 * static_cast<int>(id % nv);
+  const int64_t bh = (id / 8 / nv) * 8 + id % 8, b = bh / a.H, h = bh % a.H;
+  if (bh >= bhn) return;  // padding of the last group
+  const int col0 = 16 * static_cast<int>(id / 8 % nv);
   const int64_t segf = static_cast<int64_t>(KP) * KP + 2 * static_cast<int64_t>(KP) * Vp;
   float* base = a.seg + (static_cast<int64_t>(DIR) * bhn + bh) * a.nseg * segf;
   const float* init = DIR == 1 ? a.dsT : a.s0;
@@ -1332,7 +1341,7 @@ template <class IT, int KP>
 __global__ __launch_bounds__(kCT) void seg_combine_kernel(const Args<IT> a) {
   __shared__ __attribute__((aligned(16))) float Ps[KP * (KP + 4)];
   __shared__ __attribute__((aligned(16))) float Xs[KP * 20];
-  const int64_t n = a.B * a.H * (a.L.Vp / 16);
+  const int64_t n = combine_blocks(a);
   const int64_t id = blockIdx.x;
   if (a.dir0 == 0 && id < n)
     combine_body<IT, KP, 0>(a, id, Ps, Xs);
@@ -2215,7 +2224,7 @@ static void launch_scans(const bwd::Args<IT>& a, hipStream_t s) {
                        dim3(static_cast<unsigned>(a.B * a.H * bwd::seg_blocks(a, bwd::kSumT))), dim3(bwd::kSC), 0, s,
                        a);
   }
-  hipLaunchKernelGGL((bwd::seg_combine_kernel<IT, KP>), dim3(static_cast<unsigned>(bh * (a.L.Vp / 16))),
+  hipLaunchKernelGGL((bwd::seg_combine_kernel<IT, KP>), dim3(static_cast<unsigned>(a.ndir * bwd::combine_blocks(a))),
                      dim3(bwd::kCT), 0, s, a);
   hipLaunchKernelGGL((bwd::seg_kernel<IT, KP, bwd::kRun>), dim3(static_cast<unsigned>(bh * a.nseg)), dim3(bwd::kSC),
                      0, s, a);
@@ -2244,7 +2253,7 @@ static int run_split(const IT* q, const IT* k, const IT* v, const IT* g, const I
   a.valid = valid, a.sT = sT, a.out = out;
   set_segments(a, 1);
   const int64_t chunks = B * H * a.NC;
-  if (chunks > 0x7fffffffLL || B * H * a.nseg > 0x7fffffffLL || B * H * (a.L.Vp / 16) > 0x7fffffffLL) {
+  if (chunks > 0x7fffffffLL || B * H * a.nseg > 0x7fffffffLL || bwd::combine_blocks(a) > 0x7fffffffLL) {
     set_detail("chunk_fwd: grid too large");
     return KDA_ERR_UNSUPPORTED;
   }
@@ -2299,7 +2308,7 @@ template <class IT>
 static int run_bwd(bwd::Args<IT> a, hipStream_t s) {
   set_segments(a, 2);
   const int64_t chunks = a.B * a.H * a.NC;
-  if (chunks > 0x7fffffffLL || 2 * a.B * a.H * a.nseg > 0x7fffffffLL || 2 * a.B * a.H * (a.L.Vp / 16) > 0x7fffffffLL) {
+  if (chunks > 0x7fffffffLL || 2 * a.B * a.H * a.nseg > 0x7fffffffLL || 2 * bwd::combine_blocks(a) > 0x7fffffffLL) {
     set_detail("chunk backward: grid too large");
     return KDA_ERR_UNSUPPORTED;
   }
