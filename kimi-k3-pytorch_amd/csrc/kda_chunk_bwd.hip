@@ -1393,15 +1393,39 @@ __global__ __launch_bounds__(kOT) void out_kernel(const Args<IT> a) {
   WsTile<kC, 32, kOT> tv;
   ts.fetch(ws + a.L.S, a.L.Vp, 0, tid);
   tv.fetch(ws + a.L.Vt, a.L.Vp, 0, tid);
-  {  // the split records back to f32: Qgt[col * 64 + r] = Qg[r][col], Aqkt[j * 64 + i] = Aqk[i][j]
+  {  // the split records back to f32, eight elements at a time: Qgt[col * 64 + r] = Qg[r][col],
+     // Aqkt[j * 64 + i] = Aqk[i][j]
     const __bf16* qg = reinterpret_cast<const __bf16*>(ws + a.L.Qgt);
     const __bf16* aq = reinterpret_cast<const __bf16*>(ws + a.L.Aqkt);
-    for (int idx = tid; idx < kC * KP; idx += kOT)
-      QgT[(idx >> 6) * kRC + (idx & 63)] =
-          static_cast<float>(qg[idx]) + (kSplitOps<IT> ? static_cast<float>(qg[kC * KP + idx]) : 0.f);
-    for (int idx = tid; idx < kC * kC; idx += kOT)
-      AqT[(idx >> 6) * kRC + (idx & 63)] =
-          static_cast<float>(aq[idx]) + (kSplitOps<IT> ? static_cast<float>(aq[kC * kC + idx]) : 0.f);
+    auto unsplit = [&](const __bf16* rec, int n, float* dst) {
+      constexpr int PER = kC * KP / 8 / kOT;  // the larger record (Qg); Aqk takes the first n / 8 items
+      bf16x8 h[PER], l[PER];
+#pragma unroll
+      for (int it = 0; it < PER; ++it) {
+        const int idx = 8 * (tid + kOT * it);
+        if (idx < n) {
+          h[it] = *reinterpret_cast<const bf16x8*>(rec + idx);
+          if constexpr (kSplitOps<IT>) l[it] = *reinterpret_cast<const bf16x8*>(rec + n + idx);
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < PER; ++it) {
+        const int idx = 8 * (tid + kOT * it);
+        if (idx < n) {
+          f32x4 x0, x1;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            x0[e] = static_cast<float>(h[it][e]) + (kSplitOps<IT> ? static_cast<float>(l[it][e]) : 0.f);
+            x1[e] = static_cast<float>(h[it][4 + e]) + (kSplitOps<IT> ? static_cast<float>(l[it][4 + e]) : 0.f);
+          }
+          float* d = dst + (idx >> 6) * kRC + (idx & 63);
+          *reinterpret_cast<f32x4*>(d) = x0;
+          *reinterpret_cast<f32x4*>(d + 4) = x1;
+        }
+      }
+    };
+    unsplit(qg, kC * KP, QgT);
+    unsplit(aq, kC * kC, AqT);
   }
   const int rt = w & 3, ct = w >> 2;
   for (int s0 = 0; s0 < a.L.Vp; s0 += 32) {
