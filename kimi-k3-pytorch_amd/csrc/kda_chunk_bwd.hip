@@ -1640,12 +1640,27 @@ __device__ __forceinline__ void grad_body(const Args<IT>& a, float* sm, float* b
   const int Vp = a.L.Vp;
   float* ws = a.ws + ch * a.L.per;
   float* MS = sm + kOffM;
+  // V a multiple of the slab width: each slab's loads are issued one slab
+  // ahead, into registers; otherwise slab by slab with the edge checks.  The
+  // first slab's loads go out with beta's and N's, in one round trip.
+  const bool ahead = rows_fast(a.V, 0, Vp);
+  GradSlab<IT, KP, NT> gs;
+  if (ahead) gs.fetch(a, ws, b, t0, h, 0, tid);
+  constexpr int PN = kC * kC / 4 / NT;
+  f32x4 nv[PN];
+#pragma unroll
+  for (int it = 0; it < PN; ++it) nv[it] = *reinterpret_cast<const f32x4*>(ws + a.L.N + 4 * (tid + NT * it));
   if (tid < kC) {
     const int64_t t = t0 + tid;
     bS[tid] = t < a.T ? to_float(a.beta[tok(b, t, a.T, a.H, h)]) : 0.f;
   }
   __syncthreads();
-  for (int idx = tid; idx < kC * kC; idx += NT) MS[(idx >> 6) * kRC + (idx & 63)] = ws[a.L.N + idx] * bS[idx & 63];
+#pragma unroll
+  for (int it = 0; it < PN; ++it) {  // M = N diag(b)
+    const int idx = 4 * (tid + NT * it);
+    *reinterpret_cast<f32x4*>(&MS[(idx >> 6) * kRC + (idx & 63)]) =
+        nv[it] * *reinterpret_cast<const f32x4*>(&bS[idx & 63]);
+  }
 
   f32x4 aQ[CH], aT[CH], aW[CH], aA[2], aM[2];
 #pragma unroll
@@ -1659,12 +1674,7 @@ __device__ __forceinline__ void grad_body(const Args<IT>& a, float* sm, float* b
   float* dVf = sm + kOffdVf;
   const SMat mS{Ss, KP * kSR, kSR}, mdS{dSn, KP * kSR, kSR}, mdO{dOs, kC * kSR, kSR}, mVt{Vts, kC * kSR, kSR},
       mdVt{dVts, kC * kSR, kSR}, mv{vs, kC * kSR, kSR};
-  // V a multiple of the slab width: each slab's loads are issued one slab
-  // ahead, into registers; otherwise slab by slab with the edge checks
-  const bool ahead = rows_fast(a.V, 0, Vp);
-  GradSlab<IT, KP, NT> gs;
   WsTile<kC, KP, NT> kg;
-  if (ahead) gs.fetch(a, ws, b, t0, h, 0, tid);
   for (int s0 = 0; s0 < Vp; s0 += kSW) {  // Vp is a multiple of the slab width
     if (ahead) {
       gs.store(Ss, dSn, Vts, dVts, dVf, dOs, vs, t0, a.T, tid);
