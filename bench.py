@@ -322,32 +322,37 @@ def bench_decay_fusion(reps=20):
     return res
 
 
-def bench_backward(reps=10):
-    """The chunkwise backward (kda_chunk_bwd) on the prefill workload: all
-    input gradients and dS0 from upstream gradients of the output and the
-    final state.  `reps` back-to-back calls through the C ABI into
-    preallocated outputs, HIP events on the launch stream."""
+def bench_backward(reps=10, shape=None, dtype_name="bf16"):
+    """The chunkwise backward (kda_chunk_bwd) on the prefill workload (or
+    `shape` = (B, T, H, K, V), inputs of `dtype_name`): all input gradients
+    and dS0 from upstream gradients of the output and the final state.
+    `reps` back-to-back calls through the C ABI into preallocated outputs,
+    HIP events on the launch stream."""
     import torch
 
     from kda import _lib, _prep
 
     lib = _lib.load()
     device = torch.device("cuda", 0)
-    q, k, v, g, beta, s0 = _inputs(P_B, P_T, P_H, P_K, P_V, 0.02, 0, device)
+    headline = shape is None and dtype_name == "bf16"
+    B, T, H, K, V = (P_B, P_T, P_H, P_K, P_V) if shape is None else shape
+    dt = {"bf16": torch.bfloat16, "f32": torch.float32}[dtype_name]
+    q, k, v, g, beta, s0 = _inputs(B, T, H, K, V, 0.02, 0, device)  # bf16 values, f32 state
+    q, k, v, g, beta = (t.to(dt) for t in (q, k, v, g, beta))
     gen = torch.Generator(device=device).manual_seed(9)
-    d_out = torch.randn(P_B, P_T, P_H, P_V, generator=gen, device=device).to(torch.bfloat16)
-    d_final = torch.randn(P_B, P_H, P_K, P_V, generator=gen, device=device)
+    d_out = torch.randn(B, T, H, V, generator=gen, device=device).to(dt)
+    d_final = torch.randn(B, H, K, V, generator=gen, device=device)
     grads = [torch.empty_like(t) for t in (q, k, v, g, beta)]
     ds0 = torch.empty_like(s0)
-    code = _lib.dtype_code(torch.bfloat16)
-    nbytes = lib.kda_chunk_bwd_workspace_bytes(P_B, P_T, P_H, P_K, P_V, code)
+    code = _lib.dtype_code(dt)
+    nbytes = lib.kda_chunk_bwd_workspace_bytes(B, T, H, K, V, code)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=device)
     stream = _prep.stream(device)
 
     def call():
         _lib.check(lib.kda_chunk_bwd(q.data_ptr(), k.data_ptr(), v.data_ptr(), g.data_ptr(), beta.data_ptr(),
                                      d_out.data_ptr(), code, s0.data_ptr(), d_final.data_ptr(),
-                                     *[t.data_ptr() for t in grads], ds0.data_ptr(), P_B, P_T, P_H, P_K, P_V,
+                                     *[t.data_ptr() for t in grads], ds0.data_ptr(), B, T, H, K, V,
                                      ws.data_ptr(), nbytes, stream))
 
     _settle(call)
@@ -362,17 +367,19 @@ def bench_backward(reps=10):
     e1.record()
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / reps
-    per_kernel = [measured_traffic(k) for k in BWD_KERNELS]
-    traffic = None if None in per_kernel else sum(per_kernel)
-    return {
-        "workload": f"chunkwise backward B={P_B} T={P_T} H={P_H} K=V={P_K}, bf16 inputs, f32 arithmetic "
+    out = {
+        "workload": f"chunkwise backward B={B} T={T} H={H} K={K} V={V}, {dtype_name} inputs, f32 accumulation "
                     "(dq, dk, dv, dg, dbeta, dS0)",
         "ms": round(ms, 4),
-        "tokens_per_s": round(P_B * P_T / (ms * 1e-3), 1),
+        "tokens_per_s": round(B * T / (ms * 1e-3), 1),
         "workspace_bytes": nbytes,
-        "traffic": traffic,
-        "traffic_gbs": None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1),
     }
+    if headline:  # the counter record is of this shape
+        per_kernel = [measured_traffic(k) for k in BWD_KERNELS]
+        traffic = None if None in per_kernel else sum(per_kernel)
+        out["traffic"] = traffic
+        out["traffic_gbs"] = None if traffic is None else round(traffic / (ms * 1e-3) / 1e9, 1)
+    return out
 
 
 def bench_cache(layers=8, reps=10):
@@ -1116,6 +1123,9 @@ def main() -> int:
     result["prefill_configs"] = bench_configs(args.steps, args.warmup, counters)
     result["decay_fusion"] = bench_decay_fusion()
     result["backward"] = bench_backward()
+    # the reference's shipped head shape, and f32 inputs (split-bf16 operands)
+    result["backward"]["k64_t8192_h16"] = bench_backward(shape=(P_B, P_T, P_H, 64, 64))
+    result["backward"]["f32_inputs"] = bench_backward(dtype_name="f32")
     result["cache_reorder"] = bench_cache()
     if not args.no_cpu_baseline:
         cpu = cpu_baseline()

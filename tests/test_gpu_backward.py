@@ -107,6 +107,26 @@ def test_backward_long_context_heads_subset():
             assert e < TOL[torch.bfloat16], (name, h, e)
 
 
+def test_backward_gpu_48gb_shape_full_length():
+    # B=1 T=8192 H=16 K=V=64 bf16, the head shape of the reference's shipped
+    # GPU profiles (config/kimi_full_pipeline/gpu_48gb/model.yaml:19); two heads
+    # against the oracle at full length
+    B, T, H, K, V = 1, 8192, 16, 64, 64
+    inputs, d_out, d_final = _case(B, T, H, K, V, torch.bfloat16, seed=55)
+    got = _gpu_grads(inputs, d_out, d_final)
+    for h in (2, 13):
+        sub = [t[:, :, h:h + 1] for t in inputs[:5]] + [inputs[5][:, h:h + 1]]
+        ref = _oracle_grads(sub, d_out[:, :, h:h + 1], d_final[:, h:h + 1])
+        errs = {}
+        for name, a, b in zip(NAMES, got, ref):
+            a_h = a[:, h:h + 1] if name == "ds0" else a[:, :, h:h + 1]
+            errs[name] = rel_err(a_h, b)
+        print(f"backward K=V=64 T=8192 head {h}: " + " ".join(f"{n} {e:.2e}" for n, e in errs.items()))
+        record_margin(f"backward B=1 T=8192 H=16 K=V=64 bf16, head {h}", TOL[torch.bfloat16], **errs)
+        for name, e in errs.items():
+            assert e < TOL[torch.bfloat16], (name, h, e)
+
+
 @pytest.mark.parametrize("B,T,H,K,V", [(1, 5, 2, 2, 3), (2, 130, 2, 128, 128), (1, 70, 1, 100, 40)])
 def test_f64_backward_matches_oracle(B, T, H, K, V):
     # f64 inputs differentiate in f64 arithmetic (kda_chunk_bwd_f64.hip)
