@@ -536,6 +536,7 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
   __shared__ __attribute__((aligned(16))) float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS];
   __shared__ __attribute__((aligned(16))) float AS[kC * kRC], AqkS[kC * kRC], NS[kC * kRC];
   __shared__ __attribute__((aligned(16))) float bS[kC];
+  __shared__ __attribute__((aligned(16))) float lastS[KP];  // lg of the chunk's last row
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
@@ -657,54 +658,64 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     for (int e = 0; e < 8; ++e) x[e] = AqkS[(c0 + e) * kRC + r];
     put_split8<kSplitOps<IT>>(ws + a.L.Aqkt, kC * kC, 8 * i8, x);
   }
-  for (int i4 = tid; bwd_records && i4 < kC * Kp / 4; i4 += kPT) {  // Kg (f32), four at a time
-    const int r = (4 * i4) / Kp, col = (4 * i4) % Kp;
-    const f32x4 lg = *reinterpret_cast<const f32x4*>(&lgS[r * kRS + col]);
-    const f32x4 kk = *reinterpret_cast<const f32x4*>(&kS[r * kRS + col]);
-    f32x4 x;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) x[e] = fast_exp(lg[e]) * kk[e];
-    *reinterpret_cast<f32x4*>(ws + a.L.Kg + 4 * i4) = x;
+  if (tid < Kp) {
+    lastS[tid] = lgS[(kC - 1) * kRS + tid];
+    ws[a.L.D + tid] = fast_exp(lgS[(kC - 1) * kRS + tid]);
   }
-  for (int i8 = tid; bwd_records && i8 < kC * Kp / 8; i8 += kPT) {  // Kt split, row-major
+  __syncthreads();
+  // each element's factors once: k, q, lg become Kg = e^lg k, Kt = e^(lg_last - lg) k
+  // and Qg = e^lg q in place (the B operand of W = M Kg; the transposed records
+  // below read Kt and Qg), with the row-major Kg and Kt records written on the way
+  for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {
     const int r = (8 * i8) / Kp, c0 = (8 * i8) % Kp;
-    float x[8];
+    float* kp = &kS[r * kRS + c0];
+    float* qp = &qS[r * kRS + c0];
+    float* lp = &lgS[r * kRS + c0];
+    float kg[8], kt[8], qg[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const int col = c0 + e;
-      x[e] = fast_exp(lgS[(kC - 1) * kRS + col] - lgS[r * kRS + col]) * kS[r * kRS + col];
+    for (int u = 0; u < 2; ++u) {
+      const f32x4 kk = *reinterpret_cast<const f32x4*>(kp + 4 * u), qq = *reinterpret_cast<const f32x4*>(qp + 4 * u);
+      const f32x4 ll = *reinterpret_cast<const f32x4*>(lp + 4 * u);
+      const f32x4 la = *reinterpret_cast<const f32x4*>(&lastS[c0 + 4 * u]);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float ex = fast_exp(ll[e]);
+        kg[4 * u + e] = ex * kk[e];
+        kt[4 * u + e] = fast_exp(la[e] - ll[e]) * kk[e];
+        qg[4 * u + e] = ex * qq[e];
+      }
     }
-    put_split8<kSplitOps<IT>>(ws + a.L.Ktr, kC * Kp, 8 * i8, x);
+    if (bwd_records) {  // Kg (f32) and Kt split, row-major
+#pragma unroll
+      for (int u = 0; u < 2; ++u)
+        *reinterpret_cast<f32x4*>(ws + a.L.Kg + 8 * i8 + 4 * u) =
+            f32x4{kg[4 * u], kg[4 * u + 1], kg[4 * u + 2], kg[4 * u + 3]};
+      put_split8<kSplitOps<IT>>(ws + a.L.Ktr, kC * Kp, 8 * i8, kt);
+    }
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      *reinterpret_cast<f32x4*>(kp + 4 * u) = f32x4{kg[4 * u], kg[4 * u + 1], kg[4 * u + 2], kg[4 * u + 3]};
+      *reinterpret_cast<f32x4*>(qp + 4 * u) = f32x4{kt[4 * u], kt[4 * u + 1], kt[4 * u + 2], kt[4 * u + 3]};
+      *reinterpret_cast<f32x4*>(lp + 4 * u) = f32x4{qg[4 * u], qg[4 * u + 1], qg[4 * u + 2], qg[4 * u + 3]};
+    }
   }
+  __syncthreads();
   for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {  // Kt^T and Qg^T split, eight positions at a time
     const int col = (8 * i8) / kC, r0 = (8 * i8) % kC;
-    const float last = lgS[(kC - 1) * kRS + col];
     float xk[8], xq[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      const float lg = lgS[(r0 + e) * kRS + col];
-      xk[e] = fast_exp(last - lg) * kS[(r0 + e) * kRS + col];
-      xq[e] = fast_exp(lg) * qS[(r0 + e) * kRS + col];
+      xk[e] = qS[(r0 + e) * kRS + col];
+      xq[e] = lgS[(r0 + e) * kRS + col];
     }
     put_split8<kSplitOps<IT>>(ws + a.L.Ktt, kC * Kp, 8 * i8, xk);
     put_split8<kSplitOps<IT>>(ws + a.L.Qgt, kC * Kp, 8 * i8, xq);
   }
-  if (tid < Kp) ws[a.L.D + tid] = fast_exp(lgS[(kC - 1) * kRS + tid]);
-  __syncthreads();
   for (int i4 = tid; i4 < kC * kC / 4; i4 += kPT) {  // L's strict part b_i A_ij over A; N cleared
     const int r = (4 * i4) >> 6, cc = (4 * i4) & 63;
     f32x4* ap = reinterpret_cast<f32x4*>(&AS[r * kRC + cc]);
     *ap = *ap * bS[r];
     *reinterpret_cast<f32x4*>(&NS[r * kRC + cc]) = zero4();
-  }
-  for (int i4 = tid; i4 < kC * Kp / 4; i4 += kPT) {  // Kg over k: the B operand of W = M Kg
-    const int r = (4 * i4) / Kp, col = (4 * i4) % Kp;
-    f32x4* kp = reinterpret_cast<f32x4*>(&kS[r * kRS + col]);
-    const f32x4 lg = *reinterpret_cast<const f32x4*>(&lgS[r * kRS + col]);
-    f32x4 x = *kp;
-#pragma unroll
-    for (int e = 0; e < 4; ++e) x[e] *= fast_exp(lg[e]);
-    *kp = x;
   }
   __syncthreads();
   // v (into lg's rows once W is formed): its loads go out now and land while
