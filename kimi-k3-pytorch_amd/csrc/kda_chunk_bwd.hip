@@ -270,6 +270,40 @@ __device__ __forceinline__ void put_split8(float* rec, int n, int idx, const flo
   if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(p + n + idx) = lo;
 }
 
+// acc += A[r0:r0+16, 0:kd] B[0:kd, c0:c0+16] for f32 matrices in LDS (see
+// Mat), on split-bf16 operands formed in registers: lane (i, g) takes
+// A[r0+i][k0+8g+e] and B[k0+8g+e][c0+i], e = 0..7, per 32-deep step (three
+// bf16 MFMAs against the eight f32 ones of mma_long; kd a multiple of 32).
+__device__ __forceinline__ f32x4 mma_sb(f32x4 acc, Mat A, int r0, Mat B, int c0, int kd) {
+  const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  const float* a = A.p + (r0 + i) * A.rs + 8 * g * A.cs;
+  const float* b = B.p + 8 * g * B.rs + (c0 + i) * B.cs;
+  f32x4 acc2 = zero4();
+  for (int k0 = 0; k0 < kd; k0 += 32) {
+    float av[8], bv[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      av[e] = a[(k0 + e) * A.cs];
+      bv[e] = b[(k0 + e) * B.rs];
+    }
+    bf16x8 ah, al, bh, bl;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      __bf16 h, l;
+      split_bf16(av[e], h, l);
+      ah[e] = h;
+      al[e] = l;
+      split_bf16(bv[e], h, l);
+      bh[e] = h;
+      bl[e] = l;
+    }
+    acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);
+    acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc2, 0, 0, 0);
+    acc2 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc2, 0, 0, 0);
+  }
+  return acc + acc2;
+}
+
 __device__ __forceinline__ int64_t tok(const int64_t b, const int64_t t, const int64_t T, const int64_t H,
                                        const int64_t h) {
   return (b * T + t) * H + h;
@@ -1768,15 +1802,15 @@ __device__ __forceinline__ void grad_body(const Args<IT>& a, float* sm, float* b
   wn.fetch(ws + a.L.N, kC, 0, tid);
   wa.fetch(ws + a.L.A, kC, 0, tid);
 #pragma unroll
-  for (int j = 0; j < CH; ++j) {  // dKg = M^T dW
+  for (int j = 0; j < CH; ++j) {  // dKg = M^T dW (this stage's products on split-bf16 operands)
     const int ct = hf * CH + j;
-    const f32x4 acc = mma_long(zero4(), Mat{MS, 1, kRC}, 16 * rt, Mat{X, kRS, 1}, 16 * ct, kC);
+    const f32x4 acc = mma_sb(zero4(), Mat{MS, 1, kRC}, 16 * rt, Mat{X, kRS, 1}, 16 * ct, kC);
 #pragma unroll
     for (int r = 0; r < 4; ++r) ws[a.L.dKg + (16 * rt + 4 * lg4 + r) * Kp + 16 * ct + li] = acc[r];
   }
 #pragma unroll
   for (int j = 0; j < 2; ++j)  // dM += dW Kg^T
-    aM[j] = mma_long(aM[j], Mat{X, kRS, 1}, 16 * rt, Mat{Y, 1, kRS}, 16 * (hf * 2 + j), Kp);
+    aM[j] = mma_sb(aM[j], Mat{X, kRS, 1}, 16 * rt, Mat{Y, 1, kRS}, 16 * (hf * 2 + j), Kp);
   __syncthreads();
 
   // dbeta and dA from N: dN = dM diag(b), T1 = N^T dN, dL = -strict(T1 N^T)
