@@ -1672,9 +1672,13 @@ __device__ __forceinline__ void load_rows_split(__bf16* dst, const IT* src, int6
   }
 }
 
-// sm: kGradFloats floats of LDS, bS: kC more
-template <class IT, int KP>
-__device__ __forceinline__ void grad_body(const Args<IT>& a, float* sm, float* bS) {
+// sm: kGradFloats floats of LDS, bS: kC more; `early` runs when the slab
+// products are done (the pair stage's input loads go out there)
+struct NoOp {
+  __device__ void operator()() const {}
+};
+template <class IT, int KP, class F = NoOp>
+__device__ __forceinline__ void grad_body(const Args<IT>& a, float* sm, float* bS, const F& early = F{}) {
   constexpr int NT = 512;
   constexpr int Kp = KP, CH = KP / 32;  // K-wide column tiles per wave
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
@@ -1797,6 +1801,7 @@ __device__ __forceinline__ void grad_body(const Args<IT>& a, float* sm, float* b
   kg.template store<kRS>(Y, tid);
   if (tid < Kp) ws[a.L.dD + tid] = dd;
   __syncthreads();
+  early();
   // N and A for dbeta and dA: loaded while dKg and dM are formed
   WsTile<kC, kC, NT> wn, wa;
   wn.fetch(ws + a.L.N, kC, 0, tid);
@@ -2131,8 +2136,11 @@ __device__ __forceinline__ void pair_mfma(const Args<IT>& a, const float* ws, fl
 // The pair kernel's LDS: k, q and lg tiles [64][kRS], dA and dAqk [64][kRC],
 // and the partial sums `red` [16][128], kPairFloats floats in this order.
 constexpr int kPairFloats = 3 * kC * kRS + 2 * kC * kRC + 16 * 128;
-template <class IT, int KP, int NT>
-__device__ __forceinline__ void pair_body(const Args<IT>& a, float* lds) {
+// PRE: k, q and g of the chunk arrive in rk, rq, rg (fetched during the
+// gradient stage) when their rows take the whole-group path
+template <class IT, int KP, int NT, bool PRE>
+__device__ __forceinline__ void pair_body(const Args<IT>& a, float* lds, const RowTile<IT, KP, NT>& rk,
+                                          const RowTile<IT, KP, NT>& rq, const RowTile<IT, KP, NT>& rg) {
   static_assert(NT == 512, "the MFMA path uses eight waves");
   float *kS = lds, *qS = kS + kC * kRS, *lgS = qS + kC * kRS, *dAS = lgS + kC * kRS, *dQS = dAS + kC * kRC;
   float* red = dQS + kC * kRC;
@@ -2151,7 +2159,13 @@ __device__ __forceinline__ void pair_body(const Args<IT>& a, float* lds) {
       wa[it] = *reinterpret_cast<const f32x4*>(ws + a.L.dA + r * kC + c4);
       wq[it] = *reinterpret_cast<const f32x4*>(ws + a.L.dAqk + r * kC + c4);
     }
-    load_kqg<IT, KP, NT>(kS, qS, lgS, a, b, t0, h, tid, a.T);
+    if (PRE && rows_fast(a.K, 0, KP)) {
+      rk.template store<kRS>(kS, t0, a.T, tid);
+      rq.template store<kRS>(qS, t0, a.T, tid);
+      rg.template store<kRS>(lgS, t0, a.T, tid);
+    } else {
+      load_kqg<IT, KP, NT>(kS, qS, lgS, a, b, t0, h, tid, a.T);
+    }
 #pragma unroll
     for (int it = 0; it < PW; ++it) {
       const int item = tid + NT * it, r = item / (kC / 4), c4 = (item % (kC / 4)) * 4;
@@ -2201,9 +2215,22 @@ constexpr int kGradPairFloats = kGradFloats + kC > kPairFloats ? kGradFloats + k
 template <class IT, int KP>
 __global__ __launch_bounds__(512) void grad_pair_kernel(const Args<IT> a) {
   __shared__ __attribute__((aligned(16))) float lds[kGradPairFloats];
-  grad_body<IT, KP>(a, lds, lds + kGradFloats);
+  // single-operand inputs fetch the pair stage's k, q, g while the gradient
+  // stage forms dKg, dM, dbeta and dA (registers allow it; f32 inputs load
+  // them in the pair stage)
+  constexpr bool kPre = !kSplitOps<IT>;
+  RowTile<IT, KP, 512> rk, rq, rg;
+  const int64_t ch = blockIdx.x, c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
+  auto early = [&] {
+    if (kPre && rows_fast(a.K, 0, KP)) {
+      rk.fetch(a.k, b, c * kC, a.T, a.H, h, a.K, 0, threadIdx.x);
+      rq.fetch(a.q, b, c * kC, a.T, a.H, h, a.K, 0, threadIdx.x);
+      rg.fetch(a.g, b, c * kC, a.T, a.H, h, a.K, 0, threadIdx.x);
+    }
+  };
+  grad_body<IT, KP>(a, lds, lds + kGradFloats, early);
   __syncthreads();  // every record written and every LDS read of grad_body done
-  pair_body<IT, KP, 512>(a, lds);
+  pair_body<IT, KP, 512, kPre>(a, lds, rk, rq, rg);
 }
 
 
