@@ -1292,6 +1292,24 @@ __global__ __launch_bounds__(kSC) void seg_kernel(const Args<IT> a) {
   }
 }
 
+// The maps of both directions in one launch (the backward's scans): blocks
+// [0, n) the backward direction's value maps (the longest: they also carry
+// the dO terms), [n, 2n) the forward direction's, then the transition maps,
+// which start on the CUs that the forward value maps free first (one block
+// per CU; the transition maps alone would fill half the GPU).
+template <class IT, int KP>
+__global__ __launch_bounds__(kSC) void seg_maps_kernel(const Args<IT> a) {
+  __shared__ __attribute__((aligned(16))) unsigned char sm[SegLds<KP>::bytes];
+  const int64_t n = a.B * a.H * seg_blocks(a, kSumV);
+  const int64_t id = blockIdx.x;
+  if (id < n)
+    seg_body<IT, KP, kSumV, 1>(a, id, sm);
+  else if (id < 2 * n)
+    seg_body<IT, KP, kSumV, 0>(a, id - n, sm);
+  else
+    seg_body<IT, KP, kSumT, 0>(a, id - 2 * n, sm);
+}
+
 // X_0 = the initial value (forward S0, backward dS_T; zero when absent), then
 // X_{g+1} = P_g X_g + Q_g for each segment in scan order, one block per
 // (direction, sequence x head, 16 value columns), f32 MFMA; the next
@@ -2322,7 +2340,11 @@ static void set_segments(bwd::Args<IT>& a, int ndir) {
 template <class IT, int KP>
 static void launch_scans(const bwd::Args<IT>& a, hipStream_t s) {
   const int64_t bh = a.B * a.H * a.ndir;
-  if (a.nseg > 1) {
+  if (a.nseg > 1 && a.ndir == 2) {  // value maps of both directions and the transition maps together
+    hipLaunchKernelGGL((bwd::seg_maps_kernel<IT, KP>),
+                       dim3(static_cast<unsigned>(bh * (a.nseg - 1) + a.B * a.H * bwd::seg_blocks(a, bwd::kSumT))),
+                       dim3(bwd::kSC), 0, s, a);
+  } else if (a.nseg > 1) {
     hipLaunchKernelGGL((bwd::seg_kernel<IT, KP, bwd::kSumV>), dim3(static_cast<unsigned>(bh * (a.nseg - 1))),
                        dim3(bwd::kSC), 0, s, a);
     // transition maps: the forward direction's, which the backward reads transposed
