@@ -1318,7 +1318,8 @@ __global__ __launch_bounds__(kSC) void seg_maps_kernel(const Args<IT> a) {
 // take block indices equal mod 8: they run on one XCD, whose L2 serves P_g to
 // all but the first (blocks go to the XCDs round-robin by index; the grid is
 // padded to whole groups of 8 sequence x heads).
-constexpr int kCT = 256;
+constexpr int kCT = 512;
+constexpr int kCW = kCT / 64;  // waves; wave w takes row tiles w, w + kCW, ..
 template <class IT>
 __host__ __device__ inline int64_t combine_blocks(const Args<IT>& a) {
   return (a.B * a.H + 7) / 8 * 8 * (a.L.Vp / 16);
@@ -1343,7 +1344,8 @@ __device__ __forceinline__ void combine_body(const Args<IT>& a, int64_t id, floa
     base[KP * KP + KP * Vp + r * Vp + col0 + cc] = x;
   }
   f32x4 pf[NP];
-  float qf[2][4];
+  constexpr int RT = (KP / 16 + kCW - 1) / kCW;  // row tiles per wave
+  float qf[RT][4];
   // the backward's transition map of its segment g is the transpose of the
   // forward's map of segment nseg - 1 - g (the same chunks): staged as it is
   // and read with the strides swapped
@@ -1354,8 +1356,8 @@ __device__ __forceinline__ void combine_body(const Args<IT>& a, int64_t id, floa
 #pragma unroll
     for (int j = 0; j < NP; ++j) pf[j] = *reinterpret_cast<const f32x4*>(P + 4 * (tid + kCT * j));
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int rt = w + 4 * j;
+    for (int j = 0; j < RT; ++j) {
+      const int rt = w + kCW * j;
       if (rt < KP / 16) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) qf[j][r] = Q[(16 * rt + 4 * g4 + r) * Vp + col0 + li];
@@ -1371,23 +1373,23 @@ __device__ __forceinline__ void combine_body(const Args<IT>& a, int64_t id, floa
       const int e = 4 * (tid + kCT * j);
       *reinterpret_cast<f32x4*>(&Ps[(e / KP) * PS + e % KP]) = pf[j];
     }
-    f32x4 acc[2];
+    f32x4 acc[RT];
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < RT; ++j)
 #pragma unroll
       for (int r = 0; r < 4; ++r) acc[j][r] = qf[j][r];
     __syncthreads();
     if (gs + 2 < a.nseg) fetch(gs + 1);
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int rt = w + 4 * j;
+    for (int j = 0; j < RT; ++j) {
+      const int rt = w + kCW * j;
       if (rt < KP / 16)
         acc[j] = mma_long(acc[j], DIR == 1 ? Mat{Ps, 1, PS} : Mat{Ps, PS, 1}, 16 * rt, Mat{Xs, XS, 1}, 0, KP);
     }
     __syncthreads();  // every read of X_g is done
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int rt = w + 4 * j;
+    for (int j = 0; j < RT; ++j) {
+      const int rt = w + kCW * j;
       if (rt < KP / 16) {
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
