@@ -76,8 +76,8 @@ SETTLE_MS = 50.0
 
 PREFILL_KERNELS = ("chunk_map_kernel", "chunk_segment_kernel<summary>", "segment_combine_kernel",
                    "chunk_segment_kernel<output>")
-BWD_KERNELS = ("bwd::prep_kernel", "bwd::seg_kernel<maps Q>", "bwd::seg_kernel<maps P>", "bwd::seg_combine_kernel",
-               "bwd::seg_kernel<run>", "bwd::grad_pair_kernel")
+BWD_KERNELS = ("bwd::prep_kernel", "bwd::seg_maps_kernel", "bwd::seg_combine_kernel", "bwd::seg_kernel<run>",
+               "bwd::grad_pair_kernel")
 
 
 def prefill_bytes(B, T, H, K, V, n_state_io=2):
