@@ -50,7 +50,8 @@ def _oracle_grads(inputs, d_out, d_final, final=True):
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("B,T,H,K,V", [(2, 150, 2, 128, 128), (1, 64, 1, 64, 32), (2, 37, 3, 16, 48),
-                                       (1, 200, 2, 128, 96), (1, 70, 1, 100, 40), (1, 90, 2, 64, 200)])
+                                       (1, 200, 2, 128, 96), (1, 70, 1, 100, 40), (1, 90, 2, 64, 200),
+                                       (8, 130, 16, 64, 64)])  # B x H = 128: one segment per sequence
 def test_backward_matches_oracle(dtype, B, T, H, K, V):
     inputs, d_out, d_final = _case(B, T, H, K, V, dtype, seed=T + K)
     got = _gpu_grads(inputs, d_out, d_final)
