@@ -203,8 +203,9 @@ int kda_chunk_fwd_decay(const void* q, const void* k, const void* v, const void*
  * KDA_ERR_WORKSPACE before anything is launched (128 MiB covers one
  * 8192-token bf16 sequence at H=16, which needs 72.5 MB; shapes with
  * batch * heads >= 192 need only the small chunk maps; the split-bf16 path's
- * records, 240.5 KiB per 64 tokens and head at K = V = 128, cover about 390
- * of them).  The call performs
+ * records, 240.5 KiB per 64 tokens and head at K = V = 128 for f32 inputs and
+ * 184.5 KiB for bf16/f16 inputs, cover about 390 and 450 of them with their
+ * segment records).  The call performs
  * no device allocation.  All calls on one GPU share that GPU's array:
  * calls that overlap on one GPU (two streams, two host threads) race.  The
  * stream must belong to the current device.
