@@ -35,6 +35,8 @@ raise instead of dropping gradients.
 
 from __future__ import annotations
 
+import warnings
+
 import numpy as np
 import torch
 
@@ -91,6 +93,11 @@ def _forward(q, k, v, g, beta, initial_state, output_final_state, attention_mask
              batch, tokens, heads, key_dim, value_dim) -> KDAOperatorOutput:
     lib = _lib.load()
     (qc, kc, vc, gc, bc), kernel_dtype, arith = _prep.kernel_inputs(q, k, v, g, beta, work_dtype)
+    if key_dim > 128 and kernel_dtype != torch.float64:
+        # the chunk kernels hold at most 128 key channels per state: the exact
+        # token recurrence runs instead (f64 inputs take it by design)
+        warnings.warn(f"chunkwise_kda: key_dim {key_dim} > 128 runs the token-by-token recurrence kernel, "
+                      "not the chunk-parallel path (much slower on long sequences)", RuntimeWarning, stacklevel=3)
     device = q.device
     n_seq = batch if offsets is None else len(offsets) - 1
     total = batch * tokens

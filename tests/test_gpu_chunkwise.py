@@ -219,6 +219,18 @@ def test_chunkwise_f64_equals_oracle_recurrent(shape):
     assert rel_err(got.hidden_states, ro) < 1e-10 and rel_err(got.final_state, rs) < 1e-10
 
 
+@pytest.mark.parametrize("dtype,tol", [(torch.bfloat16, TOL16), (torch.float32, 1e-4)])
+def test_chunkwise_key_dim_past_128_runs_the_recurrence_with_a_warning(dtype, tol):
+    # K > 128: the chunk kernels hold at most 128 key channels, so the exact
+    # token recurrence runs (kda_chunk_fwd_plan -1), with a RuntimeWarning
+    assert _plan(1, 100, 2, 160, 32, dtype=dtype) == -1
+    q, k, v, g, beta, state = workload(1, 100, 2, 160, 32, state_std=0.02, seed=29, dtype=dtype)
+    ro, rs = _oracle_f32(q, k, v, g, beta, state)
+    with pytest.warns(RuntimeWarning, match="key_dim 160 > 128"):
+        got = kda.chunkwise_kda(*_dev(q, k, v, g, beta, state), True)
+    assert rel_err(got.hidden_states, ro) < tol and rel_err(got.final_state, rs) < tol
+
+
 def test_chunkwise_f32_cpu_smoke_config_within_1e4():
     # B=2, T=32, H=2, K=V=16, f32, chunk 16, g = -softplus(N(0,1)), zero state
     q, k, v, g, beta, _ = workload(2, 32, 2, 16, 16, g_shift=0.0, seed=0, dtype=torch.float32)
