@@ -27,7 +27,8 @@
 // type, stay within about 5e-3 of the oracle.  Decay products use a 16-row block factorisation on the MFMA, with
 // an exact pairwise-exponent path for chunks whose decays leave its range
 // (any g > 0, or a block decaying past e^-80).
-//   prep_kernel         one block per (sequence, head, chunk): A, Aqk, N by
+//   prep_kernel         one block per (sequence, head, chunk), two per CU
+//                       (the key channels by quarters): A, Aqk, N by
 //                       forward substitution, W, U, Kt, Qg, Kg, D;
 //   seg_kernel,         the forward scan (chunk start states S, pseudo-values
 //   seg_combine_kernel  Vt) and the backward scan (dS', dVt per chunk, dS0),
@@ -463,48 +464,55 @@ __device__ __forceinline__ void load_ws(float* dst, const float* src, int ld, in
 // Other chunks take the exact pairwise path.
 constexpr float kMaxBlockDecay = 80.f;
 
-// True when the chunk needs the exact path; lg in LDS rows of stride kRS,
-// the raw g's sign having been folded into `nonneg` by the caller.
 // lg = cumsum(g) down the chunk's 64 rows for each of the KP channels, in
-// place in lgS (row stride kRS).  Thread (channel tid % KP, quarter tid / KP)
+// place in lgS (row stride RS).  Thread (channel tid % KP, quarter tid / KP)
 // sums its quarter's 16 rows in registers, the quarter totals meet in `tmp`
-// (4 x 128 floats), and each quarter adds the totals above it: a chain of 16
+// (4 x KP floats), and each quarter adds the totals above it: a chain of 16
 // additions instead of 64 dependent LDS round trips.  Returns whether one of
 // the thread's own g values is positive; ends with the block synchronised.
-template <int KP>
+template <int KP, int RS = kRS>
 __device__ __forceinline__ bool chunk_cumsum(float* lgS, float* tmp, int tid) {
   bool rising = false;
   float v[16];
   const int c = tid % KP, p = tid / KP;
   if (p < 4) {
 #pragma unroll
-    for (int r = 0; r < 16; ++r) v[r] = lgS[(16 * p + r) * kRS + c];
+    for (int r = 0; r < 16; ++r) v[r] = lgS[(16 * p + r) * RS + c];
 #pragma unroll
     for (int r = 0; r < 16; ++r) {
       rising |= v[r] > 0.f;
       if (r > 0) v[r] += v[r - 1];
     }
-    tmp[p * 128 + c] = v[15];
+    tmp[p * KP + c] = v[15];
   }
   __syncthreads();
   if (p < 4) {
     float off = 0.f;
-    for (int q = 0; q < p; ++q) off += tmp[q * 128 + c];
+    for (int q = 0; q < p; ++q) off += tmp[q * KP + c];
 #pragma unroll
-    for (int r = 0; r < 16; ++r) lgS[(16 * p + r) * kRS + c] = v[r] + off;
+    for (int r = 0; r < 16; ++r) lgS[(16 * p + r) * RS + c] = v[r] + off;
   }
   __syncthreads();
   return rising;
 }
 
-template <int KP, int NT>
-__device__ __forceinline__ bool needs_exact(const float* lgS, bool nonneg, int tid) {
-  bool risky = nonneg;
+// Whether one of the thread's (16-row block, channel) pairs of lg (KP
+// channels, row stride RS) decays by more than kMaxBlockDecay; no barrier.
+template <int KP, int NT, int RS = kRS>
+__device__ __forceinline__ bool decay_risk(const float* lgS, int tid) {
+  bool risky = false;
   for (int idx = tid; idx < 4 * KP; idx += NT) {
     const int I = idx / KP, c = idx % KP;
-    risky |= lgS[16 * I * kRS + c] - lgS[(16 * I + 15) * kRS + c] > kMaxBlockDecay;
+    risky |= lgS[16 * I * RS + c] - lgS[(16 * I + 15) * RS + c] > kMaxBlockDecay;
   }
-  return __syncthreads_or(risky);
+  return risky;
+}
+
+// True when the chunk needs the exact path; lg in LDS rows of stride kRS,
+// the raw g's sign having been folded into `nonneg` by the caller.
+template <int KP, int NT>
+__device__ __forceinline__ bool needs_exact(const float* lgS, bool nonneg, int tid) {
+  return __syncthreads_or(nonneg || decay_risk<KP, NT>(lgS, tid));
 }
 
 // accK += sum_c (k_i e^(lg_i - r)) (k_j e^(r - lg_j)) and accQ the same with
@@ -514,7 +522,9 @@ __device__ __forceinline__ bool needs_exact(const float* lgS, bool nonneg, int t
 // v_mfma_f32_16x16x32_bf16 (hi*hi + hi*lo + lo*hi, three products per 32
 // channels against eight f32 MFMAs per 16); lane (i, g) carries channels
 // k0 + 8g .. k0 + 8g + 7 of row r0 + i and of column c0 + i, and with 16
-// channels left the lane groups g >= 2 carry zeros.
+// channels left the lane groups g >= 2 carry zeros.  Channel matrices in LDS
+// rows of stride RS.
+template <int RS = kRS>
 __device__ __forceinline__ void decay_product(f32x4& accK, f32x4& accQ, const float* kS, const float* qS,
                                               const float* lgS, int r0, int c0, int rr, int kd, int kb = 0) {
   const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
@@ -526,12 +536,12 @@ __device__ __forceinline__ void decay_product(f32x4& accK, f32x4& accQ, const fl
       const int ch = k0 + 8 * g + e;
       f32x4 r4 = zero4(), la = zero4(), lb = zero4(), ka = zero4(), qa = zero4(), kv = zero4();
       if (live) {
-        r4 = *reinterpret_cast<const f32x4*>(&lgS[rr * kRS + ch]);
-        la = *reinterpret_cast<const f32x4*>(&lgS[(r0 + i) * kRS + ch]);
-        lb = *reinterpret_cast<const f32x4*>(&lgS[(c0 + i) * kRS + ch]);
-        ka = *reinterpret_cast<const f32x4*>(&kS[(r0 + i) * kRS + ch]);
-        qa = *reinterpret_cast<const f32x4*>(&qS[(r0 + i) * kRS + ch]);
-        kv = *reinterpret_cast<const f32x4*>(&kS[(c0 + i) * kRS + ch]);
+        r4 = *reinterpret_cast<const f32x4*>(&lgS[rr * RS + ch]);
+        la = *reinterpret_cast<const f32x4*>(&lgS[(r0 + i) * RS + ch]);
+        lb = *reinterpret_cast<const f32x4*>(&lgS[(c0 + i) * RS + ch]);
+        ka = *reinterpret_cast<const f32x4*>(&kS[(r0 + i) * RS + ch]);
+        qa = *reinterpret_cast<const f32x4*>(&qS[(r0 + i) * RS + ch]);
+        kv = *reinterpret_cast<const f32x4*>(&kS[(c0 + i) * RS + ch]);
       }
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
@@ -564,18 +574,73 @@ __device__ __forceinline__ void block_pair(int p, int& I, int& J) {
 }
 
 // ---- prep_kernel: per-chunk intermediates ----------------------------------
+// The chunk's k, q and g pass through LDS kQC key channels (a quarter of 128)
+// at a time, so that the kernel's LDS (79 KB) lets two workgroups share a CU
+// and one block's loads and record stores overlap the other's work.  For each
+// quarter, its loads issued while the previous quarter is worked on:
+//   lg = cumsum(g) over the quarter's channels;
+//   the MFMA decay products of A and Aqk, accumulated in registers (each
+//   block pair's channel sum runs in the same 32-channel steps as it would
+//   over the whole chunk);
+//   Kg = e^lg k, Kt = e^(lg_last - lg) k and Qg = e^lg q in place of k, q
+//   and lg, with their records (D, Kg and Kt row-major, Kt^T, Qg^T), and Kg
+//   copied into a [64][KP] tile that stays for W = M Kg.
+// A chunk whose decays fall outside the factorisation's bounds repeats the
+// quarters for A and Aqk with exact pair exponents.  Then N = L^-1,
+// M = N diag(b), W = M Kg and U = M v.
 constexpr int kPT = 512;  // threads of prep_kernel
+constexpr int kQC = 32;   // key channels per quarter
+constexpr int kQS = 36;   // LDS row stride of the quarter tiles
+
+// k, q and g of kQC key channels from column c0: fetched into registers ahead
+// of use when the rows allow 16-byte loads, read straight into LDS otherwise
+template <class IT>
+struct QuarterTiles {
+  RowTile<IT, kQC, kPT> k, q, g;
+  __device__ __forceinline__ void fetch(const Args<IT>& a, int64_t b, int64_t t0, int64_t h, int c0, int tid) {
+    if (!rows_fast(a.K, c0, kQC)) return;
+    k.fetch(a.k, b, t0, a.T, a.H, h, a.K, c0, tid);
+    q.fetch(a.q, b, t0, a.T, a.H, h, a.K, c0, tid);
+    g.fetch(a.g, b, t0, a.T, a.H, h, a.K, c0, tid);
+  }
+  __device__ __forceinline__ void store(float* kS, float* qS, float* lgS, const Args<IT>& a, int64_t b, int64_t t0,
+                                        int64_t h, int c0, int tid, int64_t Tv) const {
+    if (rows_fast(a.K, c0, kQC)) {
+      k.template store<kQS>(kS, t0, Tv, tid);
+      q.template store<kQS>(qS, t0, Tv, tid);
+      g.template store<kQS>(lgS, t0, Tv, tid);
+    } else {
+      load_rows<IT, kQC, kQS, kPT>(kS, a.k, b, t0, a.T, a.H, h, a.K, c0, tid, Tv);
+      load_rows<IT, kQC, kQS, kPT>(qS, a.q, b, t0, a.T, a.H, h, a.K, c0, tid, Tv);
+      load_rows<IT, kQC, kQS, kPT>(lgS, a.g, b, t0, a.T, a.H, h, a.K, c0, tid, Tv);
+    }
+  }
+};
+
 template <class IT, int KP>
-__global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
-  __shared__ __attribute__((aligned(16))) float kS[kC * kRS], qS[kC * kRS], lgS[kC * kRS];
-  __shared__ __attribute__((aligned(16))) float AS[kC * kRC], AqkS[kC * kRC], NS[kC * kRC];
+__global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
+  constexpr int NQ = KP / kQC;  // quarters
+  constexpr int NW = KP / 32;   // W tiles per wave
+  static_assert(KP % kQC == 0, "whole quarters");
+  // LDS: the quarter tiles k, q, lg [64][kQS], later Aqk, then N and the
+  // inverse's scratch tiles; Kg [64][kRS] (later W, then v); A (later M)
+  constexpr int QREG = 3 * kC * kQS;
+  __shared__ __attribute__((aligned(16))) float pool[QREG + kC * kRS + kC * kRC];
   __shared__ __attribute__((aligned(16))) float bS[kC];
-  __shared__ __attribute__((aligned(16))) float lastS[KP];  // lg of the chunk's last row
+  __shared__ __attribute__((aligned(16))) float lastS[kQC];  // lg of the chunk's last row, quarter's channels
+  __shared__ __attribute__((aligned(16))) float tmpS[4 * kQC];
+  static_assert(kC * kRC + 8 * 16 * kTS <= QREG, "N and the scratch tiles fit over the quarter tiles");
+  float* const kS = pool;
+  float* const qS = pool + kC * kQS;
+  float* const lgS = pool + 2 * kC * kQS;
+  float* const AqkS = pool;          // after the quarters
+  float* const NS = pool;            // after Aqk's record
+  float* const KgS = pool + QREG;    // Kg, then W, then v
+  float* const AS = KgS + kC * kRS;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
   const int64_t t0 = c * kC;
-  constexpr int Kp = KP;
   const int Vp = a.L.Vp;
   float* ws = a.ws + ch * a.L.per;
   // padded tokens (t >= Tv) enter as zero rows: no decay, no write, no output
@@ -584,103 +649,189 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     const int64_t n = a.valid[b];
     Tv = n < 0 ? 0 : (n < a.T ? n : a.T);
   }
+  // the records only the gradient kernels read (A, N, Kg, Kt row-major, W^T)
+  // are skipped when the kernels serve the forward alone (no dO)
+  const bool bwd_records = a.dout != nullptr;
 
-  load_kqg<IT, KP, kPT>(kS, qS, lgS, a, b, t0, h, tid, Tv);
+  QuarterTiles<IT> in;
+  in.fetch(a, b, t0, h, 0, tid);
   if (tid < kC) {
     const int64_t t = t0 + tid;
     bS[tid] = t < Tv ? to_float(a.beta[tok(b, t, a.T, a.H, h)]) : 0.f;
   }
-  for (int idx = tid; idx < kC * kRC; idx += kPT) {
-    AS[idx] = 0.f;
-    AqkS[idx] = 0.f;
-  }
-  __syncthreads();
-  const bool rising = chunk_cumsum<KP>(lgS, NS, tid);  // N is formed later
-  if (!needs_exact<KP, kPT>(lgS, rising, tid)) {
-    static_assert(kPT == 512 && kC * kRC >= 4096, "eight waves; the quarter partials fit in N's tile");
-    // A and Aqk block by block on the MFMA: pair w whole on wave w, and
-    // pairs 8 and 9 in four channel quarters (one per wave), parked over N's
-    // tile and summed in a fixed order after the barrier
-    int I, J;
-    block_pair(w, I, J);
-    f32x4 ak = zero4(), aq = zero4();
-    decay_product(ak, aq, kS, qS, lgS, 16 * I, 16 * J, 16 * I, Kp);
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = 16 * I + 4 * lg4 + r, col = 16 * J + li;
-      if (col < row) AS[row * kRC + col] = ak[r];
-      if (col <= row) AqkS[row * kRC + col] = aq[r];
+  for (int idx = tid; idx < kC * kRC; idx += kPT) AS[idx] = 0.f;
+  // wave w: block pair w, and waves 0 and 1 pairs 8 and 9 as well
+  int I, J, I8, J8;
+  block_pair(w, I, J);
+  block_pair(8 + (w & 1), I8, J8);
+  const bool two = w < 2;
+  f32x4 ak = zero4(), aq = zero4(), ak8 = zero4(), aq8 = zero4();
+  bool risky = false;
+  for (int p = 0; p < NQ; ++p) {
+    const int c0 = p * kQC;
+    in.store(kS, qS, lgS, a, b, t0, h, c0, tid, Tv);
+    __syncthreads();
+    if (p + 1 < NQ) in.fetch(a, b, t0, h, c0 + kQC, tid);
+    risky |= chunk_cumsum<kQC, kQS>(lgS, tmpS, tid);
+    risky |= decay_risk<kQC, kPT, kQS>(lgS, tid);
+    decay_product<kQS>(ak, aq, kS, qS, lgS, 16 * I, 16 * J, 16 * I, kQC);
+    if (two) decay_product<kQS>(ak8, aq8, kS, qS, lgS, 16 * I8, 16 * J8, 16 * I8, kQC);
+    if (tid < kQC) {
+      const float last = lgS[(kC - 1) * kQS + tid];
+      lastS[tid] = last;
+      ws[a.L.D + c0 + tid] = fast_exp(last);
     }
-    {
-      const int pq = w >> 2, qt = w & 3;  // pair 8 + pq, channel quarter qt
-      block_pair(8 + pq, I, J);
-      ak = zero4();
-      aq = zero4();
-      decay_product(ak, aq, kS, qS, lgS, 16 * I, 16 * J, 16 * I, Kp / 4, qt * (Kp / 4));
-      float* part = NS + (pq * 4 + qt) * 512;  // [pair][quarter][A | Aqk][16 x 16]
+    __syncthreads();
+    // each element's factors once: Kg, Kt, Qg in place of k, q, lg, with Kg
+    // into its tile and the row-major Kg and Kt records written on the way
+    for (int i8 = tid; i8 < kC * kQC / 8; i8 += kPT) {
+      const int r = (8 * i8) / kQC, cl = (8 * i8) % kQC;
+      const float* kp = &kS[r * kQS + cl];
+      float* qp = &qS[r * kQS + cl];
+      float* lp = &lgS[r * kQS + cl];
+      float kg[8], kt[8], qg[8];
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        part[(4 * lg4 + r) * 16 + li] = ak[r];
-        part[256 + (4 * lg4 + r) * 16 + li] = aq[r];
+      for (int u = 0; u < 2; ++u) {
+        const f32x4 kk = *reinterpret_cast<const f32x4*>(kp + 4 * u), qq = *reinterpret_cast<const f32x4*>(qp + 4 * u);
+        const f32x4 ll = *reinterpret_cast<const f32x4*>(lp + 4 * u);
+        const f32x4 la = *reinterpret_cast<const f32x4*>(&lastS[cl + 4 * u]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float ex = fast_exp(ll[e]);
+          kg[4 * u + e] = ex * kk[e];
+          kt[4 * u + e] = fast_exp(la[e] - ll[e]) * kk[e];
+          qg[4 * u + e] = ex * qq[e];
+        }
+      }
+      if (bwd_records) {  // Kg (f32) and Kt split, row-major
+        const int idx = r * KP + c0 + cl;
+#pragma unroll
+        for (int u = 0; u < 2; ++u)
+          *reinterpret_cast<f32x4*>(ws + a.L.Kg + idx + 4 * u) =
+              f32x4{kg[4 * u], kg[4 * u + 1], kg[4 * u + 2], kg[4 * u + 3]};
+        put_split8<kSplitOps<IT>>(ws + a.L.Ktr, kC * KP, idx, kt);
+      }
+#pragma unroll
+      for (int u = 0; u < 2; ++u) {
+        *reinterpret_cast<f32x4*>(&KgS[r * kRS + c0 + cl + 4 * u]) =
+            f32x4{kg[4 * u], kg[4 * u + 1], kg[4 * u + 2], kg[4 * u + 3]};
+        *reinterpret_cast<f32x4*>(qp + 4 * u) = f32x4{kt[4 * u], kt[4 * u + 1], kt[4 * u + 2], kt[4 * u + 3]};
+        *reinterpret_cast<f32x4*>(lp + 4 * u) = f32x4{qg[4 * u], qg[4 * u + 1], qg[4 * u + 2], qg[4 * u + 3]};
       }
     }
     __syncthreads();
-    for (int e = tid; e < 1024; e += kPT) {  // [pair][A | Aqk][16 x 16]
-      const int pq = e >> 9, m = (e >> 8) & 1, idx = e & 255;
-      const float* part = NS + pq * 2048 + m * 256 + idx;
-      const float x = ((part[0] + part[512]) + part[1024]) + part[1536];
-      block_pair(8 + pq, I, J);
-      const int row = 16 * I + (idx >> 4), col = 16 * J + (idx & 15);
-      if (m == 0 && col < row) AS[row * kRC + col] = x;
-      if (m == 1 && col <= row) AqkS[row * kRC + col] = x;
-    }
-  } else
-  // A and Aqk with exact pair exponents, 2x2 blocks of (i, j <= i)
-  for (int blk = tid; blk < 528; blk += kPT) {
-    int I2 = static_cast<int>((sqrtf(8.f * blk + 1.f) - 1.f) * 0.5f);
-    while (I2 * (I2 + 1) / 2 > blk) --I2;
-    while ((I2 + 1) * (I2 + 2) / 2 <= blk) ++I2;
-    const int J2 = blk - I2 * (I2 + 1) / 2;
-    const int i0 = 2 * I2, j0 = 2 * J2;
-    const bool off_diag = I2 != J2;  // pair (i0, j0 + 1) lies above the diagonal on the diagonal block
-    float aa[2][2] = {{0.f, 0.f}, {0.f, 0.f}}, aq[2][2] = {{0.f, 0.f}, {0.f, 0.f}};
-#pragma unroll 2
-    for (int kc = 0; kc < Kp; kc += 4) {
-      f32x4 ki[2], qi[2], li[2], kj[2], lj[2];
+    for (int i8 = tid; i8 < kC * kQC / 8; i8 += kPT) {  // Kt^T and Qg^T split, eight positions at a time
+      const int col = (8 * i8) / kC, r0 = (8 * i8) % kC;
+      float xk[8], xq[8];
 #pragma unroll
-      for (int x = 0; x < 2; ++x) {
-        ki[x] = *reinterpret_cast<const f32x4*>(&kS[(i0 + x) * kRS + kc]);
-        qi[x] = *reinterpret_cast<const f32x4*>(&qS[(i0 + x) * kRS + kc]);
-        li[x] = *reinterpret_cast<const f32x4*>(&lgS[(i0 + x) * kRS + kc]);
-        kj[x] = *reinterpret_cast<const f32x4*>(&kS[(j0 + x) * kRS + kc]);
-        lj[x] = *reinterpret_cast<const f32x4*>(&lgS[(j0 + x) * kRS + kc]);
+      for (int e = 0; e < 8; ++e) {
+        xk[e] = qS[(r0 + e) * kQS + col];
+        xq[e] = lgS[(r0 + e) * kQS + col];
       }
+      put_split8<kSplitOps<IT>>(ws + a.L.Ktt, kC * KP, c0 * kC + 8 * i8, xk);
+      put_split8<kSplitOps<IT>>(ws + a.L.Qgt, kC * KP, c0 * kC + 8 * i8, xq);
+    }
+    __syncthreads();
+  }
+  const bool exact = __syncthreads_or(risky);
+  if (exact) {
+    // A and Aqk with exact pair exponents, 2x2 blocks of (i, j <= i): thread
+    // tid takes blocks tid and tid + kPT of the 528, over the quarters again
+    float ea[2][2][2], eq[2][2][2];
+    int bi[2], bj[2];
+    bool off_diag[2], live[2];
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      const int blk = tid + sl * kPT;
+      int I2 = static_cast<int>((sqrtf(8.f * blk + 1.f) - 1.f) * 0.5f);
+      while (I2 * (I2 + 1) / 2 > blk) --I2;
+      while ((I2 + 1) * (I2 + 2) / 2 <= blk) ++I2;
+      const int J2 = blk - I2 * (I2 + 1) / 2;
+      live[sl] = blk < 528;
+      bi[sl] = 2 * I2;
+      bj[sl] = 2 * J2;
+      off_diag[sl] = I2 != J2;  // pair (i0, j0 + 1) lies above the diagonal on the diagonal block
+#pragma unroll
+      for (int x = 0; x < 2; ++x)
+#pragma unroll
+        for (int y = 0; y < 2; ++y) ea[sl][x][y] = eq[sl][x][y] = 0.f;
+    }
+    for (int p = 0; p < NQ; ++p) {
+      const int c0 = p * kQC;
+      in.fetch(a, b, t0, h, c0, tid);
+      in.store(kS, qS, lgS, a, b, t0, h, c0, tid, Tv);
+      __syncthreads();
+      chunk_cumsum<kQC, kQS>(lgS, tmpS, tid);
+#pragma unroll
+      for (int sl = 0; sl < 2; ++sl) {
+        if (!live[sl]) continue;
+        const int i0 = bi[sl], j0 = bj[sl];
+#pragma unroll 2
+        for (int kc = 0; kc < kQC; kc += 4) {
+          f32x4 ki[2], qi[2], lI[2], kj[2], lj[2];
+#pragma unroll
+          for (int x = 0; x < 2; ++x) {
+            ki[x] = *reinterpret_cast<const f32x4*>(&kS[(i0 + x) * kQS + kc]);
+            qi[x] = *reinterpret_cast<const f32x4*>(&qS[(i0 + x) * kQS + kc]);
+            lI[x] = *reinterpret_cast<const f32x4*>(&lgS[(i0 + x) * kQS + kc]);
+            kj[x] = *reinterpret_cast<const f32x4*>(&kS[(j0 + x) * kQS + kc]);
+            lj[x] = *reinterpret_cast<const f32x4*>(&lgS[(j0 + x) * kQS + kc]);
+          }
+#pragma unroll
+          for (int x = 0; x < 2; ++x)
+#pragma unroll
+            for (int y = 0; y < 2; ++y) {
+              const bool ok = !(x == 0 && y == 1) || off_diag[sl];
+              const float e0 = ok ? fast_exp(lI[x].x - lj[y].x) : 0.f;
+              const float e1 = ok ? fast_exp(lI[x].y - lj[y].y) : 0.f;
+              const float e2 = ok ? fast_exp(lI[x].z - lj[y].z) : 0.f;
+              const float e3 = ok ? fast_exp(lI[x].w - lj[y].w) : 0.f;
+              ea[sl][x][y] += ki[x].x * kj[y].x * e0 + ki[x].y * kj[y].y * e1 + ki[x].z * kj[y].z * e2 +
+                              ki[x].w * kj[y].w * e3;
+              eq[sl][x][y] += qi[x].x * kj[y].x * e0 + qi[x].y * kj[y].y * e1 + qi[x].z * kj[y].z * e2 +
+                              qi[x].w * kj[y].w * e3;
+            }
+        }
+      }
+      __syncthreads();
+    }
+    for (int idx = tid; idx < kC * kRC; idx += kPT) AqkS[idx] = 0.f;
+    __syncthreads();
+#pragma unroll
+    for (int sl = 0; sl < 2; ++sl) {
+      if (!live[sl]) continue;
 #pragma unroll
       for (int x = 0; x < 2; ++x)
 #pragma unroll
         for (int y = 0; y < 2; ++y) {
-          const bool ok = !(x == 0 && y == 1) || off_diag;
-          const float e0 = ok ? fast_exp(li[x].x - lj[y].x) : 0.f;
-          const float e1 = ok ? fast_exp(li[x].y - lj[y].y) : 0.f;
-          const float e2 = ok ? fast_exp(li[x].z - lj[y].z) : 0.f;
-          const float e3 = ok ? fast_exp(li[x].w - lj[y].w) : 0.f;
-          aa[x][y] += ki[x].x * kj[y].x * e0 + ki[x].y * kj[y].y * e1 + ki[x].z * kj[y].z * e2 + ki[x].w * kj[y].w * e3;
-          aq[x][y] += qi[x].x * kj[y].x * e0 + qi[x].y * kj[y].y * e1 + qi[x].z * kj[y].z * e2 + qi[x].w * kj[y].w * e3;
+          const int i = bi[sl] + x, j = bj[sl] + y;
+          if (j < i) AS[i * kRC + j] = ea[sl][x][y];
+          if (j <= i) AqkS[i * kRC + j] = eq[sl][x][y];
         }
     }
+  } else {
+    // the pairs from registers (Aqk's tile, over the quarter tiles, written
+    // whole: the six blocks above the diagonal as zeros)
 #pragma unroll
-    for (int x = 0; x < 2; ++x)
+    for (int r = 0; r < 4; ++r) {
+      const int row = 16 * I + 4 * lg4 + r, col = 16 * J + li;
+      if (col < row) AS[row * kRC + col] = ak[r];
+      AqkS[row * kRC + col] = col <= row ? aq[r] : 0.f;
+    }
+    if (two) {
 #pragma unroll
-      for (int y = 0; y < 2; ++y) {
-        const int i = i0 + x, j = j0 + y;
-        if (j < i) AS[i * kRC + j] = aa[x][y];
-        if (j <= i) AqkS[i * kRC + j] = aq[x][y];
+      for (int r = 0; r < 4; ++r) {
+        const int row = 16 * I8 + 4 * lg4 + r, col = 16 * J8 + li;
+        if (col < row) AS[row * kRC + col] = ak8[r];
+        AqkS[row * kRC + col] = col <= row ? aq8[r] : 0.f;
       }
+    }
+    for (int e = tid; e < 6 * 256; e += kPT) {  // blocks (I, J > I)
+      const int p6 = e >> 8, I2 = p6 < 3 ? 0 : (p6 < 5 ? 1 : 2), J2 = p6 < 3 ? p6 + 1 : (p6 < 5 ? p6 - 1 : 3);
+      AqkS[(16 * I2 + ((e & 255) >> 4)) * kRC + 16 * J2 + (e & 15)] = 0.f;
+    }
   }
   __syncthreads();
-  // the records only the gradient kernels read (A, N, Kg, Kt row-major, W^T)
-  // are skipped when the kernels serve the forward alone (no dO)
-  const bool bwd_records = a.dout != nullptr;
   for (int i4 = tid; bwd_records && i4 < kC * kC / 4; i4 += kPT) {  // A, four at a time
     const int r = (4 * i4) >> 6, cc = (4 * i4) & 63;
     *reinterpret_cast<f32x4*>(ws + a.L.A + 4 * i4) = *reinterpret_cast<const f32x4*>(&AS[r * kRC + cc]);
@@ -692,68 +843,16 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     for (int e = 0; e < 8; ++e) x[e] = AqkS[(c0 + e) * kRC + r];
     put_split8<kSplitOps<IT>>(ws + a.L.Aqkt, kC * kC, 8 * i8, x);
   }
-  if (tid < Kp) {
-    lastS[tid] = lgS[(kC - 1) * kRS + tid];
-    ws[a.L.D + tid] = fast_exp(lgS[(kC - 1) * kRS + tid]);
-  }
   __syncthreads();
-  // each element's factors once: k, q, lg become Kg = e^lg k, Kt = e^(lg_last - lg) k
-  // and Qg = e^lg q in place (the B operand of W = M Kg; the transposed records
-  // below read Kt and Qg), with the row-major Kg and Kt records written on the way
-  for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {
-    const int r = (8 * i8) / Kp, c0 = (8 * i8) % Kp;
-    float* kp = &kS[r * kRS + c0];
-    float* qp = &qS[r * kRS + c0];
-    float* lp = &lgS[r * kRS + c0];
-    float kg[8], kt[8], qg[8];
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const f32x4 kk = *reinterpret_cast<const f32x4*>(kp + 4 * u), qq = *reinterpret_cast<const f32x4*>(qp + 4 * u);
-      const f32x4 ll = *reinterpret_cast<const f32x4*>(lp + 4 * u);
-      const f32x4 la = *reinterpret_cast<const f32x4*>(&lastS[c0 + 4 * u]);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float ex = fast_exp(ll[e]);
-        kg[4 * u + e] = ex * kk[e];
-        kt[4 * u + e] = fast_exp(la[e] - ll[e]) * kk[e];
-        qg[4 * u + e] = ex * qq[e];
-      }
-    }
-    if (bwd_records) {  // Kg (f32) and Kt split, row-major
-#pragma unroll
-      for (int u = 0; u < 2; ++u)
-        *reinterpret_cast<f32x4*>(ws + a.L.Kg + 8 * i8 + 4 * u) =
-            f32x4{kg[4 * u], kg[4 * u + 1], kg[4 * u + 2], kg[4 * u + 3]};
-      put_split8<kSplitOps<IT>>(ws + a.L.Ktr, kC * Kp, 8 * i8, kt);
-    }
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      *reinterpret_cast<f32x4*>(kp + 4 * u) = f32x4{kg[4 * u], kg[4 * u + 1], kg[4 * u + 2], kg[4 * u + 3]};
-      *reinterpret_cast<f32x4*>(qp + 4 * u) = f32x4{kt[4 * u], kt[4 * u + 1], kt[4 * u + 2], kt[4 * u + 3]};
-      *reinterpret_cast<f32x4*>(lp + 4 * u) = f32x4{qg[4 * u], qg[4 * u + 1], qg[4 * u + 2], qg[4 * u + 3]};
-    }
-  }
-  __syncthreads();
-  for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {  // Kt^T and Qg^T split, eight positions at a time
-    const int col = (8 * i8) / kC, r0 = (8 * i8) % kC;
-    float xk[8], xq[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      xk[e] = qS[(r0 + e) * kRS + col];
-      xq[e] = lgS[(r0 + e) * kRS + col];
-    }
-    put_split8<kSplitOps<IT>>(ws + a.L.Ktt, kC * Kp, 8 * i8, xk);
-    put_split8<kSplitOps<IT>>(ws + a.L.Qgt, kC * Kp, 8 * i8, xq);
-  }
-  for (int i4 = tid; i4 < kC * kC / 4; i4 += kPT) {  // L's strict part b_i A_ij over A; N cleared
+  for (int i4 = tid; i4 < kC * kC / 4; i4 += kPT) {  // L's strict part b_i A_ij over A; N cleared over Aqk
     const int r = (4 * i4) >> 6, cc = (4 * i4) & 63;
     f32x4* ap = reinterpret_cast<f32x4*>(&AS[r * kRC + cc]);
     *ap = *ap * bS[r];
     *reinterpret_cast<f32x4*>(&NS[r * kRC + cc]) = zero4();
   }
   __syncthreads();
-  // v (into lg's rows once W is formed): its loads go out now and land while
-  // N, M and W are formed
+  // v (over Kg's tile once W's records are out): its loads go out now and
+  // land while N, M and W are formed
   const bool v_early = (Vp & 31) == 0 && rows_fast(a.V, 0, Vp);
   RowTile<IT, 32, kPT> rv[4];  // Vp <= 128
   if (v_early) {
@@ -778,19 +877,19 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     for (int i = 0; i < 16; ++i) NS[(base + i) * kRC + base + lane] = x[i];
   }
   __syncthreads();
-  float* TS = qS + w * 16 * kTS;  // q is no longer read: 16x16 scratch per wave
-  for (int I = 1; I < 4; ++I) {
-    if (w < I) {
-      const f32x4 t = mma(zero4(), Mat{AS + 16 * w, kRC, 1}, 16 * I, Mat{NS + 16 * w * kRC, kRC, 1}, 16 * w,
-                          16 * (I - w));
+  float* TS = NS + kC * kRC + w * 16 * kTS;  // 16x16 scratch per wave
+  for (int Ib = 1; Ib < 4; ++Ib) {
+    if (w < Ib) {
+      const f32x4 t = mma(zero4(), Mat{AS + 16 * w, kRC, 1}, 16 * Ib, Mat{NS + 16 * w * kRC, kRC, 1}, 16 * w,
+                          16 * (Ib - w));
 #pragma unroll
       for (int r = 0; r < 4; ++r) TS[(4 * lg4 + r) * kTS + li] = t[r];
     }
     __syncthreads();
-    if (w < I) {
-      const f32x4 n = mma(zero4(), Mat{NS + 16 * I, kRC, 1}, 16 * I, Mat{TS, kTS, 1}, 0, 16);
+    if (w < Ib) {
+      const f32x4 n = mma(zero4(), Mat{NS + 16 * Ib, kRC, 1}, 16 * Ib, Mat{TS, kTS, 1}, 0, 16);
 #pragma unroll
-      for (int r = 0; r < 4; ++r) NS[(16 * I + 4 * lg4 + r) * kRC + 16 * w + li] = -n[r];
+      for (int r = 0; r < 4; ++r) NS[(16 * Ib + 4 * lg4 + r) * kRC + 16 * w + li] = -n[r];
     }
     __syncthreads();
   }
@@ -801,37 +900,47 @@ __global__ __launch_bounds__(kPT) void prep_kernel(const Args<IT> a) {
     *reinterpret_cast<f32x4*>(&AS[r * kRC + cc]) = n * *reinterpret_cast<const f32x4*>(&bS[cc]);
   }
   __syncthreads();
-  const int nkt = Kp / 16, nvt = Vp / 16;
-  for (int tt = w; tt < 4 * nkt; tt += kPT / 64) {  // W = M Kg, staged in f32 over q
-    const int rt = tt & 3, ct = tt >> 2;
-    const f32x4 acc = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{kS, kRS, 1}, 16 * ct, kC);
+  // W = M Kg, staged in f32 over Kg once every tile is formed
+  f32x4 wt[NW];
 #pragma unroll
-    for (int r = 0; r < 4; ++r) qS[(16 * rt + 4 * lg4 + r) * kRS + 16 * ct + li] = acc[r];
-  }
-  if (v_early) {  // v over lg (no longer read)
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      if (32 * j < Vp) rv[j].template store<kRS>(lgS + 32 * j, t0, Tv, tid);
-  } else {
-    for (int s0 = 0; s0 < Vp; s0 += 32)
-      load_rows<IT, 32, kRS, kPT>(lgS + s0, a.v, b, t0, a.T, a.H, h, a.V, s0, tid, Tv);
+  for (int j = 0; j < NW; ++j) {
+    const int tt = w + 8 * j, rt = tt & 3, ct = tt >> 2;
+    wt[j] = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{KgS, kRS, 1}, 16 * ct, kC);
   }
   __syncthreads();
-  for (int i8 = tid; i8 < kC * Kp / 8; i8 += kPT) {  // W and W^T split
+#pragma unroll
+  for (int j = 0; j < NW; ++j) {
+    const int tt = w + 8 * j, rt = tt & 3, ct = tt >> 2;
+#pragma unroll
+    for (int r = 0; r < 4; ++r) KgS[(16 * rt + 4 * lg4 + r) * kRS + 16 * ct + li] = wt[j][r];
+  }
+  __syncthreads();
+  for (int i8 = tid; i8 < kC * KP / 8; i8 += kPT) {  // W and W^T split
     float x[8], y[8];
-    const int r = (8 * i8) / Kp, c0 = (8 * i8) % Kp;
+    const int r = (8 * i8) / KP, c0 = (8 * i8) % KP;
     const int c2 = (8 * i8) / kC, r2 = (8 * i8) % kC;
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
-      x[e] = qS[r * kRS + c0 + e];
-      y[e] = qS[(r2 + e) * kRS + c2];
+      x[e] = KgS[r * kRS + c0 + e];
+      y[e] = KgS[(r2 + e) * kRS + c2];
     }
-    put_split8<kSplitOps<IT>>(ws + a.L.Wr, kC * Kp, 8 * i8, x);
-    if (bwd_records) put_split8<kSplitOps<IT>>(ws + a.L.Wt, kC * Kp, 8 * i8, y);
+    put_split8<kSplitOps<IT>>(ws + a.L.Wr, kC * KP, 8 * i8, x);
+    if (bwd_records) put_split8<kSplitOps<IT>>(ws + a.L.Wt, kC * KP, 8 * i8, y);
   }
+  __syncthreads();
+  if (v_early) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      if (32 * j < Vp) rv[j].template store<kRS>(KgS + 32 * j, t0, Tv, tid);
+  } else {
+    for (int s0 = 0; s0 < Vp; s0 += 32)
+      load_rows<IT, 32, kRS, kPT>(KgS + s0, a.v, b, t0, a.T, a.H, h, a.V, s0, tid, Tv);
+  }
+  __syncthreads();
+  const int nvt = Vp / 16;
   for (int tt = w; tt < 4 * nvt; tt += kPT / 64) {  // U = M v
     const int rt = tt & 3, ct = tt >> 2;
-    const f32x4 acc = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{lgS, kRS, 1}, 16 * ct, kC);
+    const f32x4 acc = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{KgS, kRS, 1}, 16 * ct, kC);
 #pragma unroll
     for (int r = 0; r < 4; ++r) ws[a.L.U + (16 * rt + 4 * lg4 + r) * Vp + 16 * ct + li] = acc[r];
   }

@@ -311,12 +311,14 @@ def test_many_packed_documents_backward_in_length_buckets():
             assert rel_err(a, b) < TOL[torch.float32], (name, i)
 
 
+@pytest.mark.parametrize("key_dim", [128, 64])
 @pytest.mark.parametrize("regime", ["steep", "rising"])
-def test_backward_exact_path_regimes(regime):
+def test_backward_exact_path_regimes(regime, key_dim):
     # chunks whose decay falls by more than 80 within 16 tokens, or whose g is
     # positive somewhere, take the exact pairwise path instead of the MFMA
-    # factorisation; both must match the oracle
-    B, T, H, K, V = 1, 128, 2, 128, 64
+    # factorisation (a second pass over the key channels, four quarters at
+    # key_dim 128 and two at 64); both must match the oracle
+    B, T, H, K, V = 1, 128, 2, key_dim, 64
     inputs, d_out, d_final = _case(B, T, H, K, V, torch.float32, seed=6)
     q, k, v, g, beta, s0 = inputs
     gen = torch.Generator().manual_seed(7)
