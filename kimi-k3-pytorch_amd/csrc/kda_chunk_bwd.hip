@@ -573,6 +573,14 @@ __device__ __forceinline__ void block_pair(int p, int& I, int& J) {
   J = p - I * (I + 1) / 2;
 }
 
+// A per-lane offset the compiler may not hoist out of a loop: keeps the many
+// invariant per-lane addresses of the loop from occupying registers (or
+// scratch, whose reloads wait for every earlier load and store).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // ---- prep_kernel: per-chunk intermediates ----------------------------------
 // The chunk's k, q and g pass through LDS kQC key channels (a quarter of 128)
 // at a time, so that the kernel's LDS (79 KB) lets two workgroups share a CU
@@ -669,22 +677,23 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
   bool risky = false;
   for (int p = 0; p < NQ; ++p) {
     const int c0 = p * kQC;
-    in.store(kS, qS, lgS, a, b, t0, h, c0, tid, Tv);
+    const int tq = opaque(tid);  // per-lane addresses formed in the loop
+    in.store(kS, qS, lgS, a, b, t0, h, c0, tq, Tv);
     __syncthreads();
-    if (p + 1 < NQ) in.fetch(a, b, t0, h, c0 + kQC, tid);
+    if (p + 1 < NQ) in.fetch(a, b, t0, h, c0 + kQC, tq);
     risky |= chunk_cumsum<kQC, kQS>(lgS, tmpS, tid);
     risky |= decay_risk<kQC, kPT, kQS>(lgS, tid);
     decay_product<kQS>(ak, aq, kS, qS, lgS, 16 * I, 16 * J, 16 * I, kQC);
     if (two) decay_product<kQS>(ak8, aq8, kS, qS, lgS, 16 * I8, 16 * J8, 16 * I8, kQC);
-    if (tid < kQC) {
-      const float last = lgS[(kC - 1) * kQS + tid];
-      lastS[tid] = last;
-      ws[a.L.D + c0 + tid] = fast_exp(last);
+    if (tq < kQC) {
+      const float last = lgS[(kC - 1) * kQS + tq];
+      lastS[tq] = last;
+      ws[a.L.D + c0 + tq] = fast_exp(last);
     }
     __syncthreads();
     // each element's factors once: Kg, Kt, Qg in place of k, q, lg, with Kg
     // into its tile and the row-major Kg and Kt records written on the way
-    for (int i8 = tid; i8 < kC * kQC / 8; i8 += kPT) {
+    for (int i8 = tq; i8 < kC * kQC / 8; i8 += kPT) {
       const int r = (8 * i8) / kQC, cl = (8 * i8) % kQC;
       const float* kp = &kS[r * kQS + cl];
       float* qp = &qS[r * kQS + cl];
@@ -720,7 +729,7 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
       }
     }
     __syncthreads();
-    for (int i8 = tid; i8 < kC * kQC / 8; i8 += kPT) {  // Kt^T and Qg^T split, eight positions at a time
+    for (int i8 = tq; i8 < kC * kQC / 8; i8 += kPT) {  // Kt^T and Qg^T split, eight positions at a time
       const int col = (8 * i8) / kC, r0 = (8 * i8) % kC;
       float xk[8], xq[8];
 #pragma unroll
@@ -1025,13 +1034,6 @@ struct Rec {
     }
   }
 };
-
-// A per-lane offset the compiler may not hoist out of the chunk loop: keeps
-// the many invariant per-lane addresses of the loop from occupying registers.
-__device__ __forceinline__ int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
 
 __device__ __forceinline__ bf16x8 frag_ld(const unsigned char* sm, int base, int f, int plane, int lane) {
   return *reinterpret_cast<const bf16x8*>(sm + base + f * 2048 + plane * 1024 + lane * 16);

@@ -329,9 +329,16 @@ def test_backward_exact_path_regimes(regime, key_dim):
     inputs = (q, k, v, g, beta, s0)
     got = _gpu_grads(inputs, d_out, d_final)
     ref = _oracle_grads(inputs, d_out, d_final)
-    for name, a, b in zip(NAMES, got, ref):
+    # dg is a reverse cumulative sum of terms that cancel when the decay is
+    # steep: the oracle itself evaluated in f32 misses the f64 dg by 2e-5
+    # (key_dim 128) and 8e-5 (64) while the other gradients stay near 2e-7,
+    # so each gradient is held to 2e-4 or five times plain f32's own error
+    ref32 = ora.chunkwise_backward(q.float(), k.float(), v.float(), g.float(), beta.float(), s0.float(),
+                                   d_out.float(), d_final.float(), chunk_size=64)
+    for name, a, b, c in zip(NAMES, got, ref, ref32):
         assert torch.isfinite(a).all(), name
-        assert rel_err(a, b) < TOL[torch.float32], (name, rel_err(a, b))
+        tol = max(TOL[torch.float32], 5.0 * rel_err(c, b))
+        assert rel_err(a, b) < tol, (name, rel_err(a, b), tol)
 
 
 def test_recurrent_kda_gradients_match_oracle():
