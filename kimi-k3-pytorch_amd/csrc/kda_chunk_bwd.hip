@@ -645,7 +645,10 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
   float* const NS = pool;            // after Aqk's record
   float* const KgS = pool + QREG;    // Kg, then W, then v
   float* const AS = KgS + kC * kRS;
-  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, li = lane & 15, lg4 = lane >> 4;
+  const int tid = threadIdx.x, lane = tid & 63, li = lane & 15, lg4 = lane >> 4;
+  // the wave index scalar: the block pairs and tiles derived from it stay in
+  // scalar registers instead of vector registers (or scratch)
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t ch = blockIdx.x;
   const int64_t c = ch % a.NC, bh = ch / a.NC, b = bh / a.H, h = bh % a.H;
   const int64_t t0 = c * kC;
