@@ -917,7 +917,7 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
 #pragma unroll
   for (int j = 0; j < NW; ++j) {
     const int tt = w + 8 * j, rt = tt & 3, ct = tt >> 2;
-    wt[j] = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{KgS, kRS, 1}, 16 * ct, kC);
+    wt[j] = mma_sb(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{KgS, kRS, 1}, 16 * ct, kC);
   }
   __syncthreads();
 #pragma unroll
@@ -952,7 +952,7 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
   const int nvt = Vp / 16;
   for (int tt = w; tt < 4 * nvt; tt += kPT / 64) {  // U = M v
     const int rt = tt & 3, ct = tt >> 2;
-    const f32x4 acc = mma_long(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{KgS, kRS, 1}, 16 * ct, kC);
+    const f32x4 acc = mma_sb(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{KgS, kRS, 1}, 16 * ct, kC);
 #pragma unroll
     for (int r = 0; r < 4; ++r) ws[a.L.U + (16 * rt + 4 * lg4 + r) * Vp + 16 * ct + li] = acc[r];
   }
