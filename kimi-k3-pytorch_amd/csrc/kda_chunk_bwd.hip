@@ -271,12 +271,19 @@ __device__ __forceinline__ void put_split8(float* rec, int n, int idx, const flo
   if constexpr (SPLIT) *reinterpret_cast<bf16x8*>(p + n + idx) = lo;
 }
 
+// The lane index counted from an all-ones mask (v_mbcnt: independent of the
+// execution mask), formed where it is used instead of kept live across a
+// kernel.
+__device__ __forceinline__ int lane_id() {
+  return static_cast<int>(__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)));
+}
+
 // acc += A[r0:r0+16, 0:kd] B[0:kd, c0:c0+16] for f32 matrices in LDS (see
 // Mat), on split-bf16 operands formed in registers: lane (i, g) takes
 // A[r0+i][k0+8g+e] and B[k0+8g+e][c0+i], e = 0..7, per 32-deep step (three
 // bf16 MFMAs against the eight f32 ones of mma_long; kd a multiple of 32).
 __device__ __forceinline__ f32x4 mma_sb(f32x4 acc, Mat A, int r0, Mat B, int c0, int kd) {
-  const int lane = threadIdx.x & 63, i = lane & 15, g = lane >> 4;
+  const int lane = lane_id(), i = lane & 15, g = lane >> 4;
   const float* a = A.p + (r0 + i) * A.rs + 8 * g * A.cs;
   const float* b = B.p + 8 * g * B.rs + (c0 + i) * B.cs;
   f32x4 acc2 = zero4();
@@ -824,6 +831,7 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
   } else {
     // the pairs from registers (Aqk's tile, over the quarter tiles, written
     // whole: the six blocks above the diagonal as zeros)
+    const int li = lane_id() & 15, lg4 = lane_id() >> 4;
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = 16 * I + 4 * lg4 + r, col = 16 * J + li;
@@ -844,11 +852,13 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
     }
   }
   __syncthreads();
-  for (int i4 = tid; bwd_records && i4 < kC * kC / 4; i4 += kPT) {  // A, four at a time
+  // per-lane addresses of the record stores formed here, not at the top
+  const int tr = opaque(tid);
+  for (int i4 = tr; bwd_records && i4 < kC * kC / 4; i4 += kPT) {  // A, four at a time
     const int r = (4 * i4) >> 6, cc = (4 * i4) & 63;
     *reinterpret_cast<f32x4*>(ws + a.L.A + 4 * i4) = *reinterpret_cast<const f32x4*>(&AS[r * kRC + cc]);
   }
-  for (int i8 = tid; i8 < kC * kC / 8; i8 += kPT) {  // Aqk^T split, eight positions at a time
+  for (int i8 = tr; i8 < kC * kC / 8; i8 += kPT) {  // Aqk^T split, eight positions at a time
     const int r = (8 * i8) >> 6, c0 = (8 * i8) & 63;
     float x[8];
 #pragma unroll
@@ -905,7 +915,7 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
     }
     __syncthreads();
   }
-  for (int i4 = tid; i4 < kC * kC / 4; i4 += kPT) {  // M = N diag(b) over A, four at a time
+  for (int i4 = tr; i4 < kC * kC / 4; i4 += kPT) {  // M = N diag(b) over A, four at a time
     const int r = (4 * i4) >> 6, cc = (4 * i4) & 63;
     const f32x4 n = *reinterpret_cast<const f32x4*>(&NS[r * kRC + cc]);
     if (bwd_records) *reinterpret_cast<f32x4*>(ws + a.L.N + 4 * i4) = n;
@@ -924,10 +934,10 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
   for (int j = 0; j < NW; ++j) {
     const int tt = w + 8 * j, rt = tt & 3, ct = tt >> 2;
 #pragma unroll
-    for (int r = 0; r < 4; ++r) KgS[(16 * rt + 4 * lg4 + r) * kRS + 16 * ct + li] = wt[j][r];
+    for (int r = 0; r < 4; ++r) KgS[(16 * rt + 4 * (lane_id() >> 4) + r) * kRS + 16 * ct + (lane_id() & 15)] = wt[j][r];
   }
   __syncthreads();
-  for (int i8 = tid; i8 < kC * KP / 8; i8 += kPT) {  // W and W^T split
+  for (int i8 = tr; i8 < kC * KP / 8; i8 += kPT) {  // W and W^T split
     float x[8], y[8];
     const int r = (8 * i8) / KP, c0 = (8 * i8) % KP;
     const int c2 = (8 * i8) / kC, r2 = (8 * i8) % kC;
@@ -954,7 +964,7 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
     const int rt = tt & 3, ct = tt >> 2;
     const f32x4 acc = mma_sb(zero4(), Mat{AS, kRC, 1}, 16 * rt, Mat{KgS, kRS, 1}, 16 * ct, kC);
 #pragma unroll
-    for (int r = 0; r < 4; ++r) ws[a.L.U + (16 * rt + 4 * lg4 + r) * Vp + 16 * ct + li] = acc[r];
+    for (int r = 0; r < 4; ++r) ws[a.L.U + (16 * rt + 4 * (lane_id() >> 4) + r) * Vp + 16 * ct + (lane_id() & 15)] = acc[r];
   }
 }
 
