@@ -206,16 +206,23 @@ __global__ __launch_bounds__(256) void gates_bwd_kernel(const GateBwdArgs<T> a) 
 //   dx_s = sum_j w[j] dpre_{s+j} (+ dh' where x_s went into the next history),
 //   dhist_m = sum_j w[j] dpre_{m-(K-1)+j} (+ dh' where the history row went on),
 //   dw[c][j] += sum_t dpre_t x_{t-j},  dbias[c] += sum_t dpre_t.
-// One wave per (batch row, block of 64*VEC channels, run of kConvBwdSub
-// sub-tiles of kConvBwdTile positions).  For each sub-tile it recomputes dpre
-// of its positions and the K-1 after them from the inputs (the K-1 before
-// included), so every dx of the sub-tile is complete; the weight and bias
-// gradients accumulate in registers over the run, are summed over the
-// block's 4 waves (the same channels, consecutive runs) in LDS, and go out
-// with one atomic per element and block.
-constexpr int kConvBwdTile = 8;
-constexpr int kConvBwdSub = 8;
+// One lane per (batch row, VEC channels, run of kConvBwdRun positions).  The
+// lane walks positions t0 - (KM-1) .. t0 + R + KM - 2 in order with the last
+// KM inputs and the last KM values of dpre in registers: at position t it
+// loads x_t (and dy_t), forms dpre_t (t >= t0; zero before), adds dpre_t and
+// dpre_t x_{t-j} to the bias and weight gradients while t is in the run, and
+// completes dx_s = sum_j w[j] dpre_{s+j} for s = t - (KM-1) in the run; the
+// run at t0 = 0 also completes the history rows (s < 0).  The K-1 rows on
+// either side of a run are read by both neighbouring runs (L2 hits).  A block
+// takes conv_bwd_waves<KT>() consecutive runs of one channel block (16 at a
+// compile-time kernel size, 8 for any K: its windows of kConvBwdMaxK need the
+// registers of two waves per SIMD instead of four); its waves' weight and bias
+// gradients are summed in LDS in a fixed order and go out with one atomic per
+// element and block.
+constexpr int kConvBwdRun = 16;
 constexpr int kConvBwdMaxK = 8;
+template <int KT>
+__host__ __device__ constexpr int conv_bwd_waves() { return KT > 0 ? 16 : 8; }
 
 template <class T>
 struct ConvBwdArgs {
@@ -235,31 +242,28 @@ struct ConvBwdArgs {
   float eps;
 };
 
-__host__ __device__ constexpr int64_t conv_bwd_runs(int64_t nt) {
-  return (nt + kConvBwdTile * kConvBwdSub - 1) / (kConvBwdTile * kConvBwdSub);
-}
+__host__ __device__ constexpr int64_t conv_bwd_runs(int64_t nt) { return (nt + kConvBwdRun - 1) / kConvBwdRun; }
 
 // VEC: channels per lane; KT: the kernel size, or 0 for any K <= kConvBwdMaxK;
 // G: lanes per normalised head (0: no normalisation).
 template <class T, int VEC, int KT, int G>
-__global__ __launch_bounds__(256) void conv_silu_bwd_kernel(const ConvBwdArgs<T> a) {
+__global__ __launch_bounds__(64 * conv_bwd_waves<KT>()) void conv_silu_bwd_kernel(const ConvBwdArgs<T> a) {
   using C = typename ComputeOf<T>::type;
   typedef T vec_t __attribute__((ext_vector_type(VEC)));
-  constexpr int TT = kConvBwdTile;
   constexpr int KM = KT > 0 ? KT : kConvBwdMaxK;
-  constexpr int NP = TT + KM - 1;  // positions whose dpre a sub-tile needs
-  constexpr int NX = NP + KM - 1;  // inputs those need
-  __shared__ C red[4][64 * VEC * (KM + 1)];
+  constexpr int R = kConvBwdRun, NW = conv_bwd_waves<KT>();
+  constexpr int NSTEP = R + 2 * (KM - 1);  // positions walked per run
+  __shared__ C red[NW / 2][64 * VEC * (KM + 1)];
   const int lane = threadIdx.x & 63;
   const int wv = threadIdx.x >> 6;
   const int64_t nblk = (a.nc + 64 * VEC - 1) / (64 * VEC);
   const int64_t runs = conv_bwd_runs(a.nt);
-  const int64_t rgroups = (runs + 3) / 4;  // a block takes 4 consecutive runs of one channel block
+  const int64_t rgroups = (runs + NW - 1) / NW;  // a block takes NW consecutive runs of one channel block
   const int64_t bid = blockIdx.x;
   const int64_t rg = bid % rgroups;
   const int64_t cb = (bid / rgroups) % nblk;
   const int64_t b = bid / (rgroups * nblk);
-  const int64_t run = rg * 4 + wv;
+  const int64_t t0 = (rg * NW + wv) * R;
   const int64_t c0 = (cb * 64 + lane) * VEC;
   const bool on = c0 < a.nc;
   const int K = KT > 0 ? KT : a.K;
@@ -281,96 +285,102 @@ __global__ __launch_bounds__(256) void conv_silu_bwd_kernel(const ConvBwdArgs<T>
     br[e] = (on && a.bias != nullptr) ? to_compute<C>(a.bias[c0 + e]) : C(0);
     gb[e] = C(0);
   }
-  for (int sub = 0; sub < kConvBwdSub; ++sub) {
-    const int64_t t0 = (run * kConvBwdSub + sub) * TT;
-    if (t0 >= a.nt) break;  // uniform over the wave
-    // inputs at positions t0 - (KM-1) .. t0 + NP - 1 (history below 0, zero past len)
-    vec_t xs[NX];
+  if (t0 < a.nt) {  // uniform over the wave
+    C xw[KM][VEC], pw[KM][VEC];  // x_{t-KM+1} .. x_t and dpre_{t-KM+1} .. dpre_t
 #pragma unroll
-    for (int i = 0; i < NX; ++i) {
-      const int64_t p = t0 - (KM - 1) + i;
-      vec_t z = {};
+    for (int j = 0; j < KM; ++j)
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) xw[j][e] = pw[j][e] = C(0);
+#pragma unroll 1
+    for (int i = 0; i < NSTEP; ++i) {
+      const int64_t t = t0 - (KM - 1) + i;
+      // x_t (the history below 0, zero past len)
+      vec_t xv = {};
       if (on) {
-        if (p >= 0 && p < len)
-          z = row(a.x, b * a.nt + p);
-        else if (p < 0 && p >= -H1 && a.hist_in != nullptr)
-          z = row(a.hist_in, b * H1 + H1 + p);
+        if (t >= 0 && t < len)
+          xv = row(a.x, b * a.nt + t);
+        else if (t < 0 && t >= -H1 && a.hist_in != nullptr)
+          xv = row(a.hist_in, b * H1 + H1 + t);
       }
-      xs[i] = z;
-    }
-    C dpre[NP][VEC];
 #pragma unroll
-    for (int i = 0; i < NP; ++i) {
-      const int64_t t = t0 + i;
-      const bool real = t < len;  // uniform over the wave
-      C pre[VEC], act[VEC], sg[VEC], da[VEC];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        C acc = br[e];
-#pragma unroll
-        for (int j = 0; j < KM; ++j) acc += wr[j][e] * to_compute<C>(xs[i + KM - 1 - j][e]);
-        pre[e] = acc;
-        sg[e] = sigmoid(acc);
-        act[e] = acc * sg[e];
-      }
-      vec_t dv = {};
-      if (on && real) dv = row(a.dy, b * a.nt + t);
-      if constexpr (G > 0) {
-        C ss = C(0), yd = C(0);
+      for (int j = 0; j < KM - 1; ++j)
 #pragma unroll
         for (int e = 0; e < VEC; ++e) {
-          ss += act[e] * act[e];
-          yd += act[e] * to_compute<C>(dv[e]);
+          xw[j][e] = xw[j + 1][e];
+          pw[j][e] = pw[j + 1][e];
         }
-        ss = group_sum<G>(ss);
-        yd = group_sum<G>(yd);
-        const C eps = C(a.eps);
-        if (ss > eps * eps) {
-          const C inv = frsqrt(ss);  // 1 / ||a||
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) da[e] = (to_compute<C>(dv[e]) - act[e] * yd * inv * inv) * inv;
+      for (int e = 0; e < VEC; ++e) {
+        xw[KM - 1][e] = to_compute<C>(xv[e]);
+        pw[KM - 1][e] = C(0);
+      }
+      if (i >= KM - 1) {  // t >= t0: dpre_t
+        const bool real = t < len;  // uniform over the wave
+        C pre[VEC], act[VEC], sg[VEC], da[VEC];
+#pragma unroll
+        for (int e = 0; e < VEC; ++e) {
+          C acc = br[e];
+#pragma unroll
+          for (int j = 0; j < KM; ++j) acc += wr[j][e] * xw[KM - 1 - j][e];
+          pre[e] = acc;
+          sg[e] = sigmoid(acc);
+          act[e] = acc * sg[e];
+        }
+        vec_t dv = {};
+        if (on && real) dv = row(a.dy, b * a.nt + t);
+        if constexpr (G > 0) {
+          C ss = C(0), yd = C(0);
+#pragma unroll
+          for (int e = 0; e < VEC; ++e) {
+            ss += act[e] * act[e];
+            yd += act[e] * to_compute<C>(dv[e]);
+          }
+          ss = group_sum<G>(ss);
+          yd = group_sum<G>(yd);
+          const C eps = C(a.eps);
+          if (ss > eps * eps) {
+            const C inv = frsqrt(ss);  // 1 / ||a||
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) da[e] = (to_compute<C>(dv[e]) - act[e] * yd * inv * inv) * inv;
+          } else {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) da[e] = to_compute<C>(dv[e]) / eps;
+          }
         } else {
 #pragma unroll
-          for (int e = 0; e < VEC; ++e) da[e] = to_compute<C>(dv[e]) / eps;
+          for (int e = 0; e < VEC; ++e) da[e] = to_compute<C>(dv[e]);
         }
-      } else {
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) da[e] = to_compute<C>(dv[e]);
-      }
+        for (int e = 0; e < VEC; ++e) pw[KM - 1][e] = real ? da[e] * sg[e] * (C(1) + pre[e] * (C(1) - sg[e])) : C(0);
+        if (i < KM - 1 + R) {  // t in the run
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) dpre[i][e] = real ? da[e] * sg[e] * (C(1) + pre[e] * (C(1) - sg[e])) : C(0);
-      if (i < TT) {
+          for (int e = 0; e < VEC; ++e) {
+            gb[e] += pw[KM - 1][e];
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) {
-          gb[e] += dpre[i][e];
-#pragma unroll
-          for (int j = 0; j < KM; ++j) gw[j][e] += dpre[i][e] * to_compute<C>(xs[i + KM - 1 - j][e]);
+            for (int j = 0; j < KM; ++j) gw[j][e] += pw[KM - 1][e] * xw[KM - 1 - j][e];
+          }
         }
       }
-    }
-    // dx_s = sum_j w[j] dpre_{s+j}, plus the next history's gradient
+      // s = t - (KM-1): dx_s = sum_j w[j] dpre_{s+j} (+ the next history's gradient)
+      const int64_t s = t - (KM - 1);
+      if (i >= 2 * (KM - 1)) {  // s >= t0
+        if (s < a.nt) {
+          vec_t hv = {};
+          const bool to_hist = a.dhist_out != nullptr && s < len && s >= len - H1;
+          if (on && to_hist) hv = row(a.dhist_out, b * H1 + (s - (len - H1)));
+          vec_t o;
 #pragma unroll
-    for (int i = 0; i < TT; ++i) {
-      const int64_t s = t0 + i;
-      if (s >= a.nt) break;  // uniform
-      vec_t hv = {};
-      const bool to_hist = a.dhist_out != nullptr && s < len && s >= len - H1;
-      if (on && to_hist) hv = row(a.dhist_out, b * H1 + (s - (len - H1)));
-      vec_t o;
+          for (int e = 0; e < VEC; ++e) {
+            C acc = to_compute<C>(hv[e]);
 #pragma unroll
-      for (int e = 0; e < VEC; ++e) {
-        C acc = to_compute<C>(hv[e]);
-#pragma unroll
-        for (int j = 0; j < KM; ++j) acc += wr[j][e] * dpre[i + j][e];
-        o[e] = from_compute<T>(acc);
-      }
-      if (on) *reinterpret_cast<vec_t*>(a.dx + (b * a.nt + s) * a.nc + c0) = o;
-    }
-    // the history rows' gradient (positions -H1 .. -1), by the first sub-tile
-    if (t0 == 0 && a.dhist_in != nullptr && on) {
-      for (int m = 0; m < H1; ++m) {
-        const int64_t p = m - H1;
-        const int64_t q = m - len;  // its row in the next history, if it stays there
+            for (int j = 0; j < KM; ++j) acc += wr[j][e] * pw[j][e];
+            o[e] = from_compute<T>(acc);
+          }
+          if (on) *reinterpret_cast<vec_t*>(a.dx + (b * a.nt + s) * a.nc + c0) = o;
+        }
+      } else if (t0 == 0 && s >= -H1 && a.dhist_in != nullptr && on) {
+        // history row m = s + H1 (position s < 0)
+        const int64_t m = s + H1, q = m - len;  // its row in the next history, if it stays there
         vec_t hv = {};
         if (a.dhist_out != nullptr && q >= 0 && q < H1) hv = row(a.dhist_out, b * H1 + q);
         vec_t o;
@@ -378,27 +388,39 @@ __global__ __launch_bounds__(256) void conv_silu_bwd_kernel(const ConvBwdArgs<T>
         for (int e = 0; e < VEC; ++e) {
           C acc = to_compute<C>(hv[e]);
 #pragma unroll
-          for (int j = 0; j < KM; ++j) {
-            const int64_t t = p + j;  // the output that reads position p through tap j
-            if (j < K && t >= 0 && t < NP) acc += wr[j][e] * dpre[t >= 0 && t < NP ? t : 0][e];
-          }
+          for (int j = 0; j < KM; ++j) acc += wr[j][e] * pw[j][e];
           o[e] = from_compute<T>(acc);
         }
         *reinterpret_cast<vec_t*>(a.dhist_in + (b * H1 + m) * a.nc + c0) = o;
       }
     }
   }
-  // sum the 4 waves' weight and bias gradients, then one atomic per element
+  // sum the waves' weight and bias gradients in a fixed order (the upper half
+  // onto the lower, then the lower half per element), then one atomic per
+  // element and block
   if (a.dw != nullptr || a.dbias != nullptr) {
+    if (wv >= NW / 2) {
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) {
+      for (int e = 0; e < VEC; ++e) {
 #pragma unroll
-      for (int j = 0; j < KM; ++j) red[wv][(j * 64 + lane) * VEC + e] = gw[j][e];
-      red[wv][(KM * 64 + lane) * VEC + e] = gb[e];
+        for (int j = 0; j < KM; ++j) red[wv - NW / 2][(j * 64 + lane) * VEC + e] = gw[j][e];
+        red[wv - NW / 2][(KM * 64 + lane) * VEC + e] = gb[e];
+      }
     }
     __syncthreads();
-    for (int idx = threadIdx.x; idx < 64 * VEC * (KM + 1); idx += 256) {
-      const C sum = red[0][idx] + red[1][idx] + red[2][idx] + red[3][idx];
+    if (wv < NW / 2) {
+#pragma unroll
+      for (int e = 0; e < VEC; ++e) {
+#pragma unroll
+        for (int j = 0; j < KM; ++j) red[wv][(j * 64 + lane) * VEC + e] += gw[j][e];
+        red[wv][(KM * 64 + lane) * VEC + e] += gb[e];
+      }
+    }
+    __syncthreads();
+    for (int idx = threadIdx.x; idx < 64 * VEC * (KM + 1); idx += 64 * NW) {
+      C sum = red[0][idx];
+#pragma unroll
+      for (int u = 1; u < NW / 2; ++u) sum += red[u][idx];
       const int j = idx / (64 * VEC);
       const int rem = idx % (64 * VEC);
       const int64_t ch = (cb * 64 + rem / VEC) * VEC + rem % VEC;
@@ -438,7 +460,8 @@ static bool conv_bwd_g(const fbwd::ConvBwdArgs<T>& a, int g, dim3 grid, hipStrea
   switch (g) {
 #define KDA_CONV_BWD_CASE(GG)                                                                  \
   case GG:                                                                                     \
-    hipLaunchKernelGGL((fbwd::conv_silu_bwd_kernel<T, VEC, KT, GG>), grid, dim3(256), 0, s, a); \
+    hipLaunchKernelGGL((fbwd::conv_silu_bwd_kernel<T, VEC, KT, GG>), grid, dim3(64 * fbwd::conv_bwd_waves<KT>()), 0, s, \
+                       a);                                                                                   \
     return true;
     KDA_CONV_BWD_CASE(0)
     KDA_CONV_BWD_CASE(2)
@@ -456,7 +479,8 @@ template <class T>
 static int run_conv_bwd(const fbwd::ConvBwdArgs<T>& a, int g, hipStream_t stream) {
   constexpr int VEC = sizeof(T) == 8 ? 2 : 4;
   const int64_t nblk = (a.nc + 64 * VEC - 1) / (64 * VEC);
-  const int64_t rgroups = (fbwd::conv_bwd_runs(a.nt) + 3) / 4;
+  const int nw = a.K == 4 ? fbwd::conv_bwd_waves<4>() : fbwd::conv_bwd_waves<0>();  // waves per block
+  const int64_t rgroups = (fbwd::conv_bwd_runs(a.nt) + nw - 1) / nw;
   const int64_t blocks = a.nb * nblk * rgroups;
   if (blocks == 0) return KDA_OK;
   if (blocks > 0x7fffffffLL) {

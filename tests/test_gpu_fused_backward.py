@@ -57,9 +57,10 @@ def _cmp(label, pairs, dtype):
 @pytest.mark.parametrize("normalize", [True, False])
 @pytest.mark.parametrize("tokens", [37, 300])
 def test_conv_silu_gradients(dtype, taps, normalize, tokens):
-    # T = 37 is one run of one wave; T = 300 spans several runs per wave, the
-    # four waves' LDS reduction of dw and dbias, and blocks of more than one
-    # run group (T > 256)
+    # runs of 16 positions, 16 of them per block at K = 4 (8 for other K):
+    # T = 37 is three runs of one block; T = 300 spans two blocks per channel
+    # block, the waves' LDS reduction of dw and dbias in a full block and in
+    # one with idle waves
     B, T, H, D = 2, tokens, 4, 64
     C = H * D
     x = _rand(B, T, C, seed=1, dtype=dtype)
