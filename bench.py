@@ -267,6 +267,76 @@ def bench_fused(reps=50):
     return res
 
 
+def bench_fused_backward(reps=20):
+    """The backward of the fused stages on the prefill shape (B=1, T=8192,
+    H=16, D=128, bf16), each through the C ABI `reps` times between two HIP
+    events: the ShortConv + SiLU + L2 norm backward of one projection (kernel
+    size 4, bias, weight and bias gradients), the decay and beta gates'
+    backward (decay bias and A_log gradients), and the RMSNorm x output gate
+    backward (per-head weight gradient).  Algorithmic bytes = the activations
+    and incoming gradients read once and the input gradients written once
+    (parameters and their f32 gradient accumulators, a few KiB, not counted)."""
+    import torch
+
+    from kda import _lib, _prep
+
+    lib = _lib.load()
+    device = torch.device("cuda", 0)
+    gen = torch.Generator(device=device).manual_seed(11)
+    B, T, H, D = P_B, P_T, P_H, P_K
+    C, rows = H * D, P_B * P_T
+    rnd = lambda *shape: torch.randn(*shape, generator=gen, device=device).to(torch.bfloat16)  # noqa: E731
+    f32 = lambda *shape: torch.zeros(*shape, device=device)  # noqa: E731
+    x, w, cb, dy, dx = rnd(B, T, C), 0.3 * rnd(C, 4), 0.1 * rnd(C), rnd(B, T, C), rnd(B, T, C)
+    cdw, cdb = f32(C, 4), f32(C)
+    z, zb, a_log, dg, dz = rnd(rows, H, D), rnd(H, D), torch.zeros(H, device=device), rnd(rows, H, D), rnd(rows, H, D)
+    bl, dbt, dbl = rnd(rows, H), rnd(rows, H), rnd(rows, H)
+    gdzb, gdal = f32(H, D), f32(H)
+    o, nw, gl, do, dox, dgl = rnd(rows, H, D), rnd(H, D), rnd(rows, H, D), rnd(rows, H, D), rnd(rows, H, D), \
+        rnd(rows, H, D)
+    ndw = f32(H, D)
+    bf, el = _lib.dtype_code(torch.bfloat16), 2
+    stream = _prep.stream(device)
+    cases = {
+        "conv_silu_l2norm_bwd": (
+            "conv_silu_bwd_kernel",
+            lambda: lib.kda_conv_silu_bwd(x.data_ptr(), w.data_ptr(), cb.data_ptr(), None, None, dy.data_ptr(), None,
+                                          dx.data_ptr(), None, cdw.data_ptr(), cdb.data_ptr(), B, T, C, 4, D, 1,
+                                          1e-6, bf, stream),
+            3 * B * T * C * el),
+        "decay_and_beta_gates_bwd": (
+            "gates_bwd_kernel",
+            lambda: lib.kda_gates_bwd(z.data_ptr(), zb.data_ptr(), a_log.data_ptr(), -5.0, dg.data_ptr(), None,
+                                      dz.data_ptr(), gdzb.data_ptr(), gdal.data_ptr(), bl.data_ptr(),
+                                      dbt.data_ptr(), dbl.data_ptr(), rows, H, D, bf, stream),
+            3 * rows * H * D * el + 3 * rows * H * el),
+        "rmsnorm_output_gate_bwd": (
+            "rmsnorm_gate_bwd_kernel",
+            lambda: lib.kda_rmsnorm_gate_bwd(o.data_ptr(), nw.data_ptr(), 1, gl.data_ptr(), do.data_ptr(),
+                                             dox.data_ptr(), dgl.data_ptr(), ndw.data_ptr(), rows, H, D, 1e-6, bf,
+                                             stream),
+            5 * rows * H * D * el),
+    }
+    res = {}
+    for name, (kernel, fn, nbytes) in cases.items():
+        _settle(lambda: _lib.check(fn()))
+        for _ in range(3):
+            _lib.check(fn())
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        res[name] = {"ms": round(ms, 5), "algorithmic_bytes": nbytes, "achieved_gbs": round(gbs, 1),
+                     "frac_hbm": round(gbs / HBM_PEAK_GBS, 4), "traffic": measured_traffic(kernel)}
+    return res
+
+
 def bench_decay_fusion(reps=20):
     """The decay feeding the prefill at the long-context shape, two ways:
     kda_gates_fwd writing g (bf16) followed by kda_chunk_fwd reading it, and
@@ -733,7 +803,7 @@ def profile_pass(which="all"):
     """The workload of the counter runs: after one warm-up round, one prefill at
     the benchmark shape, one in-place decode step at the benchmark shape, and a
     256 MiB device-to-device copy whose byte counts check the counters; then
-    the fused stages, the backward and the cache reorder legs once each (their
+    the fused stages and their backward, the backward and the cache reorder legs once each (their
     warm-up calls included).  With a configuration name: that prefill only,
     a warm-up call and a measured one."""
     import torch
@@ -761,6 +831,7 @@ def profile_pass(which="all"):
             dst.copy_(src)
     torch.cuda.synchronize()
     bench_fused(reps=1)
+    bench_fused_backward(reps=1)
     bench_backward(reps=1)
     bench_cache(reps=1)
     print("profile pass done", flush=True)
@@ -1105,6 +1176,10 @@ def main() -> int:
     result["fused_stages"] = {
         "workload": f"B={P_B} T={P_T} H={P_H} D={P_K} bf16, 50 back-to-back C-ABI launches each",
         "kernels": bench_fused(),
+    }
+    result["fused_stages_backward"] = {
+        "workload": f"B={P_B} T={P_T} H={P_H} D={P_K} bf16, 20 back-to-back C-ABI launches each",
+        "kernels": bench_fused_backward(),
     }
     k64_ms, k64_kernels, _, _ = bench_prefill(args.steps, args.warmup, shape=(1, 8192, 16, 64, 64),
                                               settle_ms=SETTLE_MS)

@@ -41,9 +41,11 @@ __device__ __forceinline__ void atomic_add(double* p, double v) { atomicAdd(p, v
 // n = x r, y = n * w * sigmoid(z).  Backward with dy:
 //   dz = dy n w s (1 - s),  dw += dy n s,  dn = dy w s,
 //   dx = r (dn - n * sum(dn n) / D).
-// A lane group of G lanes holds one (row, head) pair, VEC elements per lane;
-// the pairs a group visits share one head (the grid's group count is a
-// multiple of H), so its weight gradient accumulates in registers.
+// A lane group of G lanes holds one (row, head) pair, VEC elements per lane.
+// A block takes one head and 256 / G of its rows at a time, striding over the
+// rows with the other blocks of that head; the weight gradient accumulates in
+// registers, the block's groups' sums meet in LDS in a fixed order, and each
+// element goes out with one atomic per block.
 template <class T>
 struct NormBwdArgs {
   const T* x;    // [rows, H, D]
@@ -54,28 +56,27 @@ struct NormBwdArgs {
   T* dx;         // [rows, H, D]
   T* dgl;        // [rows, H*D] or null
   typename ComputeOf<T>::type* dw;  // [H, D] or [D] accumulators (zeroed by the caller) or null
-  int64_t rows, H, groups;          // groups: lane groups in the grid, a multiple of H
+  int64_t rows, H, row_blocks;      // row_blocks: blocks per head (the grid is H x row_blocks)
   float eps;
 };
 
 template <class T, int VEC, int G>
 __global__ __launch_bounds__(256) void rmsnorm_gate_bwd_kernel(const NormBwdArgs<T> a) {
   using C = typename ComputeOf<T>::type;
-  constexpr int D = G * VEC;
+  constexpr int D = G * VEC, PB = 256 / G;  // PB: lane groups (rows) per block
   typedef T vec_t __attribute__((ext_vector_type(VEC)));
-  const int lane = threadIdx.x & 63;
-  const int k = lane % G;
-  const int64_t gid = (static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x) / G;
-  const int64_t n = a.rows * a.H;
-  const int64_t head = gid % a.H;
+  __shared__ C red[PB][D];
+  const int k = threadIdx.x % G, gi = threadIdx.x / G;
+  const int64_t head = blockIdx.x % a.H, rb = blockIdx.x / a.H;
   vec_t wv = {};
   if (a.w != nullptr) wv = *reinterpret_cast<const vec_t*>(a.w + (a.w_per_head ? head * D : 0) + k * VEC);
   C dw[VEC];
 #pragma unroll
   for (int e = 0; e < VEC; ++e) dw[e] = C(0);
-  // the lanes of a group share gid, so they run the same steps (the
+  // the lanes of a group share the row, so they run the same steps (the
   // reductions stay inside the group)
-  for (int64_t pair = gid; pair < n; pair += a.groups) {
+  for (int64_t row = rb * PB + gi; row < a.rows; row += a.row_blocks * PB) {
+    const int64_t pair = row * a.H + head;
     vec_t gv = {};
     const vec_t xv = *reinterpret_cast<const vec_t*>(a.x + pair * D + k * VEC);
     const vec_t dv = *reinterpret_cast<const vec_t*>(a.dy + pair * D + k * VEC);
@@ -105,10 +106,16 @@ __global__ __launch_bounds__(256) void rmsnorm_gate_bwd_kernel(const NormBwdArgs
     *reinterpret_cast<vec_t*>(a.dx + pair * D + k * VEC) = o;
     if (a.dgl != nullptr) *reinterpret_cast<vec_t*>(a.dgl + pair * D + k * VEC) = gv;
   }
-  if (a.dw != nullptr && gid < a.groups) {
-    C* dst = a.dw + (a.w_per_head ? head * D : 0) + k * VEC;
+  if (a.dw != nullptr) {  // uniform
 #pragma unroll
-    for (int e = 0; e < VEC; ++e) atomic_add(dst + e, dw[e]);
+    for (int e = 0; e < VEC; ++e) red[gi][k * VEC + e] = dw[e];
+    __syncthreads();
+    C* dst = a.dw + (a.w_per_head ? head * D : 0);
+    for (int d = threadIdx.x; d < D; d += 256) {
+      C sum = red[0][d];
+      for (int u = 1; u < PB; ++u) sum += red[u][d];
+      atomic_add(dst + d, sum);
+    }
   }
 }
 
@@ -120,8 +127,15 @@ __global__ __launch_bounds__(256) void rmsnorm_gate_bwd_kernel(const NormBwdArgs
 //   dz = dq s,  db += dq s,  dA_log[h] += s * sum(dq u);
 //   dl = dbeta [lo <= beta' <= hi] beta' (1 - beta'),  beta' = sigmoid(l).
 // A thread owns one 16-byte vector position of a row's [H, K] block (fixed
-// head and channels) and walks the rows; the bias and A_log gradients
-// accumulate in registers and go out with one atomic each per thread.
+// head and channels) and walks a share of a block's rows: a block holds
+// kGateRowGroups groups of 256 threads over the same positions, each group
+// every kGateRowGroups-th row of the block's range.  The bias and A_log
+// gradients accumulate in registers, the groups' sums meet in LDS in a fixed
+// order, the bias gradient goes out with one atomic per element and block and
+// the A_log gradient with one per head and block (summed over the head's
+// positions in the block first): a few hundred atomics per address instead of
+// one per row.
+constexpr int kGateRowGroups = 4;
 template <class T>
 struct GateBwdArgs {
   const T* z;          // [rows, H, K] or null
@@ -140,24 +154,30 @@ struct GateBwdArgs {
 };
 
 template <class T>
-__global__ __launch_bounds__(256) void gates_bwd_kernel(const GateBwdArgs<T> a) {
+__global__ __launch_bounds__(256 * kGateRowGroups) void gates_bwd_kernel(const GateBwdArgs<T> a) {
   using C = typename ComputeOf<T>::type;
   constexpr int VEC = 16 / sizeof(T);
   typedef T vec_t __attribute__((ext_vector_type(VEC)));
+  __shared__ C red[kGateRowGroups][256][VEC + 1];
   const C lo = C(a.eps), hi = C(1) - C(a.eps);
-  if (a.z != nullptr) {
+  if (a.z != nullptr) {  // uniform
     const int64_t hkv = a.H * a.K / VEC;
-    const int64_t v = static_cast<int64_t>(blockIdx.x) * blockDim.x + threadIdx.x;
-    if (v < hkv) {
-      const int64_t h = v * VEC / a.K;
-      const C s = fexp(static_cast<C>(a.a_log[h]));
+    const int tv = threadIdx.x & 255, rg = threadIdx.x >> 8;
+    const int64_t v = static_cast<int64_t>(blockIdx.x) * 256 + tv;
+    const bool live = v < hkv;
+    const int64_t h = live ? v * VEC / a.K : 0;
+    const C s = live ? fexp(static_cast<C>(a.a_log[h])) : C(0);
+    C db[VEC];
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) db[e] = C(0);
+    C ds = C(0);
+    if (live) {
       vec_t bv = {};
       if (a.zbias != nullptr) bv = *reinterpret_cast<const vec_t*>(a.zbias + v * VEC);
-      C db[VEC];
-#pragma unroll
-      for (int e = 0; e < VEC; ++e) db[e] = C(0);
-      C ds = C(0);
-      for (int64_t r = blockIdx.y; r < a.rows; r += gridDim.y) {
+      const int64_t per = (a.rows + gridDim.y - 1) / gridDim.y;  // rows per block
+      const int64_t r0 = static_cast<int64_t>(blockIdx.y) * per;
+      const int64_t r1 = r0 + per < a.rows ? r0 + per : a.rows;
+      for (int64_t r = r0 + rg; r < r1; r += kGateRowGroups) {
         const int64_t e0 = (r * hkv + v) * VEC;
         const vec_t zv = *reinterpret_cast<const vec_t*>(a.z + e0);
         const vec_t gv = *reinterpret_cast<const vec_t*>(a.dg + e0);
@@ -179,10 +199,33 @@ __global__ __launch_bounds__(256) void gates_bwd_kernel(const GateBwdArgs<T> a) 
         }
         *reinterpret_cast<vec_t*>(a.dz + e0) = o;
       }
+    }
+#pragma unroll
+    for (int e = 0; e < VEC; ++e) red[rg][tv][e] = db[e];
+    red[rg][tv][VEC] = ds * s;
+    __syncthreads();
+    if (rg == 0 && live) {
+#pragma unroll
+      for (int e = 0; e < VEC + 1; ++e) {
+        C sum = red[0][tv][e];
+#pragma unroll
+        for (int u = 1; u < kGateRowGroups; ++u) sum += red[u][tv][e];
+        red[0][tv][e] = sum;
+      }
       if (a.dzbias != nullptr)
 #pragma unroll
-        for (int e = 0; e < VEC; ++e) atomic_add(a.dzbias + v * VEC + e, db[e]);
-      if (a.da_log != nullptr) atomic_add(a.da_log + h, ds * s);
+        for (int e = 0; e < VEC; ++e) atomic_add(a.dzbias + v * VEC + e, red[0][tv][e]);
+    }
+    __syncthreads();
+    // A_log: the first of a head's positions in this block sums the head's
+    // positions in order and adds them with one atomic
+    if (rg == 0 && live && a.da_log != nullptr && (tv == 0 || (v * VEC) % a.K == 0)) {
+      C sum = C(0);
+      for (int u = tv; u < 256 && static_cast<int64_t>(blockIdx.x) * 256 + u < hkv &&
+                       (static_cast<int64_t>(blockIdx.x) * 256 + u) * VEC / a.K == h;
+           ++u)
+        sum += red[0][u][VEC];
+      atomic_add(a.da_log + h, sum);
     }
   }
   if (a.bl != nullptr) {
@@ -561,9 +604,11 @@ template <class T>
 static int run_gates_bwd(const fbwd::GateBwdArgs<T>& a, hipStream_t stream) {
   constexpr int VEC = 16 / sizeof(T);
   dim3 grid(1, 1);
+  constexpr int NT = 256 * fbwd::kGateRowGroups;
   if (a.z != nullptr) {
+    // about 256 blocks: one per CU, each over a contiguous range of rows
     const int64_t bx = (a.H * a.K / VEC + 255) / 256;
-    int64_t by = 1024 / (bx > 0 ? bx : 1);
+    int64_t by = 256 / (bx > 0 ? bx : 1);
     if (by < 1) by = 1;
     if (by > a.rows) by = a.rows;
     if (by > 65535) by = 65535;
@@ -574,11 +619,11 @@ static int run_gates_bwd(const fbwd::GateBwdArgs<T>& a, hipStream_t stream) {
     grid = dim3(static_cast<unsigned>(bx), static_cast<unsigned>(by));
   } else {
     const int64_t n = a.rows * a.H;
-    int64_t bx = (n + 255) / 256;
-    if (bx > 4096) bx = 4096;
+    int64_t bx = (n + NT - 1) / NT;
+    if (bx > 1024) bx = 1024;
     grid = dim3(static_cast<unsigned>(bx > 0 ? bx : 1), 1);
   }
-  hipLaunchKernelGGL((fbwd::gates_bwd_kernel<T>), grid, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((fbwd::gates_bwd_kernel<T>), grid, dim3(NT), 0, stream, a);
   return check_launch("gates_bwd_kernel");
 }
 
@@ -629,28 +674,18 @@ int launch_gates_bwd(const void* z, const void* zbias, const float* a_log, doubl
 }
 
 // ---- rmsnorm ----
-static int64_t gcd64(int64_t a, int64_t b) {
-  while (b) {
-    const int64_t t = a % b;
-    a = b;
-    b = t;
-  }
-  return a;
-}
 
 template <class T, int VEC, int G>
 static int run_norm_bwd(fbwd::NormBwdArgs<T> a, hipStream_t stream) {
-  constexpr int per_block = 256 / G;  // lane groups per block
-  // the group count is a multiple of H (each group keeps one head) and of
-  // the groups in a block
-  const int64_t unit = a.H / gcd64(a.H, per_block) * per_block;
-  const int64_t n = a.rows * a.H;
-  int64_t m = (1024 * per_block) / unit;
-  if (m < 1) m = 1;
-  const int64_t need = (n + unit - 1) / unit;
-  if (m > need) m = need;
-  a.groups = m * unit;
-  const int64_t blocks = a.groups / per_block;
+  constexpr int per_block = 256 / G;  // lane groups (rows) per block
+  // about 1024 blocks: H heads x row_blocks stripes of rows
+  int64_t rb = 1024 / (a.H > 0 ? a.H : 1);
+  if (rb < 1) rb = 1;
+  const int64_t need = (a.rows + per_block - 1) / per_block;
+  if (rb > need) rb = need;
+  if (rb < 1) rb = 1;
+  a.row_blocks = rb;
+  const int64_t blocks = a.H * rb;
   if (blocks > 0x7fffffffLL) {
     set_detail("rmsnorm_gate_bwd: grid too large");
     return KDA_ERR_UNSUPPORTED;

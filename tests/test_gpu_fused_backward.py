@@ -97,10 +97,14 @@ def test_conv_silu_decode_step_gradients():
 
 
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
-def test_decay_and_beta_gradients(dtype):
-    B, T, H, K = 2, 33, 4, 64
+@pytest.mark.parametrize("T,H,K", [(33, 4, 64), (700, 64, 48)])
+def test_decay_and_beta_gradients(dtype, T, H, K):
+    # (700, 64, 48): blocks of several rows per row group, and heads whose
+    # 16-byte positions straddle a block's 256 (48 channels are 6 of them in
+    # bf16, 12 in f32, 24 in f64)
+    B = 2
     z = _rand(B, T, H, K, seed=11, scale=2.0, dtype=dtype)
-    z[0, :3] = 60.0  # saturated: clamped to 1 - eps, no gradient
+    z[0, :3] = 1000.0  # saturated for every head's exp(A_log) >= 0.2, in f64 too: clamped to 1 - eps, no gradient
     bias = _rand(H, K, seed=12, scale=0.5, dtype=dtype)
     a_log = _rand(H, seed=13, scale=0.3, dtype=torch.float32)
     bl = _rand(B, T, H, seed=14, dtype=dtype)
@@ -128,8 +132,10 @@ def test_decay_and_beta_gradients(dtype):
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("weight", ["per_head", "shared", None])
 @pytest.mark.parametrize("gate", [True, False])
-def test_rmsnorm_gate_gradients(dtype, weight, gate):
-    B, T, H, D = 2, 21, 4, 128
+@pytest.mark.parametrize("T", [21, 2100])
+def test_rmsnorm_gate_gradients(dtype, weight, gate, T):
+    # T = 2100 (4200 rows): a head's blocks stride over its rows more than once
+    B, H, D = 2, 4, 128
     x = _rand(B, T, H, D, seed=21, dtype=dtype)
     w = None if weight is None else _rand(*((H, D) if weight == "per_head" else (D,)), seed=22, scale=0.5,
                                           dtype=dtype) + 1
