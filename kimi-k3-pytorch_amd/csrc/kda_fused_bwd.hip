@@ -128,14 +128,16 @@ __global__ __launch_bounds__(256) void rmsnorm_gate_bwd_kernel(const NormBwdArgs
 //   dl = dbeta [lo <= beta' <= hi] beta' (1 - beta'),  beta' = sigmoid(l).
 // A thread owns one 16-byte vector position of a row's [H, K] block (fixed
 // head and channels) and walks a share of a block's rows: a block holds
-// kGateRowGroups groups of 256 threads over the same positions, each group
-// every kGateRowGroups-th row of the block's range.  The bias and A_log
+// kGateRowGroups groups of kGatePos threads over the same positions, each
+// group every kGateRowGroups-th row of the block's range.  The bias and A_log
 // gradients accumulate in registers, the groups' sums meet in LDS in a fixed
 // order, the bias gradient goes out with one atomic per element and block and
 // the A_log gradient with one per head and block (summed over the head's
-// positions in the block first): a few hundred atomics per address instead of
-// one per row.
-constexpr int kGateRowGroups = 4;
+// positions in the block first): about 32 atomics per address at 8192 rows
+// (256 blocks) instead of one per row, the atomics having set the time
+// (2.55 ms with one per thread and row, 71 us at 256 positions x 4 row groups,
+// 33 at 64 x 16, 27 at 32 x 32 for B=1, T=8192, H=16, K=128, bf16).
+constexpr int kGatePos = 32, kGateRowGroups = 32;
 template <class T>
 struct GateBwdArgs {
   const T* z;          // [rows, H, K] or null
@@ -154,16 +156,16 @@ struct GateBwdArgs {
 };
 
 template <class T>
-__global__ __launch_bounds__(256 * kGateRowGroups) void gates_bwd_kernel(const GateBwdArgs<T> a) {
+__global__ __launch_bounds__(kGatePos * kGateRowGroups) void gates_bwd_kernel(const GateBwdArgs<T> a) {
   using C = typename ComputeOf<T>::type;
   constexpr int VEC = 16 / sizeof(T);
   typedef T vec_t __attribute__((ext_vector_type(VEC)));
-  __shared__ C red[kGateRowGroups][256][VEC + 1];
+  __shared__ C red[kGateRowGroups][kGatePos][VEC + 1];
   const C lo = C(a.eps), hi = C(1) - C(a.eps);
   if (a.z != nullptr) {  // uniform
     const int64_t hkv = a.H * a.K / VEC;
-    const int tv = threadIdx.x & 255, rg = threadIdx.x >> 8;
-    const int64_t v = static_cast<int64_t>(blockIdx.x) * 256 + tv;
+    const int tv = threadIdx.x % kGatePos, rg = threadIdx.x / kGatePos;
+    const int64_t v = static_cast<int64_t>(blockIdx.x) * kGatePos + tv;
     const bool live = v < hkv;
     const int64_t h = live ? v * VEC / a.K : 0;
     const C s = live ? fexp(static_cast<C>(a.a_log[h])) : C(0);
@@ -221,8 +223,8 @@ __global__ __launch_bounds__(256 * kGateRowGroups) void gates_bwd_kernel(const G
     // positions in order and adds them with one atomic
     if (rg == 0 && live && a.da_log != nullptr && (tv == 0 || (v * VEC) % a.K == 0)) {
       C sum = C(0);
-      for (int u = tv; u < 256 && static_cast<int64_t>(blockIdx.x) * 256 + u < hkv &&
-                       (static_cast<int64_t>(blockIdx.x) * 256 + u) * VEC / a.K == h;
+      for (int u = tv; u < kGatePos && static_cast<int64_t>(blockIdx.x) * kGatePos + u < hkv &&
+                       (static_cast<int64_t>(blockIdx.x) * kGatePos + u) * VEC / a.K == h;
            ++u)
         sum += red[0][u][VEC];
       atomic_add(a.da_log + h, sum);
@@ -604,10 +606,10 @@ template <class T>
 static int run_gates_bwd(const fbwd::GateBwdArgs<T>& a, hipStream_t stream) {
   constexpr int VEC = 16 / sizeof(T);
   dim3 grid(1, 1);
-  constexpr int NT = 256 * fbwd::kGateRowGroups;
+  constexpr int NT = fbwd::kGatePos * fbwd::kGateRowGroups;
   if (a.z != nullptr) {
     // about 256 blocks: one per CU, each over a contiguous range of rows
-    const int64_t bx = (a.H * a.K / VEC + 255) / 256;
+    const int64_t bx = (a.H * a.K / VEC + fbwd::kGatePos - 1) / fbwd::kGatePos;
     int64_t by = 256 / (bx > 0 ? bx : 1);
     if (by < 1) by = 1;
     if (by > a.rows) by = a.rows;
