@@ -337,6 +337,64 @@ def bench_fused_backward(reps=20):
     return res
 
 
+def bench_layer_train(reps=5):
+    """One KDA layer (d_model 2048 = 16 heads x 128, ShortConv kernel 4, decay
+    rank 128, random bf16 weights in the reference's layouts) on B=1, T=8192
+    bf16 synthetic hidden states through kda.layer.kda_attention_forward in
+    chunkwise mode: the forward alone, and forward + backward of the sum of
+    the outputs (every weight and the input requiring gradients), `reps`
+    timed calls each after 2 untimed ones, between two HIP events."""
+    import math
+
+    import torch
+
+    from kda.layer import KDALayerWeights, kda_attention_forward
+
+    device = torch.device("cuda", 0)
+    gen = torch.Generator().manual_seed(41)
+    H, D, R, B, T = P_H, P_K, 128, P_B, P_T
+    dm = H * D
+    rnd = lambda *shape, s=0.02: (torch.randn(*shape, generator=gen) * s).to(device, torch.bfloat16)  # noqa: E731
+    dt = torch.exp(torch.rand(H, D, generator=gen) * (math.log(0.1) - math.log(0.001)) + math.log(0.001))
+    w = dict(num_heads=H, key_head_dim=D, value_head_dim=D,
+             q_proj=rnd(dm, dm), k_proj=rnd(dm, dm), v_proj=rnd(dm, dm),
+             q_conv=rnd(dm, 4, s=0.3), k_conv=rnd(dm, 4, s=0.3), v_conv=rnd(dm, 4, s=0.3),
+             beta_proj=rnd(H, dm), alpha_down=rnd(R, dm), alpha_up=rnd(dm, R),
+             b_alpha=(dt + torch.log(-torch.expm1(-dt))).to(device, torch.bfloat16),
+             a_log=(0.1 * torch.randn(H, generator=gen)).to(device),
+             norm_weight=(1 + 0.1 * torch.randn(H, D, generator=gen)).to(device, torch.bfloat16),
+             gate_proj=rnd(dm, dm), output_proj=rnd(dm, dm))
+    for k, v in w.items():
+        if isinstance(v, torch.Tensor):
+            v.requires_grad_()
+    weights = KDALayerWeights(**w)
+    x = (torch.randn(B, T, dm, generator=gen)).to(device, torch.bfloat16).requires_grad_()
+
+    def fwd():
+        with torch.no_grad():
+            kda_attention_forward(weights, x, mode="chunkwise")
+
+    def train():
+        out = kda_attention_forward(weights, x, mode="chunkwise")
+        out.hidden_states.float().sum().backward()
+
+    res = {"workload": f"KDA layer d_model {dm} ({H} heads x {D}), ShortConv 4, decay rank {R}, B={B} T={T} "
+                       "bf16, random weights, synthetic hidden states, chunkwise mode"}
+    for name, fn in (("forward", fwd), ("forward_backward", train)):
+        for _ in range(2):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / reps
+        res[name] = {"ms": round(ms, 4), "tokens_per_s": round(B * T / (ms * 1e-3), 1)}
+    return res
+
+
 def bench_decay_fusion(reps=20):
     """The decay feeding the prefill at the long-context shape, two ways:
     kda_gates_fwd writing g (bf16) followed by kda_chunk_fwd reading it, and
@@ -1181,6 +1239,7 @@ def main() -> int:
         "workload": f"B={P_B} T={P_T} H={P_H} D={P_K} bf16, 20 back-to-back C-ABI launches each",
         "kernels": bench_fused_backward(),
     }
+    result["layer_train"] = bench_layer_train()
     k64_ms, k64_kernels, _, _ = bench_prefill(args.steps, args.warmup, shape=(1, 8192, 16, 64, 64),
                                               settle_ms=SETTLE_MS)
     k64_bytes = prefill_bytes(1, 8192, 16, 64, 64)
