@@ -597,9 +597,9 @@ __device__ __forceinline__ int opaque(int x) {
 //   the MFMA decay products of A and Aqk, accumulated in registers (each
 //   block pair's channel sum runs in the same 32-channel steps as it would
 //   over the whole chunk);
-//   Kg = e^lg k, Kt = e^(lg_last - lg) k and Qg = e^lg q in place of k, q
-//   and lg, with their records (D, Kg and Kt row-major, Kt^T, Qg^T), and Kg
-//   copied into a [64][KP] tile that stays for W = M Kg.
+//   Kt = e^(lg_last - lg) k and Qg = e^lg q in place of q and lg, and
+//   Kg = e^lg k into a [64][KP] tile that stays for W = M Kg, with their
+//   records (D, Kg and Kt row-major, Kt^T, Qg^T).
 // A chunk whose decays fall outside the factorisation's bounds repeats the
 // quarters for A and Aqk with exact pair exponents.  Then N = L^-1,
 // M = N diag(b), W = M Kg and U = M v.
@@ -701,8 +701,8 @@ __global__ __launch_bounds__(kPT, 4) void prep_kernel(const Args<IT> a) {
       ws[a.L.D + c0 + tq] = fast_exp(last);
     }
     __syncthreads();
-    // each element's factors once: Kg, Kt, Qg in place of k, q, lg, with Kg
-    // into its tile and the row-major Kg and Kt records written on the way
+    // each element's factors once: Kt and Qg in place of q and lg, Kg into
+    // its tile, and the row-major Kg and Kt records written on the way
     for (int i8 = tq; i8 < kC * kQC / 8; i8 += kPT) {
       const int r = (8 * i8) / kQC, cl = (8 * i8) % kQC;
       const float* kp = &kS[r * kQS + cl];
