@@ -55,12 +55,12 @@ def _cmp(label, pairs, dtype):
 @pytest.mark.parametrize("dtype", [torch.float64, torch.float32, torch.bfloat16])
 @pytest.mark.parametrize("taps", [4, 3])
 @pytest.mark.parametrize("normalize", [True, False])
-@pytest.mark.parametrize("tokens", [37, 300])
+@pytest.mark.parametrize("tokens", [37, 300, 2048])
 def test_conv_silu_gradients(dtype, taps, normalize, tokens):
     # runs of 16 positions, 16 of them per block at K = 4 (8 for other K):
     # T = 37 is three runs of one block; T = 300 spans two blocks per channel
     # block, the waves' LDS reduction of dw and dbias in a full block and in
-    # one with idle waves
+    # one with idle waves; T = 2048 sums dw and dbias over 8 (16) blocks
     B, T, H, D = 2, tokens, 4, 64
     C = H * D
     x = _rand(B, T, C, seed=1, dtype=dtype)
